@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark for the SunShape compressed-KV path on MI355X.
+
+Workload (BASELINE.json metric, config 2 at T_kv = 32768): batch 1, 32 query
+heads / 8 KV heads, head_dim 128, 1-bit/dim SunShape keys (uint8 indices
+(8, 32768, 16)) and fp16 values N(0,1); one fp16 query token per step;
+codebook fit on 4096 N(0,1) keys with a per-dim scale in [0.5, 4].
+
+A step is one fused decode-attention launch over the whole cache (all 32
+query heads).  The timed region rotates over enough cache copies (> 3x the
+256 MB Infinity Cache) that every step reads its indices and values from
+HBM.  ``value`` is algorithmic HBM bytes per step / time per step.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode attention µs/step and achieved HBM GB/s (% of peak) at T_kv=32K"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--t-kv", type=int, default=32768)
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--splits", type=int, default=0, help="token splits (0 = library choice)")
+    p.add_argument("--copies", type=int, default=0, help="cache copies rotated (0 = auto)")
+    p.add_argument("--launch", choices=("eager", "graph"), default="eager")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="budget for the CPU baseline (0 disables it)")
+    p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
+                                                          "decode_fp16v_t32k_traffic.json"))
+    return p.parse_args()
+
+
+def algorithmic_bytes(b, hq, hkv, d, t_kv, nb, v_bytes=2, q_bytes=2, out_bytes=2) -> int:
+    """Bytes one step must move at minimum: every key index row and value row
+    once per (batch, KV head), the query in and the output out.  Centroids
+    (128 KB, cache-resident), split partials and GQA re-reads excluded."""
+    return b * hkv * t_kv * (nb + d * v_bytes) + b * hq * d * (q_bytes + out_bytes)
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the decode path shards by KV head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    lib = hip.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    b, hq, hkv, d, t_kv = args.batch, 32, 8, 128, args.t_kv
+    nb = d // 8
+    scale = 1.0 / math.sqrt(d)
+
+    # ---- codebook: fit on anisotropic N(0,1) * s calibration data ----
+    rng = np.random.default_rng(2)
+    s = rng.uniform(0.5, 4.0, d).astype(np.float32)
+    k_cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)
+    q_cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)
+    t0 = time.time()
+    codec = pkg.codec.SunShapeBlockCodec(d, device=dev).fit(q_cal, k_cal, kmeans_iters=15,
+                                                            seed=2)
+    log(f"codec fit {time.time() - t0:.1f}s")
+
+    # ---- cache: encode fresh keys on the GPU; fp16 values ----
+    g = torch.Generator(device=dev).manual_seed(2)
+    s_t = torch.from_numpy(s).to(dev)
+    keys = (torch.randn((b, hkv, t_kv, d), generator=g, device=dev) * s_t).to(torch.float16)
+    idx0 = torch.empty((b, hkv, t_kv, nb), dtype=torch.uint8, device=dev)
+    hip.encode_blockvq(keys, codec.permutation, codec.centroids, idx0, 8)
+    v0 = torch.randn((b, hkv, t_kv, d), generator=g, device=dev).to(torch.float16)
+    q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
+    del keys
+    per_copy = idx0.numel() + v0.numel() * 2
+    n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
+    idxs = [idx0] + [idx0.clone() for _ in range(n_copies - 1)]
+    vals = [v0] + [v0.clone() for _ in range(n_copies - 1)]
+    torch.cuda.synchronize()
+    log(f"cache ready: {n_copies} copies x {per_copy / 1e6:.1f} MB")
+
+    # ---- lean launcher: prebuilt C-ABI argument tuples, one per copy ----
+    splits = args.splits or hip.default_splits(b, hq, hkv, 1, d, t_kv)
+    ws_bytes = hip.decode_workspace_bytes(b, hq, hkv, 1, d, t_kv, splits)
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
+    fn = lib.ss_decode_attn_dense
+
+    def arg_tuples(stream_handle):
+        return [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, codec.permutation.data_ptr(),
+                 codec.centroids.data_ptr(), nb, 256, idxs[i].data_ptr(), vals[i].data_ptr(),
+                 hip.SS_F16, t_kv, t_kv, 0, 0, out.data_ptr(), hip.SS_F16, ws.data_ptr(),
+                 ws_bytes, splits, stream_handle) for i in range(n_copies)]
+
+    argv = arg_tuples(torch.cuda.current_stream().cuda_stream)
+
+    def run(n, start=0):
+        for i in range(start, start + n):
+            rc = fn(*argv[i % n_copies])
+            if rc:
+                hip.check(rc)
+
+    run(args.warmup)
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done (splits={splits}, workspace={ws_bytes} B)")
+
+    if args.launch == "graph":
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            argv = arg_tuples(torch.cuda.current_stream().cuda_stream)
+            run(n_copies)
+        torch.cuda.synchronize()
+        reps = max(1, args.steps // n_copies)
+        steps = reps * n_copies
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(reps):
+            graph.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+    else:
+        steps = args.steps
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        run(steps)
+        ev1.record()
+        torch.cuda.synchronize()
+    ms_total = ev0.elapsed_time(ev1)
+    ms_step = ms_total / steps
+    log(f"timed {steps} steps: {ms_step * 1e3:.2f} us/step")
+
+    # per-launch durations (events bracket each launch on the launch stream)
+    argv = arg_tuples(torch.cuda.current_stream().cuda_stream)
+    n_pl = min(steps, 100)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n_pl)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record()
+        hip.check(fn(*argv[i % n_copies]))
+        e1.record()
+    torch.cuda.synchronize()
+    per = np.array([e0.elapsed_time(e1) * 1e3 for e0, e1 in evs])
+
+    nbytes = algorithmic_bytes(b, hq, hkv, d, t_kv, nb)
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+
+    traffic = None
+    if os.path.exists(args.traffic_file):
+        with open(args.traffic_file) as f:
+            tr = json.load(f)
+        if tr.get("t_kv") == t_kv and tr.get("batch") == b:
+            traffic = tr.get("hbm_bytes_per_launch")
+
+    # ---- output check + CPU baseline (oracle restatement, host cores) ----
+    cpu = None
+    check = None
+    if args.cpu_seconds > 0:
+        from threadpoolctl import threadpool_limits
+
+        from oracle import sunshape_oracle as O
+
+        hip.check(fn(*argv[0]))
+        torch.cuda.synchronize()
+        gpu_out = out.float().cpu().numpy().reshape(b, hq, d)
+        perm = codec.permutation.cpu().numpy()
+        cents = codec.centroids.cpu().numpy()
+        q_np = q.cpu().numpy()
+        q_t = O.apply_permutation(O.scale_query(q_np, scale), perm).astype(np.float32)
+        q_t = q_t.reshape(b, hkv, hq // hkv, d)
+        idx_np = idx0.cpu().numpy()
+        v_np = v0.cpu().numpy()
+        with threadpool_limits(1):
+            forms = {}
+            for name, fnc, budget in (("vectorised", O.decode_cpu_vectorised, 0.7),
+                                      ("reference_shaped", O.decode_cpu_reference_shaped, 0.3)):
+                n_run, t_start, res = 0, time.perf_counter(), None
+                while True:
+                    res = fnc(q_t, cents, idx_np, v_np)
+                    n_run += 1
+                    if time.perf_counter() - t_start > args.cpu_seconds * budget:
+                        break
+                dt = (time.perf_counter() - t_start) / n_run
+                forms[name] = (dt, n_run, res)
+                log(f"cpu {name}: {dt * 1e3:.1f} ms/step over {n_run} steps")
+        dt, n_run, res = forms["vectorised"]
+        check = float(np.abs(gpu_out - res).max() / np.abs(res).max())
+        cpu = {
+            "value": round(nbytes / dt / 1e9, 3),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": (f"{n_run} full steps of the metric workload by the NumPy float32 "
+                       f"restatement (oracle.decode_cpu_vectorised, 1 BLAS thread), "
+                       f"{dt * 1e3:.1f} ms/step; reference-shaped per-(b,h,r) loop "
+                       f"{forms['reference_shaped'][0] * 1e3:.1f} ms/step"),
+            "ms_per_step": round(dt * 1e3, 3),
+            "ms_per_step_reference_shaped": round(forms["reference_shaped"][0] * 1e3, 3),
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_step": round(ms_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode B=1 Hq=32 Hkv=8 D=128 T_kv=32768, 1-bit/dim SunShape keys "
+                        "(u8 idx), fp16 values, fp16 query/output, f32 accumulate",
+            "batch": b, "n_q_heads": hq, "n_kv_heads": hkv, "head_dim": d, "t_kv": t_kv,
+            "splits": splits, "launch": args.launch, "cache_copies": n_copies,
+            "algorithmic_bytes_per_step": nbytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "per_launch_us": {"median": round(float(np.median(per)), 3),
+                          "p10": round(float(np.percentile(per, 10)), 3),
+                          "p90": round(float(np.percentile(per, 90)), 3), "n": int(n_pl)},
+        "cpu_baseline": cpu,
+        "check_max_rel_err_vs_cpu": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,204 @@
+/*
+ * sunshape_hip.h -- C ABI of libsunshape_hip.so, the MI355X (gfx950) HIP
+ * implementation of SunShape's compressed-KV attention path.
+ *
+ * The reference (gauravsaini/sunshape-mlx) has no FFI: its boundary is a set
+ * of Python launchers in kernels.py that take MLX arrays, run one Metal
+ * dispatch synchronously and return an array (or None on failure).  Each
+ * entry point below replaces one of those launchers (cited per function);
+ * the Python package sunshape_mlx_amd binds them with ctypes.
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer owned by the caller (torch
+ *    tensors in the Python layer).  The library allocates no device memory.
+ *  - Calls are asynchronous on the given stream (a hipStream_t passed as
+ *    void*; NULL is the null stream).
+ *  - Return value: SS_OK (0) or a negative SS_ERR_* code.  The text of the
+ *    last error of the calling thread is returned by ss_last_error().
+ *    Argument and shape checks happen on the host before any launch.
+ *  - Stateless and reentrant, except that calls sharing one decode workspace
+ *    must not overlap (the workspace holds per-call split partials and the
+ *    split-completion counters).
+ *  - dtype codes: SS_F32, SS_F16, SS_BF16.
+ */
+#ifndef SUNSHAPE_HIP_H
+#define SUNSHAPE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SS_OK 0
+#define SS_ERR_INVALID (-1)     /* bad argument or shape */
+#define SS_ERR_UNSUPPORTED (-2) /* valid but not implemented for this shape */
+#define SS_ERR_HIP (-3)         /* HIP runtime error */
+#define SS_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+#define SS_F32 0
+#define SS_F16 1
+#define SS_BF16 2
+
+/* Library version string, e.g. "sunshape_hip 0.1.0 gfx950". */
+const char *ss_version(void);
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *ss_last_error(void);
+
+/*
+ * Block-VQ encode (key or value quantisation) into uint8 indices.
+ * Replaces block_vq_quantize_metal (reference kernels.py:1037-1082, kernel
+ * body kernels.py:995-1027) and the permutation of codec.py:435-436.
+ *
+ * Tokens are addressed as (b, h, t) with b < n_b, h < n_h, t < n_t; element j
+ * of token (b,h,t) is keys[b*k_sb + h*k_sh + t*k_st + j] (strides in
+ * elements of keys_dtype).  perm (int32[head_dim], may be NULL) gathers the
+ * key into codec space: kp[j] = key[perm[j]].  For every block the index of
+ * the nearest centroid (squared L2, ties -> lowest index; distances within
+ * 4e-6 relative of the best are re-resolved in float64) is written to
+ * out[b*o_sb + h*o_sh + t*o_st + blk] (strides in bytes).  Writing at
+ * o_st-strided rows of a cache buffer is the KV-append path.
+ *   centroids: float32 [n_blocks][n_centroids][block_dim], n_centroids <= 256.
+ */
+int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h,
+                      int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      int head_dim, const int32_t *perm, const float *centroids,
+                      int n_blocks, int n_centroids, int block_dim, uint8_t *out,
+                      int64_t o_sb, int64_t o_sh, int64_t o_st, void *stream);
+
+/*
+ * Query x centroid table  lut[r][b][c] = sum_d q'[r][b*bd+d] * C[b][c][d]
+ * with q'[r][j] = round_to(q_dtype, q[r][perm[j]] * scale).
+ * Replaces precompute_query_centroid_dots (reference codec.py:553-573; the
+ * einsum of attention.py:52-53).  q: [n_rows][head_dim] (row stride
+ * q_row_stride elements); lut: float32 [n_rows][n_blocks][n_centroids].
+ */
+int ss_build_lut(const void *q, int q_dtype, int64_t n_rows, int64_t q_row_stride,
+                 int head_dim, const int32_t *perm, float scale,
+                 const float *centroids, int n_blocks, int n_centroids,
+                 int block_dim, float *lut, void *stream);
+
+/*
+ * Score gather  scores[r][t] = sum_b lut[r][b][idx[t*idx_row_stride + b]].
+ * Replaces block_vq_score_metal (reference kernels.py:87-116, kernel body
+ * kernels.py:59-77).  idx: uint8, row stride in bytes; scores: float32
+ * [n_rows][n_tok] (row stride out_row_stride elements).
+ */
+int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centroids,
+                    const uint8_t *idx, int64_t n_tok, int64_t idx_row_stride,
+                    float *scores, int64_t out_row_stride, void *stream);
+
+/*
+ * Workspace bytes needed by ss_decode_attn_* for the given shape and split
+ * count (n_splits <= 0 selects the library's choice for the current device).
+ * The workspace must be zero-filled once before its first use; every call
+ * leaves its counters at zero again.
+ */
+size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
+                                 int64_t t_q, int head_dim, int64_t t_kv,
+                                 int n_splits);
+
+/* Split count the library would choose (n_splits <= 0 in the calls below). */
+int ss_decode_default_splits(int64_t batch, int n_q_heads, int n_kv_heads,
+                             int64_t t_q, int head_dim, int64_t t_kv);
+
+/*
+ * Fused GQA decode/prefill attention over block-VQ keys with dense values.
+ * Replaces fused_attention_metal / fused_attention_causal_metal (reference
+ * kernels.py:233-291, 388-446) driven per (b, kv head, q head) by
+ * sunshape_sdpa (attention.py:199-305): one launch serves every query head of
+ * every KV group.
+ *   q       [batch][n_q_heads][t_q][head_dim] contiguous, q_dtype
+ *           (query head hq reads KV head hq / (n_q_heads / n_kv_heads));
+ *           the kernel forms round_to(q_dtype, q * scale), then q[perm].
+ *   idx     uint8 [batch][n_kv_heads][cap][n_blocks] (first t_kv tokens used)
+ *   values  [batch][n_kv_heads][cap][head_dim], v_dtype (SS_F16/SS_BF16/SS_F32)
+ *   out     [batch][n_q_heads][t_q][head_dim], out_dtype
+ *   causal  query row i (0 <= i < t_q) attends to keys t <= q_offset + i.
+ * Softmax is accumulated in float32; rows with no admissible key output 0.
+ */
+int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                         int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                         const int32_t *perm, const float *centroids, int n_blocks,
+                         int n_centroids, const uint8_t *idx, const void *values,
+                         int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                         int64_t q_offset, void *out, int out_dtype, void *workspace,
+                         size_t workspace_bytes, int n_splits, void *stream);
+
+/*
+ * As ss_decode_attn_dense with grouped asymmetric-quantised values decoded in
+ * registers: v = ((w >> ((d % vpw) * bits)) & (2^bits - 1)) * scale + zero.
+ * Replaces fused_attention_dequant_metal / _causal_metal (reference
+ * kernels.py:697-765, 870-928).
+ *   packed  uint32 [batch][n_kv_heads][cap][packed_dim], vpw = 32 / bits
+ *           (2-bit: 16, 3-bit: 10, 4-bit: 8 values per word)
+ *   scales, zeros  [batch][n_kv_heads][cap][head_dim / group_size], sz_dtype
+ *                  (SS_F32 as the reference stores them, or SS_F16)
+ */
+int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                           int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                           const int32_t *perm, const float *centroids, int n_blocks,
+                           int n_centroids, const uint8_t *idx, const uint32_t *packed,
+                           const void *scales, const void *zeros, int sz_dtype,
+                           int bits, int group_size, int64_t cap, int64_t t_kv,
+                           int causal, int64_t q_offset, void *out, int out_dtype,
+                           void *workspace, size_t workspace_bytes, int n_splits,
+                           void *stream);
+
+/*
+ * Grouped asymmetric min-max quantisation of values (encode-on-append).
+ * Replaces quantize_values (reference kernels.py:1173-1228): per token and
+ * group, zero = min, scale = max((max - min) / (2^bits - 1), 1e-8),
+ * q = clip(rint((v - zero) / scale), 0, 2^bits - 1), packed as pack_indices.
+ * Token (b,h,t) reads values[b*v_sb + h*v_sh + t*v_st + j] (elements) and
+ * writes packed[(b*o_sb + h*o_sh + t*o_st)*packed_dim + w] and
+ * scales/zeros[(b*o_sb + h*o_sh + t*o_st)*n_groups + g] (token-row strides
+ * o_* counted in tokens).  Codes use the float32 scale/zero; they are stored
+ * in sz_dtype.
+ */
+int ss_quantize_values_grouped(const void *values, int v_dtype, int64_t n_b,
+                               int64_t n_h, int64_t n_t, int64_t v_sb, int64_t v_sh,
+                               int64_t v_st, int head_dim, int bits, int group_size,
+                               uint32_t *packed, void *scales, void *zeros,
+                               int sz_dtype, int64_t o_sb, int64_t o_sh,
+                               int64_t o_st, void *stream);
+
+/* v[t][d] = q * scale + zero (separate float32 multiply and add), out_dtype.
+ * Replaces dequantize_values (reference kernels.py:1231-1269).  Rows are
+ * contiguous: packed [n_tok][packed_dim], scales/zeros [n_tok][n_groups],
+ * out [n_tok][head_dim]. */
+int ss_dequantize_values_grouped(const uint32_t *packed, const void *scales,
+                                 const void *zeros, int sz_dtype, int64_t n_tok,
+                                 int head_dim, int bits, int group_size, void *out,
+                                 int out_dtype, void *stream);
+
+/* Bit packing of small codes into uint32 words (reference kernels.py:1102-1163).
+ * in: uint8 [n_rows][d]; out: uint32 [n_rows][packed_dim(d, bits)]. */
+int ss_pack_indices(const uint8_t *in, int64_t n_rows, int d, int bits, uint32_t *out,
+                    void *stream);
+/* out: uint32 [n_rows][d]. */
+int ss_unpack_indices(const uint32_t *in, int64_t n_rows, int d, int bits,
+                      uint32_t *out, void *stream);
+
+/* idx[i] = #{b : v[i] > boundaries[b]} as uint8 (reference kernels.py:453-507).
+ * values float32 [n]; boundaries float32 [n_boundaries] (device). */
+int ss_scalar_quantize(const float *values, int64_t n, const float *boundaries,
+                       int n_boundaries, uint8_t *out, void *stream);
+
+/* Block-VQ decode k_hat[t][inv_perm...]: out[t][j] = C[b][idx[t][b]][d] placed at
+ * codec position j = b*bd + d, then out_orig[t][i] = out[t][inv_perm[i]]
+ * (inv_perm may be NULL).  Replaces codec.dequantize (reference
+ * codec.py:516-543) and the key reconstruction of cache.py:211-240.
+ * idx uint8 row stride in bytes; out [n_tok][head_dim] out_dtype. */
+int ss_dequantize_blockvq(const uint8_t *idx, int64_t n_tok, int64_t idx_row_stride,
+                          const float *centroids, int n_blocks, int n_centroids,
+                          int block_dim, const int32_t *inv_perm, void *out,
+                          int out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUNSHAPE_HIP_H */

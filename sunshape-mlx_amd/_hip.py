@@ -1,0 +1,410 @@
+"""ctypes binding of ``libsunshape_hip.so`` (declared in ``include/sunshape_hip.h``).
+
+Every wrapper takes torch tensors that live on a ROCm device, passes their
+data pointers and the current HIP stream to the C ABI, and raises
+``SunShapeHIPError`` on a non-zero status.  There is no CPU fallback: if the
+library is missing or a tensor is not on the GPU the call raises.
+
+torch is imported before the library is loaded so that the library binds to
+the HIP runtime torch already loaded (both carry the SONAME libamdhip64.so.7).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsunshape_hip.so")
+
+SS_OK = 0
+SS_ERR_INVALID = -1
+SS_ERR_UNSUPPORTED = -2
+SS_ERR_HIP = -3
+SS_ERR_WORKSPACE = -4
+
+SS_F32, SS_F16, SS_BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: SS_F32, torch.float16: SS_F16, torch.bfloat16: SS_BF16}
+
+
+class SunShapeHIPError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[status {status}] {message}")
+        self.status = status
+
+
+class SunShapeUnsupported(SunShapeHIPError):
+    """Valid arguments the HIP kernels do not implement (status -2)."""
+
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); the order follows include/sunshape_hip.h
+_SIGNATURES = {
+    "ss_version": (ctypes.c_char_p, []),
+    "ss_last_error": (ctypes.c_char_p, []),
+    "ss_encode_blockvq": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                                 _c_void_p, _c_void_p, _int, _int, _int, _c_void_p, _i64, _i64,
+                                 _i64, _c_void_p]),
+    "ss_build_lut": (_int, [_c_void_p, _int, _i64, _i64, _int, _c_void_p, _f32, _c_void_p,
+                            _int, _int, _int, _c_void_p, _c_void_p]),
+    "ss_score_gather": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _i64, _i64, _c_void_p,
+                               _i64, _c_void_p]),
+    "ss_decode_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
+    "ss_decode_default_splits": (_int, [_i64, _int, _int, _i64, _int, _i64]),
+    "ss_decode_attn_dense": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                    _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
+                                    _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
+                                    _int, _c_void_p]),
+    "ss_decode_attn_grouped": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                      _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
+                                      _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
+                                      _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_quantize_values_grouped": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+                                          _int, _int, _int, _c_void_p, _c_void_p, _c_void_p, _int,
+                                          _i64, _i64, _i64, _c_void_p]),
+    "ss_dequantize_values_grouped": (_int, [_c_void_p, _c_void_p, _c_void_p, _int, _i64, _int,
+                                            _int, _int, _c_void_p, _int, _c_void_p]),
+    "ss_pack_indices": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _c_void_p]),
+    "ss_unpack_indices": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _c_void_p]),
+    "ss_scalar_quantize": (_int, [_c_void_p, _i64, _c_void_p, _int, _c_void_p, _c_void_p]),
+    "ss_dequantize_blockvq": (_int, [_c_void_p, _i64, _i64, _c_void_p, _int, _int, _int,
+                                     _c_void_p, _c_void_p, _int, _c_void_p]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load_library(path: str | None = None):
+    """Load (once) and return the ctypes handle.  Raises if the library is
+    missing: build it with ``__graft_entry__.build()``."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"libsunshape_hip.so not found at {p}; build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'` from the repo root")
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def version() -> str:
+    return load_library().ss_version().decode()
+
+
+def _raise(rc: int):
+    msg = load_library().ss_last_error().decode(errors="replace")
+    if rc == SS_ERR_UNSUPPORTED:
+        raise SunShapeUnsupported(rc, msg)
+    raise SunShapeHIPError(rc, msg)
+
+
+def check(rc: int) -> None:
+    if rc != SS_OK:
+        _raise(rc)
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt} (float32, float16, bfloat16)") from None
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ValueError(
+                "SunShape HIP kernels need tensors on a ROCm GPU device "
+                f"(got device {t.device}); there is no CPU fallback")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# --------------------------------------------------------------------------- #
+#  Decode workspace (zero-filled once; kernels leave the counters at zero)     #
+# --------------------------------------------------------------------------- #
+
+_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per (device, stream) scratch for split-T partials and counters.  Calls
+    on one stream are ordered, so they never overlap on the same buffer."""
+    if nbytes <= 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           stream_handle(device))
+    ws = _ws_cache.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws_cache[key] = ws
+    return ws
+
+
+# --------------------------------------------------------------------------- #
+#  Typed wrappers                                                              #
+# --------------------------------------------------------------------------- #
+
+
+def encode_blockvq(keys: torch.Tensor, perm: torch.Tensor | None, centroids: torch.Tensor,
+                   out: torch.Tensor, block_dim: int) -> torch.Tensor:
+    """Encode keys of shape (B, H, T, D) or (N, D) into ``out`` (same leading
+    shape, last dim n_blocks, uint8; may be a strided view into a cache)."""
+    require_gpu(keys, perm, centroids, out)
+    if centroids.dtype != torch.float32 or not centroids.is_contiguous():
+        raise ValueError("centroids must be contiguous float32 (n_blocks, n_centroids, block_dim)")
+    if out.dtype != torch.uint8:
+        raise ValueError("out must be uint8")
+    k4 = keys.reshape((1, 1) + tuple(keys.shape)) if keys.dim() == 2 else keys
+    o4 = out.reshape((1, 1) + tuple(out.shape)) if out.dim() == 2 else out
+    if k4.dim() != 4 or o4.dim() != 4:
+        raise ValueError("keys must be (N, D) or (B, H, T, D)")
+    if k4.stride(-1) != 1 or o4.stride(-1) != 1:
+        raise ValueError("keys and out must be contiguous in their last dimension")
+    nb, nc, bd = centroids.shape
+    b_, h_, t_, d = k4.shape
+    if tuple(o4.shape) != (b_, h_, t_, nb):
+        raise ValueError(f"out shape {tuple(out.shape)} does not match keys {tuple(keys.shape)}")
+    if perm is not None and (perm.dtype != torch.int32 or perm.numel() != d):
+        raise ValueError("perm must be int32 of length head_dim")
+    lib = load_library()
+    check(lib.ss_encode_blockvq(
+        ptr(k4), dtype_code(k4.dtype), b_, h_, t_, k4.stride(0), k4.stride(1), k4.stride(2), d,
+        ptr(perm), ptr(centroids), nb, nc, bd, ptr(o4), o4.stride(0), o4.stride(1),
+        o4.stride(2), stream_handle(keys.device)))
+    return out
+
+
+def build_lut(q: torch.Tensor, perm: torch.Tensor | None, scale: float,
+              centroids: torch.Tensor) -> torch.Tensor:
+    """(n_rows, D) queries -> (n_rows, n_blocks, n_centroids) float32 LUT."""
+    require_gpu(q, perm, centroids)
+    if q.dim() != 2 or q.stride(-1) != 1:
+        raise ValueError("q must be (n_rows, head_dim) with unit last stride")
+    nb, nc, bd = centroids.shape
+    lut = torch.empty((q.shape[0], nb, nc), dtype=torch.float32, device=q.device)
+    check(load_library().ss_build_lut(
+        ptr(q), dtype_code(q.dtype), q.shape[0], q.stride(0), q.shape[1], ptr(perm), float(scale),
+        ptr(centroids), nb, nc, bd, ptr(lut), stream_handle(q.device)))
+    return lut
+
+
+def score_gather(lut: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """lut (R, NB, NC) f32, idx (T, NB) uint8 -> scores (R, T) f32."""
+    require_gpu(lut, idx)
+    if idx.dtype != torch.uint8 or idx.dim() != 2 or idx.stride(-1) != 1:
+        raise ValueError("indices must be uint8 (T, n_blocks) with unit last stride")
+    lut = lut.contiguous().float()
+    r_, nb, nc = lut.shape
+    scores = torch.empty((r_, idx.shape[0]), dtype=torch.float32, device=lut.device)
+    check(load_library().ss_score_gather(
+        ptr(lut), r_, nb, nc, ptr(idx), idx.shape[0], idx.stride(0), ptr(scores), idx.shape[0],
+        stream_handle(lut.device)))
+    return scores
+
+
+def dequantize_blockvq(idx: torch.Tensor, centroids: torch.Tensor, inv_perm: torch.Tensor | None,
+                       out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """idx (T, NB) uint8 -> (T, D) reconstructed vectors in the original basis."""
+    require_gpu(idx, centroids, inv_perm)
+    if idx.dtype != torch.uint8 or idx.dim() != 2 or idx.stride(-1) != 1:
+        raise ValueError("indices must be uint8 (T, n_blocks) with unit last stride")
+    nb, nc, bd = centroids.shape
+    out = torch.empty((idx.shape[0], nb * bd), dtype=out_dtype, device=idx.device)
+    check(load_library().ss_dequantize_blockvq(
+        ptr(idx), idx.shape[0], idx.stride(0), ptr(centroids), nb, nc, bd, ptr(inv_perm), ptr(out),
+        dtype_code(out_dtype), stream_handle(idx.device)))
+    return out
+
+
+def decode_workspace_bytes(batch, n_q_heads, n_kv_heads, t_q, head_dim, t_kv, n_splits=0) -> int:
+    return int(load_library().ss_decode_workspace_bytes(batch, n_q_heads, n_kv_heads, t_q,
+                                                        head_dim, t_kv, n_splits))
+
+
+def default_splits(batch, n_q_heads, n_kv_heads, t_q, head_dim, t_kv) -> int:
+    return int(load_library().ss_decode_default_splits(batch, n_q_heads, n_kv_heads, t_q,
+                                                       head_dim, t_kv))
+
+
+def _check_decode_common(q, idx, centroids, perm):
+    require_gpu(q, idx, centroids, perm)
+    if q.dim() != 4 or not q.is_contiguous():
+        raise ValueError("queries must be contiguous (B, n_q_heads, T_q, D)")
+    if idx.dim() != 4 or idx.dtype != torch.uint8 or not idx.is_contiguous():
+        raise ValueError("key indices must be a contiguous uint8 (B, n_kv_heads, cap, n_blocks) buffer")
+    if centroids.dtype != torch.float32 or not centroids.is_contiguous():
+        raise ValueError("centroids must be contiguous float32")
+    if perm is not None and perm.dtype != torch.int32:
+        raise ValueError("perm must be int32")
+
+
+def decode_attn_dense(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                      centroids: torch.Tensor, idx: torch.Tensor, values: torch.Tensor,
+                      t_kv: int, causal: bool = False, q_offset: int = 0,
+                      out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                      n_splits: int = 0) -> torch.Tensor:
+    """Fused decode over a (B, Hkv, cap, NB) index buffer and (B, Hkv, cap, D)
+    dense values; returns (B, Hq, T_q, D)."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(values)
+    if values.dim() != 4 or not values.is_contiguous():
+        raise ValueError("values must be a contiguous (B, n_kv_heads, cap, D) buffer")
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if values.shape[:3] != idx.shape[:3] or values.shape[3] != d:
+        raise ValueError(f"values {tuple(values.shape)} do not match indices {tuple(idx.shape)}")
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
+    ws = decode_workspace(q.device, ws_bytes)
+    check(load_library().ss_decode_attn_dense(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        nb, nc, ptr(idx), ptr(values), dtype_code(values.dtype), cap, int(t_kv), int(bool(causal)),
+        int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
+        int(n_splits), stream_handle(q.device)))
+    return out
+
+
+def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                        centroids: torch.Tensor, idx: torch.Tensor, packed: torch.Tensor,
+                        scales: torch.Tensor, zeros: torch.Tensor, bits: int, group_size: int,
+                        t_kv: int, causal: bool = False, q_offset: int = 0,
+                        out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                        n_splits: int = 0) -> torch.Tensor:
+    """Fused decode with grouped-quantised values decoded in registers."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(packed, scales, zeros)
+    for name, t in (("packed", packed), ("scales", scales), ("zeros", zeros)):
+        if t.dim() != 4 or not t.is_contiguous() or t.shape[:3] != idx.shape[:3]:
+            raise ValueError(f"{name} must be a contiguous (B, n_kv_heads, cap, *) buffer")
+    if packed.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("packed values must be 32-bit words")
+    if scales.dtype != zeros.dtype or scales.dtype not in (torch.float32, torch.float16):
+        raise ValueError("scales/zeros must share dtype float32 or float16")
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
+    ws = decode_workspace(q.device, ws_bytes)
+    check(load_library().ss_decode_attn_grouped(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        nb, nc, ptr(idx), ptr(packed), ptr(scales), ptr(zeros), dtype_code(scales.dtype),
+        int(bits), int(group_size), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
+        dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
+        stream_handle(q.device)))
+    return out
+
+
+def quantize_values_grouped(values: torch.Tensor, bits: int, group_size: int,
+                            packed: torch.Tensor, scales: torch.Tensor,
+                            zeros: torch.Tensor) -> None:
+    """values (B, H, T, D) (or (T, D)) -> packed/scales/zeros views of matching
+    leading shape (token rows contiguous in their last dim)."""
+    require_gpu(values, packed, scales, zeros)
+    v4 = values.reshape((1, 1) + tuple(values.shape)) if values.dim() == 2 else values
+    outs = []
+    for t in (packed, scales, zeros):
+        t4 = t.reshape((1, 1) + tuple(t.shape)) if t.dim() == 2 else t
+        if t4.stride(-1) != 1:
+            raise ValueError("outputs must be contiguous in their last dimension")
+        outs.append(t4)
+    p4, s4, z4 = outs
+    if v4.stride(-1) != 1:
+        raise ValueError("values must be contiguous in their last dimension")
+    if s4.dtype != z4.dtype:
+        raise ValueError("scales and zeros must share a dtype")
+    b_, h_, t_, d = v4.shape
+    nw = p4.shape[-1]
+    ng = s4.shape[-1]
+    # token-row strides of the outputs, in tokens
+    o_sb, o_sh, o_st = p4.stride(0) // nw, p4.stride(1) // nw, p4.stride(2) // nw
+    if (s4.stride(0) // ng, s4.stride(1) // ng, s4.stride(2) // ng) != (o_sb, o_sh, o_st):
+        raise ValueError("packed and scales/zeros buffers must share the token layout")
+    check(load_library().ss_quantize_values_grouped(
+        ptr(v4), dtype_code(v4.dtype), b_, h_, t_, v4.stride(0), v4.stride(1), v4.stride(2), d,
+        int(bits), int(group_size), ptr(p4), ptr(s4), ptr(z4), dtype_code(s4.dtype), o_sb, o_sh,
+        o_st, stream_handle(values.device)))
+
+
+def dequantize_values_grouped(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+                              head_dim: int, bits: int, group_size: int,
+                              out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    require_gpu(packed, scales, zeros)
+    p2 = packed.reshape(-1, packed.shape[-1]).contiguous()
+    s2 = scales.reshape(-1, scales.shape[-1]).contiguous()
+    z2 = zeros.reshape(-1, zeros.shape[-1]).to(s2.dtype).contiguous()
+    n = p2.shape[0]
+    out = torch.empty((n, head_dim), dtype=out_dtype, device=packed.device)
+    check(load_library().ss_dequantize_values_grouped(
+        ptr(p2), ptr(s2), ptr(z2), dtype_code(s2.dtype), n, head_dim, int(bits), int(group_size),
+        ptr(out), dtype_code(out_dtype), stream_handle(packed.device)))
+    return out.reshape(tuple(packed.shape[:-1]) + (head_dim,))
+
+
+def pack_indices(indices: torch.Tensor, bits: int) -> torch.Tensor:
+    require_gpu(indices)
+    d = indices.shape[-1]
+    x = indices.reshape(-1, d).to(torch.uint8).contiguous()
+    vpw = 32 // bits
+    nw = (d + vpw - 1) // vpw
+    out = torch.empty((x.shape[0], nw), dtype=torch.int32, device=indices.device)
+    check(load_library().ss_pack_indices(ptr(x), x.shape[0], d, int(bits), ptr(out),
+                                         stream_handle(indices.device)))
+    return out.view(torch.uint32).reshape(tuple(indices.shape[:-1]) + (nw,))
+
+
+def unpack_indices(packed: torch.Tensor, d: int, bits: int) -> torch.Tensor:
+    require_gpu(packed)
+    nw = packed.shape[-1]
+    x = packed.reshape(-1, nw).contiguous()
+    out = torch.empty((x.shape[0], d), dtype=torch.int32, device=packed.device)
+    check(load_library().ss_unpack_indices(ptr(x), x.shape[0], int(d), int(bits), ptr(out),
+                                           stream_handle(packed.device)))
+    return out.view(torch.uint32).reshape(tuple(packed.shape[:-1]) + (d,))
+
+
+def scalar_quantize(values: torch.Tensor, boundaries: torch.Tensor) -> torch.Tensor:
+    require_gpu(values, boundaries)
+    v = values.reshape(-1).float().contiguous()
+    b = boundaries.reshape(-1).float().contiguous()
+    out = torch.empty(v.shape, dtype=torch.uint8, device=values.device)
+    check(load_library().ss_scalar_quantize(ptr(v), v.numel(), ptr(b), b.numel(), ptr(out),
+                                            stream_handle(values.device)))
+    return out.reshape(values.shape)

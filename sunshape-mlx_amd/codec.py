@@ -1,0 +1,383 @@
+"""SunShape block-VQ codec (keys -> uint8 centroid indices).
+
+Same API as the reference's ``SunShapeBlockCodec`` (gauravsaini/sunshape-mlx
+codec.py:217-650).  Codec state lives in torch tensors on one device; the
+per-step operations run on the HIP kernels:
+
+  quantize                    -> ss_encode_blockvq (permutation fused)
+  dequantize / __call__       -> ss_dequantize_blockvq
+  precompute_query_centroid_dots, attention_scores
+                              -> ss_build_lut + ss_score_gather
+
+``fit`` is offline calibration (ProfilePerm + per-block Lloyd k-means, DSQ
+refinement for the local-metric mode) and, like the reference's, runs in
+NumPy on the host.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import NamedTuple
+
+import numpy as np
+import torch
+
+from . import _hip
+from .rotation import (
+    apply_permutation,
+    block_affinity_gate,
+    block_local_cov_metric,
+    covariance_block_permutation,
+    generate_rotation_matrix,
+    invert_permutation,
+    mixed_precision_block_mask,
+)
+
+PERM_MODES = ("profileperm_baseline", "profileperm_localmetric_dsq", "profileperm_mixed_precision")
+MODES = PERM_MODES + ("rotated",)
+
+
+class SunShapeQuantized(NamedTuple):
+    """Quantized keys (reference codec.py:38-45)."""
+    indices: torch.Tensor  # (n_tokens, n_blocks) uint8
+    head_dim: int
+    block_dim: int
+    n_blocks: int
+    passthrough_blocks: torch.Tensor | None = None   # (n_blocks,) bool
+    passthrough_values: torch.Tensor | None = None   # (n_tokens, n_blocks, block_dim) f32
+
+
+def _compact_index_dtype(n_centroids: int) -> torch.dtype:
+    """Smallest dtype holding indices below n_centroids (codec.py:203-209)."""
+    if n_centroids <= 256:
+        return torch.uint8
+    if n_centroids <= 65535:
+        return torch.int32  # torch has no general uint16 arithmetic; indices fit
+    return torch.int64
+
+
+def _np(x) -> np.ndarray:
+    if isinstance(x, torch.Tensor):
+        return x.detach().float().cpu().numpy()
+    return np.asarray(x, dtype=np.float32)
+
+
+def _kmeans(data: np.ndarray, n_centroids: int, n_iters: int = 25, seed: int = 0) -> np.ndarray:
+    """Lloyd k-means (reference codec.py:53-103): zero-padded codebook when
+    N <= K; initial centroids are the rows ``RandomState(seed).permutation(N)[:K]``;
+    expanded-form float32 distances with first-index argmin; empty clusters
+    keep their previous centroid."""
+    x = np.asarray(data, dtype=np.float32)
+    n, d = x.shape
+    if n <= n_centroids:
+        out = np.zeros((n_centroids, d), dtype=np.float32)
+        out[:n] = x
+        return out
+    c = x[np.random.RandomState(seed).permutation(n)[:n_centroids]].copy()
+    x_sq = np.sum(x ** 2, axis=1, keepdims=True)
+    for _ in range(n_iters):
+        dist = x_sq + np.sum(c ** 2, axis=1, keepdims=True).T - 2.0 * x @ c.T
+        a = np.argmin(dist, axis=1)
+        sums = np.zeros_like(c)
+        np.add.at(sums, a, x)
+        cnt = np.bincount(a, minlength=n_centroids).astype(np.float64)
+        live = cnt > 0
+        sums[live] /= cnt[live, None]
+        sums[~live] = c[~live]
+        c = sums
+    return c.astype(np.float32)
+
+
+def _softmax(x: np.ndarray) -> np.ndarray:
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def _refine_centroids(q_cal, k_cal, centroids, e_metric, block_dim, n_steps=3, step_size=0.1,
+                      block_affinity=None, active_blocks=None) -> np.ndarray:
+    """DSQ attention-aware centroid refinement (reference codec.py:111-189):
+    gradient of (k_hat - k) + 0.5 * d(softmax error)/dk_hat on a calibration
+    subset, applied per assigned centroid with a per-block step."""
+    head_dim = k_cal.shape[-1]
+    nb = head_dim // block_dim
+    scale = math.sqrt(head_dim)
+    q = np.asarray(q_cal[:min(128, q_cal.shape[0])], np.float32)
+    k = np.asarray(k_cal[:min(1024, k_cal.shape[0])], np.float32)
+    e = np.asarray(e_metric, np.float32)
+    cents = np.array(centroids, np.float32, copy=True)
+    ba = np.ones(nb, np.float32) if block_affinity is None else np.asarray(block_affinity)
+    ab = np.ones(nb, bool) if active_blocks is None else np.asarray(active_blocks, bool)
+    nc = cents.shape[1]
+
+    def assign(b):
+        sl = slice(b * block_dim, (b + 1) * block_dim)
+        eb = e[sl, sl]
+        ks = k[:, sl] @ eb.T
+        cs = cents[b] @ eb.T
+        return np.argmin(((ks[:, None, :] - cs[None]) ** 2).sum(-1), axis=1)
+
+    k_hat = np.zeros_like(k)
+    for b in range(nb):
+        k_hat[:, b * block_dim:(b + 1) * block_dim] = cents[b][assign(b)]
+    for _ in range(n_steps):
+        p_orig = _softmax((q @ k.T) / scale)
+        p_hat = _softmax((q @ k_hat.T) / scale)
+        grad_attn = (((p_hat - p_orig) * p_hat * (1.0 - p_hat)).T @ q) / scale
+        total = (k_hat - k) + 0.5 * grad_attn
+        for b in range(nb):
+            if not ab[b]:
+                continue
+            sl = slice(b * block_dim, (b + 1) * block_dim)
+            a = assign(b)
+            cnt = np.bincount(a, minlength=nc)
+            gsum = np.zeros((nc, block_dim), np.float32)
+            np.add.at(gsum, a, total[:, sl])
+            live = cnt > 0
+            new = cents[b].copy()
+            new[live] -= step_size * float(ba[b]) * (gsum[live] / cnt[live, None])
+            cents[b] = new
+            k_hat[:, sl] = new[a]
+    return cents
+
+
+class SunShapeBlockCodec:
+    """Block vector quantisation codec (reference codec.py:217-650).
+
+    Modes: ``profileperm_baseline``, ``profileperm_localmetric_dsq``,
+    ``profileperm_mixed_precision``, ``rotated``.
+    """
+
+    def __init__(self, head_dim: int, block_dim: int = 8, n_centroids: int = 256, c: float = 5.0,
+                 n_refine_dsq: int = 3, mode: str = "profileperm_baseline",
+                 use_rotation: bool = False, rotation_seed: int = 0, device=None):
+        if head_dim % block_dim != 0:
+            raise ValueError("head_dim must be divisible by block_dim")
+        self.head_dim = head_dim
+        self.block_dim = block_dim
+        self.n_blocks = head_dim // block_dim
+        self.n_centroids = n_centroids
+        self.c = c
+        self.mode = "rotated" if use_rotation else mode
+        if self.mode not in MODES:
+            raise ValueError(f"Unknown SunShapeBlockCodec mode: {self.mode}")
+        self.n_refine_dsq = n_refine_dsq
+        self.use_rotation = self.mode == "rotated"
+        self.last_score_backend = "none"
+        if device is None:
+            device = "cuda" if torch.cuda.is_available() else "cpu"
+        self._device = torch.device(device)
+        d, nb = head_dim, self.n_blocks
+        rot = generate_rotation_matrix(d, seed=rotation_seed) if self.use_rotation \
+            else np.eye(d, dtype=np.float32)
+        self._set_state(
+            E=np.eye(d, dtype=np.float32), E_inv=np.eye(d, dtype=np.float32),
+            centroids=np.zeros((nb, n_centroids, block_dim), np.float32),
+            dsq_block_affinity=np.ones(nb, np.float32), dsq_active_blocks=np.ones(nb, bool),
+            mixed_high_precision_blocks=np.zeros(nb, bool),
+            mixed_block_mass=np.zeros(nb, np.float32),
+            permutation=np.arange(d, dtype=np.int32), rotation=rot)
+
+    # ---------------------------------------------------------------- state
+    _STATE_KEYS = ("E", "E_inv", "centroids", "dsq_block_affinity", "dsq_active_blocks",
+                   "mixed_high_precision_blocks", "mixed_block_mass", "permutation", "rotation")
+
+    def _set_state(self, **arrays):
+        for k, v in arrays.items():
+            t = v if isinstance(v, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(v))
+            setattr(self, k, t.to(self._device).contiguous())
+        if "permutation" in arrays:
+            self.permutation = self.permutation.to(torch.int32)
+            self.inv_permutation = invert_permutation(self.permutation)
+        self._shaped_centroids = None
+
+    @property
+    def device(self) -> torch.device:
+        return self._device
+
+    def to(self, device) -> "SunShapeBlockCodec":
+        self._device = torch.device(device)
+        self._set_state(**{k: getattr(self, k) for k in self._STATE_KEYS})
+        return self
+
+    def state_dict(self) -> dict:
+        """Codec state as CPU tensors plus the configuration (the reference
+        codec has no serialisation; this is the format ``load_state_dict``
+        reads)."""
+        sd = {k: getattr(self, k).detach().cpu() for k in self._STATE_KEYS}
+        sd["config"] = dict(head_dim=self.head_dim, block_dim=self.block_dim,
+                            n_centroids=self.n_centroids, mode=self.mode, c=self.c,
+                            n_refine_dsq=self.n_refine_dsq)
+        return sd
+
+    def load_state_dict(self, sd: dict) -> "SunShapeBlockCodec":
+        cfg = sd.get("config", {})
+        for k in ("head_dim", "block_dim", "n_centroids"):
+            if k in cfg and cfg[k] != getattr(self, k):
+                raise ValueError(f"state {k}={cfg[k]} does not match codec {getattr(self, k)}")
+        if "mode" in cfg:
+            self.mode = cfg["mode"]
+            self.use_rotation = self.mode == "rotated"
+        self._set_state(**{k: sd[k] for k in self._STATE_KEYS if k in sd})
+        return self
+
+    # ------------------------------------------------------------ transforms
+    def _forward_transform(self, x: torch.Tensor) -> torch.Tensor:
+        if self.mode in PERM_MODES:
+            return apply_permutation(x, self.permutation)
+        if self.use_rotation:
+            return x.float() @ self.rotation.T
+        return x
+
+    def _inverse_transform(self, x: torch.Tensor) -> torch.Tensor:
+        if self.mode in PERM_MODES:
+            return apply_permutation(x, self.inv_permutation)
+        if self.use_rotation:
+            return x.float() @ self.rotation
+        return x
+
+    def kernel_permutation(self) -> torch.Tensor | None:
+        """The permutation the kernels apply to raw queries/keys (None when the
+        codec transform is not a permutation)."""
+        return self.permutation if self.mode in PERM_MODES else None
+
+    # ------------------------------------------------------------------ fit
+    def fit(self, q_cal, k_cal, kmeans_iters: int = 25, seed: int = 0) -> "SunShapeBlockCodec":
+        """Fit from calibration queries/keys (reference codec.py:299-418)."""
+        q = _np(q_cal)
+        k = _np(k_cal)
+        d, bd, nb = self.head_dim, self.block_dim, self.n_blocks
+        eye = np.eye(d, dtype=np.float32)
+        E, E_inv = eye, eye
+        perm = np.arange(d, dtype=np.int32)
+        ba, ab = np.ones(nb, np.float32), np.ones(nb, bool)
+        heavy, bmass = np.zeros(nb, bool), np.zeros(nb, np.float32)
+        if self.mode == "rotated":
+            r = self.rotation.detach().cpu().numpy()
+            q, k = q @ r.T, k @ r.T
+        else:
+            perm = covariance_block_permutation(q, bd)
+            q, k = q[:, perm], k[:, perm]
+            if self.mode == "profileperm_localmetric_dsq":
+                E = block_local_cov_metric(q, np.arange(d), bd)
+                E_inv = np.linalg.pinv(E).astype(np.float32)
+                ba, ab = block_affinity_gate(q, bd)
+            elif self.mode == "profileperm_mixed_precision":
+                heavy, bmass = mixed_precision_block_mask(q, bd, mass_threshold=0.5)
+        cents = []
+        for b in range(nb):
+            sl = slice(b * bd, (b + 1) * bd)
+            if self.mode == "profileperm_mixed_precision" and heavy[b]:
+                cents.append(np.zeros((self.n_centroids, bd), np.float32))
+                continue
+            ks = k[:, sl] @ E[sl, sl].T
+            c = _kmeans(ks, self.n_centroids, n_iters=kmeans_iters, seed=seed + b)
+            cents.append((c @ E_inv[sl, sl].T).astype(np.float32))
+        working = np.stack(cents)
+        if self.mode not in ("profileperm_baseline", "rotated") and self.n_refine_dsq > 0:
+            working = _refine_centroids(q, k, working, E, bd, n_steps=self.n_refine_dsq,
+                                        block_affinity=ba, active_blocks=ab)
+        self._set_state(E=E, E_inv=E_inv, centroids=working.astype(np.float32),
+                        dsq_block_affinity=ba, dsq_active_blocks=ab,
+                        mixed_high_precision_blocks=heavy, mixed_block_mass=bmass,
+                        permutation=perm)
+        return self
+
+    # ------------------------------------------------------------- quantize
+    def _local_metric_blocks(self) -> torch.Tensor:
+        nb, bd = self.n_blocks, self.block_dim
+        e = self.E.reshape(nb, bd, nb, bd)
+        return torch.stack([e[b, :, b, :] for b in range(nb)])  # (nb, bd, bd)
+
+    def _encode_centroids(self) -> torch.Tensor:
+        if self.mode == "profileperm_localmetric_dsq":
+            if self._shaped_centroids is None:
+                eb = self._local_metric_blocks()
+                self._shaped_centroids = torch.einsum(
+                    "bcd,bed->bce", self.centroids, eb).contiguous()
+            return self._shaped_centroids
+        return self.centroids
+
+    def quantize(self, keys: torch.Tensor) -> SunShapeQuantized:
+        """(N, head_dim) keys -> uint8 indices (N, n_blocks) (codec.py:424-514).
+        Ties resolve to the lowest index.  Mixed-precision heavy blocks keep
+        index 0 and carry the transformed key block in ``passthrough_values``."""
+        _hip.require_gpu(keys)
+        if self.n_centroids > 256:
+            raise NotImplementedError("HIP encoder stores uint8 indices (n_centroids <= 256)")
+        keys = keys.reshape(-1, self.head_dim)
+        n = keys.shape[0]
+        out = torch.empty((n, self.n_blocks), dtype=torch.uint8, device=keys.device)
+        if self.mode == "profileperm_baseline":
+            _hip.encode_blockvq(keys if keys.stride(-1) == 1 else keys.contiguous(),
+                                self.permutation, self.centroids, out, self.block_dim)
+        else:
+            kt = self._forward_transform(keys.float())
+            if self.mode == "profileperm_localmetric_dsq":
+                kt = torch.einsum("nbd,bed->nbe", kt.reshape(n, self.n_blocks, self.block_dim),
+                                  self._local_metric_blocks()).reshape(n, self.head_dim)
+            _hip.encode_blockvq(kt.contiguous(), None, self._encode_centroids(), out,
+                                self.block_dim)
+        passthrough_blocks = passthrough_values = None
+        if self.mode == "profileperm_mixed_precision":
+            passthrough_blocks = self.mixed_high_precision_blocks
+            if bool(passthrough_blocks.any()):
+                kt = self._forward_transform(keys.float()).reshape(n, self.n_blocks,
+                                                                   self.block_dim)
+                passthrough_values = kt * passthrough_blocks.reshape(1, -1, 1).float()
+                out[:, passthrough_blocks] = 0
+        return SunShapeQuantized(out, self.head_dim, self.block_dim, self.n_blocks,
+                                 passthrough_blocks, passthrough_values)
+
+    def dequantize(self, quantized: SunShapeQuantized) -> torch.Tensor:
+        """Reconstructed keys (N, head_dim) float32 (codec.py:516-543)."""
+        idx = quantized.indices.to(torch.uint8).contiguous()
+        inv = self.inv_permutation if (self.mode in PERM_MODES
+                                       and quantized.passthrough_values is None) else None
+        k_hat = _hip.dequantize_blockvq(idx, self.centroids, inv)
+        if inv is not None:
+            return k_hat
+        if quantized.passthrough_blocks is not None and quantized.passthrough_values is not None:
+            n = k_hat.shape[0]
+            kb = k_hat.reshape(n, self.n_blocks, self.block_dim)
+            heavy = quantized.passthrough_blocks.to(kb.device)
+            kb[:, heavy] = quantized.passthrough_values[:, heavy].to(kb.dtype)
+            k_hat = kb.reshape(n, self.head_dim)
+        elif quantized.passthrough_blocks is not None and bool(quantized.passthrough_blocks.any()):
+            raise ValueError("Mixed-precision missing passthrough values.")
+        return self._inverse_transform(k_hat)
+
+    def __call__(self, keys: torch.Tensor) -> torch.Tensor:
+        return self.dequantize(self.quantize(keys))
+
+    # -------------------------------------------------------------- scores
+    def precompute_query_centroid_dots(self, query: torch.Tensor) -> torch.Tensor:
+        """LUT (n_qh, n_blocks, n_centroids) for queries already in codec
+        space (codec.py:553-573)."""
+        _hip.require_gpu(query)
+        q = query.reshape(-1, self.head_dim)
+        return _hip.build_lut(q if q.stride(-1) == 1 else q.contiguous(), None, 1.0,
+                              self.centroids)
+
+    def attention_scores(self, query: torch.Tensor, quantized: SunShapeQuantized, *,
+                         prefer_metal: bool = True) -> torch.Tensor:
+        """Unscaled scores (n_qh, n_tokens) = q . k_hat via the query x centroid
+        table (codec.py:575-637).  Mixed-precision heavy blocks contribute 0,
+        as in the reference (their centroids are zero and the passthrough is
+        not read).  ``prefer_metal`` is accepted for signature compatibility."""
+        _hip.require_gpu(query)
+        q = query.reshape(-1, self.head_dim).float()
+        if self.mode in PERM_MODES:
+            lut = _hip.build_lut(q.contiguous(), self.permutation, 1.0, self.centroids)
+        else:
+            lut = _hip.build_lut(self._forward_transform(q).contiguous(), None, 1.0,
+                                 self.centroids)
+        scores = _hip.score_gather(lut, quantized.indices.to(torch.uint8).contiguous())
+        self.last_score_backend = "hip"
+        return scores
+
+    def heldout_logit_mse(self, q_test: torch.Tensor, k_test: torch.Tensor) -> float:
+        """E[(q . (k - k_hat))^2] (codec.py:639-650)."""
+        q = q_test.float()
+        k = k_test.float()
+        delta = k - self(k)
+        return float(((q * delta).sum(dim=1) ** 2).mean().item())

@@ -1,0 +1,700 @@
+// Fused GQA decode/prefill attention over block-VQ key indices.
+//
+// One launch computes every query row of every (batch, KV head) group:
+//   score[r][t] = sum_b LUT[r][b][idx[t][b]],  out[r] = softmax_t(score[r]) . V
+// where LUT[r][b][c] = q'[r][b*8:(b+1)*8] . C[b][c] is built in LDS by every
+// workgroup from the (scaled, rounded, permuted) query rows and the fp32
+// codebook.  Semantics follow the reference's fused Metal kernels
+// (kernels.py:142-223 and 303-378 for dense V, 588-687 and 772-860 for
+// grouped V; per-head dispatch in attention.py:268-305), reorganised for
+// CDNA4:
+//   * grid.y = (batch, KV head, row group of R query rows): the R rows of one
+//     GQA group share one pass over that head's indices and values, so K and
+//     V are streamed once per KV head instead of once per query head;
+//   * grid.x = split of the token axis ("flash-decoding"); each wave owns
+//     64-token tiles: lane i gathers the 16 LUT entries of token i from LDS,
+//     the tile's softmax is updated with wave reductions, and the value pass
+//     maps 16-byte value loads to lanes (lanes-per-token = head_dim / dims-
+//     per-lane);
+//   * splits are merged by the last workgroup of each group to finish
+//     (agent-scope release/acquire around one atomic counter), so a decode
+//     step is a single kernel launch.
+// Softmax runs in log2 units (LUT pre-multiplied by log2 e, exp2 on the
+// hardware exp unit), accumulating in float32.
+#include "ss_common.hpp"
+
+namespace ss {
+
+struct DecodeCommon {
+    const void *q;
+    const int32_t *perm;
+    const float *centroids;
+    const uint8_t *idx;
+    void *out;
+    float *partials;
+    unsigned int *counters;
+    int q_dtype, out_dtype;
+    int n_q_heads, n_kv_heads, rep, n_rg;
+    int64_t t_q, rows_total;
+    int n_centroids;
+    int64_t cap, t_kv;
+    float scale;
+    int causal;
+    int64_t q_offset;
+    int n_splits, tiles_per_split;
+};
+
+constexpr int kDecodeThreads = 256;
+constexpr int kDecodeWaves = kDecodeThreads / kWave;
+constexpr int kLutStride = 256;  // LUT entries reserved per (row, block)
+constexpr int kBlockDim = 8;
+
+constexpr int pow2_ceil(int x) { return x <= 1 ? 1 : 2 * pow2_ceil((x + 1) / 2); }
+
+// ---------------------------------------------------------------------------
+// Value formats.  Each lane of a token group holds DPL consecutive dims.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void unpack16(const uint4 &u, float *x);
+
+template <>
+__device__ __forceinline__ void unpack16<__half>(const uint4 &u, float *x) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        __half2 h = *reinterpret_cast<const __half2 *>(&w[i]);
+        float2 f = __half22float2(h);
+        x[2 * i] = f.x;
+        x[2 * i + 1] = f.y;
+    }
+}
+
+template <>
+__device__ __forceinline__ void unpack16<__hip_bfloat16>(const uint4 &u, float *x) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+template <>
+__device__ __forceinline__ void unpack16<float>(const uint4 &u, float *x) {
+    x[0] = __uint_as_float(u.x);
+    x[1] = __uint_as_float(u.y);
+    x[2] = __uint_as_float(u.z);
+    x[3] = __uint_as_float(u.w);
+}
+
+template <int D, typename T>
+struct VDense {
+    static constexpr int DPL = 16 / (int)sizeof(T);
+    static constexpr int LPT = D / DPL;
+    static constexpr int TPI = kWave / LPT;
+    static constexpr int ITERS = kWave / TPI;
+    struct Args {
+        const T *v;
+    };
+    struct Raw {
+        uint4 u;
+    };
+    __device__ static __forceinline__ Raw load(const Args &a, int64_t row, int lt, bool ok) {
+        Raw r;
+        r.u = ok ? *reinterpret_cast<const uint4 *>(a.v + row * D + lt * DPL)
+                 : make_uint4(0u, 0u, 0u, 0u);
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Args &, const Raw &r, int, float *x) {
+        unpack16<T>(r.u, x);
+    }
+};
+
+template <int D, int BITS, typename SZ>
+struct VGrouped {
+    static constexpr int VPW = 32 / BITS;
+    static constexpr int NW = (D + VPW - 1) / VPW;
+    static constexpr int DPL = VPW;
+    static constexpr int LPT = pow2_ceil(NW);
+    static constexpr int TPI = kWave / LPT;
+    static constexpr int ITERS = kWave / TPI;
+    static_assert(LPT <= kWave, "packed row too wide");
+    struct Args {
+        const uint32_t *packed;
+        const SZ *scales;
+        const SZ *zeros;
+        int group;
+        int n_groups;
+    };
+    struct Raw {
+        uint32_t w;
+        float s0, z0, s1, z1;
+    };
+    __device__ static __forceinline__ float ld(const SZ *p, int64_t i) {
+        if constexpr (sizeof(SZ) == 4)
+            return p[i];
+        else
+            return __half2float(p[i]);
+    }
+    __device__ static __forceinline__ Raw load(const Args &a, int64_t row, int lt, bool ok) {
+        Raw r{0u, 0.f, 0.f, 0.f, 0.f};
+        if (ok && lt < NW) {
+            r.w = a.packed[row * NW + lt];
+            const int d0 = lt * VPW;
+            const int d1 = min(d0 + VPW - 1, D - 1);
+            const int g0 = d0 / a.group, g1 = d1 / a.group;
+            const int64_t sb = row * a.n_groups;
+            r.s0 = ld(a.scales, sb + g0);
+            r.z0 = ld(a.zeros, sb + g0);
+            r.s1 = ld(a.scales, sb + g1);
+            r.z1 = ld(a.zeros, sb + g1);
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Args &a, const Raw &r, int lt, float *x) {
+        const int d0 = lt * VPW;
+        const int g0 = d0 / a.group;
+#pragma unroll
+        for (int k = 0; k < VPW; ++k) {
+            const float qv = (float)((r.w >> (k * BITS)) & ((1u << BITS) - 1u));
+            const bool hi = ((d0 + k) / a.group) != g0;
+            x[k] = fmaf(qv, hi ? r.s1 : r.s0, hi ? r.z1 : r.z0);
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Index rows: NB bytes per token (16 for head_dim 128, 8 for 64).
+// ---------------------------------------------------------------------------
+template <int NB>
+struct IdxRow {
+    uint32_t w[NB / 4];
+    __device__ __forceinline__ void load(const uint8_t *p, bool ok) {
+        if constexpr (NB == 16) {
+            uint4 u = ok ? *reinterpret_cast<const uint4 *>(p) : make_uint4(0u, 0u, 0u, 0u);
+            w[0] = u.x;
+            w[1] = u.y;
+            w[2] = u.z;
+            w[3] = u.w;
+        } else {
+            static_assert(NB == 8, "unsupported block count");
+            uint2 u = ok ? *reinterpret_cast<const uint2 *>(p) : make_uint2(0u, 0u);
+            w[0] = u.x;
+            w[1] = u.y;
+        }
+    }
+    __device__ __forceinline__ uint32_t at(int b) const {
+        return (w[b >> 2] >> ((b & 3) * 8)) & 0xffu;
+    }
+};
+
+template <int D, int R>
+constexpr size_t decode_lds_bytes() {
+    return sizeof(float) * ((size_t)R * (D / kBlockDim) * kLutStride + (size_t)R * D +
+                            (size_t)kDecodeWaves * kWave * R);
+}
+
+template <int D, int R, class VF>
+__global__ void __launch_bounds__(kDecodeThreads)
+    decode_attn_kernel(DecodeCommon c, typename VF::Args va) {
+    constexpr int NB = D / kBlockDim;
+    constexpr int DPL = VF::DPL, LPT = VF::LPT, TPI = VF::TPI, ITERS = VF::ITERS;
+    constexpr int CHUNK = ITERS < 16 ? ITERS : 16;
+    static_assert(ITERS % CHUNK == 0, "chunking");
+    static_assert(kDecodeWaves * R * (D + 2) <= R * NB * kLutStride, "merge scratch");
+
+    extern __shared__ __align__(16) float smem[];
+    float *lut = smem;                          // [R][NB][kLutStride]
+    float *qp = lut + R * NB * kLutStride;      // [R][D]
+    float *pbuf = qp + R * D;                   // [waves][64][R]
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid >> 6;
+    const int col = blockIdx.y;
+    const int split = blockIdx.x;
+    const int rg = col % c.n_rg;
+    const int kvh = (col / c.n_rg) % c.n_kv_heads;
+    const int64_t bb = col / (c.n_rg * c.n_kv_heads);
+    const int64_t bh = bb * c.n_kv_heads + kvh;
+
+    // Row r of this group: global row g = rg*R + r = rr*t_q + tq, query head
+    // kvh*rep + rr (attention.py:220 reshape (B, Hkv, rep, Tq, D)).
+    auto row_off = [&](int r) -> int64_t {
+        const int64_t g = (int64_t)rg * R + r;
+        const int64_t rr = g / c.t_q, tq = g - rr * c.t_q;
+        return ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+    };
+    auto row_ok = [&](int r) -> bool { return (int64_t)rg * R + r < c.rows_total; };
+
+    // 1. query rows: round_to(q_dtype, q * scale) (attention.py:208), then
+    //    the codec permutation (attention.py:228).
+    for (int i = tid; i < R * D; i += kDecodeThreads) {
+        const int r = i / D, j = i - r * D;
+        float x = 0.f;
+        if (row_ok(r)) {
+            const int src = c.perm ? c.perm[j] : j;
+            x = round_to(c.q_dtype, load_as_f32(c.q, c.q_dtype, row_off(r) + src) * c.scale);
+        }
+        qp[i] = x;
+    }
+    __syncthreads();
+
+    // 2. LUT[r][b][c] = q'[r][b-block] . C[b][c] (kernels.py:178-190), in
+    //    log2 units.
+    const int nbc = NB * c.n_centroids;
+    for (int e = tid; e < nbc; e += kDecodeThreads) {
+        const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
+        const float4 *cp = reinterpret_cast<const float4 *>(c.centroids + (int64_t)e * kBlockDim);
+        const float4 c0 = cp[0], c1 = cp[1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float *qr = qp + r * D + b * kBlockDim;
+            float dot = qr[0] * c0.x;
+            dot = fmaf(qr[1], c0.y, dot);
+            dot = fmaf(qr[2], c0.z, dot);
+            dot = fmaf(qr[3], c0.w, dot);
+            dot = fmaf(qr[4], c1.x, dot);
+            dot = fmaf(qr[5], c1.y, dot);
+            dot = fmaf(qr[6], c1.z, dot);
+            dot = fmaf(qr[7], c1.w, dot);
+            lut[(r * NB + b) * kLutStride + cc] = dot * kLog2e;
+        }
+    }
+    __syncthreads();
+
+    // 3. stream this split's tokens, 64 per wave-tile.
+    const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
+    const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
+    const int n_tiles = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
+    const uint8_t *idx_head = c.idx + bh * c.cap * NB;
+    const int64_t vrow0 = bh * c.cap;
+    const int lt = lane % LPT, tg = lane / LPT;
+
+    int64_t lim[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t g = (int64_t)rg * R + r;
+        if (!row_ok(r))
+            lim[r] = -1;
+        else if (c.causal)
+            lim[r] = c.q_offset + (g % c.t_q);
+        else
+            lim[r] = INT64_MAX;
+    }
+
+    float m[R], l[R], acc[R][DPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -1e30f;
+        l[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) acc[r][k] = 0.f;
+    }
+    float *pw = pbuf + wv * kWave * R;
+
+    for (int tile = wv; tile < n_tiles; tile += kDecodeWaves) {
+        const int64_t t0 = t_beg + (int64_t)tile * kWave;
+        typename VF::Raw vr[CHUNK];
+#pragma unroll
+        for (int j = 0; j < CHUNK; ++j) {
+            const int64_t tv = t0 + j * TPI + tg;
+            vr[j] = VF::load(va, vrow0 + tv, lt, tv < t_end);
+        }
+        const int64_t tk = t0 + lane;
+        const bool kok = tk < t_end;
+        IdxRow<NB> ir;
+        ir.load(idx_head + tk * NB, kok);
+
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float *lr = lut + r * NB * kLutStride;
+            float a = 0.f;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) a += lr[b * kLutStride + ir.at(b)];
+            s[r] = (kok && tk <= lim[r]) ? a : -INFINITY;
+        }
+        float corr[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float mn = fmaxf(m[r], wave_max(s[r]));
+            corr[r] = fast_exp2(m[r] - mn);
+            const float p = fast_exp2(s[r] - mn);
+            l[r] = fmaf(l[r], corr[r], p);
+            m[r] = mn;
+            s[r] = p;
+        }
+        if constexpr (R == 4) {
+            *reinterpret_cast<float4 *>(pw + lane * 4) = make_float4(s[0], s[1], s[2], s[3]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) pw[lane * R + r] = s[r];
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) acc[r][k] *= corr[r];
+
+#pragma unroll
+        for (int ch = 0; ch < ITERS; ch += CHUNK) {
+            if (ch > 0) {
+#pragma unroll
+                for (int j = 0; j < CHUNK; ++j) {
+                    const int64_t tv = t0 + (ch + j) * TPI + tg;
+                    vr[j] = VF::load(va, vrow0 + tv, lt, tv < t_end);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < CHUNK; ++j) {
+                const int tl = (ch + j) * TPI + tg;
+                float pr[R];
+                if constexpr (R == 4) {
+                    const float4 p4 = *reinterpret_cast<const float4 *>(pw + tl * 4);
+                    pr[0] = p4.x;
+                    pr[1] = p4.y;
+                    pr[2] = p4.z;
+                    pr[3] = p4.w;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) pr[r] = pw[tl * R + r];
+                }
+                float x[DPL];
+                VF::decode(va, vr[j], lt, x);
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int k = 0; k < DPL; ++k) acc[r][k] = fmaf(pr[r], x[k], acc[r][k]);
+            }
+        }
+        wave_lds_sync();
+    }
+
+    // 4. reduce the wave: token groups (lanes sharing lt), then l over lanes.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) {
+            float v = acc[r][k];
+#pragma unroll
+            for (int o = LPT; o < kWave; o <<= 1) v += __shfl_xor(v, o);
+            acc[r][k] = v;
+        }
+        l[r] = wave_sum(l[r]);
+    }
+    __syncthreads();  // every wave is done with the LUT; reuse it
+    float *wm = smem;                        // [waves][R]
+    float *wl = wm + kDecodeWaves * R;       // [waves][R]
+    float *wa = wl + kDecodeWaves * R;       // [waves][R][D]
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wm[wv * R + r] = m[r];
+            wl[wv * R + r] = l[r];
+        }
+    }
+    if (tg == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) {
+                const int d = lt * DPL + k;
+                if (d < D) wa[(wv * R + r) * D + d] = acc[r][k];
+            }
+    }
+    __syncthreads();
+
+    const int S = c.n_splits;
+    for (int i = tid; i < R * D; i += kDecodeThreads) {
+        const int r = i / D, d = i - r * D;
+        float M = -1e30f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, wm[w * R + r]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float f = fast_exp2(wm[w * R + r] - M);
+            L = fmaf(wl[w * R + r], f, L);
+            A = fmaf(wa[(w * R + r) * D + d], f, A);
+        }
+        if (S == 1) {
+            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+        } else {
+            float *pp = c.partials + (((int64_t)col * S + split) * R + r) * (D + 2);
+            if (d == 0) {
+                pp[0] = M;
+                pp[1] = L;
+            }
+            pp[2 + d] = A;
+        }
+    }
+    if (S == 1) return;
+
+    // 5. the last workgroup of this group to finish merges all splits.
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = (atomicAdd(&c.counters[col], 1u) == (unsigned)(S - 1));
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    const int64_t sstride = (int64_t)R * (D + 2);
+    for (int i = tid; i < R * D; i += kDecodeThreads) {
+        const int r = i / D, d = i - r * D;
+        if (!row_ok(r)) continue;
+        const float *base = c.partials + ((int64_t)col * S * R + r) * (D + 2);
+        float M = -1e30f;
+        for (int s2 = 0; s2 < S; ++s2) M = fmaxf(M, base[s2 * sstride]);
+        float L = 0.f, A = 0.f;
+        for (int s2 = 0; s2 < S; ++s2) {
+            const float *pp = base + s2 * sstride;
+            const float f = fast_exp2(pp[0] - M);
+            L = fmaf(pp[1], f, L);
+            A = fmaf(pp[2 + d], f, A);
+        }
+        store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+    }
+    if (tid == 0) c.counters[col] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct DecodeShape {
+    int R, n_rg, n_cols, S, tiles_per_split;
+};
+
+static int rows_per_group(int64_t rows_total) { return rows_total <= 1 ? 1 : 4; }
+
+static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int64_t t_kv,
+                                int n_splits) {
+    DecodeShape s;
+    const int64_t rows = (int64_t)(hq / hkv) * t_q;
+    s.R = rows_per_group(rows);
+    s.n_rg = (int)((rows + s.R - 1) / s.R);
+    s.n_cols = (int)(batch * hkv * s.n_rg);
+    const int64_t tiles = (t_kv + kWave - 1) / kWave;
+    int S = n_splits;
+    if (S <= 0) {
+        // ~2 workgroups per compute unit, each with at least one tile per wave
+        const int64_t target = 2LL * device_cu_count();
+        int64_t want = (target + s.n_cols - 1) / s.n_cols;
+        const int64_t cap = tiles / kDecodeWaves;
+        if (want > cap) want = cap;
+        S = (int)(want < 1 ? 1 : want);
+    }
+    if (tiles == 0) S = 1;
+    if (S > tiles && tiles > 0) S = (int)tiles;
+    s.tiles_per_split = tiles > 0 ? (int)((tiles + S - 1) / S) : 0;
+    if (s.tiles_per_split > 0) S = (int)((tiles + s.tiles_per_split - 1) / s.tiles_per_split);
+    s.S = S;
+    return s;
+}
+
+static size_t decode_ws_bytes(const DecodeShape &s, int head_dim) {
+    if (s.S <= 1) return 0;
+    const size_t counters = ((size_t)s.n_cols * sizeof(unsigned) + 255) / 256 * 256;
+    return counters + (size_t)s.n_cols * s.S * s.R * (head_dim + 2) * sizeof(float);
+}
+
+template <int D, int R, class VF>
+static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
+                  hipStream_t st) {
+    const size_t lds = decode_lds_bytes<D, R>();
+    auto kern = decode_attn_kernel<D, R, VF>;
+    static bool attr_set = false;  // per instantiation
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode)");
+        attr_set = true;
+    }
+    dim3 grid(s.S, s.n_cols);
+    hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), lds, st, c, va);
+    SS_LAUNCH_CHECK("decode_attn_kernel launch");
+    return SS_OK;
+}
+
+template <int D, class VF>
+static int launch_r(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
+                    hipStream_t st) {
+    if (s.R == 1) return launch<D, 1, VF>(c, va, s, st);
+    return launch<D, 4, VF>(c, va, s, st);
+}
+
+static int check_common(const void *q, int q_dtype, int64_t batch, int hq, int hkv, int64_t t_q,
+                        int head_dim, const float *centroids, int n_blocks, int n_centroids,
+                        const uint8_t *idx, int64_t cap, int64_t t_kv, void *out, int out_dtype) {
+    SS_REQUIRE(q && centroids && idx && out, "null pointer argument");
+    SS_REQUIRE(valid_dtype(q_dtype) && valid_dtype(out_dtype), "bad dtype code");
+    SS_REQUIRE(batch >= 1 && hq >= 1 && hkv >= 1 && t_q >= 1, "empty batch/heads/t_q");
+    SS_REQUIRE(hq % hkv == 0, "n_q_heads (%d) must be a multiple of n_kv_heads (%d)", hq, hkv);
+    SS_UNSUPPORTED(head_dim == 64 || head_dim == 128,
+                   "head_dim %d unsupported (64 or 128)", head_dim);
+    SS_UNSUPPORTED(n_blocks * kBlockDim == head_dim,
+                   "fused kernel needs block_dim 8 (n_blocks %d, head_dim %d)", n_blocks, head_dim);
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256,
+                   "n_centroids %d unsupported (1..256, uint8 indices)", n_centroids);
+    SS_REQUIRE(t_kv >= 0 && t_kv <= cap, "t_kv %lld outside [0, cap=%lld]", (long long)t_kv,
+               (long long)cap);
+    SS_REQUIRE(((uintptr_t)idx % 16) == 0, "idx must be 16-byte aligned");
+    SS_REQUIRE(((uintptr_t)centroids % 16) == 0, "centroids must be 16-byte aligned");
+    return SS_OK;
+}
+
+static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int q_dtype,
+                       int hq, int hkv, int64_t t_q, float scale, const int32_t *perm,
+                       const float *centroids, int n_centroids, const uint8_t *idx, int64_t cap,
+                       int64_t t_kv, int causal, int64_t q_offset, void *out, int out_dtype,
+                       void *ws, size_t ws_bytes, int head_dim) {
+    c.q = q;
+    c.perm = perm;
+    c.centroids = centroids;
+    c.idx = idx;
+    c.out = out;
+    c.q_dtype = q_dtype;
+    c.out_dtype = out_dtype;
+    c.n_q_heads = hq;
+    c.n_kv_heads = hkv;
+    c.rep = hq / hkv;
+    c.n_rg = s.n_rg;
+    c.t_q = t_q;
+    c.rows_total = (int64_t)c.rep * t_q;
+    c.n_centroids = n_centroids;
+    c.cap = cap;
+    c.t_kv = t_kv;
+    c.scale = scale;
+    c.causal = causal ? 1 : 0;
+    c.q_offset = q_offset;
+    c.n_splits = s.S;
+    c.tiles_per_split = s.tiles_per_split;
+    c.partials = nullptr;
+    c.counters = nullptr;
+    if (s.S > 1) {
+        const size_t need = decode_ws_bytes(s, head_dim);
+        if (!ws || ws_bytes < need) {
+            set_error("decode workspace too small: need %zu bytes, got %zu", need,
+                      ws ? ws_bytes : (size_t)0);
+            return SS_ERR_WORKSPACE;
+        }
+        SS_REQUIRE(((uintptr_t)ws % 256) == 0, "workspace must be 256-byte aligned");
+        c.counters = reinterpret_cast<unsigned *>(ws);
+        const size_t cbytes = ((size_t)s.n_cols * sizeof(unsigned) + 255) / 256 * 256;
+        c.partials = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
+    }
+    return SS_OK;
+}
+
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
+                                            int64_t t_q, int head_dim, int64_t t_kv,
+                                            int n_splits) {
+    if (batch < 1 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads || t_q < 1)
+        return 0;
+    return decode_ws_bytes(decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits),
+                           head_dim);
+}
+
+extern "C" int ss_decode_default_splits(int64_t batch, int n_q_heads, int n_kv_heads,
+                                        int64_t t_q, int head_dim, int64_t t_kv) {
+    (void)head_dim;
+    if (batch < 1 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads || t_q < 1)
+        return 0;
+    return decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, 0).S;
+}
+
+extern "C" int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                    int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                    const int32_t *perm, const float *centroids, int n_blocks,
+                                    int n_centroids, const uint8_t *idx, const void *values,
+                                    int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                    int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                    size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(values, "null values");
+    SS_REQUIRE(valid_dtype(v_dtype), "bad value dtype");
+    SS_REQUIRE(((uintptr_t)values % 16) == 0, "values must be 16-byte aligned");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define SS_DENSE(DD, TT)                                                                  \
+    {                                                                                     \
+        typename VDense<DD, TT>::Args va{reinterpret_cast<const TT *>(values)};           \
+        return launch_r<DD, VDense<DD, TT>>(c, va, s, st);                                \
+    }
+    if (head_dim == 128) {
+        if (v_dtype == SS_F16) SS_DENSE(128, __half)
+        if (v_dtype == SS_BF16) SS_DENSE(128, __hip_bfloat16)
+        SS_DENSE(128, float)
+    } else {
+        if (v_dtype == SS_F16) SS_DENSE(64, __half)
+        if (v_dtype == SS_BF16) SS_DENSE(64, __hip_bfloat16)
+        SS_DENSE(64, float)
+    }
+#undef SS_DENSE
+}
+
+extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                      int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                      const int32_t *perm, const float *centroids, int n_blocks,
+                                      int n_centroids, const uint8_t *idx,
+                                      const uint32_t *packed, const void *scales,
+                                      const void *zeros, int sz_dtype, int bits,
+                                      int group_size, int64_t cap, int64_t t_kv, int causal,
+                                      int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                      size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(packed && scales && zeros, "null packed/scales/zeros");
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4 (got %d)", bits);
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(group_size >= 1 && head_dim % group_size == 0,
+               "head_dim %d not divisible by group_size %d", head_dim, group_size);
+    SS_REQUIRE(!(bits == 2 && head_dim % 16) && !(bits == 4 && head_dim % 8),
+               "head_dim %d cannot be packed at %d bits", head_dim, bits);
+    // a packed word spans at most two scale groups
+    SS_UNSUPPORTED(group_size >= 32 / bits, "group_size %d < %d values per word", group_size,
+                   32 / bits);
+    SS_REQUIRE(((uintptr_t)packed % 4) == 0, "packed values must be 4-byte aligned");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int n_groups = head_dim / group_size;
+#define SS_GROUPED(DD, BB, SZT)                                                          \
+    {                                                                                    \
+        typename VGrouped<DD, BB, SZT>::Args va{packed, reinterpret_cast<const SZT *>(scales), \
+                                                reinterpret_cast<const SZT *>(zeros),    \
+                                                group_size, n_groups};                   \
+        return launch_r<DD, VGrouped<DD, BB, SZT>>(c, va, s, st);                        \
+    }
+#define SS_GROUPED_BITS(DD, SZT)            \
+    {                                       \
+        if (bits == 2) SS_GROUPED(DD, 2, SZT) \
+        if (bits == 3) SS_GROUPED(DD, 3, SZT) \
+        SS_GROUPED(DD, 4, SZT)              \
+    }
+    if (head_dim == 128) {
+        if (sz_dtype == SS_F16) SS_GROUPED_BITS(128, __half)
+        SS_GROUPED_BITS(128, float)
+    } else {
+        if (sz_dtype == SS_F16) SS_GROUPED_BITS(64, __half)
+        SS_GROUPED_BITS(64, float)
+    }
+#undef SS_GROUPED_BITS
+#undef SS_GROUPED
+}

@@ -1,0 +1,219 @@
+// Value codecs: grouped asymmetric quantisation, bit packing, scalar quantise.
+//
+// Integer outputs (codes, packed words, scalar indices) are bit-exact with the
+// reference's arithmetic: every float32 step is an IEEE operation with no
+// contraction (__fsub_rn / __fdiv_rn / rintf), mirroring kernels.py:1173-1228.
+#include "ss_common.hpp"
+
+namespace ss {
+
+__host__ __device__ constexpr int vals_per_word(int bits) { return 32 / bits; }
+
+__host__ __device__ inline int packed_words(int d, int bits) {
+    const int vpw = vals_per_word(bits);
+    return (d + vpw - 1) / vpw;
+}
+
+// One thread per token: groups' min/max -> scale/zero -> codes -> packed words.
+__global__ void __launch_bounds__(256)
+    quantize_grouped_kernel(const void *values, int v_dtype, int64_t n_h, int64_t n_t,
+                            int64_t n_tok, int64_t v_sb, int64_t v_sh, int64_t v_st, int d,
+                            int bits, int group, uint32_t *packed, void *scales, void *zeros,
+                            int sz_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st) {
+    const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= n_tok) return;
+    const int64_t b = n / (n_h * n_t);
+    const int64_t rem = n - b * n_h * n_t;
+    const int64_t h = rem / n_t;
+    const int64_t t = rem - h * n_t;
+    const int64_t vin = b * v_sb + h * v_sh + t * v_st;
+    const int64_t orow = b * o_sb + h * o_sh + t * o_st;
+    const int n_groups = d / group;
+    const int vpw = vals_per_word(bits);
+    const int nw = packed_words(d, bits);
+    const float maxv = (float)((1 << bits) - 1);
+    const uint32_t mask = (1u << bits) - 1u;
+
+    uint32_t word = 0u;
+    int word_i = 0, slot = 0;
+    for (int g = 0; g < n_groups; ++g) {
+        float mn = INFINITY, mx = -INFINITY;
+        for (int k = 0; k < group; ++k) {
+            const float v = load_as_f32(values, v_dtype, vin + g * group + k);
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+        float sc = __fdiv_rn(__fsub_rn(mx, mn), maxv);
+        if (sc < 1e-8f) sc = 1e-8f;
+        store_from_f32(scales, sz_dtype, orow * n_groups + g, sc);
+        store_from_f32(zeros, sz_dtype, orow * n_groups + g, mn);
+        for (int k = 0; k < group; ++k) {
+            const float v = load_as_f32(values, v_dtype, vin + g * group + k);
+            float qf = rintf(__fdiv_rn(__fsub_rn(v, mn), sc));
+            qf = fminf(fmaxf(qf, 0.f), maxv);
+            word |= ((uint32_t)qf & mask) << (slot * bits);
+            if (++slot == vpw) {
+                packed[orow * nw + word_i++] = word;
+                word = 0u;
+                slot = 0;
+            }
+        }
+    }
+    if (slot) packed[orow * nw + word_i] = word;  // zero-padded tail word
+}
+
+// One thread per output value.
+__global__ void __launch_bounds__(256)
+    dequantize_grouped_kernel(const uint32_t *packed, const void *scales, const void *zeros,
+                              int sz_dtype, int64_t n_tok, int d, int bits, int group, void *out,
+                              int out_dtype) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_tok * d) return;
+    const int64_t t = e / d;
+    const int i = (int)(e - t * d);
+    const int vpw = vals_per_word(bits);
+    const int nw = packed_words(d, bits);
+    const int n_groups = d / group;
+    const uint32_t w = packed[t * nw + i / vpw];
+    const float q = (float)((w >> ((i % vpw) * bits)) & ((1u << bits) - 1u));
+    const int64_t gi = t * n_groups + i / group;
+    const float sc = load_as_f32(scales, sz_dtype, gi);
+    const float zr = load_as_f32(zeros, sz_dtype, gi);
+    store_from_f32(out, out_dtype, e, __fadd_rn(__fmul_rn(q, sc), zr));
+}
+
+__global__ void __launch_bounds__(256)
+    pack_kernel(const uint8_t *in, int64_t n_rows, int d, int bits, uint32_t *out) {
+    const int nw = packed_words(d, bits);
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_rows * nw) return;
+    const int64_t r = e / nw;
+    const int w = (int)(e - r * nw);
+    const int vpw = vals_per_word(bits);
+    const uint32_t mask = (1u << bits) - 1u;
+    uint32_t word = 0u;
+    for (int k = 0; k < vpw; ++k) {
+        const int col = w * vpw + k;
+        if (col < d) word |= ((uint32_t)in[r * d + col] & mask) << (k * bits);
+    }
+    out[e] = word;
+}
+
+__global__ void __launch_bounds__(256)
+    unpack_kernel(const uint32_t *in, int64_t n_rows, int d, int bits, uint32_t *out) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_rows * d) return;
+    const int64_t r = e / d;
+    const int i = (int)(e - r * d);
+    const int vpw = vals_per_word(bits);
+    const uint32_t w = in[r * packed_words(d, bits) + i / vpw];
+    out[e] = (w >> ((i % vpw) * bits)) & ((1u << bits) - 1u);
+}
+
+__global__ void __launch_bounds__(256)
+    scalar_quantize_kernel(const float *v, int64_t n, const float *bnd, int nb, uint8_t *out) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const float x = v[e];
+    unsigned cnt = 0;
+    for (int b = 0; b < nb; ++b) cnt += x > bnd[b] ? 1u : 0u;
+    out[e] = (uint8_t)cnt;
+}
+
+static inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" int ss_quantize_values_grouped(const void *values, int v_dtype, int64_t n_b,
+                                          int64_t n_h, int64_t n_t, int64_t v_sb, int64_t v_sh,
+                                          int64_t v_st, int head_dim, int bits, int group_size,
+                                          uint32_t *packed, void *scales, void *zeros,
+                                          int sz_dtype, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                                          void *stream) {
+    SS_REQUIRE(valid_dtype(v_dtype), "bad value dtype");
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4");
+    SS_REQUIRE(group_size >= 1 && head_dim >= 1 && head_dim % group_size == 0,
+               "head_dim %d not divisible by group_size %d", head_dim, group_size);
+    SS_REQUIRE(!(bits == 2 && head_dim % 16) && !(bits == 4 && head_dim % 8),
+               "head_dim %d cannot be packed at %d bits", head_dim, bits);
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0, "negative sizes");
+    const int64_t n_tok = n_b * n_h * n_t;
+    if (n_tok == 0) return SS_OK;
+    SS_REQUIRE(values && packed && scales && zeros, "null pointer argument");
+    SS_UNSUPPORTED(n_tok < (1LL << 32), "too many tokens for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(quantize_grouped_kernel, dim3(blocks_for(n_tok)), dim3(256), 0, st, values,
+                       v_dtype, n_h, n_t, n_tok, v_sb, v_sh, v_st, head_dim, bits, group_size,
+                       packed, scales, zeros, sz_dtype, o_sb, o_sh, o_st);
+    SS_LAUNCH_CHECK("quantize_grouped_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_dequantize_values_grouped(const uint32_t *packed, const void *scales,
+                                            const void *zeros, int sz_dtype, int64_t n_tok,
+                                            int head_dim, int bits, int group_size, void *out,
+                                            int out_dtype, void *stream) {
+    SS_REQUIRE(valid_dtype(out_dtype), "bad output dtype");
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4");
+    SS_REQUIRE(group_size >= 1 && head_dim % group_size == 0, "bad group size");
+    SS_REQUIRE(n_tok >= 0, "negative sizes");
+    if (n_tok == 0) return SS_OK;
+    SS_REQUIRE(packed && scales && zeros && out, "null pointer argument");
+    const int64_t total = n_tok * head_dim;
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(dequantize_grouped_kernel, dim3(blocks_for(total)), dim3(256), 0, st,
+                       packed, scales, zeros, sz_dtype, n_tok, head_dim, bits, group_size, out,
+                       out_dtype);
+    SS_LAUNCH_CHECK("dequantize_grouped_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_pack_indices(const uint8_t *in, int64_t n_rows, int d, int bits, uint32_t *out,
+                               void *stream) {
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4");
+    SS_REQUIRE(!(bits == 2 && d % 16), "last dim must be divisible by 16 for 2-bit, got %d", d);
+    SS_REQUIRE(!(bits == 4 && d % 8), "last dim must be divisible by 8 for 4-bit, got %d", d);
+    SS_REQUIRE(n_rows >= 0 && d >= 1, "bad sizes");
+    if (n_rows == 0) return SS_OK;
+    SS_REQUIRE(in && out, "null pointer argument");
+    const int64_t total = n_rows * packed_words(d, bits);
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(pack_kernel, dim3(blocks_for(total)), dim3(256), 0, st, in, n_rows, d, bits,
+                       out);
+    SS_LAUNCH_CHECK("pack_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_unpack_indices(const uint32_t *in, int64_t n_rows, int d, int bits,
+                                 uint32_t *out, void *stream) {
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4");
+    SS_REQUIRE(n_rows >= 0 && d >= 1, "bad sizes");
+    if (n_rows == 0) return SS_OK;
+    SS_REQUIRE(in && out, "null pointer argument");
+    const int64_t total = n_rows * d;
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(unpack_kernel, dim3(blocks_for(total)), dim3(256), 0, st, in, n_rows, d,
+                       bits, out);
+    SS_LAUNCH_CHECK("unpack_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_scalar_quantize(const float *values, int64_t n, const float *boundaries,
+                                  int n_boundaries, uint8_t *out, void *stream) {
+    SS_REQUIRE(n >= 0 && n_boundaries >= 0 && n_boundaries <= 255, "bad sizes");
+    if (n == 0) return SS_OK;
+    SS_REQUIRE(values && out && (boundaries || n_boundaries == 0), "null pointer argument");
+    SS_UNSUPPORTED(n < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(scalar_quantize_kernel, dim3(blocks_for(n)), dim3(256), 0, st, values, n,
+                       boundaries, n_boundaries, out);
+    SS_LAUNCH_CHECK("scalar_quantize_kernel launch");
+    return SS_OK;
+}

@@ -1,0 +1,275 @@
+"""GPU parity of the C-ABI kernels against the CPU oracle.
+
+Bars (written in each test):
+  * integer/byte outputs (encode indices, packed words, codes, scalar
+    indices, reconstructed centroids) are bit-exact; encode excludes only
+    (token, block) pairs the oracle flags as near-ties (a centroid with a
+    different vector within 1e-6 relative distance of the best);
+  * attention outputs and scores: max |gpu - oracle| <= 1e-3 * max |oracle|
+    (fp32 accumulation on the GPU, float64 oracle).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sunshape_oracle as O
+from sunshape_mlx_amd import _hip
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+REL_TOL = 1e-3
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def decode_case(seed, b, hq, hkv, d, t_kv, t_q=1, cap=None, nc=256, v_dtype=np.float16):
+    rng = np.random.default_rng(seed)
+    nb = d // 8
+    cap = cap or t_kv
+    cents = rng.standard_normal((nb, nc, 8)).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    idx = np.zeros((b, hkv, cap, nb), np.uint8)
+    idx[:, :, :t_kv] = rng.integers(0, nc, (b, hkv, t_kv, nb))
+    vals = np.zeros((b, hkv, cap, d), v_dtype)
+    vals[:, :, :t_kv] = rng.standard_normal((b, hkv, t_kv, d)).astype(v_dtype)
+    q = rng.standard_normal((b, hq, t_q, d)).astype(np.float16)
+    return cents, perm, idx, vals, q
+
+
+@pytest.mark.parametrize(
+    "b,hq,hkv,d,t_kv,t_q,causal,splits,cap",
+    [
+        (1, 32, 8, 128, 4096, 1, False, 0, None),    # BASELINE config 2 shape
+        (1, 32, 8, 128, 4096, 1, True, 0, 4352),     # causal no-op at decode, padded cap
+        (2, 8, 2, 128, 1000, 1, False, 0, 1024),     # ragged T, B=2
+        (1, 4, 1, 128, 1, 1, False, 0, 256),         # single token
+        (1, 4, 4, 128, 777, 1, False, 1, None),      # MHA (rep 1) -> R=1 path, no split
+        (1, 4, 2, 128, 777, 1, False, 7, None),      # forced 7 splits
+        (1, 8, 2, 64, 513, 1, False, 0, None),       # head_dim 64
+        (1, 4, 1, 128, 64, 3, True, 0, None),        # prefill rows, causal q_offset
+        (2, 6, 2, 64, 300, 5, True, 3, 320),         # rows spill over several row groups
+    ])
+def test_decode_dense_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, cap):
+    cents, perm, idx, vals, q = decode_case(b * 1000 + t_kv, b, hq, hkv, d, t_kv, t_q, cap)
+    scale = 1.0 / np.sqrt(d)
+    out = _hip.decode_attn_dense(t(q), scale, t(perm), t(cents), t(idx), t(vals), t_kv,
+                                 causal=causal, q_offset=t_kv - t_q if causal else 0,
+                                 out_dtype=torch.float32, n_splits=splits)
+    torch.cuda.synchronize()
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, scale,
+                 mask="causal" if causal else None)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def test_decode_dense_metric_shape_fp16_out_and_repeatability():
+    """T_kv = 32768 (the metric shape): fp32 and fp16 outputs, and two calls
+    in a row agree bit-for-bit (split counters are reset by each call)."""
+    cents, perm, idx, vals, q = decode_case(42, 1, 32, 8, 128, 32768)
+    scale = 1.0 / np.sqrt(128)
+    args = (t(q), scale, t(perm), t(cents), t(idx), t(vals), 32768)
+    o1 = _hip.decode_attn_dense(*args, out_dtype=torch.float32)
+    o2 = _hip.decode_attn_dense(*args, out_dtype=torch.float32)
+    o16 = _hip.decode_attn_dense(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    ref = O.sdpa(q, idx, vals, cents, perm, scale)
+    assert rel_err(o1.cpu().numpy(), ref) <= REL_TOL
+    assert o16.dtype == torch.float16
+    # fp16 output: the fp32 result rounded once more (half an fp16 ulp)
+    assert rel_err(o16.float().cpu().numpy(), ref) <= REL_TOL
+
+
+def test_decode_empty_cache_outputs_zero():
+    cents, perm, idx, vals, q = decode_case(3, 1, 4, 1, 128, 0, cap=256)
+    out = _hip.decode_attn_dense(t(q), 0.1, t(perm), t(cents), t(idx), t(vals), 0,
+                                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+
+
+def test_decode_bf16_and_f32_values():
+    for vd, seed in ((np.float32, 5), (None, 6)):
+        cents, perm, idx, vals, q = decode_case(seed, 1, 8, 2, 128, 600, v_dtype=np.float32)
+        vt = t(vals) if vd is not None else t(vals).to(torch.bfloat16)
+        vref = vals if vd is not None else vt.float().cpu().numpy()
+        out = _hip.decode_attn_dense(t(q), 0.125, t(perm), t(cents), t(idx), vt, 600,
+                                     out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        ref = O.sdpa(q, idx, vref, cents, perm, 0.125)
+        assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("bits,group,sz,d,t_kv,causal,t_q", [
+    (2, 64, np.float16, 128, 2048, False, 1),   # BASELINE config 4 format
+    (2, 64, np.float32, 128, 700, False, 1),    # reference storage (f32 scale/zero)
+    (4, 64, np.float32, 128, 64, False, 1),     # known-answer [15] shape
+    (4, 64, np.float32, 128, 32, True, 4),      # [16] shape
+    (3, 16, np.float16, 128, 333, False, 1),    # 3-bit words straddle groups
+    (4, 16, np.float32, 64, 500, True, 2),
+    (2, 16, np.float16, 64, 129, False, 1),
+])
+def test_decode_grouped_matches_oracle(bits, group, sz, d, t_kv, causal, t_q):
+    b, hq, hkv = 1, 8, 2
+    cents, perm, idx, vals, q = decode_case(bits * 100 + t_kv, b, hq, hkv, d, t_kv, t_q,
+                                            v_dtype=np.float32)
+    flat = vals.reshape(-1, d)
+    packed, sc, zr, _ = O.quantize_values(flat, bits, group)
+    sc_s, zr_s = sc.astype(sz), zr.astype(sz)
+    nw = packed.shape[-1]
+    ng = d // group
+    shp = (b, hkv, t_kv)
+    deq = O.dequantize_values(packed, sc_s, zr_s, d, bits, group).reshape(shp + (d,))
+    out = _hip.decode_attn_grouped(
+        t(q), 0.1, t(perm), t(cents), t(idx), t(packed.reshape(shp + (nw,)).view(np.int32)),
+        t(sc_s.reshape(shp + (ng,))), t(zr_s.reshape(shp + (ng,))), bits, group, t_kv,
+        causal=causal, q_offset=t_kv - t_q if causal else 0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.sdpa(q, idx, deq, cents, perm, 0.1, mask="causal" if causal else None)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def _kmeans_like_codebook(rng, nb, nc, bd, scale):
+    # centroids drawn from the data distribution, with a duplicated pair per
+    # block (exact ties must resolve to the lower index)
+    c = (rng.standard_normal((nb, nc, bd)) * scale.reshape(nb, 1, bd)).astype(np.float32)
+    c[:, 7] = c[:, 3]
+    return c
+
+
+@pytest.mark.parametrize("n_tok,bd,dtype", [
+    (5, 8, np.float32),        # decode-step append path (wave per block)
+    (300, 8, np.float16),      # small path, fp16 keys
+    (4096, 8, np.float32),     # bulk path
+    (2000, 4, np.float32),
+    (1500, 16, np.float16),
+])
+def test_encode_bit_exact_except_near_ties(n_tok, bd, dtype):
+    rng = np.random.default_rng(n_tok + bd)
+    d = 128
+    nb = d // bd
+    s = np.exp(rng.uniform(np.log(0.25), np.log(8.0), d)).astype(np.float32)
+    keys = (rng.standard_normal((n_tok, d)) * s).astype(dtype)
+    perm = rng.permutation(d).astype(np.int32)
+    cents = _kmeans_like_codebook(rng, nb, 256, bd, s[perm])
+    out = torch.empty((n_tok, nb), dtype=torch.uint8, device=DEV)
+    _hip.encode_blockvq(t(keys), t(perm), t(cents), out, bd)
+    torch.cuda.synchronize()
+    ref, near = O.encode_blockvq_c(keys, cents, perm)
+    got = out.cpu().numpy()
+    ok = ~near
+    assert near.mean() < 1e-3
+    assert np.array_equal(got[ok], ref[ok]), f"{(got[ok] != ref[ok]).sum()} mismatches"
+    assert not (got == 7).any(), "duplicate centroid 7 must lose the tie to centroid 3"
+
+
+def test_encode_config3_shape_and_cache_strides():
+    """fp16 K (8 heads x 8192 tokens x 128), ProfilePerm,
+    encoded straight into a padded cache buffer (B, H, cap, 16) at an offset."""
+    rng = np.random.default_rng(3)
+    h, n, d, cap, off = 8, 8192, 128, 8192 + 512, 256
+    s = np.exp(rng.uniform(np.log(0.25), np.log(8.0), d)).astype(np.float32)
+    keys = (rng.standard_normal((1, h, n, d)) * s).astype(np.float16)
+    perm = rng.permutation(d).astype(np.int32)
+    cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)[:, perm]
+    cents = np.stack([cal[rng.permutation(4096)[:256], b * 8:(b + 1) * 8] for b in range(16)])
+    cache = torch.full((1, h, cap, 16), 255, dtype=torch.uint8, device=DEV)
+    _hip.encode_blockvq(t(keys), t(perm), t(cents), cache[:, :, off:off + n], 8)
+    torch.cuda.synchronize()
+    got = cache.cpu().numpy()
+    assert (got[:, :, :off] == 255).all() and (got[:, :, off + n:] == 255).all()
+    ref, near = O.encode_blockvq_c(keys.reshape(-1, d), cents, perm)
+    g = got[0, :, off:off + n].reshape(-1, 16)
+    ok = ~near
+    assert np.array_equal(g[ok], ref[ok]), f"{(g[ok] != ref[ok]).sum()} mismatches"
+
+
+def test_lut_and_score_gather():
+    rng = np.random.default_rng(55)
+    d, nb, nc = 128, 16, 256
+    q = rng.standard_normal((8, d)).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    cents = rng.standard_normal((nb, nc, 8)).astype(np.float32)
+    lut = _hip.build_lut(t(q), t(perm), 1.0, t(cents))
+    torch.cuda.synchronize()
+    ref_lut = O.query_centroid_dots(q[:, perm], cents)
+    assert rel_err(lut.cpu().numpy(), ref_lut) <= 1e-5
+    idx = rng.integers(0, nc, (1000, nb)).astype(np.uint8)
+    sc = _hip.score_gather(lut, t(idx))
+    torch.cuda.synchronize()
+    ref = O.gather_scores(ref_lut, idx)
+    assert rel_err(sc.cpu().numpy(), ref) <= REL_TOL
+    # [10]: n_blocks 8, n_centroids 64, score shape (2, 16)
+    qd = rng.standard_normal((2, 8, 64)).astype(np.float32)
+    i2 = rng.integers(0, 64, (16, 8)).astype(np.uint8)
+    s2 = _hip.score_gather(t(qd), t(i2))
+    torch.cuda.synchronize()
+    assert tuple(s2.shape) == (2, 16)
+    assert rel_err(s2.cpu().numpy(), O.gather_scores(qd, i2)) <= 1e-6
+
+
+def test_dequantize_blockvq_exact():
+    rng = np.random.default_rng(9)
+    cents = rng.standard_normal((16, 256, 8)).astype(np.float32)
+    idx = rng.integers(0, 256, (321, 16)).astype(np.uint8)
+    perm = rng.permutation(128).astype(np.int32)
+    inv = O.invert_permutation(perm)
+    out = _hip.dequantize_blockvq(t(idx), t(cents), t(inv))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), O.dequantize_blockvq(idx, cents, inv))
+
+
+@pytest.mark.parametrize("bits,group,d", [(2, 64, 128), (4, 64, 128), (3, 16, 128), (4, 16, 64),
+                                          (2, 16, 64)])
+def test_quantize_values_bit_exact(bits, group, d):
+    rng = np.random.default_rng(123 + bits)
+    v = rng.standard_normal((257, d)).astype(np.float32)
+    v[5] = 0.0  # constant group -> scale clamps to 1e-8
+    nw = O.packed_dim(d, bits)
+    p = torch.empty((257, nw), dtype=torch.int32, device=DEV)
+    s = torch.empty((257, d // group), dtype=torch.float32, device=DEV)
+    z = torch.empty_like(s)
+    _hip.quantize_values_grouped(t(v), bits, group, p, s, z)
+    torch.cuda.synchronize()
+    rp, rs, rz, _ = O.quantize_values(v, bits, group)
+    assert np.array_equal(p.cpu().numpy().view(np.uint32), rp)
+    assert np.array_equal(s.cpu().numpy(), rs) and np.array_equal(z.cpu().numpy(), rz)
+    deq = _hip.dequantize_values_grouped(p.view(torch.uint32), s, z, d, bits, group)
+    torch.cuda.synchronize()
+    assert np.array_equal(deq.cpu().numpy(), O.dequantize_values(rp, rs, rz, d, bits, group))
+
+
+@pytest.mark.parametrize("bits,d", [(2, 128), (3, 100), (3, 27), (4, 128), (4, 32)])
+def test_pack_unpack_bit_exact(bits, d):
+    rng = np.random.default_rng(42 + d)
+    x = rng.integers(0, 1 << bits, (32, d)).astype(np.uint8)
+    p = _hip.pack_indices(t(x), bits)
+    u = _hip.unpack_indices(p, d, bits)
+    torch.cuda.synchronize()
+    assert np.array_equal(p.cpu().numpy(), O.pack_indices(x, bits))
+    assert np.array_equal(u.cpu().numpy(), x.astype(np.uint32))
+
+
+def test_scalar_quantize_exact():
+    rng = np.random.default_rng(77)
+    v = rng.standard_normal((100, 64)).astype(np.float32)
+    bnd = np.array([-1.0, -0.5, 0.0, 0.5, 1.0], np.float32)
+    out = _hip.scalar_quantize(t(v), t(bnd))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), O.scalar_quantize(v, bnd))
+
+
+def test_invalid_arguments_raise_before_launch():
+    cents, perm, idx, vals, q = decode_case(1, 1, 6, 4, 128, 64)  # 6 % 4 != 0
+    with pytest.raises(_hip.SunShapeHIPError):
+        _hip.decode_attn_dense(t(q), 1.0, t(perm), t(cents), t(idx), t(vals), 64)
+    cents, perm, idx, vals, q = decode_case(1, 1, 4, 4, 128, 64)
+    with pytest.raises(_hip.SunShapeHIPError):
+        _hip.decode_attn_dense(t(q), 1.0, t(perm), t(cents), t(idx), t(vals), 65)  # > cap
