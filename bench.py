@@ -50,7 +50,24 @@ def parse_args():
                    help="budget for the CPU baseline (0 disables it)")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                           "decode_fp16v_t32k_traffic.json"))
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                   help="only run a plain device copy of MB megabytes --steps times (the "
+                        "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+def calibrate_copy(mb: int, steps: int) -> int:
+    import torch
+
+    n = mb * (1 << 20) // 4
+    src = torch.randn(n, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes_read": n * 4, "calibrate_copy_bytes_written": n * 4,
+                      "dispatches": steps}), flush=True)
+    return 0
 
 
 def algorithmic_bytes(b, hq, hkv, d, t_kv, nb, v_bytes=2, q_bytes=2, out_bytes=2) -> int:
@@ -67,6 +84,8 @@ def main() -> int:
               "(the decode path shards by KV head with no exchange; see DESIGN.md)",
               file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy, args.steps)
 
     import numpy as np
     import torch

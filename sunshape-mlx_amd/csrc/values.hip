@@ -67,6 +67,9 @@ __global__ void __launch_bounds__(256)
     dequantize_grouped_kernel(const uint32_t *packed, const void *scales, const void *zeros,
                               int sz_dtype, int64_t n_tok, int d, int bits, int group, void *out,
                               int out_dtype) {
+    // separate multiply and add, as the reference's elementwise ops round
+    // (device code is otherwise compiled with fp-contract=fast)
+#pragma clang fp contract(off)
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= n_tok * d) return;
     const int64_t t = e / d;
@@ -79,7 +82,8 @@ __global__ void __launch_bounds__(256)
     const int64_t gi = t * n_groups + i / group;
     const float sc = load_as_f32(scales, sz_dtype, gi);
     const float zr = load_as_f32(zeros, sz_dtype, gi);
-    store_from_f32(out, out_dtype, e, __fadd_rn(__fmul_rn(q, sc), zr));
+    const float prod = q * sc;
+    store_from_f32(out, out_dtype, e, prod + zr);
 }
 
 __global__ void __launch_bounds__(256)

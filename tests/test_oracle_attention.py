@@ -1,0 +1,203 @@
+"""Pins the oracle's LUT, score gather and fused attention (CPU only).
+
+The reference's known-answer tests [6], [7], [11], [12], [14]
+(reference test_kernels.py:163-482) are restated with their np.random.seed
+streams: the expected output is the textbook ``softmax(q k_hat^T) V`` with
+k_hat reconstructed from the codebook -- a different route from the oracle's
+LUT + gather.  Tolerances are the reference's own (1e-3 scores; 5e-3 / 1e-2
+outputs) and, where the oracle is float64, much tighter ones too.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import sunshape_oracle as O
+
+
+def k_hat_of(cents, idx):
+    return O.dequantize_blockvq(idx, cents)
+
+
+def explicit_attention(q, k_hat, v, causal=False, q_offset=0, masked=-1e30):
+    s = q.astype(np.float64) @ k_hat.astype(np.float64).T
+    if causal:
+        qp = np.arange(q_offset, q_offset + q.shape[0])
+        s = np.where(qp[:, None] >= np.arange(k_hat.shape[0])[None, :], s, masked)
+    w = np.exp(s - s.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    return w @ v.astype(np.float64)
+
+
+def test_known_answer_6_score_gather():
+    np.random.seed(55)
+    qdots = np.random.randn(4, 16, 256).astype(np.float32)
+    idx = np.random.randint(0, 256, size=(32, 16), dtype=np.uint8)
+    ref = np.take_along_axis(qdots[:, None, :, :], idx[None, :, :, None].astype(np.int64),
+                             axis=-1)[..., 0].sum(axis=2)
+    assert np.abs(O.gather_scores(qdots, idx) - ref).max() < 1e-5
+
+
+def test_scores_equal_q_dot_reconstructed_keys_in_original_basis():
+    """attention_scores == q @ dequantize(k).T (reference
+    test_sunshape_mlx.py:172-182): the permutation cancels in the dot."""
+    rng = np.random.default_rng(3)
+    cents = rng.standard_normal((16, 256, 8)).astype(np.float32)
+    perm = rng.permutation(128).astype(np.int32)
+    idx = rng.integers(0, 256, (100, 16)).astype(np.uint8)
+    q = rng.standard_normal((8, 128)).astype(np.float32)
+    k_orig = O.dequantize_blockvq(idx, cents, O.invert_permutation(perm))
+    s = O.attention_scores(q, idx, cents, perm)
+    ref = q.astype(np.float64) @ k_orig.astype(np.float64).T
+    assert np.abs(s - ref).max() < 1e-9 * np.abs(ref).max()
+    # planted mistake: forgetting the query permutation breaks it
+    bad = O.gather_scores(O.query_centroid_dots(q, cents), idx)
+    assert np.abs(bad - ref).max() > 1e-2
+
+
+def test_known_answer_7_materialized_causal():
+    np.random.seed(42)
+    t_q, t_kv, nb, nc, bd = 4, 32, 16, 256, 8
+    cents = np.random.randn(nb, nc, bd).astype(np.float32)
+    idx = np.random.randint(0, nc, size=(t_kv, nb), dtype=np.int32)
+    v = np.random.randn(t_kv, nb * bd).astype(np.float32)
+    q = np.random.randn(t_q, nb * bd).astype(np.float32)
+    ref = explicit_attention(q, k_hat_of(cents, idx), v, True, t_kv - t_q, -1e9)
+    qd = O.query_centroid_dots(q, cents)
+    out = O.materialized_block_vq_attention(qd, idx, v, t_q, t_kv)
+    assert np.abs(out - ref).max() < 5e-3
+    assert np.abs(out - ref).max() < 1e-9
+
+
+@pytest.mark.parametrize("seed,t_q,t_kv,causal,vscale,tol", [
+    (111, 1, 64, False, 1.0, 5e-3),   # [11]
+    (222, 4, 32, True, 1.0, 5e-3),    # [12]
+    (444, 1, 512, False, 0.1, 1e-2),  # [14]
+])
+def test_known_answers_fused(seed, t_q, t_kv, causal, vscale, tol):
+    np.random.seed(seed)
+    nb, nc, bd = 16, 256, 8
+    cents = np.random.randn(nb, nc, bd).astype(np.float32)
+    idx = np.random.randint(0, nc, size=(t_kv, nb), dtype=np.uint8)
+    v = (np.random.randn(t_kv, nb * bd).astype(np.float32) * vscale).astype(np.float32)
+    q = (np.random.randn(t_q, nb * bd).astype(np.float32) * vscale).astype(np.float32)
+    q_off = t_kv - t_q if causal else 0
+    ref = explicit_attention(q, k_hat_of(cents, idx), v, causal, q_off)
+    out = O.fused_attention(q, cents, idx, v, causal, q_off)
+    assert np.abs(out - ref).max() < tol
+    assert np.abs(out - ref).max() < 1e-9
+
+
+def test_online_literal_equals_two_pass():
+    rng = np.random.default_rng(9)
+    cents = rng.standard_normal((8, 64, 8)).astype(np.float32)
+    idx = rng.integers(0, 64, (150, 8)).astype(np.uint8)
+    v = rng.standard_normal((150, 64)).astype(np.float32)
+    q = rng.standard_normal((5, 64)).astype(np.float32) * 0.5
+    for causal, off in ((False, 0), (True, 145), (True, 2)):
+        a = O.fused_attention(q, cents, idx, v, causal, off)
+        b = O.fused_attention_online_literal(q, cents, idx, v, causal, off)
+        assert np.abs(a - b).max() < 1e-10
+
+
+def test_fully_masked_rows_output_zero():
+    rng = np.random.default_rng(1)
+    cents = rng.standard_normal((8, 16, 8)).astype(np.float32)
+    idx = rng.integers(0, 16, (10, 8)).astype(np.uint8)
+    v = rng.standard_normal((10, 64)).astype(np.float32)
+    q = rng.standard_normal((3, 64)).astype(np.float32)
+    # q_offset -5: row 0 admits t <= -5 (none), row 2 admits t <= -3 (none)
+    out = O.fused_attention(q, cents, idx, v, True, -5)
+    assert not out.any()
+    assert not O.fused_attention_online_literal(q, cents, idx, v, True, -5).any()
+
+
+def test_split_lse_merge_equals_whole():
+    """The split-T decomposition used on the GPU: partials (m, l, acc) of
+    token chunks merged by log-sum-exp give the same output."""
+    rng = np.random.default_rng(12)
+    s = rng.standard_normal(1000) * 3
+    v = rng.standard_normal((1000, 16))
+    whole = (np.exp(s - s.max()) @ v) / np.exp(s - s.max()).sum()
+    parts = []
+    for lo in range(0, 1000, 137):
+        ss = s[lo:lo + 137]
+        m = ss.max()
+        p = np.exp(ss - m)
+        parts.append((m, p.sum(), p @ v[lo:lo + 137]))
+    parts.append((-1e30, 0.0, np.zeros(16)))  # an empty split
+    assert np.abs(O.lse_merge(parts) - whole).max() < 1e-12
+
+
+def test_sdpa_gqa_head_mapping_and_scale():
+    """q head h*rep + r reads KV head h (attention.py:220); scale is applied in
+    the query dtype before the permutation (attention.py:208, 228)."""
+    rng = np.random.default_rng(21)
+    b_, hq, hkv, d, t = 1, 6, 2, 64, 40
+    cents = rng.standard_normal((8, 32, 8)).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    idx = rng.integers(0, 32, (b_, hkv, t, 8)).astype(np.uint8)
+    vals = rng.standard_normal((b_, hkv, t, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, 1, d)).astype(np.float16)
+    scale = 0.125
+    out = O.sdpa(q, idx, vals, cents, perm, scale)
+    inv = O.invert_permutation(perm)
+    for hh in range(hq):
+        kv = hh // (hq // hkv)
+        qs = (q[0, hh].astype(np.float32) * np.float32(scale)).astype(np.float16)
+        ref = explicit_attention(qs.astype(np.float32),
+                                 O.dequantize_blockvq(idx[0, kv], cents, inv), vals[0, kv])
+        assert np.abs(out[0, hh] - ref).max() < 1e-9
+    # planted mistake: interleaved GQA mapping (kv = hh % hkv) must differ
+    kv_wrong = 1 % hkv
+    qs = (q[0, 1].astype(np.float32) * np.float32(scale)).astype(np.float16)
+    wrong = explicit_attention(qs.astype(np.float32),
+                               O.dequantize_blockvq(idx[0, kv_wrong], cents, inv),
+                               vals[0, kv_wrong])
+    assert np.abs(out[0, 1] - wrong).max() > 1e-3
+
+
+def test_sdpa_two_pass_equals_fused_without_buffer():
+    rng = np.random.default_rng(30)
+    b_, hq, hkv, d, t = 1, 4, 2, 64, 33
+    cents = rng.standard_normal((8, 64, 8)).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    idx = rng.integers(0, 64, (b_, hkv, t, 8)).astype(np.uint8)
+    vals = rng.standard_normal((b_, hkv, t, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, 3, d)).astype(np.float16)
+    a = O.sdpa(q, idx, vals, cents, perm, 0.2, mask="causal")
+    b = O.sdpa_two_pass(q, 0.2, perm, cents, idx, None, vals, mask="causal")
+    assert np.abs(a - b).max() < 1e-10
+
+
+def test_sdpa_two_pass_buffer_scores_use_original_basis():
+    """Buffered fp16 keys are scored against the *unpermuted* scaled query
+    (attention.py:318-321)."""
+    rng = np.random.default_rng(31)
+    d = 64
+    perm = rng.permutation(d).astype(np.int32)
+    cents = rng.standard_normal((8, 16, 8)).astype(np.float32)
+    kb = rng.standard_normal((1, 1, 5, d)).astype(np.float16)
+    vals = rng.standard_normal((1, 1, 5, d)).astype(np.float16)
+    q = rng.standard_normal((1, 1, 1, d)).astype(np.float16)
+    out = O.sdpa_two_pass(q, 0.3, perm, cents, np.zeros((1, 1, 0, 8), np.uint8), kb, vals)
+    qs = O.scale_query(q, 0.3)[0, 0].astype(np.float64)
+    ref = explicit_attention(qs, kb[0, 0], vals[0, 0])
+    assert np.abs(out[0, 0] - ref).max() < 1e-12
+
+
+def test_cpu_baseline_forms_agree_with_oracle():
+    rng = np.random.default_rng(40)
+    b_, hq, hkv, d, t = 1, 8, 2, 128, 500
+    cents = rng.standard_normal((16, 256, 8)).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    idx = rng.integers(0, 256, (b_, hkv, t, 16)).astype(np.uint8)
+    vals = rng.standard_normal((b_, hkv, t, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, 1, d)).astype(np.float16)
+    ref = O.sdpa(q, idx, vals, cents, perm, 1 / math.sqrt(d))[:, :, 0]
+    qt = O.apply_permutation(O.scale_query(q, 1 / math.sqrt(d)), perm).astype(np.float32)
+    qt = qt.reshape(b_, hkv, hq // hkv, d)
+    for f in (O.decode_cpu_vectorised, O.decode_cpu_reference_shaped):
+        out = f(qt, cents, idx, vals)
+        assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-4
