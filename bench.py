@@ -46,6 +46,8 @@ def parse_args():
     p.add_argument("--splits", type=int, default=0, help="token splits (0 = library choice)")
     p.add_argument("--copies", type=int, default=0, help="cache copies rotated (0 = auto)")
     p.add_argument("--launch", choices=("eager", "graph"), default="eager")
+    p.add_argument("--layout", choices=("il8", "dense"), default="il8",
+                   help="value cache layout: 8-token interleaved (MFMA kernel) or token-major")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="budget for the CPU baseline (0 disables it)")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
@@ -121,19 +123,25 @@ def main() -> int:
     v0 = torch.randn((b, hkv, t_kv, d), generator=g, device=dev).to(torch.float16)
     q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
     del keys
-    per_copy = idx0.numel() + v0.numel() * 2
+    if args.layout == "il8":
+        # the cache's value layout: 8-token interleaved (append kernel)
+        vbuf = torch.zeros((b, hkv, t_kv // 8, d, 8), dtype=torch.float16, device=dev)
+        hip.append_values_il8(v0, vbuf, 0)
+        fn, kind = lib.ss_decode_attn_il8, hip.KIND_IL8
+    else:
+        vbuf = v0
+        fn, kind = lib.ss_decode_attn_dense, hip.KIND_DENSE
+    per_copy = idx0.numel() + vbuf.numel() * 2
     n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
     idxs = [idx0] + [idx0.clone() for _ in range(n_copies - 1)]
-    vals = [v0] + [v0.clone() for _ in range(n_copies - 1)]
+    vals = [vbuf] + [vbuf.clone() for _ in range(n_copies - 1)]
     torch.cuda.synchronize()
-    log(f"cache ready: {n_copies} copies x {per_copy / 1e6:.1f} MB")
+    log(f"cache ready: {n_copies} copies x {per_copy / 1e6:.1f} MB, layout {args.layout}")
 
     # ---- lean launcher: prebuilt C-ABI argument tuples, one per copy ----
-    splits = args.splits or hip.default_splits(b, hq, hkv, 1, d, t_kv)
-    ws_bytes = hip.decode_workspace_bytes(b, hq, hkv, 1, d, t_kv, splits)
+    splits, ws_bytes = hip.decode_plan(kind, b, hq, hkv, 1, d, t_kv, args.splits)
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
-    fn = lib.ss_decode_attn_dense
 
     def arg_tuples(stream_handle):
         return [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, codec.permutation.data_ptr(),
@@ -267,6 +275,7 @@ def main() -> int:
                         "(u8 idx), fp16 values, fp16 query/output, f32 accumulate",
             "batch": b, "n_q_heads": hq, "n_kv_heads": hkv, "head_dim": d, "t_kv": t_kv,
             "splits": splits, "launch": args.launch, "cache_copies": n_copies,
+            "value_layout": args.layout,
             "algorithmic_bytes_per_step": nbytes,
         },
         "roofline": {

@@ -17,8 +17,7 @@
  *    last error of the calling thread is returned by ss_last_error().
  *    Argument and shape checks happen on the host before any launch.
  *  - Stateless and reentrant, except that calls sharing one decode workspace
- *    must not overlap (the workspace holds per-call split partials and the
- *    split-completion counters).
+ *    must not overlap (the workspace holds the call's split partials).
  *  - dtype codes: SS_F32, SS_F16, SS_BF16.
  */
 #ifndef SUNSHAPE_HIP_H
@@ -92,9 +91,10 @@ int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centro
 
 /*
  * Workspace bytes needed by ss_decode_attn_* for the given shape and split
- * count (n_splits <= 0 selects the library's choice for the current device).
- * The workspace must be zero-filled once before its first use; every call
- * leaves its counters at zero again.
+ * count (n_splits <= 0 selects the library's choice for the current device);
+ * 0 when a single split suffices.  With more than one split a decode call is
+ * two launches on the stream: the split kernel writes per-split softmax
+ * partials (m, l, acc) to the workspace and a merge kernel combines them.
  */
 size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                  int64_t t_q, int head_dim, int64_t t_kv,
@@ -126,6 +126,44 @@ int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_head
                          int v_dtype, int64_t cap, int64_t t_kv, int causal,
                          int64_t q_offset, void *out, int out_dtype, void *workspace,
                          size_t workspace_bytes, int n_splits, void *stream);
+
+/*
+ * Split count and workspace bytes a decode call of the given kind would use
+ * (kind 0: ss_decode_attn_dense / ss_decode_attn_grouped, kind 1:
+ * ss_decode_attn_il8).  Either output pointer may be NULL.
+ */
+int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+                   int head_dim, int64_t t_kv, int n_splits, int *splits_out,
+                   size_t *workspace_bytes_out);
+
+/*
+ * As ss_decode_attn_dense for fp16 values held in the cache's 8-token
+ * interleaved layout: element (t, d) of a (batch, KV head) row lives at
+ * values_il8[((b*n_kv_heads + h)*cap/8 + t/8)*head_dim*8 + d*8 + t%8]
+ * (cap % 8 == 0).  P.V runs on the matrix cores (v_mfma_f32_16x16x16f16 with
+ * the probabilities split into fp16 hi/lo parts, fp32 accumulation); four
+ * query rows per KV group are processed together.  Same reference semantics
+ * as ss_decode_attn_dense (kernels.py:142-223, 303-378; attention.py:199-305).
+ */
+int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                       int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                       const int32_t *perm, const float *centroids, int n_blocks,
+                       int n_centroids, const uint8_t *idx, const void *values_il8,
+                       int v_dtype, int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
+                       void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                       int n_splits, void *stream);
+
+/*
+ * KV append of values into the 8-token interleaved fp16 layout read by
+ * ss_decode_attn_il8: token (b,h,t) of values (element j at
+ * values[b*v_sb + h*v_sh + t*v_st + j]) is written at cache position
+ * offset + t of out_il8 [n_b][n_h][cap/8][head_dim][8].  Replaces the value
+ * half of update_and_fetch (reference cache.py:196-200).
+ */
+int ss_append_values_il8(const void *values, int v_dtype, int64_t n_b, int64_t n_h,
+                         int64_t n_t, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                         int head_dim, void *out_il8, int64_t cap, int64_t offset,
+                         void *stream);
 
 /*
  * As ss_decode_attn_dense with grouped asymmetric-quantised values decoded in

@@ -64,6 +64,14 @@ _SIGNATURES = {
                                     _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
                                     _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
                                     _int, _c_void_p]),
+    "ss_decode_plan": (_int, [_int, _i64, _int, _int, _i64, _int, _i64, _int,
+                              ctypes.POINTER(_int), ctypes.POINTER(_size)]),
+    "ss_decode_attn_il8": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                  _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
+                                  _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
+                                  _int, _c_void_p]),
+    "ss_append_values_il8": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                                    _c_void_p, _i64, _i64, _c_void_p]),
     "ss_decode_attn_grouped": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
@@ -154,22 +162,22 @@ def stream_handle(device: torch.device | None = None) -> int:
 
 
 # --------------------------------------------------------------------------- #
-#  Decode workspace (zero-filled once; kernels leave the counters at zero)     #
+#  Decode workspace (split-T partials)                                        #
 # --------------------------------------------------------------------------- #
 
 _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per (device, stream) scratch for split-T partials and counters.  Calls
-    on one stream are ordered, so they never overlap on the same buffer."""
+    """Per (device, stream) scratch for split-T partials.  Calls on one stream
+    are ordered, so they never overlap on the same buffer."""
     if nbytes <= 0:
         return None
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            stream_handle(device))
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _ws_cache[key] = ws
     return ws
 
@@ -298,6 +306,69 @@ def decode_attn_dense(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
         int(n_splits), stream_handle(q.device)))
     return out
+
+
+KIND_DENSE, KIND_IL8 = 0, 1
+
+
+def decode_plan(kind, batch, n_q_heads, n_kv_heads, t_q, head_dim, t_kv, n_splits=0):
+    """(splits, workspace_bytes) a decode call of ``kind`` would use."""
+    sp = _int(0)
+    wb = _size(0)
+    check(load_library().ss_decode_plan(kind, batch, n_q_heads, n_kv_heads, t_q, head_dim, t_kv,
+                                        n_splits, ctypes.byref(sp), ctypes.byref(wb)))
+    return int(sp.value), int(wb.value)
+
+
+def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                    centroids: torch.Tensor, idx: torch.Tensor, values_il8: torch.Tensor,
+                    t_kv: int, causal: bool = False, q_offset: int = 0,
+                    out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                    n_splits: int = 0) -> torch.Tensor:
+    """Fused decode (MFMA P.V) over fp16 values in the 8-token interleaved
+    layout ``values_il8`` (B, Hkv, cap/8, D, 8)."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(values_il8)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
+    ws = decode_workspace(q.device, ws_bytes)
+    check(load_library().ss_decode_attn_il8(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv), int(bool(causal)),
+        int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
+        int(n_splits), stream_handle(q.device)))
+    return out
+
+
+def append_values_il8(values: torch.Tensor, out_il8: torch.Tensor, offset: int) -> None:
+    """Write (B, H, T, D) values at cache positions [offset, offset+T) of the
+    interleaved buffer (B, H, cap/8, D, 8)."""
+    require_gpu(values, out_il8)
+    if values.dim() != 4 or values.stride(-1) != 1:
+        raise ValueError("values must be (B, H, T, D) with unit last stride")
+    if out_il8.dim() != 5 or out_il8.dtype != torch.float16 or not out_il8.is_contiguous():
+        raise ValueError("out_il8 must be a contiguous float16 (B, H, cap/8, D, 8) buffer")
+    b_, h_, t_, d = values.shape
+    if tuple(out_il8.shape[:2]) != (b_, h_) or out_il8.shape[3] != d:
+        raise ValueError("values and cache shapes differ")
+    cap = out_il8.shape[2] * 8
+    check(load_library().ss_append_values_il8(
+        ptr(values), dtype_code(values.dtype), b_, h_, t_, values.stride(0), values.stride(1),
+        values.stride(2), d, ptr(out_il8), cap, int(offset), stream_handle(values.device)))
+
+
+def il8_to_dense(values_il8: torch.Tensor, t_kv: int | None = None) -> torch.Tensor:
+    """(B, H, cap/8, D, 8) interleaved -> (B, H, cap, D) token-major copy."""
+    b_, h_, c8, d, _ = values_il8.shape
+    dense = values_il8.permute(0, 1, 2, 4, 3).reshape(b_, h_, c8 * 8, d)
+    return dense[:, :, :t_kv] if t_kv is not None else dense
 
 
 def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None,

@@ -1,0 +1,572 @@
+"""SunShape KV caches on device memory (reference cache.py:1-1108).
+
+``SunShapeKVCache``: keys as uint8 block-VQ indices (B, H, cap, n_blocks),
+values in fp16 (B, H, cap, D).  ``HybridSunShapeKVCache``: a full-precision
+recent-token buffer plus compressed storage whose value backend is fp16,
+grouped 2/3/4-bit, TurboQuant or SunShape block-VQ.
+
+Layout and growth follow the reference: capacity is a multiple of 256 tokens
+and grows as needed, the first ``offset`` tokens of each (batch, head) row are
+valid.  Everything stays on the GPU: appends are one encode launch for every
+(batch, head) straight into the cache rows (the reference round-trips
+through host NumPy arrays), and ``max_tokens`` preallocates the whole
+capacity up front so a long decode never regrows.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+from .codec import PERM_MODES, SunShapeBlockCodec
+from .value_codecs import GroupedValueCodec, TurboQuantValueCodec, build_value_codec
+
+_STEP = 256
+_DEFAULT_BUFFER_SIZE = 128
+
+
+def _round_capacity(n: int) -> int:
+    return ((n + _STEP - 1) // _STEP) * _STEP
+
+
+def _packed_dim(head_dim: int, bits: int) -> int:
+    """uint32 words per row (reference cache.py:39-56)."""
+    if bits == 2:
+        if head_dim % 16 != 0:
+            raise ValueError(f"head_dim must be divisible by 16 for 2-bit packing, got {head_dim}")
+        return head_dim // 16
+    if bits == 3:
+        return (head_dim + 9) // 10
+    if bits == 4:
+        if head_dim % 8 != 0:
+            raise ValueError(f"head_dim must be divisible by 8 for 4-bit packing, got {head_dim}")
+        return head_dim // 8
+    raise ValueError(f"Unsupported bits: {bits} (must be 2, 3, or 4)")
+
+
+def _grow(buf: torch.Tensor | None, shape, dtype, device, keep: int) -> torch.Tensor:
+    """New zeroed buffer of ``shape`` holding the first ``keep`` tokens of ``buf``."""
+    new = torch.zeros(shape, dtype=dtype, device=device)
+    if buf is not None and keep > 0:
+        new[:, :, :keep] = buf[:, :, :keep]
+    return new
+
+
+def _encode_into(codec: SunShapeBlockCodec, keys: torch.Tensor, out: torch.Tensor) -> None:
+    """Encode (B, H, T, D) keys into the (B, H, T, n_blocks) uint8 view ``out``."""
+    if codec.mode == "profileperm_baseline" and codec.n_centroids <= 256:
+        k = keys if keys.stride(-1) == 1 else keys.contiguous()
+        _hip.encode_blockvq(k, codec.permutation, codec.centroids, out, codec.block_dim)
+        return
+    b_, h_, t_, d = keys.shape
+    q = codec.quantize(keys.reshape(-1, d))
+    out.copy_(q.indices.reshape(b_, h_, t_, -1).to(out.dtype))
+
+
+def _dequantize_keys(codec: SunShapeBlockCodec, idx: torch.Tensor) -> torch.Tensor:
+    """(B, H, T, NB) indices -> (B, H, T, D) float32 keys in the original basis
+    (reference cache.py:211-240)."""
+    b_, h_, t_, nb = idx.shape
+    flat = idx.reshape(-1, nb).contiguous()
+    inv = codec.inv_permutation if codec.mode in PERM_MODES else None
+    k = _hip.dequantize_blockvq(flat, codec.centroids, inv)
+    if codec.use_rotation:
+        k = k @ codec.rotation
+    return k.reshape(b_, h_, t_, codec.head_dim)
+
+
+class SunShapeKVCache:
+    """Block-VQ keys + fp16 values; drop-in for mlx-lm's KVCache protocol
+    (reference cache.py:59-336)."""
+
+    def __init__(self, codec: SunShapeBlockCodec, *, n_kv_heads: int = 1,
+                 head_dim: int | None = None, dtype: torch.dtype = torch.float16,
+                 max_tokens: int | None = None, return_dequantized_keys: bool = True):
+        self.codec = codec
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim or codec.head_dim
+        self.block_dim = codec.block_dim
+        self.n_blocks = codec.n_blocks
+        self.n_centroids = codec.n_centroids
+        self.dtype = dtype
+        self.offset = 0
+        self.max_tokens = max_tokens
+        # The reference returns dequantised keys from update_and_fetch (an
+        # O(T) reconstruction per call that the patched SDPA never reads);
+        # serving loops can switch it off.
+        self.return_dequantized_keys = return_dequantized_keys
+        self._key_indices: torch.Tensor | None = None  # (B, H, cap, NB) uint8
+        self._values: torch.Tensor | None = None       # (B, H, cap, D) dtype
+        self._capacity = 0
+
+    # -------------------------------------------------------------- storage
+    def _ensure_capacity(self, b_: int, new_tokens: int, device) -> None:
+        needed = self.offset + new_tokens
+        if needed <= self._capacity and self._key_indices is not None:
+            return
+        cap = _round_capacity(max(needed, self.max_tokens or 0))
+        self._key_indices = _grow(self._key_indices, (b_, self.n_kv_heads, cap, self.n_blocks),
+                                  torch.uint8, device, self.offset)
+        self._values = _grow(self._values, (b_, self.n_kv_heads, cap, self.head_dim), self.dtype,
+                             device, self.offset)
+        self._capacity = cap
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        """Encode new keys into the index cache, append values (reference
+        cache.py:156-205).  Returns ``(keys, values)`` as stored: dequantised
+        keys (float32) unless ``return_dequantized_keys`` is off (then None)."""
+        b_, h_, t_, d = keys.shape
+        assert h_ == self.n_kv_heads, f"Expected {self.n_kv_heads} kv heads, got {h_}"
+        assert d == self.head_dim, f"Expected head_dim {self.head_dim}, got {d}"
+        _hip.require_gpu(keys, values)
+        self._ensure_capacity(b_, t_, keys.device)
+        sl = slice(self.offset, self.offset + t_)
+        _encode_into(self.codec, keys, self._key_indices[:, :, sl])
+        self._values[:, :, sl] = values.to(self.dtype)
+        self.offset += t_
+        return (self.keys if self.return_dequantized_keys else None), self.values
+
+    # ----------------------------------------------------------- accessors
+    @property
+    def keys(self) -> torch.Tensor:
+        """Dequantised keys up to ``offset`` (float32)."""
+        if self._key_indices is None or self.offset == 0:
+            dev = self.codec.device
+            return torch.zeros((1, self.n_kv_heads, 0, self.head_dim), dtype=torch.float32,
+                               device=dev)
+        return _dequantize_keys(self.codec, self._key_indices[:, :, :self.offset])
+
+    @property
+    def values(self) -> torch.Tensor:
+        if self._values is None or self.offset == 0:
+            return torch.zeros((1, self.n_kv_heads, 0, self.head_dim), dtype=self.dtype,
+                               device=self.codec.device)
+        return self._values[:, :, :self.offset]
+
+    @property
+    def key_indices(self) -> torch.Tensor:
+        if self._key_indices is None or self.offset == 0:
+            return torch.zeros((1, self.n_kv_heads, 0, self.n_blocks), dtype=torch.uint8,
+                               device=self.codec.device)
+        return self._key_indices[:, :, :self.offset]
+
+    @property
+    def state(self):
+        z = torch.zeros((1,))
+        return (self._key_indices[:, :, :self.offset] if self._key_indices is not None else z,
+                self._values[:, :, :self.offset] if self._values is not None else z)
+
+    # -------------------------------------------------------------- metrics
+    @property
+    def nbytes(self) -> int:
+        if self._key_indices is None:
+            return 0
+        b_, t_ = self._key_indices.shape[0], self.offset
+        idx_bytes = b_ * self.n_kv_heads * t_ * self.n_blocks * (1 if self.n_centroids <= 256 else 2)
+        return idx_bytes + b_ * self.n_kv_heads * t_ * self.head_dim * 2
+
+    @property
+    def nbytes_equivalent_fp16(self) -> int:
+        if self.offset == 0:
+            return 0
+        b_ = self._key_indices.shape[0] if self._key_indices is not None else 1
+        return 2 * b_ * self.n_kv_heads * self.offset * self.head_dim * 2
+
+    @property
+    def compression_ratio(self) -> float:
+        fp16 = self.nbytes_equivalent_fp16
+        return 1.0 if fp16 == 0 else fp16 / max(1, self.nbytes)
+
+    # ---------------------------------------------------- mlx-lm protocol
+    def is_trimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int) -> None:
+        self.offset = max(0, self.offset - n)
+
+    def empty(self) -> bool:
+        return self.offset == 0
+
+    def make_mask(self, N: int, return_array: bool = False, window_size: int | None = None,
+                  **kwargs):
+        return _make_mask(self.offset, N, return_array, self.codec.device)
+
+    def __repr__(self) -> str:
+        return (f"SunShapeKVCache(offset={self.offset}, head_dim={self.head_dim}, "
+                f"n_blocks={self.n_blocks}, n_centroids={self.n_centroids}, "
+                f"compression={self.compression_ratio:.1f}x)")
+
+
+def _make_mask(t_: int, n: int, return_array: bool, device):
+    """Causal mask for N new queries at positions [T, T+N) over keys [0, T+N)
+    (reference cache.py:310-329)."""
+    if t_ == 0 and n == 0:
+        return "none"
+    if not return_array:
+        return "causal"
+    q_pos = torch.arange(t_, t_ + n, device=device)
+    k_pos = torch.arange(t_ + n, device=device)
+    causal = q_pos[:, None] >= k_pos[None, :]
+    return torch.where(causal, torch.tensor(0.0, device=device),
+                       torch.tensor(torch.finfo(torch.float16).min, device=device)).to(torch.float16)
+
+
+class HybridSunShapeKVCache:
+    """Recent tokens in a full-precision buffer, older tokens compressed
+    (reference cache.py:348-998).  ``value_scale_dtype`` selects how grouped
+    scale/zero pairs are stored (float32 as the reference, or float16)."""
+
+    def __init__(self, codec: SunShapeBlockCodec, *, n_kv_heads: int = 1,
+                 head_dim: int | None = None, dtype: torch.dtype = torch.float16,
+                 buffer_size: int = _DEFAULT_BUFFER_SIZE, value_backend: str | None = None,
+                 value_bits: int | None = None, value_group_size: int = 64, value_seed: int = 43,
+                 value_codec: SunShapeBlockCodec | None = None, prefer_metal_kernels: bool = True,
+                 value_scale_dtype: torch.dtype = torch.float32, max_tokens: int | None = None):
+        self.codec = codec
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim or codec.head_dim
+        self.block_dim = codec.block_dim
+        self.n_blocks = codec.n_blocks
+        self.n_centroids = codec.n_centroids
+        self.dtype = dtype
+        self.buffer_size = buffer_size
+        self.value_backend = value_backend or ("fp16" if value_bits is None else "grouped")
+        self.value_bits = value_bits
+        self.value_group_size = value_group_size
+        self.value_seed = value_seed
+        self.prefer_metal_kernels = prefer_metal_kernels
+        self.value_codec = value_codec
+        self.value_scale_dtype = value_scale_dtype
+        self.max_tokens = max_tokens
+        self.last_value_quant_backend = "none"
+        if self.value_backend not in {"fp16", "grouped", "turboquant", "sunshape"}:
+            raise ValueError(f"Unsupported value backend: {self.value_backend}")
+        if self.value_backend != "fp16" and self.value_bits is None:
+            raise ValueError(f"value_bits is required for value backend {self.value_backend}")
+        if self.value_backend == "grouped" and self.head_dim % self.value_group_size != 0:
+            raise ValueError(f"head_dim ({self.head_dim}) must be divisible by "
+                             f"value_group_size ({self.value_group_size}) for value quantization")
+        if value_scale_dtype not in (torch.float32, torch.float16):
+            raise ValueError("value_scale_dtype must be float32 or float16")
+        if self.value_backend == "sunshape":
+            self.value_codec = self.value_codec or codec
+            if self.value_codec.head_dim != self.head_dim:
+                raise ValueError("SunShape value codec head_dim must match cache head_dim")
+            self.value_n_blocks = self.value_codec.n_blocks
+            self.value_n_centroids = self.value_codec.n_centroids
+        else:
+            self.value_n_blocks = 0
+            self.value_n_centroids = 0
+        self._value_codec_impl = None if self.value_backend == "sunshape" else build_value_codec(
+            self.value_backend, head_dim=self.head_dim, value_bits=self.value_bits or 0,
+            value_group_size=self.value_group_size, value_seed=self.value_seed,
+            prefer_metal=self.prefer_metal_kernels)
+        self._compressed_offset = 0
+        self._buffer_offset = 0
+        self._key_buffer: torch.Tensor | None = None
+        self._value_buffer: torch.Tensor | None = None
+        self._key_indices: torch.Tensor | None = None
+        self._values_packed: torch.Tensor | None = None
+        self._value_scales: torch.Tensor | None = None
+        self._value_zeros: torch.Tensor | None = None
+        self._value_norms: torch.Tensor | None = None
+        self._value_indices: torch.Tensor | None = None
+        self._values_fp16: torch.Tensor | None = None
+        self._value_n_groups = 0
+        self._compressed_capacity = 0
+
+    @property
+    def offset(self) -> int:
+        return self._compressed_offset + self._buffer_offset
+
+    # ------------------------------------------------------------ storage
+    def _grow_compressed(self, b_: int, needed: int, device) -> None:
+        if needed <= self._compressed_capacity and self._key_indices is not None:
+            return
+        cap = _round_capacity(max(needed, self.max_tokens or 0))
+        keep = self._compressed_offset
+        h_ = self.n_kv_heads
+        self._key_indices = _grow(self._key_indices, (b_, h_, cap, self.n_blocks), torch.uint8,
+                                  device, keep)
+        if self.value_backend == "grouped":
+            gc = self._value_codec_impl
+            self._value_n_groups = gc.n_groups
+            self._values_packed = _grow(self._values_packed, (b_, h_, cap, gc.packed_dim),
+                                        torch.int32, device, keep)
+            self._value_scales = _grow(self._value_scales, (b_, h_, cap, gc.n_groups),
+                                       self.value_scale_dtype, device, keep)
+            self._value_zeros = _grow(self._value_zeros, (b_, h_, cap, gc.n_groups),
+                                      self.value_scale_dtype, device, keep)
+        elif self.value_backend == "turboquant":
+            tc = self._value_codec_impl
+            self._values_packed = _grow(self._values_packed, (b_, h_, cap, tc.packed_dim),
+                                        torch.int32, device, keep)
+            norms = self._value_norms
+            self._value_norms = torch.zeros((b_, h_, cap), dtype=torch.float32, device=device)
+            if norms is not None and keep:
+                self._value_norms[:, :, :keep] = norms[:, :, :keep]
+        elif self.value_backend == "sunshape":
+            self._value_indices = _grow(self._value_indices, (b_, h_, cap, self.value_n_blocks),
+                                        torch.uint8, device, keep)
+        else:
+            self._values_fp16 = _grow(self._values_fp16, (b_, h_, cap, self.head_dim),
+                                      self.dtype, device, keep)
+        self._compressed_capacity = cap
+
+    def _flush_buffer(self, b_: int, n_to_flush: int) -> None:
+        """Move the oldest tokens of the buffer into compressed storage
+        (reference cache.py:463-650)."""
+        if n_to_flush <= 0 or self._key_buffer is None:
+            return
+        n = min(n_to_flush, self._buffer_offset)
+        if n == 0:
+            return
+        dev = self._key_buffer.device
+        self._grow_compressed(b_, self._compressed_offset + n, dev)
+        c0, c1 = self._compressed_offset, self._compressed_offset + n
+        kf = self._key_buffer[:, :, :n]
+        vf = self._value_buffer[:, :, :n]
+        _encode_into(self.codec, kf, self._key_indices[:, :, c0:c1])
+        if self.value_backend == "grouped":
+            gc = self._value_codec_impl
+            _hip.quantize_values_grouped(vf, gc.bits, gc.group_size,
+                                         self._values_packed[:, :, c0:c1],
+                                         self._value_scales[:, :, c0:c1],
+                                         self._value_zeros[:, :, c0:c1])
+            self.last_value_quant_backend = "hip"
+        elif self.value_backend == "turboquant":
+            tc = self._value_codec_impl
+            packed, norms = tc.quantize(vf.float().reshape(-1, self.head_dim))
+            self._values_packed[:, :, c0:c1] = packed.view(torch.int32).reshape(
+                b_, self.n_kv_heads, n, -1)
+            self._value_norms[:, :, c0:c1] = norms.reshape(b_, self.n_kv_heads, n)
+            self.last_value_quant_backend = tc.last_quantize_backend
+        elif self.value_backend == "sunshape":
+            _encode_into(self.value_codec, vf, self._value_indices[:, :, c0:c1])
+            self.last_value_quant_backend = "sunshape"
+        else:
+            self._values_fp16[:, :, c0:c1] = vf.to(self.dtype)
+            self.last_value_quant_backend = "fp16"
+        remaining = self._buffer_offset - n
+        if remaining > 0:
+            self._key_buffer[:, :, :remaining] = self._key_buffer[:, :, n:n + remaining].clone()
+            self._value_buffer[:, :, :remaining] = self._value_buffer[:, :, n:n + remaining].clone()
+        self._key_buffer[:, :, remaining:] = 0
+        self._value_buffer[:, :, remaining:] = 0
+        self._compressed_offset = c1
+        self._buffer_offset = remaining
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        """Append to the buffer; flush the overflow beyond ``buffer_size``
+        (reference cache.py:656-710)."""
+        b_, h_, t_, d = keys.shape
+        assert h_ == self.n_kv_heads
+        assert d == self.head_dim
+        _hip.require_gpu(keys, values)
+        dev = keys.device
+        if self._key_buffer is None:
+            size = max(self.buffer_size, t_)
+            self._key_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
+            self._value_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
+        if self._buffer_offset + t_ > self._key_buffer.shape[2]:
+            size = max(self._buffer_offset + t_, self._key_buffer.shape[2] * 2)
+            self._key_buffer = _grow(self._key_buffer, (b_, h_, size, d), self.dtype, dev,
+                                     self._buffer_offset)
+            self._value_buffer = _grow(self._value_buffer, (b_, h_, size, d), self.dtype, dev,
+                                       self._buffer_offset)
+        sl = slice(self._buffer_offset, self._buffer_offset + t_)
+        self._key_buffer[:, :, sl] = keys.to(self.dtype)
+        self._value_buffer[:, :, sl] = values.to(self.dtype)
+        self._buffer_offset += t_
+        if self._buffer_offset > self.buffer_size:
+            self._flush_buffer(b_, self._buffer_offset - self.buffer_size)
+        return self.keys, self.values
+
+    # ---------------------------------------------------------- accessors
+    def _zeros(self, last: int, dtype) -> torch.Tensor:
+        return torch.zeros((1, self.n_kv_heads, 0, last), dtype=dtype, device=self.codec.device)
+
+    @property
+    def keys(self) -> torch.Tensor:
+        parts = []
+        if self._compressed_offset > 0 and self._key_indices is not None:
+            parts.append(_dequantize_keys(self.codec,
+                                          self._key_indices[:, :, :self._compressed_offset]))
+        if self._buffer_offset > 0 and self._key_buffer is not None:
+            parts.append(self._key_buffer[:, :, :self._buffer_offset].float())
+        if not parts:
+            return self._zeros(self.head_dim, torch.float32)
+        return torch.cat(parts, dim=2)
+
+    def _compressed_values(self) -> torch.Tensor | None:
+        tc_ = self._compressed_offset
+        if tc_ == 0:
+            return None
+        if self.value_backend == "grouped" and self._values_packed is not None:
+            gc = self._value_codec_impl
+            v = _hip.dequantize_values_grouped(self._values_packed[:, :, :tc_].view(torch.uint32),
+                                               self._value_scales[:, :, :tc_],
+                                               self._value_zeros[:, :, :tc_], self.head_dim,
+                                               gc.bits, gc.group_size)
+            return v.to(self.dtype)
+        if self.value_backend == "turboquant" and self._values_packed is not None:
+            tc = self._value_codec_impl
+            p = self._values_packed[:, :, :tc_].view(torch.uint32)
+            v = tc.dequantize(p.reshape(-1, p.shape[-1]), self._value_norms[:, :, :tc_].reshape(-1))
+            return v.reshape(p.shape[0], p.shape[1], tc_, self.head_dim).to(self.dtype)
+        if self.value_backend == "sunshape" and self._value_indices is not None:
+            return _dequantize_keys(self.value_codec,
+                                    self._value_indices[:, :, :tc_]).to(self.dtype)
+        if self._values_fp16 is not None:
+            return self._values_fp16[:, :, :tc_]
+        return None
+
+    @property
+    def values(self) -> torch.Tensor:
+        parts = []
+        cv = self._compressed_values()
+        if cv is not None:
+            parts.append(cv)
+        if self._buffer_offset > 0 and self._value_buffer is not None:
+            parts.append(self._value_buffer[:, :, :self._buffer_offset])
+        if not parts:
+            return self._zeros(self.head_dim, self.dtype)
+        return torch.cat(parts, dim=2)
+
+    @property
+    def key_indices(self) -> torch.Tensor:
+        if self._key_indices is None or self._compressed_offset == 0:
+            return self._zeros(self.n_blocks, torch.uint8)
+        return self._key_indices[:, :, :self._compressed_offset]
+
+    @property
+    def buffer_keys(self) -> torch.Tensor:
+        if self._key_buffer is None or self._buffer_offset == 0:
+            return self._zeros(self.head_dim, self.dtype)
+        return self._key_buffer[:, :, :self._buffer_offset]
+
+    @property
+    def buffer_values(self) -> torch.Tensor:
+        if self._value_buffer is None or self._buffer_offset == 0:
+            return self._zeros(self.head_dim, self.dtype)
+        return self._value_buffer[:, :, :self._buffer_offset]
+
+    @property
+    def compressed_offset(self) -> int:
+        return self._compressed_offset
+
+    @property
+    def buffer_offset(self) -> int:
+        return self._buffer_offset
+
+    @property
+    def values_packed_raw(self):
+        if self.value_backend != "grouped" or self._values_packed is None \
+                or self._compressed_offset == 0:
+            return None
+        return self._values_packed[:, :, :self._compressed_offset].view(torch.uint32)
+
+    @property
+    def value_scales_raw(self):
+        if self.value_backend != "grouped" or self._value_scales is None \
+                or self._compressed_offset == 0:
+            return None
+        return self._value_scales[:, :, :self._compressed_offset]
+
+    @property
+    def value_zeros_raw(self):
+        if self.value_backend != "grouped" or self._value_zeros is None \
+                or self._compressed_offset == 0:
+            return None
+        return self._value_zeros[:, :, :self._compressed_offset]
+
+    @property
+    def can_fuse_value_dequant(self) -> bool:
+        return (self.value_backend == "grouped" and self._compressed_offset > 0
+                and self._values_packed is not None and self._value_scales is not None
+                and self._value_zeros is not None)
+
+    # ------------------------------------------------------------ metrics
+    @property
+    def nbytes(self) -> int:
+        """Storage bytes with B taken as 1, as the reference does
+        (cache.py:904-928)."""
+        c, h_ = self._compressed_offset, self.n_kv_heads
+        idx_bytes = h_ * c * self.n_blocks * (1 if self.n_centroids <= 256 else 2)
+        if self.value_backend == "grouped" and c > 0:
+            pd = _packed_dim(self.head_dim, self.value_bits)
+            sz = 4 if self.value_scale_dtype == torch.float32 else 2
+            val_bytes = h_ * c * pd * 4 + h_ * c * self._value_n_groups * sz * 2
+        elif self.value_backend == "turboquant" and c > 0:
+            val_bytes = h_ * c * _packed_dim(self.head_dim, self.value_bits) * 4 + h_ * c * 4
+        elif self.value_backend == "sunshape" and c > 0:
+            val_bytes = h_ * c * self.value_n_blocks * (1 if self.value_n_centroids <= 256 else 2)
+        else:
+            val_bytes = h_ * c * self.head_dim * 2
+        return idx_bytes + val_bytes + h_ * self._buffer_offset * self.head_dim * 2 * 2
+
+    @property
+    def nbytes_equivalent_fp16(self) -> int:
+        return 0 if self.offset == 0 else 2 * self.n_kv_heads * self.offset * self.head_dim * 2
+
+    @property
+    def compression_ratio(self) -> float:
+        fp16 = self.nbytes_equivalent_fp16
+        return 1.0 if fp16 == 0 else fp16 / max(1, self.nbytes)
+
+    # ---------------------------------------------------- mlx-lm protocol
+    def is_trimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int) -> None:
+        """Trim the buffer first, then compressed storage (cache.py:954-963)."""
+        if n <= 0:
+            return
+        b = min(n, self._buffer_offset)
+        self._buffer_offset -= b
+        rest = n - b
+        if rest > 0:
+            self._compressed_offset = max(0, self._compressed_offset - rest)
+
+    def empty(self) -> bool:
+        return self.offset == 0
+
+    def make_mask(self, N: int, return_array: bool = False, window_size: int | None = None,
+                  **kwargs):
+        return _make_mask(self.offset, N, return_array, self.codec.device)
+
+    def __repr__(self) -> str:
+        return (f"HybridSunShapeKVCache(offset={self.offset}, "
+                f"compressed={self._compressed_offset}, buffer={self._buffer_offset}, "
+                f"value_backend={self.value_backend}, "
+                f"compression={self.compression_ratio:.1f}x)")
+
+    @property
+    def state(self):
+        parts = []
+        if self._key_indices is not None and self._compressed_offset > 0:
+            parts.append(self._key_indices[:, :, :self._compressed_offset])
+        if self._key_buffer is not None and self._buffer_offset > 0:
+            parts.append(self._key_buffer[:, :, :self._buffer_offset])
+        if not parts:
+            parts.append(torch.zeros((1,)))
+        return tuple(parts)
+
+
+def create_kv_cache(codec: SunShapeBlockCodec, *, n_kv_heads: int = 1, head_dim: int | None = None,
+                    dtype: torch.dtype = torch.float16, value_backend: str = "fp16",
+                    value_bits: int | None = None, value_group_size: int = 64,
+                    value_seed: int = 43, value_codec: SunShapeBlockCodec | None = None,
+                    buffer_size: int = _DEFAULT_BUFFER_SIZE, prefer_metal_kernels: bool = True,
+                    **kwargs):
+    """Factory (reference cache.py:1006-1107): fp16 values with the default
+    buffer -> ``SunShapeKVCache``; anything else -> ``HybridSunShapeKVCache``.
+    Extra keywords (``max_tokens``, ``value_scale_dtype``) pass through."""
+    if value_backend == "fp16" and buffer_size == _DEFAULT_BUFFER_SIZE:
+        return SunShapeKVCache(codec, n_kv_heads=n_kv_heads, head_dim=head_dim, dtype=dtype,
+                               max_tokens=kwargs.get("max_tokens"))
+    return HybridSunShapeKVCache(codec, n_kv_heads=n_kv_heads, head_dim=head_dim, dtype=dtype,
+                                 buffer_size=buffer_size, value_backend=value_backend,
+                                 value_bits=value_bits, value_group_size=value_group_size,
+                                 value_seed=value_seed, value_codec=value_codec,
+                                 prefer_metal_kernels=prefer_metal_kernels, **kwargs)

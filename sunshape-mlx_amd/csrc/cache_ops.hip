@@ -1,0 +1,55 @@
+// KV-cache value layout: append tokens into the 8-token interleaved fp16 layout.
+//
+// The decode kernel's MFMA path reads values as [cap/8][head_dim][8] per
+// (batch, KV head): the 8 consecutive tokens of one dim are 16 contiguous
+// bytes, the K-major operand of v_mfma_f32_16x16x16f16.  Appending T new
+// tokens at position `offset` scatters each token's head_dim values with a
+// 16-byte stride; the index cache keeps the token-major [cap][n_blocks]
+// layout of the reference (cache.py:102-150).
+#include "ss_common.hpp"
+
+namespace ss {
+
+__global__ void __launch_bounds__(256)
+    append_il8_kernel(const void *v, int v_dtype, int64_t n_h, int64_t n_t, int64_t n_tok,
+                      int64_t v_sb, int64_t v_sh, int64_t v_st, int d, __half *out, int64_t cap,
+                      int64_t offset) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n_tok * d) return;
+    const int64_t n = e / d;
+    const int j = (int)(e - n * d);
+    const int64_t b = n / (n_h * n_t);
+    const int64_t rem = n - b * n_h * n_t;
+    const int64_t h = rem / n_t;
+    const int64_t t = rem - h * n_t;
+    const float x = load_as_f32(v, v_dtype, b * v_sb + h * v_sh + t * v_st + j);
+    const int64_t pos = offset + t;
+    const int64_t head = b * n_h + h;
+    out[((head * (cap / 8) + pos / 8) * d + j) * 8 + (pos & 7)] = __float2half(x);
+}
+
+}  // namespace ss
+
+using namespace ss;
+
+extern "C" int ss_append_values_il8(const void *values, int v_dtype, int64_t n_b, int64_t n_h,
+                                    int64_t n_t, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                                    int head_dim, void *out_il8, int64_t cap, int64_t offset,
+                                    void *stream) {
+    SS_REQUIRE(valid_dtype(v_dtype), "bad value dtype");
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0 && head_dim >= 1, "bad sizes");
+    SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8");
+    SS_REQUIRE(offset >= 0 && offset + n_t <= cap, "tokens [%lld, %lld) exceed cap %lld",
+               (long long)offset, (long long)(offset + n_t), (long long)cap);
+    const int64_t n_tok = n_b * n_h * n_t;
+    if (n_tok == 0) return SS_OK;
+    SS_REQUIRE(values && out_il8, "null pointer argument");
+    const int64_t total = n_tok * head_dim;
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(append_il8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       values, v_dtype, n_h, n_t, n_tok, v_sb, v_sh, v_st, head_dim,
+                       reinterpret_cast<__half *>(out_il8), cap, offset);
+    SS_LAUNCH_CHECK("append_il8_kernel launch");
+    return SS_OK;
+}

@@ -31,8 +31,8 @@ struct DecodeCommon {
     const float *centroids;
     const uint8_t *idx;
     void *out;
-    float *partials;
-    unsigned int *counters;
+    float *part_ml;   // [cols][splits][R] (m, l)
+    float *part_acc;  // [cols][splits][R][D]
     int q_dtype, out_dtype;
     int n_q_heads, n_kv_heads, rep, n_rg;
     int64_t t_q, rows_total;
@@ -48,6 +48,7 @@ constexpr int kDecodeThreads = 256;
 constexpr int kDecodeWaves = kDecodeThreads / kWave;
 constexpr int kLutStride = 256;  // LUT entries reserved per (row, block)
 constexpr int kBlockDim = 8;
+constexpr int kMaxSplits = 512;  // split weights of the merge live in LDS
 
 constexpr int pow2_ceil(int x) { return x <= 1 ? 1 : 2 * pow2_ceil((x + 1) / 2); }
 
@@ -203,11 +204,11 @@ __global__ void __launch_bounds__(kDecodeThreads)
     static_assert(ITERS % CHUNK == 0, "chunking");
     static_assert(kDecodeWaves * R * (D + 2) <= R * NB * kLutStride, "merge scratch");
 
+
     extern __shared__ __align__(16) float smem[];
     float *lut = smem;                          // [R][NB][kLutStride]
     float *qp = lut + R * NB * kLutStride;      // [R][D]
     float *pbuf = qp + R * D;                   // [waves][64][R]
-    __shared__ int s_last;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -422,40 +423,398 @@ __global__ void __launch_bounds__(kDecodeThreads)
         if (S == 1) {
             if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
         } else {
-            float *pp = c.partials + (((int64_t)col * S + split) * R + r) * (D + 2);
-            if (d == 0) {
-                pp[0] = M;
-                pp[1] = L;
-            }
-            pp[2 + d] = A;
+            const int64_t slot = ((int64_t)col * S + split) * R + r;
+            c.part_acc[slot * D + d] = A;
+            if (d == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
         }
     }
-    if (S == 1) return;
+}
 
-    // 5. the last workgroup of this group to finish merges all splits.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&c.counters[col], 1u) == (unsigned)(S - 1));
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int64_t sstride = (int64_t)R * (D + 2);
-    for (int i = tid; i < R * D; i += kDecodeThreads) {
-        const int r = i / D, d = i - r * D;
-        if (!row_ok(r)) continue;
-        const float *base = c.partials + ((int64_t)col * S * R + r) * (D + 2);
-        float M = -1e30f;
-        for (int s2 = 0; s2 < S; ++s2) M = fmaxf(M, base[s2 * sstride]);
-        float L = 0.f, A = 0.f;
-        for (int s2 = 0; s2 < S; ++s2) {
-            const float *pp = base + s2 * sstride;
-            const float f = fast_exp2(pp[0] - M);
-            L = fmaf(pp[1], f, L);
-            A = fmaf(pp[2 + d], f, A);
-        }
-        store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+// ---------------------------------------------------------------------------
+// MFMA variant for fp16 values stored 8-token interleaved: value element
+// (token t, dim d) of a head lives at [t / 8][d][t % 8], so one 16-byte load
+// gives a lane 8 consecutive tokens of one dim -- the K-major operand layout of
+// v_mfma_f32_16x16x16f16.  P.V runs on the matrix cores as
+// O[row][dim] = sum_t P[row][t] V[t][dim] with M = query rows, K = tokens,
+// N = dims.  P enters as an fp16 hi/lo pair (rows 0-3 hi, rows 4-7 lo) of
+// p * 2^15, which keeps ~22 mantissa bits and stays in fp16's normal range;
+// accumulation is fp32.  Four query rows (one GQA group) per workgroup.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kPScale = 32768.f;  // 2^15
+constexpr int kMfmaRows = 4;
+
+template <int D, int NW>
+constexpr size_t mfma_lds_bytes() {
+    return sizeof(float) * ((size_t)(D / kBlockDim) * kLutStride * kMfmaRows +
+                            (size_t)kMfmaRows * D) +
+           sizeof(_Float16) * (size_t)NW * 8 * kWave;
+}
+
+// Zero the fp16 values of tokens >= n_ok (0..8) in an 8-token group.
+__device__ __forceinline__ uint4 mask_tokens(uint4 u, int n_ok) {
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (2 * i) < n_ok ? 0x0000ffffu : 0u;
+        const uint32_t hi = (2 * i + 1) < n_ok ? 0xffff0000u : 0u;
+        w[i] &= (lo | hi);
     }
-    if (tid == 0) c.counters[col] = 0u;
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <int D, int NW>
+__global__ void __launch_bounds__(NW * kWave)
+    decode_attn_mfma_kernel(DecodeCommon c, const __half *v8) {
+    constexpr int R = kMfmaRows;
+    constexpr int NB = D / kBlockDim;
+    constexpr int NT = D / 16;  // MFMA N-tiles (16 dims each)
+    constexpr int THREADS = NW * kWave;
+    static_assert(NW * R * (D + 2) <= NB * kLutStride * R, "merge scratch");
+
+    extern __shared__ __align__(16) float4 smem4[];
+    float4 *lut4 = smem4;                                      // [NB][256] (4 rows)
+    float *qp = reinterpret_cast<float *>(smem4 + NB * kLutStride);  // [R][D]
+    _Float16 *pb = reinterpret_cast<_Float16 *>(qp + R * D);   // [NW][8][64]
+    float *smem = reinterpret_cast<float *>(smem4);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = tid >> 6;
+    const int col = blockIdx.y;
+    const int split = blockIdx.x;
+    const int rg = col % c.n_rg;
+    const int kvh = (col / c.n_rg) % c.n_kv_heads;
+    const int64_t bb = col / (c.n_rg * c.n_kv_heads);
+    const int64_t bh = bb * c.n_kv_heads + kvh;
+    auto row_off = [&](int r) -> int64_t {
+        const int64_t g = (int64_t)rg * R + r;
+        const int64_t rr = g / c.t_q, tq = g - rr * c.t_q;
+        return ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+    };
+    auto row_ok = [&](int r) -> bool { return (int64_t)rg * R + r < c.rows_total; };
+
+    const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
+    const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
+    const int n_tiles = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
+    const uint8_t *idx_head = c.idx + bh * c.cap * NB;
+    const __half *vhead = v8 + bh * c.cap * D;
+    const int g = lane >> 4, l16 = lane & 15;
+
+    // Tile loads: the index row of token t0 + lane and, per 32-token half s2,
+    // the 8-token block t0/8 + 4*s2 + g of dims 16n + l16 (16 bytes).
+    auto load_tile = [&](int tile, uint4 (&v)[2][NT], IdxRow<NB> &ir) {
+        const int64_t t0 = t_beg + (int64_t)tile * kWave;
+        const int64_t tk = t0 + lane;
+        ir.load(idx_head + tk * NB, tk < t_end);
+        if (t0 + kWave <= t_end) {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const __half *vb = vhead + ((t0 / 8 + 4 * s2 + g) * D + l16) * 8;
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    v[s2][n] = *reinterpret_cast<const uint4 *>(vb + n * 16 * 8);
+            }
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int64_t blk = t0 / 8 + 4 * s2 + g;
+                const int64_t nok = t_end - blk * 8;
+                const __half *vb = vhead + (blk * D + l16) * 8;
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    uint4 u = make_uint4(0u, 0u, 0u, 0u);
+                    if (nok > 0) u = *reinterpret_cast<const uint4 *>(vb + n * 16 * 8);
+                    if (nok < 8) u = mask_tokens(u, (int)max(nok, (int64_t)0));
+                    v[s2][n] = u;
+                }
+            }
+        }
+    };
+
+    // Vector-memory loads of a wave return in issue order, so the prologue's
+    // small loads (query, permutation, this thread's codebook entries) are
+    // issued and completed first, then the wave's first tile, so the LUT is
+    // built from registers while the tile streams in.  sched_barrier keeps the compiler from reordering the
+    // groups.  Afterwards each wave keeps one tile in flight; eight waves per
+    // compute unit keep ~128 KB of loads outstanding per CU.
+    constexpr int LUT_PER_THREAD = (NB * kLutStride + THREADS - 1) / THREADS;
+    const int nbc = NB * c.n_centroids;
+    // 0a. query row element and permutation index of this thread
+    float q_raw = 0.f;
+    int q_src = 0;
+    {
+        const int r = tid / D, j = tid - r * D;
+        if (tid < R * D && row_ok(r)) {
+            q_raw = load_as_f32(c.q, c.q_dtype, row_off(r) + j);
+            q_src = c.perm ? c.perm[j] : j;
+        }
+    }
+    // 0b. codebook entries e = tid + k * THREADS
+    float4 cv[LUT_PER_THREAD][2];
+#pragma unroll
+    for (int k = 0; k < LUT_PER_THREAD; ++k) {
+        const int e = tid + k * THREADS;
+        if (e < nbc) {
+            const float4 *cp = reinterpret_cast<const float4 *>(c.centroids + (int64_t)e * kBlockDim);
+            cv[k][0] = cp[0];
+            cv[k][1] = cp[1];
+        } else {
+            cv[k][0] = cv[k][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // Wait for these explicitly: the waitcnt pass merges counts
+    // conservatively across the branches around the tile loads, so a value
+    // first used after them would otherwise wait for the whole tile.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_sched_barrier(0);
+    // 0c. first tile of this wave
+    uint4 vA[2][NT];
+    IdxRow<NB> iA;
+    int tA = wv;
+    if (tA < n_tiles) load_tile(tA, vA, iA);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 1. query rows: round_to(q_dtype, q * scale) (attention.py:208), then
+    //    the codec permutation (attention.py:228), gathered through LDS
+    float *qraw = reinterpret_cast<float *>(pb);  // [R][D] staging (pb is free here)
+    if (tid < R * D) qraw[tid] = round_to(c.q_dtype, q_raw * c.scale);
+    __syncthreads();
+    if (tid < R * D) {
+        const int r = tid / D;
+        qp[tid] = qraw[r * D + q_src];
+    }
+    __syncthreads();
+    // 2. LUT entry (b, c) holds the 4 rows' dot products, in log2 units
+#pragma unroll
+    for (int k = 0; k < LUT_PER_THREAD; ++k) {
+        const int e = tid + k * THREADS;
+        if (e < nbc) {
+            const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
+            const float4 c0 = cv[k][0], c1 = cv[k][1];
+            float dot[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float *qr = qp + r * D + b * kBlockDim;
+                float d0 = qr[0] * c0.x;
+                d0 = fmaf(qr[1], c0.y, d0);
+                d0 = fmaf(qr[2], c0.z, d0);
+                d0 = fmaf(qr[3], c0.w, d0);
+                d0 = fmaf(qr[4], c1.x, d0);
+                d0 = fmaf(qr[5], c1.y, d0);
+                d0 = fmaf(qr[6], c1.z, d0);
+                d0 = fmaf(qr[7], c1.w, d0);
+                dot[r] = d0 * kLog2e;
+            }
+            lut4[b * kLutStride + cc] = make_float4(dot[0], dot[1], dot[2], dot[3]);
+        }
+    }
+    __syncthreads();
+
+    int64_t lim[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t gr = (int64_t)rg * R + r;
+        lim[r] = !row_ok(r) ? -1 : (c.causal ? c.q_offset + (gr % c.t_q) : INT64_MAX);
+    }
+    f32x4 acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m[R], lsum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -1e30f;
+        lsum[r] = 0.f;
+    }
+    _Float16 *pw = pb + wv * 8 * kWave;
+    const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
+
+    // 3. one 64-token tile: scores from the LUT, online softmax, P.V on MFMA
+    auto process = [&](int tile, const uint4 (&v)[2][NT], const IdxRow<NB> &ir) {
+        const int64_t tk = t_beg + (int64_t)tile * kWave + lane;
+        const bool kok = tk < t_end;
+        float s[R] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float4 e = lut4[b * kLutStride + ir.at(b)];
+            s[0] += e.x;
+            s[1] += e.y;
+            s[2] += e.z;
+            s[3] += e.w;
+        }
+        float corr[R];
+        bool any_corr = false;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float sc = (kok && tk <= lim[r]) ? s[r] : -INFINITY;
+            const float mn = fmaxf(m[r], wave_max_dpp(sc));
+            corr[r] = fast_exp2(m[r] - mn);
+            any_corr |= corr[r] != 1.f;
+            const float p = fast_exp2(sc - mn);
+            lsum[r] = fmaf(lsum[r], corr[r], p);
+            m[r] = mn;
+            const float x = p * kPScale;
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            pw[r * kWave + lane] = hi;
+            pw[(r + 4) * kWave + lane] = lo;
+        }
+        wave_lds_sync();
+        if (any_corr) {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                acc[n][0] *= corr[0];
+                acc[n][1] *= corr[1];
+                acc[n][2] *= corr[2];
+                acc[n][3] *= corr[3];
+            }
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f16x4 a = f16x4{0, 0, 0, 0};
+                if (a_live)
+                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * j);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const uint4 u = v[s2][n];
+                    uint2 h = j == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
+                    const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
+                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
+                }
+            }
+        }
+        wave_lds_sync();
+    };
+
+    // 4. stream this split's tiles, one in flight per wave
+    while (tA < n_tiles) {
+        process(tA, vA, iA);
+        tA += NW;
+        if (tA < n_tiles) load_tile(tA, vA, iA);
+    }
+
+    // 5. wave results: lanes 0-15 hold rows 0-3 (hi) of dims 16n + l16,
+    //    lanes 16-31 the lo parts of the same rows
+    float out_r[R][NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = acc[n][r];
+            out_r[r][n] = (v + __shfl_down(v, 16)) * (1.f / kPScale);
+        }
+#pragma unroll
+    for (int r = 0; r < R; ++r) lsum[r] = wave_sum_dpp(lsum[r]);
+    __syncthreads();  // LUT no longer read; reuse it for the workgroup merge
+    float *wm = smem;
+    float *wl = wm + NW * R;
+    float *wa = wl + NW * R;  // [NW][R][D]
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wm[wv * R + r] = m[r];
+            wl[wv * R + r] = lsum[r];
+        }
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) wa[(wv * R + r) * D + 16 * n + lane] = out_r[r][n];
+    }
+    __syncthreads();
+    const int S = c.n_splits;
+    for (int i = tid; i < R * D; i += THREADS) {
+        const int r = i / D, d = i - r * D;
+        float M = -1e30f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w * R + r]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float f = fast_exp2(wm[w * R + r] - M);
+            L = fmaf(wl[w * R + r], f, L);
+            A = fmaf(wa[(w * R + r) * D + d], f, A);
+        }
+        if (S == 1) {
+            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+        } else {
+            const int64_t slot = ((int64_t)col * S + split) * R + r;
+            c.part_acc[slot * D + d] = A;
+            if (d == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
+        }
+    }
+}
+
+// Merge of split-T partials: one workgroup per (group, row).  One wave turns
+// the splits' (m, l) into weights exp2(m_s - M) and the merged l; every thread
+// then streams float4 slices of the accumulators of a subset of splits (loads
+// issued back to back) and the slices are reduced in LDS.  Runs as its own
+// launch: a cross-workgroup hand-off inside one kernel needs an agent-scope L2
+// write-back per workgroup on multi-XCD CDNA parts.
+template <int D>
+__global__ void __launch_bounds__(kDecodeThreads) decode_merge_kernel(DecodeCommon c, int R) {
+    constexpr int CH = D / 4;                // float4 chunks of one output row
+    constexpr int NP = kDecodeThreads / CH;  // split partitions
+    __shared__ float wsh[kMaxSplits];
+    __shared__ float lsh;
+    __shared__ float4 red[NP * CH];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid >> 6;
+    const int col = blockIdx.x, r = blockIdx.y;
+    const int64_t gr = (int64_t)(col % c.n_rg) * R + r;
+    if (gr >= c.rows_total) return;  // uniform over the workgroup
+    const int S = c.n_splits;
+    const int kvh = (col / c.n_rg) % c.n_kv_heads;
+    const int64_t bb = col / (c.n_rg * c.n_kv_heads);
+    const float *ml = c.part_ml + ((int64_t)col * S * R + r) * 2;
+    if (wv == 0) {
+        float M = -1e30f;
+        for (int s2 = lane; s2 < S; s2 += kWave) M = fmaxf(M, ml[(int64_t)s2 * R * 2]);
+        M = wave_max(M);
+        float L = 0.f;
+        for (int s2 = lane; s2 < S; s2 += kWave) {
+            const float2 v = *reinterpret_cast<const float2 *>(ml + (int64_t)s2 * R * 2);
+            const float w = fast_exp2(v.x - M);
+            wsh[s2] = w;
+            L = fmaf(v.y, w, L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) lsh = L;
+    }
+    __syncthreads();
+    {
+        const int chunk = tid % CH, part = tid / CH;
+        const float4 *ap =
+            reinterpret_cast<const float4 *>(c.part_acc + ((int64_t)col * S * R + r) * D) + chunk;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int s2 = part; s2 < S; s2 += NP) {
+            const float4 v = ap[(int64_t)s2 * R * CH];
+            const float w = wsh[s2];
+            a.x = fmaf(v.x, w, a.x);
+            a.y = fmaf(v.y, w, a.y);
+            a.z = fmaf(v.z, w, a.z);
+            a.w = fmaf(v.w, w, a.w);
+        }
+        red[part * CH + chunk] = a;
+    }
+    __syncthreads();
+    if (tid < D) {
+        const int d = tid, chunk = d >> 2;
+        float A = 0.f;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float4 v = red[p * CH + chunk];
+            A += (d & 3) == 0 ? v.x : (d & 3) == 1 ? v.y : (d & 3) == 2 ? v.z : v.w;
+        }
+        const int64_t rr = gr / c.t_q, tq = gr - rr * c.t_q;
+        const int64_t off = ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+        store_from_f32(c.out, c.out_dtype, off + d, lsh > 0.f ? A / lsh : 0.f);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -467,35 +826,84 @@ struct DecodeShape {
 
 static int rows_per_group(int64_t rows_total) { return rows_total <= 1 ? 1 : 4; }
 
+// Kernel families: the VALU kernel (any value layout/dtype, 4 waves per
+// workgroup, 1 or 4 rows) and the MFMA kernel (fp16 values 8-token
+// interleaved, kMfmaWaves waves, 4 rows).
+enum DecodeKind { kKindValu = 0, kKindMfma = 1 };
+constexpr int kMfmaWaves = 8;
+
 static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int64_t t_kv,
-                                int n_splits) {
+                                int n_splits, int kind = kKindValu) {
     DecodeShape s;
     const int64_t rows = (int64_t)(hq / hkv) * t_q;
-    s.R = rows_per_group(rows);
+    s.R = kind == kKindMfma ? kMfmaRows : rows_per_group(rows);
     s.n_rg = (int)((rows + s.R - 1) / s.R);
     s.n_cols = (int)(batch * hkv * s.n_rg);
     const int64_t tiles = (t_kv + kWave - 1) / kWave;
+    const int waves = kind == kKindMfma ? kMfmaWaves : kDecodeWaves;
     int S = n_splits;
     if (S <= 0) {
-        // ~2 workgroups per compute unit, each with at least one tile per wave
-        const int64_t target = 2LL * device_cu_count();
+        // about one (MFMA) or two (VALU) workgroups per compute unit, each
+        // with at least one 64-token tile per wave
+        const int64_t target = (kind == kKindMfma ? 1LL : 2LL) * device_cu_count();
         int64_t want = (target + s.n_cols - 1) / s.n_cols;
-        const int64_t cap = tiles / kDecodeWaves;
+        const int64_t cap = tiles / waves;
         if (want > cap) want = cap;
         S = (int)(want < 1 ? 1 : want);
     }
     if (tiles == 0) S = 1;
     if (S > tiles && tiles > 0) S = (int)tiles;
+    if (S > kMaxSplits) S = kMaxSplits;
     s.tiles_per_split = tiles > 0 ? (int)((tiles + S - 1) / S) : 0;
     if (s.tiles_per_split > 0) S = (int)((tiles + s.tiles_per_split - 1) / s.tiles_per_split);
     s.S = S;
     return s;
 }
 
+// Workspace layout: [part_ml: n_cols*S*R float2, padded to 256 B]
+//                   [part_acc: n_cols*S*R*D float]
+struct WsLayout {
+    size_t ml, acc, total;
+};
+
+static WsLayout ws_layout(const DecodeShape &s, int head_dim) {
+    auto pad = [](size_t b) { return (b + 255) / 256 * 256; };
+    WsLayout w;
+    const size_t slots = (size_t)s.n_cols * s.S * s.R;
+    w.ml = 0;
+    w.acc = w.ml + pad(slots * 2 * sizeof(float));
+    w.total = w.acc + slots * head_dim * sizeof(float);
+    return w;
+}
+
 static size_t decode_ws_bytes(const DecodeShape &s, int head_dim) {
-    if (s.S <= 1) return 0;
-    const size_t counters = ((size_t)s.n_cols * sizeof(unsigned) + 255) / 256 * 256;
-    return counters + (size_t)s.n_cols * s.S * s.R * (head_dim + 2) * sizeof(float);
+    return s.S <= 1 ? 0 : ws_layout(s, head_dim).total;
+}
+
+template <int D>
+static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t st) {
+    if (s.S <= 1) return SS_OK;
+    auto merge = decode_merge_kernel<D>;
+    hipLaunchKernelGGL(merge, dim3(s.n_cols, s.R), dim3(kDecodeThreads), 0, st, c, s.R);
+    SS_LAUNCH_CHECK("decode_merge_kernel launch");
+    return SS_OK;
+}
+
+template <int D>
+static int launch_mfma(DecodeCommon c, const __half *v8, const DecodeShape &s, hipStream_t st) {
+    constexpr int NW = kMfmaWaves;
+    const size_t lds = mfma_lds_bytes<D, NW>();
+    auto kern = decode_attn_mfma_kernel<D, NW>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(NW * kWave), lds, st, c, v8);
+    SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
+    return launch_merge<D>(c, s, st);
 }
 
 template <int D, int R, class VF>
@@ -513,7 +921,7 @@ static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape
     dim3 grid(s.S, s.n_cols);
     hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), lds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_kernel launch");
-    return SS_OK;
+    return launch_merge<D>(c, s, st);
 }
 
 template <int D, class VF>
@@ -569,8 +977,8 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.q_offset = q_offset;
     c.n_splits = s.S;
     c.tiles_per_split = s.tiles_per_split;
-    c.partials = nullptr;
-    c.counters = nullptr;
+    c.part_ml = nullptr;
+    c.part_acc = nullptr;
     if (s.S > 1) {
         const size_t need = decode_ws_bytes(s, head_dim);
         if (!ws || ws_bytes < need) {
@@ -579,9 +987,10 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
             return SS_ERR_WORKSPACE;
         }
         SS_REQUIRE(((uintptr_t)ws % 256) == 0, "workspace must be 256-byte aligned");
-        c.counters = reinterpret_cast<unsigned *>(ws);
-        const size_t cbytes = ((size_t)s.n_cols * sizeof(unsigned) + 255) / 256 * 256;
-        c.partials = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
+        const WsLayout w = ws_layout(s, head_dim);
+        char *base = reinterpret_cast<char *>(ws);
+        c.part_ml = reinterpret_cast<float *>(base + w.ml);
+        c.part_acc = reinterpret_cast<float *>(base + w.acc);
     }
     return SS_OK;
 }
@@ -697,4 +1106,44 @@ extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch,
     }
 #undef SS_GROUPED_BITS
 #undef SS_GROUPED
+}
+
+extern "C" int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+                              int head_dim, int64_t t_kv, int n_splits, int *splits_out,
+                              size_t *workspace_bytes_out) {
+    SS_REQUIRE(kind == kKindValu || kind == kKindMfma, "kind must be 0 (dense) or 1 (il8)");
+    SS_REQUIRE(batch >= 1 && n_q_heads >= 1 && n_kv_heads >= 1 && t_q >= 1 &&
+                   n_q_heads % n_kv_heads == 0,
+               "bad head/batch counts");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits, kind);
+    if (splits_out) *splits_out = s.S;
+    if (workspace_bytes_out) *workspace_bytes_out = decode_ws_bytes(s, head_dim);
+    return SS_OK;
+}
+
+extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                  int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                  const int32_t *perm, const float *centroids, int n_blocks,
+                                  int n_centroids, const uint8_t *idx, const void *values_il8,
+                                  int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                  int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                  size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(values_il8, "null values");
+    SS_UNSUPPORTED(v_dtype == SS_F16, "interleaved values must be float16");
+    SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8 for interleaved values");
+    SS_REQUIRE(((uintptr_t)values_il8 % 16) == 0, "values must be 16-byte aligned");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
+                                       kKindMfma);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const __half *v8 = reinterpret_cast<const __half *>(values_il8);
+    if (head_dim == 128) return launch_mfma<128>(c, v8, s, st);
+    return launch_mfma<64>(c, v8, s, st);
 }

@@ -78,6 +78,43 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave64 reductions on DPP lane moves (no LDS round trips): butterflies inside
+// each 16-lane row, then row_bcast:15 / row_bcast:31 fold the four rows into
+// lane 63, which is read back as a wave-uniform value.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_mov(float v) {
+    const int x = __float_as_int(v);
+    return __int_as_float(__builtin_amdgcn_update_dpp(x, x, CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));         // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_mov<0x4E>(v));         // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_mov<0x141>(v));        // row_half_mirror
+    v = fmaxf(v, dpp_mov<0x140>(v));        // row_mirror
+    v = fmaxf(v, dpp_mov<0x142, 0xa>(v));   // row_bcast:15 into rows 1, 3
+    v = fmaxf(v, dpp_mov<0x143, 0xc>(v));   // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    // rows 1 and 3 add the total of the row before them; lanes of rows 0, 2
+    // must not change, so they add 0
+    {
+        const int x = __float_as_int(v);
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+    }
+    {
+        const int x = __float_as_int(v);
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
+    }
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Orders this wave's LDS accesses (all lanes) before the ones that follow:
 // waits for outstanding LDS operations and stops the compiler from moving
 // LDS accesses across the point.

@@ -1,0 +1,167 @@
+"""Value codecs for hybrid SunShape caches (reference value_codecs.py:1-201).
+
+``GroupedValueCodec``: asymmetric per-group min-max 2/3/4-bit codes packed in
+uint32 words, one scale/zero pair per group (HIP encode/decode kernels).
+``TurboQuantValueCodec``: per-token norm, random rotation, Lloyd-Max scalar
+codes of N(0, 1/D) coordinates, packed (rotation on torch, scalar quantise and
+packing on HIP kernels).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from functools import lru_cache
+
+import numpy as np
+import torch
+
+from . import _hip
+from .kernels import (
+    dequantize_values,
+    pack_indices,
+    quantize_scalar_to_indices,
+    quantize_values,
+    unpack_indices,
+)
+from .rotation import generate_rotation_matrix
+
+
+@lru_cache(maxsize=None)
+def lloyd_max_gaussian(bits: int) -> tuple[tuple[float, ...], tuple[float, ...]]:
+    """Lloyd-Max quantiser of N(0, 1): ``(levels, boundaries)``.
+
+    Fixed point of the two optimality conditions (Max, 1960): boundaries are
+    midpoints of neighbouring levels and each level is its cell's conditional
+    mean ``(phi(a) - phi(b)) / (Phi(b) - Phi(a))``.  The reference ships the
+    same quantiser as literal tables (value_codecs.py:20-87)."""
+    from scipy.special import ndtr
+
+    def pdf(x):
+        return np.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
+
+    n = 1 << bits
+    levels = np.linspace(-2.0, 2.0, n)
+    for _ in range(5000):
+        b = 0.5 * (levels[1:] + levels[:-1])
+        lo = np.concatenate([[-np.inf], b])
+        hi = np.concatenate([b, [np.inf]])
+        pl = np.where(np.isinf(lo), 0.0, pdf(np.where(np.isinf(lo), 0.0, lo)))
+        ph = np.where(np.isinf(hi), 0.0, pdf(np.where(np.isinf(hi), 0.0, hi)))
+        new = (pl - ph) / (ndtr(hi) - ndtr(lo))
+        done = np.max(np.abs(new - levels)) < 1e-15
+        levels = new
+        if done:
+            break
+    levels = 0.5 * (levels - levels[::-1])  # exact symmetry
+    return tuple(levels.tolist()), tuple((0.5 * (levels[1:] + levels[:-1])).tolist())
+
+
+def _packed_dim(head_dim: int, bits: int) -> int:
+    if bits == 2:
+        if head_dim % 16 != 0:
+            raise ValueError(f"head_dim must be divisible by 16 for 2-bit packing, got {head_dim}")
+        return head_dim // 16
+    if bits == 3:
+        return (head_dim + 9) // 10
+    if bits == 4:
+        if head_dim % 8 != 0:
+            raise ValueError(f"head_dim must be divisible by 8 for 4-bit packing, got {head_dim}")
+        return head_dim // 8
+    raise ValueError(f"Unsupported bits: {bits}")
+
+
+@dataclass
+class GroupedValueCodec:
+    """reference value_codecs.py:104-133."""
+    head_dim: int
+    bits: int
+    group_size: int = 64
+    name: str = "grouped"
+    last_quantize_backend: str = "hip"
+
+    @property
+    def packed_dim(self) -> int:
+        return _packed_dim(self.head_dim, self.bits)
+
+    @property
+    def n_groups(self) -> int:
+        return self.head_dim // self.group_size
+
+    def quantize(self, values: torch.Tensor):
+        packed, scales, zeros, _ = quantize_values(values, bits=self.bits,
+                                                   group_size=self.group_size)
+        self.last_quantize_backend = "hip"
+        return packed, scales, zeros
+
+    def dequantize(self, packed, scales, zeros) -> torch.Tensor:
+        return dequantize_values(packed, scales, zeros, D=self.head_dim, bits=self.bits,
+                                 group_size=self.group_size)
+
+
+@dataclass
+class TurboQuantValueCodec:
+    """reference value_codecs.py:136-177.  The rotation is drawn from NumPy's
+    generator (see ``generate_rotation_matrix``)."""
+    head_dim: int
+    bits: int
+    seed: int = 43
+    prefer_metal: bool = True
+    name: str = "turboquant"
+    last_quantize_backend: str = "none"
+    device: object = field(default=None, repr=False)
+
+    def __post_init__(self) -> None:
+        if self.bits not in (2, 3, 4):
+            raise ValueError(f"TurboQuant values support 2, 3, or 4 bits, got {self.bits}")
+        levels, bounds = lloyd_max_gaussian(self.bits)
+        s = 1.0 / math.sqrt(self.head_dim)
+        dev = self.device or ("cuda" if torch.cuda.is_available() else "cpu")
+        self.centroids = torch.tensor([c * s for c in levels], dtype=torch.float32, device=dev)
+        self.boundaries = torch.tensor([b * s for b in bounds], dtype=torch.float32, device=dev)
+        self.rotation = torch.from_numpy(
+            generate_rotation_matrix(self.head_dim, seed=self.seed)).to(dev)
+        self.rotation_t = self.rotation.T.contiguous()
+
+    @property
+    def packed_dim(self) -> int:
+        return _packed_dim(self.head_dim, self.bits)
+
+    def _on(self, device):
+        if self.rotation.device != device:
+            self.centroids = self.centroids.to(device)
+            self.boundaries = self.boundaries.to(device)
+            self.rotation = self.rotation.to(device)
+            self.rotation_t = self.rotation_t.to(device)
+
+    def quantize(self, values: torch.Tensor):
+        _hip.require_gpu(values)
+        self._on(values.device)
+        v = values.float()
+        norms = torch.linalg.vector_norm(v, dim=-1, keepdim=True)
+        unit = v / torch.clamp(norms, min=1e-8)
+        rotated = unit @ self.rotation_t
+        idx, backend = quantize_scalar_to_indices(rotated, self.boundaries,
+                                                  prefer_metal=self.prefer_metal)
+        self.last_quantize_backend = backend
+        return pack_indices(idx, self.bits), norms.squeeze(-1)
+
+    def dequantize(self, packed: torch.Tensor, norms: torch.Tensor) -> torch.Tensor:
+        self._on(packed.device)
+        idx = unpack_indices(packed, self.head_dim, self.bits).to(torch.int64)
+        unit = self.centroids[idx] @ self.rotation
+        return unit * norms[..., None]
+
+
+def build_value_codec(value_backend: str, *, head_dim: int, value_bits: int,
+                      value_group_size: int = 64, value_seed: int = 43,
+                      prefer_metal: bool = True):
+    """reference value_codecs.py:180-201."""
+    if value_backend == "fp16":
+        return None
+    if value_backend == "grouped":
+        return GroupedValueCodec(head_dim=head_dim, bits=value_bits, group_size=value_group_size)
+    if value_backend == "turboquant":
+        return TurboQuantValueCodec(head_dim=head_dim, bits=value_bits, seed=value_seed,
+                                    prefer_metal=prefer_metal)
+    raise ValueError(f"Unsupported value backend: {value_backend}")

@@ -71,7 +71,7 @@ def test_decode_dense_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, c
 
 def test_decode_dense_metric_shape_fp16_out_and_repeatability():
     """T_kv = 32768 (the metric shape): fp32 and fp16 outputs, and two calls
-    in a row agree bit-for-bit (split counters are reset by each call)."""
+    in a row agree bit-for-bit (the split workspace carries no state)."""
     cents, perm, idx, vals, q = decode_case(42, 1, 32, 8, 128, 32768)
     scale = 1.0 / np.sqrt(128)
     args = (t(q), scale, t(perm), t(cents), t(idx), t(vals), 32768)
@@ -273,3 +273,68 @@ def test_invalid_arguments_raise_before_launch():
     cents, perm, idx, vals, q = decode_case(1, 1, 4, 4, 128, 64)
     with pytest.raises(_hip.SunShapeHIPError):
         _hip.decode_attn_dense(t(q), 1.0, t(perm), t(cents), t(idx), t(vals), 65)  # > cap
+
+
+def to_il8(vals_np, cap):
+    """Build the interleaved (B, H, cap/8, D, 8) cache with the append kernel."""
+    b, h, t_kv, d = vals_np.shape
+    buf = torch.zeros((b, h, cap // 8, d, 8), dtype=torch.float16, device=DEV)
+    _hip.append_values_il8(t(vals_np.astype(np.float16)), buf, 0)
+    return buf
+
+
+def test_append_values_il8_roundtrip_and_offsets():
+    rng = np.random.default_rng(0)
+    v = rng.standard_normal((2, 3, 21, 64)).astype(np.float16)
+    buf = torch.zeros((2, 3, 48 // 8, 64, 8), dtype=torch.float16, device=DEV)
+    _hip.append_values_il8(t(v[:, :, :13]), buf, 0)
+    _hip.append_values_il8(t(v[:, :, 13:]), buf, 13)   # unaligned offset
+    torch.cuda.synchronize()
+    dense = _hip.il8_to_dense(buf).cpu().numpy()
+    assert np.array_equal(dense[:, :, :21], v)
+    assert not dense[:, :, 21:].any()
+
+
+@pytest.mark.parametrize(
+    "b,hq,hkv,d,t_kv,t_q,causal,splits,cap",
+    [
+        (1, 32, 8, 128, 4096, 1, False, 0, None),    # BASELINE config 2 shape
+        (1, 32, 8, 128, 32768, 1, False, 0, None),   # metric shape
+        (2, 8, 2, 128, 1003, 1, False, 0, 1024),     # ragged T (partial 8-token block)
+        (1, 4, 1, 128, 1, 1, False, 0, 256),         # single token
+        (1, 4, 2, 128, 777, 1, False, 5, None),      # forced splits, rep 2 (rows 2-3 empty)
+        (1, 8, 2, 64, 513, 1, False, 0, None),       # head_dim 64
+        (1, 4, 1, 128, 64, 3, True, 0, None),        # prefill rows, causal
+        (2, 6, 2, 64, 300, 5, True, 3, 320),         # several row groups
+    ])
+def test_decode_il8_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, cap):
+    cap = cap or ((t_kv + 7) // 8) * 8
+    cents, perm, idx, vals, q = decode_case(b * 1000 + t_kv + 1, b, hq, hkv, d, t_kv, t_q, cap)
+    vbuf = to_il8(vals, cap)
+    if t_kv < cap:  # NaN padding after t_kv must not leak into the result
+        tail = (t_kv // 8) * 8
+        vbuf.view(b, hkv, cap // 8, d * 8)[:, :, tail // 8:] = float("nan")
+        _hip.append_values_il8(t(vals[:, :, tail:t_kv]), vbuf, tail)
+    scale = 1.0 / np.sqrt(d)
+    out = _hip.decode_attn_il8(t(q), scale, t(perm), t(cents), t(idx), vbuf, t_kv,
+                               causal=causal, q_offset=t_kv - t_q if causal else 0,
+                               out_dtype=torch.float32, n_splits=splits)
+    torch.cuda.synchronize()
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, scale,
+                 mask="causal" if causal else None)
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) <= REL_TOL
+
+
+def test_decode_il8_peaked_and_flat_softmax():
+    """Probabilities spanning many orders of magnitude (the hi/lo fp16 split
+    must keep small ones) and an almost flat softmax."""
+    for qscale, seed in ((30.0, 1), (1e-3, 2)):
+        cents, perm, idx, vals, q = decode_case(seed, 1, 4, 1, 128, 5000, cap=5000)
+        q = (q.astype(np.float32) * qscale).astype(np.float16)
+        out = _hip.decode_attn_il8(t(q), 0.0883883, t(perm), t(cents), t(idx), to_il8(vals, 5000),
+                                   5000, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        ref = O.sdpa(q, idx, vals, cents, perm, 0.0883883)
+        assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
