@@ -92,9 +92,13 @@ int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centro
 /*
  * Workspace bytes needed by ss_decode_attn_* for the given shape and split
  * count (n_splits <= 0 selects the library's choice for the current device);
- * 0 when a single split suffices.  With more than one split a decode call is
- * two launches on the stream: the split kernel writes per-split softmax
- * partials (m, l, acc) to the workspace and a merge kernel combines them.
+ * 0 when a single split suffices.  With more than one split the split
+ * workgroups write per-split softmax partials (m, l, acc) to the workspace.
+ * ss_decode_attn_il8 merges them inside its kernel (the last split of each
+ * column to finish, counted in the workspace's first 64 KiB); the other
+ * entry points merge with a second launch on the stream.  A workspace must be
+ * zero-filled once before its first use; every completed call leaves its
+ * counter area zero again.
  */
 size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                  int64_t t_q, int head_dim, int64_t t_kv,

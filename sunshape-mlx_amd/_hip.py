@@ -170,14 +170,16 @@ _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per (device, stream) scratch for split-T partials.  Calls on one stream
-    are ordered, so they never overlap on the same buffer."""
+    are ordered, so they never overlap on the same buffer.  Allocated zeroed:
+    its first 64 KiB hold the per-column split counters, which every call
+    leaves at zero."""
     if nbytes <= 0:
         return None
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            stream_handle(device))
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _ws_cache[key] = ws
     return ws
 

@@ -33,6 +33,8 @@ struct DecodeCommon {
     void *out;
     float *part_ml;   // [cols][splits][R] (m, l)
     float *part_acc;  // [cols][splits][R][D]
+    int *part_cnt;    // [cols] splits finished (in-kernel merge); zero between calls
+    int fused_merge;  // MFMA kernel: merge the splits in-kernel (else a merge launch)
     int q_dtype, out_dtype;
     int n_q_heads, n_kv_heads, rep, n_rg;
     int64_t t_q, rows_total;
@@ -431,27 +433,104 @@ __global__ void __launch_bounds__(kDecodeThreads)
 }
 
 // ---------------------------------------------------------------------------
-// MFMA variant for fp16 values stored 8-token interleaved: value element
-// (token t, dim d) of a head lives at [t / 8][d][t % 8], so one 16-byte load
-// gives a lane 8 consecutive tokens of one dim -- the K-major operand layout of
+// MFMA decode for fp16 values stored 8-token interleaved: value element
+// (token t, dim d) of a head lives at [t / 8][d][t % 8], so 16 bytes give a
+// lane 8 consecutive tokens of one dim -- the K-major operand layout of
 // v_mfma_f32_16x16x16f16.  P.V runs on the matrix cores as
 // O[row][dim] = sum_t P[row][t] V[t][dim] with M = query rows, K = tokens,
 // N = dims.  P enters as an fp16 hi/lo pair (rows 0-3 hi, rows 4-7 lo) of
 // p * 2^15, which keeps ~22 mantissa bits and stays in fp16's normal range;
 // accumulation is fp32.  Four query rows (one GQA group) per workgroup.
+//
+// The workgroup is warp-specialised: NC compute waves and one loader wave.
+// The loader streams the split's 64-token tiles (values and index rows) from
+// HBM straight into an LDS ring with global_load_lds_dwordx4 -- no registers,
+// no compute, so it can keep kDepth tiles in flight from the first cycle while
+// the compute waves build the query x centroid LUT.  A wave that issues loads
+// into a full memory pipeline stalls at the issue; only the loader ever does,
+// so the compute waves never wait on anything but data that has landed.
+// Tile j goes to slot j % kSlots and to compute wave j % NC.  Hand-off uses
+// two LDS words per slot: ready[s] = j once tile j has landed (written by the
+// loader after its vmcnt wait), done[s] = j once its consumer has copied the
+// tile into registers.  Every wait on them is bounded (kSpinLimit sleeps), so
+// a protocol error ends the kernel with wrong results instead of hanging.
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kPScale = 32768.f;  // 2^15
 constexpr int kMfmaRows = 4;
+constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
+constexpr int kSpinLimit = 1 << 20;  // bounded waits: ~0.03 s of s_sleep 1
 
-template <int D, int NW>
-constexpr size_t mfma_lds_bytes() {
-    return sizeof(float) * ((size_t)(D / kBlockDim) * kLutStride * kMfmaRows +
-                            (size_t)kMfmaRows * D) +
-           sizeof(_Float16) * (size_t)NW * 8 * kWave;
+template <class T>
+using lds_t = __attribute__((address_space(3))) T;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Cache-policy bit sc1 of gfx940+ memory instructions: agent-coherent access
+// (stores write through, loads do not hit a possibly stale line, of this
+// XCD's L2).
+constexpr int kCpolSc1 = 16;
+// Cache-policy bit nt: streaming data, read once (the tile copies), so it
+// does not displace what later steps reuse.
+constexpr int kCpolNt = 2;
+
+// Raw buffer resource over [p, p + bytes) (dword 3 of a raw gfx9 buffer
+// descriptor); accesses past `bytes` read zero and drop writes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
 }
+
+// LDS address of a shared-memory object as an address-space-3 pointer (the
+// low 32 bits of a generic pointer into LDS are the LDS offset).
+template <class T>
+__device__ __forceinline__ lds_t<T> *to_lds(const void *p) {
+    return reinterpret_cast<lds_t<T> *>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+
+// s_waitcnt vmcnt(N), leaving the other counters unconstrained (gfx9 layout:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until the oldest of k outstanding tiles (LPT loads each) has landed.
+template <int LPT, int K>
+__device__ __forceinline__ void wait_oldest_tile(int k) {
+    if constexpr (K >= 1) {
+        if (k >= K) {
+            wait_vmcnt<(K - 1) * LPT>();
+            return;
+        }
+        wait_oldest_tile<LPT, K - 1>(k);
+    }
+}
+
+template <int D, int NC>
+struct WsCfg {
+    static constexpr int kNB = D / kBlockDim;
+    static constexpr int kTileV = kWave * D * 2;  // fp16 values of a 64-token tile
+    static constexpr int kTileI = kWave * kNB;    // uint8 index rows of the tile
+    static constexpr int kSlot = kTileV + kTileI;
+    static constexpr int kLut = kNB * kLutStride * 16;  // float4 per (block, centroid)
+    static constexpr int kPst = NC * 8 * kWave * 2;     // P staging, fp16 [8][64] per wave
+    static constexpr int kFlagWords = 16;
+    static constexpr int kFlags = (2 * kFlagWords + 4) * 4;  // ready[], done[], barrier counter
+    static constexpr int kRing = kLut + kPst + kFlags;
+    static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
+    static constexpr int kSlots = kSlotsFit < 8 ? kSlotsFit : 8;
+    static constexpr int kLoadsPerTile = kTileV / 1024 + 1;
+    static constexpr int kDepthVm = 63 / kLoadsPerTile + 1;
+    static constexpr int kDepth = kSlots < kDepthVm ? kSlots : kDepthVm;
+    static constexpr int kLds = kRing + kSlots * kSlot;
+    static_assert(kSlots >= 2 && kSlots <= kFlagWords, "ring slots");
+    static_assert(kLds <= kLdsMax, "LDS budget");
+    static_assert(NC * kMfmaRows * (D + 2) * 4 <= kSlots * kSlot, "merge scratch");
+    static_assert(2 * kMfmaRows * D * 4 <= kPst, "query staging");
+    static_assert((NC * kWave) % kNB == 0 && kLutStride % ((NC * kWave) / kNB) == 0, "LUT split");
+};
 
 // Zero the fp16 values of tokens >= n_ok (0..8) in an 8-token group.
 __device__ __forceinline__ uint4 mask_tokens(uint4 u, int n_ok) {
@@ -465,24 +544,31 @@ __device__ __forceinline__ uint4 mask_tokens(uint4 u, int n_ok) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-template <int D, int NW>
-__global__ void __launch_bounds__(NW * kWave)
+template <int D, int NC>
+__global__ void __launch_bounds__((NC + 1) * kWave)
     decode_attn_mfma_kernel(DecodeCommon c, const __half *v8) {
+    using K = WsCfg<D, NC>;
     constexpr int R = kMfmaRows;
-    constexpr int NB = D / kBlockDim;
+    constexpr int NB = K::kNB;
     constexpr int NT = D / 16;  // MFMA N-tiles (16 dims each)
-    constexpr int THREADS = NW * kWave;
-    static_assert(NW * R * (D + 2) <= NB * kLutStride * R, "merge scratch");
+    constexpr int THREADS = (NC + 1) * kWave;
+    constexpr int LPT = K::kLoadsPerTile;
 
     extern __shared__ __align__(16) float4 smem4[];
-    float4 *lut4 = smem4;                                      // [NB][256] (4 rows)
-    float *qp = reinterpret_cast<float *>(smem4 + NB * kLutStride);  // [R][D]
-    _Float16 *pb = reinterpret_cast<_Float16 *>(qp + R * D);   // [NW][8][64]
-    float *smem = reinterpret_cast<float *>(smem4);
+    char *smem = reinterpret_cast<char *>(smem4);
+    float4 *lut4 = smem4;                                              // [NB][256]
+    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][8][64]
+    volatile lds_t<int> *ready = to_lds<int>(smem + K::kLut + K::kPst);
+    volatile lds_t<int> *done = ready + K::kFlagWords;
+    volatile lds_t<int> *cbar = done + K::kFlagWords;  // compute-wave barrier counter
+    char *ring = smem + K::kRing;
+    const lds_t<f32x4> *lut_l = to_lds<f32x4>(smem4);  // 16-byte LUT reads
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
-    const int wv = tid >> 6;
+    // wave-uniform (scalar) wave index: all tile control flow stays scalar
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool loader = wv == NC;
     const int col = blockIdx.y;
     const int split = blockIdx.x;
     const int rg = col % c.n_rg;
@@ -500,119 +586,82 @@ __global__ void __launch_bounds__(NW * kWave)
     const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
     const int n_tiles = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
     const uint8_t *idx_head = c.idx + bh * c.cap * NB;
-    const __half *vhead = v8 + bh * c.cap * D;
+    const char *vhead = reinterpret_cast<const char *>(v8 + bh * c.cap * D);
+    const int64_t t_last = max(t_end - 1, (int64_t)0);
+    const int64_t blk_last = t_last / 8;
     const int g = lane >> 4, l16 = lane & 15;
 
-    // Tile loads: the index row of token t0 + lane and, per 32-token half s2,
-    // the 8-token block t0/8 + 4*s2 + g of dims 16n + l16 (16 bytes).
-    auto load_tile = [&](int tile, uint4 (&v)[2][NT], IdxRow<NB> &ir) {
-        const int64_t t0 = t_beg + (int64_t)tile * kWave;
-        const int64_t tk = t0 + lane;
-        ir.load(idx_head + tk * NB, tk < t_end);
-        if (t0 + kWave <= t_end) {
+    // Barrier that orders LDS only: a wave's outstanding global loads (the
+    // loader's tile copies) do not have to land first, which __syncthreads'
+    // workgroup release fence would require.
+    auto lds_barrier = [] {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // Barrier among the NC compute waves only (the loader never joins it):
+    // each wave adds 1 to an LDS counter once its LDS writes are done and
+    // waits until all NC waves have arrived for this phase (bounded wait).
+    auto compute_barrier = [&](int phase) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) __hip_atomic_fetch_add(const_cast<lds_t<int> *>(cbar), 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_WORKGROUP);
+        int spins = 0;
+        while (*cbar < phase * NC) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) break;
+        }
+        asm volatile("" ::: "memory");
+    };
+
+    // Loader: tile j into slot j % kSlots.  The values are 8 contiguous
+    // 8-token blocks (16*D bytes each), copied in 16-byte chunks; chunks of
+    // blocks past the split's last token are clamped to that block, and index
+    // rows past it to the last token's row, so every load stays in bounds.
+    // The LDS destination of lane l is M0 + 16*l.
+    auto issue = [&](int j) {
+        const uint32_t sb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) +
+                            (uint32_t)((j % K::kSlots) * K::kSlot);
+        const int64_t t0 = t_beg + (int64_t)j * kWave;
+        const int64_t b0 = t0 / 8;
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const __half *vb = vhead + ((t0 / 8 + 4 * s2 + g) * D + l16) * 8;
-#pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    v[s2][n] = *reinterpret_cast<const uint4 *>(vb + n * 16 * 8);
-            }
+        for (int i = 0; i < K::kTileV / 1024; ++i) {
+            const int q = i * kWave + lane;  // 16-byte chunk of the tile
+            const int64_t blk = min(b0 + q / D, blk_last);
+            __builtin_amdgcn_global_load_lds(vhead + (blk * D + q % D) * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                             kCpolNt);
+        }
+        if constexpr (NB == 16) {
+            const int64_t tk = min(t0 + lane, t_last);
+            __builtin_amdgcn_global_load_lds(idx_head + tk * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + K::kTileV), 16,
+                                             0, kCpolNt);
         } else {
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const int64_t blk = t0 / 8 + 4 * s2 + g;
-                const int64_t nok = t_end - blk * 8;
-                const __half *vb = vhead + (blk * D + l16) * 8;
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    uint4 u = make_uint4(0u, 0u, 0u, 0u);
-                    if (nok > 0) u = *reinterpret_cast<const uint4 *>(vb + n * 16 * 8);
-                    if (nok < 8) u = mask_tokens(u, (int)max(nok, (int64_t)0));
-                    v[s2][n] = u;
-                }
+            static_assert(NB == 8, "unsupported block count");
+            if (lane < kWave / 2) {  // 512 bytes: two tokens per 16-byte chunk
+                const int64_t ch = min(t0 / 2 + lane, t_last / 2);
+                __builtin_amdgcn_global_load_lds(idx_head + ch * 16,
+                                                 reinterpret_cast<lds_t<void> *>(sb + K::kTileV),
+                                                 16, 0, kCpolNt);
             }
         }
     };
+    int issued = 0, landed = 0;
 
-    // Vector-memory loads of a wave return in issue order, so the prologue's
-    // small loads (query, permutation, this thread's codebook entries) are
-    // issued and completed first, then the wave's first tile, so the LUT is
-    // built from registers while the tile streams in.  sched_barrier keeps the compiler from reordering the
-    // groups.  Afterwards each wave keeps one tile in flight; eight waves per
-    // compute unit keep ~128 KB of loads outstanding per CU.
-    constexpr int LUT_PER_THREAD = (NB * kLutStride + THREADS - 1) / THREADS;
-    const int nbc = NB * c.n_centroids;
-    // 0a. query row element and permutation index of this thread
-    float q_raw = 0.f;
-    int q_src = 0;
-    {
-        const int r = tid / D, j = tid - r * D;
-        if (tid < R * D && row_ok(r)) {
-            q_raw = load_as_f32(c.q, c.q_dtype, row_off(r) + j);
-            q_src = c.perm ? c.perm[j] : j;
-        }
-    }
-    // 0b. codebook entries e = tid + k * THREADS
-    float4 cv[LUT_PER_THREAD][2];
-#pragma unroll
-    for (int k = 0; k < LUT_PER_THREAD; ++k) {
-        const int e = tid + k * THREADS;
-        if (e < nbc) {
-            const float4 *cp = reinterpret_cast<const float4 *>(c.centroids + (int64_t)e * kBlockDim);
-            cv[k][0] = cp[0];
-            cv[k][1] = cp[1];
-        } else {
-            cv[k][0] = cv[k][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    }
-    // Wait for these explicitly: the waitcnt pass merges counts
-    // conservatively across the branches around the tile loads, so a value
-    // first used after them would otherwise wait for the whole tile.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_sched_barrier(0);
-    // 0c. first tile of this wave
-    uint4 vA[2][NT];
-    IdxRow<NB> iA;
-    int tA = wv;
-    if (tA < n_tiles) load_tile(tA, vA, iA);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 1. query rows: round_to(q_dtype, q * scale) (attention.py:208), then
-    //    the codec permutation (attention.py:228), gathered through LDS
-    float *qraw = reinterpret_cast<float *>(pb);  // [R][D] staging (pb is free here)
-    if (tid < R * D) qraw[tid] = round_to(c.q_dtype, q_raw * c.scale);
-    __syncthreads();
-    if (tid < R * D) {
-        const int r = tid / D;
-        qp[tid] = qraw[r * D + q_src];
-    }
-    __syncthreads();
-    // 2. LUT entry (b, c) holds the 4 rows' dot products, in log2 units
-#pragma unroll
-    for (int k = 0; k < LUT_PER_THREAD; ++k) {
-        const int e = tid + k * THREADS;
-        if (e < nbc) {
-            const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
-            const float4 c0 = cv[k][0], c1 = cv[k][1];
-            float dot[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float *qr = qp + r * D + b * kBlockDim;
-                float d0 = qr[0] * c0.x;
-                d0 = fmaf(qr[1], c0.y, d0);
-                d0 = fmaf(qr[2], c0.z, d0);
-                d0 = fmaf(qr[3], c0.w, d0);
-                d0 = fmaf(qr[4], c1.x, d0);
-                d0 = fmaf(qr[5], c1.y, d0);
-                d0 = fmaf(qr[6], c1.z, d0);
-                d0 = fmaf(qr[7], c1.w, d0);
-                dot[r] = d0 * kLog2e;
-            }
-            lut4[b * kLutStride + cc] = make_float4(dot[0], dot[1], dot[2], dot[3]);
-        }
-    }
-    __syncthreads();
-
+    // Prologue.  The compute waves' small loads (query element, permutation
+    // entry, codebook entries) are issued before the loader's first tiles, so
+    // they sit ahead of the tiles in the compute unit's memory queue; the
+    // loader starts streaming once they have landed, and the LUT is built
+    // while the first tiles are in flight.
+    constexpr int TPB = (NC * kWave) / NB;  // LUT threads per codebook block
+    constexpr int EPT = kLutStride / TPB;   // LUT entries per thread
+    float *qraw = reinterpret_cast<float *>(pst);  // [R][D] (P staging is free here)
+    float *qp = qraw + R * D;                      // [R][D]
+    constexpr int CT = NC * kWave;             // compute threads
+    constexpr int QE = (R * D + CT - 1) / CT;  // query elements per compute thread
+    if (tid < 2 * K::kFlagWords) ready[tid] = -1;  // ready[] and done[]
+    if (tid == 0) *cbar = 0;
     int64_t lim[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -628,41 +677,205 @@ __global__ void __launch_bounds__(NW * kWave)
         m[r] = -1e30f;
         lsum[r] = 0.f;
     }
-    _Float16 *pw = pb + wv * 8 * kWave;
-    const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
 
-    // 3. one 64-token tile: scores from the LUT, online softmax, P.V on MFMA
-    auto process = [&](int tile, const uint4 (&v)[2][NT], const IdxRow<NB> &ir) {
-        const int64_t tk = t_beg + (int64_t)tile * kWave + lane;
-        const bool kok = tk < t_end;
-        float s[R] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const float4 e = lut4[b * kLutStride + ir.at(b)];
-            s[0] += e.x;
-            s[1] += e.y;
-            s[2] += e.z;
-            s[3] += e.w;
+    // The two roles run in separate branches up to the end of the tile loop
+    // (one shared LDS-only barrier, then compute-only barriers), so no code
+    // after a join inherits the loader's outstanding tile copies as pending
+    // loads, and the loader streams from the start without waiting for the
+    // LUT.
+    if (loader) {
+        // the compute waves' small loads are issued (so they are ahead of
+        // the tiles in the memory queue) and the flags are initialised
+        lds_barrier();
+        // keep kDepth tiles in flight; publish each tile once it has landed
+        int spins = 0;
+        while (landed < n_tiles) {
+            if (issued < n_tiles && issued - landed < K::kDepth &&
+                (issued < K::kSlots || done[issued % K::kSlots] == issued - K::kSlots)) {
+                asm volatile("" ::: "memory");
+                issue(issued++);
+                continue;
+            }
+            if (issued > landed) {
+                wait_oldest_tile<LPT, K::kDepth>(issued - landed);
+                asm volatile("" ::: "memory");
+                if (lane == 0) ready[landed % K::kSlots] = landed;
+                ++landed;
+                continue;
+            }
+            __builtin_amdgcn_s_sleep(1);  // slot still held by its consumer
+            if (++spins > kSpinLimit) break;
         }
-        float corr[R];
-        bool any_corr = false;
+    } else {
+        float4 cv[EPT][2];
+        uint32_t q_word[QE];
+        int perm_v[QE];
+        int64_t q_byte[QE];
+        {
+            // query elements e = tid + u*CT (row e / D, dim e % D: the aligned
+            // dword holding each) with their permutation entries, and the
+            // codebook entries of this thread's LUT slice; loads are
+            // unconditional (dummy addresses when unused)
+            const int q_es = c.q_dtype == SS_F32 ? 4 : 2;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float sc = (kok && tk <= lim[r]) ? s[r] : -INFINITY;
-            const float mn = fmaxf(m[r], wave_max_dpp(sc));
-            corr[r] = fast_exp2(m[r] - mn);
-            any_corr |= corr[r] != 1.f;
-            const float p = fast_exp2(sc - mn);
-            lsum[r] = fmaf(lsum[r], corr[r], p);
-            m[r] = mn;
-            const float x = p * kPScale;
-            const _Float16 hi = (_Float16)x;
-            const _Float16 lo = (_Float16)(x - (float)hi);
-            pw[r * kWave + lane] = hi;
-            pw[(r + 4) * kWave + lane] = lo;
+            for (int u = 0; u < QE; ++u) {
+                const int e = tid + u * CT, er = e / D, ej = e - (e / D) * D;
+                const bool live = e < R * D && row_ok(er);
+                q_byte[u] = live ? (row_off(er) + ej) * q_es : 0;
+                q_word[u] = *reinterpret_cast<const uint32_t *>(static_cast<const char *>(c.q) +
+                                                                (q_byte[u] & ~int64_t(3)));
+                const int *pp = c.perm ? c.perm + (e < R * D ? ej : 0)
+                                       : reinterpret_cast<const int *>(c.q);
+                perm_v[u] = *pp;
+            }
+            const int lb = tid / TPB, cc0 = tid % TPB;
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+                const int cc = min(cc0 + TPB * k, c.n_centroids - 1);
+                const float4 *cp = reinterpret_cast<const float4 *>(
+                    c.centroids + ((int64_t)lb * c.n_centroids + cc) * kBlockDim);
+                cv[k][0] = cp[0];
+                cv[k][1] = cp[1];
+            }
         }
-        wave_lds_sync();
-        if (any_corr) {
+        lds_barrier();  // small loads issued, flags initialised
+        // query elements: round_to(q_dtype, q * scale) (attention.py:208)
+#pragma unroll
+        for (int u = 0; u < QE; ++u) {
+            const int e = tid + u * CT, er = e / D;
+            if (e < R * D) {
+                float qv = 0.f;
+                if (row_ok(er)) {
+                    const uint32_t w = q_word[u];
+                    const uint32_t h = (q_byte[u] & 2) ? (w >> 16) : (w & 0xffffu);
+                    if (c.q_dtype == SS_F32)
+                        qv = __uint_as_float(w);
+                    else if (c.q_dtype == SS_F16)
+                        qv = __half2float(__ushort_as_half((unsigned short)h));
+                    else
+                        qv = __uint_as_float(h << 16);
+                }
+                qraw[e] = round_to(c.q_dtype, qv * c.scale);
+            }
+        }
+        compute_barrier(1);  // raw query staged
+        // codec permutation of the query dims (attention.py:228)
+#pragma unroll
+        for (int u = 0; u < QE; ++u) {
+            const int e = tid + u * CT, er = e / D, ej = e - (e / D) * D;
+            if (e < R * D) {
+                const int src = c.perm ? min(max(perm_v[u], 0), D - 1) : ej;
+                qp[e] = qraw[er * D + src];
+            }
+        }
+        compute_barrier(2);
+        {
+            // LUT entry (b, cc) holds the 4 rows' dot products, in log2 units;
+            // this thread: block b = tid / TPB, centroids cc = tid % TPB + TPB*k
+            const int lb = tid / TPB, cc0 = tid % TPB;
+            const lds_t<f32x4> *qp4 = to_lds<f32x4>(qp);
+            f32x4 qa[R], qb[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                qa[r] = qp4[(r * D + lb * kBlockDim) / 4];
+                qb[r] = qp4[(r * D + lb * kBlockDim) / 4 + 1];
+            }
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+                const int cc = cc0 + TPB * k;
+                if (cc < c.n_centroids) {
+                    const float4 c0 = cv[k][0], c1 = cv[k][1];
+                    float dot[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float d0 = qa[r].x * c0.x;
+                        d0 = fmaf(qa[r].y, c0.y, d0);
+                        d0 = fmaf(qa[r].z, c0.z, d0);
+                        d0 = fmaf(qa[r].w, c0.w, d0);
+                        d0 = fmaf(qb[r].x, c1.x, d0);
+                        d0 = fmaf(qb[r].y, c1.y, d0);
+                        d0 = fmaf(qb[r].z, c1.z, d0);
+                        d0 = fmaf(qb[r].w, c1.w, d0);
+                        dot[r] = d0 * kLog2e;
+                    }
+                    lut4[lb * kLutStride + cc] = make_float4(dot[0], dot[1], dot[2], dot[3]);
+                }
+            }
+        }
+        compute_barrier(3);  // LUT complete
+
+        _Float16 *pw = pst + wv * 8 * kWave;
+        const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
+        for (int j = wv; j < n_tiles; j += NC) {
+            const int slot = j % K::kSlots;
+            int spins = 0;
+            while (ready[slot] != j) {
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kSpinLimit) break;
+            }
+            asm volatile("" ::: "memory");
+            // copy the tile (index rows and values) into registers and
+            // release the slot at once
+            const char *sb = ring + slot * K::kSlot;
+            IdxRow<NB> ir;
+            if constexpr (NB == 16) {
+                const uint4 u = *reinterpret_cast<const uint4 *>(sb + K::kTileV + lane * 16);
+                ir.w[0] = u.x; ir.w[1] = u.y; ir.w[2] = u.z; ir.w[3] = u.w;
+            } else {
+                const uint2 u = *reinterpret_cast<const uint2 *>(sb + K::kTileV + lane * 8);
+                ir.w[0] = u.x; ir.w[1] = u.y;
+            }
+            uint4 v[2][NT];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    v[s2][n] = *reinterpret_cast<const uint4 *>(
+                        sb + ((4 * s2 + g) * D + 16 * n + l16) * 16);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (lane == 0) done[slot] = j;
+            const int64_t t0 = t_beg + (int64_t)j * kWave;
+            // tokens of this tile still inside the split (wave-uniform, 1..64)
+            const int n_in = (int)min(t_end - t0, (int64_t)kWave);
+            const bool kok = lane < n_in;
+            int lim_rel[R];  // last visible lane per row (causal), wave-uniform
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                lim_rel[r] = (int)max(min(lim[r] - t0, (int64_t)kWave), (int64_t)-1);
+            // scores from the LUT, four blocks per group of reads (bounds the
+            // registers that reads in flight hold next to the tile)
+            float s[R] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int b0 = 0; b0 < NB; b0 += 4) {
+#pragma unroll
+                for (int b = b0; b < b0 + 4; ++b) {
+                    const f32x4 e = lut_l[b * kLutStride + ir.at(b)];
+                    s[0] += e.x;
+                    s[1] += e.y;
+                    s[2] += e.z;
+                    s[3] += e.w;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            float corr[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                // masked lanes add -inf (their index rows are real, clamped
+                // tokens, so s[r] is finite); an additive mask keeps the LUT
+                // sums unconditional
+                const float sc = s[r] + ((kok && lane <= lim_rel[r]) ? 0.f : -INFINITY);
+                const float mn = fmaxf(m[r], wave_max_dpp(sc));
+                corr[r] = fast_exp2(m[r] - mn);
+                const float p = fast_exp2(sc - mn);
+                lsum[r] = fmaf(lsum[r], corr[r], p);
+                m[r] = mn;
+                const float x = p * kPScale;
+                const _Float16 hi = (_Float16)x;
+                const _Float16 lo = (_Float16)(x - (float)hi);
+                pw[r * kWave + lane] = hi;
+                pw[(r + 4) * kWave + lane] = lo;
+            }
+            wave_lds_sync();
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
                 acc[n][0] *= corr[0];
@@ -670,86 +883,227 @@ __global__ void __launch_bounds__(NW * kWave)
                 acc[n][2] *= corr[2];
                 acc[n][3] *= corr[3];
             }
-        }
+            if (n_in < kWave) {  // last, partial tile: zero tokens >= t_end
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const int n_ok = min(max(n_in - 8 * (4 * s2 + g), 0), 8);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                f16x4 a = f16x4{0, 0, 0, 0};
-                if (a_live)
-                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * j);
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    const uint4 u = v[s2][n];
-                    uint2 h = j == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
-                    const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
-                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
+                    for (int n = 0; n < NT; ++n) v[s2][n] = mask_tokens(v[s2][n], n_ok);
                 }
             }
-        }
-        wave_lds_sync();
-    };
-
-    // 4. stream this split's tiles, one in flight per wave
-    while (tA < n_tiles) {
-        process(tA, vA, iA);
-        tA += NW;
-        if (tA < n_tiles) load_tile(tA, vA, iA);
-    }
-
-    // 5. wave results: lanes 0-15 hold rows 0-3 (hi) of dims 16n + l16,
-    //    lanes 16-31 the lo parts of the same rows
-    float out_r[R][NT];
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+            for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float v = acc[n][r];
-            out_r[r][n] = (v + __shfl_down(v, 16)) * (1.f / kPScale);
-        }
+                for (int jj = 0; jj < 2; ++jj) {
+                    f16x4 a = f16x4{0, 0, 0, 0};
+                    if (a_live)
+                        a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * jj);
 #pragma unroll
-    for (int r = 0; r < R; ++r) lsum[r] = wave_sum_dpp(lsum[r]);
-    __syncthreads();  // LUT no longer read; reuse it for the workgroup merge
-    float *wm = smem;
-    float *wl = wm + NW * R;
-    float *wa = wl + NW * R;  // [NW][R][D]
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            wm[wv * R + r] = m[r];
-            wl[wv * R + r] = lsum[r];
+                    for (int n = 0; n < NT; ++n) {
+                        const uint4 u = v[s2][n];
+                        uint2 h = jj == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
+                        const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
+                        acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
+                    }
+                }
+            }
+            wave_lds_sync();
         }
     }
-    if (lane < 16) {
+    __syncthreads();  // every tile consumed; the ring is free for the merge
+
+    // wave results: lanes 0-15 hold rows 0-3 (hi) of dims 16n + l16, lanes
+    // 16-31 the lo parts of the same rows
+    float *wm = reinterpret_cast<float *>(ring);
+    float *wl = wm + NC * R;
+    float *wa = wl + NC * R;  // [NC][R][D]
+    if (!loader) {
+        float out_r[R][NT];
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int n = 0; n < NT; ++n) wa[(wv * R + r) * D + 16 * n + lane] = out_r[r][n];
+            for (int r = 0; r < R; ++r) {
+                const float v = acc[n][r];
+                out_r[r][n] = (v + __shfl_down(v, 16)) * (1.f / kPScale);
+            }
+#pragma unroll
+        for (int r = 0; r < R; ++r) lsum[r] = wave_sum_dpp(lsum[r]);
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                wm[wv * R + r] = m[r];
+                wl[wv * R + r] = lsum[r];
+            }
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int n = 0; n < NT; ++n) wa[(wv * R + r) * D + 16 * n + lane] = out_r[r][n];
+        }
     }
     __syncthreads();
-    const int S = c.n_splits;
-    for (int i = tid; i < R * D; i += THREADS) {
-        const int r = i / D, d = i - r * D;
-        float M = -1e30f;
+    // combine the compute waves' (m, l, acc) of row r into this workgroup's
+    // (M, L, A) for dims d0 .. d0+3
+    auto combine4 = [&](int r, int d0, float &M, float &L, f32x4 &A) {
+        M = -1e30f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w * R + r]);
-        float L = 0.f, A = 0.f;
+        for (int w = 0; w < NC; ++w) M = fmaxf(M, wm[w * R + r]);
+        L = 0.f;
+        A = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
+        for (int w = 0; w < NC; ++w) {
             const float f = fast_exp2(wm[w * R + r] - M);
             L = fmaf(wl[w * R + r], f, L);
-            A = fmaf(wa[(w * R + r) * D + d], f, A);
+            const float *src = wa + (w * R + r) * D + d0;
+            A[0] = fmaf(src[0], f, A[0]);
+            A[1] = fmaf(src[1], f, A[1]);
+            A[2] = fmaf(src[2], f, A[2]);
+            A[3] = fmaf(src[3], f, A[3]);
         }
-        if (S == 1) {
-            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
-        } else {
-            const int64_t slot = ((int64_t)col * S + split) * R + r;
-            c.part_acc[slot * D + d] = A;
-            if (d == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
+    };
+    const int S = c.n_splits;
+    if (S == 1) {
+        for (int i = tid; i < R * D / 4; i += THREADS) {
+            const int r = i / (D / 4), d0 = (i - r * (D / 4)) * 4;
+            float M, L;
+            f32x4 A;
+            combine4(r, d0, M, L, A);
+            if (row_ok(r)) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    store_from_f32(c.out, c.out_dtype, row_off(r) + d0 + k, L > 0.f ? A[k] / L : 0.f);
+            }
+        }
+        return;
+    }
+
+    // Split-T finish inside the kernel.  Every split stores its partial with
+    // sc1 (agent-coherent) buffer stores, which write through this XCD's L2,
+    // waits until they have completed, then adds 1 to its column's counter
+    // with an agent-scope atomic.  The split that sees S - 1 reads all the
+    // column's partials with sc1 loads (never a stale L2 line) and writes
+    // the merged rows; it also resets the counter for the next call.  No
+    // workgroup waits for another, so nothing depends on scheduling order.
+    const int n_cols = gridDim.y;
+    const __amdgpu_buffer_rsrc_t acc_rs =
+        raw_buffer(c.part_acc, (uint32_t)((int64_t)n_cols * S * R * D * 4));
+    const __amdgpu_buffer_rsrc_t ml_rs = raw_buffer(c.part_ml, (uint32_t)((int64_t)n_cols * S * R * 8));
+    const int64_t slot0 = ((int64_t)col * S + split) * R;
+    for (int i = tid; i < R * D / 4; i += THREADS) {
+        const int r = i / (D / 4), d0 = (i - r * (D / 4)) * 4;
+        float M, L;
+        f32x4 A;
+        combine4(r, d0, M, L, A);
+        __builtin_amdgcn_raw_buffer_store_b128(A, acc_rs, (uint32_t)(((slot0 + r) * D + d0) * 4), 0,
+                                               kCpolSc1);
+        if (d0 == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(M), __float_as_uint(L)}, ml_rs,
+                                                  (uint32_t)((slot0 + r) * 8), 0, kCpolSc1);
+    }
+    if (!c.fused_merge) return;  // a merge launch follows
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();
+    volatile lds_t<int> *last = cbar + 1;
+    if (tid == 0)
+        *last = __hip_atomic_fetch_add(c.part_cnt + col, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!*last) return;
+
+    // last split of this column: merge.  LDS (the ring): weights [S][R],
+    // row sums [R], the splits' (m, l) [S][R], then a chunk of the partial
+    // accumulators.  The (m, l) loads and the first chunk's copy are issued
+    // together, so the merge costs one memory round trip per chunk.
+    float *wts = reinterpret_cast<float *>(ring);  // [kMaxSplits][R]
+    float *lrow = wts + kMaxSplits * R;            // [R] (+pad)
+    u32x2 *mlb = reinterpret_cast<u32x2 *>(lrow + 64);
+    const int chunk_off = ((kMaxSplits * R + 64) * 4 + S * R * 8 + 1023) & ~1023;
+    char *chunk = ring + chunk_off;
+    const int cs_max = (K::kSlots * K::kSlot - chunk_off) / (R * D * 4);
+    static_assert(((kMaxSplits * R + 64) * 4 + kMaxSplits * R * 8 + 1023) / 1024 * 1024 +
+                          2 * R * D * 4 <= K::kSlots * K::kSlot,
+                  "merge LDS");
+    static_assert((R * D * 4) % 1024 == 0, "merge chunk granularity");
+    const uint32_t chunk_l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(chunk));
+    // copy the partial accumulators of splits s0 .. s0+cs (contiguous) into LDS
+    auto copy_chunk = [&](int s0, int cs) {
+        const char *src = reinterpret_cast<const char *>(c.part_acc) +
+                          (((int64_t)col * S + s0) * R) * D * 4;
+        const int n_kb = cs * R * D * 4 / 1024;
+        for (int kb = wv; kb < n_kb; kb += NC + 1)
+            __builtin_amdgcn_global_load_lds(src + kb * 1024 + lane * 16,
+                                             reinterpret_cast<lds_t<void> *>(chunk_l + kb * 1024), 16,
+                                             0, kCpolSc1);
+    };
+    u32x2 mlv[(kMaxSplits * R + THREADS - 1) / THREADS];
+    constexpr int MLPT = (kMaxSplits * R + THREADS - 1) / THREADS;
+#pragma unroll
+    for (int k = 0; k < MLPT; ++k) {
+        const int i2 = tid + k * THREADS;  // i2 = s * R + r
+        if (i2 < S * R)
+            mlv[k] = __builtin_amdgcn_raw_buffer_load_b64(
+                ml_rs, (uint32_t)((((int64_t)col * S) * R + i2) * 8), 0, kCpolSc1);
+    }
+    copy_chunk(0, min(cs_max, S));
+#pragma unroll
+    for (int k = 0; k < MLPT; ++k) {
+        const int i2 = tid + k * THREADS;
+        if (i2 < S * R) mlb[i2] = mlv[k];
+    }
+    __syncthreads();
+    if (wv < R) {  // wave r: weights exp2(m_s - M) and the merged l of row r
+        const int r = wv;
+        float M = -1e30f;
+        for (int s2 = lane; s2 < S; s2 += kWave) M = fmaxf(M, __uint_as_float(mlb[s2 * R + r][0]));
+        M = wave_max(M);
+        float L = 0.f;
+        for (int s2 = lane; s2 < S; s2 += kWave) {
+            const u32x2 v = mlb[s2 * R + r];
+            const float w = fast_exp2(__uint_as_float(v[0]) - M);
+            wts[s2 * R + r] = w;
+            L = fmaf(__uint_as_float(v[1]), w, L);
+        }
+        L = wave_sum(L);
+        if (lane == 0) lrow[r] = L;
+    }
+    constexpr int OPT = (R * D + THREADS - 1) / THREADS;  // outputs per thread
+    float accm[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) accm[k] = 0.f;
+    for (int s0 = 0; s0 < S; s0 += cs_max) {
+        const int cs = min(cs_max, S - s0);
+        if (s0 > 0) {
+            __syncthreads();  // previous chunk consumed
+            copy_chunk(s0, cs);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // chunk landed; weights ready
+        const float *cf = reinterpret_cast<const float *>(chunk);
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) {
+            const int i2 = tid + k * THREADS;
+            if (i2 < R * D) {
+                const int r = i2 / D, d = i2 - r * D;
+                float A = accm[k];
+                for (int s2 = 0; s2 < cs; ++s2) A = fmaf(cf[(s2 * R + r) * D + d], wts[(s0 + s2) * R + r], A);
+                accm[k] = A;
+            }
         }
     }
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+        const int i2 = tid + k * THREADS;
+        if (i2 < R * D) {
+            const int r = i2 / D, d = i2 - r * D;
+            const float L = lrow[r];
+            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? accm[k] / L : 0.f);
+        }
+    }
+    if (tid == 0) __hip_atomic_store(c.part_cnt + col, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------------------
 // Merge of split-T partials: one workgroup per (group, row).  One wave turns
 // the splits' (m, l) into weights exp2(m_s - M) and the merged l; every thread
 // then streams float4 slices of the accumulators of a subset of splits (loads
@@ -828,9 +1182,9 @@ static int rows_per_group(int64_t rows_total) { return rows_total <= 1 ? 1 : 4; 
 
 // Kernel families: the VALU kernel (any value layout/dtype, 4 waves per
 // workgroup, 1 or 4 rows) and the MFMA kernel (fp16 values 8-token
-// interleaved, kMfmaWaves waves, 4 rows).
+// interleaved, kMfmaWaves compute waves plus a loader wave, 4 rows).
 enum DecodeKind { kKindValu = 0, kKindMfma = 1 };
-constexpr int kMfmaWaves = 8;
+constexpr int kMfmaWaves = 4;
 
 static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int64_t t_kv,
                                 int n_splits, int kind = kKindValu) {
@@ -860,17 +1214,25 @@ static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int
     return s;
 }
 
-// Workspace layout: [part_ml: n_cols*S*R float2, padded to 256 B]
+// Workspace layout: [part_cnt: kCntBytes, one int per column]
+//                   [part_ml: n_cols*S*R float2, padded to 256 B]
 //                   [part_acc: n_cols*S*R*D float]
+// The MFMA path counts finished splits per column in part_cnt and its last
+// split resets the count.  The counter area has the same place and size for
+// every shape, so it must be zero before the first call on a workspace and
+// then stays zero between calls; shapes with more than kCntBytes/4 columns
+// merge with a separate launch instead.
+constexpr size_t kCntBytes = 64 * 1024;
 struct WsLayout {
-    size_t ml, acc, total;
+    size_t cnt, ml, acc, total;
 };
 
 static WsLayout ws_layout(const DecodeShape &s, int head_dim) {
     auto pad = [](size_t b) { return (b + 255) / 256 * 256; };
     WsLayout w;
     const size_t slots = (size_t)s.n_cols * s.S * s.R;
-    w.ml = 0;
+    w.cnt = 0;
+    w.ml = kCntBytes;
     w.acc = w.ml + pad(slots * 2 * sizeof(float));
     w.total = w.acc + slots * head_dim * sizeof(float);
     return w;
@@ -891,18 +1253,26 @@ static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t
 
 template <int D>
 static int launch_mfma(DecodeCommon c, const __half *v8, const DecodeShape &s, hipStream_t st) {
-    constexpr int NW = kMfmaWaves;
-    const size_t lds = mfma_lds_bytes<D, NW>();
-    auto kern = decode_attn_mfma_kernel<D, NW>;
+    constexpr int NC = kMfmaWaves;
+    using K = WsCfg<D, NC>;
+    auto kern = decode_attn_mfma_kernel<D, NC>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        int dev = 0, max_lds = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess)
+            e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev);
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(LDS)");
+        SS_UNSUPPORTED(max_lds >= K::kLds, "decode needs %d bytes of LDS per workgroup, device has %d",
+                       K::kLds, max_lds);
+        e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, K::kLds);
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(NW * kWave), lds, st, c, v8);
+    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3((NC + 1) * kWave), K::kLds, st, c, v8);
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
+    if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
     return launch_merge<D>(c, s, st);
 }
 
@@ -979,6 +1349,8 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.tiles_per_split = s.tiles_per_split;
     c.part_ml = nullptr;
     c.part_acc = nullptr;
+    c.part_cnt = nullptr;
+    c.fused_merge = s.S > 1 && (size_t)s.n_cols * sizeof(int) <= kCntBytes;
     if (s.S > 1) {
         const size_t need = decode_ws_bytes(s, head_dim);
         if (!ws || ws_bytes < need) {
@@ -989,6 +1361,7 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
         SS_REQUIRE(((uintptr_t)ws % 256) == 0, "workspace must be 256-byte aligned");
         const WsLayout w = ws_layout(s, head_dim);
         char *base = reinterpret_cast<char *>(ws);
+        c.part_cnt = reinterpret_cast<int *>(base + w.cnt);
         c.part_ml = reinterpret_cast<float *>(base + w.ml);
         c.part_acc = reinterpret_cast<float *>(base + w.acc);
     }
