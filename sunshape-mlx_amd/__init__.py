@@ -52,3 +52,18 @@ from .rotation import (  # noqa: E402
     positive_excess_kurtosis,
     safe_normalize,
 )
+from . import attention, cache, patch, value_codecs  # noqa: E402
+from .attention import sunshape_sdpa  # noqa: E402
+from .cache import HybridSunShapeKVCache, SunShapeKVCache, create_kv_cache  # noqa: E402
+from .value_codecs import GroupedValueCodec, TurboQuantValueCodec, build_value_codec  # noqa: E402
+
+__all__ = [
+    "SunShapeBlockCodec", "SunShapeQuantized", "SunShapeKVCache", "HybridSunShapeKVCache",
+    "create_kv_cache", "sunshape_sdpa", "GroupedValueCodec", "TurboQuantValueCodec",
+    "build_value_codec", "block_vq_quantize_hip", "block_vq_score_hip", "fused_attention_hip",
+    "fused_attention_causal_hip", "fused_attention_dequant_hip",
+    "fused_attention_dequant_causal_hip", "fused_block_vq_attention", "quantize_scalar_to_indices",
+    "pack_indices", "unpack_indices", "quantize_values", "dequantize_values", "get_kernel_stats",
+    "reset_kernel_stats", "apply_permutation", "invert_permutation", "generate_rotation_matrix",
+    "covariance_block_permutation",
+]

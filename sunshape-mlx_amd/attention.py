@@ -1,0 +1,167 @@
+"""SunShape SDPA: scaled dot-product attention over block-VQ keys
+(reference attention.py:1-353).
+
+Scores never need dequantised keys: with a fixed block codebook,
+``score[q, t] = sum_b LUT[q, b, idx[t, b]]`` where ``LUT[q, b, c]`` is the dot
+product of query block b with centroid c.  The fused HIP kernels build the LUT
+in LDS and run gather + online softmax + value accumulation in one pass over
+the cache, for every query head of every KV group in a single launch (the
+reference loops over (batch, KV head, q head) with one Metal dispatch each,
+attention.py:268-305).
+
+Routing follows the reference (attention.py:236-246): a compressed-only cache
+with no mask or a causal mask takes a fused kernel; a hybrid cache with
+buffered full-precision tokens, or an explicit mask array, takes the two-pass
+path (attention.py:307-350), which here also runs on the GPU (HIP LUT and
+score kernels, torch softmax and matmul).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _hip
+from .cache import HybridSunShapeKVCache, SunShapeKVCache
+from .codec import PERM_MODES, SunShapeBlockCodec
+
+
+def _kernel_query(codec: SunShapeBlockCodec, queries: torch.Tensor, scale: float):
+    """(q, scale, perm) for the fused kernels, which form
+    ``round_to(q.dtype, q * scale)`` and then permute (attention.py:208, 228).
+    The rotated mode rotates on the host: ``(q * scale) @ R^T`` in float32
+    (attention.py:230), passed with scale 1 and no permutation."""
+    if codec.mode in PERM_MODES:
+        return queries, float(scale), codec.permutation
+    if codec.use_rotation:
+        q = (queries * scale).float() @ codec.rotation.t()
+        return q.contiguous(), 1.0, None
+    return queries, float(scale), None
+
+
+def _transform_grouped(codec: SunShapeBlockCodec, q_grouped: torch.Tensor) -> torch.Tensor:
+    """Codec-space queries from scaled, grouped queries (attention.py:223-232)."""
+    if codec.mode in PERM_MODES:
+        return q_grouped[..., codec.permutation.long()]
+    if codec.use_rotation:
+        return q_grouped.float() @ codec.rotation.t()
+    return q_grouped
+
+
+def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int):
+    """One fused launch over the whole cache, or None when no fused kernel
+    applies to this cache / shape (the reference's None-fallback,
+    kernels.py:259-291)."""
+    ops = cache.fused_operands()
+    if ops is None:
+        return None
+    codec = cache.codec
+    q, kscale, perm = _kernel_query(codec, queries, scale)
+    t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
+    kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
+    try:
+        if ops["kind"] == "il8":
+            out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
+                                       **kw)
+            codec.last_score_backend = "hip_fused_mfma"
+        elif ops["kind"] == "grouped":
+            out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
+                                           ops["packed"], ops["scales"], ops["zeros"],
+                                           ops["bits"], ops["group_size"], **kw)
+            codec.last_score_backend = "hip_fused_dequant"
+        else:
+            out = _hip.decode_attn_dense(q, kscale, perm, codec.centroids, ops["idx"],
+                                         ops["values"], **kw)
+            codec.last_score_backend = "hip_fused"
+    except _hip.SunShapeUnsupported:
+        return None
+    return out
+
+
+def _compressed_scores(codec: SunShapeBlockCodec, q_t: torch.Tensor,
+                       key_indices: torch.Tensor) -> torch.Tensor:
+    """(B, Hkv, rep, Tq, Tc) float32 scores of codec-space queries q_t
+    (B, Hkv, rep, Tq, D) against (B, Hkv, Tc, NB) indices
+    (attention.py:44-73): one HIP LUT build for all rows, one gather per
+    (batch, KV head)."""
+    b_, hkv, rep, tq, d = q_t.shape
+    rows = q_t.reshape(-1, d)
+    if rows.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        rows = rows.float()
+    lut = _hip.build_lut(rows.contiguous(), None, 1.0, codec.centroids)
+    lut = lut.reshape(b_, hkv, rep * tq, codec.n_blocks, codec.n_centroids)
+    tc = key_indices.shape[2]
+    scores = torch.empty((b_, hkv, rep * tq, tc), dtype=torch.float32, device=q_t.device)
+    for b in range(b_):
+        for h in range(hkv):
+            scores[b, h] = _hip.score_gather(lut[b, h], key_indices[b, h])
+    codec.last_score_backend = "hip"
+    return scores.reshape(b_, hkv, rep, tq, tc)
+
+
+def _two_pass(cache, queries: torch.Tensor, scale: float, mask) -> torch.Tensor:
+    """Scores (compressed, then buffered keys in the original basis), mask,
+    float32 softmax, ``@ values`` (attention.py:307-350)."""
+    b_, hq, tq, d = queries.shape
+    hkv = cache.n_kv_heads
+    rep = hq // hkv
+    t_kv = cache.offset
+    codec = cache.codec
+    is_hybrid = isinstance(cache, HybridSunShapeKVCache)
+    q_scaled = queries * scale
+    q_grouped = q_scaled.reshape(b_, hkv, rep, tq, d)
+    parts = []
+    tc = cache.compressed_offset if is_hybrid else t_kv
+    if tc > 0:
+        parts.append(_compressed_scores(codec, _transform_grouped(codec, q_grouped),
+                                        cache.key_indices))
+    if is_hybrid and cache.buffer_offset > 0:
+        kb_t = cache.buffer_keys.float().transpose(-1, -2).contiguous()  # (B, Hkv, D, Tb)
+        parts.append(torch.matmul(q_grouped.float(), kb_t.unsqueeze(2)))
+    scores = parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)
+    scores = scores.reshape(b_, hq, tq, t_kv)
+    if isinstance(mask, str):
+        if mask == "causal":
+            off = t_kv - tq
+            q_pos = torch.arange(off, off + tq, device=queries.device)
+            k_pos = torch.arange(t_kv, device=queries.device)
+            keep = q_pos[:, None] >= k_pos[None, :]
+            scores = torch.where(keep, scores, torch.finfo(torch.float32).min)
+    elif mask is not None:
+        mask = mask.to(queries.device)
+        if mask.dtype == torch.bool:
+            scores = torch.where(mask, scores, torch.finfo(torch.float32).min)
+        else:
+            scores = scores + mask.float()
+    weights = torch.softmax(scores.float(), dim=-1)
+    values = cache.values.float()  # (B, Hkv, T_kv, D)
+    out = torch.matmul(weights.reshape(b_, hkv, rep * tq, t_kv), values)
+    return out.reshape(b_, hq, tq, d).to(queries.dtype)
+
+
+def sunshape_sdpa(queries: torch.Tensor, cache: SunShapeKVCache | HybridSunShapeKVCache,
+                  scale: float, mask: torch.Tensor | str | None = None) -> torch.Tensor:
+    """Attention of ``queries`` (B, n_q_heads, T_q, D) against a SunShape cache
+    (reference attention.py:166-353).  Query head ``h*rep + r`` reads KV head
+    h; ``mask`` is None, ``"causal"`` (query i sees keys ``t <= T_kv - T_q + i``)
+    or an additive / boolean array broadcastable to (B, n_q_heads, T_q, T_kv).
+    Returns (B, n_q_heads, T_q, D) in the query dtype."""
+    b_, hq, tq, d = queries.shape
+    hkv = cache.n_kv_heads
+    if hq % hkv != 0:
+        raise ValueError(f"n_q_heads ({hq}) must be a multiple of the cache's n_kv_heads ({hkv})")
+    if d != cache.head_dim:
+        raise ValueError(f"query head_dim {d} != cache head_dim {cache.head_dim}")
+    t_kv = cache.offset
+    if t_kv == 0:
+        return torch.zeros_like(queries)
+    _hip.require_gpu(queries)
+    is_hybrid = isinstance(cache, HybridSunShapeKVCache)
+    use_causal = isinstance(mask, str) and mask == "causal"
+    buffered = cache.buffer_offset if is_hybrid else 0
+    compressed = cache.compressed_offset if is_hybrid else t_kv
+    can_fuse = buffered == 0 and (mask is None or use_causal) and compressed > 0
+    if can_fuse:
+        out = _fused(cache, queries, scale, use_causal, t_kv - tq if use_causal else 0)
+        if out is not None:
+            return out
+    return _two_pass(cache, queries, scale, mask)

@@ -1,7 +1,10 @@
 """SunShape KV caches on device memory (reference cache.py:1-1108).
 
 ``SunShapeKVCache``: keys as uint8 block-VQ indices (B, H, cap, n_blocks),
-values in fp16 (B, H, cap, D).  ``HybridSunShapeKVCache``: a full-precision
+values in fp16.  For head_dim 64/128 the values are kept 8-token interleaved,
+(B, H, cap/8, D, 8): element (t, d) at [t // 8][d][t % 8], the operand layout
+of the MFMA decode kernel; ``values`` returns the token-major view the
+reference returns.  ``HybridSunShapeKVCache``: a full-precision
 recent-token buffer plus compressed storage whose value backend is fp16,
 grouped 2/3/4-bit, TurboQuant or SunShape block-VQ.
 
@@ -75,6 +78,12 @@ def _dequantize_keys(codec: SunShapeBlockCodec, idx: torch.Tensor) -> torch.Tens
     return k.reshape(b_, h_, t_, codec.head_dim)
 
 
+def _il8_ok(codec: SunShapeBlockCodec, head_dim: int, dtype: torch.dtype) -> bool:
+    """Whether values go 8-token interleaved (the MFMA decode kernel's layout)."""
+    return (dtype == torch.float16 and head_dim in (64, 128) and codec.block_dim == 8
+            and codec.n_blocks * 8 == head_dim and codec.n_centroids <= 256)
+
+
 class SunShapeKVCache:
     """Block-VQ keys + fp16 values; drop-in for mlx-lm's KVCache protocol
     (reference cache.py:59-336)."""
@@ -96,7 +105,9 @@ class SunShapeKVCache:
         # serving loops can switch it off.
         self.return_dequantized_keys = return_dequantized_keys
         self._key_indices: torch.Tensor | None = None  # (B, H, cap, NB) uint8
-        self._values: torch.Tensor | None = None       # (B, H, cap, D) dtype
+        # (B, H, cap/8, D, 8) fp16 when interleaved, else (B, H, cap, D) dtype
+        self._values: torch.Tensor | None = None
+        self.values_interleaved = _il8_ok(codec, self.head_dim, dtype)
         self._capacity = 0
 
     # -------------------------------------------------------------- storage
@@ -107,8 +118,13 @@ class SunShapeKVCache:
         cap = _round_capacity(max(needed, self.max_tokens or 0))
         self._key_indices = _grow(self._key_indices, (b_, self.n_kv_heads, cap, self.n_blocks),
                                   torch.uint8, device, self.offset)
-        self._values = _grow(self._values, (b_, self.n_kv_heads, cap, self.head_dim), self.dtype,
-                             device, self.offset)
+        if self.values_interleaved:
+            # whole 8-token groups move; the tail of the last one is zero
+            self._values = _grow(self._values, (b_, self.n_kv_heads, cap // 8, self.head_dim, 8),
+                                 torch.float16, device, (self.offset + 7) // 8)
+        else:
+            self._values = _grow(self._values, (b_, self.n_kv_heads, cap, self.head_dim),
+                                 self.dtype, device, self.offset)
         self._capacity = cap
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
@@ -122,7 +138,11 @@ class SunShapeKVCache:
         self._ensure_capacity(b_, t_, keys.device)
         sl = slice(self.offset, self.offset + t_)
         _encode_into(self.codec, keys, self._key_indices[:, :, sl])
-        self._values[:, :, sl] = values.to(self.dtype)
+        if self.values_interleaved:
+            v = values if values.stride(-1) == 1 else values.contiguous()
+            _hip.append_values_il8(v, self._values, self.offset)
+        else:
+            self._values[:, :, sl] = values.to(self.dtype)
         self.offset += t_
         return (self.keys if self.return_dequantized_keys else None), self.values
 
@@ -138,10 +158,22 @@ class SunShapeKVCache:
 
     @property
     def values(self) -> torch.Tensor:
+        """Values up to ``offset``, token-major (B, H, T, D) (a copy when the
+        storage is interleaved)."""
         if self._values is None or self.offset == 0:
             return torch.zeros((1, self.n_kv_heads, 0, self.head_dim), dtype=self.dtype,
                                device=self.codec.device)
+        if self.values_interleaved:
+            return _hip.il8_to_dense(self._values, self.offset)
         return self._values[:, :, :self.offset]
+
+    def fused_operands(self) -> dict | None:
+        """Full-capacity device buffers for the fused decode kernels:
+        {"kind": "il8"|"dense", "idx", "values"}; None when empty."""
+        if self._key_indices is None or self.offset == 0:
+            return None
+        return {"kind": "il8" if self.values_interleaved else "dense",
+                "idx": self._key_indices, "values": self._values}
 
     @property
     def key_indices(self) -> torch.Tensor:
@@ -154,7 +186,7 @@ class SunShapeKVCache:
     def state(self):
         z = torch.zeros((1,))
         return (self._key_indices[:, :, :self.offset] if self._key_indices is not None else z,
-                self._values[:, :, :self.offset] if self._values is not None else z)
+                self.values if self._values is not None else z)
 
     # -------------------------------------------------------------- metrics
     @property
@@ -479,6 +511,22 @@ class HybridSunShapeKVCache:
                 or self._compressed_offset == 0:
             return None
         return self._value_zeros[:, :, :self._compressed_offset]
+
+    def fused_operands(self) -> dict | None:
+        """Full-capacity compressed buffers for the fused decode kernels
+        ({"kind": "grouped"|"dense", ...}); None when there is nothing
+        compressed or the value backend has no fused kernel."""
+        if self._key_indices is None or self._compressed_offset == 0:
+            return None
+        if self.value_backend == "grouped":
+            gc = self._value_codec_impl
+            return {"kind": "grouped", "idx": self._key_indices,
+                    "packed": self._values_packed.view(torch.uint32),
+                    "scales": self._value_scales, "zeros": self._value_zeros,
+                    "bits": gc.bits, "group_size": gc.group_size}
+        if self.value_backend == "fp16" and self._values_fp16 is not None:
+            return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
+        return None
 
     @property
     def can_fuse_value_dequant(self) -> bool:

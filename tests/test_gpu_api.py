@@ -1,0 +1,270 @@
+"""GPU parity of the drop-in Python surface (caches, ``sunshape_sdpa``, value
+codecs, SDPA router) against the CPU oracle.
+
+Bars: key indices bit-exact except oracle-flagged near-ties; stored values
+bit-exact; attention outputs max |gpu - oracle| <= 1e-3 * max |oracle| (fp32
+accumulate, float64 oracle), with fp16 outputs compared after rounding the
+oracle to fp16 at a 2e-3 bar.
+"""
+
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sunshape_oracle as O
+import sunshape_mlx_amd as S
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+REL_TOL = 1e-3
+
+
+def rel_err(got, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def make_codec(seed, d=128, nc=256, mode="profileperm_baseline"):
+    rng = np.random.default_rng(seed)
+    nb = d // 8
+    codec = S.SunShapeBlockCodec(d, n_centroids=nc, device=DEV,
+                                 use_rotation=(mode == "rotated"), rotation_seed=seed)
+    state = {"centroids": rng.standard_normal((nb, nc, 8)).astype(np.float32)}
+    if mode != "rotated":
+        state["permutation"] = rng.permutation(d).astype(np.int32)
+    codec.load_state_dict(state)
+    return codec
+
+
+def kv(seed, b, hkv, t_, d, dtype=torch.float16):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    k = torch.randn((b, hkv, t_, d), generator=g, device=DEV).to(dtype)
+    v = torch.randn((b, hkv, t_, d), generator=g, device=DEV).to(dtype)
+    return k, v
+
+
+def oracle_indices(codec, keys):
+    cents = codec.centroids.cpu().numpy()
+    perm = codec.permutation.cpu().numpy()
+    b_, h_, t_, d = keys.shape
+    res = O.encode_blockvq(keys.float().cpu().numpy().reshape(-1, d), cents, perm)
+    idx, near = res[0], res[1]
+    return idx.reshape(b_, h_, t_, -1), near.reshape(b_, h_, t_, -1)
+
+
+@pytest.mark.parametrize("d,prefill,steps", [(128, 300, 5), (64, 17, 9)])
+def test_fp16_cache_store_and_fused_decode(d, prefill, steps):
+    codec = make_codec(1, d=d)
+    b, hq, hkv = 2, 8, 2
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, head_dim=d)
+    assert isinstance(cache, S.SunShapeKVCache) and cache.values_interleaved
+    k, v = kv(2, b, hkv, prefill + steps, d)
+    cache.update_and_fetch(k[:, :, :prefill], v[:, :, :prefill])
+    for s in range(steps):
+        sl = slice(prefill + s, prefill + s + 1)
+        keys_out, vals_out = cache.update_and_fetch(k[:, :, sl], v[:, :, sl])
+    t_kv = prefill + steps
+    assert cache.offset == t_kv
+    # stored values round-trip bit-exactly through the interleaved layout
+    assert torch.equal(cache.values, v)
+    assert torch.equal(vals_out, v)
+    # key indices: bit-exact except near-ties
+    idx_ref, near = oracle_indices(codec, k)
+    got = cache.key_indices.cpu().numpy()
+    assert np.array_equal(got[~near], idx_ref[~near])
+    # returned keys are the dequantised indices
+    cents = codec.centroids.cpu().numpy()
+    inv = codec.inv_permutation.cpu().numpy()
+    khat = O.dequantize_blockvq(got.reshape(-1, d // 8), cents, inv).reshape(b, hkv, t_kv, d)
+    assert np.array_equal(keys_out.cpu().numpy(), khat.astype(np.float32))
+    # one decode step through the fused MFMA path
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 1.0 / np.sqrt(d), mask=None)
+    assert codec.last_score_backend == "hip_fused_mfma"
+    ref = O.sdpa(q.cpu().numpy(), got, v.cpu().numpy(), cents, codec.permutation.cpu().numpy(),
+                 1.0 / np.sqrt(d))
+    assert out.dtype == torch.float16
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+
+def test_fp16_cache_causal_prefill_and_capacity_growth():
+    codec = make_codec(3)
+    b, hq, hkv, d = 1, 8, 2, 128
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv)
+    k, v = kv(4, b, hkv, 600, d)
+    cache.update_and_fetch(k[:, :, :250], v[:, :, :250])   # capacity 256
+    cache.update_and_fetch(k[:, :, 250:600], v[:, :, 250:600])  # grows to 768
+    assert torch.equal(cache.values, v)
+    tq = 16
+    q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.1, mask="causal")
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.1,
+                 mask="causal")
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+
+def test_mask_array_takes_two_pass_and_matches():
+    codec = make_codec(5)
+    b, hq, hkv, d, t_kv, tq = 1, 4, 1, 128, 96, 3
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv)
+    k, v = kv(6, b, hkv, t_kv, d)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
+    rng = np.random.default_rng(7)
+    m_add = rng.standard_normal((tq, t_kv)).astype(np.float32)
+    out = S.sunshape_sdpa(q, cache, 0.09, mask=torch.from_numpy(m_add))
+    assert codec.last_score_backend == "hip"
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.09, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(), None,
+                          v.cpu().numpy(), mask=m_add)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    m_bool = rng.random((tq, t_kv)) > 0.3
+    out = S.sunshape_sdpa(q, cache, 0.09, mask=torch.from_numpy(m_bool))
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.09, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(), None,
+                          v.cpu().numpy(), mask=m_bool)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.float16])
+def test_hybrid_grouped_fused_and_buffered(scale_dtype):
+    codec = make_codec(8)
+    b, hq, hkv, d = 1, 8, 2, 128
+    k, v = kv(9, b, hkv, 300, d)
+    # buffer_size 0: every token is compressed, the fused dequant path runs
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2,
+                              buffer_size=0, value_scale_dtype=scale_dtype)
+    cache.update_and_fetch(k, v)
+    assert cache.buffer_offset == 0 and cache.compressed_offset == 300
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    assert codec.last_score_backend == "hip_fused_dequant"
+    packed = cache.values_packed_raw.cpu().numpy()
+    sc = cache.value_scales_raw.float().cpu().numpy()
+    zr = cache.value_zeros_raw.float().cpu().numpy()
+    vals = O.dequantize_values(packed.reshape(-1, packed.shape[-1]), sc.reshape(-1, sc.shape[-1]),
+                               zr.reshape(-1, zr.shape[-1]), d, 2, 64).reshape(b, hkv, 300, d)
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # default buffer: 128 recent tokens stay fp16, the two-pass path runs
+    cache2 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2,
+                               value_scale_dtype=scale_dtype)
+    cache2.update_and_fetch(k, v)
+    assert cache2.buffer_offset == 128 and cache2.compressed_offset == 172
+    out2 = S.sunshape_sdpa(q, cache2, 0.088)
+    assert codec.last_score_backend == "hip"
+    vals_all = np.concatenate([vals[:, :, :172], v[:, :, 172:].float().cpu().numpy()], axis=2)
+    ref2 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                           codec.centroids.cpu().numpy(), cache2.key_indices.cpu().numpy(),
+                           cache2.buffer_keys.float().cpu().numpy(), vals_all)
+    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
+    # trim removes buffered tokens first (reference cache.py:954-963)
+    cache2.trim(130)
+    assert cache2.buffer_offset == 0 and cache2.compressed_offset == 170
+
+
+def test_hybrid_fp16_and_sunshape_value_backends():
+    codec = make_codec(10)
+    b, hq, hkv, d = 1, 4, 1, 128
+    k, v = kv(11, b, hkv, 200, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="fp16", buffer_size=0)
+    assert isinstance(cache, S.HybridSunShapeKVCache)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    assert codec.last_score_backend == "hip_fused"
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # SunShape-coded values: no fused kernel, two-pass over dequantised values
+    vcodec = make_codec(12)
+    cache3 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="sunshape", value_bits=8,
+                               value_codec=vcodec, buffer_size=0)
+    cache3.update_and_fetch(k, v)
+    out3 = S.sunshape_sdpa(q, cache3, 0.088)
+    vals = cache3.values.float().cpu().numpy()
+    ref3 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                           codec.centroids.cpu().numpy(), cache3.key_indices.cpu().numpy(), None,
+                           vals)
+    assert rel_err(out3.float().cpu().numpy(), ref3) <= 2e-3
+
+
+def test_rotated_codec_fused_decode():
+    codec = make_codec(13, mode="rotated")
+    b, hq, hkv, d = 1, 8, 2, 128
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv)
+    k, v = kv(14, b, hkv, 150, d)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    r = codec.rotation.cpu().numpy().astype(np.float64)
+    qs = O.scale_query(q.cpu().numpy(), 0.088).astype(np.float64)
+    qt = (qs @ r.T).astype(np.float32).reshape(b, hkv, hq // hkv, 1, d)
+    idx = cache.key_indices.cpu().numpy()
+    cents = codec.centroids.cpu().numpy()
+    vv = v.cpu().numpy()
+    ref = np.zeros((b, hq, 1, d))
+    for h in range(hkv):
+        for rr in range(hq // hkv):
+            ref[0, h * (hq // hkv) + rr] = O.fused_attention(qt[0, h, rr], cents, idx[0, h], vv[0, h])
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+
+def test_turboquant_value_codec_matches_oracle():
+    d, bits = 128, 3
+    tq = S.TurboQuantValueCodec(head_dim=d, bits=bits, seed=43, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(15)
+    vals = torch.randn((64, d), generator=g, device=DEV)
+    packed, norms = tq.quantize(vals)
+    v64 = vals.cpu().numpy().astype(np.float64)
+    rot = tq.rotation.cpu().numpy()
+    bounds = tq.boundaries.cpu().numpy()
+    ref_packed, ref_norms, _ = O.turboquant_encode(v64, rot, bounds, bits)
+    # codes equal except coordinates within 1e-5 of a boundary (fp32 rotate)
+    u = v64 / np.maximum(np.linalg.norm(v64, axis=-1, keepdims=True), 1e-8)
+    r = u @ rot.astype(np.float64).T
+    near = (np.abs(r[..., None] - bounds.astype(np.float64)) < 1e-5).any(-1)
+    got_idx = O.unpack_indices(packed.cpu().numpy(), d, bits)
+    ref_idx = O.unpack_indices(ref_packed, d, bits)
+    assert np.array_equal(got_idx[~near], ref_idx[~near])
+    assert np.allclose(norms.cpu().numpy(), ref_norms, rtol=1e-6)
+    rec = tq.dequantize(packed, norms).cpu().numpy()
+    ref_rec = O.turboquant_decode(packed.cpu().numpy(), norms.cpu().numpy(), rot,
+                                  tq.centroids.cpu().numpy(), d, bits)
+    assert rel_err(rec, ref_rec) <= 1e-5
+
+
+def test_router_sends_sunshape_caches_to_sunshape_sdpa():
+    codec = make_codec(16)
+    cache = S.create_kv_cache(codec, n_kv_heads=1)
+    k, v = kv(17, 1, 1, 40, 128)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((1, 2, 1, 128), device=DEV).to(torch.float16)
+    calls = []
+    mod = types.ModuleType("ss_test_models_base")
+
+    def original(queries, keys, values, cache, scale, mask, sinks=None):
+        calls.append("original")
+        return torch.zeros_like(queries)
+
+    mod.scaled_dot_product_attention = original
+    sys.modules["ss_test_models_base"] = mod
+    try:
+        S.patch.register_target("ss_test_models_base")
+        S.patch.apply()
+        assert S.patch.is_patched()
+        out = mod.scaled_dot_product_attention(q, None, None, cache, 0.088, None)
+        assert torch.equal(out, S.sunshape_sdpa(q, cache, 0.088))
+        mod.scaled_dot_product_attention(q, k, v, object(), 0.088, None)
+        assert calls == ["original"]
+        S.patch.revert()
+        assert mod.scaled_dot_product_attention is original and not S.patch.is_patched()
+    finally:
+        S.patch.revert()
+        S.patch._extra_targets.clear()
+        sys.modules.pop("ss_test_models_base", None)
