@@ -527,7 +527,7 @@ struct WsCfg {
     static constexpr int kLds = kRing + kSlots * kSlot;
     static_assert(kSlots >= 2 && kSlots <= kFlagWords, "ring slots");
     static_assert(kLds <= kLdsMax, "LDS budget");
-    static_assert(NC * kMfmaRows * (D + 2) * 4 <= kSlots * kSlot, "merge scratch");
+    static_assert(NC * kMfmaRows * (2 * D + 2) * 4 <= kSlots * kSlot, "merge scratch");
     static_assert(2 * kMfmaRows * D * 4 <= kPst, "query staging");
     static_assert((NC * kWave) % kNB == 0 && kLutStride % ((NC * kWave) / kNB) == 0, "LUT split");
 };
@@ -912,20 +912,15 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     }
     __syncthreads();  // every tile consumed; the ring is free for the merge
 
-    // wave results: lanes 0-15 hold rows 0-3 (hi) of dims 16n + l16, lanes
-    // 16-31 the lo parts of the same rows
+    // wave results: lanes 0-15 hold rows 0-3 (hi parts) of dims 16n + l16,
+    // lanes 16-31 the lo parts of the same rows; both go to LDS as they are
+    // (wa[w][0 = hi, 1 = lo][r][d]) and the combine adds them, so every read
+    // of the combine can be issued at once (one LDS round trip)
     float *wm = reinterpret_cast<float *>(ring);
     float *wl = wm + NC * R;
-    float *wa = wl + NC * R;  // [NC][R][D]
+    float *wa = wl + NC * R;  // [NC][2][R][D]
+    static_assert((2 * NC * R) % 4 == 0, "wa alignment");
     if (!loader) {
-        float out_r[R][NT];
-#pragma unroll
-        for (int n = 0; n < NT; ++n)
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float v = acc[n][r];
-                out_r[r][n] = (v + __shfl_down(v, 16)) * (1.f / kPScale);
-            }
 #pragma unroll
         for (int r = 0; r < R; ++r) lsum[r] = wave_sum_dpp(lsum[r]);
         if (lane == 0) {
@@ -935,31 +930,38 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 wl[wv * R + r] = lsum[r];
             }
         }
-        if (lane < 16) {
+        if (g < 2) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int n = 0; n < NT; ++n) wa[(wv * R + r) * D + 16 * n + lane] = out_r[r][n];
+                for (int n = 0; n < NT; ++n)
+                    wa[((wv * 2 + g) * R + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
         }
     }
     __syncthreads();
     // combine the compute waves' (m, l, acc) of row r into this workgroup's
     // (M, L, A) for dims d0 .. d0+3
+    const lds_t<f32x4> *wa4 = to_lds<f32x4>(wa);
     auto combine4 = [&](int r, int d0, float &M, float &L, f32x4 &A) {
+        float mw[NC], lw[NC];
+        f32x4 hi[NC], lo[NC];
+#pragma unroll
+        for (int w = 0; w < NC; ++w) {
+            mw[w] = wm[w * R + r];
+            lw[w] = wl[w * R + r];
+            hi[w] = wa4[(((w * 2 + 0) * R + r) * D + d0) / 4];
+            lo[w] = wa4[(((w * 2 + 1) * R + r) * D + d0) / 4];
+        }
         M = -1e30f;
 #pragma unroll
-        for (int w = 0; w < NC; ++w) M = fmaxf(M, wm[w * R + r]);
+        for (int w = 0; w < NC; ++w) M = fmaxf(M, mw[w]);
         L = 0.f;
         A = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < NC; ++w) {
-            const float f = fast_exp2(wm[w * R + r] - M);
-            L = fmaf(wl[w * R + r], f, L);
-            const float *src = wa + (w * R + r) * D + d0;
-            A[0] = fmaf(src[0], f, A[0]);
-            A[1] = fmaf(src[1], f, A[1]);
-            A[2] = fmaf(src[2], f, A[2]);
-            A[3] = fmaf(src[3], f, A[3]);
+            const float f = fast_exp2(mw[w] - M);
+            L = fmaf(lw[w], f, L);
+            A += (hi[w] + lo[w]) * f;
         }
     };
     const int S = c.n_splits;
@@ -1067,10 +1069,12 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         L = wave_sum(L);
         if (lane == 0) lrow[r] = L;
     }
-    constexpr int OPT = (R * D + THREADS - 1) / THREADS;  // outputs per thread
-    float accm[OPT];
-#pragma unroll
-    for (int k = 0; k < OPT; ++k) accm[k] = 0.f;
+    // thread i2 < R*D/4 accumulates dims 4*(i2 % (D/4)) .. +3 of row
+    // i2 / (D/4) over the chunk's splits (float4 LDS reads, two accumulators)
+    constexpr int CH4 = R * D / 4;
+    static_assert(CH4 <= THREADS, "one float4 chunk per thread");
+    const int mr = tid / (D / 4), md0 = (tid - (tid / (D / 4)) * (D / 4)) * 4;
+    f32x4 acc0 = f32x4{0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
     for (int s0 = 0; s0 < S; s0 += cs_max) {
         const int cs = min(cs_max, S - s0);
         if (s0 > 0) {
@@ -1079,26 +1083,23 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // chunk landed; weights ready
-        const float *cf = reinterpret_cast<const float *>(chunk);
-#pragma unroll
-        for (int k = 0; k < OPT; ++k) {
-            const int i2 = tid + k * THREADS;
-            if (i2 < R * D) {
-                const int r = i2 / D, d = i2 - r * D;
-                float A = accm[k];
-                for (int s2 = 0; s2 < cs; ++s2) A = fmaf(cf[(s2 * R + r) * D + d], wts[(s0 + s2) * R + r], A);
-                accm[k] = A;
+        if (tid < CH4) {
+            const lds_t<f32x4> *cf4 = to_lds<f32x4>(chunk);
+            int s2 = 0;
+#pragma unroll 4
+            for (; s2 + 1 < cs; s2 += 2) {
+                acc0 += cf4[((s2 * R + mr) * D + md0) / 4] * wts[(s0 + s2) * R + mr];
+                acc1 += cf4[(((s2 + 1) * R + mr) * D + md0) / 4] * wts[(s0 + s2 + 1) * R + mr];
             }
+            if (s2 < cs) acc0 += cf4[((s2 * R + mr) * D + md0) / 4] * wts[(s0 + s2) * R + mr];
         }
     }
+    if (tid < CH4 && row_ok(mr)) {
+        const float L = lrow[mr];
+        const f32x4 A = acc0 + acc1;
 #pragma unroll
-    for (int k = 0; k < OPT; ++k) {
-        const int i2 = tid + k * THREADS;
-        if (i2 < R * D) {
-            const int r = i2 / D, d = i2 - r * D;
-            const float L = lrow[r];
-            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? accm[k] / L : 0.f);
-        }
+        for (int k = 0; k < 4; ++k)
+            store_from_f32(c.out, c.out_dtype, row_off(mr) + md0 + k, L > 0.f ? A[k] / L : 0.f);
     }
     if (tid == 0) __hip_atomic_store(c.part_cnt + col, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
