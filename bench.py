@@ -143,9 +143,12 @@ def main() -> int:
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
 
+    # the il8 kernel reads the codec's split-fp16 codebook (prepared once per codec)
+    cb = codec.kernel_codebook() if args.layout == "il8" else codec.centroids
+
     def arg_tuples(stream_handle):
         return [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, codec.permutation.data_ptr(),
-                 codec.centroids.data_ptr(), nb, 256, idxs[i].data_ptr(), vals[i].data_ptr(),
+                 cb.data_ptr(), nb, 256, idxs[i].data_ptr(), vals[i].data_ptr(),
                  hip.SS_F16, t_kv, t_kv, 0, 0, out.data_ptr(), hip.SS_F16, ws.data_ptr(),
                  ws_bytes, splits, stream_handle) for i in range(n_copies)]
 

@@ -141,17 +141,37 @@ int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64
                    size_t *workspace_bytes_out);
 
 /*
+ * Codebook operand of ss_decode_attn_il8, prepared once per codebook (no
+ * reference counterpart: the reference passes float32 centroids to every
+ * fused_attention_metal call, kernels.py:233-291).  centroids float32
+ * [n_blocks][n_centroids][8] is scaled by a power of two 2^-e (max |C| * 2^-e
+ * < 2^14) and split into fp16 parts C' = hi + lo * 2^-11, stored in the
+ * kernel's operand order: for 4-block group bg < n_blocks/4 and centroid
+ * tile ct < ceil(n_centroids/16), tile (bg*ceil(n_centroids/16) + ct) holds
+ * hi[64][8] then lo[64][8], row l being centroid ct*16 + l%16 of block
+ * bg*4 + l/16 (zero past the last centroid); the float 2^e follows.
+ * n_blocks must be a multiple of 4.  ss_codebook_f16x2_bytes gives the
+ * size; out must be 16-byte aligned.
+ */
+size_t ss_codebook_f16x2_bytes(int n_blocks, int n_centroids);
+int ss_codebook_f16x2(const float *centroids, int n_blocks, int n_centroids, void *out,
+                      void *stream);
+
+/*
  * As ss_decode_attn_dense for fp16 values held in the cache's 8-token
  * interleaved layout: element (t, d) of a (batch, KV head) row lives at
  * values_il8[((b*n_kv_heads + h)*cap/8 + t/8)*head_dim*8 + d*8 + t%8]
- * (cap % 8 == 0).  P.V runs on the matrix cores (v_mfma_f32_16x16x16f16 with
- * the probabilities split into fp16 hi/lo parts, fp32 accumulation); four
- * query rows per KV group are processed together.  Same reference semantics
- * as ss_decode_attn_dense (kernels.py:142-223, 303-378; attention.py:199-305).
+ * (cap % 8 == 0), with the codebook prepared by ss_codebook_f16x2.  Both the
+ * query x centroid LUT (split-fp16 v_mfma_f32_16x16x32_f16: exact fp16
+ * products, fp32 accumulation) and P.V (v_mfma_f32_16x16x16f16 with the
+ * probabilities split into fp16 hi/lo parts) run on the matrix cores; four
+ * query rows per KV group are processed together.  Scaled queries must lie in
+ * the fp16 range (always true for fp16 queries).  Same reference semantics as
+ * ss_decode_attn_dense (kernels.py:142-223, 303-378; attention.py:199-305).
  */
 int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                        int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                       const int32_t *perm, const float *centroids, int n_blocks,
+                       const int32_t *perm, const void *codebook, int n_blocks,
                        int n_centroids, const uint8_t *idx, const void *values_il8,
                        int v_dtype, int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
                        void *out, int out_dtype, void *workspace, size_t workspace_bytes,

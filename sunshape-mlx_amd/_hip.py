@@ -70,6 +70,8 @@ _SIGNATURES = {
                                   _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
                                   _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
                                   _int, _c_void_p]),
+    "ss_codebook_f16x2_bytes": (_size, [_int, _int]),
+    "ss_codebook_f16x2": (_int, [_c_void_p, _int, _int, _c_void_p, _c_void_p]),
     "ss_append_values_il8": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                                     _c_void_p, _i64, _i64, _c_void_p]),
     "ss_decode_attn_grouped": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
@@ -322,14 +324,33 @@ def decode_plan(kind, batch, n_q_heads, n_kv_heads, t_q, head_dim, t_kv, n_split
     return int(sp.value), int(wb.value)
 
 
+def codebook_f16x2(centroids: torch.Tensor) -> torch.Tensor:
+    """Split-fp16 codebook (flat uint8 buffer) read by :func:`decode_attn_il8`
+    for float32 centroids (n_blocks, n_centroids, 8)."""
+    require_gpu(centroids)
+    if centroids.dim() != 3 or centroids.dtype != torch.float32 or not centroids.is_contiguous():
+        raise ValueError("centroids must be contiguous float32 (n_blocks, n_centroids, 8)")
+    nb, nc, _ = centroids.shape
+    lib = load_library()
+    out = torch.empty(lib.ss_codebook_f16x2_bytes(nb, nc), dtype=torch.uint8,
+                      device=centroids.device)
+    check(lib.ss_codebook_f16x2(ptr(centroids), nb, nc, ptr(out), stream_handle(centroids.device)))
+    return out
+
+
 def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                     centroids: torch.Tensor, idx: torch.Tensor, values_il8: torch.Tensor,
                     t_kv: int, causal: bool = False, q_offset: int = 0,
                     out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                    n_splits: int = 0) -> torch.Tensor:
-    """Fused decode (MFMA P.V) over fp16 values in the 8-token interleaved
-    layout ``values_il8`` (B, Hkv, cap/8, D, 8)."""
+                    n_splits: int = 0, codebook: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused decode (matrix-core LUT and P.V) over fp16 values in the 8-token
+    interleaved layout ``values_il8`` (B, Hkv, cap/8, D, 8).  ``codebook`` is
+    :func:`codebook_f16x2` of ``centroids`` (prepared here when None)."""
     _check_decode_common(q, idx, centroids, perm)
+    if codebook is None:
+        codebook = codebook_f16x2(centroids)
+    elif codebook.numel() != load_library().ss_codebook_f16x2_bytes(*centroids.shape[:2]):
+        raise ValueError("codebook does not match the centroids' shape")
     require_gpu(values_il8)
     b_, hq, tq, d = q.shape
     _, hkv, cap, nb = idx.shape
@@ -342,7 +363,7 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
     _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
     check(load_library().ss_decode_attn_il8(
-        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
         nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv), int(bool(causal)),
         int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
         int(n_splits), stream_handle(q.device)))

@@ -61,7 +61,7 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     try:
         if ops["kind"] == "il8":
             out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
-                                       **kw)
+                                       codebook=codec.kernel_codebook(), **kw)
             codec.last_score_backend = "hip_fused_mfma"
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],

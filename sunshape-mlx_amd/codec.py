@@ -288,6 +288,18 @@ class SunShapeBlockCodec:
         e = self.E.reshape(nb, bd, nb, bd)
         return torch.stack([e[b, :, b, :] for b in range(nb)])  # (nb, bd, bd)
 
+    def kernel_codebook(self) -> torch.Tensor:
+        """The centroids as the split-fp16 buffer read by the matrix-core LUT
+        build of the fused fp16-value decode, prepared once and rebuilt when
+        the centroids change (new tensor, device or in-place update)."""
+        c = self.centroids
+        key = (c.data_ptr(), c._version, str(c.device), tuple(c.shape))
+        cached = getattr(self, "_kernel_codebook", None)
+        if cached is None or cached[0] != key:
+            cached = (key, _hip.codebook_f16x2(c))
+            self._kernel_codebook = cached
+        return cached[1]
+
     def _encode_centroids(self) -> torch.Tensor:
         if self.mode == "profileperm_localmetric_dsq":
             if self._shaped_centroids is None:

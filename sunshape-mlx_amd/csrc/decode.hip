@@ -21,6 +21,8 @@
 //     step is a single kernel launch.
 // Softmax runs in log2 units (LUT pre-multiplied by log2 e, exp2 on the
 // hardware exp unit), accumulating in float32.
+#include <type_traits>
+
 #include "ss_common.hpp"
 
 namespace ss {
@@ -29,11 +31,14 @@ struct DecodeCommon {
     const void *q;
     const int32_t *perm;
     const float *centroids;
+    const uint4 *codebook;       // split-fp16 codebook of the matrix-core LUT build (il8)
+    const float *codebook_mul;   // its power-of-two scale (device memory)
     const uint8_t *idx;
     void *out;
     float *part_ml;   // [cols][splits][R] (m, l)
     float *part_acc;  // [cols][splits][R][D]
-    int *part_cnt;    // [cols] splits finished (in-kernel merge); zero between calls
+    int *part_cnt;    // [cols * cnt_stride] splits finished (in-kernel merge); zero between calls
+    int cnt_stride;   // ints between two columns' counters (own cache lines: no contention)
     int fused_merge;  // MFMA kernel: merge the splits in-kernel (else a merge launch)
     int q_dtype, out_dtype;
     int n_q_heads, n_kv_heads, rep, n_rg;
@@ -51,6 +56,12 @@ constexpr int kDecodeWaves = kDecodeThreads / kWave;
 constexpr int kLutStride = 256;  // LUT entries reserved per (row, block)
 constexpr int kBlockDim = 8;
 constexpr int kMaxSplits = 512;  // split weights of the merge live in LDS
+
+// Split-fp16 operands of the matrix-core LUT build: x = hi + lo / kSplitScale
+// with hi = fp16(x), lo = fp16((x - hi) * kSplitScale).
+constexpr float kSplitScale = 2048.f;
+// The prepared codebook is scaled by 2^-e so that max |C| * 2^-e < 2^kCbMaxExp.
+constexpr int kCbMaxExp = 14;
 
 constexpr int pow2_ceil(int x) { return x <= 1 ? 1 : 2 * pow2_ceil((x + 1) / 2); }
 
@@ -457,6 +468,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kPScale = 32768.f;  // 2^15
 constexpr int kMfmaRows = 4;
@@ -529,7 +541,11 @@ struct WsCfg {
     static_assert(kLds <= kLdsMax, "LDS budget");
     static_assert(NC * kMfmaRows * (2 * D + 2) * 4 <= kSlots * kSlot, "merge scratch");
     static_assert(2 * kMfmaRows * D * 4 <= kPst, "query staging");
-    static_assert((NC * kWave) % kNB == 0 && kLutStride % ((NC * kWave) / kNB) == 0, "LUT split");
+    // LUT build on the matrix cores: tiles of 4 blocks x 16 centroids, each
+    // compute wave owns kLutTiles of them, all in one 4-block group
+    static constexpr int kLutTiles = (kNB / 4) * (kLutStride / 16) / NC;
+    static_assert(kNB % 4 == 0 && (kNB / 4) * (kLutStride / 16) % NC == 0 &&
+                      (kLutStride / 16) % kLutTiles == 0, "LUT split");
 };
 
 // Zero the fp16 values of tokens >= n_ok (0..8) in an 8-token group.
@@ -652,10 +668,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     // Prologue.  The compute waves' small loads (query element, permutation
     // entry, codebook entries) are issued before the loader's first tiles, so
     // they sit ahead of the tiles in the compute unit's memory queue; the
-    // loader starts streaming once they have landed, and the LUT is built
-    // while the first tiles are in flight.
-    constexpr int TPB = (NC * kWave) / NB;  // LUT threads per codebook block
-    constexpr int EPT = kLutStride / TPB;   // LUT entries per thread
+    // LUT is built while the first tiles are in flight.
+    constexpr int LT = K::kLutTiles;  // LUT tiles (4 blocks x 16 centroids) per compute wave
     float *qraw = reinterpret_cast<float *>(pst);  // [R][D] (P staging is free here)
     float *qp = qraw + R * D;                      // [R][D]
     constexpr int CT = NC * kWave;             // compute threads
@@ -707,7 +721,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             if (++spins > kSpinLimit) break;
         }
     } else {
-        float4 cv[EPT][2];
+        uint4 cb_hi[LT], cb_lo[LT];
+        const float cb_mul = *c.codebook_mul;
         uint32_t q_word[QE];
         int perm_v[QE];
         int64_t q_byte[QE];
@@ -728,14 +743,17 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                                        : reinterpret_cast<const int *>(c.q);
                 perm_v[u] = *pp;
             }
-            const int lb = tid / TPB, cc0 = tid % TPB;
+            // codebook operand of LUT tile t (B of the MFMA below): lane l
+            // holds centroid ct*16 + l%16 of block bg*4 + l/16, hi and lo,
+            // stored in lane order (1 KB contiguous per load); tiles past
+            // the last centroid reload the last tile
+            const int nct = (c.n_centroids + 15) / 16;
 #pragma unroll
-            for (int k = 0; k < EPT; ++k) {
-                const int cc = min(cc0 + TPB * k, c.n_centroids - 1);
-                const float4 *cp = reinterpret_cast<const float4 *>(
-                    c.centroids + ((int64_t)lb * c.n_centroids + cc) * kBlockDim);
-                cv[k][0] = cp[0];
-                cv[k][1] = cp[1];
+            for (int t = 0; t < LT; ++t) {
+                const int flat = wv * LT + t, bg = flat / 16, ct = min(flat % 16, nct - 1);
+                const uint4 *cp = c.codebook + (bg * nct + ct) * 2 * kWave + lane;
+                cb_hi[t] = cp[0];
+                cb_lo[t] = cp[kWave];
             }
         }
         lds_barrier();  // small loads issued, flags initialised
@@ -770,37 +788,69 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         }
         compute_barrier(2);
         {
-            // LUT entry (b, cc) holds the 4 rows' dot products, in log2 units;
-            // this thread: block b = tid / TPB, centroids cc = tid % TPB + TPB*k
-            const int lb = tid / TPB, cc0 = tid % TPB;
+            // LUT entry (b, cc) holds the 4 rows' dot products, in log2 units,
+            // computed on the matrix cores: for 4 blocks bg*4+s and 16
+            // centroids at once, D[4s + r][n] = sum_k A[4s + r][k] B[k][n]
+            // with K = 32 = 4 blocks x 8 dims, A block-diagonal (row 4s + r
+            // holds query row r's dims of block s in the K slice of block s,
+            // zero elsewhere) and B[k][n] the dims of centroid n.  Operands
+            // are split fp16: x = hi + lo * 2^-11 for the codebook (prepared
+            // with a power-of-two scale) and, unless the query is already
+            // fp16, for the query; products of fp16 parts are exact and
+            // accumulate in fp32.
+            const int bg = (wv * LT) / 16;
+            const int ar = l16 & 3;                  // query row of this A lane
+            const bool a_live = (l16 >> 2) == g;     // block-diagonal
             const lds_t<f32x4> *qp4 = to_lds<f32x4>(qp);
-            f32x4 qa[R], qb[R];
+            const f32x4 x0 = qp4[(ar * D + (bg * 4 + g) * kBlockDim) / 4];
+            const f32x4 x1 = qp4[(ar * D + (bg * 4 + g) * kBlockDim) / 4 + 1];
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            f16x8 a_hi, a_lo;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                qa[r] = qp4[(r * D + lb * kBlockDim) / 4];
-                qb[r] = qp4[(r * D + lb * kBlockDim) / 4 + 1];
+            for (int i = 0; i < 8; ++i) {
+                const float x = a_live ? xs[i] : 0.f;
+                const _Float16 h = (_Float16)x;
+                a_hi[i] = h;
+                a_lo[i] = (_Float16)((x - (float)h) * kSplitScale);
             }
+            const float mul = cb_mul * kLog2e;
+            const float mul_lo = mul * (1.f / kSplitScale);
+            // all products first (back to back on the matrix core), then
+            // scale and store; tiles past the last centroid are computed on
+            // the reloaded last tile and not stored
+            auto build = [&](auto q_split) {
+                constexpr int G = 4;  // tiles per group: products of group k+1 overlap stores of k
+                static_assert(LT % G == 0, "LUT tile groups");
+                f32x4 hh[G], cr[G];
+                auto products = [&](int t0) {
 #pragma unroll
-            for (int k = 0; k < EPT; ++k) {
-                const int cc = cc0 + TPB * k;
-                if (cc < c.n_centroids) {
-                    const float4 c0 = cv[k][0], c1 = cv[k][1];
-                    float dot[R];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float d0 = qa[r].x * c0.x;
-                        d0 = fmaf(qa[r].y, c0.y, d0);
-                        d0 = fmaf(qa[r].z, c0.z, d0);
-                        d0 = fmaf(qa[r].w, c0.w, d0);
-                        d0 = fmaf(qb[r].x, c1.x, d0);
-                        d0 = fmaf(qb[r].y, c1.y, d0);
-                        d0 = fmaf(qb[r].z, c1.z, d0);
-                        d0 = fmaf(qb[r].w, c1.w, d0);
-                        dot[r] = d0 * kLog2e;
+                    for (int u = 0; u < G; ++u) {
+                        const f16x8 bh = __builtin_bit_cast(f16x8, cb_hi[t0 + u]);
+                        const f16x8 bl = __builtin_bit_cast(f16x8, cb_lo[t0 + u]);
+                        const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+                        hh[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bh, z, 0, 0, 0);
+                        cr[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_hi, bl, z, 0, 0, 0);
+                        if constexpr (decltype(q_split)::value)
+                            cr[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_lo, bh, cr[u], 0, 0, 0);
                     }
-                    lut4[lb * kLutStride + cc] = make_float4(dot[0], dot[1], dot[2], dot[3]);
+                };
+#pragma unroll
+                for (int t0 = 0; t0 < LT; t0 += G) {
+                    products(t0);
+#pragma unroll
+                    for (int u = 0; u < G; ++u) {
+                        const f32x4 e = hh[u] * mul + cr[u] * mul_lo;
+                        const int cc = ((wv * LT + t0 + u) % 16) * 16 + l16;
+                        if (cc < c.n_centroids)
+                            lut4[(bg * 4 + g) * kLutStride + cc] = make_float4(e.x, e.y, e.z, e.w);
+                    }
                 }
-            }
+            };
+            // fp16 queries have lo == 0
+            if (c.q_dtype == SS_F16)
+                build(std::false_type{});
+            else
+                build(std::true_type{});
         }
         compute_barrier(3);  // LUT complete
 
@@ -1008,7 +1058,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     __syncthreads();
     volatile lds_t<int> *last = cbar + 1;
     if (tid == 0)
-        *last = __hip_atomic_fetch_add(c.part_cnt + col, 1, __ATOMIC_RELAXED,
+        *last = __hip_atomic_fetch_add(c.part_cnt + (int64_t)col * c.cnt_stride, 1, __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT) == S - 1;
     __syncthreads();
     if (!*last) return;
@@ -1101,7 +1151,9 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         for (int k = 0; k < 4; ++k)
             store_from_f32(c.out, c.out_dtype, row_off(mr) + md0 + k, L > 0.f ? A[k] / L : 0.f);
     }
-    if (tid == 0) __hip_atomic_store(c.part_cnt + col, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0)
+        __hip_atomic_store(c.part_cnt + (int64_t)col * c.cnt_stride, 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -1215,7 +1267,7 @@ static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int
     return s;
 }
 
-// Workspace layout: [part_cnt: kCntBytes, one int per column]
+// Workspace layout: [part_cnt: kCntBytes, one int per column, spread out]
 //                   [part_ml: n_cols*S*R float2, padded to 256 B]
 //                   [part_acc: n_cols*S*R*D float]
 // The MFMA path counts finished splits per column in part_cnt and its last
@@ -1352,6 +1404,11 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.part_acc = nullptr;
     c.part_cnt = nullptr;
     c.fused_merge = s.S > 1 && (size_t)s.n_cols * sizeof(int) <= kCntBytes;
+    // columns' counters up to 4 KiB apart, so the splits of different
+    // columns never contend for one cache line
+    c.cnt_stride = 1024;
+    while (c.cnt_stride > 1 && (size_t)s.n_cols * c.cnt_stride * sizeof(int) > kCntBytes)
+        c.cnt_stride /= 2;
     if (s.S > 1) {
         const size_t need = decode_ws_bytes(s, head_dim);
         if (!ws || ws_bytes < need) {
@@ -1495,16 +1552,83 @@ extern "C" int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_h
     return SS_OK;
 }
 
+// Tiles of the prepared codebook: 16 centroids of 4 consecutive blocks.
+__host__ __device__ inline int cb_tiles(int n_blocks, int n_centroids) {
+    return (n_blocks / 4) * ((n_centroids + 15) / 16);
+}
+
+// One workgroup: max |C| over the codebook, then C' = C * 2^(kCbMaxExp - e)
+// (max |C| < 2^e) split into fp16 hi/lo, stored in the order the LUT build's
+// matrix-core operands are loaded: tile (bg, ct) of 4 blocks x 16 centroids
+// holds 64 lanes x 8 halves for hi, then the same for lo, where lane l
+// carries centroid ct*16 + l%16 of block bg*4 + l/16 (zero past the last
+// centroid).  The multiplier 2^(e - kCbMaxExp) that undoes the scale follows
+// as a float.
+__global__ void __launch_bounds__(1024) codebook_f16x2_kernel(const float *cents, int n_blocks,
+                                                              int n_centroids, _Float16 *out) {
+    __shared__ float red[1024 / kWave];
+    const int n = n_blocks * n_centroids * kBlockDim;
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < n; i += 1024) mx = fmaxf(mx, fabsf(cents[i]));
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < 1024 / kWave; ++w) mx = fmaxf(mx, red[w]);
+    int ex = 0;
+    frexpf(mx, &ex);  // mx < 2^ex
+    const int sh = kCbMaxExp - ex;
+    const int nct = (n_centroids + 15) / 16;
+    const int n_lanes = cb_tiles(n_blocks, n_centroids) * kWave;
+    for (int i = threadIdx.x; i < n_lanes * kBlockDim; i += 1024) {
+        const int j = i % kBlockDim, lane = (i / kBlockDim) % kWave, tile = i / (kBlockDim * kWave);
+        const int bg = tile / nct, ct = tile % nct;
+        const int b = bg * 4 + lane / 16, cc = ct * 16 + lane % 16;
+        const float v = cc < n_centroids
+                            ? ldexpf(cents[((int64_t)b * n_centroids + cc) * kBlockDim + j], sh)
+                            : 0.f;
+        const _Float16 hi = (_Float16)v;
+        _Float16 *o = out + (int64_t)tile * 2 * kWave * kBlockDim + lane * kBlockDim + j;
+        o[0] = hi;
+        o[kWave * kBlockDim] = (_Float16)((v - (float)hi) * kSplitScale);
+    }
+    if (threadIdx.x == 0)
+        *reinterpret_cast<float *>(out + (int64_t)n_lanes * 2 * kBlockDim) = ldexpf(1.f, -sh);
+}
+
+extern "C" size_t ss_codebook_f16x2_bytes(int n_blocks, int n_centroids) {
+    if (n_blocks < 4 || n_blocks % 4 || n_centroids < 1) return 0;
+    return (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16 + 16;
+}
+
+extern "C" int ss_codebook_f16x2(const float *centroids, int n_blocks, int n_centroids,
+                                 void *out, void *stream) {
+    SS_REQUIRE(centroids && out, "null centroids/out");
+    SS_REQUIRE(n_blocks >= 4 && n_blocks <= 64 && n_blocks % 4 == 0 && n_centroids >= 1 &&
+                   n_centroids <= kLutStride,
+               "bad codebook shape (%d blocks, %d centroids)", n_blocks, n_centroids);
+    SS_REQUIRE(((uintptr_t)out % 16) == 0, "prepared codebook must be 16-byte aligned");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(codebook_f16x2_kernel, dim3(1), dim3(1024), 0, st, centroids, n_blocks,
+                       n_centroids, static_cast<_Float16 *>(out));
+    SS_LAUNCH_CHECK("codebook_f16x2_kernel launch");
+    return SS_OK;
+}
+
 extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                                   int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                  const int32_t *perm, const float *centroids, int n_blocks,
+                                  const int32_t *perm, const void *codebook, int n_blocks,
                                   int n_centroids, const uint8_t *idx, const void *values_il8,
                                   int v_dtype, int64_t cap, int64_t t_kv, int causal,
                                   int64_t q_offset, void *out, int out_dtype, void *workspace,
                                   size_t workspace_bytes, int n_splits, void *stream) {
-    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+    const float *cents = static_cast<const float *>(codebook);
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
     if (rc) return rc;
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
     SS_REQUIRE(values_il8, "null values");
     SS_UNSUPPORTED(v_dtype == SS_F16, "interleaved values must be float16");
     SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8 for interleaved values");
@@ -1512,10 +1636,14 @@ extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int
     const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
                                        kKindMfma);
     DecodeCommon c;
-    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents,
                      n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
                      workspace_bytes, head_dim);
     if (rc) return rc;
+    c.centroids = nullptr;
+    c.codebook = static_cast<const uint4 *>(codebook);
+    c.codebook_mul = reinterpret_cast<const float *>(
+        static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const __half *v8 = reinterpret_cast<const __half *>(values_il8);
     if (head_dim == 128) return launch_mfma<128>(c, v8, s, st);

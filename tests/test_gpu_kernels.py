@@ -327,6 +327,50 @@ def test_decode_il8_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, cap
     assert rel_err(got, ref) <= REL_TOL
 
 
+def test_codebook_f16x2_reconstructs_the_centroids():
+    """hi + lo * 2^-11, times the stored power of two, gives back every
+    centroid to about 2^-22 of the codebook's largest magnitude, for codebooks
+    far outside the fp16 range, tiny ones and an all-zero one."""
+    rng = np.random.default_rng(5)
+    for mag, nc in ((1.0, 256), (3e6, 40), (2e-7, 16), (0.0, 8)):
+        c = (rng.standard_normal((16, nc, 8)) * mag).astype(np.float32)
+        c[0, 0, 0] = 0.0
+        buf = _hip.codebook_f16x2(t(c))
+        torch.cuda.synchronize()
+        raw = buf.cpu().numpy()
+        nct = (nc + 15) // 16
+        body = 4 * nct * 2048
+        assert raw.size == body + 16
+        # tile (bg, ct), part (hi, lo), lane l: centroid ct*16 + l%16 of block bg*4 + l/16
+        hl = raw[:body].view(np.float16).reshape(4, nct, 2, 4, 16, 8).astype(np.float64)
+        mul = float(raw[body:body + 4].view(np.float32)[0])
+        assert mul > 0 and np.log2(mul) == np.round(np.log2(mul))  # a power of two
+        assert np.isfinite(hl).all() and np.abs(hl[:, :, 0]).max() <= 2.0 ** 14
+        full = (hl[:, :, 0] + hl[:, :, 1] / 2048.0) * mul          # (bg, ct, bs, n, 8)
+        full = full.transpose(0, 2, 1, 3, 4).reshape(16, nct * 16, 8)
+        back = full[:, :nc]
+        assert not full[:, nc:].any()  # padding lanes are zero
+        tol = max(np.abs(c).max(), 1e-30) * 2.0 ** -21
+        assert np.abs(back - c).max() <= tol
+
+
+@pytest.mark.parametrize("q_dtype,nc,d", [(np.float32, 256, 128), (np.float32, 40, 64),
+                                          (np.float16, 40, 128), (np.float16, 8, 64)])
+def test_decode_il8_query_dtypes_and_small_codebooks(q_dtype, nc, d):
+    """fp32 queries take the split query operand of the matrix-core LUT
+    build; codebooks with fewer than 16 centroids or a partial last tile of 16
+    leave part of the LUT tiles unused."""
+    cents, perm, idx, vals, q = decode_case(900 + nc, 1, 8, 2, d, 1500, cap=1504, nc=nc)
+    q = (q.astype(np.float32) * 1.7).astype(q_dtype)
+    if q_dtype == np.float32:
+        q += np.float32(1e-4) * np.random.default_rng(3).standard_normal(q.shape).astype(np.float32)
+    out = _hip.decode_attn_il8(t(q), 0.125, t(perm), t(cents), t(idx), to_il8(vals, 1504), 1500,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.sdpa(q, idx[:, :, :1500], vals[:, :, :1500], cents, perm, 0.125)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
 def test_decode_il8_peaked_and_flat_softmax():
     """Probabilities spanning many orders of magnitude (the hi/lo fp16 split
     must keep small ones) and an almost flat softmax."""
