@@ -198,7 +198,7 @@ struct IdxRow {
         }
     }
     __device__ __forceinline__ uint32_t at(int b) const {
-        return (w[b >> 2] >> ((b & 3) * 8)) & 0xffu;
+        return __builtin_amdgcn_ubfe(w[b >> 2], (b & 3) * 8, 8);
     }
 };
 
@@ -892,31 +892,29 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 lim_rel[r] = (int)max(min(lim[r] - t0, (int64_t)kWave), (int64_t)-1);
-            // scores from the LUT, four blocks per group of reads (bounds the
-            // registers that reads in flight hold next to the tile)
-            float s[R] = {0.f, 0.f, 0.f, 0.f};
+            // scores from the LUT: every block's read in flight at once, then
+            // a tree sum (one LDS round trip)
+            f32x4 e[NB];
 #pragma unroll
-            for (int b0 = 0; b0 < NB; b0 += 4) {
+            for (int b = 0; b < NB; ++b) e[b] = lut_l[b * kLutStride + ir.at(b)];
 #pragma unroll
-                for (int b = b0; b < b0 + 4; ++b) {
-                    const f32x4 e = lut_l[b * kLutStride + ir.at(b)];
-                    s[0] += e.x;
-                    s[1] += e.y;
-                    s[2] += e.z;
-                    s[3] += e.w;
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            for (int w = 1; w < NB; w *= 2)
+#pragma unroll
+                for (int b = 0; b < NB; b += 2 * w) e[b] += e[b + w];
+            // masked lanes add -inf (their index rows are real, clamped
+            // tokens, so the sums are finite); an additive mask keeps the LUT
+            // sums unconditional
+            float sc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) sc[r] = e[0][r] + ((kok && lane <= lim_rel[r]) ? 0.f : -INFINITY);
+            float tmax[R];
+            wave_max4_dpp(sc, tmax);  // the four rows' reductions interleaved
             float corr[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                // masked lanes add -inf (their index rows are real, clamped
-                // tokens, so s[r] is finite); an additive mask keeps the LUT
-                // sums unconditional
-                const float sc = s[r] + ((kok && lane <= lim_rel[r]) ? 0.f : -INFINITY);
-                const float mn = fmaxf(m[r], wave_max_dpp(sc));
+                const float mn = fmaxf(m[r], tmax[r]);
                 corr[r] = fast_exp2(m[r] - mn);
-                const float p = fast_exp2(sc - mn);
+                const float p = fast_exp2(sc[r] - mn);
                 lsum[r] = fmaf(lsum[r], corr[r], p);
                 m[r] = mn;
                 const float x = p * kPScale;
@@ -926,12 +924,12 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 pw[(r + 4) * kWave + lane] = lo;
             }
             wave_lds_sync();
+            // rescale only when some row's running max moved (wave-uniform;
+            // after the first tiles it rarely does)
+            if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
+                const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                acc[n][0] *= corr[0];
-                acc[n][1] *= corr[1];
-                acc[n][2] *= corr[2];
-                acc[n][3] *= corr[3];
+                for (int n = 0; n < NT; ++n) acc[n] *= cv4;
             }
             if (n_in < kWave) {  // last, partial tile: zero tokens >= t_end
 #pragma unroll

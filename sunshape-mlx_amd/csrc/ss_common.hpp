@@ -87,21 +87,59 @@ __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(x, x, CTRL, ROW_MASK, 0xf, false));
 }
 
+// Order-preserving map of a float onto a signed int (negative values have
+// their magnitude bits flipped), so a float max can run as an integer max,
+// which fuses with the DPP lane move (no NaN canonicalisation; NaN never
+// occurs in the values reduced here).
+__device__ __forceinline__ int ord_key(float f) {
+    const int i = __float_as_int(f);
+    return i ^ ((i >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float ord_float(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7fffffff)); }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
+}
+
 __device__ __forceinline__ float wave_max_dpp(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));         // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_mov<0x4E>(v));         // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_mov<0x141>(v));        // row_half_mirror
-    v = fmaxf(v, dpp_mov<0x140>(v));        // row_mirror
-    v = fmaxf(v, dpp_mov<0x142, 0xa>(v));   // row_bcast:15 into rows 1, 3
-    v = fmaxf(v, dpp_mov<0x143, 0xc>(v));   // row_bcast:31 into rows 2, 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    int k = ord_key(v);
+    k = max(k, dpp_mov_i<0xB1>(k));   // quad_perm [1,0,3,2]
+    k = max(k, dpp_mov_i<0x4E>(k));   // quad_perm [2,3,0,1]
+    k = max(k, dpp_mov_i<0x141>(k));  // row_half_mirror
+    k = max(k, dpp_mov_i<0x140>(k));  // row_mirror
+    k = max(k, __builtin_amdgcn_update_dpp(k, k, 0x142, 0xa, 0xf, false));  // row_bcast:15 -> rows 1, 3
+    k = max(k, __builtin_amdgcn_update_dpp(k, k, 0x143, 0xc, 0xf, false));  // row_bcast:31 -> rows 2, 3
+    return ord_float(__builtin_amdgcn_readlane(k, 63));
+}
+
+// Four independent wave maxima, their butterfly steps interleaved so the
+// DPP read-after-write waits of one chain are filled by the others.
+__device__ __forceinline__ void wave_max4_dpp(const float (&v)[4], float (&out)[4]) {
+    int k[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = ord_key(v[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], dpp_mov_i<0xB1>(k[i]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], dpp_mov_i<0x4E>(k[i]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], dpp_mov_i<0x141>(k[i]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], dpp_mov_i<0x140>(k[i]));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], __builtin_amdgcn_update_dpp(k[i], k[i], 0x142, 0xa, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = max(k[i], __builtin_amdgcn_update_dpp(k[i], k[i], 0x143, 0xc, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = ord_float(__builtin_amdgcn_readlane(k[i], 63));
 }
 
 __device__ __forceinline__ float wave_sum_dpp(float v) {
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    v += dpp_mov<0x140>(v);
+    v += __int_as_float(dpp_mov_i<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov_i<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov_i<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_mov_i<0x140>(__float_as_int(v)));
     // rows 1 and 3 add the total of the row before them; lanes of rows 0, 2
     // must not change, so they add 0
     {
