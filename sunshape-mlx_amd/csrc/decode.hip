@@ -969,8 +969,12 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     float *wa = wl + NC * R;  // [NC][2][R][D]
     static_assert((2 * NC * R) % 4 == 0, "wa alignment");
     if (!loader) {
+        {
+            float ls[R];
+            wave_sum4_dpp(lsum, ls);
 #pragma unroll
-        for (int r = 0; r < R; ++r) lsum[r] = wave_sum_dpp(lsum[r]);
+            for (int r = 0; r < R; ++r) lsum[r] = ls[r];
+        }
         if (lane == 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {

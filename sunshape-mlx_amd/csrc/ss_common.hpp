@@ -135,6 +135,31 @@ __device__ __forceinline__ void wave_max4_dpp(const float (&v)[4], float (&out)[
     for (int i = 0; i < 4; ++i) out[i] = ord_float(__builtin_amdgcn_readlane(k[i], 63));
 }
 
+// Four independent wave sums, steps interleaved (lane moves fused into the
+// adds where the whole row is written).
+__device__ __forceinline__ void wave_sum4_dpp(const float (&v)[4], float (&out)[4]) {
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = v[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] += __int_as_float(dpp_mov_i<0xB1>(__float_as_int(a[i])));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] += __int_as_float(dpp_mov_i<0x4E>(__float_as_int(a[i])));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] += __int_as_float(dpp_mov_i<0x141>(__float_as_int(a[i])));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] += __int_as_float(dpp_mov_i<0x140>(__float_as_int(a[i])));
+    // rows 1 and 3 add the total of the row before them, rows 0 and 2 add 0
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a[i] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[i]), 0x142, 0xa, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a[i] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[i]), 0x143, 0xc, 0xf, false));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[i]), 63));
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += __int_as_float(dpp_mov_i<0xB1>(__float_as_int(v)));
     v += __int_as_float(dpp_mov_i<0x4E>(__float_as_int(v)));
