@@ -140,20 +140,24 @@ def run_hybrid(args) -> int:
     sc0 = torch.empty((b, hkv, t_kv, ng), dtype=torch.float16, device=dev)
     ze0 = torch.empty((b, hkv, t_kv, ng), dtype=torch.float16, device=dev)
     hip.quantize_values_grouped(v, bits, group, packed0, sc0, ze0)
+    # the cache's code layout: token-interleaved (16 tokens of one dim per word)
+    il0 = torch.empty((b, hkv, t_kv * bits // 32, d), dtype=torch.int32, device=dev)
+    hip.pack_grouped_il(packed0, bits, il0, 0)
     q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
     del v
-    per_copy = idx0.numel() + packed0.numel() * 4 + (sc0.numel() + ze0.numel()) * 2
+    per_copy = idx0.numel() + il0.numel() * 4 + (sc0.numel() + ze0.numel()) * 2
     n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
-    bufs = [(idx0, packed0, sc0, ze0)] + [tuple(t.clone() for t in (idx0, packed0, sc0, ze0))
-                                          for _ in range(n_copies - 1)]
+    bufs = [(idx0, il0, sc0, ze0)] + [tuple(t.clone() for t in (idx0, il0, sc0, ze0))
+                                      for _ in range(n_copies - 1)]
     torch.cuda.synchronize()
     log(f"hybrid cache ready: {n_copies} copies x {per_copy / 1e6:.1f} MB")
-    splits, ws_bytes = hip.decode_plan(hip.KIND_DENSE, b, hq, hkv, 1, d, t_kv, args.splits)
+    splits, ws_bytes = hip.decode_plan(hip.KIND_IL8, b, hq, hkv, 1, d, t_kv, args.splits)
     ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
-    fn = lib.ss_decode_attn_grouped
-    argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cents.data_ptr(),
+    fn = lib.ss_decode_attn_grouped_il
+    cb = hip.codebook_f16x2(cents)
+    argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cb.data_ptr(),
              nb, 256, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), t[3].data_ptr(), hip.SS_F16,
              bits, group, t_kv, t_kv, 0, 0, out.data_ptr(), hip.SS_F16, ws.data_ptr(), ws_bytes,
              splits, stream) for t in bufs]
@@ -185,7 +189,8 @@ def run_hybrid(args) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": "decode B=8 Hq=32 Hkv=8 D=128 T_kv=32768, u8 key indices, 2-bit "
-                               "grouped values g=64 with fp16 scale/zero, fp16 query/output",
+                               "grouped values g=64 with fp16 scale/zero (codes token-interleaved), "
+                               "fp16 query/output",
                    "t_kv": t_kv, "splits": splits, "cache_copies": n_copies,
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,

@@ -94,9 +94,10 @@ int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centro
  * count (n_splits <= 0 selects the library's choice for the current device);
  * 0 when a single split suffices.  With more than one split the split
  * workgroups write per-split softmax partials (m, l, acc) to the workspace.
- * ss_decode_attn_il8 merges them inside its kernel (the last split of each
- * column to finish, counted in the workspace's first 64 KiB); the other
- * entry points merge with a second launch on the stream.  A workspace must be
+ * ss_decode_attn_il8 and ss_decode_attn_grouped_il merge them inside their
+ * kernel (the last split of each column to finish, counted in the
+ * workspace's first 64 KiB); the other entry points merge with a second
+ * launch on the stream.  A workspace must be
  * zero-filled once before its first use; every completed call leaves its
  * counter area zero again.
  */
@@ -134,7 +135,7 @@ int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_head
 /*
  * Split count and workspace bytes a decode call of the given kind would use
  * (kind 0: ss_decode_attn_dense / ss_decode_attn_grouped, kind 1:
- * ss_decode_attn_il8).  Either output pointer may be NULL.
+ * ss_decode_attn_il8 / ss_decode_attn_grouped_il).  Either output pointer may be NULL.
  */
 int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
                    int head_dim, int64_t t_kv, int n_splits, int *splits_out,
@@ -208,6 +209,40 @@ int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_he
                            int causal, int64_t q_offset, void *out, int out_dtype,
                            void *workspace, size_t workspace_bytes, int n_splits,
                            void *stream);
+
+/*
+ * As ss_decode_attn_grouped with the 2- or 4-bit codes held in a token-
+ * interleaved layout and the codebook prepared by ss_codebook_f16x2.  Code of
+ * token t, dimension d of a (batch, KV head) row is bits
+ * [bits*(t%tpw), bits*(t%tpw+1)) of
+ * codes_il[((b*n_kv_heads + h)*cap/tpw + t/tpw)*head_dim + d], tpw = 32/bits;
+ * scales/zeros keep ss_decode_attn_grouped's [batch][n_kv_heads][cap][n_groups]
+ * layout.  group_size must be head_dim or head_dim/2, cap % 16 == 0, all
+ * operands 16-byte aligned.  The LUT and P.V run on the matrix cores (P.V in
+ * bf16 on the codes with p*scale split into bf16 hi/lo parts, the zero term
+ * added exactly in fp32).  Replaces fused_attention_dequant_metal /
+ * _causal_metal (reference kernels.py:697-765, 870-928).
+ */
+int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                              int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                              const int32_t *perm, const void *codebook, int n_blocks,
+                              int n_centroids, const uint8_t *idx, const uint32_t *codes_il,
+                              const void *scales, const void *zeros, int sz_dtype, int bits,
+                              int group_size, int64_t cap, int64_t t_kv, int causal,
+                              int64_t q_offset, void *out, int out_dtype, void *workspace,
+                              size_t workspace_bytes, int n_splits, void *stream);
+
+/*
+ * Repack grouped codes (pack_indices words, one row of packed_dim words per
+ * token: word w of token (b,h,t) at packed[b*p_sb + h*p_sh + t*p_st + w]) into
+ * the interleaved layout of ss_decode_attn_grouped_il at cache positions
+ * offset .. offset+n_t-1 of out_il [n_b][n_h][cap/tpw][head_dim]; other
+ * tokens sharing a word keep their codes.  Replaces the value-code half of
+ * the hybrid cache flush (reference cache.py:581-596).
+ */
+int ss_pack_grouped_il(const uint32_t *packed, int64_t n_b, int64_t n_h, int64_t n_t,
+                       int64_t p_sb, int64_t p_sh, int64_t p_st, int head_dim, int bits,
+                       uint32_t *out_il, int64_t cap, int64_t offset, void *stream);
 
 /*
  * Grouped asymmetric min-max quantisation of values (encode-on-append).

@@ -78,6 +78,12 @@ _SIGNATURES = {
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
                                       _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_attn_grouped_il": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                         _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
+                                         _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
+                                         _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
+                                  _c_void_p, _i64, _i64, _c_void_p]),
     "ss_quantize_values_grouped": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _int, _int, _int, _c_void_p, _c_void_p, _c_void_p, _int,
                                           _i64, _i64, _i64, _c_void_p]),
@@ -424,6 +430,83 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
         dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
         stream_handle(q.device)))
     return out
+
+
+def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                           centroids: torch.Tensor, idx: torch.Tensor, codes_il: torch.Tensor,
+                           scales: torch.Tensor, zeros: torch.Tensor, bits: int, group_size: int,
+                           t_kv: int, causal: bool = False, q_offset: int = 0,
+                           out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                           n_splits: int = 0, codebook: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused decode (matrix-core LUT and P.V) over grouped values whose codes
+    are token-interleaved: ``codes_il`` (B, Hkv, cap * bits / 32, D) 32-bit
+    words (see :func:`pack_grouped_il`), ``scales``/``zeros`` (B, Hkv, cap, D
+    / group_size).  ``codebook`` is :func:`codebook_f16x2` of ``centroids``
+    (prepared here when None)."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(codes_il, scales, zeros)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    tpw = 32 // bits if bits in (2, 4) else 0
+    if not tpw or codes_il.dim() != 4 or not codes_il.is_contiguous() or \
+            tuple(codes_il.shape) != (b_, hkv, cap // tpw, d) or \
+            codes_il.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"codes_il must be contiguous 32-bit words {(b_, hkv, cap // max(tpw, 1), d)}")
+    for name, t in (("scales", scales), ("zeros", zeros)):
+        if t.dim() != 4 or not t.is_contiguous() or t.shape[:3] != idx.shape[:3]:
+            raise ValueError(f"{name} must be a contiguous (B, n_kv_heads, cap, n_groups) buffer")
+    if scales.dtype != zeros.dtype or scales.dtype not in (torch.float32, torch.float16):
+        raise ValueError("scales/zeros must share dtype float32 or float16")
+    if codebook is None:
+        codebook = codebook_f16x2(centroids)
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
+    ws = decode_workspace(q.device, ws_bytes)
+    check(load_library().ss_decode_attn_grouped_il(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+        nb, nc, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros), dtype_code(scales.dtype),
+        int(bits), int(group_size), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
+        dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
+        stream_handle(q.device)))
+    return out
+
+
+def pack_grouped_il(packed: torch.Tensor, bits: int, codes_il: torch.Tensor, offset: int) -> None:
+    """Write the codes of reference-layout packed rows (B, H, T, D*bits/32)
+    at cache positions [offset, offset + T) of the token-interleaved buffer
+    (B, H, cap*bits/32, D); codes of other tokens sharing a word are kept."""
+    require_gpu(packed, codes_il)
+    if packed.dim() != 4 or packed.stride(-1) != 1:
+        raise ValueError("packed must be (B, H, T, words) with unit last stride")
+    if codes_il.dim() != 4 or not codes_il.is_contiguous():
+        raise ValueError("codes_il must be a contiguous (B, H, cap*bits/32, D) buffer")
+    b_, h_, t_, nw = packed.shape
+    d = codes_il.shape[3]
+    cap = codes_il.shape[2] * (32 // bits)
+    if tuple(codes_il.shape[:2]) != (b_, h_) or nw * (32 // bits) != d:
+        raise ValueError("packed rows and interleaved buffer shapes differ")
+    check(load_library().ss_pack_grouped_il(
+        ptr(packed), b_, h_, t_, packed.stride(0) // nw, packed.stride(1) // nw,
+        packed.stride(2) // nw, d, int(bits), ptr(codes_il), cap, int(offset),
+        stream_handle(packed.device)))
+
+
+def grouped_il_to_packed(codes_il: torch.Tensor, bits: int, t: int | None = None) -> torch.Tensor:
+    """(B, H, cap*bits/32, D) token-interleaved codes -> reference-layout
+    packed rows (B, H, cap, D*bits/32) uint32 (first ``t`` tokens)."""
+    b_, h_, nblk, d = codes_il.shape
+    tpw = 32 // bits
+    w = codes_il.view(torch.int32).to(torch.int64) & 0xffffffff
+    shifts = torch.arange(tpw, device=w.device, dtype=torch.int64) * bits
+    codes = (w.unsqueeze(3) >> shifts.view(1, 1, 1, tpw, 1)) & ((1 << bits) - 1)  # (B,H,blk,tpw,D)
+    codes = codes.reshape(b_, h_, nblk * tpw, d)
+    if t is not None:
+        codes = codes[:, :, :t]
+    words = (codes.reshape(b_, h_, codes.shape[2], d // tpw, tpw) << shifts).sum(-1)
+    return words.to(torch.int64).to(torch.int32).view(torch.uint32) if hasattr(torch, "uint32") \
+        else words.to(torch.int32)
 
 
 def quantize_values_grouped(values: torch.Tensor, bits: int, group_size: int,

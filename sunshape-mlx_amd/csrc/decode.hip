@@ -520,24 +520,25 @@ __device__ __forceinline__ void wait_oldest_tile(int k) {
     }
 }
 
-template <int D, int NC>
+template <int D, int NC, class VF>
 struct WsCfg {
     static constexpr int kNB = D / kBlockDim;
-    static constexpr int kTileV = kWave * D * 2;  // fp16 values of a 64-token tile
+    static constexpr int kTileV = VF::kTileV;     // value bytes of a 64-token tile
     static constexpr int kTileI = kWave * kNB;    // uint8 index rows of the tile
     static constexpr int kSlot = kTileV + kTileI;
     static constexpr int kLut = kNB * kLutStride * 16;  // float4 per (block, centroid)
-    static constexpr int kPst = NC * 8 * kWave * 2;     // P staging, fp16 [8][64] per wave
+    static constexpr int kPst = NC * VF::kPRows * kWave * 2;  // P staging, 16-bit [rows][64] per wave
     static constexpr int kFlagWords = 16;
     static constexpr int kFlags = (2 * kFlagWords + 4) * 4;  // ready[], done[], barrier counter
     static constexpr int kRing = kLut + kPst + kFlags;
     static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
-    static constexpr int kSlots = kSlotsFit < 8 ? kSlotsFit : 8;
-    static constexpr int kLoadsPerTile = kTileV / 1024 + 1;
+    static constexpr int kSlots = kSlotsFit < VF::kMaxSlots ? kSlotsFit : VF::kMaxSlots;
+    static constexpr int kLoadsPerTile = VF::kLoadsV + 1;
     static constexpr int kDepthVm = 63 / kLoadsPerTile + 1;
     static constexpr int kDepth = kSlots < kDepthVm ? kSlots : kDepthVm;
     static constexpr int kLds = kRing + kSlots * kSlot;
     static_assert(kSlots >= 2 && kSlots <= kFlagWords, "ring slots");
+    static_assert(kTileV % 16 == 0, "16-byte tile sections");
     static_assert(kLds <= kLdsMax, "LDS budget");
     static_assert(NC * kMfmaRows * (2 * D + 2) * 4 <= kSlots * kSlot, "merge scratch");
     static_assert(2 * kMfmaRows * D * 4 <= kPst, "query staging");
@@ -560,10 +561,312 @@ __device__ __forceinline__ uint4 mask_tokens(uint4 u, int n_ok) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-template <int D, int NC>
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Value formats of the matrix-core decode kernel.  A format supplies the value
+// bytes of a 64-token tile and their copies into the LDS ring (the loader),
+// its tile data in registers (each compute lane holds token `lane` for P and
+// the B operands of P.V), the P.V step for a tile given this lane's
+// probabilities, and the hand-off of the accumulators to the workgroup
+// combine as (hi, lo) parts per row and dim.  Accumulator lane layout (every
+// format): acc[n] of lane l holds MFMA rows 4*(l/16) .. +3 of dims 16n + l%16.
+
+// fp16 values, 8-token interleaved: element (t, d) at [t/8][d][t%8].  P is
+// staged as fp16 hi/lo rows of p * 2^15 (A rows 0-3 hi, 4-7 lo, 8-15 zero)
+// and P.V is v_mfma_f32_16x16x16f16.
+template <int D>
+struct VIl8 {
+    struct Args {
+        const __half *v8;
+    };
+    static constexpr int NT = D / 16;
+    static constexpr int kTileV = kWave * D * 2;
+    static constexpr int kLoadsV = kTileV / 1024;
+    static constexpr int kPRows = 8;
+    static constexpr int kMaxSlots = 8;
+    static constexpr int kComputeWaves = 4;  // one per SIMD: 272-byte tokens keep them busy
+    struct Tile {
+        uint4 v[2][NT];
+    };
+    struct State {};
+    // values of tokens t0 .. t0+63; 8-token blocks past the split's last
+    // token are clamped to that block, so every copy stays in bounds
+    __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+                                 uint32_t sb, int lane) {
+        const char *vhead = reinterpret_cast<const char *>(a.v8 + bh * cap * D);
+        const int64_t b0 = t0 / 8, blk_last = t_last / 8;
+#pragma unroll
+        for (int i = 0; i < kLoadsV; ++i) {
+            const int q = i * kWave + lane;  // 16-byte chunk of the tile
+            const int64_t blk = min(b0 + q / D, blk_last);
+            __builtin_amdgcn_global_load_lds(vhead + (blk * D + q % D) * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                             kCpolNt);
+        }
+    }
+    __device__ static void copy(Tile &tv, const char *sb, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                tv.v[s2][n] = *reinterpret_cast<const uint4 *>(sb + ((4 * s2 + g) * D + 16 * n + l16) * 16);
+    }
+    __device__ static void init(State &) {}
+    __device__ static void pv(Tile &tv, State &, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
+                              const float (&corr)[kMfmaRows], int n_in, _Float16 *pw, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; ++r) {
+            const float x = p[r] * kPScale;
+            const _Float16 hi = (_Float16)x;
+            const _Float16 lo = (_Float16)(x - (float)hi);
+            pw[r * kWave + lane] = hi;
+            pw[(r + 4) * kWave + lane] = lo;
+        }
+        wave_lds_sync();
+        // rescale only when some row's running max moved (wave-uniform;
+        // after the first tiles it rarely does)
+        if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
+            const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= cv4;
+        }
+        if (n_in < kWave) {  // last, partial tile: zero tokens >= t_end
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int n_ok = min(max(n_in - 8 * (4 * s2 + g), 0), 8);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) tv.v[s2][n] = mask_tokens(tv.v[s2][n], n_ok);
+            }
+        }
+        const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                f16x4 a = f16x4{0, 0, 0, 0};
+                if (a_live)
+                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * jj);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const uint4 u = tv.v[s2][n];
+                    uint2 h = jj == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
+                    const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
+                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
+                }
+            }
+        }
+        wave_lds_sync();
+    }
+    // lanes 0-15 hold rows 0-3 (hi parts) of dims 16n + l16, lanes 16-31 the
+    // lo parts: wa[hl][r][d] = acc / 2^15
+    __device__ static void to_lds(const f32x4 (&acc)[NT], const State &, float *wa, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        if (g < 2) {
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r)
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
+        }
+    }
+};
+
+// Float32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits_rn(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Grouped asymmetric values (bits 2 or 4, NG = 1 or 2 groups per row, scale
+// and zero of type SZT): v = code * s + z.  Codes are token-interleaved: per
+// (b, h), u32 word (blk, d) of [cap / TPW][D] holds dim d of tokens blk*TPW ..
+// +TPW-1 (token i at bits [BITS*i, BITS*(i+1))); scales/zeros [cap][NG].
+// P.V = sum_t (p_t s_t) code_t + sum_t p_t z_t.  The first sum runs on the
+// matrix cores (v_mfma_f32_16x16x32_bf16): A rows are w = p * s of each
+// (group, row) split into bf16 hi/lo (rows 8g+0..3 hi, 8g+4..7 lo of group
+// g), B the codes of 8 tokens of one dim as bf16 128 + code (bit pattern
+// 0x4300 | code, exact), so the products carry 128 * sum_t w_t, which is
+// subtracted at the end from the exact fp32 sum of the same hi + lo parts.
+// The second sum accumulates per (row, group) in fp32 on the lanes.
+template <int D, int BITS, int NG, class SZT>
+struct VGil {
+    struct Args {
+        const uint32_t *codes;
+        const SZT *scales, *zeros;
+    };
+    static constexpr int NT = D / 16;
+    static constexpr int TPW = 32 / BITS;                 // tokens per code word
+    static constexpr int kCodeBytes = kWave * D * BITS / 8;
+    static constexpr int kSzBytes = kWave * NG * (int)sizeof(SZT);
+    static constexpr int kTileV = kCodeBytes + 2 * kSzBytes;
+    static constexpr int kLoadsV = kCodeBytes / 1024 + 2;
+    static constexpr int kPRows = 16;
+    static constexpr int kMaxSlots = 16;
+    // a tile is 5x fewer bytes than fp16 values: two or three compute waves
+    // per SIMD overlap the per-tile latency chain
+    static constexpr int kComputeWaves = 8;
+    static constexpr int kGroup = D / NG;
+    static_assert(BITS == 2 || BITS == 4, "bits");
+    static_assert(NG == 1 || NG == 2, "groups per row");
+    static_assert(kCodeBytes % 1024 == 0 && kSzBytes % 16 == 0 && kSzBytes <= 1024, "tile sections");
+    struct Tile {
+        uint32_t cw[2][NT];  // codes of tokens 32*ks + 8*(lane/16) .. +7, dim 16n + lane%16
+        float s[NG], z[NG];  // scale / zero of token `lane`
+    };
+    struct State {
+        float ws[kMfmaRows][NG];  // sum of w = hi + lo over this lane's tokens
+        float zs[kMfmaRows][NG];  // sum of p * z
+    };
+    __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+                                 uint32_t sb, int lane) {
+        // codes: the tile's words are contiguous; 16-byte chunks (4 words of
+        // one block) past the split's last block clamp to that block
+        const char *chead = reinterpret_cast<const char *>(a.codes + bh * (cap / TPW) * D);
+        const int64_t wb0 = t0 / TPW, blk_last = t_last / TPW;
+#pragma unroll
+        for (int i = 0; i < kCodeBytes / 1024; ++i) {
+            const int w = (i * kWave + lane) * 4;  // first word of the chunk
+            const int64_t blk = min(wb0 + w / D, blk_last);
+            __builtin_amdgcn_global_load_lds(chead + (blk * D + w % D) * 4,
+                                             reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                             kCpolNt);
+        }
+        // scales, zeros: chunks past the one holding the last token clamp to it
+        constexpr int kTokPerChunk = 16 / (NG * (int)sizeof(SZT));
+        const int64_t ch_last = (t_last - t0) / kTokPerChunk;
+        const int64_t ch = min((int64_t)lane, ch_last);
+        if (lane < kSzBytes / 16) {
+            const char *sp = reinterpret_cast<const char *>(a.scales + (bh * cap + t0) * NG);
+            const char *zp = reinterpret_cast<const char *>(a.zeros + (bh * cap + t0) * NG);
+            __builtin_amdgcn_global_load_lds(sp + ch * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + kCodeBytes), 16, 0,
+                                             kCpolNt);
+            __builtin_amdgcn_global_load_lds(zp + ch * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + kSzBytes),
+                                             16, 0, kCpolNt);
+        }
+    }
+    __device__ static void copy(Tile &tv, const char *sb, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        const uint32_t *cw = reinterpret_cast<const uint32_t *>(sb);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int tk = 32 * ks + 8 * g;  // first of the lane's 8 tokens
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const uint32_t w = cw[(tk / TPW) * D + 16 * n + l16];
+                tv.cw[ks][n] = BITS == 2 ? (w >> (2 * (tk % TPW))) & 0xffffu : w;
+            }
+        }
+        const SZT *sp = reinterpret_cast<const SZT *>(sb + kCodeBytes);
+        const SZT *zp = reinterpret_cast<const SZT *>(sb + kCodeBytes + kSzBytes);
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            tv.s[k] = (float)sp[lane * NG + k];
+            tv.z[k] = (float)zp[lane * NG + k];
+        }
+    }
+    __device__ static void init(State &st) {
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; ++r)
+#pragma unroll
+            for (int k = 0; k < NG; ++k) st.ws[r][k] = st.zs[r][k] = 0.f;
+    }
+    // codes of 8 tokens -> bf16 128 + code, tokens in element order
+    __device__ static bf16x8 expand(uint32_t x) {
+        uint32_t d[4];
+        if constexpr (BITS == 2) {  // code i at bits 2i of the low 16 bits
+            const uint32_t y1 = x >> 2, y2 = x >> 4, y3 = x >> 6;
+            d[0] = __builtin_amdgcn_perm(y1, x, 0x0c040c00u);
+            d[1] = __builtin_amdgcn_perm(y3, y2, 0x0c040c00u);
+            d[2] = __builtin_amdgcn_perm(y1, x, 0x0c050c01u);
+            d[3] = __builtin_amdgcn_perm(y3, y2, 0x0c050c01u);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d[j] = (d[j] & 0x00030003u) | 0x43004300u;
+        } else {  // code i at bits 4i
+            const uint32_t y1 = x >> 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                d[j] = (__builtin_amdgcn_perm(y1, x, 0x0c040c00u | (uint32_t)(j << 16) | (uint32_t)j) &
+                        0x000f000fu) | 0x43004300u;
+        }
+        return __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
+    }
+    __device__ static void pv(Tile &tv, State &st, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
+                              const float (&corr)[kMfmaRows], int n_in, _Float16 *pw16, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        uint16_t *pw = reinterpret_cast<uint16_t *>(pw16);
+        // tokens past the split end carry p = 0 but possibly unwritten s, z
+        const bool ok = lane < n_in;
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; ++r) {
+#pragma unroll
+            for (int k = 0; k < NG; ++k) {
+                const float w = ok ? p[r] * tv.s[k] : 0.f;
+                const uint32_t hb = bf16_bits_rn(w);
+                const float hf = __uint_as_float(hb << 16);
+                const uint32_t lb = bf16_bits_rn(w - hf);
+                pw[(8 * k + r) * kWave + lane] = (uint16_t)hb;
+                pw[(8 * k + 4 + r) * kWave + lane] = (uint16_t)lb;
+                st.ws[r][k] = fmaf(st.ws[r][k], corr[r], hf + __uint_as_float(lb << 16));
+                st.zs[r][k] = fmaf(st.zs[r][k], corr[r], ok ? p[r] * tv.z[k] : 0.f);
+            }
+        }
+        wave_lds_sync();
+        if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
+            const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= cv4;
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            // A lane l: row l%16, tokens 32ks + 8(l/16) .. +7
+            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(pw + l16 * kWave + 32 * ks + 8 * g);
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, expand(tv.cw[ks][n]), acc[n], 0, 0, 0);
+        }
+        wave_lds_sync();
+    }
+    // n-tile n (group k = 16n / kGroup) sits in lanes 32k .. 32k+31: lanes
+    // 32k + 0..15 the hi rows, 32k + 16..31 the lo rows.  The hi part also
+    // carries sum p*z - 128 * sum w of its (row, group).
+    __device__ static void to_lds(const f32x4 (&acc)[NT], const State &st, float *wa, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        float corr_rg[kMfmaRows][NG];
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            float wsum[kMfmaRows], zsum[kMfmaRows], wv_[kMfmaRows], zv_[kMfmaRows];
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r) {
+                wv_[r] = st.ws[r][k];
+                zv_[r] = st.zs[r][k];
+            }
+            wave_sum4_dpp(wv_, wsum);
+            wave_sum4_dpp(zv_, zsum);
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r) corr_rg[r][k] = zsum[r] - 128.f * wsum[r];
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            const int k = (16 * n) / kGroup;
+            if ((g >> 1) == k) {
+                const int hl = g & 1;
+#pragma unroll
+                for (int r = 0; r < kMfmaRows; ++r)
+                    wa[(hl * kMfmaRows + r) * D + 16 * n + l16] =
+                        acc[n][r] + (hl == 0 ? corr_rg[r][k] : 0.f);
+            }
+        }
+    }
+};
+
+template <int D, int NC, class VF>
 __global__ void __launch_bounds__((NC + 1) * kWave)
-    decode_attn_mfma_kernel(DecodeCommon c, const __half *v8) {
-    using K = WsCfg<D, NC>;
+    decode_attn_mfma_kernel(DecodeCommon c, typename VF::Args va) {
+    using K = WsCfg<D, NC, VF>;
     constexpr int R = kMfmaRows;
     constexpr int NB = K::kNB;
     constexpr int NT = D / 16;  // MFMA N-tiles (16 dims each)
@@ -573,7 +876,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     extern __shared__ __align__(16) float4 smem4[];
     char *smem = reinterpret_cast<char *>(smem4);
     float4 *lut4 = smem4;                                              // [NB][256]
-    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][8][64]
+    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][kPRows][64]
     volatile lds_t<int> *ready = to_lds<int>(smem + K::kLut + K::kPst);
     volatile lds_t<int> *done = ready + K::kFlagWords;
     volatile lds_t<int> *cbar = done + K::kFlagWords;  // compute-wave barrier counter
@@ -602,9 +905,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
     const int n_tiles = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
     const uint8_t *idx_head = c.idx + bh * c.cap * NB;
-    const char *vhead = reinterpret_cast<const char *>(v8 + bh * c.cap * D);
     const int64_t t_last = max(t_end - 1, (int64_t)0);
-    const int64_t blk_last = t_last / 8;
     const int g = lane >> 4, l16 = lane & 15;
 
     // Barrier that orders LDS only: a wave's outstanding global loads (the
@@ -630,24 +931,14 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         asm volatile("" ::: "memory");
     };
 
-    // Loader: tile j into slot j % kSlots.  The values are 8 contiguous
-    // 8-token blocks (16*D bytes each), copied in 16-byte chunks; chunks of
-    // blocks past the split's last token are clamped to that block, and index
-    // rows past it to the last token's row, so every load stays in bounds.
-    // The LDS destination of lane l is M0 + 16*l.
+    // Loader: tile j into slot j % kSlots: the value format's copies, then
+    // the index rows (rows past the split's last token clamp to its row), so
+    // every load stays in bounds.  The LDS destination of lane l is M0 + 16*l.
     auto issue = [&](int j) {
         const uint32_t sb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) +
                             (uint32_t)((j % K::kSlots) * K::kSlot);
         const int64_t t0 = t_beg + (int64_t)j * kWave;
-        const int64_t b0 = t0 / 8;
-#pragma unroll
-        for (int i = 0; i < K::kTileV / 1024; ++i) {
-            const int q = i * kWave + lane;  // 16-byte chunk of the tile
-            const int64_t blk = min(b0 + q / D, blk_last);
-            __builtin_amdgcn_global_load_lds(vhead + (blk * D + q % D) * 16,
-                                             reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
-                                             kCpolNt);
-        }
+        VF::issue(va, bh, c.cap, t0, t_last, sb, lane);
         if constexpr (NB == 16) {
             const int64_t tk = min(t0 + lane, t_last);
             __builtin_amdgcn_global_load_lds(idx_head + tk * 16,
@@ -685,6 +976,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     f32x4 acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    typename VF::State vst;
+    VF::init(vst);
     float m[R], lsum[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -854,8 +1147,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         }
         compute_barrier(3);  // LUT complete
 
-        _Float16 *pw = pst + wv * 8 * kWave;
-        const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
+        _Float16 *pw = pst + wv * VF::kPRows * kWave;
         for (int j = wv; j < n_tiles; j += NC) {
             const int slot = j % K::kSlots;
             int spins = 0;
@@ -875,13 +1167,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 const uint2 u = *reinterpret_cast<const uint2 *>(sb + K::kTileV + lane * 8);
                 ir.w[0] = u.x; ir.w[1] = u.y;
             }
-            uint4 v[2][NT];
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    v[s2][n] = *reinterpret_cast<const uint4 *>(
-                        sb + ((4 * s2 + g) * D + 16 * n + l16) * 16);
+            typename VF::Tile tv;
+            VF::copy(tv, sb, lane);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             if (lane == 0) done[slot] = j;
             const int64_t t0 = t_beg + (int64_t)j * kWave;
@@ -909,61 +1196,24 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             for (int r = 0; r < R; ++r) sc[r] = e[0][r] + ((kok && lane <= lim_rel[r]) ? 0.f : -INFINITY);
             float tmax[R];
             wave_max4_dpp(sc, tmax);  // the four rows' reductions interleaved
-            float corr[R];
+            float corr[R], p[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float mn = fmaxf(m[r], tmax[r]);
                 corr[r] = fast_exp2(m[r] - mn);
-                const float p = fast_exp2(sc[r] - mn);
-                lsum[r] = fmaf(lsum[r], corr[r], p);
+                p[r] = fast_exp2(sc[r] - mn);
+                lsum[r] = fmaf(lsum[r], corr[r], p[r]);
                 m[r] = mn;
-                const float x = p * kPScale;
-                const _Float16 hi = (_Float16)x;
-                const _Float16 lo = (_Float16)(x - (float)hi);
-                pw[r * kWave + lane] = hi;
-                pw[(r + 4) * kWave + lane] = lo;
             }
-            wave_lds_sync();
-            // rescale only when some row's running max moved (wave-uniform;
-            // after the first tiles it rarely does)
-            if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
-                const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
-#pragma unroll
-                for (int n = 0; n < NT; ++n) acc[n] *= cv4;
-            }
-            if (n_in < kWave) {  // last, partial tile: zero tokens >= t_end
-#pragma unroll
-                for (int s2 = 0; s2 < 2; ++s2) {
-                    const int n_ok = min(max(n_in - 8 * (4 * s2 + g), 0), 8);
-#pragma unroll
-                    for (int n = 0; n < NT; ++n) v[s2][n] = mask_tokens(v[s2][n], n_ok);
-                }
-            }
-#pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    f16x4 a = f16x4{0, 0, 0, 0};
-                    if (a_live)
-                        a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * jj);
-#pragma unroll
-                    for (int n = 0; n < NT; ++n) {
-                        const uint4 u = v[s2][n];
-                        uint2 h = jj == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
-                        const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
-                        acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
-                    }
-                }
-            }
-            wave_lds_sync();
+            VF::pv(tv, vst, acc, p, corr, n_in, pw, lane);
         }
     }
     __syncthreads();  // every tile consumed; the ring is free for the merge
 
-    // wave results: lanes 0-15 hold rows 0-3 (hi parts) of dims 16n + l16,
-    // lanes 16-31 the lo parts of the same rows; both go to LDS as they are
-    // (wa[w][0 = hi, 1 = lo][r][d]) and the combine adds them, so every read
-    // of the combine can be issued at once (one LDS round trip)
+    // wave results: the value format hands each wave's accumulators to LDS
+    // as (hi, lo) parts (wa[w][0 = hi, 1 = lo][r][d]) and the combine adds
+    // them, so every read of the combine can be issued at once (one LDS
+    // round trip)
     float *wm = reinterpret_cast<float *>(ring);
     float *wl = wm + NC * R;
     float *wa = wl + NC * R;  // [NC][2][R][D]
@@ -982,13 +1232,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 wl[wv * R + r] = lsum[r];
             }
         }
-        if (g < 2) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    wa[((wv * 2 + g) * R + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
-        }
+        VF::to_lds(acc, vst, wa + wv * 2 * R * D, lane);
     }
     __syncthreads();
     // combine the compute waves' (m, l, acc) of row r into this workgroup's
@@ -1237,9 +1481,9 @@ static int rows_per_group(int64_t rows_total) { return rows_total <= 1 ? 1 : 4; 
 
 // Kernel families: the VALU kernel (any value layout/dtype, 4 waves per
 // workgroup, 1 or 4 rows) and the MFMA kernel (fp16 values 8-token
-// interleaved, kMfmaWaves compute waves plus a loader wave, 4 rows).
+// interleaved, 4 or 8 compute waves plus a loader wave, 4 rows).
 enum DecodeKind { kKindValu = 0, kKindMfma = 1 };
-constexpr int kMfmaWaves = 4;
+constexpr int kMfmaWaves = 4;  // fewest compute waves of an MFMA kernel (tiles per split)
 
 static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int64_t t_kv,
                                 int n_splits, int kind = kKindValu) {
@@ -1306,11 +1550,12 @@ static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t
     return SS_OK;
 }
 
-template <int D>
-static int launch_mfma(DecodeCommon c, const __half *v8, const DecodeShape &s, hipStream_t st) {
-    constexpr int NC = kMfmaWaves;
-    using K = WsCfg<D, NC>;
-    auto kern = decode_attn_mfma_kernel<D, NC>;
+template <int D, class VF>
+static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
+                       hipStream_t st) {
+    constexpr int NC = VF::kComputeWaves;
+    using K = WsCfg<D, NC, VF>;
+    auto kern = decode_attn_mfma_kernel<D, NC, VF>;
     static bool attr_set = false;
     if (!attr_set) {
         int dev = 0, max_lds = 0;
@@ -1325,7 +1570,7 @@ static int launch_mfma(DecodeCommon c, const __half *v8, const DecodeShape &s, h
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3((NC + 1) * kWave), K::kLds, st, c, v8);
+    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3((NC + 1) * kWave), K::kLds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
     if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
     return launch_merge<D>(c, s, st);
@@ -1648,6 +1893,73 @@ extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const __half *v8 = reinterpret_cast<const __half *>(values_il8);
-    if (head_dim == 128) return launch_mfma<128>(c, v8, s, st);
-    return launch_mfma<64>(c, v8, s, st);
+    if (head_dim == 128) return launch_mfma<128, VIl8<128>>(c, VIl8<128>::Args{v8}, s, st);
+    return launch_mfma<64, VIl8<64>>(c, VIl8<64>::Args{v8}, s, st);
+}
+
+extern "C" int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                         int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                         const int32_t *perm, const void *codebook, int n_blocks,
+                                         int n_centroids, const uint8_t *idx,
+                                         const uint32_t *codes_il, const void *scales,
+                                         const void *zeros, int sz_dtype, int bits,
+                                         int group_size, int64_t cap, int64_t t_kv, int causal,
+                                         int64_t q_offset, void *out, int out_dtype,
+                                         void *workspace, size_t workspace_bytes, int n_splits,
+                                         void *stream) {
+    const float *cents = static_cast<const float *>(codebook);
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(codes_il && scales && zeros, "null codes/scales/zeros");
+    SS_UNSUPPORTED(bits == 2 || bits == 4, "interleaved grouped values need bits 2 or 4 (got %d)",
+                   bits);
+    SS_UNSUPPORTED(group_size == head_dim || 2 * group_size == head_dim,
+                   "group_size %d: the fused kernel takes one or two groups per row", group_size);
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(cap % 16 == 0, "cap must be a multiple of 16 for interleaved grouped values");
+    SS_REQUIRE(((uintptr_t)codes_il % 16) == 0 && ((uintptr_t)scales % 16) == 0 &&
+                   ((uintptr_t)zeros % 16) == 0,
+               "codes, scales and zeros must be 16-byte aligned");
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
+                                       kKindMfma);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    c.centroids = nullptr;
+    c.codebook = static_cast<const uint4 *>(codebook);
+    c.codebook_mul = reinterpret_cast<const float *>(
+        static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int ng = head_dim / group_size;
+#define SS_GIL(DD, BB, NGG, SZT)                                                              \
+    {                                                                                         \
+        using VF = VGil<DD, BB, NGG, SZT>;                                                    \
+        return launch_mfma<DD, VF>(c,                                                         \
+                                   typename VF::Args{codes_il, static_cast<const SZT *>(scales), \
+                                                     static_cast<const SZT *>(zeros)},        \
+                                   s, st);                                                    \
+    }
+#define SS_GIL_SZ(DD, BB, NGG)                     \
+    {                                              \
+        if (sz_dtype == SS_F16) SS_GIL(DD, BB, NGG, __half) \
+        SS_GIL(DD, BB, NGG, float)                 \
+    }
+#define SS_GIL_NG(DD, BB)                      \
+    {                                          \
+        if (ng == 2) SS_GIL_SZ(DD, BB, 2)      \
+        SS_GIL_SZ(DD, BB, 1)                   \
+    }
+    if (head_dim == 128) {
+        if (bits == 2) SS_GIL_NG(128, 2)
+        SS_GIL_NG(128, 4)
+    }
+    if (bits == 2) SS_GIL_NG(64, 2)
+    SS_GIL_NG(64, 4)
+#undef SS_GIL_NG
+#undef SS_GIL_SZ
+#undef SS_GIL
 }

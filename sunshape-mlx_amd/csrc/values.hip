@@ -124,6 +124,36 @@ __global__ void __launch_bounds__(256)
     out[e] = (uint8_t)cnt;
 }
 
+// Interleaved code layout of the fused grouped-value decode: per (b, h), word
+// (blk, d) of [cap / vpw][D] holds dim d of tokens blk*vpw .. blk*vpw + vpw - 1,
+// token i of the block at bits [bits*i, bits*(i+1)).  One thread per (block,
+// dim) of the appended range; bits of tokens outside [offset, offset + n_t)
+// are kept.
+__global__ void __launch_bounds__(256)
+    pack_grouped_il_kernel(const uint32_t *packed, int64_t n_h, int64_t n_t, int64_t p_sb,
+                           int64_t p_sh, int64_t p_st, int d, int bits, uint32_t *out_il,
+                           int64_t cap, int64_t offset, int64_t b0, int64_t n_blk) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t bh = blockIdx.y;  // b * n_h + h
+    if (e >= n_blk * d) return;
+    const int64_t blk = b0 + e / d;
+    const int dd = (int)(e % d);
+    const int vpw = vals_per_word(bits);
+    const int nw = packed_words(d, bits);
+    const uint32_t mask = (1u << bits) - 1u;
+    const int64_t b = bh / n_h, h = bh - b * n_h;
+    uint32_t *wp = out_il + (bh * (cap / vpw) + blk) * d + dd;
+    uint32_t word = *wp;
+    for (int i = 0; i < vpw; ++i) {
+        const int64_t t = blk * vpw + i - offset;  // row of the appended chunk
+        if (t < 0 || t >= n_t) continue;
+        const uint32_t w = packed[(b * p_sb + h * p_sh + t * p_st) * nw + dd / vpw];
+        const uint32_t code = (w >> ((dd % vpw) * bits)) & mask;
+        word = (word & ~(mask << (i * bits))) | (code << (i * bits));
+    }
+    *wp = word;
+}
+
 static inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace ss
@@ -219,5 +249,29 @@ extern "C" int ss_scalar_quantize(const float *values, int64_t n, const float *b
     hipLaunchKernelGGL(scalar_quantize_kernel, dim3(blocks_for(n)), dim3(256), 0, st, values, n,
                        boundaries, n_boundaries, out);
     SS_LAUNCH_CHECK("scalar_quantize_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_pack_grouped_il(const uint32_t *packed, int64_t n_b, int64_t n_h, int64_t n_t,
+                                  int64_t p_sb, int64_t p_sh, int64_t p_st, int head_dim, int bits,
+                                  uint32_t *out_il, int64_t cap, int64_t offset, void *stream) {
+    SS_REQUIRE(bits == 2 || bits == 4, "interleaved codes need bits 2 or 4 (got %d)", bits);
+    SS_REQUIRE(head_dim >= 1 && head_dim % (32 / bits) == 0, "head_dim %d cannot be packed at %d bits",
+               head_dim, bits);
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0 && offset >= 0, "negative sizes");
+    SS_REQUIRE(cap % (32 / bits) == 0, "cap must be a multiple of %d", 32 / bits);
+    SS_REQUIRE(offset + n_t <= cap, "append range [%lld, %lld) past cap %lld", (long long)offset,
+               (long long)(offset + n_t), (long long)cap);
+    if (n_b * n_h * n_t == 0) return SS_OK;
+    SS_REQUIRE(packed && out_il, "null pointer argument");
+    SS_UNSUPPORTED(n_b * n_h < 65536, "too many (batch, head) rows for one launch");
+    const int vpw = 32 / bits;
+    const int64_t b0 = offset / vpw, b1 = (offset + n_t - 1) / vpw;
+    const int64_t n_blk = b1 - b0 + 1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(pack_grouped_il_kernel, dim3(blocks_for(n_blk * head_dim), (unsigned)(n_b * n_h)),
+                       dim3(256), 0, st, packed, n_h, n_t, p_sb, p_sh, p_st, head_dim, bits, out_il,
+                       cap, offset, b0, n_blk);
+    SS_LAUNCH_CHECK("pack_grouped_il_kernel launch");
     return SS_OK;
 }

@@ -382,3 +382,73 @@ def test_decode_il8_peaked_and_flat_softmax():
         torch.cuda.synchronize()
         ref = O.sdpa(q, idx, vals, cents, perm, 0.0883883)
         assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def grouped_case(seed, b, hkv, t_kv, d, bits, group, cap, sz_dtype=torch.float16):
+    """Grouped-quantised values of a (b, hkv, t_kv, d) N(0,1) cache: reference
+    packed rows, scales/zeros of dtype sz_dtype (cap rows, zero past t_kv)
+    and the token-interleaved codes built with the relayout kernel in three
+    unaligned appends."""
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal((b, hkv, t_kv, d)).astype(np.float16)
+    nw, ng = d * bits // 32, d // group
+    packed = torch.zeros((b, hkv, cap, nw), dtype=torch.int32, device=DEV)
+    sc = torch.zeros((b, hkv, cap, ng), dtype=sz_dtype, device=DEV)
+    ze = torch.zeros((b, hkv, cap, ng), dtype=sz_dtype, device=DEV)
+    _hip.quantize_values_grouped(t(v), bits, group, packed[:, :, :t_kv], sc[:, :, :t_kv],
+                                 ze[:, :, :t_kv])
+    il = torch.zeros((b, hkv, cap * bits // 32, d), dtype=torch.int32, device=DEV)
+    cuts = sorted({0, t_kv, min(t_kv, 7), min(t_kv, t_kv // 2 + 3)})
+    for a0, a1 in zip(cuts[:-1], cuts[1:]):
+        _hip.pack_grouped_il(packed[:, :, a0:a1], bits, il, a0)
+    return v, packed, sc, ze, il
+
+
+@pytest.mark.parametrize("bits,d,t_kv,cap", [(2, 128, 1000, 1024), (4, 128, 77, 96), (2, 64, 300, 320),
+                                             (4, 64, 16, 16)])
+def test_pack_grouped_il_roundtrip(bits, d, t_kv, cap):
+    """Token-interleaved codes written in unaligned appends read back as the
+    reference packed rows bit for bit; words past t_kv stay zero."""
+    _, packed, _, _, il = grouped_case(11 + bits, 2, 3, t_kv, d, bits, d // 2, cap)
+    torch.cuda.synchronize()
+    back = _hip.grouped_il_to_packed(il, bits).view(torch.int32).cpu().numpy()
+    assert np.array_equal(back[:, :, :t_kv], packed[:, :, :t_kv].cpu().numpy())
+    assert not back[:, :, t_kv:].any()
+
+
+@pytest.mark.parametrize(
+    "b,hq,hkv,d,t_kv,t_q,bits,group,sz,causal,splits,cap",
+    [
+        (2, 32, 8, 128, 4096, 1, 2, 64, "f16", False, 0, None),   # config 4 shape, T=4096
+        (1, 8, 2, 128, 1003, 1, 2, 64, "f32", False, 0, 1024),    # ragged T, f32 scale/zero
+        (1, 4, 1, 128, 1, 1, 4, 128, "f16", False, 0, 16),        # single token, 4-bit, 1 group
+        (1, 4, 2, 128, 777, 1, 4, 64, "f16", False, 5, 784),      # forced splits, rep 2
+        (1, 8, 2, 64, 513, 1, 2, 32, "f16", False, 0, 528),       # head_dim 64, 2 groups
+        (1, 4, 1, 64, 600, 1, 4, 64, "f32", False, 3, 608),       # head_dim 64, 1 group, f32
+        (1, 4, 1, 128, 64, 3, 2, 64, "f16", True, 0, 64),         # prefill rows, causal
+        (2, 6, 2, 128, 300, 5, 2, 64, "f16", True, 3, 320),       # several row groups
+    ])
+def test_decode_grouped_il_matches_oracle(b, hq, hkv, d, t_kv, t_q, bits, group, sz, causal, splits,
+                                          cap):
+    cap = cap or t_kv
+    cents, perm, idx, _, q = decode_case(b * 7000 + t_kv + bits, b, hq, hkv, d, t_kv, t_q, cap)
+    szt = torch.float16 if sz == "f16" else torch.float32
+    _, packed, sc, ze, il = grouped_case(b + t_kv + bits, b, hkv, t_kv, d, bits, group, cap, szt)
+    if t_kv < cap:  # unwritten scale/zero rows past t_kv must not leak into the result
+        sc[:, :, t_kv:] = float("nan")
+        ze[:, :, t_kv:] = float("nan")
+    scale = 1.0 / np.sqrt(d)
+    out = _hip.decode_attn_grouped_il(t(q), scale, t(perm), t(cents), t(idx), il, sc, ze, bits, group,
+                                      t_kv, causal=causal, q_offset=t_kv - t_q if causal else 0,
+                                      out_dtype=torch.float32, n_splits=splits)
+    torch.cuda.synchronize()
+    vals = np.stack([np.stack([
+        O.dequantize_values(packed[bi, hi, :t_kv].cpu().numpy().view(np.uint32),
+                            sc[bi, hi, :t_kv].float().cpu().numpy(),
+                            ze[bi, hi, :t_kv].float().cpu().numpy(), d, bits, group)
+        for hi in range(hkv)]) for bi in range(b)])
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals, cents, perm, scale, mask="causal" if causal else None)
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) <= REL_TOL
+
