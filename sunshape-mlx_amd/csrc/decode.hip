@@ -523,17 +523,22 @@ __device__ __forceinline__ void wait_oldest_tile(int k) {
 template <int D, int NC, class VF>
 struct WsCfg {
     static constexpr int kNB = D / kBlockDim;
-    static constexpr int kTileV = VF::kTileV;     // value bytes of a 64-token tile
-    static constexpr int kTileI = kWave * kNB;    // uint8 index rows of the tile
+    static constexpr int kSub = VF::kSub;         // 64-token sub-tiles per ring tile
+    static constexpr int kTileV = VF::kTileV;     // value bytes of a ring tile
+    static constexpr int kTileI1 = kWave * kNB;   // uint8 index rows of a sub-tile
+    static constexpr int kTileI = kSub * kTileI1;
+    static constexpr int kLoadsI = (kTileI + 1023) / 1024;
     static constexpr int kSlot = kTileV + kTileI;
     static constexpr int kLut = kNB * kLutStride * 16;  // float4 per (block, centroid)
     static constexpr int kPst = NC * VF::kPRows * kWave * 2;  // P staging, 16-bit [rows][64] per wave
     static constexpr int kFlagWords = 16;
-    static constexpr int kFlags = (2 * kFlagWords + 4) * 4;  // ready[], done[], barrier counter
+    // ready[slot], done[slot][sub], barrier counter
+    static constexpr int kFlags = (kFlagWords * (1 + kSub) + 4) * 4;
     static constexpr int kRing = kLut + kPst + kFlags;
     static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
     static constexpr int kSlots = kSlotsFit < VF::kMaxSlots ? kSlotsFit : VF::kMaxSlots;
-    static constexpr int kLoadsPerTile = VF::kLoadsV + 1;
+    static constexpr int kLoadsPerTile = VF::kLoadsV + kLoadsI;
+    static_assert(kLoadsPerTile <= 63, "one ring tile within the vmcnt range");
     static constexpr int kDepthVm = 63 / kLoadsPerTile + 1;
     static constexpr int kDepth = kSlots < kDepthVm ? kSlots : kDepthVm;
     static constexpr int kLds = kRing + kSlots * kSlot;
@@ -574,13 +579,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // fp16 values, 8-token interleaved: element (t, d) at [t/8][d][t%8].  P is
 // staged as fp16 hi/lo rows of p * 2^15 (A rows 0-3 hi, 4-7 lo, 8-15 zero)
 // and P.V is v_mfma_f32_16x16x16f16.
-template <int D>
+template <int D, int SUB = 1>
 struct VIl8 {
     struct Args {
         const __half *v8;
     };
     static constexpr int NT = D / 16;
-    static constexpr int kTileV = kWave * D * 2;
+    static constexpr int kSub = SUB;
+    static constexpr int kTileV1 = kWave * D * 2;  // one 64-token sub-tile
+    static constexpr int kTileV = kSub * kTileV1;
     static constexpr int kLoadsV = kTileV / 1024;
     static constexpr int kPRows = 8;
     static constexpr int kMaxSlots = 8;
@@ -589,12 +596,22 @@ struct VIl8 {
         uint4 v[2][NT];
     };
     struct State {};
-    // values of tokens t0 .. t0+63; 8-token blocks past the split's last
-    // token are clamped to that block, so every copy stays in bounds
+    // values of tokens t0 .. t0 + 64*kSub - 1 (contiguous); in a tile that
+    // reaches past the split's last token, 8-token blocks past it are
+    // clamped to its block, so every copy stays in bounds
     __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
                                  uint32_t sb, int lane) {
         const char *vhead = reinterpret_cast<const char *>(a.v8 + bh * cap * D);
         const int64_t b0 = t0 / 8, blk_last = t_last / 8;
+        if (t0 + kSub * kWave - 1 <= t_last) {  // uniform base + lane offset
+            const char *base = vhead + b0 * D * 16;
+#pragma unroll
+            for (int i = 0; i < kLoadsV; ++i)
+                __builtin_amdgcn_global_load_lds(base + (uint32_t)(i * 1024 + lane * 16),
+                                                 reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                                 kCpolNt);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < kLoadsV; ++i) {
             const int q = i * kWave + lane;  // 16-byte chunk of the tile
@@ -604,8 +621,9 @@ struct VIl8 {
                                              kCpolNt);
         }
     }
-    __device__ static void copy(Tile &tv, const char *sb, int lane) {
+    __device__ static void copy(Tile &tv, const char *sb, int sub, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
+        sb += sub * kTileV1;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -698,10 +716,16 @@ struct VGil {
     };
     static constexpr int NT = D / 16;
     static constexpr int TPW = 32 / BITS;                 // tokens per code word
-    static constexpr int kCodeBytes = kWave * D * BITS / 8;
-    static constexpr int kSzBytes = kWave * NG * (int)sizeof(SZT);
+    static constexpr int kCodeBytes1 = kWave * D * BITS / 8;  // codes of a 64-token sub-tile
+    static constexpr int kSzBytes1 = kWave * NG * (int)sizeof(SZT);
+    // ring tiles of up to 256 tokens (about 8 KB of codes): small per-stream
+    // requests of 64-token tiles leave HBM far from its streaming rate
+    static constexpr int kSub = 8192 / kCodeBytes1 < 4 ? 8192 / kCodeBytes1 : 4;
+    static constexpr int kCodeBytes = kSub * kCodeBytes1;
+    static constexpr int kSzBytes = kSub * kSzBytes1;
+    static constexpr int kSzLoads = (kSzBytes + 1023) / 1024;
     static constexpr int kTileV = kCodeBytes + 2 * kSzBytes;
-    static constexpr int kLoadsV = kCodeBytes / 1024 + 2;
+    static constexpr int kLoadsV = kCodeBytes / 1024 + 2 * kSzLoads;
     static constexpr int kPRows = 16;
     static constexpr int kMaxSlots = 16;
     // a tile is 5x fewer bytes than fp16 values: two or three compute waves
@@ -710,7 +734,7 @@ struct VGil {
     static constexpr int kGroup = D / NG;
     static_assert(BITS == 2 || BITS == 4, "bits");
     static_assert(NG == 1 || NG == 2, "groups per row");
-    static_assert(kCodeBytes % 1024 == 0 && kSzBytes % 16 == 0 && kSzBytes <= 1024, "tile sections");
+    static_assert(kSub >= 1 && kCodeBytes1 % 1024 == 0 && kSzBytes1 % 16 == 0, "tile sections");
     struct Tile {
         uint32_t cw[2][NT];  // codes of tokens 32*ks + 8*(lane/16) .. +7, dim 16n + lane%16
         float s[NG], z[NG];  // scale / zero of token `lane`
@@ -721,10 +745,35 @@ struct VGil {
     };
     __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
                                  uint32_t sb, int lane) {
-        // codes: the tile's words are contiguous; 16-byte chunks (4 words of
-        // one block) past the split's last block clamp to that block
         const char *chead = reinterpret_cast<const char *>(a.codes + bh * (cap / TPW) * D);
-        const int64_t wb0 = t0 / TPW, blk_last = t_last / TPW;
+        const char *sp = reinterpret_cast<const char *>(a.scales + (bh * cap + t0) * NG);
+        const char *zp = reinterpret_cast<const char *>(a.zeros + (bh * cap + t0) * NG);
+        const int64_t wb0 = t0 / TPW;
+        if (t0 + kSub * kWave - 1 <= t_last) {  // uniform bases + lane offsets
+            const char *cb = chead + wb0 * D * 4;
+#pragma unroll
+            for (int i = 0; i < kCodeBytes / 1024; ++i)
+                __builtin_amdgcn_global_load_lds(cb + (uint32_t)(i * 1024 + lane * 16),
+                                                 reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                                 kCpolNt);
+#pragma unroll
+            for (int i = 0; i < kSzLoads; ++i) {
+                const uint32_t off = (uint32_t)(i * 1024 + lane * 16);
+                if (kSzBytes % 1024 == 0 || off < (uint32_t)kSzBytes) {
+                    __builtin_amdgcn_global_load_lds(
+                        sp + off, reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + i * 1024), 16, 0,
+                        kCpolNt);
+                    __builtin_amdgcn_global_load_lds(
+                        zp + off, reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + kSzBytes + i * 1024),
+                        16, 0, kCpolNt);
+                }
+            }
+            return;
+        }
+        // a tile reaching past the split's last token: code chunks (4 words
+        // of one block) past its block clamp to that block, scale/zero
+        // chunks past the one holding it clamp to that chunk
+        const int64_t blk_last = t_last / TPW;
 #pragma unroll
         for (int i = 0; i < kCodeBytes / 1024; ++i) {
             const int w = (i * kWave + lane) * 4;  // first word of the chunk
@@ -733,24 +782,25 @@ struct VGil {
                                              reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
                                              kCpolNt);
         }
-        // scales, zeros: chunks past the one holding the last token clamp to it
         constexpr int kTokPerChunk = 16 / (NG * (int)sizeof(SZT));
         const int64_t ch_last = (t_last - t0) / kTokPerChunk;
-        const int64_t ch = min((int64_t)lane, ch_last);
-        if (lane < kSzBytes / 16) {
-            const char *sp = reinterpret_cast<const char *>(a.scales + (bh * cap + t0) * NG);
-            const char *zp = reinterpret_cast<const char *>(a.zeros + (bh * cap + t0) * NG);
-            __builtin_amdgcn_global_load_lds(sp + ch * 16,
-                                             reinterpret_cast<lds_t<void> *>(sb + kCodeBytes), 16, 0,
-                                             kCpolNt);
-            __builtin_amdgcn_global_load_lds(zp + ch * 16,
-                                             reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + kSzBytes),
-                                             16, 0, kCpolNt);
+#pragma unroll
+        for (int i = 0; i < kSzLoads; ++i) {
+            const int c = i * kWave + lane;
+            if (kSzBytes % 1024 == 0 || c * 16 < kSzBytes) {
+                const int64_t ch = min((int64_t)c, ch_last);
+                __builtin_amdgcn_global_load_lds(
+                    sp + ch * 16, reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + i * 1024), 16, 0,
+                    kCpolNt);
+                __builtin_amdgcn_global_load_lds(
+                    zp + ch * 16, reinterpret_cast<lds_t<void> *>(sb + kCodeBytes + kSzBytes + i * 1024),
+                    16, 0, kCpolNt);
+            }
         }
     }
-    __device__ static void copy(Tile &tv, const char *sb, int lane) {
+    __device__ static void copy(Tile &tv, const char *sb, int sub, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
-        const uint32_t *cw = reinterpret_cast<const uint32_t *>(sb);
+        const uint32_t *cw = reinterpret_cast<const uint32_t *>(sb + sub * kCodeBytes1);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int tk = 32 * ks + 8 * g;  // first of the lane's 8 tokens
@@ -760,8 +810,8 @@ struct VGil {
                 tv.cw[ks][n] = BITS == 2 ? (w >> (2 * (tk % TPW))) & 0xffffu : w;
             }
         }
-        const SZT *sp = reinterpret_cast<const SZT *>(sb + kCodeBytes);
-        const SZT *zp = reinterpret_cast<const SZT *>(sb + kCodeBytes + kSzBytes);
+        const SZT *sp = reinterpret_cast<const SZT *>(sb + kCodeBytes + sub * kSzBytes1);
+        const SZT *zp = reinterpret_cast<const SZT *>(sb + kCodeBytes + kSzBytes + sub * kSzBytes1);
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
             tv.s[k] = (float)sp[lane * NG + k];
@@ -878,8 +928,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     float4 *lut4 = smem4;                                              // [NB][256]
     _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][kPRows][64]
     volatile lds_t<int> *ready = to_lds<int>(smem + K::kLut + K::kPst);
-    volatile lds_t<int> *done = ready + K::kFlagWords;
-    volatile lds_t<int> *cbar = done + K::kFlagWords;  // compute-wave barrier counter
+    volatile lds_t<int> *done = ready + K::kFlagWords;               // [slot][sub]
+    volatile lds_t<int> *cbar = done + K::kFlagWords * K::kSub;  // compute-wave barrier counter
     char *ring = smem + K::kRing;
     const lds_t<f32x4> *lut_l = to_lds<f32x4>(smem4);  // 16-byte LUT reads
 
@@ -903,7 +953,9 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
 
     const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
     const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
-    const int n_tiles = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
+    // 64-token units (one per compute step) and ring tiles of kSub units
+    const int n_units = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
+    const int n_tiles = (n_units + K::kSub - 1) / K::kSub;
     const uint8_t *idx_head = c.idx + bh * c.cap * NB;
     const int64_t t_last = max(t_end - 1, (int64_t)0);
     const int g = lane >> 4, l16 = lane & 15;
@@ -931,26 +983,25 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         asm volatile("" ::: "memory");
     };
 
-    // Loader: tile j into slot j % kSlots: the value format's copies, then
-    // the index rows (rows past the split's last token clamp to its row), so
-    // every load stays in bounds.  The LDS destination of lane l is M0 + 16*l.
+    // Loader: ring tile j (tokens t_beg + 64*kSub*j ..) into slot j % kSlots:
+    // the value format's copies, then the index rows (contiguous, chunks past
+    // the one holding the split's last token clamp to it), so every load
+    // stays in bounds.  The LDS destination of lane l is M0 + 16*l.
     auto issue = [&](int j) {
         const uint32_t sb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) +
                             (uint32_t)((j % K::kSlots) * K::kSlot);
-        const int64_t t0 = t_beg + (int64_t)j * kWave;
+        const int64_t t0 = t_beg + (int64_t)j * K::kSub * kWave;
         VF::issue(va, bh, c.cap, t0, t_last, sb, lane);
-        if constexpr (NB == 16) {
-            const int64_t tk = min(t0 + lane, t_last);
-            __builtin_amdgcn_global_load_lds(idx_head + tk * 16,
-                                             reinterpret_cast<lds_t<void> *>(sb + K::kTileV), 16,
-                                             0, kCpolNt);
-        } else {
-            static_assert(NB == 8, "unsupported block count");
-            if (lane < kWave / 2) {  // 512 bytes: two tokens per 16-byte chunk
-                const int64_t ch = min(t0 / 2 + lane, t_last / 2);
-                __builtin_amdgcn_global_load_lds(idx_head + ch * 16,
-                                                 reinterpret_cast<lds_t<void> *>(sb + K::kTileV),
-                                                 16, 0, kCpolNt);
+        const uint8_t *ip = idx_head + t0 * NB;
+        const bool full = t0 + K::kSub * kWave - 1 <= t_last;
+        const int64_t ch_last = ((t_last - t0) * NB) / 16;
+#pragma unroll
+        for (int i = 0; i < K::kLoadsI; ++i) {
+            const int ch = i * kWave + lane;
+            if (K::kTileI % 1024 == 0 || ch * 16 < K::kTileI) {
+                const uint8_t *src = full ? ip + (uint32_t)(ch * 16) : ip + min((int64_t)ch, ch_last) * 16;
+                __builtin_amdgcn_global_load_lds(
+                    src, reinterpret_cast<lds_t<void> *>(sb + K::kTileV + i * 1024), 16, 0, kCpolNt);
             }
         }
     };
@@ -965,7 +1016,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     float *qp = qraw + R * D;                      // [R][D]
     constexpr int CT = NC * kWave;             // compute threads
     constexpr int QE = (R * D + CT - 1) / CT;  // query elements per compute thread
-    if (tid < 2 * K::kFlagWords) ready[tid] = -1;  // ready[] and done[]
+    if (tid < K::kFlagWords * (1 + K::kSub)) ready[tid] = -1;  // ready[] and done[][]
     if (tid == 0) *cbar = 0;
     int64_t lim[R];
 #pragma unroll
@@ -990,6 +1041,15 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     // after a join inherits the loader's outstanding tile copies as pending
     // loads, and the loader streams from the start without waiting for the
     // LUT.
+    // the slot of ring tile j has been copied out of by all consumers of
+    // tile j - kSlots
+    auto slot_free = [&](int j) {
+        const int s0 = (j % K::kSlots) * K::kSub;
+        bool ok = true;
+#pragma unroll
+        for (int u = 0; u < K::kSub; ++u) ok = ok && done[s0 + u] == j - K::kSlots;
+        return ok;
+    };
     if (loader) {
         // the compute waves' small loads are issued (so they are ahead of
         // the tiles in the memory queue) and the flags are initialised
@@ -998,7 +1058,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         int spins = 0;
         while (landed < n_tiles) {
             if (issued < n_tiles && issued - landed < K::kDepth &&
-                (issued < K::kSlots || done[issued % K::kSlots] == issued - K::kSlots)) {
+                (issued < K::kSlots || slot_free(issued))) {
                 asm volatile("" ::: "memory");
                 issue(issued++);
                 continue;
@@ -1148,7 +1208,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         compute_barrier(3);  // LUT complete
 
         _Float16 *pw = pst + wv * VF::kPRows * kWave;
-        for (int j = wv; j < n_tiles; j += NC) {
+        for (int u = wv; u < n_units; u += NC) {
+            const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
             const int slot = j % K::kSlots;
             int spins = 0;
             while (ready[slot] != j) {
@@ -1159,19 +1220,20 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             // copy the tile (index rows and values) into registers and
             // release the slot at once
             const char *sb = ring + slot * K::kSlot;
+            const char *ib = sb + K::kTileV + sub * K::kTileI1;
             IdxRow<NB> ir;
             if constexpr (NB == 16) {
-                const uint4 u = *reinterpret_cast<const uint4 *>(sb + K::kTileV + lane * 16);
-                ir.w[0] = u.x; ir.w[1] = u.y; ir.w[2] = u.z; ir.w[3] = u.w;
+                const uint4 w4 = *reinterpret_cast<const uint4 *>(ib + lane * 16);
+                ir.w[0] = w4.x; ir.w[1] = w4.y; ir.w[2] = w4.z; ir.w[3] = w4.w;
             } else {
-                const uint2 u = *reinterpret_cast<const uint2 *>(sb + K::kTileV + lane * 8);
-                ir.w[0] = u.x; ir.w[1] = u.y;
+                const uint2 w2 = *reinterpret_cast<const uint2 *>(ib + lane * 8);
+                ir.w[0] = w2.x; ir.w[1] = w2.y;
             }
             typename VF::Tile tv;
-            VF::copy(tv, sb, lane);
+            VF::copy(tv, sb, sub, lane);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) done[slot] = j;
-            const int64_t t0 = t_beg + (int64_t)j * kWave;
+            if (lane == 0) done[slot * K::kSub + sub] = j;
+            const int64_t t0 = t_beg + (int64_t)u * kWave;
             // tokens of this tile still inside the split (wave-uniform, 1..64)
             const int n_in = (int)min(t_end - t0, (int64_t)kWave);
             const bool kok = lane < n_in;
