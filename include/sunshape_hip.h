@@ -213,9 +213,10 @@ int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_he
 /*
  * As ss_decode_attn_grouped with the 2- or 4-bit codes held in a token-
  * interleaved layout and the codebook prepared by ss_codebook_f16x2.  Code of
- * token t, dimension d of a (batch, KV head) row is bits
- * [bits*(t%tpw), bits*(t%tpw+1)) of
- * codes_il[((b*n_kv_heads + h)*cap/tpw + t/tpw)*head_dim + d], tpw = 32/bits;
+ * token t, dimension d of a (batch, KV head) row is the bits-wide field at
+ * bit bits*(i/2) + 16*(i%2), i = t%tpw, of
+ * codes_il[((b*n_kv_heads + h)*cap/tpw + t/tpw)*head_dim + d], tpw = 32/bits
+ * (even tokens of the word in its low half, odd tokens in its high half);
  * scales/zeros keep ss_decode_attn_grouped's [batch][n_kv_heads][cap][n_groups]
  * layout.  group_size must be head_dim or head_dim/2, cap % 16 == 0, all
  * operands 16-byte aligned.  The LUT and P.V run on the matrix cores (P.V in

@@ -499,8 +499,11 @@ def grouped_il_to_packed(codes_il: torch.Tensor, bits: int, t: int | None = None
     b_, h_, nblk, d = codes_il.shape
     tpw = 32 // bits
     w = codes_il.view(torch.int32).to(torch.int64) & 0xffffffff
+    # token i of an interleaved word sits at bit bits*(i//2) + 16*(i%2)
+    il_shifts = torch.tensor([bits * (i // 2) + 16 * (i % 2) for i in range(tpw)],
+                             device=w.device, dtype=torch.int64)
     shifts = torch.arange(tpw, device=w.device, dtype=torch.int64) * bits
-    codes = (w.unsqueeze(3) >> shifts.view(1, 1, 1, tpw, 1)) & ((1 << bits) - 1)  # (B,H,blk,tpw,D)
+    codes = (w.unsqueeze(3) >> il_shifts.view(1, 1, 1, tpw, 1)) & ((1 << bits) - 1)  # (B,H,blk,tpw,D)
     codes = codes.reshape(b_, h_, nblk * tpw, d)
     if t is not None:
         codes = codes[:, :, :t]

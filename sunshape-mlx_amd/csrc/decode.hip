@@ -472,6 +472,10 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kPScale = 32768.f;  // 2^15
 constexpr int kMfmaRows = 4;
+// Row stride (16-bit elements) of a wave's P staging: 64 tokens plus 8 of
+// padding, so the 16 rows a matrix-core operand read touches start in
+// different LDS banks.
+constexpr int kPStride = 64 + 8;
 constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr int kSpinLimit = 1 << 20;  // bounded waits: ~0.03 s of s_sleep 1
 
@@ -530,7 +534,7 @@ struct WsCfg {
     static constexpr int kLoadsI = (kTileI + 1023) / 1024;
     static constexpr int kSlot = kTileV + kTileI;
     static constexpr int kLut = kNB * kLutStride * 16;  // float4 per (block, centroid)
-    static constexpr int kPst = NC * VF::kPRows * kWave * 2;  // P staging, 16-bit [rows][64] per wave
+    static constexpr int kPst = NC * VF::kPRows * kPStride * 2;  // P staging, 16-bit [rows][kPStride] per wave
     static constexpr int kFlagWords = 16;
     // ready[slot], done[slot][sub], barrier counter
     static constexpr int kFlags = (kFlagWords * (1 + kSub) + 4) * 4;
@@ -632,20 +636,21 @@ struct VIl8 {
     }
     __device__ static void init(State &) {}
     __device__ static void pv(Tile &tv, State &, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
-                              const float (&corr)[kMfmaRows], int n_in, _Float16 *pw, int lane) {
+                              const float (&corr)[kMfmaRows], bool rescale, int n_in, _Float16 *pw,
+                              int lane) {
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int r = 0; r < kMfmaRows; ++r) {
             const float x = p[r] * kPScale;
             const _Float16 hi = (_Float16)x;
             const _Float16 lo = (_Float16)(x - (float)hi);
-            pw[r * kWave + lane] = hi;
-            pw[(r + 4) * kWave + lane] = lo;
+            pw[r * kPStride + lane] = hi;
+            pw[(r + 4) * kPStride + lane] = lo;
         }
         wave_lds_sync();
         // rescale only when some row's running max moved (wave-uniform;
         // after the first tiles it rarely does)
-        if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
+        if (rescale) {
             const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
 #pragma unroll
             for (int n = 0; n < NT; ++n) acc[n] *= cv4;
@@ -665,7 +670,7 @@ struct VIl8 {
             for (int jj = 0; jj < 2; ++jj) {
                 f16x4 a = f16x4{0, 0, 0, 0};
                 if (a_live)
-                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kWave + 32 * s2 + 8 * g + 4 * jj);
+                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 32 * s2 + 8 * g + 4 * jj);
 #pragma unroll
                 for (int n = 0; n < NT; ++n) {
                     const uint4 u = tv.v[s2][n];
@@ -691,23 +696,38 @@ struct VIl8 {
     }
 };
 
-// Float32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_bits_rn(float x) {
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+// Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
+__device__ __forceinline__ uint32_t bf16x2_rn(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// A 32-bit value the compiler cannot see as a literal, so the bitwise
+// and-or of the code expansion below becomes a single v_and_or_b32 on
+// registers (gfx9 three-operand forms take no literal operands).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(x));
+    return r;
 }
 
 // Grouped asymmetric values (bits 2 or 4, NG = 1 or 2 groups per row, scale
 // and zero of type SZT): v = code * s + z.  Codes are token-interleaved: per
 // (b, h), u32 word (blk, d) of [cap / TPW][D] holds dim d of tokens blk*TPW ..
-// +TPW-1 (token i at bits [BITS*i, BITS*(i+1))); scales/zeros [cap][NG].
-// P.V = sum_t (p_t s_t) code_t + sum_t p_t z_t.  The first sum runs on the
-// matrix cores (v_mfma_f32_16x16x32_bf16): A rows are w = p * s of each
-// (group, row) split into bf16 hi/lo (rows 8g+0..3 hi, 8g+4..7 lo of group
-// g), B the codes of 8 tokens of one dim as bf16 128 + code (bit pattern
-// 0x4300 | code, exact), so the products carry 128 * sum_t w_t, which is
-// subtracted at the end from the exact fp32 sum of the same hi + lo parts.
-// The second sum accumulates per (row, group) in fp32 on the lanes.
+// +TPW-1, token i at bit BITS*(i/2) + 16*(i%2) (even tokens in the low half,
+// odd ones in the high half), so two neighbouring tokens' codes of one dim
+// sit in the two bf16 halves of a dword after one shift; scales/zeros are
+// [cap][NG].  P.V = sum_t (p_t s_t) code_t + sum_t p_t z_t.  The first sum
+// runs on the matrix cores (v_mfma_f32_16x16x32_bf16): A rows are w = p * s
+// of each (group, row) split into bf16 hi/lo (rows 8g+0..3 hi, 8g+4..7 lo of
+// group g), B the codes of 8 tokens of one dim as bf16 128 + code (bit
+// pattern 0x4300 | code, exact), so the products carry 128 * sum_t w_t; the
+// same A times an all-128 B (one more product per k-step) accumulates that
+// term exactly alike, and the two are subtracted at the end.  The second sum
+// accumulates per (row, group) in fp32 on the lanes.  N-tile n, column c
+// holds dim 8c + n, so a lane reads its eight dims' words as two 16-byte
+// LDS loads per k-step.
 template <int D, int BITS, int NG, class SZT>
 struct VGil {
     struct Args {
@@ -728,19 +748,25 @@ struct VGil {
     static constexpr int kLoadsV = kCodeBytes / 1024 + 2 * kSzLoads;
     static constexpr int kPRows = 16;
     static constexpr int kMaxSlots = 16;
-    // a tile is 5x fewer bytes than fp16 values: two or three compute waves
-    // per SIMD overlap the per-tile latency chain
-    static constexpr int kComputeWaves = 8;
+    // one compute wave per SIMD: a second one on the same SIMD slows both
+    // (measured: the compute-only time of a tile doubles per SIMD)
+    static constexpr int kComputeWaves = 4;
     static constexpr int kGroup = D / NG;
+    static constexpr uint32_t kCodeMask = BITS == 2 ? 0x00030003u : 0x000f000fu;
+    static constexpr uint32_t kBias = 0x43004300u;  // two bf16 128.0
     static_assert(BITS == 2 || BITS == 4, "bits");
     static_assert(NG == 1 || NG == 2, "groups per row");
+    static_assert(NT == 8 || NT == 4, "n-tiles");
     static_assert(kSub >= 1 && kCodeBytes1 % 1024 == 0 && kSzBytes1 % 16 == 0, "tile sections");
     struct Tile {
-        uint32_t cw[2][NT];  // codes of tokens 32*ks + 8*(lane/16) .. +7, dim 16n + lane%16
+        // per k-step, the lane's 8 tokens (32ks + 8*(lane/16) ..) of dims
+        // 8*(lane%16) + n: their code word, shifted so that dword j of the
+        // operand is ((cw >> BITS*j) & kCodeMask) | kBias
+        uint32_t cw[2][NT];
         float s[NG], z[NG];  // scale / zero of token `lane`
     };
     struct State {
-        float ws[kMfmaRows][NG];  // sum of w = hi + lo over this lane's tokens
+        f32x4 bias;               // 128 * sum of the staged A rows, laid out as acc
         float zs[kMfmaRows][NG];  // sum of p * z
     };
     __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
@@ -800,15 +826,26 @@ struct VGil {
     }
     __device__ static void copy(Tile &tv, const char *sb, int sub, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
-        const uint32_t *cw = reinterpret_cast<const uint32_t *>(sb + sub * kCodeBytes1);
+        const char *cb = sb + sub * kCodeBytes1;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int tk = 32 * ks + 8 * g;  // first of the lane's 8 tokens
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                const uint32_t w = cw[(tk / TPW) * D + 16 * n + l16];
-                tv.cw[ks][n] = BITS == 2 ? (w >> (2 * (tk % TPW))) & 0xffffu : w;
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(cb) + (tk / TPW) * D + (NT * l16) % D;
+            uint32_t w[NT];
+            if constexpr (NT == 8) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(src);
+                const uint4 b = *reinterpret_cast<const uint4 *>(src + 4);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+                w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+            } else {
+                const uint4 a = *reinterpret_cast<const uint4 *>(src);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
             }
+            // 2-bit words hold 16 tokens: the lane's 8 are the odd or even
+            // byte of each half
+            const int sh = BITS == 2 ? 8 * (g & 1) : 0;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) tv.cw[ks][n] = w[n] >> sh;
         }
         const SZT *sp = reinterpret_cast<const SZT *>(sb + kCodeBytes + sub * kSzBytes1);
         const SZT *zp = reinterpret_cast<const SZT *>(sb + kCodeBytes + kSzBytes + sub * kSzBytes1);
@@ -819,95 +856,103 @@ struct VGil {
         }
     }
     __device__ static void init(State &st) {
+        st.bias = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int r = 0; r < kMfmaRows; ++r)
 #pragma unroll
-            for (int k = 0; k < NG; ++k) st.ws[r][k] = st.zs[r][k] = 0.f;
-    }
-    // codes of 8 tokens -> bf16 128 + code, tokens in element order
-    __device__ static bf16x8 expand(uint32_t x) {
-        uint32_t d[4];
-        if constexpr (BITS == 2) {  // code i at bits 2i of the low 16 bits
-            const uint32_t y1 = x >> 2, y2 = x >> 4, y3 = x >> 6;
-            d[0] = __builtin_amdgcn_perm(y1, x, 0x0c040c00u);
-            d[1] = __builtin_amdgcn_perm(y3, y2, 0x0c040c00u);
-            d[2] = __builtin_amdgcn_perm(y1, x, 0x0c050c01u);
-            d[3] = __builtin_amdgcn_perm(y3, y2, 0x0c050c01u);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) d[j] = (d[j] & 0x00030003u) | 0x43004300u;
-        } else {  // code i at bits 4i
-            const uint32_t y1 = x >> 4;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                d[j] = (__builtin_amdgcn_perm(y1, x, 0x0c040c00u | (uint32_t)(j << 16) | (uint32_t)j) &
-                        0x000f000fu) | 0x43004300u;
-        }
-        return __builtin_bit_cast(bf16x8, make_uint4(d[0], d[1], d[2], d[3]));
+            for (int k = 0; k < NG; ++k) st.zs[r][k] = 0.f;
     }
     __device__ static void pv(Tile &tv, State &st, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
-                              const float (&corr)[kMfmaRows], int n_in, _Float16 *pw16, int lane) {
+                              const float (&corr)[kMfmaRows], bool rescale, int n_in, _Float16 *pw16,
+                              int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         uint16_t *pw = reinterpret_cast<uint16_t *>(pw16);
-        // tokens past the split end carry p = 0 but possibly unwritten s, z
-        const bool ok = lane < n_in;
+        float s[NG], z[NG];
 #pragma unroll
-        for (int r = 0; r < kMfmaRows; ++r) {
+        for (int k = 0; k < NG; ++k) {
+            s[k] = tv.s[k];
+            z[k] = tv.z[k];
+        }
+        if (n_in < kWave) {  // tokens past the split end: p = 0, s and z possibly unwritten
+            const bool ok = lane < n_in;
 #pragma unroll
             for (int k = 0; k < NG; ++k) {
-                const float w = ok ? p[r] * tv.s[k] : 0.f;
-                const uint32_t hb = bf16_bits_rn(w);
-                const float hf = __uint_as_float(hb << 16);
-                const uint32_t lb = bf16_bits_rn(w - hf);
-                pw[(8 * k + r) * kWave + lane] = (uint16_t)hb;
-                pw[(8 * k + 4 + r) * kWave + lane] = (uint16_t)lb;
-                st.ws[r][k] = fmaf(st.ws[r][k], corr[r], hf + __uint_as_float(lb << 16));
-                st.zs[r][k] = fmaf(st.zs[r][k], corr[r], ok ? p[r] * tv.z[k] : 0.f);
+                s[k] = ok ? s[k] : 0.f;
+                z[k] = ok ? z[k] : 0.f;
             }
         }
-        wave_lds_sync();
-        if (corr[0] != 1.f || corr[1] != 1.f || corr[2] != 1.f || corr[3] != 1.f) {
+        if (rescale) {  // some row's running max moved
             const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
 #pragma unroll
             for (int n = 0; n < NT; ++n) acc[n] *= cv4;
+            // bias rows 4*(lane/16) + i belong to query row i
+            st.bias *= cv4;
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r)
+#pragma unroll
+                for (int k = 0; k < NG; ++k) st.zs[r][k] *= corr[r];
         }
+        // w = p * s as bf16 hi + lo (both round to nearest), two rows at a time
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; r += 2) {
+                const float w0 = p[r] * s[k], w1 = p[r + 1] * s[k];
+                const uint32_t hi = bf16x2_rn(w0, w1);
+                const float l0 = w0 - __uint_as_float(hi << 16);
+                const float l1 = w1 - __uint_as_float(hi & 0xffff0000u);
+                const uint32_t lo = bf16x2_rn(l0, l1);
+                pw[(8 * k + r) * kPStride + lane] = (uint16_t)hi;
+                pw[(8 * k + r + 1) * kPStride + lane] = (uint16_t)(hi >> 16);
+                pw[(8 * k + 4 + r) * kPStride + lane] = (uint16_t)lo;
+                pw[(8 * k + 4 + r + 1) * kPStride + lane] = (uint16_t)(lo >> 16);
+                st.zs[r][k] = fmaf(p[r], z[k], st.zs[r][k]);
+                st.zs[r + 1][k] = fmaf(p[r + 1], z[k], st.zs[r + 1][k]);
+            }
+        }
+        wave_lds_sync();
+        const uint32_t cm = opaque_u32(kCodeMask), cbias = opaque_u32(kBias);
+        const bf16x8 b128 = __builtin_bit_cast(bf16x8, make_uint4(cbias, cbias, cbias, cbias));
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             // A lane l: row l%16, tokens 32ks + 8(l/16) .. +7
-            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(pw + l16 * kWave + 32 * ks + 8 * g);
+            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(pw + l16 * kPStride + 32 * ks + 8 * g);
+            st.bias = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b128, st.bias, 0, 0, 0);
 #pragma unroll
-            for (int n = 0; n < NT; ++n)
-                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, expand(tv.cw[ks][n]), acc[n], 0, 0, 0);
+            for (int n = 0; n < NT; ++n) {
+                const uint32_t y = tv.cw[ks][n];
+                uint32_t d4[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) d4[j] = ((y >> (BITS * j)) & cm) | cbias;
+                const bf16x8 bop = __builtin_bit_cast(bf16x8, make_uint4(d4[0], d4[1], d4[2], d4[3]));
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop, acc[n], 0, 0, 0);
+            }
         }
         wave_lds_sync();
     }
-    // n-tile n (group k = 16n / kGroup) sits in lanes 32k .. 32k+31: lanes
-    // 32k + 0..15 the hi rows, 32k + 16..31 the lo rows.  The hi part also
-    // carries sum p*z - 128 * sum w of its (row, group).
+    // acc[n] of lane l holds rows 4(l/16) .. +3 of dim 8(l%16) + n; rows
+    // 8g + 0..3 (hi) and 8g + 4..7 (lo) are group g's, so lanes 32g .. 32g+31
+    // carry the dims of group g.  The hi part also carries sum p*z of its
+    // (row, group).
     __device__ static void to_lds(const f32x4 (&acc)[NT], const State &st, float *wa, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
-        float corr_rg[kMfmaRows][NG];
+        float zsum[NG][kMfmaRows];
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
-            float wsum[kMfmaRows], zsum[kMfmaRows], wv_[kMfmaRows], zv_[kMfmaRows];
+            float zv_[kMfmaRows];
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r) zv_[r] = st.zs[r][k];
+            wave_sum4_dpp(zv_, zsum[k]);
+        }
+        const int k = (NT * l16) / kGroup;  // the group of this lane's dims
+        if ((g >> 1) == k) {
+            const int hl = g & 1;
 #pragma unroll
             for (int r = 0; r < kMfmaRows; ++r) {
-                wv_[r] = st.ws[r][k];
-                zv_[r] = st.zs[r][k];
-            }
-            wave_sum4_dpp(wv_, wsum);
-            wave_sum4_dpp(zv_, zsum);
+                const float zr = hl != 0 ? 0.f : (NG == 2 && k == 1 ? zsum[NG - 1][r] : zsum[0][r]);
 #pragma unroll
-            for (int r = 0; r < kMfmaRows; ++r) corr_rg[r][k] = zsum[r] - 128.f * wsum[r];
-        }
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            const int k = (16 * n) / kGroup;
-            if ((g >> 1) == k) {
-                const int hl = g & 1;
-#pragma unroll
-                for (int r = 0; r < kMfmaRows; ++r)
-                    wa[(hl * kMfmaRows + r) * D + 16 * n + l16] =
-                        acc[n][r] + (hl == 0 ? corr_rg[r][k] : 0.f);
+                for (int n = 0; n < NT; ++n)
+                    wa[(hl * kMfmaRows + r) * D + NT * l16 + n] = acc[n][r] - st.bias[r] + zr;
             }
         }
     }
@@ -926,12 +971,14 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     extern __shared__ __align__(16) float4 smem4[];
     char *smem = reinterpret_cast<char *>(smem4);
     float4 *lut4 = smem4;                                              // [NB][256]
-    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][kPRows][64]
+    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + K::kLut);     // [NC][kPRows][kPStride]
     volatile lds_t<int> *ready = to_lds<int>(smem + K::kLut + K::kPst);
     volatile lds_t<int> *done = ready + K::kFlagWords;               // [slot][sub]
     volatile lds_t<int> *cbar = done + K::kFlagWords * K::kSub;  // compute-wave barrier counter
     char *ring = smem + K::kRing;
-    const lds_t<f32x4> *lut_l = to_lds<f32x4>(smem4);  // 16-byte LUT reads
+    // 16-byte LUT reads through the LDS object itself (an address-space
+    // cast the compiler folds to the constant LDS address)
+    const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)smem4;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -1024,15 +1071,22 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         const int64_t gr = (int64_t)rg * R + r;
         lim[r] = !row_ok(r) ? -1 : (c.causal ? c.q_offset + (gr % c.t_q) : INT64_MAX);
     }
+    // last token every live row sees
+    int64_t lim_min = INT64_MAX;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (row_ok(r)) lim_min = min(lim_min, lim[r]);
     f32x4 acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     typename VF::State vst;
     VF::init(vst);
+    // running maxima; a row past the last query row gets a maximum no score
+    // reaches, so its probabilities are 0 and it never forces a reduction
     float m[R], lsum[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        m[r] = -1e30f;
+        m[r] = row_ok(r) ? -1e30f : 3e38f;
         lsum[r] = 0.f;
     }
 
@@ -1207,7 +1261,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         }
         compute_barrier(3);  // LUT complete
 
-        _Float16 *pw = pst + wv * VF::kPRows * kWave;
+        _Float16 *pw = pst + wv * VF::kPRows * kPStride;
         for (int u = wv; u < n_units; u += NC) {
             const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
             const int slot = j % K::kSlots;
@@ -1236,11 +1290,6 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             const int64_t t0 = t_beg + (int64_t)u * kWave;
             // tokens of this tile still inside the split (wave-uniform, 1..64)
             const int n_in = (int)min(t_end - t0, (int64_t)kWave);
-            const bool kok = lane < n_in;
-            int lim_rel[R];  // last visible lane per row (causal), wave-uniform
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                lim_rel[r] = (int)max(min(lim[r] - t0, (int64_t)kWave), (int64_t)-1);
             // scores from the LUT: every block's read in flight at once, then
             // a tree sum (one LDS round trip)
             f32x4 e[NB];
@@ -1250,24 +1299,50 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             for (int w = 1; w < NB; w *= 2)
 #pragma unroll
                 for (int b = 0; b < NB; b += 2 * w) e[b] += e[b + w];
-            // masked lanes add -inf (their index rows are real, clamped
-            // tokens, so the sums are finite); an additive mask keeps the LUT
-            // sums unconditional
             float sc[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) sc[r] = e[0][r] + ((kok && lane <= lim_rel[r]) ? 0.f : -INFINITY);
-            float tmax[R];
-            wave_max4_dpp(sc, tmax);  // the four rows' reductions interleaved
-            float corr[R], p[R];
+            for (int r = 0; r < R; ++r) sc[r] = e[0][r];
+            // A whole tile every row sees (no causal cut, no split end) whose
+            // scores all stay at or below the rows' running maxima keeps the
+            // maxima: no reduction, no rescale.  Otherwise masked lanes add
+            // -inf (their index rows are real, clamped tokens, so the sums
+            // are finite) and the maxima are reduced over the wave.
+            bool moved = true;
+            if (n_in == kWave && t0 + (kWave - 1) <= lim_min) {
+                uint64_t above = 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const float mn = fmaxf(m[r], tmax[r]);
-                corr[r] = fast_exp2(m[r] - mn);
-                p[r] = fast_exp2(sc[r] - mn);
-                lsum[r] = fmaf(lsum[r], corr[r], p[r]);
-                m[r] = mn;
+                for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r]);
+                moved = above != 0;
+            } else {
+                const bool kok = lane < n_in;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    // last visible lane of row r (causal), wave-uniform
+                    const int lim_rel = (int)max(min(lim[r] - t0, (int64_t)kWave), (int64_t)-1);
+                    sc[r] += (kok && lane <= lim_rel) ? 0.f : -INFINITY;
+                }
             }
-            VF::pv(tv, vst, acc, p, corr, n_in, pw, lane);
+            float corr[R], p[R];
+            if (moved) {
+                float tmax[R];
+                wave_max4_dpp(sc, tmax);  // the four rows' reductions interleaved
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float mn = fmaxf(m[r], tmax[r]);
+                    corr[r] = fast_exp2(m[r] - mn);
+                    p[r] = fast_exp2(sc[r] - mn);
+                    lsum[r] = fmaf(lsum[r], corr[r], p[r]);
+                    m[r] = mn;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    corr[r] = 1.f;
+                    p[r] = fast_exp2(sc[r] - m[r]);
+                    lsum[r] += p[r];
+                }
+            }
+            VF::pv(tv, vst, acc, p, corr, moved, n_in, pw, lane);
         }
     }
     __syncthreads();  // every tile consumed; the ring is free for the merge

@@ -149,7 +149,9 @@ __global__ void __launch_bounds__(256)
         if (t < 0 || t >= n_t) continue;
         const uint32_t w = packed[(b * p_sb + h * p_sh + t * p_st) * nw + dd / vpw];
         const uint32_t code = (w >> ((dd % vpw) * bits)) & mask;
-        word = (word & ~(mask << (i * bits))) | (code << (i * bits));
+        // token i of the word: bits*(i/2) in the low half for even i, +16 for odd i
+        const int pos = bits * (i >> 1) + 16 * (i & 1);
+        word = (word & ~(mask << pos)) | (code << pos);
     }
     *wp = word;
 }

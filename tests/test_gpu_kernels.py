@@ -414,6 +414,16 @@ def test_pack_grouped_il_roundtrip(bits, d, t_kv, cap):
     back = _hip.grouped_il_to_packed(il, bits).view(torch.int32).cpu().numpy()
     assert np.array_equal(back[:, :, :t_kv], packed[:, :, :t_kv].cpu().numpy())
     assert not back[:, :, t_kv:].any()
+    # the word layout itself: token i of a word at bit bits*(i//2) + 16*(i%2)
+    tpw, mask = 32 // bits, (1 << bits) - 1
+    pk = packed[:, :, :t_kv].cpu().numpy().view(np.uint32).astype(np.uint64)
+    dims = np.arange(d)
+    codes = (pk[..., dims // tpw] >> ((dims % tpw) * bits).astype(np.uint64)) & mask  # (B,H,T,D)
+    want = np.zeros((2, 3, cap // tpw, d), dtype=np.uint64)
+    for i in range(tpw):
+        tok = np.arange(i, t_kv, tpw)
+        want[:, :, tok // tpw, :] |= codes[:, :, tok, :] << np.uint64(bits * (i // 2) + 16 * (i % 2))
+    assert np.array_equal(il.cpu().numpy().view(np.uint32).astype(np.uint64), want)
 
 
 @pytest.mark.parametrize(
