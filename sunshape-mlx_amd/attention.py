@@ -63,6 +63,12 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
             out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
                                        codebook=codec.kernel_codebook(), **kw)
             codec.last_score_backend = "hip_fused_mfma"
+        elif ops["kind"] == "grouped_il":
+            out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.centroids, ops["idx"],
+                                              ops["codes_il"], ops["scales"], ops["zeros"],
+                                              ops["bits"], ops["group_size"],
+                                              codebook=codec.kernel_codebook(), **kw)
+            codec.last_score_backend = "hip_fused_mfma_dequant"
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
                                            ops["packed"], ops["scales"], ops["zeros"],

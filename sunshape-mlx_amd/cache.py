@@ -84,6 +84,14 @@ def _il8_ok(codec: SunShapeBlockCodec, head_dim: int, dtype: torch.dtype) -> boo
             and codec.n_blocks * 8 == head_dim and codec.n_centroids <= 256)
 
 
+def _grouped_il_ok(codec: SunShapeBlockCodec, head_dim: int, bits: int, group_size: int) -> bool:
+    """Whether grouped value codes go token-interleaved (the layout of the
+    matrix-core grouped decode kernel)."""
+    return (bits in (2, 4) and head_dim in (64, 128) and group_size in (head_dim, head_dim // 2)
+            and codec.block_dim == 8 and codec.n_blocks * 8 == head_dim
+            and codec.n_centroids <= 256)
+
+
 class SunShapeKVCache:
     """Block-VQ keys + fp16 values; drop-in for mlx-lm's KVCache protocol
     (reference cache.py:59-336)."""
@@ -306,6 +314,12 @@ class HybridSunShapeKVCache:
         self._values_fp16: torch.Tensor | None = None
         self._value_n_groups = 0
         self._compressed_capacity = 0
+        # grouped codes held token-interleaved ((B, H, cap*bits/32, D) words)
+        # for the matrix-core decode kernel; packed rows otherwise
+        self._values_il: torch.Tensor | None = None
+        self._grouped_il = (self.value_backend == "grouped" and
+                            _grouped_il_ok(codec, self.head_dim, self.value_bits or 0,
+                                           self.value_group_size))
 
     @property
     def offset(self) -> int:
@@ -323,8 +337,13 @@ class HybridSunShapeKVCache:
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
             self._value_n_groups = gc.n_groups
-            self._values_packed = _grow(self._values_packed, (b_, h_, cap, gc.packed_dim),
-                                        torch.int32, device, keep)
+            if self._grouped_il:
+                tpw = 32 // gc.bits
+                self._values_il = _grow(self._values_il, (b_, h_, cap // tpw, self.head_dim),
+                                        torch.int32, device, (keep + tpw - 1) // tpw)
+            else:
+                self._values_packed = _grow(self._values_packed, (b_, h_, cap, gc.packed_dim),
+                                            torch.int32, device, keep)
             self._value_scales = _grow(self._value_scales, (b_, h_, cap, gc.n_groups),
                                        self.value_scale_dtype, device, keep)
             self._value_zeros = _grow(self._value_zeros, (b_, h_, cap, gc.n_groups),
@@ -361,10 +380,21 @@ class HybridSunShapeKVCache:
         _encode_into(self.codec, kf, self._key_indices[:, :, c0:c1])
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
-            _hip.quantize_values_grouped(vf, gc.bits, gc.group_size,
-                                         self._values_packed[:, :, c0:c1],
-                                         self._value_scales[:, :, c0:c1],
-                                         self._value_zeros[:, :, c0:c1])
+            if self._grouped_il:
+                # quantise into contiguous rows, then interleave the codes
+                h_ = self.n_kv_heads
+                rows = torch.empty((b_, h_, n, gc.packed_dim), dtype=torch.int32, device=dev)
+                sc = torch.empty((b_, h_, n, gc.n_groups), dtype=self.value_scale_dtype, device=dev)
+                zr = torch.empty_like(sc)
+                _hip.quantize_values_grouped(vf, gc.bits, gc.group_size, rows, sc, zr)
+                self._value_scales[:, :, c0:c1] = sc
+                self._value_zeros[:, :, c0:c1] = zr
+                _hip.pack_grouped_il(rows, gc.bits, self._values_il, c0)
+            else:
+                _hip.quantize_values_grouped(vf, gc.bits, gc.group_size,
+                                             self._values_packed[:, :, c0:c1],
+                                             self._value_scales[:, :, c0:c1],
+                                             self._value_zeros[:, :, c0:c1])
             self.last_value_quant_backend = "hip"
         elif self.value_backend == "turboquant":
             tc = self._value_codec_impl
@@ -434,9 +464,9 @@ class HybridSunShapeKVCache:
         tc_ = self._compressed_offset
         if tc_ == 0:
             return None
-        if self.value_backend == "grouped" and self._values_packed is not None:
+        if self.value_backend == "grouped" and self.values_packed_raw is not None:
             gc = self._value_codec_impl
-            v = _hip.dequantize_values_grouped(self._values_packed[:, :, :tc_].view(torch.uint32),
+            v = _hip.dequantize_values_grouped(self.values_packed_raw,
                                                self._value_scales[:, :, :tc_],
                                                self._value_zeros[:, :, :tc_], self.head_dim,
                                                gc.bits, gc.group_size)
@@ -493,8 +523,15 @@ class HybridSunShapeKVCache:
 
     @property
     def values_packed_raw(self):
-        if self.value_backend != "grouped" or self._values_packed is None \
-                or self._compressed_offset == 0:
+        """Grouped codes of the compressed tokens as reference packed rows
+        (B, H, T, packed_dim) uint32 (converted from the interleaved words
+        when the cache holds those)."""
+        if self.value_backend != "grouped" or self._compressed_offset == 0:
+            return None
+        if self._values_il is not None:
+            return _hip.grouped_il_to_packed(self._values_il, self.value_bits,
+                                             self._compressed_offset).contiguous()
+        if self._values_packed is None:
             return None
         return self._values_packed[:, :, :self._compressed_offset].view(torch.uint32)
 
@@ -518,6 +555,11 @@ class HybridSunShapeKVCache:
         compressed or the value backend has no fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
             return None
+        if self.value_backend == "grouped" and self._values_il is not None:
+            gc = self._value_codec_impl
+            return {"kind": "grouped_il", "idx": self._key_indices, "codes_il": self._values_il,
+                    "scales": self._value_scales, "zeros": self._value_zeros,
+                    "bits": gc.bits, "group_size": gc.group_size}
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
             return {"kind": "grouped", "idx": self._key_indices,
@@ -531,8 +573,8 @@ class HybridSunShapeKVCache:
     @property
     def can_fuse_value_dequant(self) -> bool:
         return (self.value_backend == "grouped" and self._compressed_offset > 0
-                and self._values_packed is not None and self._value_scales is not None
-                and self._value_zeros is not None)
+                and (self._values_packed is not None or self._values_il is not None)
+                and self._value_scales is not None and self._value_zeros is not None)
 
     # ------------------------------------------------------------ metrics
     @property

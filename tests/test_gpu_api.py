@@ -142,7 +142,7 @@ def test_hybrid_grouped_fused_and_buffered(scale_dtype):
     assert cache.buffer_offset == 0 and cache.compressed_offset == 300
     q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
     out = S.sunshape_sdpa(q, cache, 0.088)
-    assert codec.last_score_backend == "hip_fused_dequant"
+    assert codec.last_score_backend == "hip_fused_mfma_dequant"
     packed = cache.values_packed_raw.cpu().numpy()
     sc = cache.value_scales_raw.float().cpu().numpy()
     zr = cache.value_zeros_raw.float().cpu().numpy()
@@ -166,6 +166,43 @@ def test_hybrid_grouped_fused_and_buffered(scale_dtype):
     # trim removes buffered tokens first (reference cache.py:954-963)
     cache2.trim(130)
     assert cache2.buffer_offset == 0 and cache2.compressed_offset == 170
+
+
+@pytest.mark.parametrize("bits,group", [(2, 64), (4, 128), (4, 64), (2, 128)])
+def test_hybrid_grouped_interleaved_appends_and_trim(bits, group):
+    """Grouped codes kept token-interleaved: appends of ragged sizes (flushes
+    that start and end inside a code word), a trim into compressed storage
+    and a re-append read back as the oracle's quantisation bit for bit, and
+    the fused decode over them matches the oracle."""
+    codec = make_codec(21)
+    b, hq, hkv, d = 2, 8, 2, 128
+    k, v = kv(22 + bits, b, hkv, 420, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=bits,
+                              value_group_size=group, buffer_size=0)
+    pos = 0
+    for n in (37, 1, 90, 200):
+        cache.update_and_fetch(k[:, :, pos:pos + n], v[:, :, pos:pos + n])
+        pos += n
+    cache.trim(50)
+    pos -= 50
+    cache.update_and_fetch(k[:, :, pos:pos + 92], v[:, :, pos:pos + 92])
+    pos += 92
+    assert cache.compressed_offset == pos == 370 and cache.buffer_offset == 0
+    vf = v[:, :, :pos].float().cpu().numpy().reshape(-1, d)
+    packed_ref, sc_ref, zr_ref, _ = O.quantize_values(vf, bits, group)
+    got = cache.values_packed_raw.cpu().numpy().reshape(-1, packed_ref.shape[-1])
+    assert np.array_equal(got.view(np.uint32), packed_ref.view(np.uint32))
+    assert np.array_equal(cache.value_scales_raw.cpu().numpy().reshape(-1, d // group), sc_ref)
+    assert np.array_equal(cache.value_zeros_raw.cpu().numpy().reshape(-1, d // group), zr_ref)
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    assert codec.last_score_backend == "hip_fused_mfma_dequant"
+    vals = O.dequantize_values(packed_ref, sc_ref, zr_ref, d, bits, group).reshape(b, hkv, pos, d)
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the dequantised values the two-pass path reads agree with the oracle's
+    assert rel_err(cache.values.float().cpu().numpy(), vals) <= 1e-3
 
 
 def test_hybrid_fp16_and_sunshape_value_backends():
