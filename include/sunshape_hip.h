@@ -234,6 +234,31 @@ int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t batch, int n_q
                               size_t workspace_bytes, int n_splits, void *stream);
 
 /*
+ * ss_decode_attn_grouped_il over a hybrid cache: the compressed tokens
+ * 0 .. t_kv-1 plus the cache's recent-token buffer of t_buf tokens at
+ * positions t_kv .. t_kv+t_buf-1, in one online softmax.  Buffer keys and
+ * values are in the original (unpermuted, unrotated) basis, buf_dtype
+ * (SS_F16/SS_BF16/SS_F32) elements at k_buf/v_buf[b*buf_sb + h*buf_sh +
+ * t*buf_st + d] (strides in elements, multiples of 8; k_buf 16-byte
+ * aligned); their scores are fp32 dot products with round_to(q_dtype,
+ * q*scale).  No reference counterpart: the reference's fused path takes
+ * only an empty buffer and otherwise falls back to the two-pass path
+ * (attention.py:238); the result equals that two-pass path's
+ * (attention.py:307-350) within the decode tolerance.
+ */
+int ss_decode_attn_grouped_il_hybrid(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                     int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                     const int32_t *perm, const void *codebook, int n_blocks,
+                                     int n_centroids, const uint8_t *idx,
+                                     const uint32_t *codes_il, const void *scales,
+                                     const void *zeros, int sz_dtype, int bits, int group_size,
+                                     int64_t cap, int64_t t_kv, const void *k_buf,
+                                     const void *v_buf, int buf_dtype, int64_t buf_sb,
+                                     int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal,
+                                     int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                     size_t workspace_bytes, int n_splits, void *stream);
+
+/*
  * Repack grouped codes (pack_indices words, one row of packed_dim words per
  * token: word w of token (b,h,t) at packed[b*p_sb + h*p_sh + t*p_st + w]) into
  * the interleaved layout of ss_decode_attn_grouped_il at cache positions

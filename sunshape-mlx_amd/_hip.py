@@ -82,6 +82,11 @@ _SIGNATURES = {
                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                          _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
                                          _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_attn_grouped_il_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                                   _c_void_p, _i64, _i64, _c_void_p]),
     "ss_quantize_values_grouped": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -437,12 +442,17 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
                            scales: torch.Tensor, zeros: torch.Tensor, bits: int, group_size: int,
                            t_kv: int, causal: bool = False, q_offset: int = 0,
                            out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                           n_splits: int = 0, codebook: torch.Tensor | None = None) -> torch.Tensor:
+                           n_splits: int = 0, codebook: torch.Tensor | None = None,
+                           buf_keys: torch.Tensor | None = None,
+                           buf_values: torch.Tensor | None = None,
+                           buf_len: int = 0) -> torch.Tensor:
     """Fused decode (matrix-core LUT and P.V) over grouped values whose codes
     are token-interleaved: ``codes_il`` (B, Hkv, cap * bits / 32, D) 32-bit
     words (see :func:`pack_grouped_il`), ``scales``/``zeros`` (B, Hkv, cap, D
     / group_size).  ``codebook`` is :func:`codebook_f16x2` of ``centroids``
-    (prepared here when None)."""
+    (prepared here when None).  A hybrid cache's recent tokens
+    ``buf_keys``/``buf_values`` (B, Hkv, >= buf_len, D, original basis)
+    join the same softmax as positions t_kv .. t_kv + buf_len - 1."""
     _check_decode_common(q, idx, centroids, perm)
     require_gpu(codes_il, scales, zeros)
     b_, hq, tq, d = q.shape
@@ -464,12 +474,26 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
-    check(load_library().ss_decode_attn_grouped_il(
-        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
-        nb, nc, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros), dtype_code(scales.dtype),
-        int(bits), int(group_size), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
-        dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
-        stream_handle(q.device)))
+    common = (ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm),
+              ptr(codebook), nb, nc, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros),
+              dtype_code(scales.dtype), int(bits), int(group_size), cap, int(t_kv))
+    tail = (ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
+            int(n_splits), stream_handle(q.device))
+    if buf_keys is None or buf_len == 0:
+        check(load_library().ss_decode_attn_grouped_il(
+            *common, int(bool(causal)), int(q_offset), *tail))
+        return out
+    require_gpu(buf_keys, buf_values)
+    if buf_keys.dim() != 4 or buf_keys.shape[:2] != (b_, hkv) or buf_keys.shape[3] != d or \
+            buf_values.shape != buf_keys.shape or buf_values.stride() != buf_keys.stride() or \
+            buf_keys.stride(-1) != 1 or buf_keys.dtype != buf_values.dtype or \
+            buf_keys.shape[2] < buf_len:
+        raise ValueError("buf_keys/buf_values must be matching (B, n_kv_heads, >= buf_len, D) "
+                         "views with unit last stride")
+    check(load_library().ss_decode_attn_grouped_il_hybrid(
+        *common, ptr(buf_keys), ptr(buf_values), dtype_code(buf_keys.dtype), buf_keys.stride(0),
+        buf_keys.stride(1), buf_keys.stride(2), int(buf_len), int(bool(causal)), int(q_offset),
+        *tail))
     return out
 
 

@@ -55,6 +55,11 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     if ops is None:
         return None
     codec = cache.codec
+    buffered = cache.buffer_offset if isinstance(cache, HybridSunShapeKVCache) else 0
+    # the buffer joins the fused softmax only on the grouped interleaved
+    # kernel, whose buffer scores use the unrotated query
+    if buffered and (ops["kind"] != "grouped_il" or codec.use_rotation):
+        return None
     q, kscale, perm = _kernel_query(codec, queries, scale)
     t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
     kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
@@ -67,8 +72,11 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
             out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.centroids, ops["idx"],
                                               ops["codes_il"], ops["scales"], ops["zeros"],
                                               ops["bits"], ops["group_size"],
-                                              codebook=codec.kernel_codebook(), **kw)
-            codec.last_score_backend = "hip_fused_mfma_dequant"
+                                              codebook=codec.kernel_codebook(),
+                                              buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
+                                              buf_len=buffered, **kw)
+            codec.last_score_backend = ("hip_fused_mfma_dequant_buffer" if buffered
+                                        else "hip_fused_mfma_dequant")
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
                                            ops["packed"], ops["scales"], ops["zeros"],
@@ -163,9 +171,10 @@ def sunshape_sdpa(queries: torch.Tensor, cache: SunShapeKVCache | HybridSunShape
     _hip.require_gpu(queries)
     is_hybrid = isinstance(cache, HybridSunShapeKVCache)
     use_causal = isinstance(mask, str) and mask == "causal"
-    buffered = cache.buffer_offset if is_hybrid else 0
     compressed = cache.compressed_offset if is_hybrid else t_kv
-    can_fuse = buffered == 0 and (mask is None or use_causal) and compressed > 0
+    # a non-empty hybrid buffer stays on the fused path where the kernel
+    # takes it (_fused returns None otherwise)
+    can_fuse = (mask is None or use_causal) and compressed > 0
     if can_fuse:
         out = _fused(cache, queries, scale, use_causal, t_kv - tq if use_causal else 0)
         if out is not None:

@@ -559,7 +559,8 @@ class HybridSunShapeKVCache:
             gc = self._value_codec_impl
             return {"kind": "grouped_il", "idx": self._key_indices, "codes_il": self._values_il,
                     "scales": self._value_scales, "zeros": self._value_zeros,
-                    "bits": gc.bits, "group_size": gc.group_size}
+                    "bits": gc.bits, "group_size": gc.group_size,
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
             return {"kind": "grouped", "idx": self._key_indices,

@@ -538,7 +538,10 @@ struct WsCfg {
     static constexpr int kFlagWords = 16;
     // ready[slot], done[slot][sub], barrier counter
     static constexpr int kFlags = (kFlagWords * (1 + kSub) + 4) * 4;
-    static constexpr int kRing = kLut + kPst + kFlags;
+    // the split's share of a hybrid cache's token buffer: its query copy,
+    // then its (m[R], l[R], acc[R][D]) partial
+    static constexpr int kBufPart = VF::kHybridBuffer ? (2 * kMfmaRows + kMfmaRows * D) * 4 : 0;
+    static constexpr int kRing = kLut + kPst + kFlags + kBufPart;
     static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
     static constexpr int kSlots = kSlotsFit < VF::kMaxSlots ? kSlotsFit : VF::kMaxSlots;
     static constexpr int kLoadsPerTile = VF::kLoadsV + kLoadsI;
@@ -592,6 +595,7 @@ struct VIl8 {
     };
     static constexpr int NT = D / 16;
     static constexpr int kSub = SUB;
+    static constexpr bool kHybridBuffer = false;  // fp16 caches have no token buffer
     static constexpr int kTileV1 = kWave * D * 2;  // one 64-token sub-tile
     static constexpr int kTileV = kSub * kTileV1;
     static constexpr int kLoadsV = kTileV / 1024;
@@ -735,6 +739,13 @@ struct VGil {
     struct Args {
         const uint32_t *codes;
         const SZT *scales, *zeros;
+        // recent-token buffer of a hybrid cache: keys and values in the
+        // original basis, buf_dtype elements at b*buf_sb + h*buf_sh +
+        // t*buf_st (+ dim), attended as positions t_kv .. t_kv + t_buf - 1
+        // after the compressed tokens (t_buf = 0: none)
+        const void *kbuf, *vbuf;
+        int buf_dtype;
+        int64_t buf_sb, buf_sh, buf_st, t_buf;
     };
     static constexpr int NT = D / 16;
     static constexpr int TPW = 32 / BITS;                 // tokens per code word
@@ -745,6 +756,7 @@ struct VGil {
     static constexpr int kSub = 8192 / kCodeBytes1 < 4 ? 8192 / kCodeBytes1 : 4;
     static constexpr int kCodeBytes = kSub * kCodeBytes1;
     static constexpr int kSzBytes = kSub * kSzBytes1;
+    static constexpr bool kHybridBuffer = true;  // hybrid caches: recent tokens join the pass
     static constexpr int kSzLoads = (kSzBytes + 1023) / 1024;
     static constexpr int kTileV = kCodeBytes + 2 * kSzBytes;
     static constexpr int kLoadsV = kCodeBytes / 1024 + 2 * kSzLoads;
@@ -979,6 +991,9 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     volatile lds_t<int> *done = ready + K::kFlagWords;               // [slot][sub]
     volatile lds_t<int> *cbar = done + K::kFlagWords * K::kSub;  // compute-wave barrier counter
     char *ring = smem + K::kRing;
+    // buffer partial: m [R], l [R], acc [R][D] (acc holds the query copy
+    // until the share is done)
+    float *bpart = reinterpret_cast<float *>(smem + K::kLut + K::kPst + K::kFlags);
     // 16-byte LUT reads through the LDS object itself (an address-space
     // cast the compiler folds to the constant LDS address)
     const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)smem4;
@@ -1009,6 +1024,13 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     const uint8_t *idx_head = c.idx + bh * c.cap * NB;
     const int64_t t_last = max(t_end - 1, (int64_t)0);
     const int g = lane >> 4, l16 = lane & 15;
+    // this split's share of the token buffer (wave-uniform)
+    int64_t t_buf = 0;
+    if constexpr (VF::kHybridBuffer) t_buf = va.t_buf;
+    const int64_t bshare = (t_buf + c.n_splits - 1) / c.n_splits;
+    const int64_t bj0 = min((int64_t)split * bshare, t_buf);
+    const int64_t bj1 = min(bj0 + bshare, t_buf);
+    const bool has_buf = VF::kHybridBuffer && bj1 > bj0;
 
     // Barrier that orders LDS only: a wave's outstanding global loads (the
     // loader's tile copies) do not have to land first, which __syncthreads'
@@ -1098,6 +1120,93 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     // after a join inherits the loader's outstanding tile copies as pending
     // loads, and the loader streams from the start without waiting for the
     // LUT.
+    // Hybrid caches: compute wave 0 attends this split's share of the token
+    // buffer (positions t_kv + bj0 ..) with fp32 dot products against the
+    // unpermuted scaled query, before its tiles; the share's (m, l, acc)
+    // join the workgroup combine as one more wave.  Keys in log2 units, as
+    // the LUT.
+    auto buffer_share = [&](const auto &bv) {
+        constexpr int DL = D / kWave;  // value dims per lane
+        float bm[R], bl[R], ba[R][DL];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            bm[r] = -1e30f;
+            bl[r] = 0.f;
+#pragma unroll
+            for (int k = 0; k < DL; ++k) ba[r][k] = 0.f;
+        }
+        const float *bq = bpart + 2 * R;  // [R][D] query copy
+        f32x4 *pb = reinterpret_cast<f32x4 *>(pst);  // wave 0's P staging: p of 64 tokens
+        const int64_t head = bb * bv.buf_sb + kvh * bv.buf_sh;
+        for (int64_t j0 = bj0; j0 < bj1; j0 += kWave) {
+            const int64_t j = j0 + lane;
+            const bool ok = j < bj1;
+            const int64_t ko = head + (ok ? j : j0) * bv.buf_st;
+            float sc[R] = {};
+            for (int d0 = 0; d0 < D; d0 += 8) {
+                float kx[8];
+                if (bv.buf_dtype == SS_F16) {
+                    unpack16<__half>(*reinterpret_cast<const uint4 *>(
+                                         static_cast<const __half *>(bv.kbuf) + ko + d0),
+                                     kx);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) kx[i] = load_as_f32(bv.kbuf, bv.buf_dtype, ko + d0 + i);
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) sc[r] = fmaf(bq[r * D + d0 + i], kx[i], sc[r]);
+            }
+            const int64_t pos = c.t_kv + j;
+#pragma unroll
+            for (int r = 0; r < R; ++r) sc[r] = (ok && pos <= lim[r]) ? sc[r] * kLog2e : -INFINITY;
+            float tmax[R], p[R], corr[R];
+            wave_max4_dpp(sc, tmax);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float mn = fmaxf(bm[r], tmax[r]);
+                corr[r] = fast_exp2(bm[r] - mn);
+                p[r] = fast_exp2(sc[r] - mn);
+                bm[r] = mn;
+            }
+            float ps[R];
+            wave_sum4_dpp(p, ps);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                bl[r] = fmaf(bl[r], corr[r], ps[r]);
+#pragma unroll
+                for (int k = 0; k < DL; ++k) ba[r][k] *= corr[r];
+            }
+            pb[lane] = f32x4{p[0], p[1], p[2], p[3]};
+            wave_lds_sync();
+            const int nj = (int)min(bj1 - j0, (int64_t)kWave);
+            for (int jj = 0; jj < nj; ++jj) {
+                const f32x4 pj = pb[jj];
+                const int64_t vo = head + (j0 + jj) * bv.buf_st + lane;
+#pragma unroll
+                for (int k = 0; k < DL; ++k) {
+                    const float v = load_as_f32(bv.vbuf, bv.buf_dtype, vo + k * kWave);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) ba[r][k] = fmaf(pj[r], v, ba[r][k]);
+                }
+            }
+            wave_lds_sync();
+        }
+        // the query copy is no longer read: the partial takes its place
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                bpart[r] = bm[r];
+                bpart[R + r] = bl[r];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int k = 0; k < DL; ++k) bpart[2 * R + r * D + k * kWave + lane] = ba[r][k];
+    };
+
     // the slot of ring tile j has been copied out of by all consumers of
     // tile j - kSlots
     auto slot_free = [&](int j) {
@@ -1184,6 +1293,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                         qv = __uint_as_float(h << 16);
                 }
                 qraw[e] = round_to(c.q_dtype, qv * c.scale);
+                if (has_buf) bpart[2 * R + e] = qraw[e];
             }
         }
         compute_barrier(1);  // raw query staged
@@ -1263,6 +1373,8 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 build(std::true_type{});
         }
         compute_barrier(3);  // LUT complete
+        if constexpr (VF::kHybridBuffer)
+            if (wv == 0 && has_buf) buffer_share(va);
 
         _Float16 *pw = pst + wv * VF::kPRows * kPStride;
         for (int u = wv; u < n_units; u += NC) {
@@ -1391,6 +1503,14 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         M = -1e30f;
 #pragma unroll
         for (int w = 0; w < NC; ++w) M = fmaxf(M, mw[w]);
+        float mb = -1e30f, lb = 0.f;
+        f32x4 ab = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (has_buf) {  // the split's share of the token buffer
+            mb = bpart[r];
+            lb = bpart[R + r];
+            ab = *reinterpret_cast<const f32x4 *>(bpart + 2 * R + r * D + d0);
+            M = fmaxf(M, mb);
+        }
         L = 0.f;
         A = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1398,6 +1518,11 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             const float f = fast_exp2(mw[w] - M);
             L = fmaf(lw[w], f, L);
             A += (hi[w] + lo[w]) * f;
+        }
+        if (has_buf) {
+            const float f = fast_exp2(mb - M);
+            L = fmaf(lb, f, L);
+            A += ab * f;
         }
     };
     const int S = c.n_splits;
@@ -2037,16 +2162,16 @@ extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int
     return launch_mfma<64, VIl8<64>>(c, VIl8<64>::Args{v8}, s, st);
 }
 
-extern "C" int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t batch, int n_q_heads,
-                                         int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                         const int32_t *perm, const void *codebook, int n_blocks,
-                                         int n_centroids, const uint8_t *idx,
-                                         const uint32_t *codes_il, const void *scales,
-                                         const void *zeros, int sz_dtype, int bits,
-                                         int group_size, int64_t cap, int64_t t_kv, int causal,
-                                         int64_t q_offset, void *out, int out_dtype,
-                                         void *workspace, size_t workspace_bytes, int n_splits,
-                                         void *stream) {
+static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                           int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                           const int32_t *perm, const void *codebook, int n_blocks,
+                           int n_centroids, const uint8_t *idx, const uint32_t *codes_il,
+                           const void *scales, const void *zeros, int sz_dtype, int bits,
+                           int group_size, int64_t cap, int64_t t_kv, int causal,
+                           int64_t q_offset, void *out, int out_dtype, void *workspace,
+                           size_t workspace_bytes, int n_splits, const void *k_buf,
+                           const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+                           int64_t buf_st, int64_t t_buf, void *stream) {
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
@@ -2073,15 +2198,27 @@ extern "C" int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t bat
     c.codebook = static_cast<const uint4 *>(codebook);
     c.codebook_mul = reinterpret_cast<const float *>(
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+    if (t_buf > 0) {
+        SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
+        SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
+                   "buffer dtype must be f16, bf16 or f32");
+        SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
+                   "buffer strides must be non-negative, token stride >= head_dim");
+        SS_REQUIRE(((uintptr_t)k_buf % 16) == 0 && buf_sb % 8 == 0 && buf_sh % 8 == 0 &&
+                       buf_st % 8 == 0,
+                   "buffer keys must be 16-byte aligned with strides a multiple of 8 elements");
+    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int ng = head_dim / group_size;
 #define SS_GIL(DD, BB, NGG, SZT)                                                              \
     {                                                                                         \
         using VF = VGil<DD, BB, NGG, SZT>;                                                    \
-        return launch_mfma<DD, VF>(c,                                                         \
-                                   typename VF::Args{codes_il, static_cast<const SZT *>(scales), \
-                                                     static_cast<const SZT *>(zeros)},        \
-                                   s, st);                                                    \
+        return launch_mfma<DD, VF>(                                                           \
+            c,                                                                                \
+            typename VF::Args{codes_il, static_cast<const SZT *>(scales),                     \
+                              static_cast<const SZT *>(zeros), k_buf, v_buf, buf_dtype,       \
+                              buf_sb, buf_sh, buf_st, t_buf > 0 ? t_buf : 0},                 \
+            s, st);                                                                           \
     }
 #define SS_GIL_SZ(DD, BB, NGG)                     \
     {                                              \
@@ -2102,4 +2239,36 @@ extern "C" int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t bat
 #undef SS_GIL_NG
 #undef SS_GIL_SZ
 #undef SS_GIL
+}
+
+extern "C" int ss_decode_attn_grouped_il(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                         int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                         const int32_t *perm, const void *codebook, int n_blocks,
+                                         int n_centroids, const uint8_t *idx,
+                                         const uint32_t *codes_il, const void *scales,
+                                         const void *zeros, int sz_dtype, int bits,
+                                         int group_size, int64_t cap, int64_t t_kv, int causal,
+                                         int64_t q_offset, void *out, int out_dtype,
+                                         void *workspace, size_t workspace_bytes, int n_splits,
+                                         void *stream) {
+    return grouped_il_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                           codebook, n_blocks, n_centroids, idx, codes_il, scales, zeros, sz_dtype,
+                           bits, group_size, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                           workspace_bytes, n_splits, nullptr, nullptr, SS_F16, 0, 0, 0, 0, stream);
+}
+
+extern "C" int ss_decode_attn_grouped_il_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint32_t *codes_il, const void *scales,
+    const void *zeros, int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv,
+    const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
+    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    SS_REQUIRE(t_buf >= 0, "negative buffer length");
+    return grouped_il_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                           codebook, n_blocks, n_centroids, idx, codes_il, scales, zeros, sz_dtype,
+                           bits, group_size, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                           workspace_bytes, n_splits, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
+                           buf_st, t_buf, stream);
 }

@@ -157,7 +157,7 @@ def test_hybrid_grouped_fused_and_buffered(scale_dtype):
     cache2.update_and_fetch(k, v)
     assert cache2.buffer_offset == 128 and cache2.compressed_offset == 172
     out2 = S.sunshape_sdpa(q, cache2, 0.088)
-    assert codec.last_score_backend == "hip"
+    assert codec.last_score_backend == "hip_fused_mfma_dequant_buffer"
     vals_all = np.concatenate([vals[:, :, :172], v[:, :, 172:].float().cpu().numpy()], axis=2)
     ref2 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                            codec.centroids.cpu().numpy(), cache2.key_indices.cpu().numpy(),
@@ -203,6 +203,51 @@ def test_hybrid_grouped_interleaved_appends_and_trim(bits, group):
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
     # the dequantised values the two-pass path reads agree with the oracle's
     assert rel_err(cache.values.float().cpu().numpy(), vals) <= 1e-3
+
+
+@pytest.mark.parametrize("buf,t_total,tq,causal,dtype", [
+    (128, 700, 1, False, torch.float16),    # decode step, default buffer
+    (200, 1000, 1, False, torch.float16),   # buffer shares longer than one 64-token chunk
+    (64, 300, 5, True, torch.float16),      # prefill rows, causal across the buffer
+    (128, 450, 1, False, torch.bfloat16),   # bf16 buffer
+    (128, 140, 1, False, torch.float32),    # mostly buffer, f32
+])
+def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
+    """Hybrid grouped caches with buffered tokens stay on the fused kernel;
+    the result equals the reference's two-pass path over the same cache."""
+    codec = make_codec(31)
+    b, hq, hkv, d = 2, 8, 2, 128
+    k, v = kv(32 + buf, b, hkv, t_total, d, dtype=dtype)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2,
+                              buffer_size=buf, dtype=dtype)
+    pos = 0
+    for n in (t_total - 37, 30, 7):
+        cache.update_and_fetch(k[:, :, pos:pos + n], v[:, :, pos:pos + n])
+        pos += n
+    assert cache.buffer_offset > 0 and cache.compressed_offset > 0
+    q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
+    mask = "causal" if causal else None
+    out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
+    assert codec.last_score_backend == "hip_fused_mfma_dequant_buffer"
+    tc = cache.compressed_offset
+    vals = cache.values.float().cpu().numpy()  # compressed values dequantised, then buffer
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
+                          cache.buffer_keys.float().cpu().numpy(), vals, mask=mask)
+    assert vals.shape[2] == tc + cache.buffer_offset
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+
+def test_hybrid_buffer_with_rotated_codec_takes_two_pass():
+    codec = make_codec(33, mode="rotated")
+    b, hq, hkv, d = 1, 4, 1, 128
+    k, v = kv(34, b, hkv, 300, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    assert codec.last_score_backend == "hip"
+    assert torch.isfinite(out).all()
 
 
 def test_hybrid_fp16_and_sunshape_value_backends():
