@@ -52,9 +52,10 @@ def parse_args():
                    help="budget for the CPU baseline (0 disables it)")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                           "decode_fp16v_t32k_traffic.json"))
-    p.add_argument("--workload", choices=("metric", "hybrid"), default="metric",
+    p.add_argument("--workload", choices=("metric", "hybrid", "encode"), default="metric",
                    help="metric: the BASELINE metric decode (fp16 values, B=1); hybrid: config 4 "
-                        "(B=8, 2-bit grouped values, g=64, fp16 scale/zero)")
+                        "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
+                        "(65,536 fp16 keys block-VQ encoded)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a plain device copy of MB megabytes --steps times (the "
                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -211,6 +212,82 @@ def run_hybrid(args) -> int:
     return 0
 
 
+VALU_FP32_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMD x 16 lanes x 2 flops x 2.4 GHz, no packed fp32
+
+
+def run_encode(args) -> int:
+    """Config 3: 65,536 fp16 keys (8 x 8192 x 128, per-dim scale
+    exp(U[ln .25, ln 8]), seed 3) block-VQ encoded against a codebook fit on
+    4096 draws of the same distribution; one ss_encode_blockvq launch per step.
+    VALU-bound (direct-form distances, N*16*256*8*3 flops); GB/s reported
+    beside TFLOP/s."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    lib = hip.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n_h, n_t, d, nb = 8, 8192, 128, 16
+    rng = np.random.default_rng(3)
+    s = np.exp(rng.uniform(np.log(0.25), np.log(8.0), d)).astype(np.float32)
+    k_cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)
+    q_cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)
+    t0 = time.time()
+    codec = pkg.codec.SunShapeBlockCodec(d, device=dev).fit(q_cal, k_cal, kmeans_iters=15, seed=3)
+    log(f"codec fit {time.time() - t0:.1f}s")
+    keys0 = torch.from_numpy((rng.standard_normal((n_h, n_t, d)) * s).astype(np.float16)).to(dev)
+    per_copy = keys0.numel() * 2
+    n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
+    keys = [keys0] + [keys0.clone() for _ in range(n_copies - 1)]
+    outs = [torch.empty((n_h, n_t, nb), dtype=torch.uint8, device=dev) for _ in range(n_copies)]
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.ss_encode_blockvq
+    argv = [(keys[i].data_ptr(), hip.SS_F16, 1, n_h, n_t, n_h * n_t * d, n_t * d, d, d,
+             codec.permutation.data_ptr(), codec.centroids.data_ptr(), nb, 256, 8,
+             outs[i].data_ptr(), n_h * n_t * nb, n_t * nb, nb, stream) for i in range(n_copies)]
+    us, per = time_launches(fn, argv, args.steps, args.warmup, hip)
+    n_tok = n_h * n_t
+    nbytes = n_tok * d * 2 + n_tok * nb
+    flops = n_tok * nb * 256 * 8 * 3
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tflops = flops / (us * 1e-6) / 1e12
+    log(f"encode: {us:.2f} us/step, {gbs:.1f} GB/s, {tflops:.1f} TFLOP/s")
+    check = None
+    if args.cpu_seconds > 0:  # bit-exact check of 512 tokens against the oracle
+        from oracle import sunshape_oracle as O
+
+        hip.check(fn(*argv[0]))
+        torch.cuda.synchronize()
+        kk = keys0[0, :512].float().cpu().numpy()
+        ref, near = O.encode_blockvq_c(kk, codec.centroids.cpu().numpy(),
+                                       codec.permutation.cpu().numpy())
+        got = outs[0][0, :512].cpu().numpy()
+        check = int(((got != ref) & ~near).sum())
+    line = {
+        "metric": "block-VQ encode throughput (config 3)", "value": round(n_tok / (us * 1e-6), 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us * 1e-3, 6), "us_per_step": round(us, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "encode 8 x 8192 fp16 keys, D=128, 16 blocks x 256 centroids "
+                               "(codec fit on 4096 draws), direct-form L2 argmin",
+                   "tokens": n_tok, "cache_copies": n_copies, "bytes_per_step": nbytes,
+                   "flops_per_step": flops},
+        "roofline": {"bound": "valu", "achieved": round(tflops, 2), "peak": VALU_FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / VALU_FP32_PEAK_TFLOPS, 4),
+                     "traffic": None, "hbm_gbs": round(gbs, 2)},
+        "per_launch_us": {"mean": round(float(np.mean(per)), 3),
+                          "median": round(float(np.median(per)), 3)},
+        "check_mismatches_vs_oracle_512_tokens": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -222,6 +299,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, args.steps)
     if args.workload == "hybrid":
         return run_hybrid(args)
+    if args.workload == "encode":
+        return run_encode(args)
 
     import numpy as np
     import torch
