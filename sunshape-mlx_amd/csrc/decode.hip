@@ -907,12 +907,25 @@ struct VGil {
 #pragma unroll
                 for (int k = 0; k < NG; ++k) st.zs[r][k] *= corr[r];
         }
+        // 2-bit codes: operand dwords 1 and 2 of a lane's 8 tokens take
+        // their codes in place, at mantissa bits 2-3 and 4-5 (128 + 4c and
+        // 128 + 16c, still exact); those tokens' weights carry the inverse
+        // power of two, so every product is unchanged
+        float sw[NG];
+#pragma unroll
+        for (int k = 0; k < NG; ++k) sw[k] = s[k];
+        if constexpr (BITS == 2) {
+            const int jt = (lane >> 1) & 3;  // dword of this token within its operand
+            const float f = jt == 1 ? 0.25f : (jt == 2 ? 0.0625f : 1.f);
+#pragma unroll
+            for (int k = 0; k < NG; ++k) sw[k] = s[k] * f;
+        }
         // w = p * s as bf16 hi + lo (both round to nearest), two rows at a time
 #pragma unroll
         for (int k = 0; k < NG; ++k) {
 #pragma unroll
             for (int r = 0; r < kMfmaRows; r += 2) {
-                const float w0 = p[r] * s[k], w1 = p[r + 1] * s[k];
+                const float w0 = p[r] * sw[k], w1 = p[r + 1] * sw[k];
                 const uint32_t hi = bf16x2_rn(w0, w1);
                 const float l0 = w0 - __uint_as_float(hi << 16);
                 const float l1 = w1 - __uint_as_float(hi & 0xffff0000u);
@@ -927,6 +940,7 @@ struct VGil {
         }
         wave_lds_sync();
         const uint32_t cm = opaque_u32(kCodeMask), cbias = opaque_u32(kBias);
+        const uint32_t cm2 = opaque_u32(kCodeMask << 2), cm4 = opaque_u32(kCodeMask << 4);
         const bf16x8 b128 = __builtin_bit_cast(bf16x8, make_uint4(cbias, cbias, cbias, cbias));
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -937,8 +951,15 @@ struct VGil {
             for (int n = 0; n < NT; ++n) {
                 const uint32_t y = tv.cw[ks][n];
                 uint32_t d4[4];
+                if constexpr (BITS == 2) {
+                    d4[0] = (y & cm) | cbias;
+                    d4[1] = (y & cm2) | cbias;
+                    d4[2] = (y & cm4) | cbias;
+                    d4[3] = ((y >> 6) & cm) | cbias;
+                } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) d4[j] = ((y >> (BITS * j)) & cm) | cbias;
+                    for (int j = 0; j < 4; ++j) d4[j] = ((y >> (BITS * j)) & cm) | cbias;
+                }
                 const bf16x8 bop = __builtin_bit_cast(bf16x8, make_uint4(d4[0], d4[1], d4[2], d4[3]));
                 acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop, acc[n], 0, 0, 0);
             }
