@@ -550,11 +550,18 @@ struct WsCfg {
     // one slot more than the tiles in flight, so a refill never waits on the
     // slowest consumer of the tile it replaces
     static constexpr int kDepth = kSlots - 1 < kDepthVm ? kSlots - 1 : kDepthVm;
-    static constexpr int kLds = kRing + kSlots * kSlot;
+    // wave-private rings (VF::kPrivateRing): no loader wave; every compute
+    // wave copies its own 64-token units, kPrivSlots of them at a time
+    static constexpr bool kPriv = VF::kPrivateRing;
+    static constexpr int kPrivSlots = 2;
+    static constexpr int kWaves = kPriv ? NC : NC + 1;
+    static constexpr int kRingBytes = kPriv ? NC * kPrivSlots * kSlot : kSlots * kSlot;
+    static constexpr int kLds = kRing + kRingBytes;
     static_assert(kSlots >= 2 && kSlots <= kFlagWords, "ring slots");
     static_assert(kTileV % 16 == 0, "16-byte tile sections");
     static_assert(kLds <= kLdsMax, "LDS budget");
-    static_assert(NC * kMfmaRows * (2 * D + 2) * 4 <= kSlots * kSlot, "merge scratch");
+    static_assert(!kPriv || kSub == 1, "private rings hold single 64-token units");
+    static_assert(NC * kMfmaRows * (2 * D + 2) * 4 <= kRingBytes, "merge scratch");
     static_assert(2 * kMfmaRows * D * 4 <= kPst, "query staging");
     // LUT build on the matrix cores: tiles of 4 blocks x 16 centroids, each
     // compute wave owns kLutTiles of them, all in one 4-block group
@@ -596,6 +603,7 @@ struct VIl8 {
     static constexpr int NT = D / 16;
     static constexpr int kSub = SUB;
     static constexpr bool kHybridBuffer = false;  // fp16 caches have no token buffer
+    static constexpr bool kPrivateRing = false;   // 17 KB units: one loader wave, shared ring
     static constexpr int kTileV1 = kWave * D * 2;  // one 64-token sub-tile
     static constexpr int kTileV = kSub * kTileV1;
     static constexpr int kLoadsV = kTileV / 1024;
@@ -751,9 +759,16 @@ struct VGil {
     static constexpr int TPW = 32 / BITS;                 // tokens per code word
     static constexpr int kCodeBytes1 = kWave * D * BITS / 8;  // codes of a 64-token sub-tile
     static constexpr int kSzBytes1 = kWave * NG * (int)sizeof(SZT);
-    // ring tiles of up to 256 tokens (about 8 KB of codes): small per-stream
-    // requests of 64-token tiles leave HBM far from its streaming rate
-    static constexpr int kSub = 8192 / kCodeBytes1 < 4 ? 8192 / kCodeBytes1 : 4;
+    // every compute wave copies its own 64-token units (3.5 KB at 2-bit)
+    // into two private LDS slots: no loader wave and no hand-off flags.
+    // Measured as a bare stream over the config-4 buffers, 8 waves x 2 units
+    // in flight reach 6.3 TB/s (a single loader wave with 64-token tiles
+    // reached 3.7 TB/s, with 256-token tiles 5.9 TB/s), and the compute
+    // waves no longer wait on flags in a congested LDS.
+    // (4-bit codes at D = 128, 5.5 KB units, do not fit 16 private slots
+    // beside the LUT: they keep the loader wave and 128-token ring tiles)
+    static constexpr bool kPrivateRing = kCodeBytes1 <= 2048;
+    static constexpr int kSub = kPrivateRing ? 1 : (8192 / kCodeBytes1 < 4 ? 8192 / kCodeBytes1 : 4);
     static constexpr int kCodeBytes = kSub * kCodeBytes1;
     static constexpr int kSzBytes = kSub * kSzBytes1;
     static constexpr bool kHybridBuffer = true;  // hybrid caches: recent tokens join the pass
@@ -995,13 +1010,13 @@ struct VGil {
 };
 
 template <int D, int NC, class VF>
-__global__ void __launch_bounds__((NC + 1) * kWave)
+__global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     decode_attn_mfma_kernel(DecodeCommon c, typename VF::Args va) {
     using K = WsCfg<D, NC, VF>;
     constexpr int R = kMfmaRows;
     constexpr int NB = K::kNB;
     constexpr int NT = D / 16;  // MFMA N-tiles (16 dims each)
-    constexpr int THREADS = (NC + 1) * kWave;
+    constexpr int THREADS = K::kWaves * kWave;
     constexpr int LPT = K::kLoadsPerTile;
 
     extern __shared__ __align__(16) float4 smem4[];
@@ -1023,7 +1038,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     const int lane = tid & (kWave - 1);
     // wave-uniform (scalar) wave index: all tile control flow stays scalar
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool loader = wv == NC;
+    const bool loader = !K::kPriv && wv == NC;
     const int col = blockIdx.y;
     const int split = blockIdx.x;
     const int rg = col % c.n_rg;
@@ -1080,9 +1095,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     // the value format's copies, then the index rows (contiguous, chunks past
     // the one holding the split's last token clamp to it), so every load
     // stays in bounds.  The LDS destination of lane l is M0 + 16*l.
-    auto issue = [&](int j) {
-        const uint32_t sb = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring)) +
-                            (uint32_t)((j % K::kSlots) * K::kSlot);
+    auto issue_at = [&](int j, uint32_t sb) {
         const int64_t t0 = t_beg + (int64_t)j * K::kSub * kWave;
         VF::issue(va, bh, c.cap, t0, t_last, sb, lane);
         const uint8_t *ip = idx_head + t0 * NB;
@@ -1098,6 +1111,11 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             }
         }
     };
+    const uint32_t ring_l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+    auto issue = [&](int j) { issue_at(j, ring_l + (uint32_t)((j % K::kSlots) * K::kSlot)); };
+    // private rings: slot s of this wave
+    auto priv_slot = [&](int s) { return (uint32_t)((wv * K::kPrivSlots + s) * K::kSlot); };
+    int nq = 0;  // private rings: units this wave has issued
     int issued = 0, landed = 0;
 
     // Prologue.  The compute waves' small loads (query element, permutation
@@ -1296,6 +1314,11 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
                 cb_lo[t] = cp[kWave];
             }
         }
+        if constexpr (K::kPriv) {
+            // this wave's first units (u = wv + k*NC) stream in while the LUT is built
+            for (; nq < K::kPrivSlots && wv + nq * NC < n_units; ++nq)
+                issue_at(wv + nq * NC, ring_l + priv_slot(nq));
+        }
         lds_barrier();  // small loads issued, flags initialised
         // query elements: round_to(q_dtype, q * scale) (attention.py:208)
 #pragma unroll
@@ -1398,18 +1421,24 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             if (wv == 0 && has_buf) buffer_share(va);
 
         _Float16 *pw = pst + wv * VF::kPRows * kPStride;
-        for (int u = wv; u < n_units; u += NC) {
+        for (int u = wv, uk = 0; u < n_units; u += NC, ++uk) {
             const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
-            const int slot = j % K::kSlots;
-            int spins = 0;
-            while (ready[slot] != j) {
-                __builtin_amdgcn_s_sleep(1);
-                if (++spins > kSpinLimit) break;
+            const int slot = K::kPriv ? uk % K::kPrivSlots : j % K::kSlots;
+            if constexpr (K::kPriv) {
+                // this wave's copies of unit u have landed (its later units
+                // stay in flight)
+                wait_oldest_tile<LPT, K::kPrivSlots>(nq - uk);
+            } else {
+                int spins = 0;
+                while (ready[slot] != j) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > kSpinLimit) break;
+                }
             }
             asm volatile("" ::: "memory");
             // copy the tile (index rows and values) into registers and
             // release the slot at once
-            const char *sb = ring + slot * K::kSlot;
+            const char *sb = K::kPriv ? ring + priv_slot(slot) : ring + slot * K::kSlot;
             const char *ib = sb + K::kTileV + sub * K::kTileI1;
             IdxRow<NB> ir;
             if constexpr (NB == 16) {
@@ -1422,7 +1451,15 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
             typename VF::Tile tv;
             VF::copy(tv, sb, sub, lane);
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if (lane == 0) done[slot * K::kSub + sub] = j;
+            if constexpr (K::kPriv) {
+                // the slot's data is in registers: refill it with this wave's next unit
+                if (wv + nq * NC < n_units) {
+                    issue_at(wv + nq * NC, ring_l + priv_slot(nq % K::kPrivSlots));
+                    ++nq;
+                }
+            } else {
+                if (lane == 0) done[slot * K::kSub + sub] = j;
+            }
             const int64_t t0 = t_beg + (int64_t)u * kWave;
             // tokens of this tile still inside the split (wave-uniform, 1..64)
             const int n_in = (int)min(t_end - t0, (int64_t)kWave);
@@ -1604,9 +1641,9 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
     u32x2 *mlb = reinterpret_cast<u32x2 *>(lrow + 64);
     const int chunk_off = ((kMaxSplits * R + 64) * 4 + S * R * 8 + 1023) & ~1023;
     char *chunk = ring + chunk_off;
-    const int cs_max = (K::kSlots * K::kSlot - chunk_off) / (R * D * 4);
+    const int cs_max = (K::kRingBytes - chunk_off) / (R * D * 4);
     static_assert(((kMaxSplits * R + 64) * 4 + kMaxSplits * R * 8 + 1023) / 1024 * 1024 +
-                          2 * R * D * 4 <= K::kSlots * K::kSlot,
+                          2 * R * D * 4 <= K::kRingBytes,
                   "merge LDS");
     static_assert((R * D * 4) % 1024 == 0, "merge chunk granularity");
     const uint32_t chunk_l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(chunk));
@@ -1615,7 +1652,7 @@ __global__ void __launch_bounds__((NC + 1) * kWave)
         const char *src = reinterpret_cast<const char *>(c.part_acc) +
                           (((int64_t)col * S + s0) * R) * D * 4;
         const int n_kb = cs * R * D * 4 / 1024;
-        for (int kb = wv; kb < n_kb; kb += NC + 1)
+        for (int kb = wv; kb < n_kb; kb += K::kWaves)
             __builtin_amdgcn_global_load_lds(src + kb * 1024 + lane * 16,
                                              reinterpret_cast<lds_t<void> *>(chunk_l + kb * 1024), 16,
                                              0, kCpolSc1);
@@ -1856,7 +1893,7 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3((NC + 1) * kWave), K::kLds, st, c, va);
+    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(K::kWaves * kWave), K::kLds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
     if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
     return launch_merge<D>(c, s, st);
