@@ -292,7 +292,7 @@ def main() -> int:
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the decode path shards by KV head with no exchange; see DESIGN.md)",
+              "(the decode path would shard by KV head, with no exchange between GPUs)",
               file=sys.stderr)
         return 2
     if args.calibrate_copy:
