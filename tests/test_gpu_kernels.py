@@ -395,8 +395,9 @@ def grouped_case(seed, b, hkv, t_kv, d, bits, group, cap, sz_dtype=torch.float16
     packed = torch.zeros((b, hkv, cap, nw), dtype=torch.int32, device=DEV)
     sc = torch.zeros((b, hkv, cap, ng), dtype=sz_dtype, device=DEV)
     ze = torch.zeros((b, hkv, cap, ng), dtype=sz_dtype, device=DEV)
-    _hip.quantize_values_grouped(t(v), bits, group, packed[:, :, :t_kv], sc[:, :, :t_kv],
-                                 ze[:, :, :t_kv])
+    if t_kv:
+        _hip.quantize_values_grouped(t(v), bits, group, packed[:, :, :t_kv], sc[:, :, :t_kv],
+                                     ze[:, :, :t_kv])
     il = torch.zeros((b, hkv, cap * bits // 32, d), dtype=torch.int32, device=DEV)
     cuts = sorted({0, t_kv, min(t_kv, 7), min(t_kv, t_kv // 2 + 3)})
     for a0, a1 in zip(cuts[:-1], cuts[1:]):
@@ -462,3 +463,35 @@ def test_decode_grouped_il_matches_oracle(b, hq, hkv, d, t_kv, t_q, bits, group,
     assert np.isfinite(got).all()
     assert rel_err(got, ref) <= REL_TOL
 
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,bits,group,splits", [
+    (1, 8, 2, 128, 0, 40, 2, 64, 0),      # buffer only (no compressed tokens)
+    (2, 8, 2, 64, 333, 70, 2, 32, 0),     # head_dim 64, buffer longer than one chunk
+    (1, 4, 1, 128, 200, 5, 4, 128, 7),    # 4-bit (loader-wave ring), 7 splits sharing 5 tokens
+])
+def test_decode_grouped_il_hybrid_buffer(b, hq, hkv, d, t_kv, t_buf, bits, group, splits):
+    """ss_decode_attn_grouped_il_hybrid: compressed tokens plus a token-major
+    fp16 buffer in one softmax equals the two-pass oracle over both."""
+    cap = max(((t_kv + 15) // 16) * 16, 16)
+    cents, perm, idx, _, q = decode_case(t_kv + t_buf + bits, b, hq, hkv, d, t_kv, 1, cap)
+    _, packed, sc, ze, il = grouped_case(t_kv + 5, b, hkv, t_kv, d, bits, group, cap)
+    rng = np.random.default_rng(t_buf)
+    kb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    scale = 1.0 / np.sqrt(d)
+    out = _hip.decode_attn_grouped_il(t(q), scale, t(perm), t(cents), t(idx), il, sc, ze, bits,
+                                      group, t_kv, out_dtype=torch.float32, n_splits=splits,
+                                      buf_keys=t(kb), buf_values=t(vb), buf_len=t_buf)
+    torch.cuda.synchronize()
+    vals = np.zeros((b, hkv, t_kv + t_buf, d), np.float64)
+    for bi in range(b):
+        for hi in range(hkv):
+            if t_kv:
+                vals[bi, hi, :t_kv] = O.dequantize_values(
+                    packed[bi, hi, :t_kv].cpu().numpy().view(np.uint32),
+                    sc[bi, hi, :t_kv].float().cpu().numpy(), ze[bi, hi, :t_kv].float().cpu().numpy(),
+                    d, bits, group)
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
