@@ -211,6 +211,33 @@ int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_he
                            void *stream);
 
 /*
+ * As ss_decode_attn_dense with TurboQuant values (reference
+ * value_codecs.py:136-177): token t's value is norms[t] * (levels[code_t] @
+ * rotation), code_t its packed BITS-bit codes.  The reference has no fused
+ * kernel for these values: it dequantises the whole cache every step and
+ * runs the two-pass SDPA (cache.py:774-784, attention.py:307-350), which this
+ * replaces.  Accumulation runs in the rotated basis; the rotation is applied
+ * once per output row (a second launch on the same stream).
+ *   packed    uint32 [batch][n_kv_heads][cap][packed_dim], pack_indices layout
+ *   norms     float  [batch][n_kv_heads][cap]
+ *   levels    HOST float[2^bits], ascending Lloyd-Max levels x 1/sqrt(head_dim)
+ *   rotation  float  [head_dim][head_dim] (device), unit = rotated @ rotation
+ *   workspace ss_decode_turboquant_workspace_bytes(...) bytes, 256-byte
+ *             aligned, always required (it holds the rotated-basis rows)
+ */
+int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                              int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                              const int32_t *perm, const float *centroids, int n_blocks,
+                              int n_centroids, const uint8_t *idx, const uint32_t *packed,
+                              const float *norms, const float *levels, const float *rotation,
+                              int bits, int64_t cap, int64_t t_kv, int causal,
+                              int64_t q_offset, void *out, int out_dtype, void *workspace,
+                              size_t workspace_bytes, int n_splits, void *stream);
+size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
+                                            int64_t t_q, int head_dim, int64_t t_kv,
+                                            int n_splits);
+
+/*
  * As ss_decode_attn_grouped with the 2- or 4-bit codes held in a token-
  * interleaved layout and the codebook prepared by ss_codebook_f16x2.  Code of
  * token t, dimension d of a (batch, KV head) row is the bits-wide field at

@@ -78,6 +78,11 @@ _SIGNATURES = {
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
                                       _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_attn_turboquant": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                         _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
+                                         _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _int,
+                                         _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
     "ss_decode_attn_grouped_il": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                          _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
@@ -432,6 +437,49 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(scales), ptr(zeros), dtype_code(scales.dtype),
         int(bits), int(group_size), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
+        dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
+        stream_handle(q.device)))
+    return out
+
+
+def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                           centroids: torch.Tensor, idx: torch.Tensor, packed: torch.Tensor,
+                           norms: torch.Tensor, levels, rotation: torch.Tensor, bits: int,
+                           t_kv: int, causal: bool = False, q_offset: int = 0,
+                           out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                           n_splits: int = 0) -> torch.Tensor:
+    """Fused decode over TurboQuant values: ``packed`` (B, Hkv, cap,
+    packed_dim) codes, ``norms`` (B, Hkv, cap) float32, ``levels`` the 2^bits
+    scaled Lloyd-Max levels (any float sequence; copied to the kernel
+    arguments), ``rotation`` (D, D) float32 with ``value = norm * (levels[code]
+    @ rotation)``."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(packed, norms, rotation)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if packed.dim() != 4 or not packed.is_contiguous() or packed.shape[:3] != idx.shape[:3] or \
+            packed.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("packed must be contiguous 32-bit words (B, n_kv_heads, cap, packed_dim)")
+    if norms.dtype != torch.float32 or not norms.is_contiguous() or \
+            tuple(norms.shape) != tuple(idx.shape[:3]):
+        raise ValueError("norms must be contiguous float32 (B, n_kv_heads, cap)")
+    if rotation.dtype != torch.float32 or not rotation.is_contiguous() or \
+            tuple(rotation.shape) != (d, d):
+        raise ValueError(f"rotation must be contiguous float32 ({d}, {d})")
+    lv = [float(x) for x in (levels.tolist() if isinstance(levels, torch.Tensor) else levels)]
+    if len(lv) != (1 << int(bits)):
+        raise ValueError(f"{1 << int(bits)} levels expected for {bits}-bit codes, got {len(lv)}")
+    lv_host = (ctypes.c_float * len(lv))(*lv)
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    lib = load_library()
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), int(n_splits))
+    ws = decode_workspace(q.device, ws_bytes)
+    check(lib.ss_decode_attn_turboquant(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        nb, nc, ptr(idx), ptr(packed), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
+        ptr(rotation), int(bits), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
         dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
         stream_handle(q.device)))
     return out

@@ -177,6 +177,60 @@ struct VGrouped {
     }
 };
 
+// TurboQuant values (reference value_codecs.py:136-177): per token a norm n
+// and one BITS-bit Lloyd-Max code per dim of the rotated unit vector, packed
+// like the grouped codes (kernels.py pack_indices).  A lane's dims decode to
+// n * level[code], the value in the rotated basis: since every token shares
+// the rotation R, sum_t p_t (n_t C[idx_t] @ R) = (sum_t p_t n_t C[idx_t]) @ R,
+// so the kernel accumulates in the rotated basis and R is applied once per
+// output row after the split merge (rotate_rows_kernel).
+template <int D, int BITS>
+struct VTurbo {
+    static constexpr int VPW = 32 / BITS;
+    static constexpr int NW = (D + VPW - 1) / VPW;
+    static constexpr int DPL = VPW;
+    static constexpr int LPT = pow2_ceil(NW);
+    static constexpr int TPI = kWave / LPT;
+    static constexpr int ITERS = kWave / TPI;
+    static_assert(LPT <= kWave, "packed row too wide");
+    struct Args {
+        const uint32_t *packed;  // [rows][NW] words
+        const float *norms;      // [rows]
+        float lv[16];            // the 2^BITS levels, ascending (already x 1/sqrt(D))
+    };
+    struct Raw {
+        uint32_t w;
+        float n;
+    };
+    __device__ static __forceinline__ Raw load(const Args &a, int64_t row, int lt, bool ok) {
+        Raw r{0u, 0.f};
+        if (ok && lt < NW) {
+            r.w = a.packed[row * NW + lt];
+            r.n = a.norms[row];
+        }
+        return r;
+    }
+    // level[code] by a select tree on the code bits (levels are uniform
+    // kernel arguments; no indexed register access)
+    __device__ static __forceinline__ float level(const Args &a, uint32_t code) {
+        float v[1 << BITS];
+#pragma unroll
+        for (int i = 0; i < (1 << BITS); ++i) v[i] = a.lv[i];
+#pragma unroll
+        for (int b = 0; b < BITS; ++b) {
+            const bool bit = (code >> b) & 1u;
+#pragma unroll
+            for (int i = 0; i < (1 << (BITS - 1 - b)); ++i) v[i] = bit ? v[2 * i + 1] : v[2 * i];
+        }
+        return v[0];
+    }
+    __device__ static __forceinline__ void decode(const Args &a, const Raw &r, int, float *x) {
+#pragma unroll
+        for (int k = 0; k < VPW; ++k)
+            x[k] = r.n * level(a, (r.w >> (k * BITS)) & ((1u << BITS) - 1u));
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Index rows: NB bytes per token (16 for head_dim 128, 8 for 64).
 // ---------------------------------------------------------------------------
@@ -1793,6 +1847,40 @@ __global__ void __launch_bounds__(kDecodeThreads) decode_merge_kernel(DecodeComm
     }
 }
 
+// out[row] = y[row] @ rot for fp32 rows of the rotated basis (the TurboQuant
+// dequant's `unit = C[idx] @ R`, value_codecs.py:173-177, applied once to the
+// attention output).  A workgroup takes kRotRows rows: thread (part, d) sums
+// rows part*RPT .. +RPT-1 of column d over k in order, reading R row k
+// (coalesced over d) once per k.
+constexpr int kRotRows = 16;
+template <int D>
+__global__ void __launch_bounds__(256)
+    rotate_rows_kernel(const float *y, const float *rot, int64_t rows, void *out, int out_dtype) {
+    constexpr int PARTS = 256 / D;
+    constexpr int RPT = kRotRows / PARTS;
+    __shared__ float ys[kRotRows][D];
+    const int64_t r0 = (int64_t)blockIdx.x * kRotRows;
+    for (int i = threadIdx.x; i < kRotRows * D; i += 256) {
+        const int64_t r = r0 + i / D;
+        ys[i / D][i % D] = r < rows ? y[r * D + i % D] : 0.f;
+    }
+    __syncthreads();
+    const int d = threadIdx.x % D, part = threadIdx.x / D;
+    float acc[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) acc[j] = 0.f;
+    for (int k = 0; k < D; ++k) {
+        const float rk = rot[k * D + d];
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) acc[j] = fmaf(ys[part * RPT + j][k], rk, acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+        const int64_t r = r0 + part * RPT + j;
+        if (r < rows) store_from_f32(out, out_dtype, r * D + d, acc[j]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -2107,6 +2195,84 @@ extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch,
     }
 #undef SS_GROUPED_BITS
 #undef SS_GROUPED
+}
+
+// Workspace of the TurboQuant decode: the split partials (as for the other
+// VALU decodes), then the fp32 output rows of the rotated basis.
+static size_t turboquant_ws_bytes(const DecodeShape &s, int64_t rows, int head_dim) {
+    const size_t part = (decode_ws_bytes(s, head_dim) + 255) / 256 * 256;
+    return part + (size_t)rows * head_dim * sizeof(float);
+}
+
+extern "C" size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads,
+                                                       int n_kv_heads, int64_t t_q, int head_dim,
+                                                       int64_t t_kv, int n_splits) {
+    if (batch < 1 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads || t_q < 1)
+        return 0;
+    return turboquant_ws_bytes(decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits),
+                               batch * n_q_heads * t_q, head_dim);
+}
+
+extern "C" int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t batch,
+                                         int n_q_heads, int n_kv_heads, int64_t t_q, int head_dim,
+                                         float scale, const int32_t *perm, const float *centroids,
+                                         int n_blocks, int n_centroids, const uint8_t *idx,
+                                         const uint32_t *packed, const float *norms,
+                                         const float *levels, const float *rotation, int bits,
+                                         int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
+                                         void *out, int out_dtype, void *workspace,
+                                         size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(packed && norms && levels && rotation, "null packed/norms/levels/rotation");
+    SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4 (got %d)", bits);
+    SS_REQUIRE(!(bits == 2 && head_dim % 16) && !(bits == 4 && head_dim % 8),
+               "head_dim %d cannot be packed at %d bits", head_dim, bits);
+    SS_REQUIRE(((uintptr_t)packed % 4) == 0 && ((uintptr_t)norms % 4) == 0 &&
+                   ((uintptr_t)rotation % 4) == 0,
+               "packed/norms/rotation must be 4-byte aligned");
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    const int64_t rows = batch * n_q_heads * t_q;
+    const size_t need = turboquant_ws_bytes(s, rows, head_dim);
+    if (!workspace || workspace_bytes < need) {
+        set_error("decode workspace too small: need %zu bytes, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+        return SS_ERR_WORKSPACE;
+    }
+    SS_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+    float *y = reinterpret_cast<float *>(static_cast<char *>(workspace) + need -
+                                         (size_t)rows * head_dim * sizeof(float));
+    // the attention output in the rotated basis goes to y (fp32), then
+    // out = y @ R in out_dtype
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, y, SS_F32, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define SS_TURBO(DD, BB)                                                   \
+    {                                                                      \
+        typename VTurbo<DD, BB>::Args va{packed, norms, {}};               \
+        for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];          \
+        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st);                   \
+    }
+    if (head_dim == 128) {
+        if (bits == 2) SS_TURBO(128, 2) else if (bits == 3) SS_TURBO(128, 3) else SS_TURBO(128, 4)
+    } else {
+        if (bits == 2) SS_TURBO(64, 2) else if (bits == 3) SS_TURBO(64, 3) else SS_TURBO(64, 4)
+    }
+#undef SS_TURBO
+    if (rc) return rc;
+    const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, rotation,
+                           rows, out, out_dtype);
+    else
+        hipLaunchKernelGGL(rotate_rows_kernel<64>, dim3(blocks), dim3(256), 0, st, y, rotation,
+                           rows, out, out_dtype);
+    SS_LAUNCH_CHECK("rotate_rows_kernel launch");
+    return SS_OK;
 }
 
 extern "C" int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,

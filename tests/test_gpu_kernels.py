@@ -495,3 +495,38 @@ def test_decode_grouped_il_hybrid_buffer(b, hq, hkv, d, t_kv, t_buf, bits, group
     vals[:, :, t_kv:] = vb[:, :, :t_buf]
     ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals)
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_q,causal,bits,splits,cap", [
+    (1, 32, 8, 128, 4096, 1, False, 2, 0, None),   # config-2 heads, 2-bit
+    (2, 8, 2, 128, 1000, 1, False, 3, 0, 1024),    # 3-bit words (10 codes, 2 pad bits)
+    (1, 8, 2, 128, 777, 1, False, 4, 7, None),     # 4-bit, forced 7 splits
+    (1, 8, 2, 64, 513, 1, False, 2, 1, None),      # head_dim 64, one split
+    (2, 6, 2, 64, 300, 5, True, 4, 3, 320),        # prefill rows, causal
+    (1, 4, 1, 128, 1, 1, False, 3, 0, 16),         # single token
+    (1, 4, 1, 128, 0, 1, False, 2, 0, 16),         # empty cache: zeros
+])
+def test_decode_turboquant_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, bits, splits, cap):
+    """ss_decode_attn_turboquant: softmax(q.k) over norm * (levels[code] @ R)
+    values equals the oracle SDPA over the TurboQuant-dequantised cache."""
+    cap = cap or t_kv
+    cents, perm, idx, _, q = decode_case(40 + bits + t_kv, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(bits * 1000 + t_kv)
+    codes = rng.integers(0, 1 << bits, (b, hkv, cap, d)).astype(np.uint8)
+    packed = O.pack_indices(codes, bits).astype(np.uint32)
+    norms = (rng.random((b, hkv, cap)) * 3 + 0.1).astype(np.float32)
+    levels = (O.lloyd_max_gaussian(bits)[0] / np.sqrt(d)).astype(np.float32)
+    rot = O.rotation_matrix(d, 43)
+    scale = 1.0 / np.sqrt(d)
+    out = _hip.decode_attn_turboquant(t(q), scale, t(perm), t(cents), t(idx),
+                                      t(packed.view(np.int32)), t(norms), levels, t(rot), bits,
+                                      t_kv, causal=causal, q_offset=t_kv - t_q if causal else 0,
+                                      out_dtype=torch.float32, n_splits=splits)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if t_kv == 0:
+        assert not got.any()
+        return
+    vals = O.turboquant_decode(packed[:, :, :t_kv], norms[:, :, :t_kv], rot, levels, d, bits)
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals, cents, perm, scale, mask="causal" if causal else None)
+    assert rel_err(got, ref) <= REL_TOL
