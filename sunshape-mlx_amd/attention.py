@@ -77,6 +77,11 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
                                               buf_len=buffered, **kw)
             codec.last_score_backend = ("hip_fused_mfma_dequant_buffer" if buffered
                                         else "hip_fused_mfma_dequant")
+        elif ops["kind"] == "turboquant":
+            out = _hip.decode_attn_turboquant(q, kscale, perm, codec.centroids, ops["idx"],
+                                              ops["packed"], ops["norms"], ops["levels"],
+                                              ops["rotation"], ops["bits"], **kw)
+            codec.last_score_backend = "hip_fused_turboquant"
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
                                            ops["packed"], ops["scales"], ops["zeros"],

@@ -551,7 +551,7 @@ class HybridSunShapeKVCache:
 
     def fused_operands(self) -> dict | None:
         """Full-capacity compressed buffers for the fused decode kernels
-        ({"kind": "grouped"|"dense", ...}); None when there is nothing
+        ({"kind": "grouped_il"|"grouped"|"turboquant"|"dense", ...}); None when there is nothing
         compressed or the value backend has no fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
             return None
@@ -567,6 +567,12 @@ class HybridSunShapeKVCache:
                     "packed": self._values_packed.view(torch.uint32),
                     "scales": self._value_scales, "zeros": self._value_zeros,
                     "bits": gc.bits, "group_size": gc.group_size}
+        if self.value_backend == "turboquant" and self._values_packed is not None:
+            tc = self._value_codec_impl
+            tc._on(self._values_packed.device)
+            return {"kind": "turboquant", "idx": self._key_indices,
+                    "packed": self._values_packed, "norms": self._value_norms,
+                    "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None

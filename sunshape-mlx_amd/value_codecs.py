@@ -127,6 +127,14 @@ class TurboQuantValueCodec:
     def packed_dim(self) -> int:
         return _packed_dim(self.head_dim, self.bits)
 
+    def levels_host(self) -> list[float]:
+        """The scaled levels as host floats (the fused decode takes them as
+        kernel arguments), read from the device once."""
+        lv = getattr(self, "_levels_host", None)
+        if lv is None:
+            lv = self._levels_host = [float(x) for x in self.centroids.cpu().tolist()]
+        return lv
+
     def _on(self, device):
         if self.rotation.device != device:
             self.centroids = self.centroids.to(device)

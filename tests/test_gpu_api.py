@@ -321,6 +321,37 @@ def test_turboquant_value_codec_matches_oracle():
     assert rel_err(rec, ref_rec) <= 1e-5
 
 
+@pytest.mark.parametrize("bits,t_q", [(2, 1), (3, 1), (4, 3)])
+def test_hybrid_turboquant_fused_decode(bits, t_q):
+    """A hybrid cache with TurboQuant values and no buffered tokens decodes in
+    one fused launch (plus the row rotation) instead of dequantising the
+    whole cache; the result equals the oracle SDPA over the oracle's
+    dequantisation of the cache's own codes and norms."""
+    codec = make_codec(30 + bits)
+    b, hq, hkv, d, n = 2, 8, 2, 128, 333
+    k, v = kv(31 + bits, b, hkv, n, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="turboquant",
+                              value_bits=bits, buffer_size=0)
+    cache.update_and_fetch(k, v)
+    assert cache.buffer_offset == 0 and cache.compressed_offset == n
+    q = torch.randn((b, hq, t_q, d), device=DEV).to(torch.float16)
+    mask = "causal" if t_q > 1 else None
+    out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
+    assert codec.last_score_backend == "hip_fused_turboquant"
+    tc = cache._value_codec_impl
+    vals = O.turboquant_decode(cache._values_packed[:, :, :n].cpu().numpy().view(np.uint32),
+                               cache._value_norms[:, :, :n].cpu().numpy(),
+                               tc.rotation.cpu().numpy(), tc.centroids.cpu().numpy(), d, bits)
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088,
+                 mask=mask)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the value codec's own dequantisation gives the same cache contents
+    rec = tc.dequantize(cache._values_packed[:, :, :n].reshape(-1, tc.packed_dim),
+                        cache._value_norms[:, :, :n].reshape(-1)).cpu().numpy()
+    assert rel_err(rec.reshape(vals.shape), vals) <= 1e-5
+
+
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():
     codec = make_codec(16)
     cache = S.create_kv_cache(codec, n_kv_heads=1)
