@@ -217,7 +217,12 @@ int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_he
  * kernel for these values: it dequantises the whole cache every step and
  * runs the two-pass SDPA (cache.py:774-784, attention.py:307-350), which this
  * replaces.  Accumulation runs in the rotated basis; the rotation is applied
- * once per output row (a second launch on the same stream).
+ * once per output row (a later launch on the same stream).  A hybrid cache's
+ * t_buf buffered tokens (k_buf/v_buf, original basis, element j of token t of
+ * (b, h) at [b*buf_sb + h*buf_sh + t*buf_st + j], buf_dtype f16/bf16/f32)
+ * join the same softmax as positions t_kv .. t_kv + t_buf - 1, as one more
+ * split partial taken into the rotated basis (reference attention.py:238
+ * sends such caches to the two-pass path instead).
  *   packed    uint32 [batch][n_kv_heads][cap][packed_dim], pack_indices layout
  *   norms     float  [batch][n_kv_heads][cap]
  *   levels    HOST float[2^bits], ascending Lloyd-Max levels x 1/sqrt(head_dim)
@@ -230,12 +235,14 @@ int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t batch, int n_q
                               const int32_t *perm, const float *centroids, int n_blocks,
                               int n_centroids, const uint8_t *idx, const uint32_t *packed,
                               const float *norms, const float *levels, const float *rotation,
-                              int bits, int64_t cap, int64_t t_kv, int causal,
+                              int bits, int64_t cap, int64_t t_kv, const void *k_buf,
+                              const void *v_buf, int buf_dtype, int64_t buf_sb,
+                              int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal,
                               int64_t q_offset, void *out, int out_dtype, void *workspace,
                               size_t workspace_bytes, int n_splits, void *stream);
 size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                             int64_t t_q, int head_dim, int64_t t_kv,
-                                            int n_splits);
+                                            int64_t t_buf, int n_splits);
 
 /*
  * As ss_decode_attn_grouped with the 2- or 4-bit codes held in a token-

@@ -78,11 +78,13 @@ _SIGNATURES = {
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
                                       _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
-    "ss_decode_attn_turboquant": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
-                                         _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
-                                         _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64, _int,
-                                         _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
-    "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
+    "ss_decode_attn_turboquant": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _i64,
+                                                     _int]),
     "ss_decode_attn_grouped_il": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                          _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
@@ -447,12 +449,16 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
                            norms: torch.Tensor, levels, rotation: torch.Tensor, bits: int,
                            t_kv: int, causal: bool = False, q_offset: int = 0,
                            out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                           n_splits: int = 0) -> torch.Tensor:
+                           n_splits: int = 0, buf_keys: torch.Tensor | None = None,
+                           buf_values: torch.Tensor | None = None,
+                           buf_len: int = 0) -> torch.Tensor:
     """Fused decode over TurboQuant values: ``packed`` (B, Hkv, cap,
     packed_dim) codes, ``norms`` (B, Hkv, cap) float32, ``levels`` the 2^bits
     scaled Lloyd-Max levels (any float sequence; copied to the kernel
     arguments), ``rotation`` (D, D) float32 with ``value = norm * (levels[code]
-    @ rotation)``."""
+    @ rotation)``.  A hybrid cache's recent tokens ``buf_keys``/``buf_values``
+    (B, Hkv, >= buf_len, D, original basis) join the same softmax as
+    positions t_kv .. t_kv + buf_len - 1."""
     _check_decode_common(q, idx, centroids, perm)
     require_gpu(packed, norms, rotation)
     b_, hq, tq, d = q.shape
@@ -473,15 +479,31 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     nc = centroids.shape[1]
     if out is None:
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    buf_len = int(buf_len)
+    if buf_len > 0:
+        require_gpu(buf_keys, buf_values)
+        for name, tb in (("buf_keys", buf_keys), ("buf_values", buf_values)):
+            if tb.dim() != 4 or tb.shape[0] != b_ or tb.shape[1] != hkv or tb.shape[3] != d or \
+                    tb.shape[2] < buf_len or tb.stride(3) != 1:
+                raise ValueError(f"{name} must be (B, n_kv_heads, >= {buf_len}, {d}) with unit "
+                                 "element stride")
+        if buf_keys.stride() != buf_values.stride() or buf_keys.dtype != buf_values.dtype:
+            raise ValueError("buffer keys and values must share dtype and strides")
+        bsb, bsh, bst = buf_keys.stride()[:3]
+        bdt = dtype_code(buf_keys.dtype)
+    else:
+        buf_keys = buf_values = None
+        bsb = bsh = bst = bdt = 0
     lib = load_library()
-    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), int(n_splits))
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
+                                                        int(n_splits))
     ws = decode_workspace(q.device, ws_bytes)
     check(lib.ss_decode_attn_turboquant(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
-        ptr(rotation), int(bits), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
-        dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
-        stream_handle(q.device)))
+        ptr(rotation), int(bits), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
+        bst, buf_len, int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
     return out
 
 

@@ -572,7 +572,8 @@ class HybridSunShapeKVCache:
             tc._on(self._values_packed.device)
             return {"kind": "turboquant", "idx": self._key_indices,
                     "packed": self._values_packed, "norms": self._value_norms,
-                    "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits}
+                    "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits,
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None

@@ -1881,6 +1881,141 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// A hybrid cache's buffered tokens (original basis, element j of token t of
+// (b, h) at buf[b*sb + h*sh + t*st + j]) as split partial `slot` of the
+// TurboQuant decode, so they join the compressed tokens' softmax in the merge
+// (the reference runs its two-pass path instead, attention.py:307-350).  One
+// workgroup per column.  Scores are fp32 dot products with the unpermuted
+// scaled query, in log2 units, at positions t_kv + t; online softmax over
+// chunks of 256 tokens; P.V in the original basis.  The accumulators are then
+// taken into the rotated basis, acc @ R^T (R orthogonal), where the merge
+// adds them to the compressed splits' before the output rotation.
+template <int D, int R>
+__global__ void __launch_bounds__(256)
+    buffer_partial_kernel(DecodeCommon c, const void *kbuf, const void *vbuf, int buf_dtype,
+                          int64_t sb, int64_t sh, int64_t st, int64_t t_buf, const float *rot,
+                          int slot) {
+    constexpr int T = 256, NW = T / kWave;
+    __shared__ float qs[R][D];
+    __shared__ float pr[R][T];
+    __shared__ float red[NW][R];
+    __shared__ float acc_s[R][D];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid >> 6;
+    const int col = blockIdx.x;
+    const int rg = col % c.n_rg;
+    const int kvh = (col / c.n_rg) % c.n_kv_heads;
+    const int64_t bb = col / (c.n_rg * c.n_kv_heads);
+    auto row_ok = [&](int r) { return (int64_t)rg * R + r < c.rows_total; };
+    auto row_off = [&](int r) -> int64_t {
+        const int64_t g = (int64_t)rg * R + r;
+        const int64_t rr = g / c.t_q, tq = g - rr * c.t_q;
+        return ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+    };
+    for (int i = tid; i < R * D; i += T) {
+        const int r = i / D, j = i - r * D;
+        qs[r][j] = row_ok(r) ? round_to(c.q_dtype, load_as_f32(c.q, c.q_dtype, row_off(r) + j) *
+                                                        c.scale)
+                             : 0.f;
+    }
+    int64_t lim[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t g = (int64_t)rg * R + r;
+        lim[r] = !row_ok(r) ? -1 : c.causal ? c.q_offset + (g % c.t_q) : INT64_MAX;
+    }
+    const int64_t base = bb * sb + kvh * sh;
+    // thread (r, d) of the P.V: rows r = tid / D + k * (T / D)
+    constexpr int RPT = (R * D + T - 1) / T;
+    float m[R], l[R], acc[RPT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) m[r] = -1e30f, l[r] = 0.f;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) acc[k] = 0.f;
+    __syncthreads();
+    for (int64_t j0 = 0; j0 < t_buf; j0 += T) {
+        const int64_t j = j0 + tid;
+        float s[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[r] = 0.f;
+        if (j < t_buf) {
+            for (int d = 0; d < D; ++d) {
+                const float kv = load_as_f32(kbuf, buf_dtype, base + j * st + d);
+#pragma unroll
+                for (int r = 0; r < R; ++r) s[r] = fmaf(qs[r][d], kv, s[r]);
+            }
+        }
+        float cm[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool ok = j < t_buf && c.t_kv + j <= lim[r];
+            s[r] = ok ? s[r] * kLog2e : -INFINITY;
+            cm[r] = wave_max(s[r]);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[wv][r] = cm[r];
+        __syncthreads();
+        float corr[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float mx = red[0][r];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red[w][r]);
+            const float mn = fmaxf(m[r], mx);
+            corr[r] = fast_exp2(m[r] - mn);
+            m[r] = mn;
+            pr[r][tid] = fast_exp2(s[r] - mn);
+        }
+        __syncthreads();  // probabilities staged; red free
+        float ps[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) ps[r] = wave_sum(pr[r][tid]);
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[wv][r] = ps[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += red[w][r];
+            l[r] = fmaf(l[r], corr[r], sum);
+        }
+        const int n = (int)min((int64_t)T, t_buf - j0);
+#pragma unroll
+        for (int k = 0; k < RPT; ++k) {
+            const int e = tid + k * T;
+            if (e < R * D) {
+                const int r = e / D, d = e - r * D;
+                float a = acc[k] * corr[r];
+                for (int i = 0; i < n; ++i)
+                    a = fmaf(pr[r][i], load_as_f32(vbuf, buf_dtype, base + (j0 + i) * st + d), a);
+                acc[k] = a;
+            }
+        }
+        __syncthreads();  // pr and red reused by the next chunk
+    }
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int e = tid + k * T;
+        if (e < R * D) acc_s[e / D][e % D] = acc[k];
+    }
+    __syncthreads();
+    const int64_t slot0 = ((int64_t)col * c.n_splits + slot) * R;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int e = tid + k * T;
+        if (e < R * D) {
+            const int r = e / D, kk = e - r * D;
+            float a = 0.f;
+            for (int d = 0; d < D; ++d) a = fmaf(acc_s[r][d], rot[kk * D + d], a);
+            c.part_acc[(slot0 + r) * D + kk] = a;
+            if (kk == 0)
+                *reinterpret_cast<float2 *>(c.part_ml + (slot0 + r) * 2) = make_float2(m[r], l[r]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1989,7 +2124,7 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
 
 template <int D, int R, class VF>
 static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
-                  hipStream_t st) {
+                  hipStream_t st, bool merge = true) {
     const size_t lds = decode_lds_bytes<D, R>();
     auto kern = decode_attn_kernel<D, R, VF>;
     static bool attr_set = false;  // per instantiation
@@ -2002,14 +2137,14 @@ static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape
     dim3 grid(s.S, s.n_cols);
     hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), lds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_kernel launch");
-    return launch_merge<D>(c, s, st);
+    return merge ? launch_merge<D>(c, s, st) : SS_OK;
 }
 
 template <int D, class VF>
 static int launch_r(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
-                    hipStream_t st) {
-    if (s.R == 1) return launch<D, 1, VF>(c, va, s, st);
-    return launch<D, 4, VF>(c, va, s, st);
+                    hipStream_t st, bool merge = true) {
+    if (s.R == 1) return launch<D, 1, VF>(c, va, s, st, merge);
+    return launch<D, 4, VF>(c, va, s, st, merge);
 }
 
 static int check_common(const void *q, int q_dtype, int64_t batch, int hq, int hkv, int64_t t_q,
@@ -2198,30 +2333,35 @@ extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch,
 }
 
 // Workspace of the TurboQuant decode: the split partials (as for the other
-// VALU decodes), then the fp32 output rows of the rotated basis.
-static size_t turboquant_ws_bytes(const DecodeShape &s, int64_t rows, int head_dim) {
-    const size_t part = (decode_ws_bytes(s, head_dim) + 255) / 256 * 256;
+// VALU decodes, plus one slot per column for buffered tokens), then the fp32
+// output rows of the rotated basis.
+static DecodeShape with_buffer_slot(DecodeShape s, int64_t t_buf) {
+    if (t_buf > 0) s.S += 1;
+    return s;
+}
+
+static size_t turboquant_ws_bytes(const DecodeShape &sw, int64_t rows, int head_dim) {
+    const size_t part = (decode_ws_bytes(sw, head_dim) + 255) / 256 * 256;
     return part + (size_t)rows * head_dim * sizeof(float);
 }
 
 extern "C" size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads,
                                                        int n_kv_heads, int64_t t_q, int head_dim,
-                                                       int64_t t_kv, int n_splits) {
+                                                       int64_t t_kv, int64_t t_buf, int n_splits) {
     if (batch < 1 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads || t_q < 1)
         return 0;
-    return turboquant_ws_bytes(decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits),
-                               batch * n_q_heads * t_q, head_dim);
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    return turboquant_ws_bytes(with_buffer_slot(s, t_buf), batch * n_q_heads * t_q, head_dim);
 }
 
-extern "C" int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t batch,
-                                         int n_q_heads, int n_kv_heads, int64_t t_q, int head_dim,
-                                         float scale, const int32_t *perm, const float *centroids,
-                                         int n_blocks, int n_centroids, const uint8_t *idx,
-                                         const uint32_t *packed, const float *norms,
-                                         const float *levels, const float *rotation, int bits,
-                                         int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
-                                         void *out, int out_dtype, void *workspace,
-                                         size_t workspace_bytes, int n_splits, void *stream) {
+extern "C" int ss_decode_attn_turboquant(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint32_t *packed, const float *norms,
+    const float *levels, const float *rotation, int bits, int64_t cap, int64_t t_kv,
+    const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
+    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
     if (rc) return rc;
@@ -2232,9 +2372,18 @@ extern "C" int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t bat
     SS_REQUIRE(((uintptr_t)packed % 4) == 0 && ((uintptr_t)norms % 4) == 0 &&
                    ((uintptr_t)rotation % 4) == 0,
                "packed/norms/rotation must be 4-byte aligned");
+    SS_REQUIRE(t_buf >= 0, "negative buffer length");
+    if (t_buf > 0) {
+        SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
+        SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
+                   "buffer dtype must be f16, bf16 or f32");
+        SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
+                   "buffer strides must be non-negative, token stride >= head_dim");
+    }
     const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    const DecodeShape sw = with_buffer_slot(s, t_buf);  // partial slots incl. the buffer's
     const int64_t rows = batch * n_q_heads * t_q;
-    const size_t need = turboquant_ws_bytes(s, rows, head_dim);
+    const size_t need = turboquant_ws_bytes(sw, rows, head_dim);
     if (!workspace || workspace_bytes < need) {
         set_error("decode workspace too small: need %zu bytes, got %zu", need,
                   workspace ? workspace_bytes : (size_t)0);
@@ -2246,16 +2395,18 @@ extern "C" int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t bat
     // the attention output in the rotated basis goes to y (fp32), then
     // out = y @ R in out_dtype
     DecodeCommon c;
-    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+    rc = fill_common(c, sw, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
                      n_centroids, idx, cap, t_kv, causal, q_offset, y, SS_F32, workspace,
                      workspace_bytes, head_dim);
     if (rc) return rc;
+    c.tiles_per_split = s.tiles_per_split;  // the compressed tokens' splits: grid s.S
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const bool merge_here = t_buf == 0;  // else the buffer partial comes first
 #define SS_TURBO(DD, BB)                                                   \
     {                                                                      \
         typename VTurbo<DD, BB>::Args va{packed, norms, {}};               \
         for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];          \
-        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st);                   \
+        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, merge_here);       \
     }
     if (head_dim == 128) {
         if (bits == 2) SS_TURBO(128, 2) else if (bits == 3) SS_TURBO(128, 3) else SS_TURBO(128, 4)
@@ -2264,6 +2415,20 @@ extern "C" int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t bat
     }
 #undef SS_TURBO
     if (rc) return rc;
+    if (t_buf > 0) {
+#define SS_BUFP(DD, RR)                                                                       \
+    hipLaunchKernelGGL((buffer_partial_kernel<DD, RR>), dim3(sw.n_cols), dim3(256), 0, st, c,   \
+                       k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, rotation, s.S)
+        if (head_dim == 128) {
+            if (sw.R == 1) SS_BUFP(128, 1); else SS_BUFP(128, 4);
+        } else {
+            if (sw.R == 1) SS_BUFP(64, 1); else SS_BUFP(64, 4);
+        }
+#undef SS_BUFP
+        SS_LAUNCH_CHECK("buffer_partial_kernel launch");
+        rc = head_dim == 128 ? launch_merge<128>(c, sw, st) : launch_merge<64>(c, sw, st);
+        if (rc) return rc;
+    }
     const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
     if (head_dim == 128)
         hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, rotation,

@@ -346,6 +346,22 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088,
                  mask=mask)
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the default buffer: recent fp16 tokens join the same fused softmax
+    cache2 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="turboquant",
+                               value_bits=bits)
+    cache2.update_and_fetch(k, v)
+    nc, nb = cache2.compressed_offset, cache2.buffer_offset
+    assert nb == 128 and nc == n - 128
+    out2 = S.sunshape_sdpa(q, cache2, 0.088, mask=mask)
+    assert codec.last_score_backend == "hip_fused_turboquant_buffer"
+    vals2 = O.turboquant_decode(cache2._values_packed[:, :, :nc].cpu().numpy().view(np.uint32),
+                                cache2._value_norms[:, :, :nc].cpu().numpy(),
+                                tc.rotation.cpu().numpy(), tc.centroids.cpu().numpy(), d, bits)
+    vals_all = np.concatenate([vals2, v[:, :, nc:].float().cpu().numpy()], axis=2)
+    ref2 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                           codec.centroids.cpu().numpy(), cache2.key_indices.cpu().numpy(),
+                           cache2.buffer_keys.float().cpu().numpy(), vals_all, mask=mask)
+    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
     # the value codec's own dequantisation gives the same cache contents
     rec = tc.dequantize(cache._values_packed[:, :, :n].reshape(-1, tc.packed_dim),
                         cache._value_norms[:, :, :n].reshape(-1)).cpu().numpy()

@@ -530,3 +530,42 @@ def test_decode_turboquant_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, bits
     vals = O.turboquant_decode(packed[:, :, :t_kv], norms[:, :, :t_kv], rot, levels, d, bits)
     ref = O.sdpa(q, idx[:, :, :t_kv], vals, cents, perm, scale, mask="causal" if causal else None)
     assert rel_err(got, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,t_q,bits,splits", [
+    (1, 32, 8, 128, 2048, 128, 1, 2, 0),   # default hybrid buffer
+    (2, 8, 2, 64, 333, 300, 1, 4, 3),      # buffer longer than one 256-token chunk
+    (1, 4, 1, 128, 0, 40, 1, 3, 0),        # buffer only
+    (1, 8, 2, 128, 200, 20, 4, 2, 1),      # prefill rows, causal across the buffer
+])
+def test_decode_turboquant_with_buffer(b, hq, hkv, d, t_kv, t_buf, t_q, bits, splits):
+    """Buffered fp16 tokens join the TurboQuant decode as one more split
+    partial (taken into the rotated basis); the result equals the two-pass
+    oracle over the dequantised cache followed by the buffer."""
+    cap = max(((t_kv + 15) // 16) * 16, 16)
+    cents, perm, idx, _, q = decode_case(60 + bits + t_buf, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(t_buf + 7)
+    codes = rng.integers(0, 1 << bits, (b, hkv, cap, d)).astype(np.uint8)
+    packed = O.pack_indices(codes, bits).astype(np.uint32)
+    norms = (rng.random((b, hkv, cap)) * 3 + 0.1).astype(np.float32)
+    levels = (O.lloyd_max_gaussian(bits)[0] / np.sqrt(d)).astype(np.float32)
+    rot = O.rotation_matrix(d, 43)
+    kb = rng.standard_normal((b, hkv, t_buf + 5, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 5, d)).astype(np.float16)
+    scale = 1.0 / np.sqrt(d)
+    causal = t_q > 1
+    total = t_kv + t_buf
+    out = _hip.decode_attn_turboquant(t(q), scale, t(perm), t(cents), t(idx),
+                                      t(packed.view(np.int32)), t(norms), levels, t(rot), bits,
+                                      t_kv, causal=causal, q_offset=total - t_q if causal else 0,
+                                      out_dtype=torch.float32, n_splits=splits,
+                                      buf_keys=t(kb), buf_values=t(vb), buf_len=t_buf)
+    torch.cuda.synchronize()
+    vals = np.zeros((b, hkv, total, d), np.float64)
+    if t_kv:
+        vals[:, :, :t_kv] = O.turboquant_decode(packed[:, :, :t_kv], norms[:, :, :t_kv], rot,
+                                                levels, d, bits)
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                          mask="causal" if causal else None)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
