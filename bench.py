@@ -17,6 +17,7 @@ Prints one JSON line on stdout; progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -52,10 +53,12 @@ def parse_args():
                    help="budget for the CPU baseline (0 disables it)")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                           "decode_fp16v_t32k_traffic.json"))
-    p.add_argument("--workload", choices=("metric", "hybrid", "encode"), default="metric",
+    p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant"),
+                   default="metric",
                    help="metric: the BASELINE metric decode (fp16 values, B=1); hybrid: config 4 "
                         "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
-                        "(65,536 fp16 keys block-VQ encoded)")
+                        "(65,536 fp16 keys block-VQ encoded); turboquant: the config-4 shape "
+                        "with 2-bit TurboQuant values")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a plain device copy of MB megabytes --steps times (the "
                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -212,6 +215,94 @@ def run_hybrid(args) -> int:
     return 0
 
 
+def run_turboquant(args) -> int:
+    """Config-4 shape (B=8, 32/8 heads, D=128, T_kv=32768, u8 key indices)
+    with 2-bit TurboQuant values (codes + fp32 norm per token): one
+    ss_decode_attn_turboquant call per step (decode kernel, split merge and
+    output-row rotation on one stream)."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    lib = hip.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b, hq, hkv, d, t_kv, nb, bits = 8, 32, 8, 128, args.t_kv, 16, 2
+    scale = 1.0 / math.sqrt(d)
+    g = torch.Generator(device=dev).manual_seed(6)
+    cents = torch.randn((nb, 256, 8), generator=g, device=dev)
+    perm = torch.randperm(d, generator=g, device=dev).to(torch.int32)
+    idx0 = torch.randint(0, 256, (b, hkv, t_kv, nb), generator=g, device=dev).to(torch.uint8)
+    pd = d * bits // 32
+    pk0 = torch.randint(-2 ** 31, 2 ** 31 - 1, (b, hkv, t_kv, pd), generator=g, device=dev,
+                        dtype=torch.int64).to(torch.int32)
+    nm0 = torch.rand((b, hkv, t_kv), generator=g, device=dev) * 3 + 0.1
+    tq = pkg.TurboQuantValueCodec(head_dim=d, bits=bits, seed=43, device=dev)
+    levels = tq.levels_host()
+    lv_host = (ctypes.c_float * len(levels))(*levels)
+    rot = tq.rotation.contiguous()
+    q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
+    per_copy = idx0.numel() + pk0.numel() * 4 + nm0.numel() * 4
+    n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
+    bufs = [(idx0, pk0, nm0)] + [tuple(t.clone() for t in (idx0, pk0, nm0))
+                                 for _ in range(n_copies - 1)]
+    torch.cuda.synchronize()
+    log(f"turboquant cache ready: {n_copies} copies x {per_copy / 1e6:.1f} MB")
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b, hq, hkv, 1, d, t_kv, 0, args.splits)
+    splits = lib.ss_decode_default_splits(b, hq, hkv, 1, d, t_kv) if args.splits <= 0 else args.splits
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.ss_decode_attn_turboquant
+    lv_ptr = ctypes.cast(lv_host, ctypes.c_void_p).value
+    argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cents.data_ptr(),
+             nb, 256, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), lv_ptr, rot.data_ptr(),
+             bits, t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0, out.data_ptr(), hip.SS_F16,
+             ws.data_ptr(), ws_bytes, args.splits, stream) for t in bufs]
+    us, per = time_launches(fn, argv, args.steps, args.warmup, hip)
+    nbytes = b * hkv * t_kv * (nb + pd * 4 + 4) + b * hq * d * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"turboquant: {us:.2f} us/step, {gbs:.1f} GB/s (splits={splits})")
+
+    check = None
+    if args.cpu_seconds > 0:  # output check of one (b, KV head) against the oracle
+        from oracle import sunshape_oracle as O
+
+        hip.check(fn(*argv[0]))
+        torch.cuda.synchronize()
+        bi, hi = 2, 6
+        vals = O.turboquant_decode(pk0[bi, hi].cpu().numpy().view(np.uint32),
+                                   nm0[bi, hi].cpu().numpy(), rot.cpu().numpy(),
+                                   np.asarray(levels, np.float32), d, bits)
+        qh = q[bi:bi + 1, hi * 4:(hi + 1) * 4].cpu().numpy()
+        ref = O.sdpa(qh, idx0[bi:bi + 1, hi:hi + 1].cpu().numpy(), vals[None, None],
+                     cents.cpu().numpy(), perm.cpu().numpy(), scale)
+        got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
+        check = float(np.abs(got - ref).max() / np.abs(ref).max())
+
+    line = {
+        "metric": "TurboQuant-value decode attention µs/step and achieved HBM GB/s",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us * 1e-3, 6), "us_per_step": round(us, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "decode B=8 Hq=32 Hkv=8 D=128 T_kv=32768, u8 key indices, 2-bit "
+                               "TurboQuant values (packed codes + fp32 norm), fp16 query/output",
+                   "t_kv": t_kv, "splits": splits, "cache_copies": n_copies,
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "per_launch_us": {"mean": round(float(np.mean(per)), 3),
+                          "median": round(float(np.median(per)), 3)},
+        "check_max_rel_err_vs_oracle": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 VALU_FP32_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMD x 16 lanes x 2 flops x 2.4 GHz, no packed fp32
 
 
@@ -299,6 +390,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, args.steps)
     if args.workload == "hybrid":
         return run_hybrid(args)
+    if args.workload == "turboquant":
+        return run_turboquant(args)
     if args.workload == "encode":
         return run_encode(args)
 

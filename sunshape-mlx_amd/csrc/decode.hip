@@ -183,7 +183,8 @@ struct VGrouped {
 // n * level[code], the value in the rotated basis: since every token shares
 // the rotation R, sum_t p_t (n_t C[idx_t] @ R) = (sum_t p_t n_t C[idx_t]) @ R,
 // so the kernel accumulates in the rotated basis and R is applied once per
-// output row after the split merge (rotate_rows_kernel).
+// output row: by the split-merge launch, or by rotate_rows_kernel when a
+// single split writes the rows itself.
 template <int D, int BITS>
 struct VTurbo {
     static constexpr int VPW = 32 / BITS;
@@ -1787,12 +1788,14 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 // launch: a cross-workgroup hand-off inside one kernel needs an agent-scope L2
 // write-back per workgroup on multi-XCD CDNA parts.
 template <int D>
-__global__ void __launch_bounds__(kDecodeThreads) decode_merge_kernel(DecodeCommon c, int R) {
+__global__ void __launch_bounds__(kDecodeThreads)
+    decode_merge_kernel(DecodeCommon c, int R, const float *rot, void *rot_out, int rot_dtype) {
     constexpr int CH = D / 4;                // float4 chunks of one output row
     constexpr int NP = kDecodeThreads / CH;  // split partitions
     __shared__ float wsh[kMaxSplits];
     __shared__ float lsh;
     __shared__ float4 red[NP * CH];
+    __shared__ float yrow[D];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid >> 6;
     const int col = blockIdx.x, r = blockIdx.y;
     const int64_t gr = (int64_t)(col % c.n_rg) * R + r;
@@ -1843,7 +1846,24 @@ __global__ void __launch_bounds__(kDecodeThreads) decode_merge_kernel(DecodeComm
         }
         const int64_t rr = gr / c.t_q, tq = gr - rr * c.t_q;
         const int64_t off = ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
-        store_from_f32(c.out, c.out_dtype, off + d, lsh > 0.f ? A / lsh : 0.f);
+        const float y = lsh > 0.f ? A / lsh : 0.f;
+        if (rot)
+            yrow[d] = y;
+        else
+            store_from_f32(c.out, c.out_dtype, off + d, y);
+    }
+    if (rot) {
+        // the merged row is in the TurboQuant rotated basis: out = y @ R,
+        // summed over k in order as rotate_rows_kernel does
+        __syncthreads();
+        if (tid < D) {
+            const int64_t rr = gr / c.t_q, tq = gr - rr * c.t_q;
+            const int64_t off = ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+            float a = 0.f;
+#pragma unroll 8
+            for (int k = 0; k < D; ++k) a = fmaf(yrow[k], rot[k * D + tid], a);
+            store_from_f32(rot_out, rot_dtype, off + tid, a);
+        }
     }
 }
 
@@ -2088,10 +2108,12 @@ static size_t decode_ws_bytes(const DecodeShape &s, int head_dim) {
 }
 
 template <int D>
-static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t st) {
+static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t st,
+                        const float *rot = nullptr, void *rot_out = nullptr, int rot_dtype = 0) {
     if (s.S <= 1) return SS_OK;
     auto merge = decode_merge_kernel<D>;
-    hipLaunchKernelGGL(merge, dim3(s.n_cols, s.R), dim3(kDecodeThreads), 0, st, c, s.R);
+    hipLaunchKernelGGL(merge, dim3(s.n_cols, s.R), dim3(kDecodeThreads), 0, st, c, s.R, rot,
+                       rot_out, rot_dtype);
     SS_LAUNCH_CHECK("decode_merge_kernel launch");
     return SS_OK;
 }
@@ -2401,12 +2423,13 @@ extern "C" int ss_decode_attn_turboquant(
     if (rc) return rc;
     c.tiles_per_split = s.tiles_per_split;  // the compressed tokens' splits: grid s.S
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    const bool merge_here = t_buf == 0;  // else the buffer partial comes first
+    // with several partial slots the merge launch also applies the rotation
+    // (after the buffer's partial, if any); a single split writes y here
 #define SS_TURBO(DD, BB)                                                   \
     {                                                                      \
         typename VTurbo<DD, BB>::Args va{packed, norms, {}};               \
         for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];          \
-        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, merge_here);       \
+        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, false);            \
     }
     if (head_dim == 128) {
         if (bits == 2) SS_TURBO(128, 2) else if (bits == 3) SS_TURBO(128, 3) else SS_TURBO(128, 4)
@@ -2426,9 +2449,10 @@ extern "C" int ss_decode_attn_turboquant(
         }
 #undef SS_BUFP
         SS_LAUNCH_CHECK("buffer_partial_kernel launch");
-        rc = head_dim == 128 ? launch_merge<128>(c, sw, st) : launch_merge<64>(c, sw, st);
-        if (rc) return rc;
     }
+    if (sw.S > 1)
+        return head_dim == 128 ? launch_merge<128>(c, sw, st, rotation, out, out_dtype)
+                               : launch_merge<64>(c, sw, st, rotation, out, out_dtype);
     const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
     if (head_dim == 128)
         hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, rotation,
