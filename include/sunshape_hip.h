@@ -245,6 +245,33 @@ size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_
                                             int64_t t_buf, int n_splits);
 
 /*
+ * As ss_decode_attn_turboquant with SunShape block-VQ values (value backend
+ * "sunshape", reference cache.py:614-623): token t's value is the value
+ * codec's dequantisation of its indices, concat_b v_centroids[b][v_idx[t][b]]
+ * taken back to the original basis by v_transform.  The reference has no
+ * fused kernel for these values: it dequantises the whole cache on the CPU
+ * every step (cache.py:785-800) and runs the two-pass SDPA.
+ *   v_idx        uint8 [batch][n_kv_heads][cap][head_dim / v_block_dim]
+ *   v_centroids  float [head_dim / v_block_dim][v_n_centroids][v_block_dim],
+ *                v_block_dim 4 or 8, v_n_centroids <= 256
+ *   v_transform  float [head_dim][head_dim] (device): original = codec-space
+ *                row @ v_transform (the inverse permutation as a 0/1 matrix,
+ *                or the codec rotation)
+ *   workspace    ss_decode_turboquant_workspace_bytes(...) bytes (same layout)
+ */
+int ss_decode_attn_sunshape_v(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                              int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                              const int32_t *perm, const float *centroids, int n_blocks,
+                              int n_centroids, const uint8_t *idx, const uint8_t *v_idx,
+                              const float *v_centroids, int v_block_dim, int v_n_centroids,
+                              const float *v_transform, int64_t cap, int64_t t_kv,
+                              const void *k_buf, const void *v_buf, int buf_dtype,
+                              int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
+                              int causal, int64_t q_offset, void *out, int out_dtype,
+                              void *workspace, size_t workspace_bytes, int n_splits,
+                              void *stream);
+
+/*
  * As ss_decode_attn_grouped with the 2- or 4-bit codes held in a token-
  * interleaved layout and the codebook prepared by ss_codebook_f16x2.  Code of
  * token t, dimension d of a (batch, KV head) row is the bits-wide field at

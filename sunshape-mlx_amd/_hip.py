@@ -85,6 +85,11 @@ _SIGNATURES = {
         _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _i64,
                                                      _int]),
+    "ss_decode_attn_sunshape_v": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _c_void_p, _int, _int, _c_void_p, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_attn_grouped_il": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                          _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
@@ -444,6 +449,70 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
     return out
 
 
+def _buffer_args(buf_keys, buf_values, buf_len: int, b_: int, hkv: int, d: int):
+    """(keys, values, dtype code, strides) of a hybrid buffer for the
+    transformed-basis decodes; Nones and zeros when nothing is buffered."""
+    if buf_len <= 0:
+        return None, None, 0, 0, 0, 0
+    require_gpu(buf_keys, buf_values)
+    for name, tb in (("buf_keys", buf_keys), ("buf_values", buf_values)):
+        if tb.dim() != 4 or tb.shape[0] != b_ or tb.shape[1] != hkv or tb.shape[3] != d or \
+                tb.shape[2] < buf_len or tb.stride(3) != 1:
+            raise ValueError(f"{name} must be (B, n_kv_heads, >= {buf_len}, {d}) with unit "
+                             "element stride")
+    if buf_keys.stride() != buf_values.stride() or buf_keys.dtype != buf_values.dtype:
+        raise ValueError("buffer keys and values must share dtype and strides")
+    bsb, bsh, bst = buf_keys.stride()[:3]
+    return buf_keys, buf_values, dtype_code(buf_keys.dtype), bsb, bsh, bst
+
+
+def decode_attn_sunshape_v(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                           centroids: torch.Tensor, idx: torch.Tensor, v_idx: torch.Tensor,
+                           v_centroids: torch.Tensor, v_transform: torch.Tensor, t_kv: int,
+                           causal: bool = False, q_offset: int = 0,
+                           out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                           n_splits: int = 0, buf_keys: torch.Tensor | None = None,
+                           buf_values: torch.Tensor | None = None,
+                           buf_len: int = 0) -> torch.Tensor:
+    """Fused decode over SunShape block-VQ values: ``v_idx`` (B, Hkv, cap,
+    D / bd) uint8, ``v_centroids`` (D / bd, nc, bd) float32, ``v_transform``
+    (D, D) float32 taking a codec-space row to the original basis.  Buffered
+    tokens join the softmax as in :func:`decode_attn_turboquant`."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(v_idx, v_centroids, v_transform)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if v_centroids.dim() != 3 or v_centroids.dtype != torch.float32 or \
+            not v_centroids.is_contiguous():
+        raise ValueError("v_centroids must be contiguous float32 (n_blocks, n_centroids, block_dim)")
+    nbv, vnc, vbd = v_centroids.shape
+    if nbv * vbd != d:
+        raise ValueError(f"value codebook covers {nbv * vbd} dims, head_dim is {d}")
+    if v_idx.dtype != torch.uint8 or v_idx.dim() != 4 or not v_idx.is_contiguous() or \
+            tuple(v_idx.shape) != (b_, hkv, cap, nbv):
+        raise ValueError(f"v_idx must be contiguous uint8 {(b_, hkv, cap, nbv)}")
+    if v_transform.dtype != torch.float32 or not v_transform.is_contiguous() or \
+            tuple(v_transform.shape) != (d, d):
+        raise ValueError(f"v_transform must be contiguous float32 ({d}, {d})")
+    nc = centroids.shape[1]
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    buf_len = int(buf_len)
+    buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
+                                                            b_, hkv, d)
+    lib = load_library()
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
+                                                        int(n_splits))
+    ws = decode_workspace(q.device, ws_bytes)
+    check(lib.ss_decode_attn_sunshape_v(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
+        nb, nc, ptr(idx), ptr(v_idx), ptr(v_centroids), vbd, vnc, ptr(v_transform), cap,
+        int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh, bst, buf_len,
+        int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
+    return out
+
+
 def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                            centroids: torch.Tensor, idx: torch.Tensor, packed: torch.Tensor,
                            norms: torch.Tensor, levels, rotation: torch.Tensor, bits: int,
@@ -480,20 +549,8 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     if out is None:
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     buf_len = int(buf_len)
-    if buf_len > 0:
-        require_gpu(buf_keys, buf_values)
-        for name, tb in (("buf_keys", buf_keys), ("buf_values", buf_values)):
-            if tb.dim() != 4 or tb.shape[0] != b_ or tb.shape[1] != hkv or tb.shape[3] != d or \
-                    tb.shape[2] < buf_len or tb.stride(3) != 1:
-                raise ValueError(f"{name} must be (B, n_kv_heads, >= {buf_len}, {d}) with unit "
-                                 "element stride")
-        if buf_keys.stride() != buf_values.stride() or buf_keys.dtype != buf_values.dtype:
-            raise ValueError("buffer keys and values must share dtype and strides")
-        bsb, bsh, bst = buf_keys.stride()[:3]
-        bdt = dtype_code(buf_keys.dtype)
-    else:
-        buf_keys = buf_values = None
-        bsb = bsh = bst = bdt = 0
+    buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
+                                                            b_, hkv, d)
     lib = load_library()
     ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
                                                         int(n_splits))

@@ -56,9 +56,11 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return None
     codec = cache.codec
     buffered = cache.buffer_offset if isinstance(cache, HybridSunShapeKVCache) else 0
-    # the buffer joins the fused softmax on the grouped interleaved and the
-    # TurboQuant kernels, whose buffer scores use the unrotated query
-    if buffered and (ops["kind"] not in ("grouped_il", "turboquant") or codec.use_rotation):
+    # the buffer joins the fused softmax on the grouped interleaved,
+    # TurboQuant and SunShape-value kernels, whose buffer scores use the
+    # unrotated query
+    if buffered and (ops["kind"] not in ("grouped_il", "turboquant", "sunshape_v")
+                     or codec.use_rotation):
         return None
     q, kscale, perm = _kernel_query(codec, queries, scale)
     t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
@@ -85,6 +87,13 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
                                               buf_len=buffered, **kw)
             codec.last_score_backend = ("hip_fused_turboquant_buffer" if buffered
                                         else "hip_fused_turboquant")
+        elif ops["kind"] == "sunshape_v":
+            out = _hip.decode_attn_sunshape_v(q, kscale, perm, codec.centroids, ops["idx"],
+                                              ops["v_idx"], ops["v_centroids"], ops["v_transform"],
+                                              buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
+                                              buf_len=buffered, **kw)
+            codec.last_score_backend = ("hip_fused_sunshape_v_buffer" if buffered
+                                        else "hip_fused_sunshape_v")
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
                                            ops["packed"], ops["scales"], ops["zeros"],

@@ -551,8 +551,9 @@ class HybridSunShapeKVCache:
 
     def fused_operands(self) -> dict | None:
         """Full-capacity compressed buffers for the fused decode kernels
-        ({"kind": "grouped_il"|"grouped"|"turboquant"|"dense", ...}); None when there is nothing
-        compressed or the value backend has no fused kernel."""
+        ({"kind": "grouped_il"|"grouped"|"turboquant"|"sunshape_v"|"dense", ...});
+        None when there is nothing compressed or the value backend has no
+        fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
             return None
         if self.value_backend == "grouped" and self._values_il is not None:
@@ -573,6 +574,13 @@ class HybridSunShapeKVCache:
             return {"kind": "turboquant", "idx": self._key_indices,
                     "packed": self._values_packed, "norms": self._value_norms,
                     "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits,
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+        if self.value_backend == "sunshape" and self._value_indices is not None \
+                and self.value_codec.n_centroids <= 256:
+            vc = self.value_codec
+            return {"kind": "sunshape_v", "idx": self._key_indices, "v_idx": self._value_indices,
+                    "v_centroids": vc.centroids.float().contiguous(),
+                    "v_transform": vc.kernel_value_transform(),
                     "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}

@@ -288,6 +288,33 @@ class SunShapeBlockCodec:
         e = self.E.reshape(nb, bd, nb, bd)
         return torch.stack([e[b, :, b, :] for b in range(nb)])  # (nb, bd, bd)
 
+    def kernel_value_transform(self) -> torch.Tensor:
+        """(D, D) float32 matrix taking a codec-space row to the original
+        basis, ``x_orig = x_codec @ M`` (the inverse permutation as a 0/1
+        matrix, the rotation, or the identity): the last step of the fused
+        decode over values quantised with this codec.  Rebuilt when the
+        transform changes."""
+        if self.mode in PERM_MODES:
+            src = self.inv_permutation
+        elif self.use_rotation:
+            src = self.rotation
+        else:
+            src = None
+        key = (self.mode, None if src is None else (src.data_ptr(), src._version), str(self.device))
+        cached = getattr(self, "_kernel_value_transform", None)
+        if cached is None or cached[0] != key:
+            d = self.head_dim
+            if self.mode in PERM_MODES:
+                m = torch.zeros((d, d), dtype=torch.float32, device=self.device)
+                m[self.inv_permutation.long(), torch.arange(d, device=self.device)] = 1.0
+            elif self.use_rotation:
+                m = self.rotation.float().contiguous()
+            else:
+                m = torch.eye(d, dtype=torch.float32, device=self.device)
+            cached = (key, m)
+            self._kernel_value_transform = cached
+        return cached[1]
+
     def kernel_codebook(self) -> torch.Tensor:
         """The centroids as the split-fp16 buffer read by the matrix-core LUT
         build of the fused fp16-value decode, prepared once and rebuilt when

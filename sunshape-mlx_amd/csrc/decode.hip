@@ -232,6 +232,60 @@ struct VTurbo {
     }
 };
 
+// SunShape block-VQ values (value backend "sunshape", reference
+// cache.py:614-623, 785-800): per token NBV = D / BD uint8 centroid indices
+// of BD-dim blocks in the value codec's basis.  A lane takes 16 consecutive
+// codec dims (16 / BD blocks, one 4- or 2-byte index group) and gathers their
+// float32 centroids (an L2-resident codebook); accumulation runs in the codec
+// basis and the transform back to the original basis (inverse permutation or
+// rotation, as a D x D matrix) is applied per output row after the merge.
+template <int D, int BD>
+struct VSunV {
+    static constexpr int DPL = 16;
+    static constexpr int BPL = DPL / BD;  // blocks per lane
+    static constexpr int NBV = D / BD;
+    static constexpr int LPT = D / DPL;
+    static constexpr int TPI = kWave / LPT;
+    static constexpr int ITERS = kWave / TPI;
+    static_assert(BD == 4 || BD == 8, "value block_dim 4 or 8");
+    struct Args {
+        const uint8_t *idx;  // [rows][NBV]
+        const float *cb;     // [NBV][n_centroids][BD]
+        int n_centroids;
+    };
+    struct Raw {
+        uint32_t w;
+    };
+    __device__ static __forceinline__ Raw load(const Args &a, int64_t row, int lt, bool ok) {
+        Raw r{0u};
+        if (ok) {
+            const uint8_t *p = a.idx + row * NBV + lt * BPL;
+            if constexpr (BPL == 4)
+                r.w = *reinterpret_cast<const uint32_t *>(p);
+            else
+                r.w = *reinterpret_cast<const uint16_t *>(p);
+        }
+        return r;
+    }
+    __device__ static __forceinline__ void decode(const Args &a, const Raw &r, int lt, float *x) {
+#pragma unroll
+        for (int i = 0; i < BPL; ++i) {
+            const int b = lt * BPL + i;
+            const uint32_t cc = (r.w >> (8 * i)) & 0xffu;
+            const float4 *p =
+                reinterpret_cast<const float4 *>(a.cb + ((int64_t)b * a.n_centroids + cc) * BD);
+#pragma unroll
+            for (int h = 0; h < BD / 4; ++h) {
+                const float4 v = p[h];
+                x[i * BD + 4 * h + 0] = v.x;
+                x[i * BD + 4 * h + 1] = v.y;
+                x[i * BD + 4 * h + 2] = v.z;
+                x[i * BD + 4 * h + 3] = v.w;
+            }
+        }
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Index rows: NB bytes per token (16 for head_dim 128, 8 for 64).
 // ---------------------------------------------------------------------------
@@ -2376,6 +2430,79 @@ extern "C" size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_he
     return turboquant_ws_bytes(with_buffer_slot(s, t_buf), batch * n_q_heads * t_q, head_dim);
 }
 
+// Shared host side of the decodes whose values accumulate in a transformed
+// basis (TurboQuant's rotation, a SunShape value codec's permutation or
+// rotation): the VALU decode writes y (fp32, that basis) or split partials;
+// buffered original-basis tokens become one more partial, taken into that
+// basis with transform^T (orthogonal); the merge launch, or rotate_rows_kernel
+// for a single split, writes out = y @ transform in out_dtype.
+template <class MainLaunch>
+static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq, int hkv,
+                              int64_t t_q, int head_dim, float scale, const int32_t *perm,
+                              const float *centroids, int n_centroids, const uint8_t *idx,
+                              int64_t cap, int64_t t_kv, const float *transform,
+                              const void *k_buf, const void *v_buf, int buf_dtype,
+                              int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
+                              int causal, int64_t q_offset, void *out, int out_dtype,
+                              void *workspace, size_t workspace_bytes, int n_splits,
+                              void *stream, MainLaunch &&launch_main) {
+    SS_REQUIRE(transform && ((uintptr_t)transform % 4) == 0,
+               "null or misaligned transform/rotation matrix");
+    SS_REQUIRE(t_buf >= 0, "negative buffer length");
+    if (t_buf > 0) {
+        SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
+        SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
+                   "buffer dtype must be f16, bf16 or f32");
+        SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
+                   "buffer strides must be non-negative, token stride >= head_dim");
+    }
+    const DecodeShape s = decode_shape(batch, hq, hkv, t_q, t_kv, n_splits);
+    const DecodeShape sw = with_buffer_slot(s, t_buf);  // partial slots incl. the buffer's
+    const int64_t rows = batch * hq * t_q;
+    const size_t need = turboquant_ws_bytes(sw, rows, head_dim);
+    if (!workspace || workspace_bytes < need) {
+        set_error("decode workspace too small: need %zu bytes, got %zu", need,
+                  workspace ? workspace_bytes : (size_t)0);
+        return SS_ERR_WORKSPACE;
+    }
+    SS_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
+    float *y = reinterpret_cast<float *>(static_cast<char *>(workspace) + need -
+                                         (size_t)rows * head_dim * sizeof(float));
+    DecodeCommon c;
+    int rc = fill_common(c, sw, q, q_dtype, hq, hkv, t_q, scale, perm, centroids, n_centroids,
+                         idx, cap, t_kv, causal, q_offset, y, SS_F32, workspace, workspace_bytes,
+                         head_dim);
+    if (rc) return rc;
+    c.tiles_per_split = s.tiles_per_split;  // the compressed tokens' splits: grid s.S
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    rc = launch_main(c, s, st);  // no merge: it follows the buffer's partial
+    if (rc) return rc;
+    if (t_buf > 0) {
+#define SS_BUFP(DD, RR)                                                                       \
+    hipLaunchKernelGGL((buffer_partial_kernel<DD, RR>), dim3(sw.n_cols), dim3(256), 0, st, c,   \
+                       k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, transform, s.S)
+        if (head_dim == 128) {
+            if (sw.R == 1) SS_BUFP(128, 1); else SS_BUFP(128, 4);
+        } else {
+            if (sw.R == 1) SS_BUFP(64, 1); else SS_BUFP(64, 4);
+        }
+#undef SS_BUFP
+        SS_LAUNCH_CHECK("buffer_partial_kernel launch");
+    }
+    if (sw.S > 1)
+        return head_dim == 128 ? launch_merge<128>(c, sw, st, transform, out, out_dtype)
+                               : launch_merge<64>(c, sw, st, transform, out, out_dtype);
+    const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
+    if (head_dim == 128)
+        hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, transform,
+                           rows, out, out_dtype);
+    else
+        hipLaunchKernelGGL(rotate_rows_kernel<64>, dim3(blocks), dim3(256), 0, st, y, transform,
+                           rows, out, out_dtype);
+    SS_LAUNCH_CHECK("rotate_rows_kernel launch");
+    return SS_OK;
+}
+
 extern "C" int ss_decode_attn_turboquant(
     const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
     int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
@@ -2391,77 +2518,67 @@ extern "C" int ss_decode_attn_turboquant(
     SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4 (got %d)", bits);
     SS_REQUIRE(!(bits == 2 && head_dim % 16) && !(bits == 4 && head_dim % 8),
                "head_dim %d cannot be packed at %d bits", head_dim, bits);
-    SS_REQUIRE(((uintptr_t)packed % 4) == 0 && ((uintptr_t)norms % 4) == 0 &&
-                   ((uintptr_t)rotation % 4) == 0,
-               "packed/norms/rotation must be 4-byte aligned");
-    SS_REQUIRE(t_buf >= 0, "negative buffer length");
-    if (t_buf > 0) {
-        SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
-        SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
-                   "buffer dtype must be f16, bf16 or f32");
-        SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
-                   "buffer strides must be non-negative, token stride >= head_dim");
+    SS_REQUIRE(((uintptr_t)packed % 4) == 0 && ((uintptr_t)norms % 4) == 0,
+               "packed/norms must be 4-byte aligned");
+    auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
+#define SS_TURBO(DD, BB)                                                    \
+    {                                                                       \
+        typename VTurbo<DD, BB>::Args va{packed, norms, {}};                \
+        for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];           \
+        return launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, false);           \
     }
-    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
-    const DecodeShape sw = with_buffer_slot(s, t_buf);  // partial slots incl. the buffer's
-    const int64_t rows = batch * n_q_heads * t_q;
-    const size_t need = turboquant_ws_bytes(sw, rows, head_dim);
-    if (!workspace || workspace_bytes < need) {
-        set_error("decode workspace too small: need %zu bytes, got %zu", need,
-                  workspace ? workspace_bytes : (size_t)0);
-        return SS_ERR_WORKSPACE;
-    }
-    SS_REQUIRE(((uintptr_t)workspace % 256) == 0, "workspace must be 256-byte aligned");
-    float *y = reinterpret_cast<float *>(static_cast<char *>(workspace) + need -
-                                         (size_t)rows * head_dim * sizeof(float));
-    // the attention output in the rotated basis goes to y (fp32), then
-    // out = y @ R in out_dtype
-    DecodeCommon c;
-    rc = fill_common(c, sw, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
-                     n_centroids, idx, cap, t_kv, causal, q_offset, y, SS_F32, workspace,
-                     workspace_bytes, head_dim);
-    if (rc) return rc;
-    c.tiles_per_split = s.tiles_per_split;  // the compressed tokens' splits: grid s.S
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // with several partial slots the merge launch also applies the rotation
-    // (after the buffer's partial, if any); a single split writes y here
-#define SS_TURBO(DD, BB)                                                   \
-    {                                                                      \
-        typename VTurbo<DD, BB>::Args va{packed, norms, {}};               \
-        for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];          \
-        rc = launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, false);            \
-    }
-    if (head_dim == 128) {
-        if (bits == 2) SS_TURBO(128, 2) else if (bits == 3) SS_TURBO(128, 3) else SS_TURBO(128, 4)
-    } else {
-        if (bits == 2) SS_TURBO(64, 2) else if (bits == 3) SS_TURBO(64, 3) else SS_TURBO(64, 4)
-    }
-#undef SS_TURBO
-    if (rc) return rc;
-    if (t_buf > 0) {
-#define SS_BUFP(DD, RR)                                                                       \
-    hipLaunchKernelGGL((buffer_partial_kernel<DD, RR>), dim3(sw.n_cols), dim3(256), 0, st, c,   \
-                       k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, rotation, s.S)
         if (head_dim == 128) {
-            if (sw.R == 1) SS_BUFP(128, 1); else SS_BUFP(128, 4);
-        } else {
-            if (sw.R == 1) SS_BUFP(64, 1); else SS_BUFP(64, 4);
+            if (bits == 2) SS_TURBO(128, 2)
+            if (bits == 3) SS_TURBO(128, 3)
+            SS_TURBO(128, 4)
         }
-#undef SS_BUFP
-        SS_LAUNCH_CHECK("buffer_partial_kernel launch");
+        if (bits == 2) SS_TURBO(64, 2)
+        if (bits == 3) SS_TURBO(64, 3)
+        SS_TURBO(64, 4)
+#undef SS_TURBO
+    };
+    return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                              centroids, n_centroids, idx, cap, t_kv, rotation, k_buf, v_buf,
+                              buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
+                              out_dtype, workspace, workspace_bytes, n_splits, stream, main);
+}
+
+extern "C" int ss_decode_attn_sunshape_v(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint8_t *v_idx, const float *v_centroids,
+    int v_block_dim, int v_n_centroids, const float *v_transform, int64_t cap, int64_t t_kv,
+    const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
+    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(v_idx && v_centroids, "null value indices/centroids");
+    SS_UNSUPPORTED(v_block_dim == 4 || v_block_dim == 8, "value block_dim %d unsupported (4 or 8)",
+                   v_block_dim);
+    SS_UNSUPPORTED(v_n_centroids >= 1 && v_n_centroids <= 256,
+                   "value n_centroids %d unsupported (1..256, uint8 indices)", v_n_centroids);
+    SS_REQUIRE(((uintptr_t)v_idx % 4) == 0, "value indices must be 4-byte aligned");
+    SS_REQUIRE(((uintptr_t)v_centroids % 16) == 0, "value centroids must be 16-byte aligned");
+    auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
+#define SS_SUNV(DD, BB)                                                     \
+    {                                                                       \
+        typename VSunV<DD, BB>::Args va{v_idx, v_centroids, v_n_centroids}; \
+        return launch_r<DD, VSunV<DD, BB>>(c, va, s, st, false);            \
     }
-    if (sw.S > 1)
-        return head_dim == 128 ? launch_merge<128>(c, sw, st, rotation, out, out_dtype)
-                               : launch_merge<64>(c, sw, st, rotation, out, out_dtype);
-    const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
-    if (head_dim == 128)
-        hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, rotation,
-                           rows, out, out_dtype);
-    else
-        hipLaunchKernelGGL(rotate_rows_kernel<64>, dim3(blocks), dim3(256), 0, st, y, rotation,
-                           rows, out, out_dtype);
-    SS_LAUNCH_CHECK("rotate_rows_kernel launch");
-    return SS_OK;
+        if (head_dim == 128) {
+            if (v_block_dim == 4) SS_SUNV(128, 4)
+            SS_SUNV(128, 8)
+        }
+        if (v_block_dim == 4) SS_SUNV(64, 4)
+        SS_SUNV(64, 8)
+#undef SS_SUNV
+    };
+    return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                              centroids, n_centroids, idx, cap, t_kv, v_transform, k_buf, v_buf,
+                              buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
+                              out_dtype, workspace, workspace_bytes, n_splits, stream, main);
 }
 
 extern "C" int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,

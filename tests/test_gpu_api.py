@@ -263,12 +263,13 @@ def test_hybrid_fp16_and_sunshape_value_backends():
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
-    # SunShape-coded values: no fused kernel, two-pass over dequantised values
+    # SunShape-coded values: the fused decode over gathered value centroids
     vcodec = make_codec(12)
     cache3 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="sunshape", value_bits=8,
                                value_codec=vcodec, buffer_size=0)
     cache3.update_and_fetch(k, v)
     out3 = S.sunshape_sdpa(q, cache3, 0.088)
+    assert codec.last_score_backend == "hip_fused_sunshape_v"
     vals = cache3.values.float().cpu().numpy()
     ref3 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                            codec.centroids.cpu().numpy(), cache3.key_indices.cpu().numpy(), None,
@@ -366,6 +367,41 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
     rec = tc.dequantize(cache._values_packed[:, :, :n].reshape(-1, tc.packed_dim),
                         cache._value_norms[:, :, :n].reshape(-1)).cpu().numpy()
     assert rel_err(rec.reshape(vals.shape), vals) <= 1e-5
+
+
+@pytest.mark.parametrize("vbd,buffer_size", [(4, 0), (8, 128)])
+def test_hybrid_sunshape_values_fused_decode(vbd, buffer_size):
+    """A hybrid cache with SunShape (block-VQ) values decodes in the fused
+    kernel, with or without buffered tokens, and equals the oracle SDPA over
+    the oracle's dequantisation of the cache's own value indices."""
+    codec = make_codec(40 + vbd)
+    rng = np.random.default_rng(vbd)
+    d = 128
+    vcodec = S.SunShapeBlockCodec(d, block_dim=vbd, n_centroids=256, device=DEV)
+    vcodec.load_state_dict({"centroids": rng.standard_normal((d // vbd, 256, vbd)).astype(np.float32),
+                            "permutation": rng.permutation(d).astype(np.int32)})
+    b, hq, hkv, n = 2, 8, 2, 400
+    k, v = kv(41 + vbd, b, hkv, n, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="sunshape", value_bits=8,
+                              value_codec=vcodec, buffer_size=buffer_size)
+    cache.update_and_fetch(k, v)
+    nc, nbuf = cache.compressed_offset, cache.buffer_offset
+    assert nbuf == buffer_size and nc == n - buffer_size
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    assert codec.last_score_backend == ("hip_fused_sunshape_v_buffer" if buffer_size
+                                        else "hip_fused_sunshape_v")
+    vi = cache._value_indices[:, :, :nc].cpu().numpy()
+    inv = vcodec.inv_permutation.cpu().numpy()
+    vals = np.stack([np.stack([O.dequantize_blockvq(vi[bi, hi], vcodec.centroids.cpu().numpy(), inv)
+                               for hi in range(hkv)]) for bi in range(b)])
+    vals_all = np.concatenate([vals, v[:, :, nc:].float().cpu().numpy()], axis=2)
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
+                          cache.buffer_keys.float().cpu().numpy() if nbuf else None, vals_all)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the cache's own (two-pass) value read-back agrees with the oracle
+    assert rel_err(cache.values[:, :, :nc].float().cpu().numpy(), vals) <= 1e-3
 
 
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():

@@ -569,3 +569,51 @@ def test_decode_turboquant_with_buffer(b, hq, hkv, d, t_kv, t_buf, t_q, bits, sp
     ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
                           mask="causal" if causal else None)
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,t_q,bd,vnc,transform,splits", [
+    (1, 32, 8, 128, 2048, 0, 1, 4, 256, "perm", 0),     # config-5 value codec (block_dim 4)
+    (2, 8, 2, 128, 700, 128, 1, 8, 256, "perm", 0),     # block_dim 8, with a buffer
+    (1, 8, 2, 64, 513, 0, 1, 4, 100, "rot", 3),         # head_dim 64, rotated codec, 100 centroids
+    (2, 6, 2, 128, 300, 20, 5, 8, 256, "rot", 1),       # prefill rows, causal across the buffer
+])
+def test_decode_sunshape_v_matches_oracle(b, hq, hkv, d, t_kv, t_buf, t_q, bd, vnc, transform,
+                                          splits):
+    """ss_decode_attn_sunshape_v: values given as block-VQ indices of a value
+    codec (gathered centroids taken back to the original basis by the codec's
+    inverse permutation or rotation) equal the oracle SDPA over the oracle's
+    block-VQ dequantisation."""
+    cap = max(((t_kv + 15) // 16) * 16, 16)
+    cents, perm, idx, _, q = decode_case(80 + bd + t_kv, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(bd * 100 + t_buf)
+    nbv = d // bd
+    v_cents = rng.standard_normal((nbv, vnc, bd)).astype(np.float32)
+    v_idx = rng.integers(0, vnc, (b, hkv, cap, nbv)).astype(np.uint8)
+    if transform == "perm":
+        vperm = rng.permutation(d).astype(np.int32)
+        inv = O.invert_permutation(vperm)
+        m = np.zeros((d, d), np.float32)
+        m[inv, np.arange(d)] = 1.0
+    else:
+        inv = None
+        m = O.rotation_matrix(d, 5)
+    kb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    scale = 1.0 / np.sqrt(d)
+    causal = t_q > 1
+    total = t_kv + t_buf
+    out = _hip.decode_attn_sunshape_v(t(q), scale, t(perm), t(cents), t(idx), t(v_idx),
+                                      t(v_cents), t(m), t_kv, causal=causal,
+                                      q_offset=total - t_q if causal else 0,
+                                      out_dtype=torch.float32, n_splits=splits,
+                                      buf_keys=t(kb), buf_values=t(vb), buf_len=t_buf)
+    torch.cuda.synchronize()
+    vals = np.zeros((b, hkv, total, d), np.float64)
+    for bi in range(b):
+        for hi in range(hkv):
+            kc = O.dequantize_blockvq(v_idx[bi, hi, :t_kv], v_cents, inv)
+            vals[bi, hi, :t_kv] = kc if inv is not None else kc.astype(np.float64) @ m
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                          mask="causal" if causal else None)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
