@@ -53,12 +53,14 @@ def parse_args():
                    help="budget for the CPU baseline (0 disables it)")
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                           "decode_fp16v_t32k_traffic.json"))
-    p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant"),
+    p.add_argument("--layers", type=int, default=28, help="config5: decoder layers per step")
+    p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5"),
                    default="metric",
                    help="metric: the BASELINE metric decode (fp16 values, B=1); hybrid: config 4 "
                         "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
                         "(65,536 fp16 keys block-VQ encoded); turboquant: the config-4 shape "
-                        "with 2-bit TurboQuant values")
+                        "with 2-bit TurboQuant values; config5: 28 layers x B=16, "
+                        "T_kv=131072, mixed-precision keys, SunShape values")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a plain device copy of MB megabytes --steps times (the "
                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -303,6 +305,117 @@ def run_turboquant(args) -> int:
     return 0
 
 
+def run_config5(args) -> int:
+    """Config 5: one decode step of a 28-layer Qwen-style 4B model's attention
+    (32 query / 8 KV heads, D=128, B=16, T_kv=131072 per layer).  Keys: 16
+    uint8 indices per token of a profileperm_mixed_precision codec with its 4
+    heavy blocks' centroids zero (the reference's semantics: heavy blocks
+    contribute nothing to the scores); values: SunShape block-VQ, block_dim 4,
+    256 centroids (32 index bytes per token), permutation transform.  Random
+    N(0,1) codebooks and uniform indices; 28 distinct layer caches (22.5 GB),
+    one ss_decode_attn_sunshape_v call per layer."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    lib = hip.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    layers = args.layers
+    b, hq, hkv, d, t_kv, nb, vbd = 16, 32, 8, 128, args.t_kv, 16, 4
+    nbv = d // vbd
+    scale = 1.0 / math.sqrt(d)
+    g = torch.Generator(device=dev).manual_seed(5)
+    cents = torch.randn((nb, 256, 8), generator=g, device=dev)
+    heavy = torch.randperm(nb, generator=g, device=dev)[:4]
+    cents[heavy] = 0.0  # mixed-precision heavy blocks: zero centroids (reference semantics)
+    perm = torch.randperm(d, generator=g, device=dev).to(torch.int32)
+    v_cents = torch.randn((nbv, 256, vbd), generator=g, device=dev)
+    vperm = torch.randperm(d, generator=g, device=dev)
+    inv = torch.argsort(vperm)
+    v_transform = torch.zeros((d, d), dtype=torch.float32, device=dev)
+    v_transform[inv, torch.arange(d, device=dev)] = 1.0
+    caches = []
+    for _ in range(layers):
+        caches.append((torch.randint(0, 256, (b, hkv, t_kv, nb), generator=g, device=dev,
+                                     dtype=torch.uint8),
+                       torch.randint(0, 256, (b, hkv, t_kv, nbv), generator=g, device=dev,
+                                     dtype=torch.uint8)))
+    q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
+    torch.cuda.synchronize()
+    per_layer = b * hkv * t_kv * (nb + nbv)
+    log(f"config 5 caches ready: {layers} layers x {per_layer / 1e6:.1f} MB")
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b, hq, hkv, 1, d, t_kv, 0, args.splits)
+    splits = lib.ss_decode_default_splits(b, hq, hkv, 1, d, t_kv) if args.splits <= 0 else args.splits
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out = torch.empty((b, hq, 1, d), dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.ss_decode_attn_sunshape_v
+    argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cents.data_ptr(),
+             nb, 256, ki.data_ptr(), vi.data_ptr(), v_cents.data_ptr(), vbd, 256,
+             v_transform.data_ptr(), t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0, out.data_ptr(),
+             hip.SS_F16, ws.data_ptr(), ws_bytes, args.splits, stream) for ki, vi in caches]
+
+    def step():
+        for a in argv:
+            rc = fn(*a)
+            if rc:
+                hip.check(rc)
+
+    steps, warmup = max(1, args.steps // 20), max(1, args.warmup // 10)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    nbytes = layers * (per_layer + b * hq * d * 4)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"config 5: {us:.1f} us/step ({us / layers:.1f} us/layer), {gbs:.1f} GB/s")
+
+    check = None
+    if args.cpu_seconds > 0:  # output check of one (b, KV head) of layer 0 against the oracle
+        from oracle import sunshape_oracle as O
+
+        hip.check(fn(*argv[0]))
+        torch.cuda.synchronize()
+        bi, hi = 11, 3
+        ki, vi = caches[0]
+        vals = O.dequantize_blockvq(vi[bi, hi].cpu().numpy(), v_cents.cpu().numpy(),
+                                    inv.cpu().numpy())
+        qh = q[bi:bi + 1, hi * 4:(hi + 1) * 4].cpu().numpy()
+        ref = O.sdpa(qh, ki[bi:bi + 1, hi:hi + 1].cpu().numpy(), vals[None, None],
+                     cents.cpu().numpy(), perm.cpu().numpy(), scale)
+        got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
+        check = float(np.abs(got - ref).max() / np.abs(ref).max())
+
+    line = {
+        "metric": "28-layer decode step attention µs/step and achieved HBM GB/s (config 5)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(us * 1e-3, 6), "us_per_step": round(us, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{layers} layers x decode B=16 Hq=32 Hkv=8 D=128 T_kv={t_kv}, "
+                               "mixed-precision keys (16 u8 indices, 4 heavy blocks zero), "
+                               "SunShape values block_dim 4 / 256 centroids (32 u8 indices), "
+                               "fp16 query/output",
+                   "t_kv": t_kv, "layers": layers, "splits": splits,
+                   "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "check_max_rel_err_vs_oracle": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 VALU_FP32_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMD x 16 lanes x 2 flops x 2.4 GHz, no packed fp32
 
 
@@ -390,6 +503,10 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, args.steps)
     if args.workload == "hybrid":
         return run_hybrid(args)
+    if args.workload == "config5":
+        if args.t_kv == 32768 and "--t-kv" not in sys.argv:
+            args.t_kv = 131072
+        return run_config5(args)
     if args.workload == "turboquant":
         return run_turboquant(args)
     if args.workload == "encode":
