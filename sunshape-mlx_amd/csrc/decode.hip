@@ -234,28 +234,36 @@ struct VTurbo {
 
 // SunShape block-VQ values (value backend "sunshape", reference
 // cache.py:614-623, 785-800): per token NBV = D / BD uint8 centroid indices
-// of BD-dim blocks in the value codec's basis.  A lane takes 16 consecutive
-// codec dims (16 / BD blocks, one 4- or 2-byte index group) and gathers their
-// float32 centroids (an L2-resident codebook); accumulation runs in the codec
-// basis and the transform back to the original basis (inverse permutation or
-// rotation, as a D x D matrix) is applied per output row after the merge.
+// of BD-dim blocks in the value codec's basis.  The value codebook is staged
+// in LDS beside the key LUT: a workgroup takes one slab of the head dim
+// (kSlabs slabs, at most 64 KB of float32 centroids each, so D = 128 runs as
+// two workgroups per split and column that share the scores and split the
+// dims).  A lane takes 16 consecutive codec dims of its slab (16 / BD blocks,
+// one 4- or 2-byte index group) and reads their centroids from LDS;
+// accumulation runs in the codec basis and the transform back to the
+// original basis (inverse permutation or rotation, as a D x D matrix) is
+// applied per output row after the merge.
 template <int D, int BD>
 struct VSunV {
+    static constexpr int kSlabs = D * 256 * 4 > 65536 ? 2 : 1;
+    static constexpr int DS = D / kSlabs;            // dims of one workgroup
+    static constexpr int kLdsBytes = DS * 256 * 4;   // this slab's centroids, 256 per block
     static constexpr int DPL = 16;
     static constexpr int BPL = DPL / BD;  // blocks per lane
-    static constexpr int NBV = D / BD;
-    static constexpr int LPT = D / DPL;
+    static constexpr int NBV = D / BD, NBVS = DS / BD;
+    static constexpr int LPT = DS / DPL;
     static constexpr int TPI = kWave / LPT;
     static constexpr int ITERS = kWave / TPI;
     static_assert(BD == 4 || BD == 8, "value block_dim 4 or 8");
     struct Args {
         const uint8_t *idx;  // [rows][NBV]
-        const float *cb;     // [NBV][n_centroids][BD]
+        const float *cb;     // [NBV][n_centroids][BD], n_centroids <= 256
         int n_centroids;
     };
     struct Raw {
         uint32_t w;
     };
+    // lt: lane group over the whole head dim (slab * LPT + lane group)
     __device__ static __forceinline__ Raw load(const Args &a, int64_t row, int lt, bool ok) {
         Raw r{0u};
         if (ok) {
@@ -267,16 +275,31 @@ struct VSunV {
         }
         return r;
     }
-    __device__ static __forceinline__ void decode(const Args &a, const Raw &r, int lt, float *x) {
+    // the slab's centroids -> lds [NBVS][256][BD] (entries past n_centroids zero)
+    __device__ static __forceinline__ void stage(float *lds, const Args &a, int slab, int tid,
+                                                 int nt) {
+        float4 *l4 = reinterpret_cast<float4 *>(lds);
+        for (int i = tid; i < NBVS * 256 * BD / 4; i += nt) {
+            const int f = i * 4, bl = f / (256 * BD), within = f - bl * (256 * BD);
+            const int cc = within / BD;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (cc < a.n_centroids)
+                v = *reinterpret_cast<const float4 *>(
+                    a.cb + ((int64_t)(slab * NBVS + bl) * a.n_centroids + cc) * BD + within % BD);
+            l4[i] = v;
+        }
+    }
+    // lt: lane group within the slab
+    __device__ static __forceinline__ void decode_lds(const float *lds, const Args &, const Raw &r,
+                                                      int lt, float *x) {
+        const float4 *l4 = reinterpret_cast<const float4 *>(lds);
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
-            const int b = lt * BPL + i;
-            const uint32_t cc = (r.w >> (8 * i)) & 0xffu;
-            const float4 *p =
-                reinterpret_cast<const float4 *>(a.cb + ((int64_t)b * a.n_centroids + cc) * BD);
+            const int bl = lt * BPL + i;
+            const int cc = (int)((r.w >> (8 * i)) & 0xffu);
 #pragma unroll
             for (int h = 0; h < BD / 4; ++h) {
-                const float4 v = p[h];
+                const float4 v = l4[((bl * 256 + cc) * BD) / 4 + h];
                 x[i * BD + 4 * h + 0] = v.x;
                 x[i * BD + 4 * h + 1] = v.y;
                 x[i * BD + 4 * h + 2] = v.z;
@@ -284,6 +307,25 @@ struct VSunV {
             }
         }
     }
+};
+
+// Dim slabs (workgroups sharing a split and column) and staged LDS bytes of a
+// VALU value format: 1 and 0 unless the format declares kSlabs / kLdsBytes.
+template <class VF, class = void>
+struct VfSlabs {
+    static constexpr int value = 1;
+};
+template <class VF>
+struct VfSlabs<VF, std::void_t<decltype(VF::kSlabs)>> {
+    static constexpr int value = VF::kSlabs;
+};
+template <class VF, class = void>
+struct VfLds {
+    static constexpr int value = 0;
+};
+template <class VF>
+struct VfLds<VF, std::void_t<decltype(VF::kLdsBytes)>> {
+    static constexpr int value = VF::kLdsBytes;
 };
 
 // ---------------------------------------------------------------------------
@@ -325,12 +367,17 @@ __global__ void __launch_bounds__(kDecodeThreads)
     constexpr int CHUNK = ITERS < 16 ? ITERS : 16;
     static_assert(ITERS % CHUNK == 0, "chunking");
     static_assert(kDecodeWaves * R * (D + 2) <= R * NB * kLutStride, "merge scratch");
-
+    // a format may split the head dim over SL workgroups (blockIdx.z) and
+    // stage VLDS bytes of its own in LDS
+    constexpr int SL = VfSlabs<VF>::value, DS = D / SL, VLDS = VfLds<VF>::value;
+    static_assert(LPT * DPL >= DS, "value lanes cover the workgroup's dims");
 
     extern __shared__ __align__(16) float smem[];
     float *lut = smem;                          // [R][NB][kLutStride]
     float *qp = lut + R * NB * kLutStride;      // [R][D]
     float *pbuf = qp + R * D;                   // [waves][64][R]
+    float *vlds = pbuf + kDecodeWaves * kWave * R;  // the format's staged data
+    const int slab = SL > 1 ? (int)blockIdx.z : 0;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -385,6 +432,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
             lut[(r * NB + b) * kLutStride + cc] = dot * kLog2e;
         }
     }
+    if constexpr (VLDS > 0) VF::stage(vlds, va, slab, tid, kDecodeThreads);
     __syncthreads();
 
     // 3. stream this split's tokens, 64 per wave-tile.
@@ -423,7 +471,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
 #pragma unroll
         for (int j = 0; j < CHUNK; ++j) {
             const int64_t tv = t0 + j * TPI + tg;
-            vr[j] = VF::load(va, vrow0 + tv, lt, tv < t_end);
+            vr[j] = VF::load(va, vrow0 + tv, slab * LPT + lt, tv < t_end);
         }
         const int64_t tk = t0 + lane;
         const bool kok = tk < t_end;
@@ -467,7 +515,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
 #pragma unroll
                 for (int j = 0; j < CHUNK; ++j) {
                     const int64_t tv = t0 + (ch + j) * TPI + tg;
-                    vr[j] = VF::load(va, vrow0 + tv, lt, tv < t_end);
+                    vr[j] = VF::load(va, vrow0 + tv, slab * LPT + lt, tv < t_end);
                 }
             }
 #pragma unroll
@@ -485,7 +533,10 @@ __global__ void __launch_bounds__(kDecodeThreads)
                     for (int r = 0; r < R; ++r) pr[r] = pw[tl * R + r];
                 }
                 float x[DPL];
-                VF::decode(va, vr[j], lt, x);
+                if constexpr (VLDS > 0)
+                    VF::decode_lds(vlds, va, vr[j], lt, x);
+                else
+                    VF::decode(va, vr[j], lt, x);
 #pragma unroll
                 for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -510,7 +561,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
     __syncthreads();  // every wave is done with the LUT; reuse it
     float *wm = smem;                        // [waves][R]
     float *wl = wm + kDecodeWaves * R;       // [waves][R]
-    float *wa = wl + kDecodeWaves * R;       // [waves][R][D]
+    float *wa = wl + kDecodeWaves * R;       // [waves][R][DS]
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -524,14 +575,14 @@ __global__ void __launch_bounds__(kDecodeThreads)
 #pragma unroll
             for (int k = 0; k < DPL; ++k) {
                 const int d = lt * DPL + k;
-                if (d < D) wa[(wv * R + r) * D + d] = acc[r][k];
+                if (d < DS) wa[(wv * R + r) * DS + d] = acc[r][k];
             }
     }
     __syncthreads();
 
     const int S = c.n_splits;
-    for (int i = tid; i < R * D; i += kDecodeThreads) {
-        const int r = i / D, d = i - r * D;
+    for (int i = tid; i < R * DS; i += kDecodeThreads) {
+        const int r = i / DS, d = i - r * DS, dd = slab * DS + d;
         float M = -1e30f;
 #pragma unroll
         for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, wm[w * R + r]);
@@ -540,14 +591,15 @@ __global__ void __launch_bounds__(kDecodeThreads)
         for (int w = 0; w < kDecodeWaves; ++w) {
             const float f = fast_exp2(wm[w * R + r] - M);
             L = fmaf(wl[w * R + r], f, L);
-            A = fmaf(wa[(w * R + r) * D + d], f, A);
+            A = fmaf(wa[(w * R + r) * DS + d], f, A);
         }
         if (S == 1) {
-            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + dd, L > 0.f ? A / L : 0.f);
         } else {
             const int64_t slot = ((int64_t)col * S + split) * R + r;
-            c.part_acc[slot * D + d] = A;
-            if (d == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
+            c.part_acc[slot * D + dd] = A;
+            // every slab computes the same (M, L); slab 0 stores them
+            if (dd == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
         }
     }
 }
@@ -2201,7 +2253,7 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
 template <int D, int R, class VF>
 static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
                   hipStream_t st, bool merge = true) {
-    const size_t lds = decode_lds_bytes<D, R>();
+    const size_t lds = decode_lds_bytes<D, R>() + VfLds<VF>::value;
     auto kern = decode_attn_kernel<D, R, VF>;
     static bool attr_set = false;  // per instantiation
     if (!attr_set) {
@@ -2210,7 +2262,7 @@ static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode)");
         attr_set = true;
     }
-    dim3 grid(s.S, s.n_cols);
+    dim3 grid(s.S, s.n_cols, VfSlabs<VF>::value);
     hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), lds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_kernel launch");
     return merge ? launch_merge<D>(c, s, st) : SS_OK;
