@@ -56,6 +56,7 @@ from . import attention, cache, patch, value_codecs  # noqa: E402
 from .attention import sunshape_sdpa  # noqa: E402
 from .cache import HybridSunShapeKVCache, SunShapeKVCache, create_kv_cache  # noqa: E402
 from .value_codecs import GroupedValueCodec, TurboQuantValueCodec, build_value_codec  # noqa: E402
+from .serialize import load_cache, load_codec, save_cache, save_codec  # noqa: E402
 
 __all__ = [
     "SunShapeBlockCodec", "SunShapeQuantized", "SunShapeKVCache", "HybridSunShapeKVCache",
@@ -65,5 +66,5 @@ __all__ = [
     "fused_attention_dequant_causal_hip", "fused_block_vq_attention", "quantize_scalar_to_indices",
     "pack_indices", "unpack_indices", "quantize_values", "dequantize_values", "get_kernel_stats",
     "reset_kernel_stats", "apply_permutation", "invert_permutation", "generate_rotation_matrix",
-    "covariance_block_permutation",
+    "covariance_block_permutation", "save_codec", "load_codec", "save_cache", "load_cache",
 ]
