@@ -381,6 +381,25 @@ int ss_dequantize_blockvq(const uint8_t *idx, int64_t n_tok, int64_t idx_row_str
                           int block_dim, const int32_t *inv_perm, void *out,
                           int out_dtype, void *stream);
 
+/*
+ * Lloyd k-means of every codec block at once (codec fitting on the GPU;
+ * replaces the per-block NumPy k-means of the reference's fit,
+ * codec.py:53-103 called from codec.py:389-392).  One workgroup per block.
+ *   data       float [n_blocks][n_points][block_dim] (block-major, contiguous)
+ *   centroids  float [n_blocks][n_centroids][block_dim]: the initial
+ *              centroids in (the reference draws them as data rows
+ *              RandomState(seed + b).permutation(n)[:K]), the fitted ones out
+ *   assign     uint8 [n_blocks][n_points] final assignments, or NULL
+ * Each iteration: expanded-form float32 distances with first-index argmin,
+ * per-centroid float32 sums in point order divided in double; empty clusters
+ * keep their centroid.  block_dim 4 or 8, n_centroids <= 256 < n_points <=
+ * 131072 (a block with no more points than centroids is the caller's
+ * zero-padded codebook, as in the reference).
+ */
+int ss_kmeans_blocks(const float *data, int n_blocks, int64_t n_points, int block_dim,
+                     int n_centroids, int iters, float *centroids, uint8_t *assign,
+                     void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -85,6 +85,8 @@ _SIGNATURES = {
         _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _i64,
                                                      _int]),
+    "ss_kmeans_blocks": (_int, [_c_void_p, _int, _i64, _int, _int, _int, _c_void_p, _c_void_p,
+                                _c_void_p]),
     "ss_decode_attn_sunshape_v": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _c_void_p, _int, _int, _c_void_p, _i64, _i64,
@@ -447,6 +449,25 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
         dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0, int(n_splits),
         stream_handle(q.device)))
     return out
+
+
+def kmeans_blocks(data: torch.Tensor, init: torch.Tensor, iters: int,
+                  return_assign: bool = False):
+    """Lloyd k-means of every block at once: ``data`` (n_blocks, n, bd)
+    float32, ``init`` (n_blocks, K, bd) float32 initial centroids.  Returns
+    the fitted centroids (and the final uint8 assignments (n_blocks, n))."""
+    require_gpu(data, init)
+    if data.dim() != 3 or init.dim() != 3 or data.shape[0] != init.shape[0] or \
+            data.shape[2] != init.shape[2]:
+        raise ValueError("data (n_blocks, n, bd) and init (n_blocks, K, bd) must agree")
+    data = data.float().contiguous()
+    cents = init.float().contiguous().clone()
+    nb, n, bd = data.shape
+    k = cents.shape[1]
+    assign = torch.empty((nb, n), dtype=torch.uint8, device=data.device) if return_assign else None
+    check(load_library().ss_kmeans_blocks(ptr(data), nb, n, bd, k, int(iters), ptr(cents),
+                                          ptr(assign), stream_handle(data.device)))
+    return (cents, assign) if return_assign else cents
 
 
 def _buffer_args(buf_keys, buf_values, buf_len: int, b_: int, hkv: int, d: int):

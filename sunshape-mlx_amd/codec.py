@@ -241,8 +241,12 @@ class SunShapeBlockCodec:
         return self.permutation if self.mode in PERM_MODES else None
 
     # ------------------------------------------------------------------ fit
-    def fit(self, q_cal, k_cal, kmeans_iters: int = 25, seed: int = 0) -> "SunShapeBlockCodec":
-        """Fit from calibration queries/keys (reference codec.py:299-418)."""
+    def fit(self, q_cal, k_cal, kmeans_iters: int = 25, seed: int = 0,
+            kmeans_device=None) -> "SunShapeBlockCodec":
+        """Fit from calibration queries/keys (reference codec.py:299-418).
+        The per-block k-means runs on ``kmeans_device`` (default: the
+        codec's device): on a GPU every block at once (``ss_kmeans_blocks``),
+        else in NumPy; both start from the reference's initial rows."""
         q = _np(q_cal)
         k = _np(k_cal)
         d, bd, nb = self.head_dim, self.block_dim, self.n_blocks
@@ -263,15 +267,32 @@ class SunShapeBlockCodec:
                 ba, ab = block_affinity_gate(q, bd)
             elif self.mode == "profileperm_mixed_precision":
                 heavy, bmass = mixed_precision_block_mask(q, bd, mass_threshold=0.5)
+        dev = torch.device(kmeans_device) if kmeans_device is not None else self.device
+        active = [b for b in range(nb)
+                  if not (self.mode == "profileperm_mixed_precision" and heavy[b])]
+        ks = {b: k[:, b * bd:(b + 1) * bd] @ E[b * bd:(b + 1) * bd, b * bd:(b + 1) * bd].T
+              for b in active}
+        fitted = {}
+        n_pts = k.shape[0]
+        if dev.type == "cuda" and active and n_pts > self.n_centroids:
+            # reference initial centroids: rows RandomState(seed + b).permutation(N)[:K]
+            init = np.stack([ks[b][np.random.RandomState(seed + b).permutation(n_pts)
+                                   [:self.n_centroids]] for b in active])
+            data = torch.from_numpy(np.ascontiguousarray(np.stack([ks[b] for b in active]),
+                                                         dtype=np.float32)).to(dev)
+            out = _hip.kmeans_blocks(data, torch.from_numpy(init.astype(np.float32)).to(dev),
+                                     kmeans_iters).cpu().numpy()
+            fitted = {b: out[i] for i, b in enumerate(active)}
+        else:
+            fitted = {b: _kmeans(ks[b], self.n_centroids, n_iters=kmeans_iters, seed=seed + b)
+                      for b in active}
         cents = []
         for b in range(nb):
             sl = slice(b * bd, (b + 1) * bd)
-            if self.mode == "profileperm_mixed_precision" and heavy[b]:
+            if b not in fitted:
                 cents.append(np.zeros((self.n_centroids, bd), np.float32))
                 continue
-            ks = k[:, sl] @ E[sl, sl].T
-            c = _kmeans(ks, self.n_centroids, n_iters=kmeans_iters, seed=seed + b)
-            cents.append((c @ E_inv[sl, sl].T).astype(np.float32))
+            cents.append((fitted[b] @ E_inv[sl, sl].T).astype(np.float32))
         working = np.stack(cents)
         if self.mode not in ("profileperm_baseline", "rotated") and self.n_refine_dsq > 0:
             working = _refine_centroids(q, k, working, E, bd, n_steps=self.n_refine_dsq,

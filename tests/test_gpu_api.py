@@ -404,6 +404,30 @@ def test_hybrid_sunshape_values_fused_decode(vbd, buffer_size):
     assert rel_err(cache.values[:, :, :nc].float().cpu().numpy(), vals) <= 1e-3
 
 
+@pytest.mark.parametrize("mode", ["profileperm_baseline", "profileperm_mixed_precision"])
+def test_codec_fit_on_gpu_matches_cpu_fit(mode):
+    """SunShapeBlockCodec.fit with the k-means on the GPU (every block in one
+    launch) gives the NumPy fit's permutation and heavy blocks and a codebook
+    of the same quality (reconstruction error within 1 %)."""
+    rng = np.random.default_rng(42)
+    s = rng.uniform(0.5, 4.0, 128).astype(np.float32)
+    q_cal = (rng.standard_normal((1024, 128)) * s).astype(np.float32)
+    k_cal = (rng.standard_normal((2048, 128)) * s).astype(np.float32)
+    gpu = S.SunShapeBlockCodec(128, device=DEV, mode=mode, n_refine_dsq=0).fit(
+        q_cal, k_cal, kmeans_iters=15, seed=42)
+    cpu = S.SunShapeBlockCodec(128, device=DEV, mode=mode, n_refine_dsq=0).fit(
+        q_cal, k_cal, kmeans_iters=15, seed=42, kmeans_device="cpu")
+    assert torch.equal(gpu.permutation.cpu(), cpu.permutation.cpu())
+    assert torch.equal(gpu.mixed_high_precision_blocks.cpu(), cpu.mixed_high_precision_blocks.cpu())
+    kt = torch.from_numpy(k_cal).to(DEV)
+
+    def err(codec):
+        rec = codec.dequantize(codec.quantize(kt)).float()
+        return float(((rec - kt) ** 2).mean())
+
+    assert abs(err(gpu) / err(cpu) - 1.0) <= 0.01
+
+
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():
     codec = make_codec(16)
     cache = S.create_kv_cache(codec, n_kv_heads=1)

@@ -617,3 +617,44 @@ def test_decode_sunshape_v_matches_oracle(b, hq, hkv, d, t_kv, t_buf, t_q, bd, v
     ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
                           mask="causal" if causal else None)
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def _inertia(x, c):
+    x = np.asarray(x, np.float64)
+    c = np.asarray(c, np.float64)
+    return float(((x[:, None, :] - c[None]) ** 2).sum(-1).min(1).mean())
+
+
+@pytest.mark.parametrize("bd,n,k", [(8, 2048, 256), (4, 4096, 256), (8, 700, 100)])
+def test_kmeans_blocks_matches_oracle(bd, n, k):
+    """ss_kmeans_blocks: from the oracle's initial rows, one Lloyd step gives
+    the oracle's assignments away from near-ties and bit-identical centroids
+    for every cluster no near-tie point touches; 15 steps reach the oracle's
+    inertia within 1 %."""
+    rng = np.random.default_rng(bd + n)
+    nbk = 3
+    scales = rng.uniform(0.5, 4, (nbk, 1, bd))
+    data = (rng.standard_normal((nbk, n, bd)) * scales).astype(np.float32)
+    init = np.stack([data[b][np.random.RandomState(7 + b).permutation(n)[:k]] for b in range(nbk)])
+    c1, a1 = _hip.kmeans_blocks(t(data), t(init), 1, return_assign=True)
+    c1, a1 = c1.cpu().numpy(), a1.cpu().numpy()
+    for b in range(nbk):
+        x, c = data[b], init[b]
+        # the oracle's float32 expanded-form distances and argmin
+        dist = (np.sum(x ** 2, axis=1, keepdims=True) + np.sum(c ** 2, axis=1, keepdims=True).T
+                - 2.0 * x @ c.T)
+        a_ref = np.argmin(dist, axis=1)
+        d64 = ((x.astype(np.float64)[:, None, :] - c.astype(np.float64)[None]) ** 2).sum(-1)
+        srt = np.sort(d64, axis=1)
+        scale = (x.astype(np.float64) ** 2).sum(1) + (c.astype(np.float64) ** 2).sum(1).max()
+        near = (srt[:, 1] - srt[:, 0]) <= 1e-5 * scale
+        assert near.mean() < 0.01
+        assert np.array_equal(a1[b][~near], a_ref[~near])
+        touched = set(a1[b][near].tolist()) | set(a_ref[near].tolist())
+        ref1 = O.kmeans(x, k, 1, 7 + b)
+        keep = np.array([kk not in touched for kk in range(k)])
+        assert np.array_equal(c1[b][keep], ref1[keep])
+    c15 = _hip.kmeans_blocks(t(data), t(init), 15).cpu().numpy()
+    for b in range(nbk):
+        ref = O.kmeans(data[b], k, 15, 7 + b)
+        assert abs(_inertia(data[b], c15[b]) / _inertia(data[b], ref) - 1.0) <= 0.01
