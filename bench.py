@@ -285,6 +285,14 @@ def run_turboquant(args) -> int:
         got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
         check = float(np.abs(got - ref).max() / np.abs(ref).max())
 
+    traffic = None  # HBM bytes per call from the committed counter runs
+    tf = os.path.join(ROOT, "profiles", "decode_turboquant2b_t32k_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            tr = json.load(f)
+        if tr.get("t_kv") == t_kv and tr.get("batch") == b:
+            traffic = tr.get("hbm_bytes_per_launch")
+
     line = {
         "metric": "TurboQuant-value decode attention µs/step and achieved HBM GB/s",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -296,7 +304,7 @@ def run_turboquant(args) -> int:
                    "t_kv": t_kv, "splits": splits, "cache_copies": n_copies,
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "per_launch_us": {"mean": round(float(np.mean(per)), 3),
                           "median": round(float(np.median(per)), 3)},
         "check_max_rel_err_vs_oracle": check,
