@@ -180,7 +180,8 @@ struct VGrouped {
 // TurboQuant values (reference value_codecs.py:136-177): per token a norm n
 // and one BITS-bit Lloyd-Max code per dim of the rotated unit vector, packed
 // like the grouped codes (kernels.py pack_indices).  A lane's dims decode to
-// n * level[code], the value in the rotated basis: since every token shares
+// level[code] and the token's weight carries n, so the kernel accumulates
+// p * n * level[code], the value in the rotated basis: since every token shares
 // the rotation R, sum_t p_t (n_t C[idx_t] @ R) = (sum_t p_t n_t C[idx_t]) @ R,
 // so the kernel accumulates in the rotated basis and R is applied once per
 // output row: by the split-merge launch, or by rotate_rows_kernel when a
@@ -225,11 +226,30 @@ struct VTurbo {
         }
         return v[0];
     }
-    __device__ static __forceinline__ void decode(const Args &a, const Raw &r, int, float *x) {
-#pragma unroll
-        for (int k = 0; k < VPW; ++k)
-            x[k] = r.n * level(a, (r.w >> (k * BITS)) & ((1u << BITS) - 1u));
+    // Levels of every pair of adjacent codes, staged in LDS as float2: a
+    // word decodes with one bit-field extract and one 8-byte LDS read per two
+    // codes; the token's norm scales its softmax weight instead of each value.
+    static constexpr int kPairs = 1 << (2 * BITS);
+    static constexpr int kLdsBytes = kPairs * 8;
+    static constexpr bool kTokenScale = true;
+    static_assert(VPW % 2 == 0, "codes pair up within a word");
+    __device__ static __forceinline__ void stage(float *lds, const Args &a, int, int tid, int nt) {
+        float2 *t2 = reinterpret_cast<float2 *>(lds);
+        for (int i = tid; i < kPairs; i += nt)
+            t2[i] = make_float2(level(a, (uint32_t)i & ((1u << BITS) - 1u)),
+                                level(a, (uint32_t)i >> BITS));
     }
+    __device__ static __forceinline__ void decode_lds(const float *lds, const Args &, const Raw &r,
+                                                      int, float *x) {
+        const float2 *t2 = reinterpret_cast<const float2 *>(lds);
+#pragma unroll
+        for (int k = 0; k < VPW; k += 2) {
+            const float2 v = t2[__builtin_amdgcn_ubfe(r.w, k * BITS, 2 * BITS)];
+            x[k] = v.x;
+            x[k + 1] = v.y;
+        }
+    }
+    __device__ static __forceinline__ float token_scale(const Raw &r) { return r.n; }
 };
 
 // SunShape block-VQ values (value backend "sunshape", reference
@@ -318,6 +338,14 @@ struct VfSlabs {
 template <class VF>
 struct VfSlabs<VF, std::void_t<decltype(VF::kSlabs)>> {
     static constexpr int value = VF::kSlabs;
+};
+template <class VF, class = void>
+struct VfScaled {  // the format scales each token's weight (VF::token_scale)
+    static constexpr bool value = false;
+};
+template <class VF>
+struct VfScaled<VF, std::void_t<decltype(VF::kTokenScale)>> {
+    static constexpr bool value = VF::kTokenScale;
 };
 template <class VF, class = void>
 struct VfLds {
@@ -537,6 +565,11 @@ __global__ void __launch_bounds__(kDecodeThreads)
                     VF::decode_lds(vlds, va, vr[j], lt, x);
                 else
                     VF::decode(va, vr[j], lt, x);
+                if constexpr (VfScaled<VF>::value) {
+                    const float ts = VF::token_scale(vr[j]);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) pr[r] *= ts;
+                }
 #pragma unroll
                 for (int r = 0; r < R; ++r)
 #pragma unroll
