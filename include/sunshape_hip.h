@@ -257,6 +257,14 @@ size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_
  *   v_transform  float [head_dim][head_dim] (device): original = codec-space
  *                row @ v_transform (the inverse permutation as a 0/1 matrix,
  *                or the codec rotation)
+ *   k_heavy      NULL, or fp16 [batch][n_kv_heads][cap][n_heavy_dims]: the
+ *                heavy blocks' key dims of a mixed-precision codec (codec
+ *                basis), scored exactly beside the LUT; heavy_dims int32
+ *                [n_heavy_dims] are their codec-basis dims (n_heavy_dims a
+ *                multiple of 8, at most 64).  The reference zeroes these
+ *                blocks' centroids and drops them from the scores
+ *                (codec.py:381-388, cache.py:187-189) although its README
+ *                calls them fp16 blocks; NULL keeps the reference's scores.
  *   workspace    ss_decode_turboquant_workspace_bytes(...) bytes (same layout)
  */
 int ss_decode_attn_sunshape_v(const void *q, int q_dtype, int64_t batch, int n_q_heads,
@@ -264,7 +272,9 @@ int ss_decode_attn_sunshape_v(const void *q, int q_dtype, int64_t batch, int n_q
                               const int32_t *perm, const float *centroids, int n_blocks,
                               int n_centroids, const uint8_t *idx, const uint8_t *v_idx,
                               const float *v_centroids, int v_block_dim, int v_n_centroids,
-                              const float *v_transform, int64_t cap, int64_t t_kv,
+                              const float *v_transform, const void *k_heavy,
+                              const int32_t *heavy_dims, int n_heavy_dims, int64_t cap,
+                              int64_t t_kv,
                               const void *k_buf, const void *v_buf, int buf_dtype,
                               int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
                               int causal, int64_t q_offset, void *out, int out_dtype,

@@ -470,13 +470,19 @@ def sdpa(queries, key_indices, values, centroids, perm, scale, mask=None):
 
 
 def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
-                  values_all, mask=None):
+                  values_all, mask=None, heavy_keys=None, heavy_dims=None):
     """The two-pass fallback of attention.py:307-350 used when a hybrid cache
     has buffered fp16 tokens: compressed scores ``q_t . k_hat`` concatenated
     with ``q_scaled . k_buf^T`` (original basis), causal or additive/boolean
     mask, softmax, ``@ values`` (compressed values dequantized, then buffer).
     ``key_indices`` (B, Hkv, Tc, NB), ``buffer_keys`` (B, Hkv, Tb, D) or None,
-    ``values_all`` (B, Hkv, Tc + Tb, D)."""
+    ``values_all`` (B, Hkv, Tc + Tb, D).
+
+    ``heavy_keys`` (B, Hkv, Tc, nhd) with ``heavy_dims`` (nhd,): the build's
+    extension for mixed-precision codecs (heavy blocks kept in fp16, the
+    intent of README.md:87, where the reference zeroes their centroids,
+    codec.py:381-388): the compressed scores gain the exact dot products
+    ``q_t[heavy_dims] . k_heavy``."""
     q = scale_query(queries, scale)
     b_, hq, tq, d = q.shape
     hkv = values_all.shape[1]
@@ -491,7 +497,12 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
                 parts = []
                 if key_indices is not None and key_indices.shape[2] > 0:
                     lut = query_centroid_dots(qt[b, h, r].astype(np.float32), centroids)
-                    parts.append(gather_scores(lut, key_indices[b, h]))
+                    sc = gather_scores(lut, key_indices[b, h])
+                    if heavy_keys is not None:
+                        hd = np.asarray(heavy_dims, np.int64)
+                        sc = sc + (qt[b, h, r][:, hd].astype(np.float64)
+                                   @ np.asarray(heavy_keys[b, h], np.float64).T)
+                    parts.append(sc)
                 if buffer_keys is not None and buffer_keys.shape[2] > 0:
                     parts.append(qg[b, h, r].astype(np.float64)
                                  @ np.asarray(buffer_keys[b, h], np.float64).T)

@@ -89,8 +89,8 @@ _SIGNATURES = {
                                 _c_void_p]),
     "ss_decode_attn_sunshape_v": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
-        _c_void_p, _c_void_p, _c_void_p, _int, _int, _c_void_p, _i64, _i64,
-        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _c_void_p, _int,
+        _i64, _i64, _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
         _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_attn_grouped_il": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
@@ -494,11 +494,14 @@ def decode_attn_sunshape_v(q: torch.Tensor, scale: float, perm: torch.Tensor | N
                            out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                            n_splits: int = 0, buf_keys: torch.Tensor | None = None,
                            buf_values: torch.Tensor | None = None,
-                           buf_len: int = 0) -> torch.Tensor:
+                           buf_len: int = 0, k_heavy: torch.Tensor | None = None,
+                           heavy_dims: torch.Tensor | None = None) -> torch.Tensor:
     """Fused decode over SunShape block-VQ values: ``v_idx`` (B, Hkv, cap,
     D / bd) uint8, ``v_centroids`` (D / bd, nc, bd) float32, ``v_transform``
     (D, D) float32 taking a codec-space row to the original basis.  Buffered
-    tokens join the softmax as in :func:`decode_attn_turboquant`."""
+    tokens join the softmax as in :func:`decode_attn_turboquant`.
+    ``k_heavy`` (B, Hkv, cap, nhd) fp16 with ``heavy_dims`` (nhd,) int32: a
+    mixed-precision codec's heavy-block key dims, scored exactly."""
     _check_decode_common(q, idx, centroids, perm)
     require_gpu(v_idx, v_centroids, v_transform)
     b_, hq, tq, d = q.shape
@@ -518,6 +521,14 @@ def decode_attn_sunshape_v(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     nc = centroids.shape[1]
     if out is None:
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    nhd = 0
+    if k_heavy is not None:
+        require_gpu(k_heavy, heavy_dims)
+        nhd = int(heavy_dims.numel())
+        if k_heavy.dtype != torch.float16 or not k_heavy.is_contiguous() or \
+                tuple(k_heavy.shape) != (b_, hkv, cap, nhd) or heavy_dims.dtype != torch.int32:
+            raise ValueError(f"k_heavy must be contiguous fp16 {(b_, hkv, cap, nhd)} with int32 "
+                             "heavy_dims")
     buf_len = int(buf_len)
     buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
                                                             b_, hkv, d)
@@ -527,7 +538,8 @@ def decode_attn_sunshape_v(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     ws = decode_workspace(q.device, ws_bytes)
     check(lib.ss_decode_attn_sunshape_v(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
-        nb, nc, ptr(idx), ptr(v_idx), ptr(v_centroids), vbd, vnc, ptr(v_transform), cap,
+        nb, nc, ptr(idx), ptr(v_idx), ptr(v_centroids), vbd, vnc, ptr(v_transform),
+        ptr(k_heavy), ptr(heavy_dims), nhd, cap,
         int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh, bst, buf_len,
         int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
         ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))

@@ -267,7 +267,11 @@ template <int D, int BD>
 struct VSunV {
     static constexpr int kSlabs = D * 256 * 4 > 65536 ? 2 : 1;
     static constexpr int DS = D / kSlabs;            // dims of one workgroup
-    static constexpr int kLdsBytes = DS * 256 * 4;   // this slab's centroids, 256 per block
+    // this slab's centroids (256 per block), then the heavy dims' query values
+    static constexpr int kMaxHeavyDims = 64;
+    static constexpr int kHeavyOffset = DS * 256;  // floats
+    static constexpr int kLdsBytes = (DS * 256 + 4 * kMaxHeavyDims) * 4;
+    static constexpr bool kHeavyKeys = true;
     static constexpr int DPL = 16;
     static constexpr int BPL = DPL / BD;  // blocks per lane
     static constexpr int NBV = D / BD, NBVS = DS / BD;
@@ -279,6 +283,11 @@ struct VSunV {
         const uint8_t *idx;  // [rows][NBV]
         const float *cb;     // [NBV][n_centroids][BD], n_centroids <= 256
         int n_centroids;
+        // keys of mixed-precision codecs: the heavy blocks' dims kept in
+        // fp16 ([rows][nhd], codec basis), scored exactly beside the LUT
+        const __half *kheavy;    // or null
+        const int *heavy_dims;   // [nhd] codec-basis dims
+        int nhd;                 // multiple of 8, <= kMaxHeavyDims
     };
     struct Raw {
         uint32_t w;
@@ -338,6 +347,14 @@ struct VfSlabs {
 template <class VF>
 struct VfSlabs<VF, std::void_t<decltype(VF::kSlabs)>> {
     static constexpr int value = VF::kSlabs;
+};
+template <class VF, class = void>
+struct VfHeavy {  // the format's Args may carry fp16 heavy-block keys
+    static constexpr bool value = false;
+};
+template <class VF>
+struct VfHeavy<VF, std::void_t<decltype(VF::kHeavyKeys)>> {
+    static constexpr bool value = VF::kHeavyKeys;
 };
 template <class VF, class = void>
 struct VfScaled {  // the format scales each token's weight (VF::token_scale)
@@ -461,6 +478,15 @@ __global__ void __launch_bounds__(kDecodeThreads)
         }
     }
     if constexpr (VLDS > 0) VF::stage(vlds, va, slab, tid, kDecodeThreads);
+    if constexpr (VfHeavy<VF>::value) {
+        // heavy dims' query values, in log2 units like the LUT
+        float *qh = vlds + VF::kHeavyOffset;
+        if (va.kheavy)
+            for (int i = tid; i < R * va.nhd; i += kDecodeThreads) {
+                const int r = i / va.nhd, j = i - r * va.nhd;
+                qh[i] = qp[r * D + min(max(va.heavy_dims[j], 0), D - 1)] * kLog2e;
+            }
+    }
     __syncthreads();
 
     // 3. stream this split's tokens, 64 per wave-tile.
@@ -513,8 +539,30 @@ __global__ void __launch_bounds__(kDecodeThreads)
             float a = 0.f;
 #pragma unroll
             for (int b = 0; b < NB; ++b) a += lr[b * kLutStride + ir.at(b)];
-            s[r] = (kok && tk <= lim[r]) ? a : -INFINITY;
+            s[r] = a;
         }
+        if constexpr (VfHeavy<VF>::value) {
+            if (va.kheavy) {  // uniform: exact dot products over the heavy dims
+                const float *qh = vlds + VF::kHeavyOffset;
+                const uint4 *kp = reinterpret_cast<const uint4 *>(va.kheavy + (vrow0 + tk) * va.nhd);
+                float hs[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) hs[r] = 0.f;
+                for (int j8 = 0; j8 < va.nhd / 8; ++j8) {
+                    float kv[8];
+                    unpack16<__half>(kok ? kp[j8] : make_uint4(0u, 0u, 0u, 0u), kv);
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            hs[r] = fmaf(qh[r * va.nhd + j8 * 8 + e], kv[e], hs[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) s[r] += hs[r];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[r] = (kok && tk <= lim[r]) ? s[r] : -INFINITY;
         float corr[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -2632,7 +2680,8 @@ extern "C" int ss_decode_attn_sunshape_v(
     const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
     int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
     int n_centroids, const uint8_t *idx, const uint8_t *v_idx, const float *v_centroids,
-    int v_block_dim, int v_n_centroids, const float *v_transform, int64_t cap, int64_t t_kv,
+    int v_block_dim, int v_n_centroids, const float *v_transform, const void *k_heavy,
+    const int32_t *heavy_dims, int n_heavy_dims, int64_t cap, int64_t t_kv,
     const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
     int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
     void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
@@ -2646,10 +2695,19 @@ extern "C" int ss_decode_attn_sunshape_v(
                    "value n_centroids %d unsupported (1..256, uint8 indices)", v_n_centroids);
     SS_REQUIRE(((uintptr_t)v_idx % 4) == 0, "value indices must be 4-byte aligned");
     SS_REQUIRE(((uintptr_t)v_centroids % 16) == 0, "value centroids must be 16-byte aligned");
+    if (k_heavy) {
+        SS_REQUIRE(heavy_dims, "null heavy_dims");
+        SS_UNSUPPORTED(n_heavy_dims > 0 && n_heavy_dims % 8 == 0 && n_heavy_dims <= 64,
+                       "n_heavy_dims %d unsupported (a positive multiple of 8, at most 64)",
+                       n_heavy_dims);
+        SS_REQUIRE(((uintptr_t)k_heavy % 16) == 0, "heavy keys must be 16-byte aligned");
+    }
     auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
 #define SS_SUNV(DD, BB)                                                     \
     {                                                                       \
-        typename VSunV<DD, BB>::Args va{v_idx, v_centroids, v_n_centroids}; \
+        typename VSunV<DD, BB>::Args va{v_idx, v_centroids, v_n_centroids,    \
+                                        static_cast<const __half *>(k_heavy), \
+                                        heavy_dims, k_heavy ? n_heavy_dims : 0}; \
         return launch_r<DD, VSunV<DD, BB>>(c, va, s, st, false);            \
     }
         if (head_dim == 128) {

@@ -658,3 +658,60 @@ def test_kmeans_blocks_matches_oracle(bd, n, k):
     for b in range(nbk):
         ref = O.kmeans(data[b], k, 15, 7 + b)
         assert abs(_inertia(data[b], c15[b]) / _inertia(data[b], ref) - 1.0) <= 0.01
+
+
+@pytest.mark.parametrize("b,hq,hkv,t_kv,t_buf,t_q,n_heavy,splits", [
+    (2, 32, 8, 1500, 0, 1, 4, 0),    # config-5 shape: 4 heavy blocks (32 fp16 dims)
+    (1, 8, 2, 333, 40, 3, 1, 2),     # one heavy block, buffer, causal prefill rows
+])
+def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, splits):
+    """Mixed-precision keys with their heavy blocks in fp16: the fused decode
+    adds the exact heavy-dim dot products to the LUT scores, as the oracle's
+    two-pass SDPA with heavy keys does."""
+    d, bd = 128, 4
+    cap = ((t_kv + 15) // 16) * 16
+    cents, perm, idx, _, q = decode_case(90 + n_heavy, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(91 + n_heavy)
+    heavy = np.sort(rng.permutation(16)[:n_heavy])
+    cents[heavy] = 0.0
+    hd = np.concatenate([np.arange(x * 8, x * 8 + 8) for x in heavy]).astype(np.int32)
+    kh = np.zeros((b, hkv, cap, hd.size), np.float16)
+    kh[:, :, :t_kv] = rng.standard_normal((b, hkv, t_kv, hd.size)).astype(np.float16)
+    nbv = d // bd
+    v_cents = rng.standard_normal((nbv, 256, bd)).astype(np.float32)
+    v_idx = rng.integers(0, 256, (b, hkv, cap, nbv)).astype(np.uint8)
+    vperm = rng.permutation(d).astype(np.int32)
+    inv = O.invert_permutation(vperm)
+    m = np.zeros((d, d), np.float32)
+    m[inv, np.arange(d)] = 1.0
+    kb = rng.standard_normal((b, hkv, t_buf + 2, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 2, d)).astype(np.float16)
+    scale = 1.0 / np.sqrt(d)
+    causal = t_q > 1
+    total = t_kv + t_buf
+    out = _hip.decode_attn_sunshape_v(t(q), scale, t(perm), t(cents), t(idx), t(v_idx),
+                                      t(v_cents), t(m), t_kv, causal=causal,
+                                      q_offset=total - t_q if causal else 0,
+                                      out_dtype=torch.float32, n_splits=splits,
+                                      buf_keys=t(kb), buf_values=t(vb), buf_len=t_buf,
+                                      k_heavy=t(kh), heavy_dims=t(hd))
+    torch.cuda.synchronize()
+    vals = np.zeros((b, hkv, total, d), np.float64)
+    for bi in range(b):
+        for hi in range(hkv):
+            vals[bi, hi, :t_kv] = O.dequantize_blockvq(v_idx[bi, hi, :t_kv], v_cents, inv)
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                          mask="causal" if causal else None, heavy_keys=kh[:, :, :t_kv],
+                          heavy_dims=hd)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+    # without k_heavy the kernel keeps the reference's scores (heavy blocks contribute 0)
+    out0 = _hip.decode_attn_sunshape_v(t(q), scale, t(perm), t(cents), t(idx), t(v_idx),
+                                       t(v_cents), t(m), t_kv, causal=causal,
+                                       q_offset=total - t_q if causal else 0,
+                                       out_dtype=torch.float32, n_splits=splits,
+                                       buf_keys=t(kb), buf_values=t(vb), buf_len=t_buf)
+    torch.cuda.synchronize()
+    ref0 = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                           mask="causal" if causal else None)
+    assert rel_err(out0.cpu().numpy(), ref0) <= REL_TOL

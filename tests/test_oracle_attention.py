@@ -187,6 +187,36 @@ def test_sdpa_two_pass_buffer_scores_use_original_basis():
     assert np.abs(out[0, 0] - ref).max() < 1e-12
 
 
+def test_sdpa_heavy_blocks_score_as_exact_key_dots():
+    """Mixed-precision extension: with the heavy blocks' centroids zero and
+    their key dims kept in fp16, each compressed score is q . k_hat where
+    k_hat takes the centroids on light blocks and the fp16 dims on heavy
+    ones, all in the original basis (pinned against attention written out
+    over the reconstructed keys, not the LUT)."""
+    rng = np.random.default_rng(32)
+    b_, hq, hkv, d, t, bd = 1, 2, 1, 64, 40, 8
+    nb = d // bd
+    perm = rng.permutation(d).astype(np.int32)
+    cents = rng.standard_normal((nb, 32, bd)).astype(np.float32)
+    heavy = np.array([1, 6])
+    cents[heavy] = 0.0
+    hd = np.concatenate([np.arange(b * bd, (b + 1) * bd) for b in heavy]).astype(np.int32)
+    keys = rng.standard_normal((b_, hkv, t, d)).astype(np.float32)
+    idx = np.stack([O.encode_blockvq(keys[0, 0], cents, perm)[0]])[None]
+    kh = O.apply_permutation(keys[0, 0], perm)[:, hd].astype(np.float16)[None, None]
+    vals = rng.standard_normal((b_, hkv, t, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, 1, d)).astype(np.float16)
+    out = O.sdpa_two_pass(q, 0.25, perm, cents, idx, None, vals, heavy_keys=kh, heavy_dims=hd)
+    # k_hat in codec space: centroids of light blocks, fp16 dims of heavy ones
+    kc = O.dequantize_blockvq(idx[0, 0], cents).astype(np.float64)
+    kc[:, hd] = kh[0, 0].astype(np.float64)
+    k_orig = kc[:, O.invert_permutation(perm)]
+    qs = O.scale_query(q, 0.25)[0].astype(np.float64)
+    for h in range(hq):
+        ref = explicit_attention(qs[h], k_orig, vals[0, 0])
+        assert np.abs(out[0, h] - ref).max() < 1e-9
+
+
 def test_cpu_baseline_forms_agree_with_oracle():
     rng = np.random.default_rng(40)
     b_, hq, hkv, d, t = 1, 8, 2, 128, 500
