@@ -91,7 +91,8 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
             out = _hip.decode_attn_sunshape_v(q, kscale, perm, codec.centroids, ops["idx"],
                                               ops["v_idx"], ops["v_centroids"], ops["v_transform"],
                                               buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
-                                              buf_len=buffered, **kw)
+                                              buf_len=buffered, k_heavy=ops["k_heavy"],
+                                              heavy_dims=ops["heavy_dims"], **kw)
             codec.last_score_backend = ("hip_fused_sunshape_v_buffer" if buffered
                                         else "hip_fused_sunshape_v")
         elif ops["kind"] == "grouped":
@@ -143,8 +144,13 @@ def _two_pass(cache, queries: torch.Tensor, scale: float, mask) -> torch.Tensor:
     parts = []
     tc = cache.compressed_offset if is_hybrid else t_kv
     if tc > 0:
-        parts.append(_compressed_scores(codec, _transform_grouped(codec, q_grouped),
-                                        cache.key_indices))
+        q_t = _transform_grouped(codec, q_grouped)
+        sc = _compressed_scores(codec, q_t, cache.key_indices)
+        hd = getattr(cache, "_heavy_dims", None)
+        if hd is not None:  # fp16 heavy blocks scored exactly (codec basis)
+            kh = cache._key_heavy[:, :, :tc].float().transpose(-1, -2).contiguous()
+            sc = sc + torch.matmul(q_t[..., hd.long()].float(), kh.unsqueeze(2))
+        parts.append(sc)
     if is_hybrid and cache.buffer_offset > 0:
         kb_t = cache.buffer_keys.float().transpose(-1, -2).contiguous()  # (B, Hkv, D, Tb)
         parts.append(torch.matmul(q_grouped.float(), kb_t.unsqueeze(2)))

@@ -317,6 +317,11 @@ class HybridSunShapeKVCache:
         # grouped codes held token-interleaved ((B, H, cap*bits/32, D) words)
         # for the matrix-core decode kernel; packed rows otherwise
         self._values_il: torch.Tensor | None = None
+        # mixed-precision codecs with fp16 heavy blocks: those key dims
+        # (codec basis) per token, (B, H, cap, n_heavy_dims) fp16
+        self._key_heavy: torch.Tensor | None = None
+        hd = codec.heavy_dims()
+        self._heavy_dims = hd
         self._grouped_il = (self.value_backend == "grouped" and
                             _grouped_il_ok(codec, self.head_dim, self.value_bits or 0,
                                            self.value_group_size))
@@ -332,6 +337,9 @@ class HybridSunShapeKVCache:
         cap = _round_capacity(max(needed, self.max_tokens or 0))
         keep = self._compressed_offset
         h_ = self.n_kv_heads
+        if self._heavy_dims is not None:
+            self._key_heavy = _grow(self._key_heavy, (b_, h_, cap, self._heavy_dims.numel()),
+                                    torch.float16, device, keep)
         self._key_indices = _grow(self._key_indices, (b_, h_, cap, self.n_blocks), torch.uint8,
                                   device, keep)
         if self.value_backend == "grouped":
@@ -378,6 +386,9 @@ class HybridSunShapeKVCache:
         kf = self._key_buffer[:, :, :n]
         vf = self._value_buffer[:, :, :n]
         _encode_into(self.codec, kf, self._key_indices[:, :, c0:c1])
+        if self._heavy_dims is not None:
+            kp = kf[..., self.codec.permutation.long()]
+            self._key_heavy[:, :, c0:c1] = kp[..., self._heavy_dims.long()].to(torch.float16)
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
             if self._grouped_il:
@@ -452,8 +463,11 @@ class HybridSunShapeKVCache:
     def keys(self) -> torch.Tensor:
         parts = []
         if self._compressed_offset > 0 and self._key_indices is not None:
-            parts.append(_dequantize_keys(self.codec,
-                                          self._key_indices[:, :, :self._compressed_offset]))
+            k = _dequantize_keys(self.codec, self._key_indices[:, :, :self._compressed_offset])
+            if self._heavy_dims is not None:  # fp16 heavy dims: codec dim j is key dim perm[j]
+                od = self.codec.permutation.long()[self._heavy_dims.long()]
+                k[..., od] = self._key_heavy[:, :, :self._compressed_offset].float()
+            parts.append(k)
         if self._buffer_offset > 0 and self._key_buffer is not None:
             parts.append(self._key_buffer[:, :, :self._buffer_offset].float())
         if not parts:
@@ -556,6 +570,8 @@ class HybridSunShapeKVCache:
         fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
             return None
+        if self._heavy_dims is not None and self.value_backend != "sunshape":
+            return None  # fp16 heavy blocks: only the SunShape-value kernel scores them
         if self.value_backend == "grouped" and self._values_il is not None:
             gc = self._value_codec_impl
             return {"kind": "grouped_il", "idx": self._key_indices, "codes_il": self._values_il,
@@ -581,7 +597,8 @@ class HybridSunShapeKVCache:
             return {"kind": "sunshape_v", "idx": self._key_indices, "v_idx": self._value_indices,
                     "v_centroids": vc.centroids.float().contiguous(),
                     "v_transform": vc.kernel_value_transform(),
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer,
+                    "k_heavy": self._key_heavy, "heavy_dims": self._heavy_dims}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None

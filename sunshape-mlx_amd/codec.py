@@ -149,7 +149,8 @@ class SunShapeBlockCodec:
 
     def __init__(self, head_dim: int, block_dim: int = 8, n_centroids: int = 256, c: float = 5.0,
                  n_refine_dsq: int = 3, mode: str = "profileperm_baseline",
-                 use_rotation: bool = False, rotation_seed: int = 0, device=None):
+                 use_rotation: bool = False, rotation_seed: int = 0, device=None,
+                 heavy_fp16: bool = False):
         if head_dim % block_dim != 0:
             raise ValueError("head_dim must be divisible by block_dim")
         self.head_dim = head_dim
@@ -161,6 +162,10 @@ class SunShapeBlockCodec:
         if self.mode not in MODES:
             raise ValueError(f"Unknown SunShapeBlockCodec mode: {self.mode}")
         self.n_refine_dsq = n_refine_dsq
+        # mixed precision: keep the heavy blocks' key dims in fp16 and score
+        # them exactly (the intent of README.md:87); False keeps the
+        # reference's zero contribution (codec.py:381-388)
+        self.heavy_fp16 = bool(heavy_fp16)
         self.use_rotation = self.mode == "rotated"
         self.last_score_backend = "none"
         if device is None:
@@ -206,7 +211,7 @@ class SunShapeBlockCodec:
         sd = {k: getattr(self, k).detach().cpu() for k in self._STATE_KEYS}
         sd["config"] = dict(head_dim=self.head_dim, block_dim=self.block_dim,
                             n_centroids=self.n_centroids, mode=self.mode, c=self.c,
-                            n_refine_dsq=self.n_refine_dsq)
+                            n_refine_dsq=self.n_refine_dsq, heavy_fp16=self.heavy_fp16)
         return sd
 
     def load_state_dict(self, sd: dict) -> "SunShapeBlockCodec":
@@ -214,6 +219,8 @@ class SunShapeBlockCodec:
         for k in ("head_dim", "block_dim", "n_centroids"):
             if k in cfg and cfg[k] != getattr(self, k):
                 raise ValueError(f"state {k}={cfg[k]} does not match codec {getattr(self, k)}")
+        if "heavy_fp16" in cfg:
+            self.heavy_fp16 = bool(cfg["heavy_fp16"])
         if "mode" in cfg:
             self.mode = cfg["mode"]
             self.use_rotation = self.mode == "rotated"
@@ -308,6 +315,18 @@ class SunShapeBlockCodec:
         nb, bd = self.n_blocks, self.block_dim
         e = self.E.reshape(nb, bd, nb, bd)
         return torch.stack([e[b, :, b, :] for b in range(nb)])  # (nb, bd, bd)
+
+    def heavy_dims(self) -> torch.Tensor | None:
+        """int32 codec-basis dims of the heavy blocks whose keys a cache keeps
+        in fp16 (mixed-precision mode with ``heavy_fp16``), else None."""
+        if self.mode != "profileperm_mixed_precision" or not self.heavy_fp16:
+            return None
+        hb = torch.nonzero(self.mixed_high_precision_blocks.to(torch.bool)).flatten()
+        if hb.numel() == 0:
+            return None
+        bd = self.block_dim
+        dims = (hb[:, None] * bd + torch.arange(bd, device=hb.device)[None]).flatten()
+        return dims.to(torch.int32).to(self.device)
 
     def kernel_value_transform(self) -> torch.Tensor:
         """(D, D) float32 matrix taking a codec-space row to the original

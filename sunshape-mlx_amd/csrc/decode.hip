@@ -2550,7 +2550,12 @@ static DecodeShape with_buffer_slot(DecodeShape s, int64_t t_buf) {
 }
 
 static size_t turboquant_ws_bytes(const DecodeShape &sw, int64_t rows, int head_dim) {
-    const size_t part = (decode_ws_bytes(sw, head_dim) + 255) / 256 * 256;
+    // the rows never overlap the split counters at the workspace's start,
+    // which the matrix-core decodes sharing this workspace rely on being zero
+    // (with one split there are no partials, but the counter area stays)
+    size_t part = decode_ws_bytes(sw, head_dim);
+    if (part < kCntBytes) part = kCntBytes;
+    part = (part + 255) / 256 * 256;
     return part + (size_t)rows * head_dim * sizeof(float);
 }
 

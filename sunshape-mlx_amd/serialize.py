@@ -35,7 +35,7 @@ _CACHE_TENSORS = {
     "SunShapeKVCache": ("_key_indices", "_values"),
     "HybridSunShapeKVCache": ("_key_indices", "_values_packed", "_values_il", "_value_scales",
                               "_value_zeros", "_value_norms", "_value_indices", "_values_fp16",
-                              "_key_buffer", "_value_buffer"),
+                              "_key_buffer", "_value_buffer", "_key_heavy"),
 }
 # integer bookkeeping restored alongside the buffers
 _CACHE_SCALARS = {
@@ -68,7 +68,8 @@ def _codec_from(tensors: dict, prefix: str, cfg: dict, device) -> SunShapeBlockC
                                n_centroids=cfg["n_centroids"], c=cfg.get("c", 5.0),
                                n_refine_dsq=cfg.get("n_refine_dsq", 3), mode=cfg["mode"],
                                use_rotation=cfg["mode"] == "rotated",
-                               rotation_seed=cfg.get("rotation_seed", 0), device=device)
+                               rotation_seed=cfg.get("rotation_seed", 0), device=device,
+                               heavy_fp16=cfg.get("heavy_fp16", False))
     sd = {k[len(prefix) + 1:]: v for k, v in tensors.items() if k.startswith(prefix + ".")}
     sd["config"] = cfg
     return codec.load_state_dict(sd)

@@ -428,6 +428,60 @@ def test_codec_fit_on_gpu_matches_cpu_fit(mode):
     assert abs(err(gpu) / err(cpu) - 1.0) <= 0.01
 
 
+@pytest.mark.parametrize("value_backend,buffer_size", [("sunshape", 0), ("sunshape", 64),
+                                                       ("fp16", 32)])
+def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
+    """A mixed-precision codec with ``heavy_fp16``: the hybrid cache keeps the
+    heavy blocks' key dims in fp16, returns them in ``keys``, and attention
+    scores them exactly -- fused for SunShape values, two-pass otherwise --
+    matching the oracle with heavy keys."""
+    rng = np.random.default_rng(50)
+    d, nb = 128, 16
+    heavy = np.zeros(nb, bool)
+    heavy[[3, 7, 8, 12]] = True
+    cents = rng.standard_normal((nb, 256, 8)).astype(np.float32)
+    cents[heavy] = 0.0
+    perm = rng.permutation(d).astype(np.int32)
+    codec = S.SunShapeBlockCodec(d, device=DEV, mode="profileperm_mixed_precision",
+                                 heavy_fp16=True)
+    codec.load_state_dict({"centroids": cents, "permutation": perm,
+                           "mixed_high_precision_blocks": heavy})
+    hd = codec.heavy_dims().cpu().numpy()
+    assert hd.size == 32
+    b, hq, hkv, n = 2, 8, 2, 300
+    k, v = kv(51, b, hkv, n, d)
+    kw = dict(n_kv_heads=hkv, buffer_size=buffer_size)
+    if value_backend == "sunshape":
+        vcodec = S.SunShapeBlockCodec(d, block_dim=4, n_centroids=256, device=DEV)
+        vcodec.load_state_dict({"centroids": rng.standard_normal((32, 256, 4)).astype(np.float32),
+                                "permutation": rng.permutation(d).astype(np.int32)})
+        cache = S.create_kv_cache(codec, value_backend="sunshape", value_bits=8,
+                                  value_codec=vcodec, **kw)
+    else:
+        cache = S.create_kv_cache(codec, value_backend="fp16", **kw)
+    cache.update_and_fetch(k, v)
+    nc = cache.compressed_offset
+    # returned keys carry the fp16 heavy dims in the original basis
+    od = perm[hd]
+    assert torch.equal(cache.keys[:, :, :nc][..., od].half().cpu(), k[:, :, :nc][..., od].cpu())
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    expect = {"sunshape": "hip_fused_sunshape_v_buffer" if buffer_size else "hip_fused_sunshape_v",
+              "fp16": "hip"}[value_backend]
+    assert codec.last_score_backend == expect
+    kh = k[:, :, :nc].cpu().numpy()[..., perm][..., hd]
+    vals = cache.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, cache.key_indices.cpu().numpy(),
+                          cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset else None,
+                          vals, heavy_keys=kh, heavy_dims=hd)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the reference's semantics (heavy blocks contribute nothing) differ
+    ref0 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, cache.key_indices.cpu().numpy(),
+                           cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset else None,
+                           vals)
+    assert rel_err(ref0, ref) > 1e-2
+
+
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():
     codec = make_codec(16)
     cache = S.create_kv_cache(codec, n_kv_heads=1)

@@ -715,3 +715,29 @@ def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, s
     ref0 = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
                            mask="causal" if causal else None)
     assert rel_err(out0.cpu().numpy(), ref0) <= REL_TOL
+
+
+def test_transformed_decode_leaves_split_counters_zero():
+    """Regression: a single-split TurboQuant / SunShape-value decode keeps its
+    transformed-basis rows clear of the workspace's split counters, so a
+    matrix-core decode with an in-kernel merge on the same (per-stream)
+    workspace still merges correctly afterwards."""
+    b, hq, hkv, d, t_small, t_big = 2, 8, 2, 128, 200, 4000
+    cents, perm, idx, vals, q = decode_case(123, b, hq, hkv, d, t_big, 1, t_big)
+    rng = np.random.default_rng(124)
+    packed = O.pack_indices(rng.integers(0, 4, (b, hkv, t_big, d)), 2).astype(np.uint32)
+    norms = (rng.random((b, hkv, t_big)) + 0.5).astype(np.float32)
+    levels = (O.lloyd_max_gaussian(2)[0] / np.sqrt(d)).astype(np.float32)
+    rot = O.rotation_matrix(d, 43)
+    scale = 1.0 / np.sqrt(d)
+    for _ in range(2):
+        _hip.decode_attn_turboquant(t(q), scale, t(perm), t(cents), t(idx),
+                                    t(packed.view(np.int32)), t(norms), levels, t(rot), 2,
+                                    t_small, out_dtype=torch.float32, n_splits=1)
+        out = _hip.decode_attn_il8(t(q), scale, t(perm), t(cents), t(idx), to_il8(vals, t_big),
+                                   t_big, out_dtype=torch.float32, n_splits=8)
+        torch.cuda.synchronize()
+        ws = _hip.decode_workspace(torch.device(DEV), 1)
+        assert not ws[:64 * 1024].any()
+        ref = O.sdpa(q, idx, vals, cents, perm, scale)
+        assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
