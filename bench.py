@@ -54,6 +54,9 @@ def parse_args():
     p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles",
                                                           "decode_fp16v_t32k_traffic.json"))
     p.add_argument("--layers", type=int, default=28, help="config5: decoder layers per step")
+    p.add_argument("--reference-mixed", action="store_true",
+                   help="config5: drop the heavy blocks from the scores as the reference does "
+                        "(default: keep them in fp16 and score them exactly)")
     p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5"),
                    default="metric",
                    help="metric: the BASELINE metric decode (fp16 values, B=1); hybrid: config 4 "
@@ -315,13 +318,14 @@ def run_turboquant(args) -> int:
 
 def run_config5(args) -> int:
     """Config 5: one decode step of a 28-layer Qwen-style 4B model's attention
-    (32 query / 8 KV heads, D=128, B=16, T_kv=131072 per layer).  Keys: 16
-    uint8 indices per token of a profileperm_mixed_precision codec with its 4
-    heavy blocks' centroids zero (the reference's semantics: heavy blocks
-    contribute nothing to the scores); values: SunShape block-VQ, block_dim 4,
-    256 centroids (32 index bytes per token), permutation transform.  Random
-    N(0,1) codebooks and uniform indices; 28 distinct layer caches (22.5 GB),
-    one ss_decode_attn_sunshape_v call per layer."""
+    (32 query / 8 KV heads, D=128, B=16, T_kv=131072 per layer).  Keys: a
+    profileperm_mixed_precision codec's 16 uint8 indices per token (the 4
+    heavy blocks' centroids zero) plus those 4 blocks' 32 dims in fp16,
+    scored exactly (the config's "4 heaviest blocks fp16"; --reference-mixed
+    drops them, as the reference does); values: SunShape block-VQ,
+    block_dim 4, 256 centroids (32 index bytes per token), permutation
+    transform.  Random N(0,1) codebooks, keys and uniform indices; 28 distinct
+    layer caches (52.6 GB), one ss_decode_attn_sunshape_v call per layer."""
     import numpy as np
     import torch
 
@@ -339,7 +343,11 @@ def run_config5(args) -> int:
     g = torch.Generator(device=dev).manual_seed(5)
     cents = torch.randn((nb, 256, 8), generator=g, device=dev)
     heavy = torch.randperm(nb, generator=g, device=dev)[:4]
-    cents[heavy] = 0.0  # mixed-precision heavy blocks: zero centroids (reference semantics)
+    cents[heavy] = 0.0  # mixed-precision heavy blocks: zero centroids
+    heavy_fp16 = not args.reference_mixed
+    hd = torch.sort(heavy).values
+    heavy_dims = (hd[:, None] * 8 + torch.arange(8, device=dev)[None]).flatten().to(torch.int32)
+    nhd = heavy_dims.numel() if heavy_fp16 else 0
     perm = torch.randperm(d, generator=g, device=dev).to(torch.int32)
     v_cents = torch.randn((nbv, 256, vbd), generator=g, device=dev)
     vperm = torch.randperm(d, generator=g, device=dev)
@@ -351,10 +359,12 @@ def run_config5(args) -> int:
         caches.append((torch.randint(0, 256, (b, hkv, t_kv, nb), generator=g, device=dev,
                                      dtype=torch.uint8),
                        torch.randint(0, 256, (b, hkv, t_kv, nbv), generator=g, device=dev,
-                                     dtype=torch.uint8)))
+                                     dtype=torch.uint8),
+                       torch.randn((b, hkv, t_kv, nhd), generator=g, device=dev).half()
+                       if heavy_fp16 else None))
     q = torch.randn((b, hq, 1, d), generator=g, device=dev).to(torch.float16)
     torch.cuda.synchronize()
-    per_layer = b * hkv * t_kv * (nb + nbv)
+    per_layer = b * hkv * t_kv * (nb + nbv + 2 * nhd)
     log(f"config 5 caches ready: {layers} layers x {per_layer / 1e6:.1f} MB")
     ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b, hq, hkv, 1, d, t_kv, 0, args.splits)
     splits = lib.ss_decode_default_splits(b, hq, hkv, 1, d, t_kv) if args.splits <= 0 else args.splits
@@ -364,8 +374,10 @@ def run_config5(args) -> int:
     fn = lib.ss_decode_attn_sunshape_v
     argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cents.data_ptr(),
              nb, 256, ki.data_ptr(), vi.data_ptr(), v_cents.data_ptr(), vbd, 256,
-             v_transform.data_ptr(), t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0, out.data_ptr(),
-             hip.SS_F16, ws.data_ptr(), ws_bytes, args.splits, stream) for ki, vi in caches]
+             v_transform.data_ptr(), kh.data_ptr() if kh is not None else None,
+             heavy_dims.data_ptr(), nhd, t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0,
+             out.data_ptr(), hip.SS_F16, ws.data_ptr(), ws_bytes, args.splits, stream)
+            for ki, vi, kh in caches]
 
     def step():
         for a in argv:
@@ -395,12 +407,15 @@ def run_config5(args) -> int:
         hip.check(fn(*argv[0]))
         torch.cuda.synchronize()
         bi, hi = 11, 3
-        ki, vi = caches[0]
+        ki, vi, kh = caches[0]
         vals = O.dequantize_blockvq(vi[bi, hi].cpu().numpy(), v_cents.cpu().numpy(),
                                     inv.cpu().numpy())
         qh = q[bi:bi + 1, hi * 4:(hi + 1) * 4].cpu().numpy()
-        ref = O.sdpa(qh, ki[bi:bi + 1, hi:hi + 1].cpu().numpy(), vals[None, None],
-                     cents.cpu().numpy(), perm.cpu().numpy(), scale)
+        ref = O.sdpa_two_pass(qh, scale, perm.cpu().numpy(), cents.cpu().numpy(),
+                              ki[bi:bi + 1, hi:hi + 1].cpu().numpy(), None, vals[None, None],
+                              heavy_keys=(kh[bi:bi + 1, hi:hi + 1].cpu().numpy()
+                                          if kh is not None else None),
+                              heavy_dims=heavy_dims.cpu().numpy())
         got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
         check = float(np.abs(got - ref).max() / np.abs(ref).max())
 
@@ -411,7 +426,10 @@ def run_config5(args) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"{layers} layers x decode B=16 Hq=32 Hkv=8 D=128 T_kv={t_kv}, "
-                               "mixed-precision keys (16 u8 indices, 4 heavy blocks zero), "
+                               + ("mixed-precision keys (16 u8 indices + 4 heavy blocks' 32 dims "
+                                  "fp16, scored exactly), " if heavy_fp16 else
+                                  "mixed-precision keys (16 u8 indices, 4 heavy blocks zero as in "
+                                  "the reference), ") +
                                "SunShape values block_dim 4 / 256 centroids (32 u8 indices), "
                                "fp16 query/output",
                    "t_kv": t_kv, "layers": layers, "splits": splits,
