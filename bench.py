@@ -59,7 +59,7 @@ def parse_args():
                         "(default: keep them in fp16 and score them exactly)")
     p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5"),
                    default="metric",
-                   help="metric: the BASELINE metric decode (fp16 values, B=1); hybrid: config 4 "
+                   help="metric: the headline metric decode (fp16 values, B=1); hybrid: config 4 "
                         "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
                         "(65,536 fp16 keys block-VQ encoded); turboquant: the config-4 shape "
                         "with 2-bit TurboQuant values; config5: 28 layers x B=16, "

@@ -47,7 +47,7 @@ def decode_case(seed, b, hq, hkv, d, t_kv, t_q=1, cap=None, nc=256, v_dtype=np.f
 @pytest.mark.parametrize(
     "b,hq,hkv,d,t_kv,t_q,causal,splits,cap",
     [
-        (1, 32, 8, 128, 4096, 1, False, 0, None),    # BASELINE config 2 shape
+        (1, 32, 8, 128, 4096, 1, False, 0, None),    # config-2 shape (the metric decode)
         (1, 32, 8, 128, 4096, 1, True, 0, 4352),     # causal no-op at decode, padded cap
         (2, 8, 2, 128, 1000, 1, False, 0, 1024),     # ragged T, B=2
         (1, 4, 1, 128, 1, 1, False, 0, 256),         # single token
@@ -108,7 +108,7 @@ def test_decode_bf16_and_f32_values():
 
 
 @pytest.mark.parametrize("bits,group,sz,d,t_kv,causal,t_q", [
-    (2, 64, np.float16, 128, 2048, False, 1),   # BASELINE config 4 format
+    (2, 64, np.float16, 128, 2048, False, 1),   # config-4 value format
     (2, 64, np.float32, 128, 700, False, 1),    # reference storage (f32 scale/zero)
     (4, 64, np.float32, 128, 64, False, 1),     # known-answer [15] shape
     (4, 64, np.float32, 128, 32, True, 4),      # [16] shape
@@ -171,7 +171,7 @@ def test_encode_bit_exact_except_near_ties(n_tok, bd, dtype):
 
 
 def test_encode_config3_shape_and_cache_strides():
-    """fp16 K (8 heads x 8192 tokens x 128), ProfilePerm,
+    """Config 3: fp16 K (8 heads x 8192 tokens x 128), ProfilePerm,
     encoded straight into a padded cache buffer (B, H, cap, 16) at an offset."""
     rng = np.random.default_rng(3)
     h, n, d, cap, off = 8, 8192, 128, 8192 + 512, 256
@@ -298,7 +298,7 @@ def test_append_values_il8_roundtrip_and_offsets():
 @pytest.mark.parametrize(
     "b,hq,hkv,d,t_kv,t_q,causal,splits,cap",
     [
-        (1, 32, 8, 128, 4096, 1, False, 0, None),    # BASELINE config 2 shape
+        (1, 32, 8, 128, 4096, 1, False, 0, None),    # config-2 shape (the metric decode)
         (1, 32, 8, 128, 32768, 1, False, 0, None),   # metric shape
         (2, 8, 2, 128, 1003, 1, False, 0, 1024),     # ragged T (partial 8-token block)
         (1, 4, 1, 128, 1, 1, False, 0, 256),         # single token
