@@ -2040,15 +2040,31 @@ __global__ void __launch_bounds__(kDecodeThreads)
             store_from_f32(c.out, c.out_dtype, off + d, y);
     }
     if (rot) {
-        // the merged row is in the TurboQuant rotated basis: out = y @ R,
-        // summed over k in order as rotate_rows_kernel does
+        // the merged row is in a transformed basis (TurboQuant rotation, a
+        // value codec's permutation or rotation): out = y @ M.  Every thread
+        // takes one output dim and a contiguous share of k (two interleaved
+        // accumulators), reading row k of M coalesced over the dims; the
+        // shares are added in LDS.
+        constexpr int PARTS = kDecodeThreads / D, KP = D / PARTS;
+        __shared__ float rsum[PARTS][D];
+        __syncthreads();
+        {
+            const int dd = tid % D, part = tid / D, k0 = part * KP;
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+            for (int k = k0; k < k0 + KP; k += 2) {
+                a0 = fmaf(yrow[k], rot[k * D + dd], a0);
+                a1 = fmaf(yrow[k + 1], rot[(k + 1) * D + dd], a1);
+            }
+            rsum[part][dd] = a0 + a1;
+        }
         __syncthreads();
         if (tid < D) {
             const int64_t rr = gr / c.t_q, tq = gr - rr * c.t_q;
             const int64_t off = ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
             float a = 0.f;
-#pragma unroll 8
-            for (int k = 0; k < D; ++k) a = fmaf(yrow[k], rot[k * D + tid], a);
+#pragma unroll
+            for (int pp = 0; pp < PARTS; ++pp) a += rsum[pp][tid];
             store_from_f32(rot_out, rot_dtype, off + tid, a);
         }
     }
