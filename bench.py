@@ -57,7 +57,8 @@ def parse_args():
     p.add_argument("--reference-mixed", action="store_true",
                    help="config5: drop the heavy blocks from the scores as the reference does "
                         "(default: keep them in fp16 and score them exactly)")
-    p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5"),
+    p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5",
+                                          "fit"),
                    default="metric",
                    help="metric: the headline metric decode (fp16 values, B=1); hybrid: config 4 "
                         "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
@@ -442,6 +443,66 @@ def run_config5(args) -> int:
     return 0
 
 
+def run_fit(args) -> int:
+    """Codec fit of config 1 (seed 42: q_cal (1024, 128) and k_cal (2048, 128)
+    N(0,1), profileperm_baseline, 15 k-means iterations): the per-block
+    k-means of every block in one ss_kmeans_blocks launch, timed with HIP
+    events, beside the NumPy k-means loop of the same fit on the host."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(42)
+    k_cal = rng.standard_normal((2048, 128)).astype(np.float32)
+    nb, bd, k, iters = 16, 8, 256, 15
+    data = torch.from_numpy(np.ascontiguousarray(k_cal.reshape(2048, nb, bd).transpose(1, 0, 2))).to(dev)
+    init = torch.stack([data[b][torch.from_numpy(np.random.RandomState(42 + b).permutation(2048)[:k])
+                                .to(dev)] for b in range(nb)])
+    for _ in range(2):
+        hip.kmeans_blocks(data, init, iters)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(3, args.steps // 20)
+    ev0.record()
+    for _ in range(n):
+        out = hip.kmeans_blocks(data, init, iters)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / n
+    t0 = time.perf_counter()
+    ref = [pkg.codec._kmeans(data[b].cpu().numpy(), k, n_iters=iters, seed=42 + b) for b in range(nb)]
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    x = data.cpu().numpy().astype(np.float64)
+
+    def inertia(c):
+        return float(np.mean([((x[b][:, None] - np.asarray(c[b], np.float64)[None]) ** 2)
+                              .sum(-1).min(1).mean() for b in range(nb)]))
+
+    flops = nb * iters * 2048 * k * bd * 2
+    line = {
+        "metric": "codec fit k-means ms (config 1: 16 blocks, 2048 points, 256 centroids, 15 iterations)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": n, "warmup": 2,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "ss_kmeans_blocks over the 16 blocks of k_cal (2048 x 128, seed 42)",
+                   "assignment_flops_per_step": flops},
+        "roofline": {"bound": "valu", "achieved": round(flops / (ms * 1e-3) / 1e12, 3),
+                     "peak": VALU_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flops / (ms * 1e-3) / 1e12 / VALU_FP32_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": {"value": round(cpu_ms, 2), "unit": "ms", "cores": 1, "kind": "port",
+                         "sample": "the same 16-block k-means in NumPy (codec._kmeans), once"},
+        "inertia": {"gpu": round(inertia(out.cpu().numpy()), 6), "numpy": round(inertia(ref), 6)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 VALU_FP32_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMD x 16 lanes x 2 flops x 2.4 GHz, no packed fp32
 
 
@@ -529,6 +590,8 @@ def main() -> int:
         return calibrate_copy(args.calibrate_copy, args.steps)
     if args.workload == "hybrid":
         return run_hybrid(args)
+    if args.workload == "fit":
+        return run_fit(args)
     if args.workload == "config5":
         if args.t_kv == 32768 and "--t-kv" not in sys.argv:
             args.t_kv = 131072
