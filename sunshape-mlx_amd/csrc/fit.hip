@@ -77,13 +77,22 @@ __global__ void __launch_bounds__(kFitThreads)
 #pragma unroll
             for (int j = 0; j < BD; ++j) s[j] = 0.f;
             int64_t cnt = 0;
-            for (int64_t i = 0; i < n; ++i) {
-                if (asg[i] == tid) {
-                    ++cnt;
+            auto take = [&](int64_t i) {
+                ++cnt;
 #pragma unroll
-                    for (int j = 0; j < BD; ++j) s[j] = __fadd_rn(s[j], x[i * BD + j]);
-                }
+                for (int j = 0; j < BD; ++j) s[j] = __fadd_rn(s[j], x[i * BD + j]);
+            };
+            // four assignments per LDS read, still in point order
+            const uint32_t *asg4 = reinterpret_cast<const uint32_t *>(asg);
+            const int64_t n4 = n / 4;
+            for (int64_t w = 0; w < n4; ++w) {
+                const uint32_t v = asg4[w];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (((v >> (8 * q)) & 0xffu) == (uint32_t)tid) take(w * 4 + q);
             }
+            for (int64_t i = n4 * 4; i < n; ++i)
+                if (asg[i] == tid) take(i);
             if (cnt > 0) {
 #pragma unroll
                 for (int j = 0; j < BD; ++j)
