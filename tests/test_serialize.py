@@ -63,7 +63,24 @@ def _caches():
                                                         buffer_size=16)),
         ("hybrid-fp16", lambda c: S.create_kv_cache(c, n_kv_heads=2, value_bits=None,
                                                     value_backend="fp16", buffer_size=48)),
+        ("hybrid-sunshape-heavy-fp16", lambda c: S.create_kv_cache(
+            _heavy_codec(c), n_kv_heads=2, value_backend="sunshape", value_bits=8,
+            value_codec=_codec(10, device="cuda", bd=4), buffer_size=24)),
     ]
+
+
+def _heavy_codec(base):
+    """A mixed-precision codec with 4 heavy blocks kept in fp16, built from
+    ``base``'s arrays."""
+    heavy = np.zeros(16, bool)
+    heavy[[1, 4, 9, 15]] = True
+    cents = base.centroids.cpu().numpy().copy()
+    cents[heavy] = 0.0
+    codec = S.SunShapeBlockCodec(128, device=base.device, mode="profileperm_mixed_precision",
+                                 heavy_fp16=True)
+    return codec.load_state_dict({"centroids": cents,
+                                  "permutation": base.permutation.cpu().numpy(),
+                                  "mixed_high_precision_blocks": heavy})
 
 
 @pytest.mark.gpu
