@@ -35,6 +35,7 @@ extern "C" {
 #define SS_ERR_UNSUPPORTED (-2) /* valid but not implemented for this shape */
 #define SS_ERR_HIP (-3)         /* HIP runtime error */
 #define SS_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+#define SS_ERR_WAIT (-5)        /* a bounded in-kernel wait gave up (ss_decode_wait_failures) */
 
 #define SS_F32 0
 #define SS_F16 1
@@ -104,6 +105,30 @@ int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centro
 size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                  int64_t t_q, int head_dim, int64_t t_kv,
                                  int n_splits);
+
+/*
+ * Bounded-wait failures of the matrix-core fused decodes
+ * (ss_decode_attn_il8, ss_decode_attn_grouped_il[_hybrid]) on the current
+ * device.  Their waves hand tiles over through LDS flags and wait for each
+ * other at compute-wave barriers; every such wait gives up after a bounded
+ * number of sleeps, so a broken hand-off ends the kernel instead of hanging
+ * it, and sets a bit in a sticky per-device word (1 compute barrier, 2 ring
+ * slot, 4 ring tile).  The output of such a launch is invalid.  This call
+ * synchronizes `stream`, stores the word in *flags (may be NULL), clears it
+ * when `clear` is nonzero and returns SS_ERR_WAIT if it was nonzero, else
+ * SS_OK.  No reference counterpart: the reference's Metal kernels
+ * (kernels.py:142-446, 588-928) have no cross-wave hand-off.
+ */
+int ss_decode_wait_failures(void *stream, int clear, unsigned int *flags);
+
+/*
+ * Test hook: the number of sleeps after which those waits give up, for
+ * launches issued after this call (process-wide); a negative value restores
+ * the default (2^20, about 0.03 s).  A small limit makes waits give up while
+ * every wave still ends normally, which is how the failure report above is
+ * tested.  No reference counterpart.
+ */
+int ss_debug_set_spin_limit(int limit);
 
 /* Split count the library would choose (n_splits <= 0 in the calls below). */
 int ss_decode_default_splits(int64_t batch, int n_q_heads, int n_kv_heads,
@@ -259,12 +284,15 @@ size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_
  *                or the codec rotation)
  *   k_heavy      NULL, or fp16 [batch][n_kv_heads][cap][n_heavy_dims]: the
  *                heavy blocks' key dims of a mixed-precision codec (codec
- *                basis), scored exactly beside the LUT; heavy_dims int32
- *                [n_heavy_dims] are their codec-basis dims (n_heavy_dims a
- *                multiple of 8, at most 64).  The reference zeroes these
- *                blocks' centroids and drops them from the scores
- *                (codec.py:381-388, cache.py:187-189) although its README
- *                calls them fp16 blocks; NULL keeps the reference's scores.
+ *                basis), scored exactly in place of the LUT; heavy_dims
+ *                int32 [n_heavy_dims] are their codec-basis dims
+ *                (n_heavy_dims a multiple of 8, at most 64).  Every block
+ *                holding a heavy dim leaves the centroid sum, whatever its
+ *                centroids hold.  The reference zeroes these blocks'
+ *                centroids at fit time (codec.py:381-388; its DSQ
+ *                refinement can move them again, codec.py:400-410) and
+ *                scores index 0 of them, although its README calls them
+ *                fp16 blocks; NULL keeps the reference's scores.
  *   workspace    ss_decode_turboquant_workspace_bytes(...) bytes (same layout)
  */
 int ss_decode_attn_sunshape_v(const void *q, int q_dtype, int64_t batch, int n_q_heads,

@@ -33,12 +33,24 @@ fused_attention(_grouped)      textbook softmax(q k_hat^T) V with k_hat from
 pack/unpack_indices            bit layout closed form, [1]-[3], [9]
 quantize/dequantize_values     per-group min/max closed form, error bounds [4]
 scalar_quantize                == searchsorted on sorted boundaries ([5])
-lloyd_max_gaussian             1-bit closed form sqrt(2/pi); Max (1960) table
+lloyd_max_gaussian             the reference's literal table: symmetric,
+                               midpoint boundaries, 1-bit closed form
+                               sqrt(2/pi), within 1e-9 (2, 3 bits) and
+                               4e-4 (4 bits) of the Lloyd-Max fixed point
 turboquant_encode/decode       rotation orthogonality; round-trip MSE bound
 sdpa                           per-head loop == fused_attention per (b,h,r);
                                GQA head mapping h*rep + r (attention.py:220)
-kmeans / covariance_perm       (fixture generation only) monotone distortion,
-                               permutation validity
+kmeans                         hand-worked Lloyd steps from the reference's
+                               initial rows (seeds 0, 1), empty cluster kept,
+                               zero-padded short data, non-increasing
+                               distortion, converged centroids = cluster
+                               means (tests/test_oracle_fit.py)
+covariance_block_permutation   hand-worked greedy packings of exact factor
+                               covariances (2 and 3 blocks; the zeroed
+                               diagonal decides the seed), identity for
+                               uncorrelated dims, permutation validity
+fit_profileperm_baseline       per-block initial rows RandomState(seed + b)
+                               in closed form, zero-padded short data
 =============================  ===============================================
 """
 
@@ -379,12 +391,51 @@ def scalar_quantize(values, boundaries) -> np.ndarray:
     return out
 
 
-def lloyd_max_gaussian(bits: int, iters: int = 2000, tol: float = 1e-15):
-    """Lloyd-Max quantizer of N(0, 1) (levels, boundaries), computed by the
-    classical fixed-point iteration (Max, 1960): boundaries are midpoints of
-    adjacent levels; each level is the conditional mean of its cell,
-    ``(phi(a) - phi(b)) / (Phi(b) - Phi(a))``.  The reference ships these as
-    literal tables (value_codecs.py:20-87)."""
+# The reference's TurboQuant codebooks (value_codecs.py:20-87): Lloyd-Max
+# levels and boundaries of N(0, 1), stored there as literal tables and kept
+# here as the same data, levels then boundaries.
+_REF_LLOYD_MAX = {
+    1: ([-0.7978845608028654, 0.7978845608028654], [0.0]),
+    2: ([-1.510417608611893, -0.4527800346911237, 0.4527800346911237, 1.510417608611893],
+        [-0.9815988216515084, 0.0, 0.9815988216515084]),
+    3: ([-2.151945705166112, -1.3439092791423422, -0.7560052816730181, -0.2450941791152904,
+         0.2450941791152904, 0.7560052816730181, 1.3439092791423422, 2.151945705166112],
+        [-1.7479274921542272, -1.0499572804076802, -0.5005497303941542, 0.0,
+         0.5005497303941542, 1.0499572804076802, 1.7479274921542272]),
+    4: ([-2.732896755154294, -2.069364258154187, -1.618400443227723, -1.2565648452462146,
+         -0.9426291036999694, -0.6569817464411519, -0.38818871416000605,
+         -0.12844300124876415, 0.12844300124876415, 0.38818871416000605,
+         0.6569817464411519, 0.9426291036999694, 1.2565648452462146, 1.618400443227723,
+         2.069364258154187, 2.732896755154294],
+        [-2.4011305066542405, -1.8438823506909552, -1.4374826442369688, -1.099596974473092,
+         -0.7998054250705606, -0.522585230300579, -0.2583158577043851, 0.0,
+         0.2583158577043851, 0.522585230300579, 0.7998054250705606, 1.099596974473092,
+         1.4374826442369688, 1.8438823506909552, 2.4011305066542405]),
+}
+
+
+def lloyd_max_gaussian(bits: int):
+    """The reference's Lloyd-Max tables of N(0, 1) (value_codecs.py:20-87):
+    ``(levels, boundaries)`` as float64 arrays."""
+    lv, bd = _REF_LLOYD_MAX[bits]
+    return np.array(lv, np.float64), np.array(bd, np.float64)
+
+
+def turboquant_tables(bits: int, d: int):
+    """Scaled float32 tables of ``TurboQuantValueCodec`` (value_codecs.py:
+    148-151): python-float products ``x * (1 / sqrt(d))`` rounded to
+    float32.  Returns ``(centroids, boundaries)``."""
+    lv, bd = _REF_LLOYD_MAX[bits]
+    s = 1.0 / math.sqrt(d)
+    return (np.array([x * s for x in lv], np.float32), np.array([x * s for x in bd], np.float32))
+
+
+def lloyd_max_fixed_point(bits: int, iters: int = 2000, tol: float = 1e-15):
+    """Lloyd-Max quantizer of N(0, 1) computed by the classical fixed-point
+    iteration (Max, 1960): boundaries are midpoints of adjacent levels; each
+    level is the conditional mean of its cell,
+    ``(phi(a) - phi(b)) / (Phi(b) - Phi(a))``.  Used to pin the literal
+    tables above."""
     from scipy.stats import norm
 
     n = 1 << bits
@@ -481,8 +532,14 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
     ``heavy_keys`` (B, Hkv, Tc, nhd) with ``heavy_dims`` (nhd,): the build's
     extension for mixed-precision codecs (heavy blocks kept in fp16, the
     intent of README.md:87, where the reference zeroes their centroids,
-    codec.py:381-388): the compressed scores gain the exact dot products
-    ``q_t[heavy_dims] . k_heavy``."""
+    codec.py:381-388): the heavy blocks (those holding ``heavy_dims``) leave
+    the centroid sum, whatever their centroids hold (the fit's DSQ
+    refinement moves centroid 0, codec.py:400-410), and the exact dot
+    products ``q_t[heavy_dims] . k_heavy`` take their place."""
+    if heavy_keys is not None:
+        bd = np.asarray(centroids).shape[2]
+        centroids = np.array(centroids, dtype=np.float32, copy=True)
+        centroids[np.unique(np.asarray(heavy_dims, np.int64) // bd)] = 0.0
     q = scale_query(queries, scale)
     b_, hq, tq, d = q.shape
     hkv = values_all.shape[1]

@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+from collections import defaultdict
 
 import torch
 
@@ -24,6 +25,7 @@ SS_ERR_INVALID = -1
 SS_ERR_UNSUPPORTED = -2
 SS_ERR_HIP = -3
 SS_ERR_WORKSPACE = -4
+SS_ERR_WAIT = -5
 
 SS_F32, SS_F16, SS_BF16 = 0, 1, 2
 _DTYPE_CODE = {torch.float32: SS_F32, torch.float16: SS_F16, torch.bfloat16: SS_BF16}
@@ -39,6 +41,11 @@ class SunShapeHIPError(RuntimeError):
 
 class SunShapeUnsupported(SunShapeHIPError):
     """Valid arguments the HIP kernels do not implement (status -2)."""
+
+
+class SunShapeWaitError(SunShapeHIPError):
+    """A bounded in-kernel wait of a fused decode gave up (status -5): the
+    output of that launch is invalid."""
 
 
 _c_void_p = ctypes.c_void_p
@@ -59,6 +66,8 @@ _SIGNATURES = {
     "ss_score_gather": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _i64, _i64, _c_void_p,
                                _i64, _c_void_p]),
     "ss_decode_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
+    "ss_decode_wait_failures": (_int, [_c_void_p, _int, ctypes.POINTER(ctypes.c_uint)]),
+    "ss_debug_set_spin_limit": (_int, [_int]),
     "ss_decode_default_splits": (_int, [_i64, _int, _int, _i64, _int, _i64]),
     "ss_decode_attn_dense": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                     _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
@@ -153,12 +162,36 @@ def _raise(rc: int):
     msg = load_library().ss_last_error().decode(errors="replace")
     if rc == SS_ERR_UNSUPPORTED:
         raise SunShapeUnsupported(rc, msg)
+    if rc == SS_ERR_WAIT:
+        raise SunShapeWaitError(rc, msg)
     raise SunShapeHIPError(rc, msg)
 
 
 def check(rc: int) -> None:
     if rc != SS_OK:
         _raise(rc)
+
+
+# Kernel dispatch counters (reference kernels.py:33-47, incremented at every
+# Metal dispatch, kernels.py:113, 288, 443, 498, 762, 925, 1079): every
+# wrapper below that launches a kernel counts its launch here once the call
+# has been accepted, whichever Python route (cache, SDPA, codec, launcher)
+# reached it.  ``kernels.get_kernel_stats`` reads this table.
+_KERNEL_STATS: dict[str, int] = defaultdict(int)
+
+
+def record_dispatch(name: str) -> None:
+    _KERNEL_STATS[name] += 1
+
+
+def _launched(name: str, rc: int) -> None:
+    """``check(rc)``, then count one dispatch of ``name``."""
+    check(rc)
+    _KERNEL_STATS[name] += 1
+
+
+def _attn_stat(stem: str, causal) -> str:
+    return f"{stem}_causal_hip" if causal else f"{stem}_hip"
 
 
 def dtype_code(dt: torch.dtype) -> int:
@@ -186,6 +219,50 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def stream_handle(device: torch.device | None = None) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+# --------------------------------------------------------------------------- #
+#  Bounded-wait failures of the matrix-core decodes                           #
+# --------------------------------------------------------------------------- #
+
+# Check the wait-failure word after every matrix-core decode launch (one
+# stream synchronisation per call); off by default, on with
+# SUNSHAPE_CHECK_WAITS=1 or set_wait_checks(True).
+_check_waits = os.environ.get("SUNSHAPE_CHECK_WAITS", "0") == "1"
+
+
+def set_wait_checks(enabled: bool) -> bool:
+    """Turn the per-call wait check on or off; returns the previous setting."""
+    global _check_waits
+    prev, _check_waits = _check_waits, bool(enabled)
+    return prev
+
+
+def decode_wait_failures(device: torch.device | None = None, clear: bool = True) -> int:
+    """Synchronise the current stream of ``device`` and return the sticky
+    wait-failure flags of the matrix-core decodes (0 if every wait ended in
+    time; bit 1 compute barrier, 2 ring slot, 4 ring tile), clearing them
+    when ``clear``."""
+    flags = ctypes.c_uint(0)
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        rc = load_library().ss_decode_wait_failures(stream_handle(device), int(clear),
+                                                    ctypes.byref(flags))
+    if rc not in (SS_OK, SS_ERR_WAIT):
+        _raise(rc)
+    return int(flags.value)
+
+
+def check_decode_waits(device: torch.device | None = None) -> None:
+    """Raise ``SunShapeWaitError`` (and clear the flags) if a bounded wait
+    of a matrix-core decode launched on ``device`` has given up."""
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        check(load_library().ss_decode_wait_failures(stream_handle(device), 1, None))
+
+
+def set_spin_limit(limit: int | None) -> None:
+    """Test hook: sleeps before a bounded wait gives up, for later launches
+    (None restores the default)."""
+    check(load_library().ss_debug_set_spin_limit(-1 if limit is None else int(limit)))
 
 
 # --------------------------------------------------------------------------- #
@@ -238,7 +315,7 @@ def encode_blockvq(keys: torch.Tensor, perm: torch.Tensor | None, centroids: tor
     if perm is not None and (perm.dtype != torch.int32 or perm.numel() != d):
         raise ValueError("perm must be int32 of length head_dim")
     lib = load_library()
-    check(lib.ss_encode_blockvq(
+    _launched("sunshape_block_vq_quantize_hip", lib.ss_encode_blockvq(
         ptr(k4), dtype_code(k4.dtype), b_, h_, t_, k4.stride(0), k4.stride(1), k4.stride(2), d,
         ptr(perm), ptr(centroids), nb, nc, bd, ptr(o4), o4.stride(0), o4.stride(1),
         o4.stride(2), stream_handle(keys.device)))
@@ -253,7 +330,7 @@ def build_lut(q: torch.Tensor, perm: torch.Tensor | None, scale: float,
         raise ValueError("q must be (n_rows, head_dim) with unit last stride")
     nb, nc, bd = centroids.shape
     lut = torch.empty((q.shape[0], nb, nc), dtype=torch.float32, device=q.device)
-    check(load_library().ss_build_lut(
+    _launched("sunshape_query_centroid_dots_hip", load_library().ss_build_lut(
         ptr(q), dtype_code(q.dtype), q.shape[0], q.stride(0), q.shape[1], ptr(perm), float(scale),
         ptr(centroids), nb, nc, bd, ptr(lut), stream_handle(q.device)))
     return lut
@@ -267,7 +344,7 @@ def score_gather(lut: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     lut = lut.contiguous().float()
     r_, nb, nc = lut.shape
     scores = torch.empty((r_, idx.shape[0]), dtype=torch.float32, device=lut.device)
-    check(load_library().ss_score_gather(
+    _launched("sunshape_block_vq_score_hip", load_library().ss_score_gather(
         ptr(lut), r_, nb, nc, ptr(idx), idx.shape[0], idx.stride(0), ptr(scores), idx.shape[0],
         stream_handle(lut.device)))
     return scores
@@ -281,7 +358,7 @@ def dequantize_blockvq(idx: torch.Tensor, centroids: torch.Tensor, inv_perm: tor
         raise ValueError("indices must be uint8 (T, n_blocks) with unit last stride")
     nb, nc, bd = centroids.shape
     out = torch.empty((idx.shape[0], nb * bd), dtype=out_dtype, device=idx.device)
-    check(load_library().ss_dequantize_blockvq(
+    _launched("sunshape_block_vq_dequantize_hip", load_library().ss_dequantize_blockvq(
         ptr(idx), idx.shape[0], idx.stride(0), ptr(centroids), nb, nc, bd, ptr(inv_perm), ptr(out),
         dtype_code(out_dtype), stream_handle(idx.device)))
     return out
@@ -329,7 +406,7 @@ def decode_attn_dense(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
-    check(load_library().ss_decode_attn_dense(
+    _launched(_attn_stat("sunshape_fused_attention", causal), load_library().ss_decode_attn_dense(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(values), dtype_code(values.dtype), cap, int(t_kv), int(bool(causal)),
         int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
@@ -387,11 +464,13 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
-    check(load_library().ss_decode_attn_il8(
+    _launched(_attn_stat("sunshape_fused_attention_mfma", causal), load_library().ss_decode_attn_il8(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
         nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv), int(bool(causal)),
         int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
         int(n_splits), stream_handle(q.device)))
+    if _check_waits:
+        check_decode_waits(q.device)
     return out
 
 
@@ -442,7 +521,7 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
-    check(load_library().ss_decode_attn_grouped(
+    _launched(_attn_stat("sunshape_fused_attention_dequant", causal), load_library().ss_decode_attn_grouped(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(scales), ptr(zeros), dtype_code(scales.dtype),
         int(bits), int(group_size), cap, int(t_kv), int(bool(causal)), int(q_offset), ptr(out),
@@ -465,7 +544,7 @@ def kmeans_blocks(data: torch.Tensor, init: torch.Tensor, iters: int,
     nb, n, bd = data.shape
     k = cents.shape[1]
     assign = torch.empty((nb, n), dtype=torch.uint8, device=data.device) if return_assign else None
-    check(load_library().ss_kmeans_blocks(ptr(data), nb, n, bd, k, int(iters), ptr(cents),
+    _launched("sunshape_kmeans_hip", load_library().ss_kmeans_blocks(ptr(data), nb, n, bd, k, int(iters), ptr(cents),
                                           ptr(assign), stream_handle(data.device)))
     return (cents, assign) if return_assign else cents
 
@@ -536,7 +615,7 @@ def decode_attn_sunshape_v(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
                                                         int(n_splits))
     ws = decode_workspace(q.device, ws_bytes)
-    check(lib.ss_decode_attn_sunshape_v(
+    _launched(_attn_stat("sunshape_fused_attention_sunshape_v", causal), lib.ss_decode_attn_sunshape_v(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(v_idx), ptr(v_centroids), vbd, vnc, ptr(v_transform),
         ptr(k_heavy), ptr(heavy_dims), nhd, cap,
@@ -588,7 +667,7 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
                                                         int(n_splits))
     ws = decode_workspace(q.device, ws_bytes)
-    check(lib.ss_decode_attn_turboquant(
+    _launched(_attn_stat("sunshape_fused_attention_turboquant", causal), lib.ss_decode_attn_turboquant(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
         ptr(rotation), int(bits), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
@@ -640,8 +719,10 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     tail = (ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
             int(n_splits), stream_handle(q.device))
     if buf_keys is None or buf_len == 0:
-        check(load_library().ss_decode_attn_grouped_il(
+        _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il(
             *common, int(bool(causal)), int(q_offset), *tail))
+        if _check_waits:
+            check_decode_waits(q.device)
         return out
     require_gpu(buf_keys, buf_values)
     if buf_keys.dim() != 4 or buf_keys.shape[:2] != (b_, hkv) or buf_keys.shape[3] != d or \
@@ -650,10 +731,12 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
             buf_keys.shape[2] < buf_len:
         raise ValueError("buf_keys/buf_values must be matching (B, n_kv_heads, >= buf_len, D) "
                          "views with unit last stride")
-    check(load_library().ss_decode_attn_grouped_il_hybrid(
+    _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il_hybrid(
         *common, ptr(buf_keys), ptr(buf_values), dtype_code(buf_keys.dtype), buf_keys.stride(0),
         buf_keys.stride(1), buf_keys.stride(2), int(buf_len), int(bool(causal)), int(q_offset),
         *tail))
+    if _check_waits:
+        check_decode_waits(q.device)
     return out
 
 
@@ -721,7 +804,7 @@ def quantize_values_grouped(values: torch.Tensor, bits: int, group_size: int,
     o_sb, o_sh, o_st = p4.stride(0) // nw, p4.stride(1) // nw, p4.stride(2) // nw
     if (s4.stride(0) // ng, s4.stride(1) // ng, s4.stride(2) // ng) != (o_sb, o_sh, o_st):
         raise ValueError("packed and scales/zeros buffers must share the token layout")
-    check(load_library().ss_quantize_values_grouped(
+    _launched("sunshape_quantize_values_hip", load_library().ss_quantize_values_grouped(
         ptr(v4), dtype_code(v4.dtype), b_, h_, t_, v4.stride(0), v4.stride(1), v4.stride(2), d,
         int(bits), int(group_size), ptr(p4), ptr(s4), ptr(z4), dtype_code(s4.dtype), o_sb, o_sh,
         o_st, stream_handle(values.device)))
@@ -769,6 +852,6 @@ def scalar_quantize(values: torch.Tensor, boundaries: torch.Tensor) -> torch.Ten
     v = values.reshape(-1).float().contiguous()
     b = boundaries.reshape(-1).float().contiguous()
     out = torch.empty(v.shape, dtype=torch.uint8, device=values.device)
-    check(load_library().ss_scalar_quantize(ptr(v), v.numel(), ptr(b), b.numel(), ptr(out),
+    _launched("sunshape_scalar_quantize_hip", load_library().ss_scalar_quantize(ptr(v), v.numel(), ptr(b), b.numel(), ptr(out),
                                             stream_handle(values.device)))
     return out.reshape(values.shape)

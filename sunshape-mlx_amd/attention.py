@@ -88,7 +88,7 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
             codec.last_score_backend = ("hip_fused_turboquant_buffer" if buffered
                                         else "hip_fused_turboquant")
         elif ops["kind"] == "sunshape_v":
-            out = _hip.decode_attn_sunshape_v(q, kscale, perm, codec.centroids, ops["idx"],
+            out = _hip.decode_attn_sunshape_v(q, kscale, perm, codec.scoring_centroids(), ops["idx"],
                                               ops["v_idx"], ops["v_centroids"], ops["v_transform"],
                                               buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
                                               buf_len=buffered, k_heavy=ops["k_heavy"],
@@ -114,12 +114,13 @@ def _compressed_scores(codec: SunShapeBlockCodec, q_t: torch.Tensor,
     """(B, Hkv, rep, Tq, Tc) float32 scores of codec-space queries q_t
     (B, Hkv, rep, Tq, D) against (B, Hkv, Tc, NB) indices
     (attention.py:44-73): one HIP LUT build for all rows, one gather per
-    (batch, KV head)."""
+    (batch, KV head).  Fp16 heavy blocks add nothing here (their exact dot
+    products are added by the caller)."""
     b_, hkv, rep, tq, d = q_t.shape
     rows = q_t.reshape(-1, d)
     if rows.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         rows = rows.float()
-    lut = _hip.build_lut(rows.contiguous(), None, 1.0, codec.centroids)
+    lut = _hip.build_lut(rows.contiguous(), None, 1.0, codec.scoring_centroids())
     lut = lut.reshape(b_, hkv, rep * tq, codec.n_blocks, codec.n_centroids)
     tc = key_indices.shape[2]
     scores = torch.empty((b_, hkv, rep * tq, tc), dtype=torch.float32, device=q_t.device)

@@ -355,11 +355,34 @@ class SunShapeBlockCodec:
             self._kernel_value_transform = cached
         return cached[1]
 
-    def kernel_codebook(self) -> torch.Tensor:
-        """The centroids as the split-fp16 buffer read by the matrix-core LUT
-        build of the fused fp16-value decode, prepared once and rebuilt when
-        the centroids change (new tensor, device or in-place update)."""
+    def scoring_centroids(self) -> torch.Tensor:
+        """The centroids a cache's scores read.  With fp16 heavy blocks
+        (``heavy_dims()`` not None) those blocks are scored exactly from
+        their stored key dims, so their table entries must add nothing: a
+        copy of the centroids with the heavy blocks zeroed (the fit's DSQ
+        refinement moves a heavy block's centroid 0 away from zero,
+        reference codec.py:400-410).  Otherwise the centroids themselves, so
+        a heavy block's index 0 adds ``q . C[b][0]`` as in the reference
+        (codec.py:575-637).  Cached until the centroids or the heavy mask
+        change."""
         c = self.centroids
+        if self.heavy_dims() is None:
+            return c
+        hb = self.mixed_high_precision_blocks
+        key = (c.data_ptr(), c._version, hb.data_ptr(), hb._version, str(c.device))
+        cached = getattr(self, "_scoring_centroids", None)
+        if cached is None or cached[0] != key:
+            z = c.clone()
+            z[hb.to(torch.bool).to(z.device)] = 0.0
+            cached = (key, z.contiguous())
+            self._scoring_centroids = cached
+        return cached[1]
+
+    def kernel_codebook(self) -> torch.Tensor:
+        """``scoring_centroids()`` as the split-fp16 buffer read by the
+        matrix-core LUT build of the fused decodes, prepared once and rebuilt
+        when the centroids change (new tensor, device or in-place update)."""
+        c = self.scoring_centroids()
         key = (c.data_ptr(), c._version, str(c.device), tuple(c.shape))
         cached = getattr(self, "_kernel_codebook", None)
         if cached is None or cached[0] != key:
@@ -439,10 +462,12 @@ class SunShapeBlockCodec:
 
     def attention_scores(self, query: torch.Tensor, quantized: SunShapeQuantized, *,
                          prefer_metal: bool = True) -> torch.Tensor:
-        """Unscaled scores (n_qh, n_tokens) = q . k_hat via the query x centroid
-        table (codec.py:575-637).  Mixed-precision heavy blocks contribute 0,
-        as in the reference (their centroids are zero and the passthrough is
-        not read).  ``prefer_metal`` is accepted for signature compatibility."""
+        """Unscaled scores (n_qh, n_tokens) = sum_b q_b . C[b][idx[t, b]] via
+        the query x centroid table (codec.py:575-637).  As in the reference,
+        the passthrough values are not read: a mixed-precision heavy block's
+        index 0 adds ``q_b . C[b][0]``, which is zero after a fit without DSQ
+        refinement (its centroids start at zero) and not after one.
+        ``prefer_metal`` is accepted for signature compatibility."""
         _hip.require_gpu(query)
         q = query.reshape(-1, self.head_dim).float()
         if self.mode in PERM_MODES:

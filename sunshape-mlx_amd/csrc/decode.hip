@@ -21,6 +21,8 @@
 //     step is a single kernel launch.
 // Softmax runs in log2 units (LUT pre-multiplied by log2 e, exp2 on the
 // hardware exp unit), accumulating in float32.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "ss_common.hpp"
@@ -49,7 +51,16 @@ struct DecodeCommon {
     int causal;
     int64_t q_offset;
     int n_splits, tiles_per_split;
+    // bounded waits of the matrix-core kernel: sleeps before a wait gives
+    // up, and the sticky per-device word a give-up sets (kWait* bits)
+    int spin_limit;
+    unsigned int *wait_fail;
 };
+
+// Bits of the wait-failure word: which bounded wait gave up.
+constexpr unsigned kWaitBarrier = 1u;  // compute-wave barrier
+constexpr unsigned kWaitSlot = 2u;     // loader: ring slot still held by its consumer
+constexpr unsigned kWaitTile = 4u;     // compute wave: ring tile not yet published
 
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeWaves = kDecodeThreads / kWave;
@@ -457,7 +468,13 @@ __global__ void __launch_bounds__(kDecodeThreads)
     __syncthreads();
 
     // 2. LUT[r][b][c] = q'[r][b-block] . C[b][c] (kernels.py:178-190), in
-    //    log2 units.
+    //    log2 units.  With fp16 heavy-block keys the blocks holding heavy
+    //    dims are scored from those keys alone: their entries are 0.
+    uint32_t heavy_blocks = 0;
+    if constexpr (VfHeavy<VF>::value)
+        if (va.kheavy)
+            for (int j = 0; j < va.nhd; ++j)
+                heavy_blocks |= 1u << (min(max(va.heavy_dims[j], 0), D - 1) / kBlockDim);
     const int nbc = NB * c.n_centroids;
     for (int e = tid; e < nbc; e += kDecodeThreads) {
         const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
@@ -474,7 +491,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
             dot = fmaf(qr[5], c1.y, dot);
             dot = fmaf(qr[6], c1.z, dot);
             dot = fmaf(qr[7], c1.w, dot);
-            lut[(r * NB + b) * kLutStride + cc] = dot * kLog2e;
+            lut[(r * NB + b) * kLutStride + cc] = ((heavy_blocks >> b) & 1u) ? 0.f : dot * kLog2e;
         }
     }
     if constexpr (VLDS > 0) VF::stage(vlds, va, slab, tid, kDecodeThreads);
@@ -705,8 +722,10 @@ __global__ void __launch_bounds__(kDecodeThreads)
 // Tile j goes to slot j % kSlots and to compute wave j % NC.  Hand-off uses
 // two LDS words per slot: ready[s] = j once tile j has landed (written by the
 // loader after its vmcnt wait), done[s] = j once its consumer has copied the
-// tile into registers.  Every wait on them is bounded (kSpinLimit sleeps), so
-// a protocol error ends the kernel with wrong results instead of hanging.
+// tile into registers.  Every wait on them is bounded (c.spin_limit sleeps,
+// kSpinLimit by default): a wait that gives up sets its bit in the sticky
+// per-device word c.wait_fail and the kernel ends normally with an invalid
+// output, which ss_decode_wait_failures reports to the host.
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -1318,6 +1337,12 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
+    // A bounded wait gave up: record which kind in the sticky word (one
+    // vector atomic per wave; the host reads and clears it).
+    auto wait_gave_up = [&](unsigned kind) {
+        if (lane == 0)
+            __hip_atomic_fetch_or(c.wait_fail, kind, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     // Barrier among the NC compute waves only (the loader never joins it):
     // each wave adds 1 to an LDS counter once its LDS writes are done and
     // waits until all NC waves have arrived for this phase (bounded wait).
@@ -1328,7 +1353,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         int spins = 0;
         while (*cbar < phase * NC) {
             __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) break;
+            if (++spins > c.spin_limit) {
+                wait_gave_up(kWaitBarrier);
+                break;
+            }
         }
         asm volatile("" ::: "memory");
     };
@@ -1518,7 +1546,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 continue;
             }
             __builtin_amdgcn_s_sleep(1);  // slot still held by its consumer
-            if (++spins > kSpinLimit) break;
+            if (++spins > c.spin_limit) {
+                wait_gave_up(kWaitSlot);
+                break;
+            }
         }
     } else {
         uint4 cb_hi[LT], cb_lo[LT];
@@ -1674,7 +1705,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 int spins = 0;
                 while (ready[slot] != j) {
                     __builtin_amdgcn_s_sleep(1);
-                    if (++spins > kSpinLimit) break;
+                    if (++spins > c.spin_limit) {
+                        wait_gave_up(kWaitTile);
+                        break;
+                    }
                 }
             }
             asm volatile("" ::: "memory");
@@ -2392,6 +2426,32 @@ static int check_common(const void *q, int q_dtype, int64_t batch, int hq, int h
     return SS_OK;
 }
 
+// Sticky wait-failure word of this code object, one per device (kWait* bits).
+__device__ unsigned int g_wait_fail_word;
+
+// Spin limit of the bounded waits for later launches (ss_debug_set_spin_limit).
+static std::atomic<int> g_spin_limit{kSpinLimit};
+
+// Device address of g_wait_fail_word on the current device, looked up once
+// per device.
+static int wait_word(unsigned int **out) {
+    static std::mutex mu;
+    static unsigned int *addr[64] = {nullptr};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    SS_UNSUPPORTED(dev >= 0 && dev < 64, "device ordinal %d beyond 63", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_wait_fail_word));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(wait word)");
+        addr[dev] = static_cast<unsigned int *>(p);
+    }
+    *out = addr[dev];
+    return SS_OK;
+}
+
 static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int q_dtype,
                        int hq, int hkv, int64_t t_q, float scale, const int32_t *perm,
                        const float *centroids, int n_centroids, const uint8_t *idx, int64_t cap,
@@ -2418,6 +2478,11 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.q_offset = q_offset;
     c.n_splits = s.S;
     c.tiles_per_split = s.tiles_per_split;
+    c.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
+    {
+        const int rc = wait_word(&c.wait_fail);
+        if (rc != SS_OK) return rc;
+    }
     c.part_ml = nullptr;
     c.part_acc = nullptr;
     c.part_cnt = nullptr;
@@ -2447,6 +2512,36 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
 }  // namespace ss
 
 using namespace ss;
+
+extern "C" int ss_decode_wait_failures(void *stream, int clear, unsigned int *flags) {
+    unsigned int *w = nullptr;
+    int rc = wait_word(&w);
+    if (rc != SS_OK) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    unsigned int v = 0;
+    e = hipMemcpy(&v, w, sizeof(v), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy(wait word)");
+    if (flags) *flags = v;
+    if (v && clear) {
+        const unsigned int zero = 0;
+        e = hipMemcpy(w, &zero, sizeof(zero), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy(clear wait word)");
+    }
+    if (v) {
+        set_error("a bounded wait of a fused decode gave up (flags 0x%x: %s%s%s); the output of "
+                  "that launch is invalid", v, (v & kWaitBarrier) ? "compute barrier " : "",
+                  (v & kWaitSlot) ? "ring slot " : "", (v & kWaitTile) ? "ring tile" : "");
+        return SS_ERR_WAIT;
+    }
+    return SS_OK;
+}
+
+extern "C" int ss_debug_set_spin_limit(int limit) {
+    g_spin_limit.store(limit < 0 ? kSpinLimit : limit, std::memory_order_relaxed);
+    return SS_OK;
+}
 
 extern "C" size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                             int64_t t_q, int head_dim, int64_t t_kv,

@@ -11,17 +11,15 @@ against the reference runs unchanged.
 
 from __future__ import annotations
 
-from collections import defaultdict
-
 import torch
 
 from . import _hip
 
-_KERNEL_STATS: dict[str, int] = defaultdict(int)
-
-
-def _record_kernel_dispatch(name: str) -> None:
-    _KERNEL_STATS[name] += 1
+# The dispatch counters live in the C-ABI binding layer, where every kernel
+# launch of every route (launchers below, caches, SDPA, codecs) is counted
+# (reference kernels.py:33-37).
+_KERNEL_STATS: dict[str, int] = _hip._KERNEL_STATS
+_record_kernel_dispatch = _hip.record_dispatch
 
 
 def reset_kernel_stats() -> None:
@@ -54,7 +52,6 @@ def block_vq_score_hip(qdots: torch.Tensor, indices: torch.Tensor, n_qh: int, T_
         return None
     q = qdots.reshape(n_qh, n_blocks, n_centroids).float()
     out = _hip.score_gather(q, _as_u8_indices(indices.reshape(T_kv, n_blocks)))
-    _record_kernel_dispatch("sunshape_block_vq_score_hip")
     return out
 
 
@@ -77,7 +74,7 @@ def fused_attention_hip(queries, centroids, indices, values, n_qh: int, T_kv: in
     already-transformed (and scaled) queries -> (n_qh, head_dim) float32.
     Reference: fused_attention_metal (kernels.py:233-291)."""
     return _fused_dense(queries, centroids, indices, values, n_qh, T_kv, n_blocks, n_centroids,
-                        head_dim, False, 0, "sunshape_fused_attention_hip")
+                        head_dim, False, 0)
 
 
 def fused_attention_causal_hip(queries, centroids, indices, values, n_qh: int, T_kv: int,
@@ -86,11 +83,11 @@ def fused_attention_causal_hip(queries, centroids, indices, values, n_qh: int, T
     """As ``fused_attention_hip`` with row r attending to keys t <= q_offset + r.
     Reference: fused_attention_causal_metal (kernels.py:388-446)."""
     return _fused_dense(queries, centroids, indices, values, n_qh, T_kv, n_blocks, n_centroids,
-                        head_dim, True, q_offset, "sunshape_fused_attention_causal_hip")
+                        head_dim, True, q_offset)
 
 
 def _fused_dense(queries, centroids, indices, values, n_qh, T_kv, n_blocks, n_centroids,
-                 head_dim, causal, q_offset, stat):
+                 head_dim, causal, q_offset):
     _hip.require_gpu(queries, centroids, indices, values)
     if T_kv == 0:
         return torch.zeros((n_qh, head_dim), dtype=torch.float32, device=queries.device)
@@ -101,7 +98,6 @@ def _fused_dense(queries, centroids, indices, values, n_qh, T_kv, n_blocks, n_ce
     v = values.reshape(1, 1, T_kv, head_dim).contiguous()
     out = _hip.decode_attn_dense(q, 1.0, None, centroids.float().contiguous(), idx, v, T_kv,
                                  causal=causal, q_offset=q_offset, out_dtype=torch.float32)
-    _record_kernel_dispatch(stat)
     return out.reshape(n_qh, head_dim)
 
 
@@ -111,8 +107,7 @@ def fused_attention_dequant_hip(queries, centroids, indices, packed_values, scal
     """Fused attention with grouped values dequantised in registers.
     Reference: fused_attention_dequant_metal (kernels.py:697-765)."""
     return _fused_grouped(queries, centroids, indices, packed_values, scales, zeros, n_qh, T_kv,
-                          n_blocks, n_centroids, head_dim, bits, group_size, False, 0,
-                          "sunshape_fused_attention_dequant_hip")
+                          n_blocks, n_centroids, head_dim, bits, group_size, False, 0)
 
 
 def fused_attention_dequant_causal_hip(queries, centroids, indices, packed_values, scales, zeros,
@@ -122,12 +117,11 @@ def fused_attention_dequant_causal_hip(queries, centroids, indices, packed_value
     """Causal variant.  Reference: fused_attention_dequant_causal_metal
     (kernels.py:870-928)."""
     return _fused_grouped(queries, centroids, indices, packed_values, scales, zeros, n_qh, T_kv,
-                          n_blocks, n_centroids, head_dim, bits, group_size, True, q_offset,
-                          "sunshape_fused_attention_dequant_causal_hip")
+                          n_blocks, n_centroids, head_dim, bits, group_size, True, q_offset)
 
 
 def _fused_grouped(queries, centroids, indices, packed, scales, zeros, n_qh, T_kv, n_blocks,
-                   n_centroids, head_dim, bits, group_size, causal, q_offset, stat):
+                   n_centroids, head_dim, bits, group_size, causal, q_offset):
     _hip.require_gpu(queries, centroids, indices, packed, scales, zeros)
     if T_kv == 0:
         return torch.zeros((n_qh, head_dim), dtype=torch.float32, device=queries.device)
@@ -150,7 +144,6 @@ def _fused_grouped(queries, centroids, indices, packed, scales, zeros, n_qh, T_k
     out = _hip.decode_attn_grouped(q, 1.0, None, centroids.float().contiguous(), idx, p, sc, zr,
                                    bits, group_size, T_kv, causal=causal, q_offset=q_offset,
                                    out_dtype=torch.float32)
-    _record_kernel_dispatch(stat)
     return out.reshape(n_qh, head_dim)
 
 
@@ -165,7 +158,6 @@ def quantize_scalar_to_indices(values: torch.Tensor, boundaries: torch.Tensor, *
     Reference: kernels.py:473-507.  ``prefer_metal`` is accepted for
     signature compatibility; the HIP kernel always runs."""
     out = _hip.scalar_quantize(values, boundaries.to(values.device))
-    _record_kernel_dispatch("sunshape_scalar_quantize_hip")
     return out, "hip"
 
 
@@ -208,7 +200,6 @@ def block_vq_quantize_hip(keys_transformed: torch.Tensor, centroids: torch.Tenso
         k = k.contiguous()
     out = torch.empty((k.shape[0], n_blocks), dtype=torch.uint8, device=k.device)
     _hip.encode_blockvq(k, None, centroids.float().contiguous(), out, block_dim)
-    _record_kernel_dispatch("sunshape_block_vq_quantize_hip")
     return out
 
 
@@ -255,7 +246,6 @@ def quantize_values(values: torch.Tensor, bits: int = 4, group_size: int = 64):
     zeros = torch.empty((T, ng), dtype=torch.float32, device=values.device)
     v = values if values.stride(-1) == 1 else values.contiguous()
     _hip.quantize_values_grouped(v, bits, group_size, packed, scales, zeros)
-    _record_kernel_dispatch("sunshape_quantize_values_hip")
     return packed.view(torch.uint32), scales, zeros, ng
 
 

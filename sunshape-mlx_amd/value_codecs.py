@@ -27,34 +27,33 @@ from .kernels import (
 from .rotation import generate_rotation_matrix
 
 
+# Positive levels of the Lloyd-Max quantiser of N(0, 1) (Max, 1960) at 1-4
+# bits, the values the reference ships as literal tables
+# (value_codecs.py:20-87).  Its tables are exactly symmetric and each
+# boundary is exactly the midpoint of its two levels, so the full tables are
+# rebuilt below bit for bit.  The 4-bit levels sit up to 3.5e-4 away from
+# the exact fixed point of the Lloyd-Max conditions; they are kept as data
+# (not recomputed) so that TurboQuant codes equal the reference's.
+_LLOYD_MAX_POSITIVE: dict[int, tuple[float, ...]] = {
+    1: (0.7978845608028654,),
+    2: (0.4527800346911237, 1.510417608611893),
+    3: (0.2450941791152904, 0.7560052816730181, 1.3439092791423422, 2.151945705166112),
+    4: (0.12844300124876415, 0.38818871416000605, 0.6569817464411519, 0.9426291036999694,
+        1.2565648452462146, 1.618400443227723, 2.069364258154187, 2.732896755154294),
+}
+
+
 @lru_cache(maxsize=None)
 def lloyd_max_gaussian(bits: int) -> tuple[tuple[float, ...], tuple[float, ...]]:
-    """Lloyd-Max quantiser of N(0, 1): ``(levels, boundaries)``.
-
-    Fixed point of the two optimality conditions (Max, 1960): boundaries are
-    midpoints of neighbouring levels and each level is its cell's conditional
-    mean ``(phi(a) - phi(b)) / (Phi(b) - Phi(a))``.  The reference ships the
-    same quantiser as literal tables (value_codecs.py:20-87)."""
-    from scipy.special import ndtr
-
-    def pdf(x):
-        return np.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
-
-    n = 1 << bits
-    levels = np.linspace(-2.0, 2.0, n)
-    for _ in range(5000):
-        b = 0.5 * (levels[1:] + levels[:-1])
-        lo = np.concatenate([[-np.inf], b])
-        hi = np.concatenate([b, [np.inf]])
-        pl = np.where(np.isinf(lo), 0.0, pdf(np.where(np.isinf(lo), 0.0, lo)))
-        ph = np.where(np.isinf(hi), 0.0, pdf(np.where(np.isinf(hi), 0.0, hi)))
-        new = (pl - ph) / (ndtr(hi) - ndtr(lo))
-        done = np.max(np.abs(new - levels)) < 1e-15
-        levels = new
-        if done:
-            break
-    levels = 0.5 * (levels - levels[::-1])  # exact symmetry
-    return tuple(levels.tolist()), tuple((0.5 * (levels[1:] + levels[:-1])).tolist())
+    """Lloyd-Max quantiser of N(0, 1) at ``bits`` bits: ``(levels,
+    boundaries)`` in ascending order, equal to the reference's
+    ``_TURBOQUANT_CODEBOOKS[bits]`` (value_codecs.py:20-87)."""
+    if bits not in _LLOYD_MAX_POSITIVE:
+        raise ValueError(f"Lloyd-Max tables exist for 1-4 bits, got {bits}")
+    pos = _LLOYD_MAX_POSITIVE[bits]
+    levels = tuple(-x for x in reversed(pos)) + pos
+    bounds = tuple(0.5 * (a + b) for a, b in zip(levels[:-1], levels[1:]))
+    return levels, bounds
 
 
 def _packed_dim(head_dim: int, bits: int) -> int:
@@ -115,6 +114,7 @@ class TurboQuantValueCodec:
         if self.bits not in (2, 3, 4):
             raise ValueError(f"TurboQuant values support 2, 3, or 4 bits, got {self.bits}")
         levels, bounds = lloyd_max_gaussian(self.bits)
+        # python-float products rounded once to float32 (value_codecs.py:148-151)
         s = 1.0 / math.sqrt(self.head_dim)
         dev = self.device or ("cuda" if torch.cuda.is_available() else "cpu")
         self.centroids = torch.tensor([c * s for c in levels], dtype=torch.float32, device=dev)

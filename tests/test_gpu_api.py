@@ -298,27 +298,39 @@ def test_rotated_codec_fused_decode():
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
 
 
-def test_turboquant_value_codec_matches_oracle():
-    d, bits = 128, 3
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_turboquant_value_codec_matches_oracle(bits):
+    """TurboQuantValueCodec.quantize (value_codecs.py:159-171) against the
+    oracle with the oracle's own copy of the reference's Lloyd-Max tables:
+    codes bit-exact except coordinates within 1e-5 of a boundary (the
+    rotation runs in float32 on the GPU), zero rows included (zero norm,
+    every coordinate at the lower-middle code)."""
+    d = 128
     tq = S.TurboQuantValueCodec(head_dim=d, bits=bits, seed=43, device=DEV)
-    g = torch.Generator(device=DEV).manual_seed(15)
+    cents, bounds = O.turboquant_tables(bits, d)
+    # R is data (the reference draws it from MLX's generator, which is
+    # unavailable): the codec's own, checked orthogonal
+    rot = tq.rotation.cpu().numpy()
+    assert np.abs(rot.astype(np.float64) @ rot.T - np.eye(d)).max() < 1e-5
+    g = torch.Generator(device=DEV).manual_seed(15 + bits)
     vals = torch.randn((64, d), generator=g, device=DEV)
+    vals[[0, 17, 63]] = 0.0
     packed, norms = tq.quantize(vals)
     v64 = vals.cpu().numpy().astype(np.float64)
-    rot = tq.rotation.cpu().numpy()
-    bounds = tq.boundaries.cpu().numpy()
     ref_packed, ref_norms, _ = O.turboquant_encode(v64, rot, bounds, bits)
-    # codes equal except coordinates within 1e-5 of a boundary (fp32 rotate)
     u = v64 / np.maximum(np.linalg.norm(v64, axis=-1, keepdims=True), 1e-8)
     r = u @ rot.astype(np.float64).T
     near = (np.abs(r[..., None] - bounds.astype(np.float64)) < 1e-5).any(-1)
+    near[[0, 17, 63]] = False  # zero rows: exact zeros on both sides
     got_idx = O.unpack_indices(packed.cpu().numpy(), d, bits)
     ref_idx = O.unpack_indices(ref_packed, d, bits)
     assert np.array_equal(got_idx[~near], ref_idx[~near])
+    assert near.mean() < 0.01
+    assert (got_idx[[0, 17, 63]] == (1 << (bits - 1)) - 1).all()
     assert np.allclose(norms.cpu().numpy(), ref_norms, rtol=1e-6)
+    assert (norms.cpu().numpy()[[0, 17, 63]] == 0).all()
     rec = tq.dequantize(packed, norms).cpu().numpy()
-    ref_rec = O.turboquant_decode(packed.cpu().numpy(), norms.cpu().numpy(), rot,
-                                  tq.centroids.cpu().numpy(), d, bits)
+    ref_rec = O.turboquant_decode(packed.cpu().numpy(), norms.cpu().numpy(), rot, cents, d, bits)
     assert rel_err(rec, ref_rec) <= 1e-5
 
 
@@ -407,25 +419,35 @@ def test_hybrid_sunshape_values_fused_decode(vbd, buffer_size):
 @pytest.mark.parametrize("mode", ["profileperm_baseline", "profileperm_mixed_precision"])
 def test_codec_fit_on_gpu_matches_cpu_fit(mode):
     """SunShapeBlockCodec.fit with the k-means on the GPU (every block in one
-    launch) gives the NumPy fit's permutation and heavy blocks and a codebook
-    of the same quality (reconstruction error within 1 %)."""
+    launch).  Baseline mode against the oracle's fit (codec.py:299-418):
+    the same permutation and a codebook of the same quality (reconstruction
+    error within 1 %).  Mixed-precision mode (whose heavy-block selection
+    the oracle does not restate) against the package's own NumPy k-means
+    from the same initial rows: same permutation and heavy blocks, same
+    quality."""
     rng = np.random.default_rng(42)
     s = rng.uniform(0.5, 4.0, 128).astype(np.float32)
     q_cal = (rng.standard_normal((1024, 128)) * s).astype(np.float32)
     k_cal = (rng.standard_normal((2048, 128)) * s).astype(np.float32)
     gpu = S.SunShapeBlockCodec(128, device=DEV, mode=mode, n_refine_dsq=0).fit(
         q_cal, k_cal, kmeans_iters=15, seed=42)
-    cpu = S.SunShapeBlockCodec(128, device=DEV, mode=mode, n_refine_dsq=0).fit(
-        q_cal, k_cal, kmeans_iters=15, seed=42, kmeans_device="cpu")
-    assert torch.equal(gpu.permutation.cpu(), cpu.permutation.cpu())
-    assert torch.equal(gpu.mixed_high_precision_blocks.cpu(), cpu.mixed_high_precision_blocks.cpu())
     kt = torch.from_numpy(k_cal).to(DEV)
-
-    def err(codec):
-        rec = codec.dequantize(codec.quantize(kt)).float()
-        return float(((rec - kt) ** 2).mean())
-
-    assert abs(err(gpu) / err(cpu) - 1.0) <= 0.01
+    err_gpu = float(((gpu.dequantize(gpu.quantize(kt)).float() - kt) ** 2).mean())
+    if mode == "profileperm_baseline":
+        perm, cents = O.fit_profileperm_baseline(q_cal, k_cal, block_dim=8, n_centroids=256,
+                                                 kmeans_iters=15, seed=42)
+        assert np.array_equal(gpu.permutation.cpu().numpy(), perm)
+        idx, _ = O.encode_blockvq(k_cal, cents, perm)
+        rec = O.dequantize_blockvq(idx, cents, O.invert_permutation(perm)).astype(np.float64)
+        err_ref = float(((rec - k_cal.astype(np.float64)) ** 2).mean())
+    else:
+        cpu = S.SunShapeBlockCodec(128, device=DEV, mode=mode, n_refine_dsq=0).fit(
+            q_cal, k_cal, kmeans_iters=15, seed=42, kmeans_device="cpu")
+        assert torch.equal(gpu.permutation.cpu(), cpu.permutation.cpu())
+        assert torch.equal(gpu.mixed_high_precision_blocks.cpu(),
+                           cpu.mixed_high_precision_blocks.cpu())
+        err_ref = float(((cpu.dequantize(cpu.quantize(kt)).float() - kt) ** 2).mean())
+    assert abs(err_gpu / err_ref - 1.0) <= 0.01
 
 
 @pytest.mark.parametrize("value_backend,buffer_size", [("sunshape", 0), ("sunshape", 64),
@@ -439,8 +461,9 @@ def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
     d, nb = 128, 16
     heavy = np.zeros(nb, bool)
     heavy[[3, 7, 8, 12]] = True
+    # nonzero heavy-block centroids (as after a fit with DSQ refinement): the
+    # exact heavy dot products replace them
     cents = rng.standard_normal((nb, 256, 8)).astype(np.float32)
-    cents[heavy] = 0.0
     perm = rng.permutation(d).astype(np.int32)
     codec = S.SunShapeBlockCodec(d, device=DEV, mode="profileperm_mixed_precision",
                                  heavy_fp16=True)
@@ -480,6 +503,68 @@ def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
                            cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset else None,
                            vals)
     assert rel_err(ref0, ref) > 1e-2
+
+
+@pytest.mark.parametrize("value_backend", ["sunshape", "fp16"])
+def test_fitted_mixed_codec_heavy_fp16_with_buffer(value_backend):
+    """A profileperm_mixed_precision codec fitted with DSQ refinement (which
+    moves the heavy blocks' centroid 0 away from zero, reference
+    codec.py:400-410) and heavy_fp16: a hybrid cache with buffered tokens
+    scores the heavy blocks from their fp16 keys only, matching the oracle's
+    attention over keys rebuilt from the light-block centroids and the fp16
+    heavy dims."""
+    rng = np.random.default_rng(60)
+    d = 128
+    s = rng.uniform(0.5, 4.0, d).astype(np.float32)
+    q_cal = (rng.standard_normal((1024, d)) * s).astype(np.float32)
+    k_cal = (rng.standard_normal((2048, d)) * s).astype(np.float32)
+    codec = S.SunShapeBlockCodec(d, device=DEV, mode="profileperm_mixed_precision",
+                                 n_refine_dsq=3, heavy_fp16=True).fit(
+        q_cal, k_cal, kmeans_iters=5, seed=42)
+    heavy = codec.mixed_high_precision_blocks.cpu().numpy().astype(bool)
+    cents = codec.centroids.cpu().numpy()
+    assert heavy.any() and np.abs(cents[heavy]).max() > 0.0  # the case the fix is for
+    hd = codec.heavy_dims().cpu().numpy()
+    perm = codec.permutation.cpu().numpy()
+    b, hq, hkv, n = 2, 8, 2, 300
+    k = torch.from_numpy((rng.standard_normal((b, hkv, n, d)) * s).astype(np.float16)).to(DEV)
+    v = torch.from_numpy(rng.standard_normal((b, hkv, n, d)).astype(np.float16)).to(DEV)
+    kw = dict(n_kv_heads=hkv, buffer_size=64)
+    if value_backend == "sunshape":
+        vcodec = S.SunShapeBlockCodec(d, block_dim=4, n_centroids=256, device=DEV)
+        vcodec.load_state_dict({"centroids": rng.standard_normal((32, 256, 4)).astype(np.float32),
+                                "permutation": rng.permutation(d).astype(np.int32)})
+        cache = S.create_kv_cache(codec, value_backend="sunshape", value_bits=8,
+                                  value_codec=vcodec, **kw)
+    else:
+        cache = S.create_kv_cache(codec, value_backend="fp16", **kw)
+    cache.update_and_fetch(k, v)
+    assert cache.buffer_offset > 0 and cache.compressed_offset > 0
+    nc = cache.compressed_offset
+    q = torch.from_numpy((rng.standard_normal((b, hq, 1, d)) * s).astype(np.float16)).to(DEV)
+    out = S.sunshape_sdpa(q, cache, 0.088)
+    kh = k[:, :, :nc].cpu().numpy()[..., perm][..., hd]
+    vals = cache.values.float().cpu().numpy()
+    idx = cache.key_indices.cpu().numpy()
+    kb = cache.buffer_keys.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, idx, kb, vals,
+                          heavy_keys=kh, heavy_dims=hd)
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    # the same attention written out over rebuilt keys (codec basis: light
+    # blocks from their centroids, heavy dims from the fp16 keys)
+    qs = O.scale_query(q.cpu().numpy(), 0.088).astype(np.float64)
+    inv = O.invert_permutation(perm)
+    for bi in range(b):
+        for h in range(hkv):
+            kc = O.dequantize_blockvq(idx[bi, h], cents).astype(np.float64)
+            kc[:, hd] = kh[bi, h].astype(np.float64)
+            keys = np.concatenate([kc[:, inv], kb[bi, h].astype(np.float64)], axis=0)
+            for r in range(hq // hkv):
+                sc = qs[bi, h * (hq // hkv) + r, 0] @ keys.T
+                w = np.exp(sc - sc.max())
+                o = (w / w.sum()) @ vals[bi, h].astype(np.float64)
+                got = out[bi, h * (hq // hkv) + r, 0].float().cpu().numpy()
+                assert np.abs(got - o).max() <= 2e-3 * np.abs(o).max()
 
 
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():

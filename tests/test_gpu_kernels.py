@@ -666,14 +666,14 @@ def test_kmeans_blocks_matches_oracle(bd, n, k):
 ])
 def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, splits):
     """Mixed-precision keys with their heavy blocks in fp16: the fused decode
-    adds the exact heavy-dim dot products to the LUT scores, as the oracle's
-    two-pass SDPA with heavy keys does."""
+    scores the heavy blocks from their fp16 dims in place of the LUT (their
+    centroids are nonzero, as after a fit with DSQ refinement, and must add
+    nothing), as the oracle's two-pass SDPA with heavy keys does."""
     d, bd = 128, 4
     cap = ((t_kv + 15) // 16) * 16
     cents, perm, idx, _, q = decode_case(90 + n_heavy, b, hq, hkv, d, t_kv, t_q, cap)
     rng = np.random.default_rng(91 + n_heavy)
     heavy = np.sort(rng.permutation(16)[:n_heavy])
-    cents[heavy] = 0.0
     hd = np.concatenate([np.arange(x * 8, x * 8 + 8) for x in heavy]).astype(np.int32)
     kh = np.zeros((b, hkv, cap, hd.size), np.float16)
     kh[:, :, :t_kv] = rng.standard_normal((b, hkv, t_kv, hd.size)).astype(np.float16)
@@ -705,7 +705,8 @@ def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, s
                           mask="causal" if causal else None, heavy_keys=kh[:, :, :t_kv],
                           heavy_dims=hd)
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
-    # without k_heavy the kernel keeps the reference's scores (heavy blocks contribute 0)
+    # without k_heavy the kernel keeps the reference's scores (a heavy block's
+    # index adds its centroid's dot product like any other block)
     out0 = _hip.decode_attn_sunshape_v(t(q), scale, t(perm), t(cents), t(idx), t(v_idx),
                                        t(v_cents), t(m), t_kv, causal=causal,
                                        q_offset=total - t_q if causal else 0,
@@ -741,3 +742,38 @@ def test_transformed_decode_leaves_split_counters_zero():
         assert not ws[:64 * 1024].any()
         ref = O.sdpa(q, idx, vals, cents, perm, scale)
         assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+def test_bounded_wait_failure_reaches_python():
+    """A bounded in-kernel wait that gives up is reported, not hidden: with
+    the spin limit forced to 0 from the host (every wait gives up after one
+    sleep while every wave still ends normally) the matrix-core decode sets
+    the sticky wait-failure word, ss_decode_wait_failures returns SS_ERR_WAIT
+    and the Python layer raises SunShapeWaitError (per call when wait checks
+    are on).  With the default limit restored the same decode is correct and
+    reports nothing."""
+    b, hq, hkv, d, t_kv = 1, 32, 8, 128, 32768
+    cents, perm, idx, vals, q = decode_case(71, b, hq, hkv, d, t_kv)
+    args = (t(q), 1.0 / np.sqrt(d), t(perm), t(cents), t(idx), to_il8(vals, t_kv), t_kv)
+    assert _hip.decode_wait_failures() == 0
+    prev = _hip.set_wait_checks(False)
+    try:
+        _hip.set_spin_limit(0)
+        _hip.decode_attn_il8(*args, out_dtype=torch.float32)
+        flags = _hip.decode_wait_failures(clear=False)
+        assert flags != 0 and flags & ~7 == 0
+        with pytest.raises(_hip.SunShapeWaitError):
+            _hip.check_decode_waits()
+        assert _hip.decode_wait_failures() == 0  # cleared by the check
+        _hip.set_wait_checks(True)
+        with pytest.raises(_hip.SunShapeWaitError):
+            _hip.decode_attn_il8(*args, out_dtype=torch.float32)
+    finally:
+        _hip.set_spin_limit(None)
+        _hip.set_wait_checks(prev)
+        _hip.decode_wait_failures()
+    out = _hip.decode_attn_il8(*args, out_dtype=torch.float32)
+    assert _hip.decode_wait_failures() == 0
+    _hip.check_decode_waits()
+    ref = O.sdpa(q, idx, vals, cents, perm, 1.0 / np.sqrt(d))
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL

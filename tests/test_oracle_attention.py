@@ -188,18 +188,18 @@ def test_sdpa_two_pass_buffer_scores_use_original_basis():
 
 
 def test_sdpa_heavy_blocks_score_as_exact_key_dots():
-    """Mixed-precision extension: with the heavy blocks' centroids zero and
-    their key dims kept in fp16, each compressed score is q . k_hat where
-    k_hat takes the centroids on light blocks and the fp16 dims on heavy
-    ones, all in the original basis (pinned against attention written out
-    over the reconstructed keys, not the LUT)."""
+    """Mixed-precision extension: with the heavy blocks' key dims kept in
+    fp16, each compressed score is q . k_hat where k_hat takes the centroids
+    on light blocks and the fp16 dims on heavy ones, all in the original
+    basis (pinned against attention written out over the reconstructed keys,
+    not the LUT).  The heavy blocks' centroids are nonzero (as after a fit
+    with DSQ refinement) and must not add to the scores."""
     rng = np.random.default_rng(32)
     b_, hq, hkv, d, t, bd = 1, 2, 1, 64, 40, 8
     nb = d // bd
     perm = rng.permutation(d).astype(np.int32)
     cents = rng.standard_normal((nb, 32, bd)).astype(np.float32)
     heavy = np.array([1, 6])
-    cents[heavy] = 0.0
     hd = np.concatenate([np.arange(b * bd, (b + 1) * bd) for b in heavy]).astype(np.int32)
     keys = rng.standard_normal((b_, hkv, t, d)).astype(np.float32)
     idx = np.stack([O.encode_blockvq(keys[0, 0], cents, perm)[0]])[None]

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import sunshape_oracle as O
+import sunshape_mlx_amd as S
 
 
 @pytest.mark.parametrize("bits,d", [(2, 128), (3, 100), (4, 128)])
@@ -109,21 +110,59 @@ def test_known_answers_fused_dequant(seed, bits, t_q, t_kv, causal):
 
 
 def test_lloyd_max_tables():
-    """1 bit: +-sqrt(2/pi) (closed form); 2 bits: Max (1960) levels +-0.4528,
-    +-1.510 and threshold 0.9816; every table symmetric with midpoint
-    boundaries."""
+    """The reference's literal tables (value_codecs.py:20-87), pinned by what
+    the Lloyd-Max conditions fix: 1 bit is +-sqrt(2/pi) (closed form); every
+    table is symmetric with boundaries at the midpoints of adjacent levels
+    (middle boundary exactly 0, so a zero coordinate gets the upper-middle
+    code); the levels are the fixed point of the conditions computed here
+    independently, to 1e-9 at 2 and 3 bits and 4e-4 at 4 bits, where the
+    literals are measurably off it (so they must be kept as data)."""
     l1, b1 = O.lloyd_max_gaussian(1)
-    assert np.allclose(l1, [-math.sqrt(2 / math.pi), math.sqrt(2 / math.pi)], atol=1e-12)
-    assert np.allclose(b1, [0.0])
+    assert np.allclose(l1, [-math.sqrt(2 / math.pi), math.sqrt(2 / math.pi)], atol=1e-15)
+    assert b1.tolist() == [0.0]
+    for bits, tol in ((2, 1e-9), (3, 1e-9), (4, 4e-4)):
+        lv, bd = O.lloyd_max_gaussian(bits)
+        assert lv.size == 1 << bits and bd.size == lv.size - 1
+        assert np.array_equal(lv, -lv[::-1])
+        assert np.array_equal(bd, 0.5 * (lv[1:] + lv[:-1]))
+        assert bd[bd.size // 2] == 0.0
+        fl, fb = O.lloyd_max_fixed_point(bits)
+        assert np.abs(lv - fl).max() < tol and np.abs(bd - fb).max() < tol
+    l4, _ = O.lloyd_max_gaussian(4)
+    assert np.abs(l4 - O.lloyd_max_fixed_point(4)[0]).max() > 1e-4
+    # Max (1960), table I, to its printed precision
     l2, b2 = O.lloyd_max_gaussian(2)
     assert np.allclose(l2, [-1.510, -0.4528, 0.4528, 1.510], atol=5e-4)
     assert np.allclose(b2, [-0.9816, 0.0, 0.9816], atol=5e-4)
-    for bits in (3, 4):
-        lv, bd = O.lloyd_max_gaussian(bits)
-        assert np.allclose(lv, -lv[::-1], atol=1e-12)
-        assert np.allclose(bd, 0.5 * (lv[1:] + lv[:-1]))
     l3, _ = O.lloyd_max_gaussian(3)
     assert np.allclose(l3[4:], [0.2451, 0.7560, 1.344, 2.152], atol=5e-4)
+
+
+def test_scalar_quantize_zero_coordinate_takes_lower_middle_code():
+    """With the exact-zero middle boundary, ``#(0 > boundaries)`` counts only
+    the negative boundaries: a zero value row (zero norm, zero rotated
+    coordinates) gets code 2^(bits-1) - 1 at every bit width (code 1 at 2
+    bits, as in the reference)."""
+    for bits in (2, 3, 4):
+        _, b = O.turboquant_tables(bits, 128)
+        assert O.scalar_quantize(np.zeros(5, np.float32), b).tolist() == [(1 << (bits - 1)) - 1] * 5
+
+
+def test_turboquant_codec_tables_equal_reference_literals():
+    """The product's TurboQuant tables (built from its own copy of the
+    positive levels) equal the reference's literal tables scaled by
+    1/sqrt(D) and rounded to float32 (value_codecs.py:148-151), bit for bit,
+    at every bit width and D = 64, 128."""
+    for bits in (2, 3, 4):
+        for d in (64, 128):
+            tq = S.TurboQuantValueCodec(head_dim=d, bits=bits, device="cpu")
+            c, b = O.turboquant_tables(bits, d)
+            assert np.array_equal(tq.centroids.numpy(), c)
+            assert np.array_equal(tq.boundaries.numpy(), b)
+    for bits in (1, 2, 3, 4):
+        lv, bd = S.value_codecs.lloyd_max_gaussian(bits)
+        rl, rb = O.lloyd_max_gaussian(bits)
+        assert list(lv) == rl.tolist() and list(bd) == rb.tolist()
 
 
 def test_rotation_orthogonal_and_turboquant_roundtrip():
