@@ -17,7 +17,9 @@
  *    last error of the calling thread is returned by ss_last_error().
  *    Argument and shape checks happen on the host before any launch.
  *  - Stateless and reentrant, except that calls sharing one decode workspace
- *    must not overlap (the workspace holds the call's split partials).
+ *    must not overlap (the workspace holds the call's split partials), and
+ *    calls of ss_decode_attn_il8_noalloc on one GPU share its static scratch
+ *    and must not overlap either.
  *  - dtype codes: SS_F32, SS_F16, SS_BF16.
  */
 #ifndef SUNSHAPE_HIP_H
@@ -202,6 +204,34 @@ int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                        int v_dtype, int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
                        void *out, int out_dtype, void *workspace, size_t workspace_bytes,
                        int n_splits, void *stream);
+
+/*
+ * ss_decode_attn_il8 without a workspace: the same kernel, arguments and
+ * result, with its split partials and per-column split counters in a static
+ * device array of the library (ss_decode_static_scratch_bytes() = 4 MiB,
+ * one per GPU, held until the process ends).  The call allocates nothing
+ * (no hipMalloc, no allocating library routine), for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation.  No counterpart in the reference.
+ *  - A shape whose split scratch exceeds the static array returns
+ *    SS_ERR_WORKSPACE (pass fewer splits, or use ss_decode_attn_il8).
+ *  - The first call on a device looks the array up and clears its counter
+ *    area with a fill kernel on `stream`; every completed call leaves the
+ *    counters zero again.
+ *  - All calls on one GPU share the array: calls that overlap in time on
+ *    the same GPU (different streams or threads) race and give undefined
+ *    results.
+ */
+int ss_decode_attn_il8_noalloc(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                               int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                               const int32_t *perm, const void *codebook, int n_blocks,
+                               int n_centroids, const uint8_t *idx, const void *values_il8,
+                               int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                               int64_t q_offset, void *out, int out_dtype, int n_splits,
+                               void *stream);
+
+/* Bytes of the static scratch array of ss_decode_attn_il8_noalloc (4 MiB). */
+size_t ss_decode_static_scratch_bytes(void);
 
 /*
  * KV append of values into the 8-token interleaved fp16 layout read by

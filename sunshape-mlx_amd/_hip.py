@@ -79,6 +79,11 @@ _SIGNATURES = {
                                   _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
                                   _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
                                   _int, _c_void_p]),
+    "ss_decode_attn_il8_noalloc": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
+                                          _int, _i64, _i64, _int, _i64, _c_void_p, _int, _int,
+                                          _c_void_p]),
+    "ss_decode_static_scratch_bytes": (_size, []),
     "ss_codebook_f16x2_bytes": (_size, [_int, _int]),
     "ss_codebook_f16x2": (_int, [_c_void_p, _int, _int, _c_void_p, _c_void_p]),
     "ss_append_values_il8": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
@@ -469,6 +474,37 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv), int(bool(causal)),
         int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
         int(n_splits), stream_handle(q.device)))
+    if _check_waits:
+        check_decode_waits(q.device)
+    return out
+
+
+def decode_attn_il8_noalloc(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                            centroids: torch.Tensor, idx: torch.Tensor, values_il8: torch.Tensor,
+                            t_kv: int, out: torch.Tensor, codebook: torch.Tensor,
+                            causal: bool = False, q_offset: int = 0,
+                            n_splits: int = 0) -> torch.Tensor:
+    """:func:`decode_attn_il8` through ``ss_decode_attn_il8_noalloc``: no
+    workspace (the library's static per-GPU scratch holds the split
+    partials), ``out`` and the prepared ``codebook`` supplied by the caller,
+    so the call allocates nothing.  Calls that overlap on one GPU race."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(values_il8, out, codebook)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    if tuple(out.shape) != (b_, hq, tq, d) or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous {(b_, hq, tq, d)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(*centroids.shape[:2]):
+        raise ValueError("codebook does not match the centroids' shape")
+    _launched(_attn_stat("sunshape_fused_attention_mfma", causal), lib.ss_decode_attn_il8_noalloc(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+        nb, centroids.shape[1], ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv),
+        int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), int(n_splits),
+        stream_handle(q.device)))
     if _check_waits:
         check_decode_waits(q.device)
     return out

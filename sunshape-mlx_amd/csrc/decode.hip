@@ -2951,6 +2951,83 @@ extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int
     return launch_mfma<64, VIl8<64>>(c, VIl8<64>::Args{v8}, s, st);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free variant of ss_decode_attn_il8.  Its split partials and
+// per-column counters live in a file-scope device array (one per GPU, held
+// until the process ends) instead of a caller workspace.  Host code never
+// uses the array's name as an address: the per-device address comes from
+// hipGetSymbolAddress at the first call on each device, which also clears
+// the counter area with a fill kernel; every completed call leaves it zero.
+// ---------------------------------------------------------------------------
+constexpr size_t kStaticScratchBytes = 4u << 20;  // 4 MiB per device
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t *p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device, looked up (and its
+// counter area cleared on `st`) at the first call on that device.
+static int static_scratch(void **out, hipStream_t st) {
+    static std::mutex mu;
+    static void *addr[64] = {nullptr};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    SS_UNSUPPORTED(dev >= 0 && dev < 64, "device ordinal %d beyond 63", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st,
+                           static_cast<uint32_t *>(p), (int64_t)(kCntBytes / 4));
+        SS_LAUNCH_CHECK("zero_words_kernel launch");
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return SS_OK;
+}
+
+extern "C" size_t ss_decode_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+extern "C" int ss_decode_attn_il8_noalloc(const void *q, int q_dtype, int64_t batch,
+                                          int n_q_heads, int n_kv_heads, int64_t t_q,
+                                          int head_dim, float scale, const int32_t *perm,
+                                          const void *codebook, int n_blocks, int n_centroids,
+                                          const uint8_t *idx, const void *values_il8,
+                                          int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                          int64_t q_offset, void *out, int out_dtype,
+                                          int n_splits, void *stream) {
+    SS_REQUIRE(batch >= 1 && n_q_heads >= 1 && n_kv_heads >= 1 && t_q >= 1 &&
+                   n_q_heads % n_kv_heads == 0,
+               "bad head/batch counts");
+    SS_UNSUPPORTED(head_dim == 64 || head_dim == 128, "head_dim %d unsupported (64 or 128)",
+                   head_dim);
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
+                                       kKindMfma);
+    const size_t need = decode_ws_bytes(s, head_dim);
+    if (need > kStaticScratchBytes) {
+        set_error("ss_decode_attn_il8_noalloc: this shape needs %zu bytes of split scratch "
+                  "(%d splits), the static scratch holds %zu; pass fewer splits or use "
+                  "ss_decode_attn_il8 with a workspace",
+                  need, s.S, kStaticScratchBytes);
+        return SS_ERR_WORKSPACE;
+    }
+    void *ws = nullptr;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (need > 0) {
+        const int rc = static_scratch(&ws, st);
+        if (rc) return rc;
+    }
+    return ss_decode_attn_il8(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale,
+                              perm, codebook, n_blocks, n_centroids, idx, values_il8, v_dtype,
+                              cap, t_kv, causal, q_offset, out, out_dtype, ws,
+                              need > 0 ? kStaticScratchBytes : 0, n_splits, stream);
+}
+
 static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                            int n_kv_heads, int64_t t_q, int head_dim, float scale,
                            const int32_t *perm, const void *codebook, int n_blocks,
