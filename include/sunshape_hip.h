@@ -132,6 +132,16 @@ int ss_decode_wait_failures(void *stream, int clear, unsigned int *flags);
  */
 int ss_debug_set_spin_limit(int limit);
 
+/*
+ * Read-ceiling kernel (measurement, no reference counterpart): streams
+ * `bytes` (a multiple of 16) from `buf` with plain 16-byte non-temporal
+ * loads over n_workgroups x 256 threads; `sink` receives at most one word.
+ * bench.py times it over the bytes of a decode step to state the fastest a
+ * single launch can read them on this device.
+ */
+int ss_stream_read(const void *buf, int64_t bytes, int n_workgroups, uint32_t *sink,
+                   void *stream);
+
 /* Split count the library would choose (n_splits <= 0 in the calls below). */
 int ss_decode_default_splits(int64_t batch, int n_q_heads, int n_kv_heads,
                              int64_t t_q, int head_dim, int64_t t_kv);

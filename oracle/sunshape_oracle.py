@@ -710,6 +710,48 @@ def decode_cpu_vectorised(q_t, centroids, key_indices, values):
     return out.reshape(b_, hkv * rep, d)
 
 
+def decode_cpu_parallel(q_t, centroids, key_indices, values, n_threads: int,
+                        chunk: int = 4096):
+    """The vectorised CPU decode spread over ``n_threads`` host threads:
+    one LUT einsum for all heads, then every (b, KV head, token chunk) is an
+    independent unit -- gather, chunk-local softmax partial (m, l, acc) in
+    float32 -- and the chunks of a head are merged by log-sum-exp (the split
+    scheme of the GPU kernels, on the host).  NumPy releases the GIL in the
+    gather, exp and matmul, so the units run in parallel; run it with one
+    BLAS thread per worker."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    b_, hkv, rep, d = q_t.shape
+    nb = key_indices.shape[-1]
+    t_kv = key_indices.shape[2]
+    cents = np.asarray(centroids, np.float32)
+    qb = q_t.astype(np.float32).reshape(b_, hkv, rep, nb, -1)
+    lut = np.einsum("xhrbd,bcd->xhrbc", qb, cents)
+    ar = np.arange(nb)[None, :]
+    units = [(b, h, t0) for b in range(b_) for h in range(hkv) for t0 in range(0, t_kv, chunk)]
+
+    def part(u):
+        b, h, t0 = u
+        idx = key_indices[b, h, t0:t0 + chunk].astype(np.int64)
+        s = lut[b, h][:, ar, idx].sum(-1)  # (rep, chunk)
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        return m[:, 0], p.sum(1), p @ values[b, h, t0:t0 + chunk].astype(np.float32)
+
+    with ThreadPoolExecutor(max_workers=max(1, n_threads)) as ex:
+        parts = list(ex.map(part, units))
+    out = np.zeros((b_, hkv, rep, d), np.float32)
+    n_ch = (t_kv + chunk - 1) // chunk
+    for i in range(b_ * hkv):
+        ms = np.stack([parts[i * n_ch + c][0] for c in range(n_ch)])  # (n_ch, rep)
+        mx = ms.max(0)
+        w = np.exp(ms - mx)
+        l_ = sum(parts[i * n_ch + c][1] * w[c] for c in range(n_ch))
+        acc = sum(parts[i * n_ch + c][2] * w[c][:, None] for c in range(n_ch))
+        out[i // hkv, i % hkv] = acc / l_[:, None]
+    return out.reshape(b_, hkv * rep, d)
+
+
 # --------------------------------------------------------------------------- #
 #  C restatement of the encoder (oracle/encode_ref.c)                          #
 # --------------------------------------------------------------------------- #

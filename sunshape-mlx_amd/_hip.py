@@ -68,6 +68,7 @@ _SIGNATURES = {
     "ss_decode_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
     "ss_decode_wait_failures": (_int, [_c_void_p, _int, ctypes.POINTER(ctypes.c_uint)]),
     "ss_debug_set_spin_limit": (_int, [_int]),
+    "ss_stream_read": (_int, [_c_void_p, _i64, _int, _c_void_p, _c_void_p]),
     "ss_decode_default_splits": (_int, [_i64, _int, _int, _i64, _int, _i64]),
     "ss_decode_attn_dense": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                     _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,

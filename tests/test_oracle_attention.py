@@ -228,6 +228,7 @@ def test_cpu_baseline_forms_agree_with_oracle():
     ref = O.sdpa(q, idx, vals, cents, perm, 1 / math.sqrt(d))[:, :, 0]
     qt = O.apply_permutation(O.scale_query(q, 1 / math.sqrt(d)), perm).astype(np.float32)
     qt = qt.reshape(b_, hkv, hq // hkv, d)
-    for f in (O.decode_cpu_vectorised, O.decode_cpu_reference_shaped):
+    for f in (O.decode_cpu_vectorised, O.decode_cpu_reference_shaped,
+              lambda *a: O.decode_cpu_parallel(*a, n_threads=4, chunk=128)):
         out = f(qt, cents, idx, vals)
         assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-4
