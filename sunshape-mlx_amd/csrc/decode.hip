@@ -266,22 +266,22 @@ struct VTurbo {
 // SunShape block-VQ values (value backend "sunshape", reference
 // cache.py:614-623, 785-800): per token NBV = D / BD uint8 centroid indices
 // of BD-dim blocks in the value codec's basis.  The value codebook is staged
-// in LDS beside the key LUT: a workgroup takes one slab of the head dim
-// (kSlabs slabs, at most 64 KB of float32 centroids each, so D = 128 runs as
-// two workgroups per split and column that share the scores and split the
-// dims).  A lane takes 16 consecutive codec dims of its slab (16 / BD blocks,
-// one 4- or 2-byte index group) and reads their centroids from LDS;
+// in LDS beside the key LUT as fp16 (64 KB at D = 128, so one workgroup
+// covers the whole head dim and computes each score once; rounding a
+// centroid to fp16 changes it by at most 2^-12 of itself, and the products
+// accumulate in fp32).  A lane takes 16 consecutive codec dims (16 / BD
+// blocks, one 4- or 2-byte index group) and reads their centroids from LDS;
 // accumulation runs in the codec basis and the transform back to the
 // original basis (inverse permutation or rotation, as a D x D matrix) is
 // applied per output row after the merge.
 template <int D, int BD>
 struct VSunV {
-    static constexpr int kSlabs = D * 256 * 4 > 65536 ? 2 : 1;
+    static constexpr int kSlabs = D * 256 * 2 > 65536 ? 2 : 1;
     static constexpr int DS = D / kSlabs;            // dims of one workgroup
-    // this slab's centroids (256 per block), then the heavy dims' query values
+    // the slab's fp16 centroids (256 per block), then the heavy dims' query values
     static constexpr int kMaxHeavyDims = 64;
-    static constexpr int kHeavyOffset = DS * 256;  // floats
-    static constexpr int kLdsBytes = (DS * 256 + 4 * kMaxHeavyDims) * 4;
+    static constexpr int kHeavyOffset = DS * 256 / 2;  // floats
+    static constexpr int kLdsBytes = DS * 256 * 2 + 4 * kMaxHeavyDims * 4;
     static constexpr bool kHeavyKeys = true;
     static constexpr int DPL = 16;
     static constexpr int BPL = DPL / BD;  // blocks per lane
@@ -315,10 +315,11 @@ struct VSunV {
         }
         return r;
     }
-    // the slab's centroids -> lds [NBVS][256][BD] (entries past n_centroids zero)
+    // the slab's centroids -> lds [NBVS][256][BD] fp16, rounded to nearest
+    // (entries past n_centroids zero)
     __device__ static __forceinline__ void stage(float *lds, const Args &a, int slab, int tid,
                                                  int nt) {
-        float4 *l4 = reinterpret_cast<float4 *>(lds);
+        uint2 *l2 = reinterpret_cast<uint2 *>(lds);  // 4 halves per entry
         for (int i = tid; i < NBVS * 256 * BD / 4; i += nt) {
             const int f = i * 4, bl = f / (256 * BD), within = f - bl * (256 * BD);
             const int cc = within / BD;
@@ -326,24 +327,28 @@ struct VSunV {
             if (cc < a.n_centroids)
                 v = *reinterpret_cast<const float4 *>(
                     a.cb + ((int64_t)(slab * NBVS + bl) * a.n_centroids + cc) * BD + within % BD);
-            l4[i] = v;
+            const __half2 lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
+            l2[i] = make_uint2(*reinterpret_cast<const uint32_t *>(&lo),
+                               *reinterpret_cast<const uint32_t *>(&hi));
         }
     }
     // lt: lane group within the slab
     __device__ static __forceinline__ void decode_lds(const float *lds, const Args &, const Raw &r,
                                                       int lt, float *x) {
-        const float4 *l4 = reinterpret_cast<const float4 *>(lds);
+        const uint2 *l2 = reinterpret_cast<const uint2 *>(lds);
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             const int bl = lt * BPL + i;
             const int cc = (int)((r.w >> (8 * i)) & 0xffu);
 #pragma unroll
             for (int h = 0; h < BD / 4; ++h) {
-                const float4 v = l4[((bl * 256 + cc) * BD) / 4 + h];
-                x[i * BD + 4 * h + 0] = v.x;
-                x[i * BD + 4 * h + 1] = v.y;
-                x[i * BD + 4 * h + 2] = v.z;
-                x[i * BD + 4 * h + 3] = v.w;
+                const uint2 v = l2[((bl * 256 + cc) * BD) / 4 + h];
+                const float2 a = __half22float2(*reinterpret_cast<const __half2 *>(&v.x));
+                const float2 b = __half22float2(*reinterpret_cast<const __half2 *>(&v.y));
+                x[i * BD + 4 * h + 0] = a.x;
+                x[i * BD + 4 * h + 1] = a.y;
+                x[i * BD + 4 * h + 2] = b.x;
+                x[i * BD + 4 * h + 3] = b.y;
             }
         }
     }
