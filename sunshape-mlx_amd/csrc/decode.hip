@@ -276,6 +276,8 @@ struct VTurbo {
 // applied per output row after the merge.
 template <int D, int BD>
 struct VSunV {
+    // two waves per SIMD: the LDS gathers of one hide behind the other's FMAs
+    static constexpr int kThreads = 512;
     static constexpr int kSlabs = D * 256 * 2 > 65536 ? 2 : 1;
     static constexpr int DS = D / kSlabs;            // dims of one workgroup
     // the slab's fp16 centroids (256 per block), then the heavy dims' query values
@@ -414,20 +416,30 @@ struct IdxRow {
     }
 };
 
-template <int D, int R>
+template <class VF, class = void>
+struct VfThreads {  // workgroup size of the VALU decode for this format
+    static constexpr int value = kDecodeThreads;
+};
+template <class VF>
+struct VfThreads<VF, std::void_t<decltype(VF::kThreads)>> {
+    static constexpr int value = VF::kThreads;
+};
+
+template <int D, int R, int WAVES = kDecodeWaves>
 constexpr size_t decode_lds_bytes() {
     return sizeof(float) * ((size_t)R * (D / kBlockDim) * kLutStride + (size_t)R * D +
-                            (size_t)kDecodeWaves * kWave * R);
+                            (size_t)WAVES * kWave * R);
 }
 
 template <int D, int R, class VF>
-__global__ void __launch_bounds__(kDecodeThreads)
+__global__ void __launch_bounds__(VfThreads<VF>::value)
     decode_attn_kernel(DecodeCommon c, typename VF::Args va) {
+    constexpr int TH = VfThreads<VF>::value, WV = TH / kWave;
     constexpr int NB = D / kBlockDim;
     constexpr int DPL = VF::DPL, LPT = VF::LPT, TPI = VF::TPI, ITERS = VF::ITERS;
     constexpr int CHUNK = ITERS < 16 ? ITERS : 16;
     static_assert(ITERS % CHUNK == 0, "chunking");
-    static_assert(kDecodeWaves * R * (D + 2) <= R * NB * kLutStride, "merge scratch");
+    static_assert(WV * R * (D + 2) <= R * NB * kLutStride, "merge scratch");
     // a format may split the head dim over SL workgroups (blockIdx.z) and
     // stage VLDS bytes of its own in LDS
     constexpr int SL = VfSlabs<VF>::value, DS = D / SL, VLDS = VfLds<VF>::value;
@@ -437,7 +449,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
     float *lut = smem;                          // [R][NB][kLutStride]
     float *qp = lut + R * NB * kLutStride;      // [R][D]
     float *pbuf = qp + R * D;                   // [waves][64][R]
-    float *vlds = pbuf + kDecodeWaves * kWave * R;  // the format's staged data
+    float *vlds = pbuf + WV * kWave * R;  // the format's staged data
     const int slab = SL > 1 ? (int)blockIdx.z : 0;
 
     const int tid = threadIdx.x;
@@ -461,7 +473,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
 
     // 1. query rows: round_to(q_dtype, q * scale) (attention.py:208), then
     //    the codec permutation (attention.py:228).
-    for (int i = tid; i < R * D; i += kDecodeThreads) {
+    for (int i = tid; i < R * D; i += TH) {
         const int r = i / D, j = i - r * D;
         float x = 0.f;
         if (row_ok(r)) {
@@ -481,7 +493,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
             for (int j = 0; j < va.nhd; ++j)
                 heavy_blocks |= 1u << (min(max(va.heavy_dims[j], 0), D - 1) / kBlockDim);
     const int nbc = NB * c.n_centroids;
-    for (int e = tid; e < nbc; e += kDecodeThreads) {
+    for (int e = tid; e < nbc; e += TH) {
         const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
         const float4 *cp = reinterpret_cast<const float4 *>(c.centroids + (int64_t)e * kBlockDim);
         const float4 c0 = cp[0], c1 = cp[1];
@@ -499,12 +511,12 @@ __global__ void __launch_bounds__(kDecodeThreads)
             lut[(r * NB + b) * kLutStride + cc] = ((heavy_blocks >> b) & 1u) ? 0.f : dot * kLog2e;
         }
     }
-    if constexpr (VLDS > 0) VF::stage(vlds, va, slab, tid, kDecodeThreads);
+    if constexpr (VLDS > 0) VF::stage(vlds, va, slab, tid, TH);
     if constexpr (VfHeavy<VF>::value) {
         // heavy dims' query values, in log2 units like the LUT
         float *qh = vlds + VF::kHeavyOffset;
         if (va.kheavy)
-            for (int i = tid; i < R * va.nhd; i += kDecodeThreads) {
+            for (int i = tid; i < R * va.nhd; i += TH) {
                 const int r = i / va.nhd, j = i - r * va.nhd;
                 qh[i] = qp[r * D + min(max(va.heavy_dims[j], 0), D - 1)] * kLog2e;
             }
@@ -541,7 +553,7 @@ __global__ void __launch_bounds__(kDecodeThreads)
     }
     float *pw = pbuf + wv * kWave * R;
 
-    for (int tile = wv; tile < n_tiles; tile += kDecodeWaves) {
+    for (int tile = wv; tile < n_tiles; tile += WV) {
         const int64_t t0 = t_beg + (int64_t)tile * kWave;
         typename VF::Raw vr[CHUNK];
 #pragma unroll
@@ -663,8 +675,8 @@ __global__ void __launch_bounds__(kDecodeThreads)
     }
     __syncthreads();  // every wave is done with the LUT; reuse it
     float *wm = smem;                        // [waves][R]
-    float *wl = wm + kDecodeWaves * R;       // [waves][R]
-    float *wa = wl + kDecodeWaves * R;       // [waves][R][DS]
+    float *wl = wm + WV * R;       // [waves][R]
+    float *wa = wl + WV * R;       // [waves][R][DS]
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -684,14 +696,14 @@ __global__ void __launch_bounds__(kDecodeThreads)
     __syncthreads();
 
     const int S = c.n_splits;
-    for (int i = tid; i < R * DS; i += kDecodeThreads) {
+    for (int i = tid; i < R * DS; i += TH) {
         const int r = i / DS, d = i - r * DS, dd = slab * DS + d;
         float M = -1e30f;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, wm[w * R + r]);
+        for (int w = 0; w < WV; ++w) M = fmaxf(M, wm[w * R + r]);
         float L = 0.f, A = 0.f;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
+        for (int w = 0; w < WV; ++w) {
             const float f = fast_exp2(wm[w * R + r] - M);
             L = fmaf(wl[w * R + r], f, L);
             A = fmaf(wa[(w * R + r) * DS + d], f, A);
@@ -2389,7 +2401,8 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
 template <int D, int R, class VF>
 static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
                   hipStream_t st, bool merge = true) {
-    const size_t lds = decode_lds_bytes<D, R>() + VfLds<VF>::value;
+    constexpr int TH = VfThreads<VF>::value;
+    const size_t lds = decode_lds_bytes<D, R, TH / kWave>() + VfLds<VF>::value;
     auto kern = decode_attn_kernel<D, R, VF>;
     static bool attr_set = false;  // per instantiation
     if (!attr_set) {
@@ -2399,7 +2412,7 @@ static int launch(DecodeCommon c, const typename VF::Args &va, const DecodeShape
         attr_set = true;
     }
     dim3 grid(s.S, s.n_cols, VfSlabs<VF>::value);
-    hipLaunchKernelGGL(kern, grid, dim3(kDecodeThreads), lds, st, c, va);
+    hipLaunchKernelGGL(kern, grid, dim3(TH), lds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_kernel launch");
     return merge ? launch_merge<D>(c, s, st) : SS_OK;
 }
