@@ -276,8 +276,8 @@ struct VTurbo {
 // applied per output row after the merge.
 template <int D, int BD>
 struct VSunV {
-    // two waves per SIMD: the LDS gathers of one hide behind the other's FMAs
-    static constexpr int kThreads = 512;
+    // three waves per SIMD: the LDS gathers of one hide behind the others' FMAs
+    static constexpr int kThreads = 768;
     static constexpr int kSlabs = D * 256 * 2 > 65536 ? 2 : 1;
     static constexpr int DS = D / kSlabs;            // dims of one workgroup
     // the slab's fp16 centroids (256 per block), then the heavy dims' query values
@@ -597,10 +597,16 @@ __global__ void __launch_bounds__(VfThreads<VF>::value)
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) s[r] = (kok && tk <= lim[r]) ? s[r] : -INFINITY;
-        float corr[R];
+        float corr[R], tmax[R];
+        if constexpr (R == 4) {
+            wave_max4_dpp(s, tmax);  // DPP lane moves, the four rows interleaved
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) tmax[r] = wave_max(s[r]);
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const float mn = fmaxf(m[r], wave_max(s[r]));
+            const float mn = fmaxf(m[r], tmax[r]);
             corr[r] = fast_exp2(m[r] - mn);
             const float p = fast_exp2(s[r] - mn);
             l[r] = fmaf(l[r], corr[r], p);
