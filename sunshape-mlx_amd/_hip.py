@@ -223,7 +223,21 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def device_index(device) -> int:
+    if isinstance(device, int):
+        return device
+    if device is None or device.index is None:
+        return torch.cuda.current_device()
+    return device.index
+
+
 def stream_handle(device: torch.device | None = None) -> int:
+    """hipStream_t of the current stream of ``device``."""
+    if _raw_stream is not None:
+        return _raw_stream(device_index(device))
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -278,20 +292,119 @@ def set_spin_limit(limit: int | None) -> None:
 _ws_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 
-def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def decode_workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Per (device, stream) scratch for split-T partials.  Calls on one stream
     are ordered, so they never overlap on the same buffer.  Allocated zeroed:
     its first 64 KiB hold the per-column split counters, which every call
     leaves at zero."""
     if nbytes <= 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           stream_handle(device))
+    dev = device_index(device)
+    key = (dev, stream if stream is not None else stream_handle(dev))
     ws = _ws_cache.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", dev))
         _ws_cache[key] = ws
     return ws
+
+
+class PreparedDecode:
+    """A matrix-core decode (ss_decode_attn_il8 or ss_decode_attn_grouped_il)
+    over fixed cache buffers, codebook and query shape: the C-ABI arguments
+    that do not change between steps are checked and built once, and a call
+    fills in the query, the output, the cache length, the causal offset and
+    the current stream.  The split workspace is the per-(device, stream) one,
+    passed at its allocated size; a call that needs more grows it and
+    launches then (the library checks the size before it launches anything).
+    The caller keeps the buffers alive (the cache that built the plan owns
+    them) and builds a new plan when any of them changes."""
+
+    __slots__ = ("fn", "pre", "dev", "shape", "dtype", "plan_args", "stat")
+
+    def __init__(self, fn, pre: tuple, q: torch.Tensor, stat: str):
+        self.fn = fn
+        self.pre = pre
+        self.dev = device_index(q.device)
+        self.shape = tuple(q.shape)
+        self.dtype = q.dtype
+        self.plan_args = tuple(q.shape[:1]) + (pre[2], pre[3]) + tuple(q.shape[2:])
+        self.stat = stat
+
+    def __call__(self, q: torch.Tensor, t_kv: int, causal: bool = False, q_offset: int = 0,
+                 out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if q.shape != self.shape or q.dtype != self.dtype or not q.is_contiguous() or \
+                q.device.index != self.dev:
+            raise ValueError(f"query must be contiguous {self.dtype} {self.shape} on cuda:{self.dev}")
+        if out is None:
+            out = torch.empty(self.shape, dtype=out_dtype or self.dtype, device=q.device)
+        elif tuple(out.shape) != self.shape or not out.is_contiguous() or out.device != q.device:
+            raise ValueError(f"out must be contiguous {self.shape} on cuda:{self.dev}")
+        st = stream_handle(self.dev)
+        ws = _ws_cache.get((self.dev, st))
+        if ws is None:
+            ws = decode_workspace(self.dev, 1, st)
+        tail = (int(t_kv), int(bool(causal)), int(q_offset), out.data_ptr(),
+                dtype_code(out.dtype))
+        rc = self.fn(q.data_ptr(), *self.pre, *tail, ws.data_ptr(), ws.numel(), 0, st)
+        if rc == SS_ERR_WORKSPACE:
+            _, need = decode_plan(KIND_IL8, *self.plan_args, int(t_kv), 0)
+            ws = decode_workspace(self.dev, need, st)
+            rc = self.fn(q.data_ptr(), *self.pre, *tail, ws.data_ptr(), ws.numel(), 0, st)
+        _launched(_attn_stat(self.stat, causal), rc)
+        if _check_waits:
+            check_decode_waits(self.dev)
+        return out
+
+
+def prepare_decode_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                       codebook: torch.Tensor, n_blocks: int, n_centroids: int,
+                       idx: torch.Tensor, values_il8: torch.Tensor) -> PreparedDecode:
+    """:class:`PreparedDecode` of :func:`decode_attn_il8` for queries shaped
+    like ``q`` (the same checks, done once)."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(values_il8, codebook)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if nb != n_blocks or values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(n_blocks, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+           nb, n_centroids, ptr(idx), ptr(values_il8), SS_F16, cap)
+    return PreparedDecode(lib.ss_decode_attn_il8, pre, q, "sunshape_fused_attention_mfma")
+
+
+def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                              codebook: torch.Tensor, n_blocks: int, n_centroids: int,
+                              idx: torch.Tensor, codes_il: torch.Tensor, scales: torch.Tensor,
+                              zeros: torch.Tensor, bits: int, group_size: int) -> PreparedDecode:
+    """:class:`PreparedDecode` of :func:`decode_attn_grouped_il` (no token
+    buffer) for queries shaped like ``q``."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(codes_il, scales, zeros, codebook)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    tpw = 32 // bits if bits in (2, 4) else 0
+    if nb != n_blocks or not tpw or codes_il.dim() != 4 or not codes_il.is_contiguous() or \
+            tuple(codes_il.shape) != (b_, hkv, cap // tpw, d) or \
+            codes_il.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("codes_il does not match the cache shape")
+    for t in (scales, zeros):
+        if t.dim() != 4 or not t.is_contiguous() or t.shape[:3] != idx.shape[:3]:
+            raise ValueError("scales/zeros must be contiguous (B, n_kv_heads, cap, n_groups)")
+    if scales.dtype != zeros.dtype or scales.dtype not in (torch.float32, torch.float16):
+        raise ValueError("scales/zeros must share dtype float32 or float16")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(n_blocks, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+           nb, n_centroids, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros),
+           dtype_code(scales.dtype), int(bits), int(group_size), cap)
+    return PreparedDecode(lib.ss_decode_attn_grouped_il, pre, q,
+                          "sunshape_fused_attention_dequant_mfma")
 
 
 # --------------------------------------------------------------------------- #
@@ -386,7 +499,7 @@ def _check_decode_common(q, idx, centroids, perm):
         raise ValueError("queries must be contiguous (B, n_q_heads, T_q, D)")
     if idx.dim() != 4 or idx.dtype != torch.uint8 or not idx.is_contiguous():
         raise ValueError("key indices must be a contiguous uint8 (B, n_kv_heads, cap, n_blocks) buffer")
-    if centroids.dtype != torch.float32 or not centroids.is_contiguous():
+    if centroids is not None and (centroids.dtype != torch.float32 or not centroids.is_contiguous()):
         raise ValueError("centroids must be contiguous float32")
     if perm is not None and perm.dtype != torch.int32:
         raise ValueError("perm must be int32")

@@ -18,6 +18,8 @@ score kernels, torch softmax and matmul).
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _hip
@@ -47,6 +49,36 @@ def _transform_grouped(codec: SunShapeBlockCodec, q_grouped: torch.Tensor) -> to
     return q_grouped
 
 
+def _prepared_decode(cache, ops: dict, codec: SunShapeBlockCodec, q: torch.Tensor,
+                     kscale: float, perm):
+    """The cache's prepared matrix-core decode (``_hip.PreparedDecode``) for
+    queries shaped like ``q``: built on the first call and again whenever a
+    cache buffer, the codebook or the query layout changes (the plan holds
+    weak references, so it never keeps a replaced buffer alive)."""
+    kind = ops["kind"]
+    cb = codec.kernel_codebook()
+    if kind == "il8":
+        tensors = (ops["idx"], ops["values"], cb)
+    else:
+        tensors = (ops["idx"], ops["codes_il"], ops["scales"], ops["zeros"], cb)
+    if perm is not None:
+        tensors += (perm,)
+    key = (kind, q.shape, q.dtype, q.device, kscale, ops.get("bits"), ops.get("group_size"))
+    held = getattr(cache, "_decode_prepared", None)
+    if held is not None and held[0] == key and len(held[1]) == len(tensors) and \
+            all(r() is t for r, t in zip(held[1], tensors)):
+        return held[2]
+    nb, nc = codec.n_blocks, codec.n_centroids
+    if kind == "il8":
+        plan = _hip.prepare_decode_il8(q, kscale, perm, cb, nb, nc, ops["idx"], ops["values"])
+    else:
+        plan = _hip.prepare_decode_grouped_il(q, kscale, perm, cb, nb, nc, ops["idx"],
+                                              ops["codes_il"], ops["scales"], ops["zeros"],
+                                              ops["bits"], ops["group_size"])
+    cache._decode_prepared = (key, tuple(weakref.ref(t) for t in tensors), plan)
+    return plan
+
+
 def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int):
     """One fused launch over the whole cache, or None when no fused kernel
     applies to this cache / shape (the reference's None-fallback,
@@ -64,13 +96,20 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return None
     q, kscale, perm = _kernel_query(codec, queries, scale)
     t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
+    kind = ops["kind"]
+    # the matrix-core decodes without a token buffer: one prepared launch
+    # (argument checks, codebook and split plan done once per cache layout)
+    if kind == "il8" or (kind == "grouped_il" and not buffered):
+        try:
+            plan = _prepared_decode(cache, ops, codec, q, kscale, perm)
+            out = plan(q, t_kv, causal, q_offset, out_dtype=queries.dtype)
+        except _hip.SunShapeUnsupported:
+            return None
+        codec.last_score_backend = "hip_fused_mfma" if kind == "il8" else "hip_fused_mfma_dequant"
+        return out
     kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
     try:
-        if ops["kind"] == "il8":
-            out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
-                                       codebook=codec.kernel_codebook(), **kw)
-            codec.last_score_backend = "hip_fused_mfma"
-        elif ops["kind"] == "grouped_il":
+        if kind == "grouped_il":
             out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.centroids, ops["idx"],
                                               ops["codes_il"], ops["scales"], ops["zeros"],
                                               ops["bits"], ops["group_size"],

@@ -383,12 +383,11 @@ class SunShapeBlockCodec:
         matrix-core LUT build of the fused decodes, prepared once and rebuilt
         when the centroids change (new tensor, device or in-place update)."""
         c = self.scoring_centroids()
-        key = (c.data_ptr(), c._version, str(c.device), tuple(c.shape))
         cached = getattr(self, "_kernel_codebook", None)
-        if cached is None or cached[0] != key:
-            cached = (key, _hip.codebook_f16x2(c))
+        if cached is None or cached[0] is not c or cached[1] != c._version:
+            cached = (c, c._version, _hip.codebook_f16x2(c))
             self._kernel_codebook = cached
-        return cached[1]
+        return cached[2]
 
     def _encode_centroids(self) -> torch.Tensor:
         if self.mode == "profileperm_localmetric_dsq":

@@ -107,6 +107,72 @@ def test_fp16_cache_causal_prefill_and_capacity_growth():
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
 
 
+def test_prepared_decode_follows_the_cache_and_matches_direct_launch():
+    """``sunshape_sdpa`` launches the matrix-core decode through a plan kept
+    on the cache.  It must give the same bits as the checked one-shot
+    launcher, be rebuilt when the cache's buffers are replaced (capacity
+    growth) or the query dtype changes, follow the current stream, and grow
+    a workspace too small for the split plan before it launches."""
+    codec = make_codec(31)
+    b, hq, hkv, d, scale = 2, 8, 2, 128, 0.09
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv)
+    k, v = kv(32, b, hkv, 700, d)
+    cache.update_and_fetch(k[:, :, :200], v[:, :, :200])
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+
+    def direct(qq, t_kv):
+        ops = cache.fused_operands()
+        return S._hip.decode_attn_il8(qq, scale, codec.permutation, codec.centroids, ops["idx"],
+                                      ops["values"], t_kv, codebook=codec.kernel_codebook())
+
+    out1 = S.sunshape_sdpa(q, cache, scale)
+    plan1 = cache._decode_prepared[2]
+    assert torch.equal(out1, direct(q, 200))
+    assert S.sunshape_sdpa(q, cache, scale) is not out1 and cache._decode_prepared[2] is plan1
+    idx_before = cache.fused_operands()["idx"]
+    cache.update_and_fetch(k[:, :, 200:700], v[:, :, 200:700])  # capacity grows
+    assert cache.fused_operands()["idx"] is not idx_before
+    out2 = S.sunshape_sdpa(q, cache, scale)
+    assert cache._decode_prepared[2] is not plan1
+    assert torch.equal(out2, direct(q, 700))
+    ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), scale)
+    assert rel_err(out2.float().cpu().numpy(), ref) <= 2e-3
+    qb = q.to(torch.bfloat16)
+    out3 = S.sunshape_sdpa(qb, cache, scale)
+    assert out3.dtype == torch.bfloat16 and torch.equal(out3, direct(qb, 700))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out4 = S.sunshape_sdpa(q, cache, scale)
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(out4, out2)
+
+
+def test_prepared_decode_grows_a_small_workspace():
+    """A split plan that needs more than the per-stream workspace holds: the
+    prepared launch sees the library's workspace error (raised before any
+    launch), grows the workspace and launches once."""
+    codec = make_codec(33)
+    b, hq, hkv, d, t_kv = 8, 32, 8, 128, 4096
+    splits, need = S._hip.decode_plan(S._hip.KIND_IL8, b, hq, hkv, 1, d, t_kv)
+    assert splits > 1 and need > (256 << 10)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, max_tokens=t_kv)
+    k, v = kv(34, b, hkv, t_kv, d)
+    cache.update_and_fetch(k, v)
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    key = (0, S._hip.stream_handle(DEV))
+    S._hip._ws_cache[key] = torch.zeros(256 << 10, dtype=torch.uint8, device=DEV)
+    disp = S.get_kernel_stats().get("sunshape_fused_attention_mfma_hip", 0)
+    out = S.sunshape_sdpa(q, cache, 0.05)
+    assert S.get_kernel_stats().get("sunshape_fused_attention_mfma_hip", 0) == disp + 1
+    assert S._hip._ws_cache[key].numel() >= need
+    ops = cache.fused_operands()
+    ref = S._hip.decode_attn_il8(q, 0.05, codec.permutation, codec.centroids, ops["idx"],
+                                 ops["values"], t_kv, codebook=codec.kernel_codebook())
+    assert torch.equal(out, ref)
+
+
 def test_mask_array_takes_two_pass_and_matches():
     codec = make_codec(5)
     b, hq, hkv, d, t_kv, tq = 1, 4, 1, 128, 96, 3
