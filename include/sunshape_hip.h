@@ -216,6 +216,27 @@ int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                        int n_splits, void *stream);
 
 /*
+ * ss_decode_attn_il8 over a hybrid cache whose compressed tokens keep fp16
+ * values (value_backend "fp16"): compressed tokens 0 .. t_kv-1 plus the
+ * recent-token buffer of t_buf tokens at positions t_kv .. t_kv+t_buf-1, in
+ * one online softmax, with the buffer conventions of
+ * ss_decode_attn_grouped_il_hybrid (keys and values in the original basis,
+ * buf_dtype elements at k_buf/v_buf[b*buf_sb + h*buf_sh + t*buf_st + d]).
+ * No reference counterpart: the reference takes a buffered hybrid cache to
+ * its two-pass path (attention.py:238, 307-350), whose result this equals
+ * within the decode tolerance.  t_buf = 0 is ss_decode_attn_il8.
+ */
+int ss_decode_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                              int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                              const int32_t *perm, const void *codebook, int n_blocks,
+                              int n_centroids, const uint8_t *idx, const void *values_il8,
+                              int v_dtype, int64_t cap, int64_t t_kv, const void *k_buf,
+                              const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+                              int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset,
+                              void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+                              int n_splits, void *stream);
+
+/*
  * ss_decode_attn_il8 without a workspace: the same kernel, arguments and
  * result, with its split partials and per-column split counters in a static
  * device array of the library (ss_decode_static_scratch_bytes() = 4 MiB,

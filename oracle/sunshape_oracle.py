@@ -521,7 +521,7 @@ def sdpa(queries, key_indices, values, centroids, perm, scale, mask=None):
 
 
 def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
-                  values_all, mask=None, heavy_keys=None, heavy_dims=None):
+                  values_all, mask=None, heavy_keys=None, heavy_dims=None, rotation=None):
     """The two-pass fallback of attention.py:307-350 used when a hybrid cache
     has buffered fp16 tokens: compressed scores ``q_t . k_hat`` concatenated
     with ``q_scaled . k_buf^T`` (original basis), causal or additive/boolean
@@ -535,7 +535,11 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
     codec.py:381-388): the heavy blocks (those holding ``heavy_dims``) leave
     the centroid sum, whatever their centroids hold (the fit's DSQ
     refinement moves centroid 0, codec.py:400-410), and the exact dot
-    products ``q_t[heavy_dims] . k_heavy`` take their place."""
+    products ``q_t[heavy_dims] . k_heavy`` take their place.
+
+    ``rotation`` (D, D): a rotated codec's codec-space queries are
+    ``q_scaled @ R^T`` (attention.py:229-230) in place of the permutation;
+    buffered keys are still scored in the original basis (attention.py:323)."""
     if heavy_keys is not None:
         bd = np.asarray(centroids).shape[2]
         centroids = np.array(centroids, dtype=np.float32, copy=True)
@@ -546,7 +550,10 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
     rep = hq // hkv
     t_kv = values_all.shape[2]
     qg = q.reshape(b_, hkv, rep, tq, d)
-    qt = apply_permutation(qg, perm)
+    if rotation is not None:
+        qt = (qg.astype(np.float64) @ np.asarray(rotation, np.float64).T).astype(np.float32)
+    else:
+        qt = apply_permutation(qg, perm)
     out = np.zeros((b_, hq, tq, d))
     for b in range(b_):
         for h in range(hkv):

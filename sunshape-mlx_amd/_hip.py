@@ -80,6 +80,11 @@ _SIGNATURES = {
                                   _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
                                   _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p, _size,
                                   _int, _c_void_p]),
+    "ss_decode_attn_il8_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_attn_il8_noalloc": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                           _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                           _int, _i64, _i64, _int, _i64, _c_void_p, _int, _int,
@@ -559,14 +564,26 @@ def codebook_f16x2(centroids: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len):
+    """The C-ABI buffer arguments (k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
+    buf_st, t_buf) of a hybrid cache's buffered tokens."""
+    kb, vb, code, sb, sh, st = _buffer_args(buf_keys, buf_values, buf_len, b_, hkv, d)
+    return ptr(kb), ptr(vb), code, sb, sh, st, int(buf_len)
+
+
 def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                     centroids: torch.Tensor, idx: torch.Tensor, values_il8: torch.Tensor,
                     t_kv: int, causal: bool = False, q_offset: int = 0,
                     out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                    n_splits: int = 0, codebook: torch.Tensor | None = None) -> torch.Tensor:
+                    n_splits: int = 0, codebook: torch.Tensor | None = None,
+                    buf_keys: torch.Tensor | None = None,
+                    buf_values: torch.Tensor | None = None, buf_len: int = 0) -> torch.Tensor:
     """Fused decode (matrix-core LUT and P.V) over fp16 values in the 8-token
     interleaved layout ``values_il8`` (B, Hkv, cap/8, D, 8).  ``codebook`` is
-    :func:`codebook_f16x2` of ``centroids`` (prepared here when None)."""
+    :func:`codebook_f16x2` of ``centroids`` (prepared here when None).  A
+    hybrid cache's recent tokens ``buf_keys``/``buf_values`` (B, Hkv,
+    >= buf_len, D, original basis) join the same softmax as positions t_kv ..
+    t_kv + buf_len - 1 (``ss_decode_attn_il8_hybrid``)."""
     _check_decode_common(q, idx, centroids, perm)
     if codebook is None:
         codebook = codebook_f16x2(centroids)
@@ -583,11 +600,16 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
     _, ws_bytes = decode_plan(KIND_IL8, b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
-    _launched(_attn_stat("sunshape_fused_attention_mfma", causal), load_library().ss_decode_attn_il8(
-        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
-        nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv), int(bool(causal)),
-        int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
-        int(n_splits), stream_handle(q.device)))
+    common = (ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm),
+              ptr(codebook), nb, nc, ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv))
+    tail = (int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+            ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device))
+    stat = _attn_stat("sunshape_fused_attention_mfma", causal)
+    if buf_keys is None or buf_len == 0:
+        _launched(stat, load_library().ss_decode_attn_il8(*common, *tail))
+    else:
+        buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len)
+        _launched(stat, load_library().ss_decode_attn_il8_hybrid(*common, *buf, *tail))
     if _check_waits:
         check_decode_waits(q.device)
     return out
@@ -874,17 +896,9 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
         if _check_waits:
             check_decode_waits(q.device)
         return out
-    require_gpu(buf_keys, buf_values)
-    if buf_keys.dim() != 4 or buf_keys.shape[:2] != (b_, hkv) or buf_keys.shape[3] != d or \
-            buf_values.shape != buf_keys.shape or buf_values.stride() != buf_keys.stride() or \
-            buf_keys.stride(-1) != 1 or buf_keys.dtype != buf_values.dtype or \
-            buf_keys.shape[2] < buf_len:
-        raise ValueError("buf_keys/buf_values must be matching (B, n_kv_heads, >= buf_len, D) "
-                         "views with unit last stride")
+    buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len)
     _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il_hybrid(
-        *common, ptr(buf_keys), ptr(buf_values), dtype_code(buf_keys.dtype), buf_keys.stride(0),
-        buf_keys.stride(1), buf_keys.stride(2), int(buf_len), int(bool(causal)), int(q_offset),
-        *tail))
+        *common, *buf, int(bool(causal)), int(q_offset), *tail))
     if _check_waits:
         check_decode_waits(q.device)
     return out

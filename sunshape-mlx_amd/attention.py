@@ -88,18 +88,25 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return None
     codec = cache.codec
     buffered = cache.buffer_offset if isinstance(cache, HybridSunShapeKVCache) else 0
-    # the buffer joins the fused softmax on the grouped interleaved,
-    # TurboQuant and SunShape-value kernels, whose buffer scores use the
-    # unrotated query
-    if buffered and (ops["kind"] not in ("grouped_il", "turboquant", "sunshape_v")
-                     or codec.use_rotation):
+    # the buffer joins the fused softmax on the interleaved fp16, grouped
+    # interleaved, TurboQuant and SunShape-value kernels
+    if buffered and ops["kind"] not in ("il8", "grouped_il", "turboquant", "sunshape_v"):
         return None
     q, kscale, perm = _kernel_query(codec, queries, scale)
+    if buffered and codec.mode not in PERM_MODES and codec.use_rotation:
+        # the kernels score buffered keys against the query they are given,
+        # here the rotated one: (q R^T) . (k R^T) = q . k for orthogonal R,
+        # so the buffer's keys go in rotated (float32, with float32 values
+        # to share their layout)
+        nb_ = buffered
+        ops = dict(ops, buf_keys=(ops["buf_keys"][:, :, :nb_].float()
+                                  @ codec.rotation.t()).contiguous(),
+                   buf_values=ops["buf_values"][:, :, :nb_].float().contiguous())
     t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
     kind = ops["kind"]
     # the matrix-core decodes without a token buffer: one prepared launch
     # (argument checks, codebook and split plan done once per cache layout)
-    if kind == "il8" or (kind == "grouped_il" and not buffered):
+    if not buffered and kind in ("il8", "grouped_il"):
         try:
             plan = _prepared_decode(cache, ops, codec, q, kscale, perm)
             out = plan(q, t_kv, causal, q_offset, out_dtype=queries.dtype)
@@ -109,7 +116,12 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return out
     kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
     try:
-        if kind == "grouped_il":
+        if kind == "il8":
+            out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
+                                       codebook=codec.kernel_codebook(), buf_keys=ops["buf_keys"],
+                                       buf_values=ops["buf_values"], buf_len=buffered, **kw)
+            codec.last_score_backend = "hip_fused_mfma_buffer"
+        elif kind == "grouped_il":
             out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.centroids, ops["idx"],
                                               ops["codes_il"], ops["scales"], ops["zeros"],
                                               ops["bits"], ops["group_size"],

@@ -312,6 +312,11 @@ class HybridSunShapeKVCache:
         self._value_norms: torch.Tensor | None = None
         self._value_indices: torch.Tensor | None = None
         self._values_fp16: torch.Tensor | None = None
+        # fp16 values of compressed tokens kept 8-token interleaved ((B, H,
+        # cap/8, D, 8), the matrix-core decode's layout) where the codec
+        # allows it, else token-major in _values_fp16
+        self._values_il8: torch.Tensor | None = None
+        self._fp16_il8 = self.value_backend == "fp16" and _il8_ok(codec, self.head_dim, dtype)
         self._value_n_groups = 0
         self._compressed_capacity = 0
         # grouped codes held token-interleaved ((B, H, cap*bits/32, D) words)
@@ -367,6 +372,10 @@ class HybridSunShapeKVCache:
         elif self.value_backend == "sunshape":
             self._value_indices = _grow(self._value_indices, (b_, h_, cap, self.value_n_blocks),
                                         torch.uint8, device, keep)
+        elif self._fp16_il8:
+            # whole 8-token groups move; the tail of the last one is zero
+            self._values_il8 = _grow(self._values_il8, (b_, h_, cap // 8, self.head_dim, 8),
+                                     torch.float16, device, (keep + 7) // 8)
         else:
             self._values_fp16 = _grow(self._values_fp16, (b_, h_, cap, self.head_dim),
                                       self.dtype, device, keep)
@@ -417,6 +426,9 @@ class HybridSunShapeKVCache:
         elif self.value_backend == "sunshape":
             _encode_into(self.value_codec, vf, self._value_indices[:, :, c0:c1])
             self.last_value_quant_backend = "sunshape"
+        elif self._fp16_il8:
+            _hip.append_values_il8(vf, self._values_il8, c0)
+            self.last_value_quant_backend = "fp16"
         else:
             self._values_fp16[:, :, c0:c1] = vf.to(self.dtype)
             self.last_value_quant_backend = "fp16"
@@ -493,6 +505,8 @@ class HybridSunShapeKVCache:
         if self.value_backend == "sunshape" and self._value_indices is not None:
             return _dequantize_keys(self.value_codec,
                                     self._value_indices[:, :, :tc_]).to(self.dtype)
+        if self._values_il8 is not None:
+            return _hip.il8_to_dense(self._values_il8, tc_)
         if self._values_fp16 is not None:
             return self._values_fp16[:, :, :tc_]
         return None
@@ -599,6 +613,9 @@ class HybridSunShapeKVCache:
                     "v_transform": vc.kernel_value_transform(),
                     "buf_keys": self._key_buffer, "buf_values": self._value_buffer,
                     "k_heavy": self._key_heavy, "heavy_dims": self._heavy_dims}
+        if self.value_backend == "fp16" and self._values_il8 is not None:
+            return {"kind": "il8", "idx": self._key_indices, "values": self._values_il8,
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None

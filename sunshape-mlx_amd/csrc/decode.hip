@@ -901,7 +901,8 @@ struct VIl8 {
     // values of tokens t0 .. t0 + 64*kSub - 1 (contiguous); in a tile that
     // reaches past the split's last token, 8-token blocks past it are
     // clamped to its block, so every copy stays in bounds
-    __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+    template <class A>
+    __device__ static void issue(const A &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
                                  uint32_t sb, int lane) {
         const char *vhead = reinterpret_cast<const char *>(a.v8 + bh * cap * D);
         const int64_t b0 = t0 / 8, blk_last = t_last / 8;
@@ -992,6 +993,21 @@ struct VIl8 {
                     wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
         }
     }
+};
+
+// VIl8 over a hybrid cache: the same compressed tiles, and the recent-token
+// buffer (keys and values in the original basis, buf_dtype elements at
+// b*buf_sb + h*buf_sh + t*buf_st (+ dim)) attended as positions t_kv ..
+// t_kv + t_buf - 1 in the same softmax.
+template <int D>
+struct VIl8Hyb : VIl8<D> {
+    struct Args {
+        const __half *v8;
+        const void *kbuf, *vbuf;
+        int buf_dtype;
+        int64_t buf_sb, buf_sh, buf_st, t_buf;
+    };
+    static constexpr bool kHybridBuffer = true;
 };
 
 // Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
@@ -2942,13 +2958,31 @@ extern "C" int ss_codebook_f16x2(const float *centroids, int n_blocks, int n_cen
     return SS_OK;
 }
 
-extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
-                                  int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                  const int32_t *perm, const void *codebook, int n_blocks,
-                                  int n_centroids, const uint8_t *idx, const void *values_il8,
-                                  int v_dtype, int64_t cap, int64_t t_kv, int causal,
-                                  int64_t q_offset, void *out, int out_dtype, void *workspace,
-                                  size_t workspace_bytes, int n_splits, void *stream) {
+// Checks shared by the hybrid entry points: t_buf buffered tokens at k_buf /
+// v_buf with element strides buf_sb, buf_sh, buf_st.
+static int check_buffer(const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb,
+                        int64_t buf_sh, int64_t buf_st, int64_t t_buf, int head_dim) {
+    SS_REQUIRE(t_buf >= 0, "negative buffer length");
+    if (t_buf == 0) return SS_OK;
+    SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
+    SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
+               "buffer dtype must be f16, bf16 or f32");
+    SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
+               "buffer strides must be non-negative, token stride >= head_dim");
+    SS_REQUIRE(((uintptr_t)k_buf % 16) == 0 && buf_sb % 8 == 0 && buf_sh % 8 == 0 &&
+                   buf_st % 8 == 0,
+               "buffer keys must be 16-byte aligned with strides a multiple of 8 elements");
+    return SS_OK;
+}
+
+static int il8_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads,
+                    int64_t t_q, int head_dim, float scale, const int32_t *perm,
+                    const void *codebook, int n_blocks, int n_centroids, const uint8_t *idx,
+                    const void *values_il8, int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                    int64_t q_offset, void *out, int out_dtype, void *workspace,
+                    size_t workspace_bytes, int n_splits, const void *k_buf, const void *v_buf,
+                    int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
+                    int64_t t_buf, void *stream) {
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
@@ -2969,10 +3003,47 @@ extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int
     c.codebook = static_cast<const uint4 *>(codebook);
     c.codebook_mul = reinterpret_cast<const float *>(
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+    rc = check_buffer(k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, head_dim);
+    if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const __half *v8 = reinterpret_cast<const __half *>(values_il8);
+    if (t_buf > 0) {
+        if (head_dim == 128)
+            return launch_mfma<128, VIl8Hyb<128>>(
+                c, VIl8Hyb<128>::Args{v8, k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf},
+                s, st);
+        return launch_mfma<64, VIl8Hyb<64>>(
+            c, VIl8Hyb<64>::Args{v8, k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf}, s,
+            st);
+    }
     if (head_dim == 128) return launch_mfma<128, VIl8<128>>(c, VIl8<128>::Args{v8}, s, st);
     return launch_mfma<64, VIl8<64>>(c, VIl8<64>::Args{v8}, s, st);
+}
+
+extern "C" int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                  int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                  const int32_t *perm, const void *codebook, int n_blocks,
+                                  int n_centroids, const uint8_t *idx, const void *values_il8,
+                                  int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                  int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                  size_t workspace_bytes, int n_splits, void *stream) {
+    return il8_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                    codebook, n_blocks, n_centroids, idx, values_il8, v_dtype, cap, t_kv, causal,
+                    q_offset, out, out_dtype, workspace, workspace_bytes, n_splits, nullptr,
+                    nullptr, SS_F16, 0, 0, 0, 0, stream);
+}
+
+extern "C" int ss_decode_attn_il8_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, int n_blocks,
+    int n_centroids, const uint8_t *idx, const void *values_il8, int v_dtype, int64_t cap,
+    int64_t t_kv, const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb,
+    int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out,
+    int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    return il8_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                    codebook, n_blocks, n_centroids, idx, values_il8, v_dtype, cap, t_kv, causal,
+                    q_offset, out, out_dtype, workspace, workspace_bytes, n_splits, k_buf, v_buf,
+                    buf_dtype, buf_sb, buf_sh, buf_st, t_buf, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -3088,16 +3159,8 @@ static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_he
     c.codebook = static_cast<const uint4 *>(codebook);
     c.codebook_mul = reinterpret_cast<const float *>(
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
-    if (t_buf > 0) {
-        SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
-        SS_REQUIRE(buf_dtype == SS_F16 || buf_dtype == SS_BF16 || buf_dtype == SS_F32,
-                   "buffer dtype must be f16, bf16 or f32");
-        SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
-                   "buffer strides must be non-negative, token stride >= head_dim");
-        SS_REQUIRE(((uintptr_t)k_buf % 16) == 0 && buf_sb % 8 == 0 && buf_sh % 8 == 0 &&
-                       buf_st % 8 == 0,
-                   "buffer keys must be 16-byte aligned with strides a multiple of 8 elements");
-    }
+    rc = check_buffer(k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, head_dim);
+    if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int ng = head_dim / group_size;
 #define SS_GIL(DD, BB, NGG, SZT)                                                              \

@@ -25,6 +25,7 @@ import torch
 from safetensors import safe_open
 from safetensors.torch import save_file
 
+from . import _hip
 from .cache import HybridSunShapeKVCache, SunShapeKVCache
 from .codec import SunShapeBlockCodec
 
@@ -35,7 +36,7 @@ _CACHE_TENSORS = {
     "SunShapeKVCache": ("_key_indices", "_values"),
     "HybridSunShapeKVCache": ("_key_indices", "_values_packed", "_values_il", "_value_scales",
                               "_value_zeros", "_value_norms", "_value_indices", "_values_fp16",
-                              "_key_buffer", "_value_buffer", "_key_heavy"),
+                              "_values_il8", "_key_buffer", "_value_buffer", "_key_heavy"),
 }
 # integer bookkeeping restored alongside the buffers
 _CACHE_SCALARS = {
@@ -158,4 +159,15 @@ def load_cache(path: str, device=None):
             setattr(cache, name, tensors[key].to(dev))
     for k, v in json.loads(meta["cache_scalars"]).items():
         setattr(cache, k, int(v))
+    if kind == "HybridSunShapeKVCache" and cache._fp16_il8 and cache._values_fp16 is not None:
+        # fp16 values written token-major (files of earlier versions): move
+        # them into the interleaved layout the cache now keeps
+        vf = cache._values_fp16
+        b_, h_, cap, d = vf.shape
+        cache._values_il8 = torch.zeros((b_, h_, (cap + 7) // 8, d, 8), dtype=torch.float16,
+                                        device=vf.device)
+        if cache._compressed_offset:
+            _hip.append_values_il8(vf[:, :, :cache._compressed_offset].to(torch.float16),
+                                   cache._values_il8, 0)
+        cache._values_fp16 = None
     return cache

@@ -304,16 +304,68 @@ def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
 
 
-def test_hybrid_buffer_with_rotated_codec_takes_two_pass():
+@pytest.mark.parametrize("buf,t_total,tq,causal", [
+    (96, 700, 1, False),     # decode step (a 128-token buffer makes a SunShapeKVCache)
+    (64, 300, 5, True),      # prefill rows, causal across the buffer
+    (120, 140, 1, False),    # mostly buffer
+])
+def test_hybrid_fp16_buffer_joins_fused_decode(buf, t_total, tq, causal):
+    """Hybrid fp16-value caches keep compressed values 8-token interleaved;
+    with buffered tokens they stay on the matrix-core kernel, equal to the
+    reference's two-pass path over the same cache, and a trim into
+    compressed storage followed by appends keeps the values exact."""
+    codec = make_codec(41)
+    b, hq, hkv, d = 2, 8, 2, 128
+    k, v = kv(42 + buf, b, hkv, t_total + 40, d)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="fp16", buffer_size=buf)
+    assert isinstance(cache, S.HybridSunShapeKVCache)
+    pos = 0
+    for n in (t_total - 37, 30, 7):
+        cache.update_and_fetch(k[:, :, pos:pos + n], v[:, :, pos:pos + n])
+        pos += n
+    assert cache.buffer_offset > 0 and cache.compressed_offset > 0
+    assert torch.equal(cache.values, v[:, :, :pos])
+    q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
+    mask = "causal" if causal else None
+
+    def check():
+        out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
+        assert codec.last_score_backend == "hip_fused_mfma_buffer"
+        vals = cache.values.float().cpu().numpy()
+        ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                              codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
+                              cache.buffer_keys.float().cpu().numpy(), vals, mask=mask)
+        assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+
+    check()
+    cache.trim(buf + 5)  # all of the buffer and 5 compressed tokens
+    pos -= buf + 5
+    cache.update_and_fetch(k[:, :, pos:pos + 40], v[:, :, pos:pos + 40])
+    pos += 40
+    assert torch.equal(cache.values, v[:, :, :pos])
+    if cache.buffer_offset and cache.compressed_offset:
+        check()
+
+
+@pytest.mark.parametrize("backend", ["grouped", "turboquant"])
+def test_hybrid_buffer_with_rotated_codec_fused(backend):
+    """A rotated codec's buffered tokens join the fused softmax too: their
+    keys are rotated like the query, (q R^T) . (k R^T) = q . k, and the
+    result equals the two-pass path with the rotated query."""
     codec = make_codec(33, mode="rotated")
-    b, hq, hkv, d = 1, 4, 1, 128
+    b, hq, hkv, d = 2, 8, 2, 128
     k, v = kv(34, b, hkv, 300, d)
-    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2)
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend=backend, value_bits=2)
     cache.update_and_fetch(k, v)
+    assert cache.buffer_offset > 0 and cache.compressed_offset > 0
     q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
     out = S.sunshape_sdpa(q, cache, 0.088)
-    assert codec.last_score_backend == "hip"
-    assert torch.isfinite(out).all()
+    assert codec.last_score_backend.endswith("_buffer")
+    vals = cache.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, None, codec.centroids.cpu().numpy(),
+                          cache.key_indices.cpu().numpy(), cache.buffer_keys.float().cpu().numpy(),
+                          vals, rotation=codec.rotation.cpu().numpy())
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
 
 
 def test_hybrid_fp16_and_sunshape_value_backends():
@@ -323,9 +375,10 @@ def test_hybrid_fp16_and_sunshape_value_backends():
     cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="fp16", buffer_size=0)
     assert isinstance(cache, S.HybridSunShapeKVCache)
     cache.update_and_fetch(k, v)
+    assert torch.equal(cache.values, v)  # fp16 values kept 8-token interleaved
     q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
     out = S.sunshape_sdpa(q, cache, 0.088)
-    assert codec.last_score_backend == "hip_fused"
+    assert codec.last_score_backend == "hip_fused_mfma"
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3

@@ -464,6 +464,26 @@ def test_decode_grouped_il_matches_oracle(b, hq, hkv, d, t_kv, t_q, bits, group,
     assert rel_err(got, ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_grouped_il_peaked_and_flat_softmax(bits):
+    """The grouped matrix-core decode carries softmax weights as a bf16 hi/lo
+    pair: probabilities spanning many orders of magnitude (a peaked softmax,
+    where the small weights must survive the split) and an almost flat one
+    (thousands of near-equal weights summed) stay within the bar."""
+    t_kv, cap, d, group = 5000, 5008, 128, 64
+    for qscale, seed in ((30.0, 1), (1e-3, 2)):
+        cents, perm, idx, _, q = decode_case(seed + 40 * bits, 1, 4, 1, d, t_kv, cap=cap)
+        q = (q.astype(np.float32) * qscale).astype(np.float16)
+        _, packed, sc, ze, il = grouped_case(seed + 50 * bits, 1, 1, t_kv, d, bits, group, cap)
+        out = _hip.decode_attn_grouped_il(t(q), 0.0883883, t(perm), t(cents), t(idx), il, sc, ze,
+                                          bits, group, t_kv, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        vals = O.dequantize_values(packed[0, 0, :t_kv].cpu().numpy().view(np.uint32),
+                                   sc[0, 0, :t_kv].float().cpu().numpy(),
+                                   ze[0, 0, :t_kv].float().cpu().numpy(), d, bits, group)[None, None]
+        ref = O.sdpa(q, idx[:, :, :t_kv], vals, cents, perm, 0.0883883)
+        assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
 
 @pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,bits,group,splits", [
     (1, 8, 2, 128, 0, 40, 2, 64, 0),      # buffer only (no compressed tokens)
@@ -494,6 +514,36 @@ def test_decode_grouped_il_hybrid_buffer(b, hq, hkv, d, t_kv, t_buf, bits, group
                     d, bits, group)
     vals[:, :, t_kv:] = vb[:, :, :t_buf]
     ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,t_q,splits,bdt", [
+    (1, 8, 2, 128, 0, 40, 1, 0, np.float16),       # buffer only (no compressed tokens)
+    (2, 8, 2, 64, 333, 70, 1, 0, np.float16),      # head_dim 64, buffer longer than one chunk
+    (1, 4, 1, 128, 200, 5, 1, 7, np.float32),      # 7 splits sharing 5 tokens, f32 buffer
+    (1, 32, 8, 128, 4096, 128, 1, 0, np.float16),  # config-2 heads, default buffer
+    (1, 8, 2, 128, 300, 64, 4, 3, np.float16),     # prefill rows, causal across the buffer
+])
+def test_decode_il8_hybrid_buffer(b, hq, hkv, d, t_kv, t_buf, t_q, splits, bdt):
+    """ss_decode_attn_il8_hybrid: compressed fp16 tokens (interleaved) plus a
+    token-major buffer in one softmax equals the two-pass oracle over both
+    (causal rows see the buffer up to their own position)."""
+    cap = max(((t_kv + 7) // 8) * 8, 8)
+    cents, perm, idx, vals, q = decode_case(t_kv + t_buf + 3, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(t_buf + 1)
+    kb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(bdt)
+    vb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(bdt)
+    scale = 1.0 / np.sqrt(d)
+    causal = t_q > 1
+    out = _hip.decode_attn_il8(t(q), scale, t(perm), t(cents), t(idx), to_il8(vals, cap), t_kv,
+                               causal=causal, q_offset=t_kv + t_buf - t_q if causal else 0,
+                               out_dtype=torch.float32, n_splits=splits, buf_keys=t(kb),
+                               buf_values=t(vb), buf_len=t_buf)
+    torch.cuda.synchronize()
+    vals_all = np.concatenate([vals[:, :, :t_kv].astype(np.float64),
+                               vb[:, :, :t_buf].astype(np.float64)], axis=2)
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals_all,
+                          mask="causal" if causal else None)
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
 
 

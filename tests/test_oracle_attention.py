@@ -187,6 +187,37 @@ def test_sdpa_two_pass_buffer_scores_use_original_basis():
     assert np.abs(out[0, 0] - ref).max() < 1e-12
 
 
+def test_sdpa_two_pass_rotation_scores_as_reconstructed_keys():
+    """Rotated codecs: codec-space queries are q_scaled @ R^T
+    (attention.py:229-230), so a compressed score is q . (C[idx] R), the
+    query against the key reconstructed in the original basis (pinned
+    against attention over those keys written out, so R in place of R^T
+    fails for a non-symmetric rotation); buffered keys stay in the original
+    basis.  A permutation matrix as R gives the permutation path."""
+    rng = np.random.default_rng(33)
+    b_, hq, hkv, d, t, tb = 1, 2, 1, 64, 30, 6
+    rot, _ = np.linalg.qr(rng.standard_normal((d, d)))
+    rot = rot.astype(np.float32)
+    cents = rng.standard_normal((8, 32, 8)).astype(np.float32)
+    idx = rng.integers(0, 32, (b_, hkv, t, 8)).astype(np.uint8)
+    kb = rng.standard_normal((b_, hkv, tb, d)).astype(np.float16)
+    vals = rng.standard_normal((b_, hkv, t + tb, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, 1, d)).astype(np.float16)
+    out = O.sdpa_two_pass(q, 0.2, None, cents, idx, kb, vals, rotation=rot)
+    k_orig = O.dequantize_blockvq(idx[0, 0], cents).astype(np.float64) @ rot.astype(np.float64)
+    keys = np.concatenate([k_orig, kb[0, 0].astype(np.float64)])
+    qs = O.scale_query(q, 0.2)[0].astype(np.float64)
+    for h in range(hq):
+        ref = explicit_attention(qs[h], keys, vals[0, 0])
+        assert np.abs(out[0, h] - ref).max() < 1e-5
+    perm = rng.permutation(d).astype(np.int32)
+    pmat = np.zeros((d, d), np.float32)
+    pmat[np.arange(d), perm] = 1.0  # (q @ P^T)[j] = q[perm[j]]
+    a = O.sdpa_two_pass(q, 0.2, perm, cents, idx, kb, vals)
+    b = O.sdpa_two_pass(q, 0.2, None, cents, idx, kb, vals, rotation=pmat)
+    assert np.abs(a - b).max() < 1e-12
+
+
 def test_sdpa_heavy_blocks_score_as_exact_key_dots():
     """Mixed-precision extension: with the heavy blocks' key dims kept in
     fp16, each compressed score is q . k_hat where k_hat takes the centroids
