@@ -2041,6 +2041,345 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 }
 
 // ---------------------------------------------------------------------------
+// SunShape-value decode on the matrix cores: head_dim 128, value block_dim 4,
+// at most 256 value centroids, four query rows per column.  Scores as in
+// decode_attn_kernel (fp32 query x centroid LUT in LDS, built here on the
+// vector ALUs, plus exact dot products over fp16 heavy-block key dims when
+// NH8 > 0, NH8*8 of them).  P.V runs as O[row][dim] = sum_t P[row][t] V[t][dim]
+// on v_mfma_f32_16x16x16f16 with P entering as fp16 hi/lo rows of p * 2^15
+// (rows 0-3 hi, 4-7 lo, as in VIl8) and V gathered from the value codebook
+// staged in LDS as fp16: the B operand of lane l (4 consecutive tokens of one
+// dim) is four 16-bit LDS reads at (codebook row of the token's index byte),
+// so no value is converted or multiplied on the vector ALUs.  MFMA column n
+// of n-tile nt holds codec dim ((8*(n/4) + nt)*4 + n%4): a lane's eight
+// n-tiles read index bytes 8*(n/4) .. +7 of a token, one 8-byte load per
+// token.  There is no loader wave and no LDS ring: each wave loads its next
+// 64-token unit (index rows, heavy keys, value indices) into registers while
+// it computes the current one (that load is clamped to the split's last unit
+// rather than skipped, so the loop stays straight-line and the wait for a
+// unit's data is a plain vmcnt).  The workgroup writes its split's
+// (m, l, acc) partials, or with one split the fp32 rows, in the codec basis,
+// for the transformed-basis merge.
+// ---------------------------------------------------------------------------
+constexpr int kSvNB = 16;    // key blocks of head_dim 128
+constexpr int kSvNBV = 32;   // value blocks of block_dim 4
+constexpr int kSvD = 128;
+constexpr int kSvWaves = 8;
+constexpr int kSvVcbBytes = kSvNBV * 256 * 8;  // fp16 [value block][256][4], at LDS offset 0
+constexpr int kSvLutBytes = kSvNB * 256 * 16;  // float4 (4 rows) [key block][256]
+constexpr int kSvQhBytes = 64 * 16;            // float4 (4 rows) [heavy dim]
+constexpr int kSvPstBytes = kSvWaves * 8 * kPStride * 2;
+constexpr int kSvLdsBytes = kSvVcbBytes + kSvLutBytes + kSvQhBytes + kSvPstBytes;
+static_assert(kSvLdsBytes <= kLdsMax, "SunShape-value MFMA LDS budget");
+static_assert(kSvVcbBytes <= 65536, "value codebook addressed with 16-bit LDS offsets");
+
+template <int NH8>
+struct SvUnit {
+    uint4 k;                          // key index row of token t0 + lane
+    uint4 kh[NH8 > 0 ? NH8 : 1];      // its heavy key dims (fp16)
+    uint2 vi[16];                     // value index bytes 8q..8q+7 of tokens 16ks + 4g + i
+};
+
+template <int NH8>
+__global__ void __launch_bounds__(kSvWaves * kWave)
+    sunv_mfma_kernel(DecodeCommon c, typename VSunV<128, 4>::Args va) {
+    constexpr int NC = kSvWaves, TH = NC * kWave, R = kMfmaRows, D = kSvD;
+    extern __shared__ __align__(16) float4 smem4[];
+    char *smem = reinterpret_cast<char *>(smem4);
+    uint2 *vcb = reinterpret_cast<uint2 *>(smem);                            // [32][256]
+    float4 *lut4 = reinterpret_cast<float4 *>(smem + kSvVcbBytes);           // [16][256]
+    float4 *qh4 = reinterpret_cast<float4 *>(smem + kSvVcbBytes + kSvLutBytes);  // [64]
+    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + kSvVcbBytes + kSvLutBytes + kSvQhBytes);
+    const lds_t<_Float16> *vh = (const lds_t<_Float16> *)smem;
+    const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)(smem + kSvVcbBytes);
+    const lds_t<f32x4> *qh_l = (const lds_t<f32x4> *)(smem + kSvVcbBytes + kSvLutBytes);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, l16 = lane & 15;
+    const int col = blockIdx.y;
+    const int split = blockIdx.x;
+    const int rg = col % c.n_rg;
+    const int kvh = (col / c.n_rg) % c.n_kv_heads;
+    const int64_t bb = col / (c.n_rg * c.n_kv_heads);
+    const int64_t bh = bb * c.n_kv_heads + kvh;
+    auto row_off = [&](int r) -> int64_t {
+        const int64_t gr = (int64_t)rg * R + r;
+        const int64_t rr = gr / c.t_q, tq = gr - rr * c.t_q;
+        return ((bb * c.n_q_heads + kvh * c.rep + rr) * c.t_q + tq) * D;
+    };
+    auto row_ok = [&](int r) -> bool { return (int64_t)rg * R + r < c.rows_total; };
+
+    // 1. query rows round_to(q_dtype, q * scale), permuted (attention.py:208,
+    //    228), staged in the P area; heavy blocks of the codec
+    float *qp = reinterpret_cast<float *>(pst);  // [R][D], 2 KB of the P area
+    for (int i = tid; i < R * D; i += TH) {
+        const int r = i / D, j = i - r * D;
+        float x = 0.f;
+        if (row_ok(r)) {
+            const int src = c.perm ? min(max(c.perm[j], 0), D - 1) : j;
+            x = round_to(c.q_dtype, load_as_f32(c.q, c.q_dtype, row_off(r) + src) * c.scale);
+        }
+        qp[i] = x;
+    }
+    uint32_t heavy_blocks = 0;
+    for (int j = 0; j < NH8 * 8; ++j)
+        heavy_blocks |= 1u << (min(max(va.heavy_dims[j], 0), D - 1) / kBlockDim);
+    // value codebook -> fp16 (rounded to nearest), entries past n_centroids zero
+    for (int i = tid; i < kSvNBV * 256; i += TH) {
+        const int vb = i >> 8, cc = i & 255;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (cc < va.n_centroids)
+            v = *reinterpret_cast<const float4 *>(va.cb + ((int64_t)vb * va.n_centroids + cc) * 4);
+        const __half2 lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
+        vcb[i] = make_uint2(*reinterpret_cast<const uint32_t *>(&lo),
+                            *reinterpret_cast<const uint32_t *>(&hi));
+    }
+    __syncthreads();
+    // 2. LUT[b][cc] = the 4 rows' q'[b-block] . C[b][cc] in log2 units
+    //    (kernels.py:178-190); heavy blocks score from their fp16 keys: 0
+    for (int e = tid; e < kSvNB * c.n_centroids; e += TH) {
+        const int b = e / c.n_centroids, cc = e - b * c.n_centroids;
+        const float4 *cp = reinterpret_cast<const float4 *>(c.centroids + (int64_t)e * kBlockDim);
+        const float4 c0 = cp[0], c1 = cp[1];
+        float dt[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float *qr = qp + r * D + b * kBlockDim;
+            float dot = qr[0] * c0.x;
+            dot = fmaf(qr[1], c0.y, dot);
+            dot = fmaf(qr[2], c0.z, dot);
+            dot = fmaf(qr[3], c0.w, dot);
+            dot = fmaf(qr[4], c1.x, dot);
+            dot = fmaf(qr[5], c1.y, dot);
+            dot = fmaf(qr[6], c1.z, dot);
+            dot = fmaf(qr[7], c1.w, dot);
+            dt[r] = ((heavy_blocks >> b) & 1u) ? 0.f : dot * kLog2e;
+        }
+        lut4[b * 256 + cc] = make_float4(dt[0], dt[1], dt[2], dt[3]);
+    }
+    if constexpr (NH8 > 0)
+        for (int j = tid; j < NH8 * 8; j += TH) {
+            const int hd = min(max(va.heavy_dims[j], 0), D - 1);
+            qh4[j] = make_float4(qp[hd] * kLog2e, qp[D + hd] * kLog2e, qp[2 * D + hd] * kLog2e,
+                                 qp[3 * D + hd] * kLog2e);
+        }
+    __syncthreads();  // LUT, codebook and heavy query staged; the P area is free
+
+    // 3. this split's 64-token units, wave wv taking units wv, wv + NC, ...
+    const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
+    const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
+    const int n_units = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
+    const int64_t t_last = max(t_end - 1, (int64_t)0);
+    const uint8_t *idx_head = c.idx + bh * c.cap * kSvNB;
+    const int64_t vrow0 = bh * c.cap;
+    const int q4 = l16 >> 2, w4 = l16 & 3;
+    // halves: codebook row (8*q4 + nt, byte), dim w4
+    const int vbase = (8 * q4) * 256 * 4 + w4;
+
+    int64_t lim[R];
+    int64_t lim_min = INT64_MAX;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t gr = (int64_t)rg * R + r;
+        lim[r] = !row_ok(r) ? -1 : c.causal ? c.q_offset + (gr % c.t_q) : INT64_MAX;
+        lim_min = min(lim_min, lim[r]);
+    }
+
+    // token offsets within the head are 32-bit (cap < 2^26 checked on the
+    // host), so each load is a uniform base plus one 32-bit lane offset
+    const char *kidx_b = reinterpret_cast<const char *>(idx_head);
+    const char *kh_b = reinterpret_cast<const char *>(va.kheavy + (NH8 > 0 ? vrow0 * (NH8 * 8) : 0));
+    const char *vi_b = reinterpret_cast<const char *>(va.idx + vrow0 * kSvNBV);
+    const uint32_t t_last32 = (uint32_t)t_last;
+    auto at = [](const char *base, uint32_t byte_off) { return base + byte_off; };
+    auto load_unit = [&](SvUnit<NH8> &U, int u) {
+        const uint32_t t0 = (uint32_t)t_beg + (uint32_t)u * kWave;
+        const uint32_t tk = min(t0 + (uint32_t)lane, t_last32);
+        U.k = *reinterpret_cast<const uint4 *>(at(kidx_b, tk * kSvNB));
+        if constexpr (NH8 > 0) {
+#pragma unroll
+            for (int j = 0; j < NH8; ++j)
+                U.kh[j] = *reinterpret_cast<const uint4 *>(at(kh_b, tk * (NH8 * 16) + j * 16));
+        }
+        const uint32_t tg = t0 + 4u * g;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                U.vi[ks * 4 + i] = *reinterpret_cast<const uint2 *>(
+                    at(vi_b, min(tg + 16u * ks + i, t_last32) * kSvNBV + 8u * q4));
+    };
+
+    float m[R], lsum[R];
+    f32x4 acc[8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -1e30f;
+        lsum[r] = 0.f;
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    _Float16 *pw = pst + wv * 8 * kPStride;
+
+    auto compute_unit = [&](const SvUnit<NH8> &cur, int u) {
+        const int64_t t0 = t_beg + (int64_t)u * kWave;
+        const int n_in = (int)min(t_end - t0, (int64_t)kWave);
+        // scores: the 16 LUT reads in flight at once, then a tree sum
+        f32x4 e[kSvNB];
+#pragma unroll
+        for (int b = 0; b < kSvNB; ++b) {
+            const uint32_t w = b < 4 ? cur.k.x : b < 8 ? cur.k.y : b < 12 ? cur.k.z : cur.k.w;
+            e[b] = lut_l[b * 256 + __builtin_amdgcn_ubfe(w, (b & 3) * 8, 8)];
+        }
+#pragma unroll
+        for (int w = 1; w < kSvNB; w *= 2)
+#pragma unroll
+            for (int b = 0; b < kSvNB; b += 2 * w) e[b] += e[b + w];
+        f32x4 s4 = e[0];
+        if constexpr (NH8 > 0) {
+#pragma unroll
+            for (int j = 0; j < NH8; ++j) {
+                float kx[8];
+                unpack16<__half>(cur.kh[j], kx);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s4 += qh_l[j * 8 + i] * kx[i];
+            }
+        }
+        float sc[R] = {s4.x, s4.y, s4.z, s4.w};
+        bool moved = true;
+        if (n_in == kWave && t0 + (kWave - 1) <= lim_min) {
+            uint64_t above = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r]);
+            moved = above != 0;
+        } else {
+            const bool kok = lane < n_in;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int lim_rel = (int)max(min(lim[r] - t0, (int64_t)kWave), (int64_t)-1);
+                sc[r] += (kok && lane <= lim_rel) ? 0.f : -INFINITY;
+            }
+        }
+        float corr[R], p[R];
+        if (moved) {
+            float tmax[R];
+            wave_max4_dpp(sc, tmax);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float mn = fmaxf(m[r], tmax[r]);
+                corr[r] = fast_exp2(m[r] - mn);
+                p[r] = fast_exp2(sc[r] - mn);
+                lsum[r] = fmaf(lsum[r], corr[r], p[r]);
+                m[r] = mn;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                corr[r] = 1.f;
+                p[r] = fast_exp2(sc[r] - m[r]);
+                lsum[r] += p[r];
+            }
+        }
+        // P as fp16 hi/lo rows (A rows 0-3 hi, 4-7 lo, 8-15 zero)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float x = p[r] * kPScale;
+            const _Float16 hi = (_Float16)x;
+            pw[r * kPStride + lane] = hi;
+            pw[(r + 4) * kPStride + lane] = (_Float16)(x - (float)hi);
+        }
+        wave_lds_sync();
+        if (moved) {
+            const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) acc[nt] *= cv4;
+        }
+        const bool a_live = l16 < 8;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            f16x4 a = f16x4{0, 0, 0, 0};
+            if (a_live) a = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 16 * ks + 4 * g);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+                f16x4 bop;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint2 w2 = cur.vi[ks * 4 + i];
+                    const uint32_t byte = __builtin_amdgcn_ubfe(nt < 4 ? w2.x : w2.y, (nt & 3) * 8, 8);
+                    bop[i] = vh[vbase + (int)byte * 4 + nt * 1024];
+                }
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[nt], 0, 0, 0);
+            }
+        }
+        wave_lds_sync();
+    };
+    // two register sets in turn: the next unit's loads are issued before the
+    // current unit is computed
+    SvUnit<NH8> ua, ub;
+    if (wv < n_units) load_unit(ua, wv);
+    for (int u = wv; u < n_units; u += 2 * NC) {
+        load_unit(ub, min(u + NC, n_units - 1));
+        compute_unit(ua, u);
+        if (u + NC >= n_units) break;
+        load_unit(ua, min(u + 2 * NC, n_units - 1));
+        compute_unit(ub, u + NC);
+    }
+
+    // 4. the workgroup combine: waves' (m, l) and (hi, lo) accumulators in
+    //    LDS (over the LUT, which no wave reads any more)
+    {
+        float ls[R];
+        wave_sum4_dpp(lsum, ls);
+#pragma unroll
+        for (int r = 0; r < R; ++r) lsum[r] = ls[r];
+    }
+    __syncthreads();
+    float *wm = reinterpret_cast<float *>(smem + kSvVcbBytes);  // [NC][R]
+    float *wl = wm + NC * R;                                     // [NC][R]
+    float *wa = wl + NC * R;                                     // [NC][2][R][D]
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wm[wv * R + r] = m[r];
+            wl[wv * R + r] = lsum[r];
+        }
+    }
+    if (g < 2) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+            const int d = (8 * q4 + nt) * 4 + w4;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wa[((wv * 2 + g) * R + r) * D + d] = acc[nt][r] * (1.f / kPScale);
+        }
+    }
+    __syncthreads();
+    const int S = c.n_splits;
+    for (int i = tid; i < R * D; i += TH) {
+        const int r = i / D, d = i - r * D;
+        float M = -1e30f;
+#pragma unroll
+        for (int w = 0; w < NC; ++w) M = fmaxf(M, wm[w * R + r]);
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < NC; ++w) {
+            const float f = fast_exp2(wm[w * R + r] - M);
+            L = fmaf(wl[w * R + r], f, L);
+            A = fmaf(wa[((w * 2) * R + r) * D + d] + wa[((w * 2 + 1) * R + r) * D + d], f, A);
+        }
+        if (S == 1) {
+            if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
+        } else {
+            const int64_t slot = ((int64_t)col * S + split) * R + r;
+            c.part_acc[slot * D + d] = A;
+            if (d == 0) *reinterpret_cast<float2 *>(c.part_ml + slot * 2) = make_float2(M, L);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Merge of split-T partials: one workgroup per (group, row).  One wave turns
 // the splits' (m, l) into weights exp2(m_s - M) and the merged l; every thread
 // then streams float4 slices of the accumulators of a subset of splits (loads
@@ -2418,6 +2757,23 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
     if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
     return launch_merge<D>(c, s, st);
+}
+
+template <int NH8>
+static int launch_sunv_mfma(const DecodeCommon &c, const typename VSunV<128, 4>::Args &va,
+                            const DecodeShape &s, hipStream_t st) {
+    auto kern = sunv_mfma_kernel<NH8>;
+    static bool attr_set = false;  // per instantiation
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kSvLdsBytes);
+        if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(sunv mfma)");
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(kSvWaves * kWave), kSvLdsBytes, st, c, va);
+    SS_LAUNCH_CHECK("sunv_mfma_kernel launch");
+    return SS_OK;
 }
 
 template <int D, int R, class VF>
@@ -2858,7 +3214,25 @@ extern "C" int ss_decode_attn_sunshape_v(
                        n_heavy_dims);
         SS_REQUIRE(((uintptr_t)k_heavy % 16) == 0, "heavy keys must be 16-byte aligned");
     }
+    // the matrix-core kernel: head_dim 128, value block_dim 4, four query
+    // rows per column, 0/8/16/32/64 heavy dims, 8-byte aligned value indices
+    const int nh8 = k_heavy ? n_heavy_dims / 8 : 0;
+    const bool sv_mfma = head_dim == 128 && v_block_dim == 4 && ((uintptr_t)v_idx % 8) == 0 &&
+                         cap < (int64_t(1) << 26) &&
+                         (nh8 == 0 || nh8 == 1 || nh8 == 2 || nh8 == 4 || nh8 == 8);
     auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
+        if (sv_mfma && s.R == kMfmaRows) {
+            const typename VSunV<128, 4>::Args va{v_idx, v_centroids, v_n_centroids,
+                                                  static_cast<const __half *>(k_heavy),
+                                                  heavy_dims, k_heavy ? n_heavy_dims : 0};
+            switch (nh8) {
+                case 1: return launch_sunv_mfma<1>(c, va, s, st);
+                case 2: return launch_sunv_mfma<2>(c, va, s, st);
+                case 4: return launch_sunv_mfma<4>(c, va, s, st);
+                case 8: return launch_sunv_mfma<8>(c, va, s, st);
+                default: return launch_sunv_mfma<0>(c, va, s, st);
+            }
+        }
 #define SS_SUNV(DD, BB)                                                     \
     {                                                                       \
         typename VSunV<DD, BB>::Args va{v_idx, v_centroids, v_n_centroids,    \

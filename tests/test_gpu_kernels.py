@@ -626,6 +626,8 @@ def test_decode_turboquant_with_buffer(b, hq, hkv, d, t_kv, t_buf, t_q, bits, sp
     (2, 8, 2, 128, 700, 128, 1, 8, 256, "perm", 0),     # block_dim 8, with a buffer
     (1, 8, 2, 64, 513, 0, 1, 4, 100, "rot", 3),         # head_dim 64, rotated codec, 100 centroids
     (2, 6, 2, 128, 300, 20, 5, 8, 256, "rot", 1),       # prefill rows, causal across the buffer
+    (1, 8, 2, 128, 999, 0, 1, 4, 100, "rot", 5),        # matrix-core path: ragged T, 100 centroids
+    (2, 8, 2, 128, 64, 7, 3, 4, 256, "perm", 0),        # matrix-core path: one unit, causal rows
 ])
 def test_decode_sunshape_v_matches_oracle(b, hq, hkv, d, t_kv, t_buf, t_q, bd, vnc, transform,
                                           splits):
@@ -713,6 +715,8 @@ def test_kmeans_blocks_matches_oracle(bd, n, k):
 @pytest.mark.parametrize("b,hq,hkv,t_kv,t_buf,t_q,n_heavy,splits", [
     (2, 32, 8, 1500, 0, 1, 4, 0),    # config-5 shape: 4 heavy blocks (32 fp16 dims)
     (1, 8, 2, 333, 40, 3, 1, 2),     # one heavy block, buffer, causal prefill rows
+    (1, 8, 2, 700, 0, 1, 2, 0),      # two heavy blocks
+    (1, 4, 1, 257, 16, 1, 8, 3),     # eight heavy blocks (64 dims), a partial last unit
 ])
 def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, splits):
     """Mixed-precision keys with their heavy blocks in fp16: the fused decode
