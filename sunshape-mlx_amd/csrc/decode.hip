@@ -2048,12 +2048,18 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 // NH8 > 0, NH8*8 of them).  P.V runs as O[row][dim] = sum_t P[row][t] V[t][dim]
 // on v_mfma_f32_16x16x16f16 with P entering as fp16 hi/lo rows of p * 2^15
 // (rows 0-3 hi, 4-7 lo, as in VIl8) and V gathered from the value codebook
-// staged in LDS as fp16: the B operand of lane l (4 consecutive tokens of one
-// dim) is four 16-bit LDS reads at (codebook row of the token's index byte),
-// so no value is converted or multiplied on the vector ALUs.  MFMA column n
-// of n-tile nt holds codec dim ((8*(n/4) + nt)*4 + n%4): a lane's eight
-// n-tiles read index bytes 8*(n/4) .. +7 of a token, one 8-byte load per
-// token.  There is no loader wave and no LDS ring: each wave loads its next
+// staged in LDS as fp16 by transposing reads (ds_read_b64_tr_b16): in each
+// 16-lane group lane j reads the 4-dim codebook row of (token j/4, value
+// block 8*(j%4) + nt), and the read hands lane i the column i of that 4 x 16
+// block, i.e. dim i%4 of block 8*(i/4) + nt for the 4 tokens -- the B operand,
+// with no value converted, packed or multiplied on the vector ALUs.  MFMA
+// column n of n-tile nt therefore holds codec dim ((8*(n/4) + nt)*4 + n%4),
+// and a lane's eight n-tiles read index bytes 8*(n%4) .. +7 of one token, an
+// 8-byte load per 16 tokens.  The heavy-dim dot products run on
+// v_mfma_f32_4x4x4f16 (16 blocks of 4 tokens: A = the 4 query rows' heavy
+// dims, B = each token's own fp16 heavy dims, D = the token's 4 row scores in
+// its own lane), with an fp16 hi/lo split of the query unless it is already
+// fp16.  There is no loader wave and no LDS ring: each wave loads its next
 // 64-token unit (index rows, heavy keys, value indices) into registers while
 // it computes the current one (that load is clamped to the split's last unit
 // rather than skipped, so the loop stays straight-line and the wait for a
@@ -2067,17 +2073,26 @@ constexpr int kSvD = 128;
 constexpr int kSvWaves = 8;
 constexpr int kSvVcbBytes = kSvNBV * 256 * 8;  // fp16 [value block][256][4], at LDS offset 0
 constexpr int kSvLutBytes = kSvNB * 256 * 16;  // float4 (4 rows) [key block][256]
-constexpr int kSvQhBytes = 64 * 16;            // float4 (4 rows) [heavy dim]
 constexpr int kSvPstBytes = kSvWaves * 8 * kPStride * 2;
-constexpr int kSvLdsBytes = kSvVcbBytes + kSvLutBytes + kSvQhBytes + kSvPstBytes;
+constexpr int kSvLdsBytes = kSvVcbBytes + kSvLutBytes + kSvPstBytes;
 static_assert(kSvLdsBytes <= kLdsMax, "SunShape-value MFMA LDS budget");
 static_assert(kSvVcbBytes <= 65536, "value codebook addressed with 16-bit LDS offsets");
+
+// ds_read_b64_tr_b16 at LDS byte offset `off` of the dynamic LDS block: in
+// each 16-lane group, lane j reads 4 halves; lane i receives column i of the
+// 4 x 16 block they form (row r from lane 4r + i/4, element i%4).
+__device__ __forceinline__ f16x4 ds_read_tr16(const char *lds_base, uint32_t off) {
+    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf16x4;
+    typedef __attribute__((address_space(3))) hf16x4 lhf16x4;
+    lhf16x4 *p = (lhf16x4 *)(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base)) + off);
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(p));
+}
 
 template <int NH8>
 struct SvUnit {
     uint4 k;                          // key index row of token t0 + lane
     uint4 kh[NH8 > 0 ? NH8 : 1];      // its heavy key dims (fp16)
-    uint2 vi[16];                     // value index bytes 8q..8q+7 of tokens 16ks + 4g + i
+    uint2 vi[4];                      // value index bytes 8*(l16%4) .. +7 of token 16ks + 4g + l16/4
 };
 
 template <int NH8>
@@ -2088,11 +2103,8 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
     char *smem = reinterpret_cast<char *>(smem4);
     uint2 *vcb = reinterpret_cast<uint2 *>(smem);                            // [32][256]
     float4 *lut4 = reinterpret_cast<float4 *>(smem + kSvVcbBytes);           // [16][256]
-    float4 *qh4 = reinterpret_cast<float4 *>(smem + kSvVcbBytes + kSvLutBytes);  // [64]
-    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + kSvVcbBytes + kSvLutBytes + kSvQhBytes);
-    const lds_t<_Float16> *vh = (const lds_t<_Float16> *)smem;
+    _Float16 *pst = reinterpret_cast<_Float16 *>(smem + kSvVcbBytes + kSvLutBytes);
     const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)(smem + kSvVcbBytes);
-    const lds_t<f32x4> *qh_l = (const lds_t<f32x4> *)(smem + kSvVcbBytes + kSvLutBytes);
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -2159,13 +2171,23 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
         }
         lut4[b * 256 + cc] = make_float4(dt[0], dt[1], dt[2], dt[3]);
     }
-    if constexpr (NH8 > 0)
-        for (int j = tid; j < NH8 * 8; j += TH) {
-            const int hd = min(max(va.heavy_dims[j], 0), D - 1);
-            qh4[j] = make_float4(qp[hd] * kLog2e, qp[D + hd] * kLog2e, qp[2 * D + hd] * kLog2e,
-                                 qp[3 * D + hd] * kLog2e);
-        }
-    __syncthreads();  // LUT, codebook and heavy query staged; the P area is free
+    // A operands of the heavy-dim products: query row lane%4, heavy dims
+    // 4kk .. 4kk+3, as fp16 hi and (scaled by 2^11) lo parts
+    const bool qsplit = c.q_dtype != SS_F16;
+    f16x4 ah[NH8 > 0 ? 2 * NH8 : 1], al[NH8 > 0 ? 2 * NH8 : 1];
+    if constexpr (NH8 > 0) {
+#pragma unroll
+        for (int kk = 0; kk < 2 * NH8; ++kk)
+#pragma unroll
+            for (int e2 = 0; e2 < 4; ++e2) {
+                const int hd = min(max(va.heavy_dims[4 * kk + e2], 0), D - 1);
+                const float x = qp[(lane & 3) * D + hd];
+                const _Float16 h = (_Float16)x;
+                ah[kk][e2] = h;
+                al[kk][e2] = (_Float16)((x - (float)h) * kSplitScale);
+            }
+    }
+    __syncthreads();  // LUT and codebook staged, query read; the P area is free
 
     // 3. this split's 64-token units, wave wv taking units wv, wv + NC, ...
     const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
@@ -2175,8 +2197,9 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
     const uint8_t *idx_head = c.idx + bh * c.cap * kSvNB;
     const int64_t vrow0 = bh * c.cap;
     const int q4 = l16 >> 2, w4 = l16 & 3;
-    // halves: codebook row (8*q4 + nt, byte), dim w4
-    const int vbase = (8 * q4) * 256 * 4 + w4;
+    // bytes: codebook row (block 8*w4 + nt, byte) this lane reads for the
+    // transposing gather (nt * 2048 goes in the instruction's offset)
+    const uint32_t vbase = (uint32_t)(8 * w4) * 256 * 8;
 
     int64_t lim[R];
     int64_t lim_min = INT64_MAX;
@@ -2203,13 +2226,11 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
             for (int j = 0; j < NH8; ++j)
                 U.kh[j] = *reinterpret_cast<const uint4 *>(at(kh_b, tk * (NH8 * 16) + j * 16));
         }
-        const uint32_t tg = t0 + 4u * g;
+        const uint32_t tg = t0 + 4u * g + (uint32_t)q4;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                U.vi[ks * 4 + i] = *reinterpret_cast<const uint2 *>(
-                    at(vi_b, min(tg + 16u * ks + i, t_last32) * kSvNBV + 8u * q4));
+            U.vi[ks] = *reinterpret_cast<const uint2 *>(
+                at(vi_b, min(tg + 16u * ks, t_last32) * kSvNBV + 8u * w4));
     };
 
     float m[R], lsum[R];
@@ -2239,13 +2260,27 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
             for (int b = 0; b < kSvNB; b += 2 * w) e[b] += e[b + w];
         f32x4 s4 = e[0];
         if constexpr (NH8 > 0) {
+            // heavy dims on the matrix cores: D[row][token lane] in this lane
+            f32x4 hs = f32x4{0.f, 0.f, 0.f, 0.f}, hl = hs;
 #pragma unroll
             for (int j = 0; j < NH8; ++j) {
-                float kx[8];
-                unpack16<__half>(cur.kh[j], kx);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) s4 += qh_l[j * 8 + i] * kx[i];
+                const uint4 kv = cur.kh[j];
+                const f16x4 b0 = __builtin_bit_cast(f16x4, make_uint2(kv.x, kv.y));
+                const f16x4 b1 = __builtin_bit_cast(f16x4, make_uint2(kv.z, kv.w));
+                hs = __builtin_amdgcn_mfma_f32_4x4x4f16(ah[2 * j], b0, hs, 0, 0, 0);
+                hs = __builtin_amdgcn_mfma_f32_4x4x4f16(ah[2 * j + 1], b1, hs, 0, 0, 0);
             }
+            if (qsplit) {
+#pragma unroll
+                for (int j = 0; j < NH8; ++j) {
+                    const uint4 kv = cur.kh[j];
+                    const f16x4 b0 = __builtin_bit_cast(f16x4, make_uint2(kv.x, kv.y));
+                    const f16x4 b1 = __builtin_bit_cast(f16x4, make_uint2(kv.z, kv.w));
+                    hl = __builtin_amdgcn_mfma_f32_4x4x4f16(al[2 * j], b0, hl, 0, 0, 0);
+                    hl = __builtin_amdgcn_mfma_f32_4x4x4f16(al[2 * j + 1], b1, hl, 0, 0, 0);
+                }
+            }
+            s4 += (hs + hl * (1.f / kSplitScale)) * kLog2e;
         }
         float sc[R] = {s4.x, s4.y, s4.z, s4.w};
         bool moved = true;
@@ -2303,13 +2338,9 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
             if (a_live) a = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 16 * ks + 4 * g);
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                f16x4 bop;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint2 w2 = cur.vi[ks * 4 + i];
-                    const uint32_t byte = __builtin_amdgcn_ubfe(nt < 4 ? w2.x : w2.y, (nt & 3) * 8, 8);
-                    bop[i] = vh[vbase + (int)byte * 4 + nt * 1024];
-                }
+                const uint2 w2 = cur.vi[ks];
+                const uint32_t byte = __builtin_amdgcn_ubfe(nt < 4 ? w2.x : w2.y, (nt & 3) * 8, 8);
+                const f16x4 bop = ds_read_tr16(smem, vbase + byte * 8 + nt * 2048);
                 acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[nt], 0, 0, 0);
             }
         }

@@ -772,6 +772,40 @@ def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, s
     assert rel_err(out0.cpu().numpy(), ref0) <= REL_TOL
 
 
+@pytest.mark.parametrize("q_dtype", [np.float32, "bf16"])
+def test_decode_sunshape_v_heavy_blocks_wide_queries(q_dtype):
+    """bf16 and fp32 queries on the matrix-core SunShape-value decode: the
+    heavy-dim products take the query as an fp16 hi/lo pair (exact for fp32
+    only to ~22 bits, within the bar), the LUT takes it in fp32."""
+    b, hq, hkv, t_kv, d, bd = 1, 8, 2, 900, 128, 4
+    cap = 912
+    cents, perm, idx, _, q16 = decode_case(95, b, hq, hkv, d, t_kv, 1, cap)
+    rng = np.random.default_rng(96)
+    q = (q16.astype(np.float32) * 1.3 + 1e-3 * rng.standard_normal(q16.shape)).astype(np.float32)
+    hd = np.concatenate([np.arange(x * 8, x * 8 + 8) for x in (1, 6, 9, 12)]).astype(np.int32)
+    kh = np.zeros((b, hkv, cap, hd.size), np.float16)
+    kh[:, :, :t_kv] = rng.standard_normal((b, hkv, t_kv, hd.size)).astype(np.float16)
+    v_cents = rng.standard_normal((d // bd, 256, bd)).astype(np.float32)
+    v_idx = rng.integers(0, 256, (b, hkv, cap, d // bd)).astype(np.uint8)
+    vperm = rng.permutation(d).astype(np.int32)
+    inv = O.invert_permutation(vperm)
+    m = np.zeros((d, d), np.float32)
+    m[inv, np.arange(d)] = 1.0
+    # bf16 queries come pre-scaled (scale 1): q * 1 rounds to itself in bf16
+    # and in the float32 the oracle sees
+    qt, scale = (t(q), 0.088) if q_dtype == np.float32 else (t(q * 0.088).to(torch.bfloat16), 1.0)
+    qref = qt.float().cpu().numpy()
+    out = _hip.decode_attn_sunshape_v(qt, scale, t(perm), t(cents), t(idx), t(v_idx), t(v_cents),
+                                      t(m), t_kv, out_dtype=torch.float32, k_heavy=t(kh),
+                                      heavy_dims=t(hd))
+    torch.cuda.synchronize()
+    vals = np.stack([np.stack([O.dequantize_blockvq(v_idx[0, hi, :t_kv], v_cents, inv)
+                               for hi in range(hkv)])])
+    ref = O.sdpa_two_pass(qref, scale, perm, cents, idx[:, :, :t_kv], None, vals,
+                          heavy_keys=kh[:, :, :t_kv], heavy_dims=hd)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
 def test_transformed_decode_leaves_split_counters_zero():
     """Regression: a single-split TurboQuant / SunShape-value decode keeps its
     transformed-basis rows clear of the workspace's split counters, so a
