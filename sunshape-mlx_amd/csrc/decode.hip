@@ -2694,7 +2694,9 @@ static int rows_per_group(int64_t rows_total) { return rows_total <= 1 ? 1 : 4; 
 // Kernel families: the VALU kernel (any value layout/dtype, 4 waves per
 // workgroup, 1 or 4 rows) and the MFMA kernel (fp16 values 8-token
 // interleaved, 4 or 8 compute waves plus a loader wave, 4 rows).
-enum DecodeKind { kKindValu = 0, kKindMfma = 1 };
+// kKindSunv: the matrix-core SunShape-value decode (one 136 KB-LDS
+// workgroup per compute unit, eight waves)
+enum DecodeKind { kKindValu = 0, kKindMfma = 1, kKindSunv = 2 };
 constexpr int kMfmaWaves = 4;  // fewest compute waves of an MFMA kernel (tiles per split)
 
 static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int64_t t_kv,
@@ -2705,12 +2707,12 @@ static DecodeShape decode_shape(int64_t batch, int hq, int hkv, int64_t t_q, int
     s.n_rg = (int)((rows + s.R - 1) / s.R);
     s.n_cols = (int)(batch * hkv * s.n_rg);
     const int64_t tiles = (t_kv + kWave - 1) / kWave;
-    const int waves = kind == kKindMfma ? kMfmaWaves : kDecodeWaves;
+    const int waves = kind == kKindMfma ? kMfmaWaves : kind == kKindSunv ? 8 : kDecodeWaves;
     int S = n_splits;
     if (S <= 0) {
         // about one (MFMA) or two (VALU) workgroups per compute unit, each
         // with at least one 64-token tile per wave
-        const int64_t target = (kind == kKindMfma ? 1LL : 2LL) * device_cu_count();
+        const int64_t target = (kind == kKindValu ? 2LL : 1LL) * device_cu_count();
         int64_t want = (target + s.n_cols - 1) / s.n_cols;
         const int64_t cap = tiles / waves;
         if (want > cap) want = cap;
@@ -3121,7 +3123,7 @@ static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq,
                               int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
                               int causal, int64_t q_offset, void *out, int out_dtype,
                               void *workspace, size_t workspace_bytes, int n_splits,
-                              void *stream, MainLaunch &&launch_main) {
+                              void *stream, MainLaunch &&launch_main, int kind = kKindValu) {
     SS_REQUIRE(transform && ((uintptr_t)transform % 4) == 0,
                "null or misaligned transform/rotation matrix");
     SS_REQUIRE(t_buf >= 0, "negative buffer length");
@@ -3132,7 +3134,7 @@ static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq,
         SS_REQUIRE(buf_sb >= 0 && buf_sh >= 0 && buf_st >= head_dim,
                    "buffer strides must be non-negative, token stride >= head_dim");
     }
-    const DecodeShape s = decode_shape(batch, hq, hkv, t_q, t_kv, n_splits);
+    const DecodeShape s = decode_shape(batch, hq, hkv, t_q, t_kv, n_splits, kind);
     const DecodeShape sw = with_buffer_slot(s, t_buf);  // partial slots incl. the buffer's
     const int64_t rows = batch * hq * t_q;
     const size_t need = turboquant_ws_bytes(sw, rows, head_dim);
@@ -3279,10 +3281,14 @@ extern "C" int ss_decode_attn_sunshape_v(
         SS_SUNV(64, 8)
 #undef SS_SUNV
     };
+    // the matrix-core kernel's split policy asks no more splits (and so no
+    // more workspace) than the VALU one ss_decode_turboquant_workspace_bytes
+    // sizes for
     return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
                               centroids, n_centroids, idx, cap, t_kv, v_transform, k_buf, v_buf,
                               buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
-                              out_dtype, workspace, workspace_bytes, n_splits, stream, main);
+                              out_dtype, workspace, workspace_bytes, n_splits, stream, main,
+                              sv_mfma ? kKindSunv : kKindValu);
 }
 
 extern "C" int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
