@@ -546,6 +546,14 @@ def run_config5(args) -> int:
         got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
         check = float(np.abs(got - ref).max() / np.abs(ref).max())
 
+    traffic = None  # HBM bytes per layer launch from the committed counter runs
+    tf = os.path.join(ROOT, "profiles", "decode_sunshape_v_config5_traffic.json")
+    if heavy_fp16 and os.path.exists(tf):
+        with open(tf) as f:
+            tr = json.load(f)
+        if tr.get("t_kv") == t_kv and tr.get("batch") == b:
+            traffic = tr.get("hbm_bytes_per_launch")
+
     line = {
         "metric": "28-layer decode step attention µs/step and achieved HBM GB/s (config 5)",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -562,7 +570,8 @@ def run_config5(args) -> int:
                    "t_kv": t_kv, "layers": layers, "splits": splits,
                    "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_per": "one layer's decode launch"},
         "check_max_rel_err_vs_oracle": check,
     }
     print(json.dumps(line), flush=True)
