@@ -256,9 +256,10 @@ def run_prefill(args) -> int:
     attended causally against the cache that holds the same T tokens (u8
     key indices, fp16 values 8-token interleaved), as mlx-lm's prefill does
     after update_and_fetch: sunshape_sdpa(q, cache, scale, mask="causal"),
-    whose fused path is one ss_decode_attn_il8 launch with t_q = T.  Reported
+    whose fused path is one ss_prefill_attn_il8 launch.  Reported
     as µs per prompt and attention TFLOP/s (QK^T and P.V over the causal
-    half, 4 * B * Hq * D * T^2 / 2 flops)."""
+    half, 4 * B * Hq * D * T^2 / 2 flops); the decode-shaped kernel's time on
+    the same prompt is reported beside it."""
     import numpy as np
     import torch
 
@@ -280,20 +281,27 @@ def run_prefill(args) -> int:
     v8 = torch.zeros((b, hkv, t // 8, d, 8), dtype=torch.float16, device=dev)
     hip.append_values_il8(v, v8, 0)
     q = torch.randn((b, hq, t, d), generator=g, device=dev).to(torch.float16)
-    splits, ws_bytes = hip.decode_plan(hip.KIND_IL8, b, hq, hkv, t, d, t, args.splits)
-    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     out = torch.empty((b, hq, t, d), dtype=torch.float16, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
     cb = hip.codebook_f16x2(cents)
-    fn = lib.ss_decode_attn_il8
+    fn = lib.ss_prefill_attn_il8
     argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, t, d, scale, perm.data_ptr(), cb.data_ptr(),
              nb, 256, idx.data_ptr(), v8.data_ptr(), hip.SS_F16, t, t, 1, 0, out.data_ptr(),
-             hip.SS_F16, ws.data_ptr(), ws_bytes, splits, stream)]
+             hip.SS_F16, stream)]
     steps, warmup = max(1, args.steps // 10), max(1, args.warmup // 4)
     us, per = time_launches(fn, argv, steps, warmup, hip)
     flops = 4 * b * hq * d * t * t // 2
     tflops = flops / (us * 1e-6) / 1e12
-    log(f"prefill T={t}: {us:.1f} us/prompt, {tflops:.2f} TFLOP/s (splits={splits})")
+    log(f"prefill T={t}: {us:.1f} us/prompt, {tflops:.2f} TFLOP/s")
+    # the decode-shaped kernel on the same prompt, for comparison
+    splits, ws_bytes = hip.decode_plan(hip.KIND_IL8, b, hq, hkv, t, d, t, args.splits)
+    ws = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    out_dec = torch.empty_like(out)
+    argv_dec = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, t, d, scale, perm.data_ptr(), cb.data_ptr(),
+                 nb, 256, idx.data_ptr(), v8.data_ptr(), hip.SS_F16, t, t, 1, 0,
+                 out_dec.data_ptr(), hip.SS_F16, ws.data_ptr(), ws_bytes, splits, stream)]
+    us_dec, _ = time_launches(lib.ss_decode_attn_il8, argv_dec, max(1, steps // 4), 1, hip)
+    log(f"decode-shaped kernel on the same prompt: {us_dec:.1f} us")
 
     check = None
     if args.cpu_seconds > 0:  # one (KV head, query head) of the last 64 rows vs the oracle
@@ -334,13 +342,14 @@ def run_prefill(args) -> int:
         "data": "synthetic",
         "config": {"workload": f"prefill B=1 Hq=32 Hkv=8 D=128 T_q=T_kv={t} causal, u8 key "
                                "indices, fp16 values (il8), fp16 query/output",
-                   "t": t, "splits": splits, "attention_flops": flops},
+                   "t": t, "attention_flops": flops, "kernel": "ss_prefill_attn_il8"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 5), "traffic": None},
         "per_launch_us": {"mean": round(float(np.mean(per)), 3),
                           "median": round(float(np.median(per)), 3)},
         "sdpa_end_to_end": {"us_per_prompt": round(sdpa_us, 1), "same_output": same,
                             "backend": cache.codec.last_score_backend},
+        "decode_shaped_kernel_us": round(us_dec, 1),
         "check_max_rel_err_vs_oracle": check,
     }
     print(json.dumps(line), flush=True)

@@ -237,6 +237,27 @@ int ss_decode_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q
                               int n_splits, void *stream);
 
 /*
+ * Causal (or unmasked) attention of a prompt's T_q query rows per head
+ * against an ss_decode_attn_il8 cache (same arguments and layouts, no
+ * workspace): the shape of the reference's fused causal kernels at T_q > 1
+ * (kernels.py:303-378; attention.py:244-298 with mask "causal").  Keys are
+ * reconstructed from the prepared split-fp16 codebook (held in LDS) and
+ * Q.K^T and P.V both run on the matrix cores; every workgroup takes
+ * ss_prefill_rows_per_workgroup() query rows of one KV group (its rep query
+ * heads at consecutive positions), so the GQA group size must divide that
+ * number.  head_dim 128, 16 blocks of 8, <= 256 centroids, fp16 values.
+ * Row i of a head (position q_offset + i) sees keys 0 .. q_offset + i when
+ * causal.  Results equal ss_decode_attn_il8's within the decode tolerance.
+ */
+int ss_prefill_rows_per_workgroup(void);
+int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                        int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                        const int32_t *perm, const void *codebook, int n_blocks,
+                        int n_centroids, const uint8_t *idx, const void *values_il8,
+                        int v_dtype, int64_t cap, int64_t t_kv, int causal, int64_t q_offset,
+                        void *out, int out_dtype, void *stream);
+
+/*
  * ss_decode_attn_il8 without a workspace: the same kernel, arguments and
  * result, with its split partials and per-column split counters in a static
  * device array of the library (ss_decode_static_scratch_bytes() = 4 MiB,

@@ -85,6 +85,10 @@ _SIGNATURES = {
         _c_void_p, _c_void_p, _int, _i64, _i64,
         _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
         _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_prefill_rows_per_workgroup": (_int, []),
+    "ss_prefill_attn_il8": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                   _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
+                                   _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p]),
     "ss_decode_attn_il8_noalloc": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                           _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                           _int, _i64, _i64, _int, _i64, _c_void_p, _int, _int,
@@ -613,6 +617,45 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
     if _check_waits:
         check_decode_waits(q.device)
     return out
+
+
+def prefill_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                     codebook: torch.Tensor, n_centroids: int, idx: torch.Tensor,
+                     values_il8: torch.Tensor, t_kv: int, causal: bool = True, q_offset: int = 0,
+                     out: torch.Tensor | None = None,
+                     out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Prompt attention (``ss_prefill_attn_il8``) of queries (B, Hq, T_q,
+    128) against an interleaved fp16 cache: keys reconstructed from the
+    prepared ``codebook`` (:func:`codebook_f16x2`), Q.K^T and P.V on the
+    matrix cores.  Row i of a head sees keys 0 .. q_offset + i when causal."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(values_il8, codebook)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(nb, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    _launched(_attn_stat("sunshape_prefill_attention_mfma", causal), lib.ss_prefill_attn_il8(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+        nb, int(n_centroids), ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv),
+        int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype),
+        stream_handle(q.device)))
+    return out
+
+
+def prefill_supported(n_q_heads: int, n_kv_heads: int, t_q: int, head_dim: int,
+                      n_blocks: int) -> bool:
+    """Whether :func:`prefill_attn_il8` takes this shape and is the better
+    kernel for it (at least one workgroup's worth of positions)."""
+    rows = int(load_library().ss_prefill_rows_per_workgroup())
+    rep = n_q_heads // n_kv_heads
+    return (head_dim == 128 and n_blocks == 16 and rows % rep == 0
+            and t_q >= rows // rep)
 
 
 def decode_attn_il8_noalloc(q: torch.Tensor, scale: float, perm: torch.Tensor | None,

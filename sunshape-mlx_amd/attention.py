@@ -104,6 +104,19 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
                    buf_values=ops["buf_values"][:, :, :nb_].float().contiguous())
     t_kv = cache.compressed_offset if isinstance(cache, HybridSunShapeKVCache) else cache.offset
     kind = ops["kind"]
+    # a prompt (many query rows per head) against an fp16 cache: keys
+    # reconstructed from the codebook, both products on the matrix cores
+    b_, hq, tq, d = queries.shape
+    if not buffered and kind == "il8" and tq > 1 and \
+            _hip.prefill_supported(hq, cache.n_kv_heads, tq, d, codec.n_blocks):
+        try:
+            out = _hip.prefill_attn_il8(q, kscale, perm, codec.kernel_codebook(), codec.n_centroids,
+                                        ops["idx"], ops["values"], t_kv, causal=causal,
+                                        q_offset=q_offset, out_dtype=queries.dtype)
+        except _hip.SunShapeUnsupported:
+            return None
+        codec.last_score_backend = "hip_prefill_mfma"
+        return out
     # the matrix-core decodes without a token buffer: one prepared launch
     # (argument checks, codebook and split plan done once per cache layout)
     if not buffered and kind in ("il8", "grouped_il"):

@@ -1,0 +1,340 @@
+// Causal prefill attention over block-VQ keys and 8-token interleaved fp16
+// values: the prompt's query rows (T_q of them per query head) against the
+// cache that holds them, the shape of the reference's fused causal kernels
+// (kernels.py:303-378) at T_q > 1, reorganised for the matrix cores.
+//
+// A decode kernel builds one query x centroid LUT per 4 query rows and
+// gathers scores from it; for a prompt that means one LUT and one pass over
+// the cache prefix per 4 rows.  Here the keys are reconstructed instead: the
+// prepared split-fp16 codebook (hi + lo * 2^-11 of C * 2^-e, the operand of
+// the decode kernels' LUT build) is copied row-major into LDS once per
+// workgroup, and the scores of 16 tokens x 16 query rows are
+//   S^T[token][row] = sum_k Khat[token][k] * Q'[row][k]
+// on v_mfma_f32_16x16x32_f16: A = the tokens' codebook rows (lane l holds
+// block 4*ks + l/16 of token l%16: one 16-byte LDS read each for hi and lo),
+// B = the query rows (round_to(q_dtype, q * scale), codec-permuted, as
+// registers for the whole kernel; fp16 hi and lo parts unless the query is
+// fp16).  The accumulator of S^T gives lane l the scores of row l%16 for
+// tokens 4*(l/16) .. +3, which is exactly the A operand layout of
+//   O[row][dim] += sum_t P[row][t] * V[t][dim]
+// on v_mfma_f32_16x16x16f16, so the probabilities never leave registers
+// (hi and lo fp16 parts of p * 2^15, two products); B = 4 consecutive tokens
+// of one dim, 8 bytes of the interleaved value layout.
+//
+// A workgroup of kPfWaves waves takes 16 * kPfWaves query rows of one KV
+// group: (rows / rep) consecutive positions of its rep query heads, the
+// heads sharing every key and value read.  Each wave owns 16 rows outright
+// (its own online softmax and accumulators), so there is no split, merge or
+// cross-wave combine.  Causal rows stop at q_offset + position.
+#include "ss_common.hpp"
+
+namespace ss {
+
+namespace {
+
+typedef _Float16 pf_f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfWaves = 8;
+constexpr int kPfRows = 16 * kPfWaves;   // query rows of a workgroup
+constexpr int kPfD = 128;
+constexpr int kPfNB = 16;
+constexpr int kPfRowBytes = 32;          // one codebook row: 8 hi halves, 8 lo halves
+constexpr int kPfLdsBytes = kPfNB * 256 * kPfRowBytes;  // 128 KB
+constexpr float kPfSplit = 2048.f;       // lo parts carry 2^11
+constexpr float kPfPScale = 32768.f;     // p * 2^15 keeps small weights normal in fp16
+
+struct PrefillArgs {
+    const void *q;
+    int q_dtype;
+    int n_q_heads, n_kv_heads, rep;
+    int64_t t_q;
+    float scale;
+    const int32_t *perm;
+    const uint4 *codebook;   // prepared split-fp16 tiles (ss_codebook_f16x2)
+    const float *cb_mul;     // their power-of-two multiplier
+    int nct;                 // centroid tiles of 16
+    const uint8_t *idx;      // [B][Hkv][cap][16]
+    const __half *v8;        // [B][Hkv][cap/8][128][8]
+    int64_t cap, t_kv;
+    int causal;
+    int64_t q_offset;
+    void *out;
+    int out_dtype;
+    int npos;                // positions per workgroup = kPfRows / rep
+    int n_pg;                // position groups
+};
+
+__device__ __forceinline__ float xor_max(float x, int m) {
+    return fmaxf(x, __shfl_xor(x, m));
+}
+
+}  // namespace
+
+__global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillArgs a) {
+    constexpr int TH = kPfWaves * kWave;
+    extern __shared__ __align__(16) float4 pf_smem[];
+    char *lds = reinterpret_cast<char *>(pf_smem);
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, l16 = lane & 15;
+    // the longest causal ranges first: position groups in reverse order
+    const int pg = a.n_pg - 1 - (int)blockIdx.x;
+    const int64_t bh = blockIdx.y;
+    const int64_t bb = bh / a.n_kv_heads;
+    const int kvh = (int)(bh - bb * a.n_kv_heads);
+
+    // 1. the prepared codebook, row-major: row (block, centroid) at
+    //    (block * 256 + centroid) * 32 bytes, hi then lo.  Tile t = (bg, ct)
+    //    holds 64 lanes' rows: block bg*4 + l/16, centroid ct*16 + l%16.
+    for (int i = tid; i < 4 * a.nct * kWave; i += TH) {
+        const int t = i >> 6, l = i & 63, bg = t / a.nct, ct = t - bg * a.nct;
+        const uint4 hi = a.codebook[(int64_t)t * 2 * kWave + l];
+        const uint4 lo = a.codebook[(int64_t)t * 2 * kWave + kWave + l];
+        uint4 *d = reinterpret_cast<uint4 *>(lds + ((bg * 4 + (l >> 4)) * 256 + ct * 16 + (l & 15)) *
+                                                       kPfRowBytes);
+        d[0] = hi;
+        d[1] = lo;
+    }
+
+    // 2. this lane's query row (the S^T column l%16 of wave wv): B operands
+    //    of the 4 k-steps, dims 32*ks + 8*g .. +7, codec-permuted
+    const int r = wv * 16 + l16;
+    const int p = r / a.rep, h = r - p * a.rep;
+    const int64_t pos = (int64_t)pg * a.npos + p;
+    const bool rok = pos < a.t_q;
+    const int64_t qoff = ((bb * a.n_q_heads + (int64_t)kvh * a.rep + h) * a.t_q + (rok ? pos : 0)) *
+                         kPfD;
+    pf_f16x8 qh[4], ql[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int j = 32 * ks + 8 * g + e;
+            const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
+            const float x =
+                rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
+            const _Float16 hx = (_Float16)x;
+            qh[ks][e] = hx;
+            ql[ks][e] = (_Float16)((x - (float)hx) * kPfSplit);
+        }
+    const bool qsplit = a.q_dtype != SS_F16;
+    __syncthreads();
+
+    const float mul = *a.cb_mul * kLog2e;
+    const float mul_lo = mul * (1.f / kPfSplit);
+    // keys this workgroup reads: causal rows stop at q_offset + position
+    const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
+    const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;
+    const int64_t lim = !rok ? -1 : a.causal ? a.q_offset + pos : INT64_MAX;  // this lane's row
+    const int n_tiles = t_end > 0 ? (int)((t_end + kWave - 1) / kWave) : 0;
+    const int64_t t_last = max(t_end - 1, (int64_t)0);
+    const uint8_t *idx_head = a.idx + bh * a.cap * kPfNB;
+    const __half *v_head = a.v8 + bh * a.cap * kPfD;
+
+    float m = -1e30f, lsum = 0.f;  // row l16 (lsum: this lane's share)
+    pf_f32x4 acc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[nt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto load_idx = [&](uint4 (&ir)[4], int tile) {
+        const int64_t t0 = (int64_t)tile * kWave;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            ir[j] = *reinterpret_cast<const uint4 *>(idx_head + min(t0 + 16 * j + l16, t_last) * kPfNB);
+    };
+    uint4 ir_cur[4], ir_nxt[4];
+    if (n_tiles > 0) load_idx(ir_cur, 0);
+
+    for (int tile = 0; tile < n_tiles; ++tile) {
+        const int64_t t0 = (int64_t)tile * kWave;
+        // the tile's value operands (4 tokens of one dim, 8 bytes), issued
+        // first so they land while the scores are computed; 8-token blocks
+        // past the last key clamp to its block (their weights are zero)
+        uint2 vop[4][8];
+        const int64_t blk_last = t_last >> 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t blk = min((t0 + 16 * j + 4 * g) >> 3, blk_last);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+                vop[j][nt] = *reinterpret_cast<const uint2 *>(
+                    v_head + (blk * kPfD + 16 * nt + l16) * 8 + ((4 * g) & 7));
+        }
+        load_idx(ir_nxt, min(tile + 1, n_tiles - 1));
+        // scores S^T of 4 sub-tiles of 16 tokens, log2 units
+        float sv[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            pf_f32x4 sh = pf_f32x4{0.f, 0.f, 0.f, 0.f}, sl = sh;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const uint32_t w = ks == 0 ? ir_cur[j].x : ks == 1 ? ir_cur[j].y
+                                 : ks == 2 ? ir_cur[j].z : ir_cur[j].w;
+                const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * g, 8);
+                const char *row = lds + ((4 * ks + g) * 256 + c) * kPfRowBytes;
+                const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
+                const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + 16);
+                sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ks], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ks], sl, 0, 0, 0);
+                if (qsplit) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ks], sl, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t t = t0 + 16 * j + 4 * g + i;
+                const float s = sh[i] * mul + sl[i] * mul_lo;
+                sv[j][i] = (t < t_end && t <= lim) ? s : -INFINITY;
+            }
+        }
+        // online softmax of row l16 over the tile's 64 tokens (16 here, the
+        // rest in lanes l16 + 16, + 32, + 48)
+        float mx = sv[0][0];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[j][i]);
+        mx = xor_max(mx, 16);
+        mx = xor_max(mx, 32);
+        const float mn = fmaxf(m, mx);
+        const float corr = fast_exp2(m - mn);
+        m = mn;
+        float ps = 0.f;
+        pf_f16x4 phi[4], plo[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = fast_exp2(sv[j][i] - mn);
+                ps += pr;
+                const float x = pr * kPfPScale;
+                const _Float16 hx = (_Float16)x;
+                phi[j][i] = hx;
+                plo[j][i] = (_Float16)(x - (float)hx);
+            }
+        lsum = fmaf(lsum, corr, ps);
+        // accumulator rows 4g + i take the correction of their own rows
+        if (__builtin_amdgcn_ballot_w64(corr != 1.f) != 0) {
+            pf_f32x4 c4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c4[i] = __shfl(corr, 4 * g + i);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) acc[nt] *= c4;
+        }
+        const bool last = t0 + kWave > t_end;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // zero the values of tokens past the last key (their weights are
+            // zero, the stale halves need not be finite)
+            int n_ok = 4;
+            if (last) n_ok = (int)max(min(t_end - (t0 + 16 * j + 4 * g), (int64_t)4), (int64_t)0);
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt) {
+                uint2 v = vop[j][nt];
+                if (n_ok < 4) {
+                    v.x &= n_ok >= 2 ? 0xffffffffu : n_ok == 1 ? 0x0000ffffu : 0u;
+                    v.y &= n_ok >= 4 ? 0xffffffffu : n_ok == 3 ? 0x0000ffffu : 0u;
+                }
+                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, v);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi[j], b, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[j], b, acc[nt], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ir_cur[j] = ir_nxt[j];
+    }
+
+    // 3. rows 4g + i of the accumulators: their l (the row's four lane
+    //    shares summed), then the output
+    float L = lsum + __shfl_xor(lsum, 16);
+    L += __shfl_xor(L, 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float Li = __shfl(L, 4 * g + i);
+        const int rr = wv * 16 + 4 * g + i;
+        const int pp = rr / a.rep, hh = rr - pp * a.rep;
+        const int64_t opos = (int64_t)pg * a.npos + pp;
+        if (opos < a.t_q) {
+            const int64_t off =
+                ((bb * a.n_q_heads + (int64_t)kvh * a.rep + hh) * a.t_q + opos) * kPfD;
+            const float inv = Li > 0.f ? 1.f / (Li * kPfPScale) : 0.f;
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+                store_from_f32(a.out, a.out_dtype, off + 16 * nt + l16, acc[nt][i] * inv);
+        }
+    }
+}
+
+}  // namespace ss
+
+using namespace ss;
+
+// Query rows per workgroup of ss_prefill_attn_il8 (the rep of a GQA group
+// must divide it) and the fewest query tokens it is meant for.
+extern "C" int ss_prefill_rows_per_workgroup(void) { return kPfRows; }
+
+extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                   int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                   const int32_t *perm, const void *codebook, int n_blocks,
+                                   int n_centroids, const uint8_t *idx, const void *values_il8,
+                                   int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                   int64_t q_offset, void *out, int out_dtype, void *stream) {
+    SS_REQUIRE(q && codebook && idx && values_il8 && out, "null pointer argument");
+    SS_REQUIRE(valid_dtype(q_dtype) && valid_dtype(out_dtype), "bad dtype code");
+    SS_REQUIRE(batch >= 1 && n_q_heads >= 1 && n_kv_heads >= 1 && t_q >= 1 &&
+                   n_q_heads % n_kv_heads == 0,
+               "bad head/batch counts");
+    SS_UNSUPPORTED(head_dim == kPfD && n_blocks == kPfNB,
+                   "prefill kernel takes head_dim 128 with 16 blocks of 8 (got %d, %d)", head_dim,
+                   n_blocks);
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256, "n_centroids %d unsupported (1..256)",
+                   n_centroids);
+    const int rep = n_q_heads / n_kv_heads;
+    SS_UNSUPPORTED(kPfRows % rep == 0, "GQA group of %d query heads does not divide %d rows", rep,
+                   kPfRows);
+    SS_UNSUPPORTED(v_dtype == SS_F16, "interleaved values must be float16");
+    SS_REQUIRE(cap % 8 == 0 && t_kv >= 0 && t_kv <= cap, "bad cap/t_kv (cap %% 8 == 0, t_kv <= cap)");
+    SS_REQUIRE(q_offset >= 0, "negative q_offset");
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0 && ((uintptr_t)idx % 16) == 0 &&
+                   ((uintptr_t)values_il8 % 16) == 0,
+               "codebook, idx and values must be 16-byte aligned");
+    PrefillArgs a;
+    a.q = q;
+    a.q_dtype = q_dtype;
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.rep = rep;
+    a.t_q = t_q;
+    a.scale = scale;
+    a.perm = perm;
+    a.codebook = static_cast<const uint4 *>(codebook);
+    a.nct = (n_centroids + 15) / 16;
+    a.cb_mul = reinterpret_cast<const float *>(static_cast<const char *>(codebook) +
+                                               (size_t)(kPfNB / 4) * a.nct * 2 * kWave * 16);
+    a.idx = idx;
+    a.v8 = static_cast<const __half *>(values_il8);
+    a.cap = cap;
+    a.t_kv = t_kv;
+    a.causal = causal ? 1 : 0;
+    a.q_offset = q_offset;
+    a.out = out;
+    a.out_dtype = out_dtype;
+    a.npos = kPfRows / rep;
+    const int64_t n_pg = (t_q + a.npos - 1) / a.npos;
+    SS_UNSUPPORTED(n_pg <= 0x7fffffff && batch * n_kv_heads <= 65535, "grid too large");
+    a.n_pg = (int)n_pg;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_il8_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 kPfLdsBytes);
+        if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(prefill)");
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(prefill_il8_kernel, dim3(a.n_pg, (unsigned)(batch * n_kv_heads)),
+                       dim3(kPfWaves * kWave), kPfLdsBytes, reinterpret_cast<hipStream_t>(stream),
+                       a);
+    SS_LAUNCH_CHECK("prefill_il8_kernel launch");
+    return SS_OK;
+}

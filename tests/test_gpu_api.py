@@ -107,6 +107,32 @@ def test_fp16_cache_causal_prefill_and_capacity_growth():
     assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
 
 
+def test_prompt_prefill_takes_the_prefill_kernel():
+    """A prompt (32 query / 8 KV heads, 300 tokens, mask "causal") through
+    update_and_fetch and sunshape_sdpa, as mlx-lm's prefill runs it: the
+    prefill kernel serves it and matches the oracle; a second chunk of 70
+    tokens (chunked prefill, rows offset by the 300 cached ones) too."""
+    codec = make_codec(51)
+    b, hq, hkv, d = 1, 32, 8, 128
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv)
+    k, v = kv(52, b, hkv, 370, d)
+    q = torch.randn((b, hq, 370, d), device=DEV).to(torch.float16)
+    cache.update_and_fetch(k[:, :, :300], v[:, :, :300])
+    out = S.sunshape_sdpa(q[:, :, :300].contiguous(), cache, 0.088, mask="causal")
+    assert codec.last_score_backend == "hip_prefill_mfma"
+    cents = codec.centroids.cpu().numpy()
+    perm = codec.permutation.cpu().numpy()
+    ref = O.sdpa(q[:, :, :300].cpu().numpy(), cache.key_indices.cpu().numpy(),
+                 v[:, :, :300].cpu().numpy(), cents, perm, 0.088, mask="causal")
+    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    cache.update_and_fetch(k[:, :, 300:], v[:, :, 300:])
+    out2 = S.sunshape_sdpa(q[:, :, 300:].contiguous(), cache, 0.088, mask="causal")
+    assert codec.last_score_backend == "hip_prefill_mfma"
+    ref2 = O.sdpa(q[:, :, 300:].cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
+                  cents, perm, 0.088, mask="causal")
+    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
+
+
 def test_prepared_decode_follows_the_cache_and_matches_direct_launch():
     """``sunshape_sdpa`` launches the matrix-core decode through a plan kept
     on the cache.  It must give the same bits as the checked one-shot

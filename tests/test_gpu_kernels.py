@@ -865,3 +865,43 @@ def test_bounded_wait_failure_reaches_python():
     _hip.check_decode_waits()
     ref = O.sdpa(q, idx, vals, cents, perm, 1.0 / np.sqrt(d))
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,t_q,t_kv,causal,qdt,nc", [
+    (1, 32, 8, 200, 200, True, "f16", 256),      # rep 4: 32 positions per workgroup, ragged
+    (2, 8, 8, 96, 300, True, "f16", 256),        # rep 1, chunked prefill after 204 cached tokens
+    (1, 16, 2, 64, 64, False, "f16", 256),       # rep 8, unmasked
+    (1, 8, 2, 130, 1000, True, "bf16", 100),     # bf16 queries (hi/lo split), 100 centroids
+    (1, 4, 1, 33, 77, True, "f32", 256),         # f32 queries, partial tiles everywhere
+])
+def test_prefill_il8_matches_oracle(b, hq, hkv, t_q, t_kv, causal, qdt, nc):
+    """ss_prefill_attn_il8: a prompt's rows (keys reconstructed from the
+    prepared codebook, both products on the matrix cores) equal the oracle
+    SDPA, causal rows seeing keys up to q_offset + i, and agree with the
+    decode kernel on the same inputs."""
+    d = 128
+    cap = ((t_kv + 15) // 16) * 16
+    cents, perm, idx, vals, q16 = decode_case(700 + t_q + t_kv, b, hq, hkv, d, t_kv, t_q, cap, nc=nc)
+    scale = 1.0 / np.sqrt(d)
+    if qdt == "f16":
+        qt = t(q16)
+    elif qdt == "bf16":  # pre-scaled: q * 1 rounds to itself in bf16 and in the oracle's float32
+        qt = t(q16.astype(np.float32) * scale).to(torch.bfloat16)
+        scale = 1.0
+    else:
+        qt = t(q16.astype(np.float32) * 1.3 + 1e-3)
+    qref = qt.float().cpu().numpy() if qdt != "f16" else q16
+    v8 = to_il8(vals, cap)
+    cb = _hip.codebook_f16x2(t(cents))
+    q_off = t_kv - t_q if causal else 0
+    out = _hip.prefill_attn_il8(qt, scale, t(perm), cb, nc, t(idx), v8, t_kv, causal=causal,
+                                q_offset=q_off, out_dtype=torch.float32)
+    ref_dec = _hip.decode_attn_il8(qt, scale, t(perm), t(cents), t(idx), v8, t_kv, causal=causal,
+                                   q_offset=q_off, out_dtype=torch.float32, codebook=cb)
+    torch.cuda.synchronize()
+    ref = O.sdpa(qref, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, scale,
+                 mask="causal" if causal else None)
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) <= REL_TOL
+    assert rel_err(got, ref_dec.cpu().numpy()) <= REL_TOL
