@@ -40,10 +40,9 @@ constexpr int kPfWaves = 8;
 constexpr int kPfRows = 16 * kPfWaves;   // query rows of a workgroup
 constexpr int kPfD = 128;
 constexpr int kPfNB = 16;
-constexpr int kPfRowBytes = 32;          // one codebook row: 8 hi halves, 8 lo halves
-constexpr int kPfLdsBytes = kPfNB * 256 * kPfRowBytes;  // 128 KB
+constexpr int kPfRows16 = kPfNB * 256;   // codebook rows (block, centroid), 16 bytes each
+constexpr int kPfLdsBytes = 2 * kPfRows16 * 16;  // hi rows, then lo rows: 128 KB
 constexpr float kPfSplit = 2048.f;       // lo parts carry 2^11
-constexpr float kPfPScale = 32768.f;     // p * 2^15 keeps small weights normal in fp16
 
 struct PrefillArgs {
     const void *q;
@@ -86,17 +85,17 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
     const int64_t bb = bh / a.n_kv_heads;
     const int kvh = (int)(bh - bb * a.n_kv_heads);
 
-    // 1. the prepared codebook, row-major: row (block, centroid) at
-    //    (block * 256 + centroid) * 32 bytes, hi then lo.  Tile t = (bg, ct)
-    //    holds 64 lanes' rows: block bg*4 + l/16, centroid ct*16 + l%16.
+    // 1. the prepared codebook, row-major: the hi part of row (block,
+    //    centroid) at (block * 256 + centroid) * 16 bytes, its lo part 64 KB
+    //    further (16-byte rows spread random gathers over 16 bank groups).
+    //    Tile t = (bg, ct) holds 64 lanes' rows: block bg*4 + l/16, centroid
+    //    ct*16 + l%16.
+    uint4 *lds4 = reinterpret_cast<uint4 *>(lds);
     for (int i = tid; i < 4 * a.nct * kWave; i += TH) {
         const int t = i >> 6, l = i & 63, bg = t / a.nct, ct = t - bg * a.nct;
-        const uint4 hi = a.codebook[(int64_t)t * 2 * kWave + l];
-        const uint4 lo = a.codebook[(int64_t)t * 2 * kWave + kWave + l];
-        uint4 *d = reinterpret_cast<uint4 *>(lds + ((bg * 4 + (l >> 4)) * 256 + ct * 16 + (l & 15)) *
-                                                       kPfRowBytes);
-        d[0] = hi;
-        d[1] = lo;
+        const int row = (bg * 4 + (l >> 4)) * 256 + ct * 16 + (l & 15);
+        lds4[row] = a.codebook[(int64_t)t * 2 * kWave + l];
+        lds4[kPfRows16 + row] = a.codebook[(int64_t)t * 2 * kWave + kWave + l];
     }
 
     // 2. this lane's query row (the S^T column l%16 of wave wv): B operands
@@ -122,17 +121,27 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
         }
     const bool qsplit = a.q_dtype != SS_F16;
     __syncthreads();
+    // a wave whose rows all lie past the prompt has nothing to do (no
+    // barrier follows)
+    const int64_t wave_pos0 = (int64_t)pg * a.npos + (wv * 16) / a.rep;
+    if (wave_pos0 >= a.t_q) return;
 
     const float mul = *a.cb_mul * kLog2e;
     const float mul_lo = mul * (1.f / kPfSplit);
     // keys this workgroup reads: causal rows stop at q_offset + position
     const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
     const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;
-    const int64_t lim = !rok ? -1 : a.causal ? a.q_offset + pos : INT64_MAX;  // this lane's row
-    const int n_tiles = t_end > 0 ? (int)((t_end + kWave - 1) / kWave) : 0;
-    const int64_t t_last = max(t_end - 1, (int64_t)0);
+    // token indices below are 32-bit (cap < 2^24 checked on the host)
+    const int t_end32 = (int)t_end;
+    // this lane's row limit; rows past the prompt are never stored, so they
+    // need no mask
+    const int lim32 = (!rok || !a.causal) ? 0x7fffffff : (int)(a.q_offset + pos);
+    // the wave's smallest limit: tiles entirely below it need no mask
+    const int lim_min32 = a.causal ? (int)(a.q_offset + wave_pos0) : 0x7fffffff;
+    const int n_tiles = t_end32 > 0 ? (t_end32 + kWave - 1) / kWave : 0;
+    const int t_last = max(t_end32 - 1, 0);
     const uint8_t *idx_head = a.idx + bh * a.cap * kPfNB;
-    const __half *v_head = a.v8 + bh * a.cap * kPfD;
+    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap * kPfD);
 
     float m = -1e30f, lsum = 0.f;  // row l16 (lsum: this lane's share)
     pf_f32x4 acc[8];
@@ -140,31 +149,36 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
     for (int nt = 0; nt < 8; ++nt) acc[nt] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto load_idx = [&](uint4 (&ir)[4], int tile) {
-        const int64_t t0 = (int64_t)tile * kWave;
+        const int t0 = tile * kWave;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            ir[j] = *reinterpret_cast<const uint4 *>(idx_head + min(t0 + 16 * j + l16, t_last) * kPfNB);
+            ir[j] = *reinterpret_cast<const uint4 *>(
+                idx_head + (uint32_t)min(t0 + 16 * j + l16, t_last) * kPfNB);
     };
     uint4 ir_cur[4], ir_nxt[4];
     if (n_tiles > 0) load_idx(ir_cur, 0);
 
     for (int tile = 0; tile < n_tiles; ++tile) {
-        const int64_t t0 = (int64_t)tile * kWave;
+        const int t0 = tile * kWave;
         // the tile's value operands (4 tokens of one dim, 8 bytes), issued
         // first so they land while the scores are computed; 8-token blocks
         // past the last key clamp to its block (their weights are zero)
         uint2 vop[4][8];
-        const int64_t blk_last = t_last >> 3;
+        const int blk_last = t_last >> 3;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int64_t blk = min((t0 + 16 * j + 4 * g) >> 3, blk_last);
+            const uint32_t blk = (uint32_t)min((t0 + 16 * j + 4 * g) >> 3, blk_last);
+            const uint32_t off = ((blk * kPfD + l16) * 8 + ((4 * g) & 7)) * 2;
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt)
-                vop[j][nt] = *reinterpret_cast<const uint2 *>(
-                    v_head + (blk * kPfD + 16 * nt + l16) * 8 + ((4 * g) & 7));
+                vop[j][nt] = *reinterpret_cast<const uint2 *>(v_head + off + nt * 256);
         }
         load_idx(ir_nxt, min(tile + 1, n_tiles - 1));
-        // scores S^T of 4 sub-tiles of 16 tokens, log2 units
+        // scores S^T of 4 sub-tiles of 16 tokens, log2 units; a tile below
+        // every row's limit and the last key is not masked (wave-uniform)
+        const bool full = t0 + kWave - 1 < t_end32 && t0 + kWave - 1 <= lim_min32;
+        const int rem_end = t_end32 - t0 - 4 * g, rem_lim = lim32 == 0x7fffffff ? 0x7fffffff
+                                                                             : lim32 - t0 - 4 * g;
         float sv[4][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -174,18 +188,21 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
                 const uint32_t w = ks == 0 ? ir_cur[j].x : ks == 1 ? ir_cur[j].y
                                  : ks == 2 ? ir_cur[j].z : ir_cur[j].w;
                 const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * g, 8);
-                const char *row = lds + ((4 * ks + g) * 256 + c) * kPfRowBytes;
+                const char *row = lds + ((4 * ks + g) * 256 + c) * 16;
                 const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
-                const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + 16);
+                const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
                 sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qh[ks], sh, 0, 0, 0);
                 sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, qh[ks], sl, 0, 0, 0);
                 if (qsplit) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ks], sl, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t t = t0 + 16 * j + 4 * g + i;
-                const float s = sh[i] * mul + sl[i] * mul_lo;
-                sv[j][i] = (t < t_end && t <= lim) ? s : -INFINITY;
+            for (int i = 0; i < 4; ++i) sv[j][i] = fmaf(sl[i], mul_lo, sh[i] * mul);
+            if (!full) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int k = 16 * j + i;
+                    sv[j][i] = (k < rem_end && k <= rem_lim) ? sv[j][i] : -INFINITY;
+                }
             }
         }
         // online softmax of row l16 over the tile's 64 tokens (16 here, the
@@ -200,15 +217,17 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
         const float mn = fmaxf(m, mx);
         const float corr = fast_exp2(m - mn);
         m = mn;
+        // x = p * 2^15 (exp2 of the score minus mn - 15), split into fp16
+        // hi and lo; l sums x and is scaled back at the end
         float ps = 0.f;
+        const float mn15 = mn - 15.f;
         pf_f16x4 phi[4], plo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pr = fast_exp2(sv[j][i] - mn);
-                ps += pr;
-                const float x = pr * kPfPScale;
+                const float x = fast_exp2(sv[j][i] - mn15);
+                ps += x;
                 const _Float16 hx = (_Float16)x;
                 phi[j][i] = hx;
                 plo[j][i] = (_Float16)(x - (float)hx);
@@ -222,21 +241,26 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) acc[nt] *= c4;
         }
-        const bool last = t0 + kWave > t_end;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        if (t0 + kWave > t_end32) {  // the last tile (wave-uniform)
             // zero the values of tokens past the last key (their weights are
             // zero, the stale halves need not be finite)
-            int n_ok = 4;
-            if (last) n_ok = (int)max(min(t_end - (t0 + 16 * j + 4 * g), (int64_t)4), (int64_t)0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n_ok = max(min(rem_end - 16 * j, 4), 0);
+                const uint32_t mx_ = n_ok >= 2 ? 0xffffffffu : n_ok == 1 ? 0x0000ffffu : 0u;
+                const uint32_t my_ = n_ok >= 4 ? 0xffffffffu : n_ok == 3 ? 0x0000ffffu : 0u;
+#pragma unroll
+                for (int nt = 0; nt < 8; ++nt) {
+                    vop[j][nt].x &= mx_;
+                    vop[j][nt].y &= my_;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                uint2 v = vop[j][nt];
-                if (n_ok < 4) {
-                    v.x &= n_ok >= 2 ? 0xffffffffu : n_ok == 1 ? 0x0000ffffu : 0u;
-                    v.y &= n_ok >= 4 ? 0xffffffffu : n_ok == 3 ? 0x0000ffffu : 0u;
-                }
-                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, v);
+                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, vop[j][nt]);
                 acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi[j], b, acc[nt], 0, 0, 0);
                 acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[j], b, acc[nt], 0, 0, 0);
             }
@@ -258,7 +282,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
         if (opos < a.t_q) {
             const int64_t off =
                 ((bb * a.n_q_heads + (int64_t)kvh * a.rep + hh) * a.t_q + opos) * kPfD;
-            const float inv = Li > 0.f ? 1.f / (Li * kPfPScale) : 0.f;
+            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^15
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt)
                 store_from_f32(a.out, a.out_dtype, off + 16 * nt + l16, acc[nt][i] * inv);
@@ -295,6 +319,8 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
                    kPfRows);
     SS_UNSUPPORTED(v_dtype == SS_F16, "interleaved values must be float16");
     SS_REQUIRE(cap % 8 == 0 && t_kv >= 0 && t_kv <= cap, "bad cap/t_kv (cap %% 8 == 0, t_kv <= cap)");
+    SS_UNSUPPORTED(cap < (int64_t(1) << 24) && t_q + q_offset < (int64_t(1) << 30),
+                   "prefill kernel takes caches below 2^24 tokens");
     SS_REQUIRE(q_offset >= 0, "negative q_offset");
     SS_REQUIRE(((uintptr_t)codebook % 16) == 0 && ((uintptr_t)idx % 16) == 0 &&
                    ((uintptr_t)values_il8 % 16) == 0,
