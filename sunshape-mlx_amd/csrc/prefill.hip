@@ -126,8 +126,9 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
     const int64_t wave_pos0 = (int64_t)pg * a.npos + (wv * 16) / a.rep;
     if (wave_pos0 >= a.t_q) return;
 
+    // scores stay in the prepared codebook's units (hi + lo * 2^-11); mul
+    // takes them to log2 units inside the exponent
     const float mul = *a.cb_mul * kLog2e;
-    const float mul_lo = mul * (1.f / kPfSplit);
     // keys this workgroup reads: causal rows stop at q_offset + position
     const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
     const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;
@@ -155,10 +156,10 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
             ir[j] = *reinterpret_cast<const uint4 *>(
                 idx_head + (uint32_t)min(t0 + 16 * j + l16, t_last) * kPfNB);
     };
-    uint4 ir_cur[4], ir_nxt[4];
-    if (n_tiles > 0) load_idx(ir_cur, 0);
+    uint4 ir_a[4], ir_b[4];
+    if (n_tiles > 0) load_idx(ir_a, 0);
 
-    for (int tile = 0; tile < n_tiles; ++tile) {
+    auto do_tile = [&](const uint4 (&ir_cur)[4], uint4 (&ir_nxt)[4], int tile) {
         const int t0 = tile * kWave;
         // the tile's value operands (4 tokens of one dim, 8 bytes), issued
         // first so they land while the scores are computed; 8-token blocks
@@ -196,7 +197,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
                 if (qsplit) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ql[ks], sl, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sv[j][i] = fmaf(sl[i], mul_lo, sh[i] * mul);
+            for (int i = 0; i < 4; ++i) sv[j][i] = fmaf(sl[i], 1.f / kPfSplit, sh[i]);
             if (!full) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -214,23 +215,23 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[j][i]);
         mx = xor_max(mx, 16);
         mx = xor_max(mx, 32);
-        const float mn = fmaxf(m, mx);
-        const float corr = fast_exp2(m - mn);
+        const float mn = fmaxf(m, mx);  // raw units (mul > 0)
+        const float corr = fast_exp2((m - mn) * mul);
         m = mn;
-        // x = p * 2^15 (exp2 of the score minus mn - 15), split into fp16
-        // hi and lo; l sums x and is scaled back at the end
+        // x = p * 2^15 = exp2(s * mul - (mn * mul - 15)), split into fp16 hi
+        // and lo; l sums x and is scaled back at the end
         float ps = 0.f;
-        const float mn15 = mn - 15.f;
+        const float off = fmaf(mn, mul, -15.f);
         pf_f16x4 phi[4], plo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float x = fast_exp2(sv[j][i] - mn15);
+                const float x = fast_exp2(fmaf(sv[j][i], mul, -off));
                 ps += x;
                 const _Float16 hx = (_Float16)x;
                 phi[j][i] = hx;
-                plo[j][i] = (_Float16)(x - (float)hx);
+                plo[j][i] = (_Float16)__builtin_fmaf((float)hx, -1.f, x);
             }
         lsum = fmaf(lsum, corr, ps);
         // accumulator rows 4g + i take the correction of their own rows
@@ -265,8 +266,11 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
                 acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[j], b, acc[nt], 0, 0, 0);
             }
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ir_cur[j] = ir_nxt[j];
+    };
+    for (int tile = 0; tile < n_tiles; tile += 2) {
+        do_tile(ir_a, ir_b, tile);
+        if (tile + 1 >= n_tiles) break;
+        do_tile(ir_b, ir_a, tile + 1);
     }
 
     // 3. rows 4g + i of the accumulators: their l (the row's four lane
