@@ -71,6 +71,38 @@ int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h
                       int64_t o_sb, int64_t o_sh, int64_t o_st, void *stream);
 
 /*
+ * Codebook of the matrix-core encoder, prepared once per codebook (no
+ * reference counterpart: block_vq_quantize_metal, kernels.py:1037-1082,
+ * reads the float32 centroids on every call).  centroids float32
+ * [n_blocks <= 16][n_centroids <= 256][8].  Per block b: a power-of-two scale
+ * s_b bringing the largest |centroid element| into [8, 16) (0 when the
+ * block holds a non-finite value), the MFMA operand of every 16-centroid
+ * tile (fp16 s_b*C split into hi and lo, and the split (1 - 2^-15)|s_b C|^2),
+ * the squared norms |s_b C|^2 and their maximum.  ss_encode_codebook_bytes
+ * gives the size; prepared must be 16-byte aligned.
+ */
+size_t ss_encode_codebook_bytes(int n_blocks);
+int ss_encode_codebook(const float *centroids, int n_blocks, int n_centroids, int block_dim,
+                       void *prepared, void *stream);
+
+/*
+ * ss_encode_blockvq with the prepared codebook of the same centroids (same
+ * arguments, same indices; replaces block_vq_quantize_metal, reference
+ * kernels.py:1037-1082).  Bulk encodes (block_dim 8, n_blocks <= 16, more
+ * than 4096 (token, block) pairs) rank the codebook on the matrix cores:
+ * a lower bound of every squared distance from v_mfma_f32_16x16x32_f16,
+ * accepted when its runner-up clears the float error bound, otherwise the
+ * block is ranked exactly as ss_encode_blockvq does.  Other shapes run the
+ * ss_encode_blockvq kernels; prepared may then be null.
+ */
+int ss_encode_blockvq_prepared(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h,
+                               int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                               int head_dim, const int32_t *perm, const float *centroids,
+                               int n_blocks, int n_centroids, int block_dim, uint8_t *out,
+                               int64_t o_sb, int64_t o_sh, int64_t o_st, const void *prepared,
+                               void *stream);
+
+/*
  * Query x centroid table  lut[r][b][c] = sum_d q'[r][b*bd+d] * C[b][c][d]
  * with q'[r][j] = round_to(q_dtype, q[r][perm[j]] * scale).
  * Replaces precompute_query_centroid_dots (reference codec.py:553-573; the

@@ -61,6 +61,11 @@ _SIGNATURES = {
     "ss_encode_blockvq": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                                  _c_void_p, _c_void_p, _int, _int, _int, _c_void_p, _i64, _i64,
                                  _i64, _c_void_p]),
+    "ss_encode_blockvq_prepared": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+                                          _int, _c_void_p, _c_void_p, _int, _int, _int, _c_void_p,
+                                          _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "ss_encode_codebook_bytes": (_size, [_int]),
+    "ss_encode_codebook": (_int, [_c_void_p, _int, _int, _int, _c_void_p, _c_void_p]),
     "ss_build_lut": (_int, [_c_void_p, _int, _i64, _i64, _int, _c_void_p, _f32, _c_void_p,
                             _int, _int, _int, _c_void_p, _c_void_p]),
     "ss_score_gather": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _i64, _i64, _c_void_p,
@@ -421,10 +426,34 @@ def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
 # --------------------------------------------------------------------------- #
 
 
+def encode_codebook(centroids: torch.Tensor) -> torch.Tensor:
+    """Prepared codebook (flat uint8 buffer) of the matrix-core encoder for
+    float32 centroids (n_blocks <= 16, n_centroids <= 256, 8): per block a
+    power-of-two scale, the split-fp16 MFMA operands and the squared norms."""
+    require_gpu(centroids)
+    if centroids.dim() != 3 or centroids.dtype != torch.float32 or not centroids.is_contiguous():
+        raise ValueError("centroids must be contiguous float32 (n_blocks, n_centroids, 8)")
+    nb, nc, bd = centroids.shape
+    lib = load_library()
+    out = torch.empty(lib.ss_encode_codebook_bytes(nb), dtype=torch.uint8, device=centroids.device)
+    check(lib.ss_encode_codebook(ptr(centroids), nb, nc, bd, ptr(out),
+                                 stream_handle(centroids.device)))
+    return out
+
+
+def encode_codebook_supported(centroids: torch.Tensor) -> bool:
+    """Shapes the prepared (matrix-core) encoder takes."""
+    nb, nc, bd = centroids.shape
+    return bd == 8 and 1 <= nb <= 16 and 1 <= nc <= 256
+
+
 def encode_blockvq(keys: torch.Tensor, perm: torch.Tensor | None, centroids: torch.Tensor,
-                   out: torch.Tensor, block_dim: int) -> torch.Tensor:
+                   out: torch.Tensor, block_dim: int,
+                   prepared: torch.Tensor | None = None) -> torch.Tensor:
     """Encode keys of shape (B, H, T, D) or (N, D) into ``out`` (same leading
-    shape, last dim n_blocks, uint8; may be a strided view into a cache)."""
+    shape, last dim n_blocks, uint8; may be a strided view into a cache).
+    With ``prepared`` (:func:`encode_codebook` of the same centroids) bulk
+    encodes run on the matrix cores; the indices are the same."""
     require_gpu(keys, perm, centroids, out)
     if centroids.dtype != torch.float32 or not centroids.is_contiguous():
         raise ValueError("centroids must be contiguous float32 (n_blocks, n_centroids, block_dim)")
@@ -443,10 +472,17 @@ def encode_blockvq(keys: torch.Tensor, perm: torch.Tensor | None, centroids: tor
     if perm is not None and (perm.dtype != torch.int32 or perm.numel() != d):
         raise ValueError("perm must be int32 of length head_dim")
     lib = load_library()
-    _launched("sunshape_block_vq_quantize_hip", lib.ss_encode_blockvq(
-        ptr(k4), dtype_code(k4.dtype), b_, h_, t_, k4.stride(0), k4.stride(1), k4.stride(2), d,
-        ptr(perm), ptr(centroids), nb, nc, bd, ptr(o4), o4.stride(0), o4.stride(1),
-        o4.stride(2), stream_handle(keys.device)))
+    args = (ptr(k4), dtype_code(k4.dtype), b_, h_, t_, k4.stride(0), k4.stride(1), k4.stride(2), d,
+            ptr(perm), ptr(centroids), nb, nc, bd, ptr(o4), o4.stride(0), o4.stride(1),
+            o4.stride(2))
+    if prepared is not None:
+        require_gpu(prepared)
+        if prepared.dtype != torch.uint8 or prepared.numel() < lib.ss_encode_codebook_bytes(nb):
+            raise ValueError("prepared must be the uint8 buffer of encode_codebook(centroids)")
+        st = lib.ss_encode_blockvq_prepared(*args, ptr(prepared), stream_handle(keys.device))
+    else:
+        st = lib.ss_encode_blockvq(*args, stream_handle(keys.device))
+    _launched("sunshape_block_vq_quantize_hip", st)
     return out
 
 

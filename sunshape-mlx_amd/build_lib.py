@@ -36,6 +36,12 @@ COMMON_FLAGS = [
 ]
 
 
+# per-source flags: the encoder's distance filter consumes every matrix-core
+# result on the vector ALUs, so its results are kept in VGPRs (no
+# v_accvgpr_read per element)
+FILE_FLAGS = {"encode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     return exe
@@ -43,7 +49,7 @@ def hipcc() -> str:
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

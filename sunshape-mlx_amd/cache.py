@@ -59,7 +59,8 @@ def _encode_into(codec: SunShapeBlockCodec, keys: torch.Tensor, out: torch.Tenso
     """Encode (B, H, T, D) keys into the (B, H, T, n_blocks) uint8 view ``out``."""
     if codec.mode == "profileperm_baseline" and codec.n_centroids <= 256:
         k = keys if keys.stride(-1) == 1 else keys.contiguous()
-        _hip.encode_blockvq(k, codec.permutation, codec.centroids, out, codec.block_dim)
+        _hip.encode_blockvq(k, codec.permutation, codec.centroids, out, codec.block_dim,
+                            prepared=codec.encode_codebook())
         return
     b_, h_, t_, d = keys.shape
     q = codec.quantize(keys.reshape(-1, d))

@@ -389,6 +389,19 @@ class SunShapeBlockCodec:
             self._kernel_codebook = cached
         return cached[2]
 
+    def encode_codebook(self, centroids: torch.Tensor | None = None) -> torch.Tensor | None:
+        """The prepared codebook of the matrix-core encoder for ``centroids``
+        (default: the codec's), built once and rebuilt when they change; None
+        for shapes that encoder does not take (the plain encoder runs)."""
+        c = self.centroids if centroids is None else centroids
+        if not _hip.encode_codebook_supported(c):
+            return None
+        cached = getattr(self, "_encode_codebook", None)
+        if cached is None or cached[0] is not c or cached[1] != c._version:
+            cached = (c, c._version, _hip.encode_codebook(c))
+            self._encode_codebook = cached
+        return cached[2]
+
     def _encode_centroids(self) -> torch.Tensor:
         if self.mode == "profileperm_localmetric_dsq":
             if self._shaped_centroids is None:
@@ -410,14 +423,16 @@ class SunShapeBlockCodec:
         out = torch.empty((n, self.n_blocks), dtype=torch.uint8, device=keys.device)
         if self.mode == "profileperm_baseline":
             _hip.encode_blockvq(keys if keys.stride(-1) == 1 else keys.contiguous(),
-                                self.permutation, self.centroids, out, self.block_dim)
+                                self.permutation, self.centroids, out, self.block_dim,
+                                prepared=self.encode_codebook())
         else:
             kt = self._forward_transform(keys.float())
             if self.mode == "profileperm_localmetric_dsq":
                 kt = torch.einsum("nbd,bed->nbe", kt.reshape(n, self.n_blocks, self.block_dim),
                                   self._local_metric_blocks()).reshape(n, self.head_dim)
-            _hip.encode_blockvq(kt.contiguous(), None, self._encode_centroids(), out,
-                                self.block_dim)
+            ec = self._encode_centroids()
+            _hip.encode_blockvq(kt.contiguous(), None, ec, out, self.block_dim,
+                                prepared=self.encode_codebook(ec))
         passthrough_blocks = passthrough_values = None
         if self.mode == "profileperm_mixed_precision":
             passthrough_blocks = self.mixed_high_precision_blocks

@@ -111,23 +111,12 @@ __global__ void __launch_bounds__(kEncThreads) encode_bulk_kernel(EncodeArgs a) 
     }
 }
 
-// ---- small: wave per (token, block) ----
+// Exact nearest codeword of one block, the whole wave cooperating: lanes
+// split the codebook, direct-form float32 ranking, (distance, index)
+// reduced across the wave with lowest-index ties, and a float64 re-rank
+// when the runner-up is within kSuspectRel of the best.
 template <int BD>
-__global__ void __launch_bounds__(kEncThreads) encode_small_kernel(EncodeArgs a) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t job = (int64_t)blockIdx.x * (kEncThreads / kWave) + (threadIdx.x >> 6);
-    if (job >= a.n_tok * a.n_blocks) return;  // wave-uniform
-    const int64_t n = job / a.n_blocks;
-    const int blk = (int)(job - n * a.n_blocks);
-    const TokAddr ad = token_addr(a, n);
-    float kv[BD];
-#pragma unroll
-    for (int k = 0; k < BD; ++k) {
-        const int j = blk * BD + k;
-        kv[k] = load_as_f32(a.keys, a.keys_dtype, ad.key + (a.perm ? a.perm[j] : j));
-    }
-    const int nc = a.n_centroids;
-    const float *cb = a.centroids + (int64_t)blk * nc * BD;
+__device__ int exact_block_wave(const float (&kv)[BD], const float *cb, int nc, int lane) {
     float best = INFINITY, second = INFINITY;
     int bi = 0x7fffffff;
     for (int c = lane; c < nc; c += kWave) {
@@ -181,8 +170,437 @@ __global__ void __launch_bounds__(kEncThreads) encode_small_kernel(EncodeArgs a)
         }
         bi = i64;
     }
-    if (bi == 0x7fffffff) bi = 0;  // every distance NaN: the reference keeps index 0
+    return bi == 0x7fffffff ? 0 : bi;  // every distance NaN: the reference keeps index 0
+}
+
+// ---- small: wave per (token, block) ----
+template <int BD>
+__global__ void __launch_bounds__(kEncThreads) encode_small_kernel(EncodeArgs a) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t job = (int64_t)blockIdx.x * (kEncThreads / kWave) + (threadIdx.x >> 6);
+    if (job >= a.n_tok * a.n_blocks) return;  // wave-uniform
+    const int64_t n = job / a.n_blocks;
+    const int blk = (int)(job - n * a.n_blocks);
+    const TokAddr ad = token_addr(a, n);
+    float kv[BD];
+#pragma unroll
+    for (int k = 0; k < BD; ++k) {
+        const int j = blk * BD + k;
+        kv[k] = load_as_f32(a.keys, a.keys_dtype, ad.key + (a.perm ? a.perm[j] : j));
+    }
+    const int bi = exact_block_wave<BD>(kv, a.centroids + (int64_t)blk * a.n_centroids * BD,
+                                        a.n_centroids, lane);
     if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
+}
+
+// ---- bulk on the matrix cores (block_dim 8): a bounded filter, then exact ties ----
+//
+// Per block b the codebook and the keys are scaled by s_b, a power of two
+// that brings the block's largest centroid element into [8, 16) (exact),
+// and split into fp16 parts x = x_hi + x_lo (x_lo = fp16(x - x_hi)).  Two
+// v_mfma_f32_32x32x16_f16 (32 centroids x 32 tokens, the second
+// accumulating onto the first) give
+//
+//   D(c) = (1-e)|y_c|^2 - 2 x.y_c + (1+e)|x|^2 + 2e max_c|y_c|^2 + 3 a0
+//
+// (K slots: -2x_hi.y_hi, -2x_hi.y_lo, -2x_lo.y_hi, the split (1-e)|y_c|^2
+// and the split constant), fp16 products exact, fp32 sums.  Its float error
+// e'(c) is below e_acc (2|x|^2 + 2|y_c|^2) + a_abs, e_acc < 2^-16.9 (33 fp32
+// additions rounded either way; the 2^-22 relative / 2^-25 absolute split
+// error of each operand), a_abs < 2^-21; with e = 2^-15 and a0 = 2^-19:
+//   * D(c) >= 0, so D's bits order as unsigned integers (no float min/max
+//     canonicalisation, no denormal flushing);
+//   * for any two centroids, d(c) - d(c1) >= D(c) - D(c1)
+//     - 2e (|x|^2 + |y_c1|^2) - 2 a0 (d the exact squared distance).
+// Each lane keeps the two smallest D of its 128 centroids (16 per product,
+// 8 tiles), with (tile, register) in the low 7 mantissa bits (at most 127
+// ulps, 2^-16 relative); the two lane halves of a token are merged into the
+// smallest D1 (centroid c1) and the runner-up D2.  If D2 - D1 exceeds
+// 2e (|x|^2 + |y_c1|^2) + 2 a0 + 2^-15 D2, every other centroid's exact
+// distance exceeds c1's, and c1 is the exact nearest codeword.  Otherwise
+// the (token, block) joins a per-wave queue ranked exactly by the whole
+// wave (exact_block_wave: direct-form float32, float64 on near-ties), as do
+// keys outside the scaled fp16 range and blocks with non-finite centroids.
+// The index is therefore the exact-arithmetic argmin with lowest-index
+// ties, the same as encode_bulk_kernel's.
+//
+// Persistent workgroups of 16 waves, one per CU: wave b owns block b and
+// keeps its 256 centroids' operands in registers for the whole launch;
+// each tile of 128 tokens is gathered (permuted, scaled, split) into LDS by
+// all threads, with the next tile's loads in flight during the products.
+constexpr int kEmTokens = 128;   // tokens per tile (4 groups of 32)
+constexpr int kEmWaves = 16;     // wave b ranks block b
+constexpr int kEmQueue = 64;     // per-wave queue of (token, block) to rank exactly
+constexpr float kEmEps = 1.0f / 32768.f;
+constexpr float kEmAbs = 1.0f / 524288.f;
+constexpr int kEmTiles = 8;      // 8 centroid tiles of 32
+constexpr float kEmMaxQ = 60000.f;  // |x|^2 bound: the split constant stays in fp16
+
+template <class T>
+using lds_ptr = __attribute__((address_space(3))) T *;
+typedef _Float16 em_f16x8 __attribute__((ext_vector_type(8)));
+typedef float em_f32x16 __attribute__((ext_vector_type(16)));
+
+// median of three unsigned words in one v_med3_u32 (the compiler expands the
+// min/max form into two instructions)
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+struct EncOps {  // the prepared codebook (ss_encode_codebook)
+    static size_t ops_bytes(int nb) { return (size_t)nb * kEmTiles * kWave * 16; }  // A operands
+    static size_t qpk_bytes(int nb) { return (size_t)nb * 256 * 4; }                // split (1-e)|y|^2
+    static size_t n2_bytes(int nb) { return (size_t)nb * 256 * 4; }                 // |y|^2
+    // then [nb] scales s_b and [nb] max |y|^2
+    static size_t bytes(int nb) {
+        return ops_bytes(nb) + qpk_bytes(nb) + n2_bytes(nb) + (((size_t)nb * 8 + 15) & ~size_t(15));
+    }
+};
+
+// One workgroup per block: the scale s_b, then for centroid c of tile
+// t = c/32 its A operand (lane c%32: y_hi, lane 32 + c%32: y_lo), the split
+// (1-e)|y_c|^2 (fp16 hi, lo packed in a word), |y_c|^2 and the block's max
+// |y|^2.  A codebook with a non-finite entry gets s_b = 0 (every token of
+// the block ranked exactly).
+__global__ void __launch_bounds__(256) encode_codebook_kernel(const float *cents, int nb, int nc,
+                                                              uint4 *ops, uint32_t *qpk, float *n2t,
+                                                              float *sig) {
+    __shared__ float red[256];
+    const int b = blockIdx.x, c = threadIdx.x;
+    float y[8];
+    float ma = 0.f;
+    bool fin = true;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        y[d] = c < nc ? cents[((int64_t)b * nc + c) * 8 + d] : 0.f;
+        fin = fin && fabsf(y[d]) <= 3.0e38f;
+        ma = fmaxf(ma, fabsf(y[d]));
+    }
+    const int bad = __syncthreads_or(!fin);
+    red[c] = fin ? ma : 0.f;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if (c < s2) red[c] = fmaxf(red[c], red[c + s2]);
+        __syncthreads();
+    }
+    float sg = 1.f;
+    if (red[0] > 0.f) {
+        int e;
+        frexpf(red[0], &e);
+        sg = ldexpf(1.f, min(max(4 - e, -120), 120));
+    }
+    if (bad) sg = 0.f;
+    if (c == 0) sig[b] = sg;
+    em_f16x8 hi, lo;
+    float q = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        const float x = bad ? 0.f : y[d] * sg;
+        hi[d] = (_Float16)x;
+        lo[d] = (_Float16)(x - (float)hi[d]);
+        q = fmaf(x, x, q);
+    }
+    const float qs = q * (1.f - kEmEps);
+    const _Float16 qh = (_Float16)qs, ql = (_Float16)(qs - (float)qh);
+    uint4 *o = ops + ((int64_t)b * kEmTiles + (c >> 5)) * kWave + (c & 31);
+    o[0] = __builtin_bit_cast(uint4, hi);
+    o[32] = __builtin_bit_cast(uint4, lo);
+    qpk[b * 256 + c] = (uint32_t)__builtin_bit_cast(uint16_t, qh) | ((uint32_t)__builtin_bit_cast(uint16_t, ql) << 16);
+    n2t[b * 256 + c] = q;
+    __syncthreads();
+    red[c] = q;
+    __syncthreads();
+    for (int s2 = 128; s2 > 0; s2 >>= 1) {
+        if (c < s2) red[c] = fmaxf(red[c], red[c + s2]);
+        __syncthreads();
+    }
+    if (c == 0) sig[nb + b] = red[0];
+}
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(__half v) { return __half2float(v); }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
+// a key element from its LDS-DMA dword slot (2-byte types in the low half)
+template <class KT>
+__device__ __forceinline__ float slot_f32(uint32_t w) {
+    if constexpr (std::is_same<KT, float>::value) return __uint_as_float(w);
+    else if constexpr (std::is_same<KT, __half>::value) return __half2float(__ushort_as_half((unsigned short)w));
+    else return __uint_as_float(w << 16);
+}
+
+// LDS of encode_mfma_kernel (one workgroup per CU)
+template <class KT>
+struct EmLds {
+    static constexpr bool KLO = !std::is_same<KT, __half>::value;  // keys carry an fp16 lo part
+    static constexpr int T = KLO ? 64 : 128;                      // tokens per tile
+    static constexpr int KW = KLO ? 32 : 16;                      // key operand bytes per (token, block)
+    static size_t bytes(int nb) {
+        return (size_t)T * (nb * KW + 16)          // operands
+               + (size_t)T * nb * 9                // split constant, |x|^2, indices
+               + (size_t)nb * 8 * 4                // permutation
+               + (size_t)kEmWaves * kEmQueue * 4   // queues
+               + (size_t)kEmWaves * 4              // queue lengths
+               + (size_t)kEmWaves * 256 * 4        // |y_c|^2 of each wave's block
+               + (size_t)T * nb * 8 * sizeof(KT);  // the next tile's key rows
+    }
+};
+
+template <class KT, bool FULL>  // key element type; FULL: 256 centroids (no partial tile)
+__global__ void __launch_bounds__(kEmWaves * kWave)
+    encode_mfma_kernel(EncodeArgs a, const uint4 *ops, const uint32_t *qpk, const float *n2t, const float *sig) {
+    using L = EmLds<KT>;
+    constexpr bool KLO = L::KLO;
+    constexpr int T = L::T, KW = L::KW;
+    constexpr int TH = kEmWaves * kWave;
+    const int NB = a.n_blocks, nc = a.n_centroids, nt = FULL ? kEmTiles : (nc + 31) >> 5;
+    // token rows padded by 16 bytes: consecutive tokens' 16-byte reads hit
+    // distinct bank groups
+    const int tstr = NB * KW + 16;
+    extern __shared__ __align__(16) char sm[];
+    char *kop = sm;                                                // [T][tstr]: -2 x_hi (, -2 x_lo)
+    uint32_t *kck = reinterpret_cast<uint32_t *>(sm + T * tstr);   // [T][NB] split constant (fp16 hi, lo)
+    float *kn2 = reinterpret_cast<float *>(kck + T * NB);          // [T][NB] |x|^2 (-1: rank exactly)
+    float *n2w = kn2 + T * NB;                                     // [kEmWaves][256] |y_c|^2
+    int *perm_l = reinterpret_cast<int *>(n2w + kEmWaves * 256);   // [NB * 8]
+    int *queue = perm_l + NB * 8;                                  // [kEmWaves][kEmQueue]
+    int *qlen = queue + kEmWaves * kEmQueue;                       // [kEmWaves]
+    KT *raw = reinterpret_cast<KT *>(qlen + kEmWaves);             // [T][D] key rows of the tile
+    uint8_t *oix = reinterpret_cast<uint8_t *>(raw + T * NB * 8);  // [T][NB] indices
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int D = NB * 8;
+    const int64_t n_tiles = (a.n_tok + T - 1) / T;
+    const bool owner = wv < NB;  // this wave ranks block wv
+
+    for (int j = tid; j < D; j += TH) perm_l[j] = a.perm ? min(max(a.perm[j], 0), D - 1) : j;
+    for (int j = tid; j < kEmWaves * 256; j += TH) n2w[j] = (j >> 8) < NB ? n2t[j] : 0.f;
+    // this wave's codebook operands (block wv), kept for the whole launch:
+    // Y[t] (lanes 0-31 y_hi, 32-63 y_lo of centroid 32t + lane%32) and the
+    // split (1-e)|y|^2 of that centroid
+    em_f16x8 Y[kEmTiles];
+    uint32_t Qd[kEmTiles];
+    if (owner) {
+#pragma unroll
+        for (int t = 0; t < kEmTiles; ++t)
+            if (t < nt) {
+                Y[t] = __builtin_bit_cast(em_f16x8, ops[((int64_t)wv * kEmTiles + t) * kWave + lane]);
+                Qd[t] = qpk[wv * 256 + 32 * t + (lane & 31)];
+            }
+    }
+    const float *n2b = n2w + (owner ? wv : 0) * 256;
+    __syncthreads();
+
+    // The tile's key rows are copied whole into LDS (global_load_lds of 16
+    // bytes per lane: 64 lanes move 1 KB of consecutive rows), issued one
+    // tile ahead; the permutation is applied from LDS.  Rows are 16-byte
+    // aligned (checked by the host).
+    constexpr int RC = 16 / (int)sizeof(KT);     // elements per 16-byte chunk
+    const int row_chunks = D / RC;               // chunks per key row
+    const int n_chunks = T * row_chunks;         // chunks per tile
+    const uint32_t raw_l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(raw));
+    auto gather = [&](int64_t tile) {
+        if (tile >= n_tiles) return;
+        for (int c0 = wv * kWave; c0 < n_chunks; c0 += TH) {  // wave-uniform
+            const int c = c0 + lane;
+            const int row = c / row_chunks, ch = c - row * row_chunks;
+            const int64_t n = min(tile * T + row, a.n_tok - 1);  // clamped: stays in bounds
+            const KT *src = static_cast<const KT *>(a.keys) + token_addr(a, n).key + ch * RC;
+            if (c < n_chunks)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const char *>(src),
+                                                 reinterpret_cast<lds_ptr<void>>(raw_l + (uint32_t)c0 * 16u), 16, 0, 0);
+        }
+    };
+    // permute, scale, range-check and split the tile's keys into the LDS
+    // operands: item i = (token i / NB, block i % NB)
+    auto stage = [&](int64_t tile) {
+        for (int i = tid; i < T * NB; i += TH) {
+            const int tl = i / NB, b = i - tl * NB;
+            const bool live = tile * T + tl < a.n_tok;
+            const float sg = sig[b];
+            const KT *xr = raw + tl * D;
+            float q = 0.f;
+            em_f16x8 h, l;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const float xs = to_f32(xr[perm_l[b * 8 + d]]) * sg;
+                q = fmaf(xs, xs, q);
+                h[d] = (_Float16)xs;
+                l[d] = (_Float16)(xs - (float)h[d]);
+            }
+            // NaN, inf and keys too far out for the fp16 operands fail
+            const bool ok = live && sg > 0.f && q < kEmMaxQ;
+            if (!ok) h = l = em_f16x8{};
+            *reinterpret_cast<em_f16x8 *>(kop + tl * tstr + b * KW) = h * (_Float16)(-2.0f);
+            if constexpr (KLO) *reinterpret_cast<em_f16x8 *>(kop + tl * tstr + b * KW + 16) = l * (_Float16)(-2.0f);
+            const float ck = ok ? fmaf(q, 1.f + kEmEps, fmaf(2.f * kEmEps, sig[NB + b], 3.f * kEmAbs)) : 0.f;
+            const _Float16 ch = (_Float16)ck, cl = (_Float16)(ck - (float)ch);
+            kck[i] = (uint32_t)__builtin_bit_cast(uint16_t, ch) | ((uint32_t)__builtin_bit_cast(uint16_t, cl) << 16);
+            kn2[i] = ok ? q : -1.f;
+        }
+    };
+
+    const int h = lane >> 5, j32 = lane & 31;
+    int *wq = queue + wv * kEmQueue;
+    int qn = 0;  // entries in this wave's queue (wave-uniform)
+    // Rank the queued (iteration, token, block) entries exactly, the whole
+    // wave per entry.  Each lane first loads the key elements of entry
+    // lane (one memory round trip for the batch).  Entries of the tile in
+    // progress (iteration cur) go to its LDS indices; earlier tiles' rows
+    // have been stored already, so theirs go straight to the output.
+    // Rank n_ent entries exactly, the whole wave per entry; entry j is
+    // ent_of(j) = (iteration << 15) | (token << 8) | block.  Each lane first
+    // loads the key elements of entry lane (one memory round trip per 64
+    // entries).  Entries of the tile in progress (iteration cur) go to its
+    // LDS indices; earlier tiles' rows are stored already, so theirs go
+    // straight to the output.
+    auto rank_entries = [&](int n_ent, auto ent_of, int cur) {
+        for (int j0 = 0; j0 < n_ent; j0 += kWave) {
+            const int ent_l = j0 + lane < n_ent ? ent_of(j0 + lane) : 0;
+            const int it_l = ent_l >> 15, tl_l = (ent_l >> 8) & 127, b_l = ent_l & 255;
+            const int64_t n_l = min(((int64_t)blockIdx.x + (int64_t)it_l * gridDim.x) * T + tl_l, a.n_tok - 1);
+            const TokAddr ad_l = token_addr(a, n_l);
+            float kvl[8];
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+                kvl[d] = to_f32(static_cast<const KT *>(a.keys)[ad_l.key + perm_l[min(b_l, NB - 1) * 8 + d]]);
+            const int ne = min(n_ent - j0, kWave);
+            for (int e = 0; e < ne; ++e) {
+                float kv[8];
+#pragma unroll
+                for (int d = 0; d < 8; ++d) kv[d] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kvl[d]), e));
+                const int ent = __builtin_amdgcn_readlane(ent_l, e);
+                const int it = ent >> 15, tl = (ent >> 8) & 127, b = ent & 255;
+                const int bi = exact_block_wave<8>(kv, a.centroids + (int64_t)b * nc * 8, nc, lane);
+                if (lane == 0) {
+                    if (it == cur)
+                        oix[tl * NB + b] = (uint8_t)bi;
+                    else
+                        a.out[token_addr(a, ((int64_t)blockIdx.x + (int64_t)it * gridDim.x) * T + tl).out + b] =
+                            (uint8_t)bi;
+                }
+            }
+        }
+    };
+    // this wave's queue, when full
+    auto flush = [&](int cur) {
+        wave_lds_sync();
+        rank_entries(qn, [&](int j) { return wq[j]; }, cur);
+        wave_lds_sync();
+        qn = 0;
+    };
+
+    int64_t tile = blockIdx.x;
+    gather(tile);
+    for (int it = 0; tile < n_tiles; tile += gridDim.x, ++it) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's row copies have landed
+        __syncthreads();                                     // ... and every other wave's
+        stage(tile);
+        __syncthreads();
+        gather(tile + gridDim.x);  // the next tile's keys stream in during the products
+        if (owner) {
+            const int b = wv;
+            for (int q0 = 0; q0 < T; q0 += 32) {
+                const int tl = q0 + j32;
+                // products per centroid tile (32 centroids x 32 tokens):
+                //   Y . [-2x_hi; -2x_hi]       y_hi.x_hi (lanes 0-31), y_lo.x_hi (32-63)
+                //   Y . [-2x_lo; -2x_lo]       (float32 / bfloat16 keys)
+                //   [q_hi, q_lo, 1, 1, 0..] . [1, 1, c_hi, c_lo, 0..; 0]   (1-e)|y|^2 + constant
+                const em_f16x8 B0 = *reinterpret_cast<const em_f16x8 *>(kop + tl * tstr + b * KW);
+                em_f16x8 B1 = {};
+                if constexpr (KLO) B1 = *reinterpret_cast<const em_f16x8 *>(kop + tl * tstr + b * KW + 16);
+                em_f16x8 B3 = {};
+                if (h == 0) {
+                    const uint32_t ck = kck[tl * NB + b];
+                    B3[0] = (_Float16)1.0f;
+                    B3[1] = (_Float16)1.0f;
+                    B3[2] = __builtin_bit_cast(_Float16, (uint16_t)(ck & 0xffffu));
+                    B3[3] = __builtin_bit_cast(_Float16, (uint16_t)(ck >> 16));
+                }
+                // two trackers (tiles 0-3 and 4-7), so the (tile, register)
+                // code stays an inline constant (0..63) of v_and_or_b32
+                uint32_t m1[2] = {0xffffffffu, 0xffffffffu}, m2[2] = {0xffffffffu, 0xffffffffu};
+#pragma unroll
+                for (int t = 0; t < kEmTiles; ++t) {
+                    if (FULL || t < nt) {
+                        em_f32x16 Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(Y[t], B0, em_f32x16{}, 0, 0, 0);
+                        if constexpr (KLO) Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(Y[t], B1, Dv, 0, 0, 0);
+                        const em_f16x8 A3 = __builtin_bit_cast(em_f16x8, uint4{Qd[t], 0x3c003c00u, 0u, 0u});
+                        Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(A3, B3, Dv, 0, 0, 0);
+                        const int hk = t >> 2;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            uint32_t p = (__float_as_uint(Dv[r]) & 0xffffff80u) | (uint32_t)((t & 3) * 16 + r);
+                            // centroid row of register r: 8*(r/4) + 4*h + r%4
+                            if (!FULL && t == nt - 1)
+                                p = (32 * t + 8 * (r >> 2) + 4 * h + (r & 3) < nc) ? p : 0xffffffffu;
+                            m2[hk] = umed3(m1[hk], m2[hk], p);
+                            m1[hk] = min(m1[hk], p);
+                        }
+                    }
+                }
+                // the two trackers (codes of tiles 4-7 get 64 added) ...
+                const bool lo_win = m1[0] < m1[1];
+                const uint32_t t2 = umed3(m1[0], m1[1], min(m2[0], m2[1]));
+                const uint32_t t1 = lo_win ? m1[0] : m1[1];
+                const int tcode = (int)(t1 & 63u) + (lo_win ? 0 : 64);
+                // ... then the token's other lane half (centroid rows 4..7 of each 8)
+                const uint32_t o1 = __shfl_xor(t1, 32), o2 = __shfl_xor(t2, 32);
+                const int ocode = __shfl_xor(tcode, 32);
+                const uint32_t M2 = umed3(t1, o1, min(t2, o2));
+                const bool mine = t1 < o1;
+                const uint32_t M1 = mine ? t1 : o1;
+                const int hw = mine ? h : 1 - h;
+                const int code = mine ? tcode : ocode, rr = code & 15;
+                const int C1 = 32 * (code >> 4) + 8 * (rr >> 2) + 4 * hw + (rr & 3);
+                const bool tok = h == 0 && tile * T + tl < a.n_tok;
+                const float qk = kn2[tl * NB + b];
+                bool accept = false;
+                if (tok && qk >= 0.f && C1 < nc && t1 != o1) {
+                    const float qc = n2b[C1];
+                    const float f1 = __uint_as_float(M1), f2 = __uint_as_float(M2);
+                    const float win = fmaf(2.01f * kEmEps, qk + qc, 2.f * kEmAbs) + f2 * (1.f / 32768.f);
+                    // M2 = 0xffffffff (NaN): a single centroid, nothing to beat
+                    accept = f2 - f1 > win || M2 == 0xffffffffu;
+                }
+                if (tok && accept) oix[tl * NB + b] = (uint8_t)C1;
+                const bool need = tok && !accept;
+                const uint64_t bal = __ballot(need);
+                if (need) {
+                    const int pos = qn + (int)__builtin_amdgcn_mbcnt_hi(
+                                             (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+                    wq[pos] = (it << 15) | (tl << 8) | b;
+                }
+                qn += __popcll(bal);
+                if (qn > kEmQueue - 32) flush(it);
+            }
+            // entries wait for a full queue or the end of the launch (the
+            // iteration field holds 16 bits)
+            if (it >= 0xfffe && qn > 0) flush(it);
+        }
+        __syncthreads();
+        for (int i = tid; i < T * NB; i += TH) {
+            const int tl = i / NB, b = i - tl * NB;
+            const int64_t n = tile * T + tl;
+            if (n < a.n_tok) a.out[token_addr(a, n).out + b] = oix[i];
+        }
+    }
+    // What is left in the queues is ranked by all 16 waves together (entry
+    // k of the concatenated queues by wave k % 16); the last tile's rows are
+    // stored, ordered before these stores by the barrier.
+    if (lane == 0) qlen[wv] = owner ? qn : 0;
+    __syncthreads();
+    int tot = 0;
+#pragma unroll
+    for (int q = 0; q < kEmWaves; ++q) tot += qlen[q];
+    const int mine = tot > wv ? (tot - wv + kEmWaves - 1) / kEmWaves : 0;
+    rank_entries(mine, [&](int j) {
+        int k = wv + j * kEmWaves;  // index into the concatenated queues
+        int q = 0;
+        while (k >= qlen[q]) k -= qlen[q++];
+        return queue[q * kEmQueue + k];
+    }, -1);
 }
 
 template <int BD>
@@ -214,11 +632,11 @@ static int launch_encode(const EncodeArgs &a, hipStream_t st) {
 
 using namespace ss;
 
-extern "C" int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h,
-                                 int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                                 int head_dim, const int32_t *perm, const float *centroids,
-                                 int n_blocks, int n_centroids, int block_dim, uint8_t *out,
-                                 int64_t o_sb, int64_t o_sh, int64_t o_st, void *stream) {
+static int encode_impl(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h, int64_t n_t,
+                       int64_t k_sb, int64_t k_sh, int64_t k_st, int head_dim, const int32_t *perm,
+                       const float *centroids, int n_blocks, int n_centroids, int block_dim,
+                       uint8_t *out, int64_t o_sb, int64_t o_sh, int64_t o_st, const void *prepared,
+                       void *stream) {
     SS_REQUIRE(valid_dtype(keys_dtype), "bad key dtype");
     SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0, "negative token counts");
     SS_REQUIRE(head_dim > 0 && block_dim > 0 && n_blocks * block_dim == head_dim,
@@ -233,7 +651,83 @@ extern "C" int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, 
     EncodeArgs a{keys, keys_dtype, n_h,  n_t,        n_tok,     k_sb, k_sh, k_st,
                  perm, centroids,  n_blocks, n_centroids, out, o_sb, o_sh, o_st};
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    // the matrix-core encoder copies whole key rows in 16-byte pieces
+    const int ksz = dtype_bytes(keys_dtype);
+    const bool rows16 = ((uintptr_t)keys % 16) == 0 && (k_sb * ksz) % 16 == 0 && (k_sh * ksz) % 16 == 0 &&
+                        (k_st * ksz) % 16 == 0;
+    if (prepared && rows16 && block_dim == 8 && n_blocks <= 16 && n_tok * n_blocks > 4096) {
+        SS_REQUIRE(((uintptr_t)prepared % 16) == 0, "prepared codebook must be 16-byte aligned");
+        const char *p = static_cast<const char *>(prepared);
+        const uint4 *ops = reinterpret_cast<const uint4 *>(p);
+        const uint32_t *qpk = reinterpret_cast<const uint32_t *>(p + EncOps::ops_bytes(n_blocks));
+        const float *n2t =
+            reinterpret_cast<const float *>(p + EncOps::ops_bytes(n_blocks) + EncOps::qpk_bytes(n_blocks));
+        const float *sig = n2t + (size_t)n_blocks * 256;
+        auto go = [&](auto kt, auto full) -> int {
+            using KT = decltype(kt);
+            constexpr bool FULL = decltype(full)::value;
+            const size_t lds = EmLds<KT>::bytes(n_blocks);
+            const void *fn = reinterpret_cast<const void *>(encode_mfma_kernel<KT, FULL>);
+            if (lds > 65536) {
+                hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(encode_mfma)");
+            }
+            const int64_t n_tiles = (n_tok + EmLds<KT>::T - 1) / EmLds<KT>::T;
+            dim3 grid((unsigned)std::min<int64_t>(n_tiles, device_cu_count()));
+            hipLaunchKernelGGL((encode_mfma_kernel<KT, FULL>), grid, dim3(kEmWaves * kWave), lds, st, a, ops,
+                               qpk, n2t, sig);
+            return SS_OK;
+        };
+        auto go2 = [&](auto kt) -> int {
+            return n_centroids == 256 ? go(kt, std::true_type{}) : go(kt, std::false_type{});
+        };
+        const int rc = keys_dtype == SS_F16 ? go2(__half{}) : keys_dtype == SS_BF16 ? go2(__hip_bfloat16{}) : go2(float{});
+        if (rc != SS_OK) return rc;
+        SS_LAUNCH_CHECK("encode_mfma_kernel launch");
+        return SS_OK;
+    }
     if (block_dim == 8) return launch_encode<8>(a, st);
     if (block_dim == 4) return launch_encode<4>(a, st);
     return launch_encode<16>(a, st);
+}
+
+extern "C" int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h,
+                                 int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                 int head_dim, const int32_t *perm, const float *centroids,
+                                 int n_blocks, int n_centroids, int block_dim, uint8_t *out,
+                                 int64_t o_sb, int64_t o_sh, int64_t o_st, void *stream) {
+    return encode_impl(keys, keys_dtype, n_b, n_h, n_t, k_sb, k_sh, k_st, head_dim, perm, centroids,
+                       n_blocks, n_centroids, block_dim, out, o_sb, o_sh, o_st, nullptr, stream);
+}
+
+extern "C" size_t ss_encode_codebook_bytes(int n_blocks) {
+    return n_blocks > 0 ? EncOps::bytes(n_blocks) : 0;
+}
+
+extern "C" int ss_encode_codebook(const float *centroids, int n_blocks, int n_centroids,
+                                  int block_dim, void *prepared, void *stream) {
+    SS_REQUIRE(centroids && prepared, "null pointer argument");
+    SS_UNSUPPORTED(block_dim == 8, "block_dim %d unsupported for the prepared codebook (8)", block_dim);
+    SS_UNSUPPORTED(n_blocks >= 1 && n_blocks <= 16, "n_blocks %d unsupported (1..16)", n_blocks);
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256, "n_centroids %d unsupported (1..256)",
+                   n_centroids);
+    SS_REQUIRE(((uintptr_t)prepared % 16) == 0, "prepared codebook must be 16-byte aligned");
+    char *p = static_cast<char *>(prepared);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint32_t *qpk = reinterpret_cast<uint32_t *>(p + EncOps::ops_bytes(n_blocks));
+    float *n2t = reinterpret_cast<float *>(p + EncOps::ops_bytes(n_blocks) + EncOps::qpk_bytes(n_blocks));
+    hipLaunchKernelGGL(encode_codebook_kernel, dim3(n_blocks), dim3(256), 0, st, centroids, n_blocks,
+                       n_centroids, reinterpret_cast<uint4 *>(p), qpk, n2t, n2t + (size_t)n_blocks * 256);
+    SS_LAUNCH_CHECK("encode_codebook_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_encode_blockvq_prepared(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h,
+                                          int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                          int head_dim, const int32_t *perm, const float *centroids,
+                                          int n_blocks, int n_centroids, int block_dim, uint8_t *out,
+                                          int64_t o_sb, int64_t o_sh, int64_t o_st,
+                                          const void *prepared, void *stream) {
+    return encode_impl(keys, keys_dtype, n_b, n_h, n_t, k_sb, k_sh, k_st, head_dim, perm, centroids,
+                       n_blocks, n_centroids, block_dim, out, o_sb, o_sh, o_st, prepared, stream);
 }

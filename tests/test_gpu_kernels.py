@@ -170,6 +170,70 @@ def test_encode_bit_exact_except_near_ties(n_tok, bd, dtype):
     assert not (got == 7).any(), "duplicate centroid 7 must lose the tie to centroid 3"
 
 
+@pytest.mark.parametrize("n_tok,dtype,nc,seed", [
+    (4096, np.float16, 256, 1),
+    (4000, np.float32, 256, 2),   # keys carry an fp16 lo part
+    (3001, "bf16", 256, 3),
+    (2500, np.float32, 100, 4),   # partial last centroid tile
+    (2000, np.float16, 17, 5),
+    (1030, np.float32, 1, 6),     # one centroid: nothing to beat
+    (20000, np.float32, 256, 7),  # several tiles per persistent workgroup
+])
+def test_encode_prepared_matches_plain_encoder_and_oracle(n_tok, dtype, nc, seed):
+    """Matrix-core encoder (prepared codebook): indices identical to the
+    plain encoder on every (token, block), including rows that must take the
+    exact path (keys equal to a centroid, a duplicated centroid pair, zero
+    rows, keys beyond the scaled fp16 range, a NaN block); and bit-exact
+    against the float64 oracle away from its flagged near-ties."""
+    rng = np.random.default_rng(seed)
+    d, bd = 128, 8
+    nb = d // bd
+    s = np.exp(rng.uniform(np.log(0.25), np.log(8.0), d)).astype(np.float32)
+    keys = (rng.standard_normal((n_tok, d)) * s).astype(np.float32)
+    perm = rng.permutation(d).astype(np.int32)
+    cents = _kmeans_like_codebook(rng, nb, nc, bd, s[perm]) if nc >= 8 else \
+        (rng.standard_normal((nb, nc, bd)) * s[perm].reshape(nb, 1, bd)).astype(np.float32)
+    inv = np.argsort(perm)
+    keys[10] = cents[np.arange(nb), 0].reshape(-1)[inv]   # exactly centroid 0 of every block
+    keys[11] = 0.0
+    if nc >= 8:
+        keys[12] = cents[np.arange(nb), 3].reshape(-1)[inv]  # on the duplicated pair 3 / 7
+    nan_row = dtype is np.float32
+    if nan_row:
+        keys[13, perm[:8]] = np.nan                       # block 0 of row 13
+        keys[14, perm[8:16]] = 3.0e6                      # block 1 beyond the fp16 range
+    if dtype == "bf16":
+        kt = t(keys).to(torch.bfloat16)
+        keys = kt.float().cpu().numpy()
+    else:
+        keys = keys.astype(dtype)
+        kt = t(keys)
+    # the rounded key rows become the centroids they were drawn from, so the
+    # distances are exactly 0
+    kp = keys.astype(np.float32)[:, perm].reshape(n_tok, nb, bd)
+    cents[:, 0] = kp[10]
+    if nc >= 8:
+        cents[:, 3] = cents[:, 7] = kp[12]
+    ct = t(cents)
+    prep = _hip.encode_codebook(ct)
+    plain = torch.empty((n_tok, nb), dtype=torch.uint8, device=DEV)
+    fast = torch.full((n_tok, nb), 255, dtype=torch.uint8, device=DEV)
+    _hip.encode_blockvq(kt, t(perm), ct, plain, bd)
+    _hip.encode_blockvq(kt, t(perm), ct, fast, bd, prepared=prep)
+    torch.cuda.synchronize()
+    got, base = fast.cpu().numpy(), plain.cpu().numpy()
+    assert np.array_equal(got, base), f"{(got != base).sum()} pairs differ from the plain encoder"
+    finite = np.isfinite(keys).all(1)
+    ref, near = O.encode_blockvq_c(keys[finite].astype(np.float32), cents, perm)
+    ok = ~near
+    assert np.array_equal(got[finite][ok], ref[ok]), f"{(got[finite][ok] != ref[ok]).sum()} mismatches"
+    assert (got[10] == 0).all()
+    if nc >= 8:
+        assert (got[12] == 3).all() and not (got == 7).any()
+    if nan_row:
+        assert got[13, 0] == 0
+
+
 def test_encode_config3_shape_and_cache_strides():
     """Config 3: fp16 K (8 heads x 8192 tokens x 128), ProfilePerm,
     encoded straight into a padded cache buffer (B, H, cap, 16) at an offset."""
@@ -180,15 +244,20 @@ def test_encode_config3_shape_and_cache_strides():
     perm = rng.permutation(d).astype(np.int32)
     cal = (rng.standard_normal((4096, d)) * s).astype(np.float32)[:, perm]
     cents = np.stack([cal[rng.permutation(4096)[:256], b * 8:(b + 1) * 8] for b in range(16)])
-    cache = torch.full((1, h, cap, 16), 255, dtype=torch.uint8, device=DEV)
-    _hip.encode_blockvq(t(keys), t(perm), t(cents), cache[:, :, off:off + n], 8)
-    torch.cuda.synchronize()
-    got = cache.cpu().numpy()
-    assert (got[:, :, :off] == 255).all() and (got[:, :, off + n:] == 255).all()
     ref, near = O.encode_blockvq_c(keys.reshape(-1, d), cents, perm)
-    g = got[0, :, off:off + n].reshape(-1, 16)
     ok = ~near
-    assert np.array_equal(g[ok], ref[ok]), f"{(g[ok] != ref[ok]).sum()} mismatches"
+    ct = t(cents)
+    outs = []
+    for prep in (None, _hip.encode_codebook(ct)):  # plain and matrix-core encoders
+        cache = torch.full((1, h, cap, 16), 255, dtype=torch.uint8, device=DEV)
+        _hip.encode_blockvq(t(keys), t(perm), ct, cache[:, :, off:off + n], 8, prepared=prep)
+        torch.cuda.synchronize()
+        got = cache.cpu().numpy()
+        assert (got[:, :, :off] == 255).all() and (got[:, :, off + n:] == 255).all()
+        g = got[0, :, off:off + n].reshape(-1, 16)
+        assert np.array_equal(g[ok], ref[ok]), f"{(g[ok] != ref[ok]).sum()} mismatches"
+        outs.append(g)
+    assert np.array_equal(outs[0], outs[1])
 
 
 def test_lut_and_score_gather():
