@@ -342,7 +342,7 @@ struct EmLds {
                + (size_t)nb * 8 * 4                // permutation
                + (size_t)kEmWaves * kEmQueue * 4   // queues
                + (size_t)kEmWaves * 4              // queue lengths
-               + (size_t)kEmWaves * 256 * 4        // |y_c|^2 of each wave's block
+               + (size_t)kEmWaves * 256 * 4        // split (1-e)|y_c|^2 of each wave's block
                + (size_t)T * nb * 8 * sizeof(KT);  // the next tile's key rows
     }
 };
@@ -362,8 +362,8 @@ __global__ void __launch_bounds__(kEmWaves * kWave)
     char *kop = sm;                                                // [T][tstr]: -2 x_hi (, -2 x_lo)
     uint32_t *kck = reinterpret_cast<uint32_t *>(sm + T * tstr);   // [T][NB] split constant (fp16 hi, lo)
     float *kn2 = reinterpret_cast<float *>(kck + T * NB);          // [T][NB] |x|^2 (-1: rank exactly)
-    float *n2w = kn2 + T * NB;                                     // [kEmWaves][256] |y_c|^2
-    int *perm_l = reinterpret_cast<int *>(n2w + kEmWaves * 256);   // [NB * 8]
+    uint32_t *qw = reinterpret_cast<uint32_t *>(kn2 + T * NB);     // [kEmWaves][256] split (1-e)|y_c|^2
+    int *perm_l = reinterpret_cast<int *>(qw + kEmWaves * 256);    // [NB * 8]
     int *queue = perm_l + NB * 8;                                  // [kEmWaves][kEmQueue]
     int *qlen = queue + kEmWaves * kEmQueue;                       // [kEmWaves]
     KT *raw = reinterpret_cast<KT *>(qlen + kEmWaves);             // [T][D] key rows of the tile
@@ -373,23 +373,21 @@ __global__ void __launch_bounds__(kEmWaves * kWave)
     const int D = NB * 8;
     const int64_t n_tiles = (a.n_tok + T - 1) / T;
     const bool owner = wv < NB;  // this wave ranks block wv
+    // 16 blocks and 16-byte aligned output rows: whole rows are stored at once
+    const bool out16 = NB == 16 && ((uintptr_t)a.out % 16) == 0 && a.o_sb % 16 == 0 && a.o_sh % 16 == 0 &&
+                       a.o_st % 16 == 0;
 
     for (int j = tid; j < D; j += TH) perm_l[j] = a.perm ? min(max(a.perm[j], 0), D - 1) : j;
-    for (int j = tid; j < kEmWaves * 256; j += TH) n2w[j] = (j >> 8) < NB ? n2t[j] : 0.f;
-    // this wave's codebook operands (block wv), kept for the whole launch:
-    // Y[t] (lanes 0-31 y_hi, 32-63 y_lo of centroid 32t + lane%32) and the
-    // split (1-e)|y|^2 of that centroid
+    for (int j = tid; j < kEmWaves * 256; j += TH) qw[j] = (j >> 8) < NB ? qpk[j] : 0u;
+    // this wave's codebook operand (block wv), kept for the whole launch:
+    // Y[t] (lanes 0-31 y_hi, 32-63 y_lo of centroid 32t + lane%32)
     em_f16x8 Y[kEmTiles];
-    uint32_t Qd[kEmTiles];
     if (owner) {
 #pragma unroll
         for (int t = 0; t < kEmTiles; ++t)
-            if (t < nt) {
-                Y[t] = __builtin_bit_cast(em_f16x8, ops[((int64_t)wv * kEmTiles + t) * kWave + lane]);
-                Qd[t] = qpk[wv * 256 + 32 * t + (lane & 31)];
-            }
+            if (t < nt) Y[t] = __builtin_bit_cast(em_f16x8, ops[((int64_t)wv * kEmTiles + t) * kWave + lane]);
     }
-    const float *n2b = n2w + (owner ? wv : 0) * 256;
+    const uint32_t *qb = qw + (owner ? wv : 0) * 256;
     __syncthreads();
 
     // The tile's key rows are copied whole into LDS (global_load_lds of 16
@@ -526,7 +524,8 @@ __global__ void __launch_bounds__(kEmWaves * kWave)
                     if (FULL || t < nt) {
                         em_f32x16 Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(Y[t], B0, em_f32x16{}, 0, 0, 0);
                         if constexpr (KLO) Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(Y[t], B1, Dv, 0, 0, 0);
-                        const em_f16x8 A3 = __builtin_bit_cast(em_f16x8, uint4{Qd[t], 0x3c003c00u, 0u, 0u});
+                        const em_f16x8 A3 =
+                            __builtin_bit_cast(em_f16x8, uint4{qb[32 * t + (lane & 31)], 0x3c003c00u, 0u, 0u});
                         Dv = __builtin_amdgcn_mfma_f32_32x32x16_f16(A3, B3, Dv, 0, 0, 0);
                         const int hk = t >> 2;
 #pragma unroll
@@ -558,7 +557,11 @@ __global__ void __launch_bounds__(kEmWaves * kWave)
                 const float qk = kn2[tl * NB + b];
                 bool accept = false;
                 if (tok && qk >= 0.f && C1 < nc && t1 != o1) {
-                    const float qc = n2b[C1];
+                    // |y_c1|^2 from its split (1-e)|y|^2, rounded up
+                    const uint32_t qv = qb[C1];
+                    const float qc = ((float)__builtin_bit_cast(_Float16, (uint16_t)(qv & 0xffffu)) +
+                                      (float)__builtin_bit_cast(_Float16, (uint16_t)(qv >> 16))) *
+                                     (1.f + 2.f * kEmEps);
                     const float f1 = __uint_as_float(M1), f2 = __uint_as_float(M2);
                     const float win = fmaf(2.01f * kEmEps, qk + qc, 2.f * kEmAbs) + f2 * (1.f / 32768.f);
                     // M2 = 0xffffffff (NaN): a single centroid, nothing to beat
@@ -580,10 +583,16 @@ __global__ void __launch_bounds__(kEmWaves * kWave)
             if (it >= 0xfffe && qn > 0) flush(it);
         }
         __syncthreads();
-        for (int i = tid; i < T * NB; i += TH) {
-            const int tl = i / NB, b = i - tl * NB;
-            const int64_t n = tile * T + tl;
-            if (n < a.n_tok) a.out[token_addr(a, n).out + b] = oix[i];
+        if (out16) {  // one 16-byte store per token row
+            if (tid < T && tile * T + tid < a.n_tok)
+                *reinterpret_cast<uint4 *>(a.out + token_addr(a, tile * T + tid).out) =
+                    *reinterpret_cast<const uint4 *>(oix + tid * 16);
+        } else {
+            for (int i = tid; i < T * NB; i += TH) {
+                const int tl = i / NB, b = i - tl * NB;
+                const int64_t n = tile * T + tl;
+                if (n < a.n_tok) a.out[token_addr(a, n).out + b] = oix[i];
+            }
         }
     }
     // What is left in the queues is ranked by all 16 waves together (entry
