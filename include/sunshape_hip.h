@@ -384,6 +384,33 @@ size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_
                                             int64_t t_buf, int n_splits);
 
 /*
+ * ss_decode_attn_turboquant for 2-bit codes held token-interleaved, on the
+ * matrix cores (the same replacement of the reference's TurboQuant two-pass
+ * path, value_codecs.py:136-177 with attention.py:307-350): the LUT is built
+ * from the prepared codebook (ss_codebook_f16x2) and P.V runs as
+ * v_mfma_f32_16x16x32_bf16 products, using that a symmetric 2-bit level
+ * table is affine in the two code bits (levels[3] = levels[2] + levels[1] -
+ * levels[0], else SS_ERR_UNSUPPORTED).  Arguments as ss_decode_attn_turboquant
+ * except:
+ *   codebook  ss_codebook_f16x2 of the key centroids (16-byte aligned)
+ *   codes_il  uint32 [batch][n_kv_heads][cap/16][head_dim], the layout of
+ *             ss_decode_attn_grouped_il's 2-bit words (ss_pack_grouped_il
+ *             writes it from pack_indices rows); cap % 16 == 0
+ *   norms     float [batch][n_kv_heads][cap], 16-byte aligned
+ *   levels    HOST float[4]
+ */
+int ss_decode_attn_turboquant_il(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                 int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                 const int32_t *perm, const void *codebook, int n_blocks,
+                                 int n_centroids, const uint8_t *idx, const uint32_t *codes_il,
+                                 const float *norms, const float *levels, const float *rotation,
+                                 int64_t cap, int64_t t_kv, const void *k_buf, const void *v_buf,
+                                 int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
+                                 int64_t t_buf, int causal, int64_t q_offset, void *out,
+                                 int out_dtype, void *workspace, size_t workspace_bytes,
+                                 int n_splits, void *stream);
+
+/*
  * As ss_decode_attn_turboquant with SunShape block-VQ values (value backend
  * "sunshape", reference cache.py:614-623): token t's value is the value
  * codec's dequantisation of its indices, concat_b v_centroids[b][v_idx[t][b]]

@@ -114,6 +114,11 @@ _SIGNATURES = {
         _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _i64,
                                                      _int]),
+    "ss_decode_attn_turboquant_il": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
+        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_kmeans_blocks": (_int, [_c_void_p, _int, _i64, _int, _int, _int, _c_void_p, _c_void_p,
                                 _c_void_p]),
     "ss_decode_attn_sunshape_v": (_int, [
@@ -922,6 +927,72 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
         ptr(rotation), int(bits), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
+        bst, buf_len, int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
+    return out
+
+
+def turboquant_il_levels_ok(levels) -> bool:
+    """Whether a 2-bit level table is affine in the code bits (what the
+    matrix-core TurboQuant decode needs): L3 = L2 + L1 - L0."""
+    lv = [float(x) for x in (levels.tolist() if isinstance(levels, torch.Tensor) else levels)]
+    return len(lv) == 4 and abs(lv[3] - (lv[2] + lv[1] - lv[0])) <= 1e-6 * max(abs(lv[0]),
+                                                                               abs(lv[3]), 1e-30)
+
+
+def decode_attn_turboquant_il(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                              centroids: torch.Tensor, idx: torch.Tensor, codes_il: torch.Tensor,
+                              norms: torch.Tensor, levels, rotation: torch.Tensor, t_kv: int,
+                              causal: bool = False, q_offset: int = 0,
+                              out: torch.Tensor | None = None,
+                              out_dtype: torch.dtype | None = None, n_splits: int = 0,
+                              codebook: torch.Tensor | None = None,
+                              buf_keys: torch.Tensor | None = None,
+                              buf_values: torch.Tensor | None = None,
+                              buf_len: int = 0) -> torch.Tensor:
+    """Fused decode (matrix-core LUT and P.V) over 2-bit TurboQuant values
+    whose codes are token-interleaved (``codes_il`` (B, Hkv, cap/16, D) words,
+    written by :func:`pack_grouped_il`), ``norms`` (B, Hkv, cap) float32,
+    ``levels`` the four scaled Lloyd-Max levels (affine in the code bits),
+    ``rotation`` (D, D) with ``value = norm * (levels[code] @ rotation)``.
+    ``codebook``: :func:`codebook_f16x2` of ``centroids`` (built if None).
+    A hybrid cache's recent tokens join the softmax as in
+    :func:`decode_attn_turboquant`."""
+    _check_decode_common(q, idx, centroids, perm)
+    require_gpu(codes_il, norms, rotation)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if codes_il.dim() != 4 or not codes_il.is_contiguous() or \
+            tuple(codes_il.shape) != (b_, hkv, cap // 16, d) or \
+            codes_il.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("codes_il must be contiguous 32-bit words (B, n_kv_heads, cap/16, D)")
+    if norms.dtype != torch.float32 or not norms.is_contiguous() or \
+            tuple(norms.shape) != tuple(idx.shape[:3]):
+        raise ValueError("norms must be contiguous float32 (B, n_kv_heads, cap)")
+    if rotation.dtype != torch.float32 or not rotation.is_contiguous() or \
+            tuple(rotation.shape) != (d, d):
+        raise ValueError(f"rotation must be contiguous float32 ({d}, {d})")
+    lv = [float(x) for x in (levels.tolist() if isinstance(levels, torch.Tensor) else levels)]
+    if len(lv) != 4:
+        raise ValueError(f"4 levels expected for 2-bit codes, got {len(lv)}")
+    lv_host = (ctypes.c_float * 4)(*lv)
+    nc = centroids.shape[1]
+    if codebook is None:
+        codebook = codebook_f16x2(centroids)
+    if out is None:
+        out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    buf_len = int(buf_len)
+    buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
+                                                            b_, hkv, d)
+    lib = load_library()
+    ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
+                                                        int(n_splits))
+    ws = decode_workspace(q.device, ws_bytes)
+    _launched(_attn_stat("sunshape_fused_attention_turboquant", causal),
+              lib.ss_decode_attn_turboquant_il(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+        nb, nc, ptr(idx), ptr(codes_il), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
+        ptr(rotation), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
         bst, buf_len, int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
         ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
     return out

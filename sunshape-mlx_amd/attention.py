@@ -89,8 +89,9 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     codec = cache.codec
     buffered = cache.buffer_offset if isinstance(cache, HybridSunShapeKVCache) else 0
     # the buffer joins the fused softmax on the interleaved fp16, grouped
-    # interleaved, TurboQuant and SunShape-value kernels
-    if buffered and ops["kind"] not in ("il8", "grouped_il", "turboquant", "sunshape_v"):
+    # interleaved, TurboQuant (both layouts) and SunShape-value kernels
+    if buffered and ops["kind"] not in ("il8", "grouped_il", "turboquant_il", "turboquant",
+                                        "sunshape_v"):
         return None
     q, kscale, perm = _kernel_query(codec, queries, scale)
     if buffered and codec.mode not in PERM_MODES and codec.use_rotation:
@@ -143,6 +144,15 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
                                               buf_len=buffered, **kw)
             codec.last_score_backend = ("hip_fused_mfma_dequant_buffer" if buffered
                                         else "hip_fused_mfma_dequant")
+        elif kind == "turboquant_il":
+            out = _hip.decode_attn_turboquant_il(q, kscale, perm, codec.centroids, ops["idx"],
+                                                 ops["codes_il"], ops["norms"], ops["levels"],
+                                                 ops["rotation"], codebook=codec.kernel_codebook(),
+                                                 buf_keys=ops["buf_keys"],
+                                                 buf_values=ops["buf_values"], buf_len=buffered,
+                                                 **kw)
+            codec.last_score_backend = ("hip_fused_mfma_turboquant_buffer" if buffered
+                                        else "hip_fused_mfma_turboquant")
         elif ops["kind"] == "turboquant":
             out = _hip.decode_attn_turboquant(q, kscale, perm, codec.centroids, ops["idx"],
                                               ops["packed"], ops["norms"], ops["levels"],

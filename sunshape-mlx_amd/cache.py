@@ -331,6 +331,12 @@ class HybridSunShapeKVCache:
         self._grouped_il = (self.value_backend == "grouped" and
                             _grouped_il_ok(codec, self.head_dim, self.value_bits or 0,
                                            self.value_group_size))
+        # 2-bit TurboQuant codes held token-interleaved as well (the layout of
+        # the matrix-core TurboQuant decode, whose level table must be affine
+        # in the code bits)
+        self._turbo_il = (self.value_backend == "turboquant" and self.value_bits == 2 and
+                          _grouped_il_ok(codec, self.head_dim, 2, self.head_dim) and
+                          _hip.turboquant_il_levels_ok(self._value_codec_impl.levels_host()))
 
     @property
     def offset(self) -> int:
@@ -364,8 +370,12 @@ class HybridSunShapeKVCache:
                                       self.value_scale_dtype, device, keep)
         elif self.value_backend == "turboquant":
             tc = self._value_codec_impl
-            self._values_packed = _grow(self._values_packed, (b_, h_, cap, tc.packed_dim),
-                                        torch.int32, device, keep)
+            if self._turbo_il:
+                self._values_il = _grow(self._values_il, (b_, h_, cap // 16, self.head_dim),
+                                        torch.int32, device, (keep + 15) // 16)
+            else:
+                self._values_packed = _grow(self._values_packed, (b_, h_, cap, tc.packed_dim),
+                                            torch.int32, device, keep)
             norms = self._value_norms
             self._value_norms = torch.zeros((b_, h_, cap), dtype=torch.float32, device=device)
             if norms is not None and keep:
@@ -420,8 +430,11 @@ class HybridSunShapeKVCache:
         elif self.value_backend == "turboquant":
             tc = self._value_codec_impl
             packed, norms = tc.quantize(vf.float().reshape(-1, self.head_dim))
-            self._values_packed[:, :, c0:c1] = packed.view(torch.int32).reshape(
-                b_, self.n_kv_heads, n, -1)
+            rows = packed.view(torch.int32).reshape(b_, self.n_kv_heads, n, -1)
+            if self._turbo_il:
+                _hip.pack_grouped_il(rows, 2, self._values_il, c0)
+            else:
+                self._values_packed[:, :, c0:c1] = rows
             self._value_norms[:, :, c0:c1] = norms.reshape(b_, self.n_kv_heads, n)
             self.last_value_quant_backend = tc.last_quantize_backend
         elif self.value_backend == "sunshape":
@@ -498,9 +511,13 @@ class HybridSunShapeKVCache:
                                                self._value_zeros[:, :, :tc_], self.head_dim,
                                                gc.bits, gc.group_size)
             return v.to(self.dtype)
-        if self.value_backend == "turboquant" and self._values_packed is not None:
+        if self.value_backend == "turboquant" and (self._values_packed is not None or
+                                                   self._values_il is not None):
             tc = self._value_codec_impl
-            p = self._values_packed[:, :, :tc_].view(torch.uint32)
+            if self._values_il is not None:
+                p = _hip.grouped_il_to_packed(self._values_il, 2, tc_).contiguous()
+            else:
+                p = self._values_packed[:, :, :tc_].view(torch.uint32)
             v = tc.dequantize(p.reshape(-1, p.shape[-1]), self._value_norms[:, :, :tc_].reshape(-1))
             return v.reshape(p.shape[0], p.shape[1], tc_, self.head_dim).to(self.dtype)
         if self.value_backend == "sunshape" and self._value_indices is not None:
@@ -580,7 +597,8 @@ class HybridSunShapeKVCache:
 
     def fused_operands(self) -> dict | None:
         """Full-capacity compressed buffers for the fused decode kernels
-        ({"kind": "grouped_il"|"grouped"|"turboquant"|"sunshape_v"|"dense", ...});
+        ({"kind": "grouped_il"|"grouped"|"turboquant_il"|"turboquant"|"sunshape_v"|"il8"|"dense",
+        ...});
         None when there is nothing compressed or the value backend has no
         fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
@@ -599,6 +617,13 @@ class HybridSunShapeKVCache:
                     "packed": self._values_packed.view(torch.uint32),
                     "scales": self._value_scales, "zeros": self._value_zeros,
                     "bits": gc.bits, "group_size": gc.group_size}
+        if self.value_backend == "turboquant" and self._values_il is not None:
+            tc = self._value_codec_impl
+            tc._on(self._values_il.device)
+            return {"kind": "turboquant_il", "idx": self._key_indices, "codes_il": self._values_il,
+                    "norms": self._value_norms, "levels": tc.levels_host(),
+                    "rotation": tc.rotation,
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
         if self.value_backend == "turboquant" and self._values_packed is not None:
             tc = self._value_codec_impl
             tc._on(self._values_packed.device)

@@ -375,6 +375,10 @@ struct VfHeavy<VF, std::void_t<decltype(VF::kHeavyKeys)>> {
     static constexpr bool value = VF::kHeavyKeys;
 };
 template <class VF, class = void>
+struct VfArgsToLds : std::false_type {};  // the format's accumulator hand-off reads its Args
+template <class VF>
+struct VfArgsToLds<VF, std::void_t<decltype(&VF::to_lds_args)>> : std::true_type {};
+template <class VF, class = void>
 struct VfScaled {  // the format scales each token's weight (VF::token_scale)
     static constexpr bool value = false;
 };
@@ -1309,6 +1313,202 @@ struct VGil {
     }
 };
 
+// TurboQuant 2-bit values (reference value_codecs.py:136-177) on the matrix
+// cores: per token a norm and 2-bit codes of the rotated unit vector, held
+// token-interleaved as VGil's words ([cap/16][D] per (b, h)); norms [cap].
+// The value is norm * L(code) with the four Lloyd-Max levels L ascending.  A
+// symmetric table is affine in the two code bits:
+//   L(c) = L0 + (L1 - L0) c + (L2 - 2 L1 + L0) bit1(c)        (L3 = L2 + L1 - L0)
+// so P.V = L0 sum w + (L1 - L0) sum w c + (L2 - 2 L1 + L0) sum w bit1 with
+// w = p * norm: VGil's products (A = w as bf16 hi/lo rows, B = 128 + code)
+// give sum w c, one more product per (k-step, N-tile) with B = 128 + 2 bit1
+// (the bit left in place, the same per-token powers of two as the codes)
+// gives sum w bit1, and sum w accumulates in fp32 on the lanes.  Rows 8-15 of A are
+// unused (one group per row).  The accumulation is in the rotated basis; the
+// rotation is applied per output row after the merge (transformed_decode).
+template <int D>
+struct VTq {
+    struct Args {
+        const uint32_t *codes;  // token-interleaved 2-bit words
+        const float *norms;     // [rows]
+        float l0, l1, l2;       // levels L0, L1 - L0, L2 - 2 L1 + L0
+    };
+    static constexpr int NT = D / 16;
+    static constexpr int BITS = 2, TPW = 16;
+    static constexpr int kCodeBytes1 = kWave * D * BITS / 8;  // 2 KB at D = 128
+    static constexpr int kSzBytes1 = kWave * 4;               // the 64 norms
+    static constexpr bool kPrivateRing = true;
+    static constexpr int kSub = 1;
+    static constexpr int kCodeBytes = kCodeBytes1;
+    static constexpr int kSzBytes = kSzBytes1;
+    static constexpr bool kHybridBuffer = false;  // the buffer joins as its own rotated partial
+    static constexpr int kTileV = kCodeBytes + 1024;
+    static constexpr int kLoadsV = kCodeBytes / 1024 + 1;
+    static constexpr int kPRows = 16;
+    static constexpr int kMaxSlots = 16;
+    static constexpr int kComputeWaves = 8;
+    static constexpr uint32_t kCodeMask = 0x00030003u;
+    static constexpr uint32_t kBit1Mask = 0x00020002u;
+    static constexpr uint32_t kBias = 0x43004300u;  // two bf16 128.0
+    static_assert(NT == 8 || NT == 4, "n-tiles");
+    struct Tile {
+        uint32_t cw[2][NT];  // as VGil: the lane's 8 tokens of dims 8*(lane%16) + n
+        float n;             // norm of token `lane`
+    };
+    struct State {
+        f32x4 bias;          // 128 * sum of the staged A rows, laid out as acc
+        f32x4 b1[NT];        // sum_t A (128 + 2 bit1)
+        float ws[kMfmaRows]; // sum of p * norm of this lane's tokens
+    };
+    __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+                                 uint32_t sb, int lane) {
+        const char *chead = reinterpret_cast<const char *>(a.codes + bh * (cap / TPW) * D);
+        const char *np = reinterpret_cast<const char *>(a.norms + bh * cap + t0);
+        const int64_t wb0 = t0 / TPW;
+        if (t0 + kWave - 1 <= t_last) {
+            const char *cb = chead + wb0 * D * 4;
+#pragma unroll
+            for (int i = 0; i < kCodeBytes / 1024; ++i)
+                __builtin_amdgcn_global_load_lds(cb + (uint32_t)(i * 1024 + lane * 16),
+                                                 reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                                 kCpolNt);
+            if (lane < kSzBytes / 16)
+                __builtin_amdgcn_global_load_lds(np + lane * 16,
+                                                 reinterpret_cast<lds_t<void> *>(sb + kCodeBytes), 16, 0,
+                                                 kCpolNt);
+            return;
+        }
+        // past the split's last token: code chunks clamp to its block, norm
+        // chunks to the one holding it
+        const int64_t blk_last = t_last / TPW;
+#pragma unroll
+        for (int i = 0; i < kCodeBytes / 1024; ++i) {
+            const int w = (i * kWave + lane) * 4;
+            const int64_t blk = min(wb0 + w / D, blk_last);
+            __builtin_amdgcn_global_load_lds(chead + (blk * D + w % D) * 4,
+                                             reinterpret_cast<lds_t<void> *>(sb + i * 1024), 16, 0,
+                                             kCpolNt);
+        }
+        const int64_t ch_last = (t_last - t0) / 4;
+        if (lane < kSzBytes / 16)
+            __builtin_amdgcn_global_load_lds(np + min((int64_t)lane, ch_last) * 16,
+                                             reinterpret_cast<lds_t<void> *>(sb + kCodeBytes), 16, 0,
+                                             kCpolNt);
+    }
+    __device__ static void copy(Tile &tv, const char *sb, int sub, int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int tk = 32 * ks + 8 * g;
+            const uint32_t *src = reinterpret_cast<const uint32_t *>(sb) + (tk / TPW) * D + (NT * l16) % D;
+            uint32_t w[NT];
+            if constexpr (NT == 8) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(src);
+                const uint4 b = *reinterpret_cast<const uint4 *>(src + 4);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+                w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+            } else {
+                const uint4 a = *reinterpret_cast<const uint4 *>(src);
+                w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+            }
+            const int sh = 8 * (g & 1);  // the lane's 8 tokens: odd or even byte of each half
+#pragma unroll
+            for (int n = 0; n < NT; ++n) tv.cw[ks][n] = w[n] >> sh;
+        }
+        tv.n = reinterpret_cast<const float *>(sb + kCodeBytes)[lane];
+        (void)sub;
+    }
+    __device__ static void init(State &st) {
+        st.bias = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int n = 0; n < NT; ++n) st.b1[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; ++r) st.ws[r] = 0.f;
+    }
+    __device__ static void pv(Tile &tv, State &st, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
+                              const float (&corr)[kMfmaRows], bool rescale, int n_in, _Float16 *pw16,
+                              int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        uint16_t *pw = reinterpret_cast<uint16_t *>(pw16);
+        float s = tv.n;
+        if (n_in < kWave) s = lane < n_in ? s : 0.f;  // past the split end: p = 0, norm unwritten
+        if (rescale) {
+            const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                acc[n] *= cv4;
+                st.b1[n] *= cv4;
+            }
+            st.bias *= cv4;
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r) st.ws[r] *= corr[r];
+        }
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; ++r) st.ws[r] = fmaf(p[r], s, st.ws[r]);
+        // the codes of dwords 1 and 2 of a lane's 8 tokens stay in place
+        // (x4, x16): those tokens' weights carry 1/4 and 1/16 (as VGil)
+        const int jt = (lane >> 1) & 3;
+        const float sw = s * (jt == 1 ? 0.25f : (jt == 2 ? 0.0625f : 1.f));
+#pragma unroll
+        for (int r = 0; r < kMfmaRows; r += 2) {
+            const float w0 = p[r] * sw, w1 = p[r + 1] * sw;
+            const uint32_t hi = bf16x2_rn(w0, w1);
+            const float l0 = w0 - __uint_as_float(hi << 16);
+            const float l1 = w1 - __uint_as_float(hi & 0xffff0000u);
+            const uint32_t lo = bf16x2_rn(l0, l1);
+            pw[r * kPStride + lane] = (uint16_t)hi;
+            pw[(r + 1) * kPStride + lane] = (uint16_t)(hi >> 16);
+            pw[(4 + r) * kPStride + lane] = (uint16_t)lo;
+            pw[(4 + r + 1) * kPStride + lane] = (uint16_t)(lo >> 16);
+        }
+        wave_lds_sync();
+        const uint32_t cm = opaque_u32(kCodeMask), cbias = opaque_u32(kBias);
+        const uint32_t cm2 = opaque_u32(kCodeMask << 2), cm4 = opaque_u32(kCodeMask << 4);
+        const uint32_t bm = opaque_u32(kBit1Mask), bm2 = opaque_u32(kBit1Mask << 2),
+                       bm4 = opaque_u32(kBit1Mask << 4);
+        const bf16x8 b128 = __builtin_bit_cast(bf16x8, make_uint4(cbias, cbias, cbias, cbias));
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(pw + l16 * kPStride + 32 * ks + 8 * g);
+            st.bias = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b128, st.bias, 0, 0, 0);
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const uint32_t y = tv.cw[ks][n];
+                const uint32_t y6 = y >> 6;
+                const bf16x8 bc = __builtin_bit_cast(
+                    bf16x8, make_uint4((y & cm) | cbias, (y & cm2) | cbias, (y & cm4) | cbias, (y6 & cm) | cbias));
+                const bf16x8 bb = __builtin_bit_cast(
+                    bf16x8, make_uint4((y & bm) | cbias, (y & bm2) | cbias, (y & bm4) | cbias, (y6 & bm) | cbias));
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bc, acc[n], 0, 0, 0);
+                st.b1[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb, st.b1[n], 0, 0, 0);
+            }
+        }
+        wave_lds_sync();
+    }
+    // rows 0-3 (lanes 0-15) hold the hi parts, rows 4-7 (lanes 16-31) the lo
+    // parts of the four query rows: acc - bias = sum w c and (b1 - bias)/2 =
+    // sum w bit1 of each part (the A rows carry w times the in-place powers
+    // of two, the bias the same).  The L0 sum w term, from the lanes' fp32
+    // sums of p * norm, goes with the hi part.
+    __device__ static void to_lds_args(const f32x4 (&acc)[NT], const State &st, const Args &a, float *wa,
+                                       int lane) {
+        const int g = lane >> 4, l16 = lane & 15;
+        float wsum[kMfmaRows];
+        wave_sum4_dpp(st.ws, wsum);
+        if (g < 2) {
+#pragma unroll
+            for (int r = 0; r < kMfmaRows; ++r) {
+                const float bz = st.bias[r];
+                const float c0 = g == 0 ? a.l0 * wsum[r] : 0.f;
+#pragma unroll
+                for (int n = 0; n < NT; ++n)
+                    wa[(g * kMfmaRows + r) * D + NT * l16 + n] =
+                        c0 + a.l1 * (acc[n][r] - bz) + a.l2 * 0.5f * (st.b1[n][r] - bz);
+            }
+        }
+    }
+};
+
 template <int D, int NC, class VF>
 __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     decode_attn_mfma_kernel(DecodeCommon c, typename VF::Args va) {
@@ -1857,7 +2057,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 wl[wv * R + r] = lsum[r];
             }
         }
-        VF::to_lds(acc, vst, wa + wv * 2 * R * D, lane);
+        if constexpr (VfArgsToLds<VF>::value)
+            VF::to_lds_args(acc, vst, va, wa + wv * 2 * R * D, lane);
+        else
+            VF::to_lds(acc, vst, wa + wv * 2 * R * D, lane);
     }
     __syncthreads();
     // combine the compute waves' (m, l, acc) of row r into this workgroup's
@@ -3104,8 +3307,15 @@ extern "C" size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_he
                                                        int64_t t_kv, int64_t t_buf, int n_splits) {
     if (batch < 1 || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads % n_kv_heads || t_q < 1)
         return 0;
-    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
-    return turboquant_ws_bytes(with_buffer_slot(s, t_buf), batch * n_q_heads * t_q, head_dim);
+    // enough for every split policy of the transformed-basis decodes (the
+    // VALU kernel's, the matrix-core TurboQuant and SunShape-value kernels')
+    size_t need = 0;
+    for (int kind : {kKindValu, kKindMfma, kKindSunv}) {
+        const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits, kind);
+        need = std::max(need, turboquant_ws_bytes(with_buffer_slot(s, t_buf), batch * n_q_heads * t_q,
+                                                  head_dim));
+    }
+    return need;
 }
 
 // Shared host side of the decodes whose values accumulate in a transformed
@@ -3635,4 +3845,60 @@ extern "C" int ss_decode_attn_grouped_il_hybrid(
                            bits, group_size, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
                            workspace_bytes, n_splits, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
                            buf_st, t_buf, stream);
+}
+
+extern "C" int ss_decode_attn_turboquant_il(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint32_t *codes_il, const float *norms,
+    const float *levels, const float *rotation, int64_t cap, int64_t t_kv, const void *k_buf,
+    const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
+    int causal, int64_t q_offset, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+    int n_splits, void *stream) {
+    const float *cents = static_cast<const float *>(codebook);
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents, n_blocks,
+                          n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(codes_il && norms && levels && rotation, "null codes/norms/levels/rotation");
+    SS_REQUIRE(cap % 16 == 0, "cap must be a multiple of 16 for interleaved 2-bit codes");
+    SS_REQUIRE(((uintptr_t)codes_il % 16) == 0 && ((uintptr_t)norms % 16) == 0,
+               "codes and norms must be 16-byte aligned");
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
+    // the levels must be affine in the two code bits (a symmetric table)
+    const float lmax = fmaxf(fmaxf(fabsf(levels[0]), fabsf(levels[3])), 1e-30f);
+    SS_UNSUPPORTED(fabsf(levels[3] - (levels[2] + levels[1] - levels[0])) <= 1e-6f * lmax,
+                   "2-bit levels are not affine in the code bits (L3 != L2 + L1 - L0)");
+    typename VTq<128>::Args va128{codes_il, norms, levels[0], levels[1] - levels[0],
+                                  levels[2] - 2.f * levels[1] + levels[0]};
+    auto main = [&](const DecodeCommon &c0, const DecodeShape &s, hipStream_t st) -> int {
+        DecodeCommon c = c0;
+        c.centroids = nullptr;
+        c.codebook = static_cast<const uint4 *>(codebook);
+        c.codebook_mul = reinterpret_cast<const float *>(
+            static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+        c.fused_merge = 0;  // transformed_decode merges (buffer partial, rotation)
+        auto go = [&](auto dd) -> int {
+            constexpr int DD = decltype(dd)::value;
+            using VF = VTq<DD>;
+            constexpr int NC = VF::kComputeWaves;
+            using K = WsCfg<DD, NC, VF>;
+            auto kern = decode_attn_mfma_kernel<DD, NC, VF>;
+            static bool attr_set = false;
+            if (!attr_set) {
+                const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, K::kLds);
+                if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode turboquant mfma)");
+                attr_set = true;
+            }
+            const typename VF::Args va{va128.codes, va128.norms, va128.l0, va128.l1, va128.l2};
+            hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(K::kWaves * kWave), K::kLds, st, c, va);
+            SS_LAUNCH_CHECK("decode_attn_mfma_kernel (turboquant) launch");
+            return SS_OK;
+        };
+        return head_dim == 128 ? go(std::integral_constant<int, 128>{}) : go(std::integral_constant<int, 64>{});
+    };
+    return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm, cents,
+                              n_centroids, idx, cap, t_kv, rotation, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
+                              buf_st, t_buf, causal, q_offset, out, out_dtype, workspace, workspace_bytes,
+                              n_splits, stream, main, kKindMfma);
 }

@@ -159,6 +159,16 @@ def load_cache(path: str, device=None):
             setattr(cache, name, tensors[key].to(dev))
     for k, v in json.loads(meta["cache_scalars"]).items():
         setattr(cache, k, int(v))
+    if kind == "HybridSunShapeKVCache" and cache._turbo_il and cache._values_packed is not None:
+        # 2-bit TurboQuant codes written as packed rows (files of earlier
+        # versions): interleave them as the cache now keeps them
+        rows = cache._values_packed
+        b_, h_, cap, _ = rows.shape
+        cache._values_il = torch.zeros((b_, h_, cap // 16, cache.head_dim), dtype=torch.int32,
+                                       device=rows.device)
+        if cache._compressed_offset:
+            _hip.pack_grouped_il(rows[:, :, :cache._compressed_offset], 2, cache._values_il, 0)
+        cache._values_packed = None
     if kind == "HybridSunShapeKVCache" and cache._fp16_il8 and cache._values_fp16 is not None:
         # fp16 values written token-major (files of earlier versions): move
         # them into the interleaved layout the cache now keeps

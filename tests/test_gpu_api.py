@@ -479,7 +479,15 @@ def test_turboquant_value_codec_matches_oracle(bits):
     assert rel_err(rec, ref_rec) <= 1e-5
 
 
-@pytest.mark.parametrize("bits,t_q", [(2, 1), (3, 1), (4, 3)])
+def _tq_rows(cache, n):
+    """The cache's TurboQuant codes of its first n compressed tokens as
+    reference packed rows (uint32), whichever layout it keeps."""
+    if cache._values_il is not None:
+        return S._hip.grouped_il_to_packed(cache._values_il, 2, n).cpu().numpy().view(np.uint32)
+    return cache._values_packed[:, :, :n].cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("bits,t_q", [(2, 1), (3, 1), (4, 3), (2, 3)])
 def test_hybrid_turboquant_fused_decode(bits, t_q):
     """A hybrid cache with TurboQuant values and no buffered tokens decodes in
     one fused launch (plus the row rotation) instead of dequantising the
@@ -495,9 +503,12 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
     q = torch.randn((b, hq, t_q, d), device=DEV).to(torch.float16)
     mask = "causal" if t_q > 1 else None
     out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
-    assert codec.last_score_backend == "hip_fused_turboquant"
+    # 2-bit codes: token-interleaved, matrix-core P.V
+    mfma = "mfma_" if bits == 2 else ""
+    assert (cache._values_il is not None) == (bits == 2)
+    assert codec.last_score_backend == f"hip_fused_{mfma}turboquant"
     tc = cache._value_codec_impl
-    vals = O.turboquant_decode(cache._values_packed[:, :, :n].cpu().numpy().view(np.uint32),
+    vals = O.turboquant_decode(_tq_rows(cache, n),
                                cache._value_norms[:, :, :n].cpu().numpy(),
                                tc.rotation.cpu().numpy(), tc.centroids.cpu().numpy(), d, bits)
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
@@ -511,8 +522,8 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
     nc, nb = cache2.compressed_offset, cache2.buffer_offset
     assert nb == 128 and nc == n - 128
     out2 = S.sunshape_sdpa(q, cache2, 0.088, mask=mask)
-    assert codec.last_score_backend == "hip_fused_turboquant_buffer"
-    vals2 = O.turboquant_decode(cache2._values_packed[:, :, :nc].cpu().numpy().view(np.uint32),
+    assert codec.last_score_backend == f"hip_fused_{mfma}turboquant_buffer"
+    vals2 = O.turboquant_decode(_tq_rows(cache2, nc),
                                 cache2._value_norms[:, :, :nc].cpu().numpy(),
                                 tc.rotation.cpu().numpy(), tc.centroids.cpu().numpy(), d, bits)
     vals_all = np.concatenate([vals2, v[:, :, nc:].float().cpu().numpy()], axis=2)
@@ -521,7 +532,8 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
                            cache2.buffer_keys.float().cpu().numpy(), vals_all, mask=mask)
     assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
     # the value codec's own dequantisation gives the same cache contents
-    rec = tc.dequantize(cache._values_packed[:, :, :n].reshape(-1, tc.packed_dim),
+    rows = torch.from_numpy(_tq_rows(cache, n).view(np.int32)).to(DEV)
+    rec = tc.dequantize(rows.reshape(-1, tc.packed_dim),
                         cache._value_norms[:, :, :n].reshape(-1)).cpu().numpy()
     assert rel_err(rec.reshape(vals.shape), vals) <= 1e-5
 

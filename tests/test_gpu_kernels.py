@@ -690,6 +690,64 @@ def test_decode_turboquant_with_buffer(b, hq, hkv, d, t_kv, t_buf, t_q, bits, sp
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,t_q,causal,splits,peak", [
+    (1, 32, 8, 128, 4096, 0, 1, False, 0, False),   # config-2 heads
+    (8, 32, 8, 128, 2000, 128, 1, False, 0, False),  # config-4 heads, hybrid buffer
+    (1, 8, 2, 64, 517, 0, 1, False, 3, False),      # head_dim 64, ragged T, 3 splits
+    (2, 6, 2, 128, 300, 20, 5, True, 1, False),     # prefill rows, causal across the buffer
+    (1, 8, 2, 128, 1000, 0, 1, False, 0, True),     # sharper softmax (query x 4)
+    (1, 4, 1, 128, 0, 40, 1, False, 0, False),      # buffer only
+    (1, 4, 1, 128, 0, 0, 1, False, 0, False),       # empty cache: zeros
+])
+def test_decode_turboquant_il_matches_oracle(b, hq, hkv, d, t_kv, t_buf, t_q, causal, splits,
+                                             peak):
+    """ss_decode_attn_turboquant_il (2-bit codes token-interleaved, P.V on the
+    matrix cores through the bit-affine split of the level table): equals the
+    oracle over the TurboQuant-dequantised cache, with the hybrid buffer as the
+    two-pass oracle's trailing tokens."""
+    cap = max(((t_kv + 15) // 16) * 16, 16)
+    cents, perm, idx, _, q = decode_case(80 + t_kv + t_buf, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(t_kv + 3 * t_buf + 11)
+    codes = rng.integers(0, 4, (b, hkv, cap, d)).astype(np.uint8)
+    packed = O.pack_indices(codes, 2).astype(np.uint32)
+    norms = (rng.random((b, hkv, cap)) * 3 + 0.1).astype(np.float32)
+    levels = (O.lloyd_max_gaussian(2)[0] / np.sqrt(d)).astype(np.float32)
+    rot = O.rotation_matrix(d, 43)
+    scale = 1.0 / np.sqrt(d)
+    if peak and t_kv:
+        # row r of every head sees one token whose key scores far above the rest
+        q = q.astype(np.float32) * 4
+        q = q.astype(np.float16)
+    codes_il = torch.zeros((b, hkv, cap // 16, d), dtype=torch.int32, device=DEV)
+    _hip.pack_grouped_il(t(packed.view(np.int32)), 2, codes_il, 0)
+    kb = rng.standard_normal((b, hkv, t_buf + 5, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 5, d)).astype(np.float16)
+    total = t_kv + t_buf
+    out = _hip.decode_attn_turboquant_il(t(q), scale, t(perm), t(cents), t(idx), codes_il,
+                                         t(norms), levels, t(rot), t_kv, causal=causal,
+                                         q_offset=total - t_q if causal else 0,
+                                         out_dtype=torch.float32, n_splits=splits,
+                                         buf_keys=t(kb) if t_buf else None,
+                                         buf_values=t(vb) if t_buf else None, buf_len=t_buf)
+    torch.cuda.synchronize()
+    _hip.check_decode_waits()
+    got = out.cpu().numpy()
+    if total == 0:
+        assert not got.any()
+        return
+    vals = np.zeros((b, hkv, total, d), np.float64)
+    if t_kv:
+        vals[:, :, :t_kv] = O.turboquant_decode(packed[:, :, :t_kv], norms[:, :, :t_kv], rot,
+                                                levels, d, 2)
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                          mask="causal" if causal else None)
+    assert rel_err(got, ref) <= REL_TOL
+    # the interleaved words hold the packed rows' codes
+    back = _hip.grouped_il_to_packed(codes_il, 2, cap).cpu().numpy().view(np.uint32)
+    assert np.array_equal(back, packed)
+
+
 @pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,t_q,bd,vnc,transform,splits", [
     (1, 32, 8, 128, 2048, 0, 1, 4, 256, "perm", 0),     # config-5 value codec (block_dim 4)
     (2, 8, 2, 128, 700, 128, 1, 8, 256, "perm", 0),     # block_dim 8, with a buffer
