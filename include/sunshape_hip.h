@@ -76,7 +76,7 @@ int ss_encode_blockvq(const void *keys, int keys_dtype, int64_t n_b, int64_t n_h
  * reads the float32 centroids on every call).  centroids float32
  * [n_blocks <= 16][n_centroids <= 256][8].  Per block b: a power-of-two scale
  * s_b bringing the largest |centroid element| into [8, 16) (0 when the
- * block holds a non-finite value), the MFMA operand of every 16-centroid
+ * block holds a non-finite value), the MFMA operand of every 32-centroid
  * tile (fp16 s_b*C split into hi and lo, and the split (1 - 2^-15)|s_b C|^2),
  * the squared norms |s_b C|^2 and their maximum.  ss_encode_codebook_bytes
  * gives the size; prepared must be 16-byte aligned.
@@ -90,7 +90,7 @@ int ss_encode_codebook(const float *centroids, int n_blocks, int n_centroids, in
  * arguments, same indices; replaces block_vq_quantize_metal, reference
  * kernels.py:1037-1082).  Bulk encodes (block_dim 8, n_blocks <= 16, more
  * than 4096 (token, block) pairs) rank the codebook on the matrix cores:
- * a lower bound of every squared distance from v_mfma_f32_16x16x32_f16,
+ * a lower bound of every squared distance from v_mfma_f32_32x32x16_f16,
  * accepted when its runner-up clears the float error bound, otherwise the
  * block is ranked exactly as ss_encode_blockvq does.  Other shapes run the
  * ss_encode_blockvq kernels; prepared may then be null.
@@ -257,6 +257,17 @@ int ss_decode_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
  * No reference counterpart: the reference takes a buffered hybrid cache to
  * its two-pass path (attention.py:238, 307-350), whose result this equals
  * within the decode tolerance.  t_buf = 0 is ss_decode_attn_il8.
+ *   k_heavy  NULL, or fp16 [batch][n_kv_heads][cap][n_heavy_dims] (16-byte
+ *            aligned rows, n_heavy_dims a multiple of 8, at most 32): the
+ *            heavy blocks' key dims of a mixed-precision codec (codec basis,
+ *            dims heavy_dims[], device int32), scored exactly on the matrix
+ *            cores beside the LUT; the codebook must then hold zeros for
+ *            those blocks (as SunShapeBlockCodec.scoring_centroids does).
+ *            The same arguments follow t_buf in ss_decode_attn_grouped_il_hybrid
+ *            (not for 4-bit codes at head_dim 128: SS_ERR_UNSUPPORTED),
+ *            ss_decode_attn_turboquant_il (at most 32 dims) and
+ *            ss_decode_attn_turboquant (at most 64; there the float32
+ *            centroids' heavy blocks are skipped by the kernel).
  */
 int ss_decode_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                               int n_kv_heads, int64_t t_q, int head_dim, float scale,
@@ -264,9 +275,10 @@ int ss_decode_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q
                               int n_centroids, const uint8_t *idx, const void *values_il8,
                               int v_dtype, int64_t cap, int64_t t_kv, const void *k_buf,
                               const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
-                              int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset,
-                              void *out, int out_dtype, void *workspace, size_t workspace_bytes,
-                              int n_splits, void *stream);
+                              int64_t buf_st, int64_t t_buf, const void *k_heavy,
+                              const int32_t *heavy_dims, int n_heavy_dims, int causal,
+                              int64_t q_offset, void *out, int out_dtype, void *workspace,
+                              size_t workspace_bytes, int n_splits, void *stream);
 
 /*
  * Causal (or unmasked) attention of a prompt's T_q query rows per head
@@ -376,9 +388,11 @@ int ss_decode_attn_turboquant(const void *q, int q_dtype, int64_t batch, int n_q
                               const float *norms, const float *levels, const float *rotation,
                               int bits, int64_t cap, int64_t t_kv, const void *k_buf,
                               const void *v_buf, int buf_dtype, int64_t buf_sb,
-                              int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal,
-                              int64_t q_offset, void *out, int out_dtype, void *workspace,
-                              size_t workspace_bytes, int n_splits, void *stream);
+                              int64_t buf_sh, int64_t buf_st, int64_t t_buf,
+                              const void *k_heavy, const int32_t *heavy_dims, int n_heavy_dims,
+                              int causal, int64_t q_offset, void *out, int out_dtype,
+                              void *workspace, size_t workspace_bytes, int n_splits,
+                              void *stream);
 size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
                                             int64_t t_q, int head_dim, int64_t t_kv,
                                             int64_t t_buf, int n_splits);
@@ -406,7 +420,8 @@ int ss_decode_attn_turboquant_il(const void *q, int q_dtype, int64_t batch, int 
                                  const float *norms, const float *levels, const float *rotation,
                                  int64_t cap, int64_t t_kv, const void *k_buf, const void *v_buf,
                                  int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
-                                 int64_t t_buf, int causal, int64_t q_offset, void *out,
+                                 int64_t t_buf, const void *k_heavy, const int32_t *heavy_dims,
+                                 int n_heavy_dims, int causal, int64_t q_offset, void *out,
                                  int out_dtype, void *workspace, size_t workspace_bytes,
                                  int n_splits, void *stream);
 
@@ -494,9 +509,11 @@ int ss_decode_attn_grouped_il_hybrid(const void *q, int q_dtype, int64_t batch, 
                                      const void *zeros, int sz_dtype, int bits, int group_size,
                                      int64_t cap, int64_t t_kv, const void *k_buf,
                                      const void *v_buf, int buf_dtype, int64_t buf_sb,
-                                     int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal,
-                                     int64_t q_offset, void *out, int out_dtype, void *workspace,
-                                     size_t workspace_bytes, int n_splits, void *stream);
+                                     int64_t buf_sh, int64_t buf_st, int64_t t_buf,
+                                     const void *k_heavy, const int32_t *heavy_dims,
+                                     int n_heavy_dims, int causal, int64_t q_offset, void *out,
+                                     int out_dtype, void *workspace, size_t workspace_bytes,
+                                     int n_splits, void *stream);
 
 /*
  * Repack grouped codes (pack_indices words, one row of packed_dim words per

@@ -88,8 +88,8 @@ _SIGNATURES = {
     "ss_decode_attn_il8_hybrid": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _int, _i64, _i64,
-        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
-        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_prefill_rows_per_workgroup": (_int, []),
     "ss_prefill_attn_il8": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                    _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
@@ -110,15 +110,15 @@ _SIGNATURES = {
     "ss_decode_attn_turboquant": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
-        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
-        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_turboquant_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _i64,
                                                      _int]),
     "ss_decode_attn_turboquant_il": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
-        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
-        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_kmeans_blocks": (_int, [_c_void_p, _int, _i64, _int, _int, _int, _c_void_p, _c_void_p,
                                 _c_void_p]),
     "ss_decode_attn_sunshape_v": (_int, [
@@ -133,8 +133,8 @@ _SIGNATURES = {
     "ss_decode_attn_grouped_il_hybrid": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64,
-        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _i64,
-        _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                                   _c_void_p, _i64, _i64, _c_void_p]),
     "ss_quantize_values_grouped": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -609,6 +609,22 @@ def codebook_f16x2(centroids: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _heavy_args(k_heavy, heavy_dims, b_, hkv, cap, max_dims):
+    """(k_heavy, heavy_dims, n) pointers of a mixed-precision codec's fp16
+    heavy-block key dims (B, Hkv, cap, n) for the hybrid entry points."""
+    if k_heavy is None:
+        return None, None, 0
+    require_gpu(k_heavy, heavy_dims)
+    nhd = int(heavy_dims.numel())
+    if k_heavy.dtype != torch.float16 or not k_heavy.is_contiguous() or \
+            tuple(k_heavy.shape) != (b_, hkv, cap, nhd) or heavy_dims.dtype != torch.int32:
+        raise ValueError(f"k_heavy must be contiguous fp16 {(b_, hkv, cap, nhd)} with int32 "
+                         "heavy_dims")
+    if nhd % 8 or nhd > max_dims:
+        raise SunShapeUnsupported(-2, f"{nhd} heavy dims (a multiple of 8, at most {max_dims})")
+    return ptr(k_heavy), ptr(heavy_dims), nhd
+
+
 def _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len):
     """The C-ABI buffer arguments (k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
     buf_st, t_buf) of a hybrid cache's buffered tokens."""
@@ -622,13 +638,18 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                     out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                     n_splits: int = 0, codebook: torch.Tensor | None = None,
                     buf_keys: torch.Tensor | None = None,
-                    buf_values: torch.Tensor | None = None, buf_len: int = 0) -> torch.Tensor:
+                    buf_values: torch.Tensor | None = None, buf_len: int = 0,
+                    k_heavy: torch.Tensor | None = None,
+                    heavy_dims: torch.Tensor | None = None) -> torch.Tensor:
     """Fused decode (matrix-core LUT and P.V) over fp16 values in the 8-token
     interleaved layout ``values_il8`` (B, Hkv, cap/8, D, 8).  ``codebook`` is
     :func:`codebook_f16x2` of ``centroids`` (prepared here when None).  A
     hybrid cache's recent tokens ``buf_keys``/``buf_values`` (B, Hkv,
     >= buf_len, D, original basis) join the same softmax as positions t_kv ..
-    t_kv + buf_len - 1 (``ss_decode_attn_il8_hybrid``)."""
+    t_kv + buf_len - 1, and a mixed-precision codec's fp16 heavy-block key
+    dims ``k_heavy`` (B, Hkv, cap, nhd <= 32) with ``heavy_dims`` (nhd,)
+    int32 are scored exactly (``ss_decode_attn_il8_hybrid``; the centroids
+    must then hold zeros for those blocks)."""
     _check_decode_common(q, idx, centroids, perm)
     if codebook is None:
         codebook = codebook_f16x2(centroids)
@@ -650,11 +671,12 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
     tail = (int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
             ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device))
     stat = _attn_stat("sunshape_fused_attention_mfma", causal)
-    if buf_keys is None or buf_len == 0:
+    heavy = _heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32)
+    if (buf_keys is None or buf_len == 0) and k_heavy is None:
         _launched(stat, load_library().ss_decode_attn_il8(*common, *tail))
     else:
-        buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len)
-        _launched(stat, load_library().ss_decode_attn_il8_hybrid(*common, *buf, *tail))
+        buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len if buf_keys is not None else 0)
+        _launched(stat, load_library().ss_decode_attn_il8_hybrid(*common, *buf, *heavy, *tail))
     if _check_waits:
         check_decode_waits(q.device)
     return out
@@ -888,7 +910,8 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
                            out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
                            n_splits: int = 0, buf_keys: torch.Tensor | None = None,
                            buf_values: torch.Tensor | None = None,
-                           buf_len: int = 0) -> torch.Tensor:
+                           buf_len: int = 0, k_heavy: torch.Tensor | None = None,
+                           heavy_dims: torch.Tensor | None = None) -> torch.Tensor:
     """Fused decode over TurboQuant values: ``packed`` (B, Hkv, cap,
     packed_dim) codes, ``norms`` (B, Hkv, cap) float32, ``levels`` the 2^bits
     scaled Lloyd-Max levels (any float sequence; copied to the kernel
@@ -927,7 +950,7 @@ def decode_attn_turboquant(q: torch.Tensor, scale: float, perm: torch.Tensor | N
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(centroids),
         nb, nc, ptr(idx), ptr(packed), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
         ptr(rotation), int(bits), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
-        bst, buf_len, int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        bst, buf_len, *_heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 64), int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
         ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
     return out
 
@@ -949,7 +972,8 @@ def decode_attn_turboquant_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
                               codebook: torch.Tensor | None = None,
                               buf_keys: torch.Tensor | None = None,
                               buf_values: torch.Tensor | None = None,
-                              buf_len: int = 0) -> torch.Tensor:
+                              buf_len: int = 0, k_heavy: torch.Tensor | None = None,
+                              heavy_dims: torch.Tensor | None = None) -> torch.Tensor:
     """Fused decode (matrix-core LUT and P.V) over 2-bit TurboQuant values
     whose codes are token-interleaved (``codes_il`` (B, Hkv, cap/16, D) words,
     written by :func:`pack_grouped_il`), ``norms`` (B, Hkv, cap) float32,
@@ -993,7 +1017,7 @@ def decode_attn_turboquant_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
         nb, nc, ptr(idx), ptr(codes_il), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
         ptr(rotation), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
-        bst, buf_len, int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        bst, buf_len, *_heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32), int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
         ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
     return out
 
@@ -1006,7 +1030,8 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
                            n_splits: int = 0, codebook: torch.Tensor | None = None,
                            buf_keys: torch.Tensor | None = None,
                            buf_values: torch.Tensor | None = None,
-                           buf_len: int = 0) -> torch.Tensor:
+                           buf_len: int = 0, k_heavy: torch.Tensor | None = None,
+                           heavy_dims: torch.Tensor | None = None) -> torch.Tensor:
     """Fused decode (matrix-core LUT and P.V) over grouped values whose codes
     are token-interleaved: ``codes_il`` (B, Hkv, cap * bits / 32, D) 32-bit
     words (see :func:`pack_grouped_il`), ``scales``/``zeros`` (B, Hkv, cap, D
@@ -1040,15 +1065,16 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
               dtype_code(scales.dtype), int(bits), int(group_size), cap, int(t_kv))
     tail = (ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
             int(n_splits), stream_handle(q.device))
-    if buf_keys is None or buf_len == 0:
+    heavy = _heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32)
+    if (buf_keys is None or buf_len == 0) and k_heavy is None:
         _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il(
             *common, int(bool(causal)), int(q_offset), *tail))
         if _check_waits:
             check_decode_waits(q.device)
         return out
-    buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len)
+    buf = _buffer_ptrs(b_, hkv, d, buf_keys, buf_values, buf_len if buf_keys is not None else 0)
     _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il_hybrid(
-        *common, *buf, int(bool(causal)), int(q_offset), *tail))
+        *common, *buf, *heavy, int(bool(causal)), int(q_offset), *tail))
     if _check_waits:
         check_decode_waits(q.device)
     return out

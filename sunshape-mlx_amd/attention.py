@@ -108,7 +108,8 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     # a prompt (many query rows per head) against an fp16 cache: keys
     # reconstructed from the codebook, both products on the matrix cores
     b_, hq, tq, d = queries.shape
-    if not buffered and kind == "il8" and tq > 1 and \
+    hv = {"k_heavy": ops.get("k_heavy"), "heavy_dims": ops.get("heavy_dims")}
+    if not buffered and kind == "il8" and tq > 1 and hv["k_heavy"] is None and \
             _hip.prefill_supported(hq, cache.n_kv_heads, tq, d, codec.n_blocks):
         try:
             out = _hip.prefill_attn_il8(q, kscale, perm, codec.kernel_codebook(), codec.n_centroids,
@@ -120,7 +121,7 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return out
     # the matrix-core decodes without a token buffer: one prepared launch
     # (argument checks, codebook and split plan done once per cache layout)
-    if not buffered and kind in ("il8", "grouped_il"):
+    if not buffered and kind in ("il8", "grouped_il") and hv["k_heavy"] is None:
         try:
             plan = _prepared_decode(cache, ops, codec, q, kscale, perm)
             out = plan(q, t_kv, causal, q_offset, out_dtype=queries.dtype)
@@ -131,26 +132,29 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
     try:
         if kind == "il8":
-            out = _hip.decode_attn_il8(q, kscale, perm, codec.centroids, ops["idx"], ops["values"],
-                                       codebook=codec.kernel_codebook(), buf_keys=ops["buf_keys"],
-                                       buf_values=ops["buf_values"], buf_len=buffered, **kw)
-            codec.last_score_backend = "hip_fused_mfma_buffer"
+            out = _hip.decode_attn_il8(q, kscale, perm, codec.scoring_centroids(), ops["idx"],
+                                       ops["values"], codebook=codec.kernel_codebook(),
+                                       buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
+                                       buf_len=buffered, **hv, **kw)
+            codec.last_score_backend = ("hip_fused_mfma_buffer" if buffered
+                                        else "hip_fused_mfma_heavy")
         elif kind == "grouped_il":
-            out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.centroids, ops["idx"],
-                                              ops["codes_il"], ops["scales"], ops["zeros"],
-                                              ops["bits"], ops["group_size"],
+            out = _hip.decode_attn_grouped_il(q, kscale, perm, codec.scoring_centroids(),
+                                              ops["idx"], ops["codes_il"], ops["scales"],
+                                              ops["zeros"], ops["bits"], ops["group_size"],
                                               codebook=codec.kernel_codebook(),
                                               buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
-                                              buf_len=buffered, **kw)
+                                              buf_len=buffered, **hv, **kw)
             codec.last_score_backend = ("hip_fused_mfma_dequant_buffer" if buffered
                                         else "hip_fused_mfma_dequant")
         elif kind == "turboquant_il":
-            out = _hip.decode_attn_turboquant_il(q, kscale, perm, codec.centroids, ops["idx"],
-                                                 ops["codes_il"], ops["norms"], ops["levels"],
-                                                 ops["rotation"], codebook=codec.kernel_codebook(),
+            out = _hip.decode_attn_turboquant_il(q, kscale, perm, codec.scoring_centroids(),
+                                                 ops["idx"], ops["codes_il"], ops["norms"],
+                                                 ops["levels"], ops["rotation"],
+                                                 codebook=codec.kernel_codebook(),
                                                  buf_keys=ops["buf_keys"],
                                                  buf_values=ops["buf_values"], buf_len=buffered,
-                                                 **kw)
+                                                 **hv, **kw)
             codec.last_score_backend = ("hip_fused_mfma_turboquant_buffer" if buffered
                                         else "hip_fused_mfma_turboquant")
         elif ops["kind"] == "turboquant":
@@ -158,15 +162,14 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
                                               ops["packed"], ops["norms"], ops["levels"],
                                               ops["rotation"], ops["bits"],
                                               buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
-                                              buf_len=buffered, **kw)
+                                              buf_len=buffered, **hv, **kw)
             codec.last_score_backend = ("hip_fused_turboquant_buffer" if buffered
                                         else "hip_fused_turboquant")
         elif ops["kind"] == "sunshape_v":
             out = _hip.decode_attn_sunshape_v(q, kscale, perm, codec.scoring_centroids(), ops["idx"],
                                               ops["v_idx"], ops["v_centroids"], ops["v_transform"],
                                               buf_keys=ops["buf_keys"], buf_values=ops["buf_values"],
-                                              buf_len=buffered, k_heavy=ops["k_heavy"],
-                                              heavy_dims=ops["heavy_dims"], **kw)
+                                              buf_len=buffered, **hv, **kw)
             codec.last_score_backend = ("hip_fused_sunshape_v_buffer" if buffered
                                         else "hip_fused_sunshape_v")
         elif ops["kind"] == "grouped":

@@ -603,14 +603,20 @@ class HybridSunShapeKVCache:
         fused kernel."""
         if self._key_indices is None or self._compressed_offset == 0:
             return None
-        if self._heavy_dims is not None and self.value_backend != "sunshape":
-            return None  # fp16 heavy blocks: only the SunShape-value kernel scores them
+        # fp16 heavy-block key dims of a mixed-precision codec, scored exactly
+        # by every fused kernel of this cache's layouts but the reference-
+        # layout grouped and token-major fp16 ones
+        heavy = {"k_heavy": self._key_heavy, "heavy_dims": self._heavy_dims}
         if self.value_backend == "grouped" and self._values_il is not None:
             gc = self._value_codec_impl
             return {"kind": "grouped_il", "idx": self._key_indices, "codes_il": self._values_il,
                     "scales": self._value_scales, "zeros": self._value_zeros,
                     "bits": gc.bits, "group_size": gc.group_size,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+        if self._heavy_dims is not None and (self.value_backend == "grouped" or
+                                             (self.value_backend == "fp16" and
+                                              self._values_il8 is None)):
+            return None
         if self.value_backend == "grouped":
             gc = self._value_codec_impl
             return {"kind": "grouped", "idx": self._key_indices,
@@ -623,25 +629,24 @@ class HybridSunShapeKVCache:
             return {"kind": "turboquant_il", "idx": self._key_indices, "codes_il": self._values_il,
                     "norms": self._value_norms, "levels": tc.levels_host(),
                     "rotation": tc.rotation,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
         if self.value_backend == "turboquant" and self._values_packed is not None:
             tc = self._value_codec_impl
             tc._on(self._values_packed.device)
             return {"kind": "turboquant", "idx": self._key_indices,
                     "packed": self._values_packed, "norms": self._value_norms,
                     "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
         if self.value_backend == "sunshape" and self._value_indices is not None \
                 and self.value_codec.n_centroids <= 256:
             vc = self.value_codec
             return {"kind": "sunshape_v", "idx": self._key_indices, "v_idx": self._value_indices,
                     "v_centroids": vc.centroids.float().contiguous(),
                     "v_transform": vc.kernel_value_transform(),
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer,
-                    "k_heavy": self._key_heavy, "heavy_dims": self._heavy_dims}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
         if self.value_backend == "fp16" and self._values_il8 is not None:
             return {"kind": "il8", "idx": self._key_indices, "values": self._values_il8,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer}
+                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None

@@ -55,7 +55,14 @@ struct DecodeCommon {
     // up, and the sticky per-device word a give-up sets (kWait* bits)
     int spin_limit;
     unsigned int *wait_fail;
+    // fp16 heavy-block key dims of a mixed-precision codec (matrix-core
+    // kernels of hybrid caches): [rows][nhd] halves of codec-basis dims
+    // heavy_dims[0..nhd); nhd 0: none (every block scores from the LUT)
+    const __half *kheavy;
+    const int32_t *heavy_dims;
+    int nhd;
 };
+constexpr int kMaxHeavyMfma = 32;  // heavy dims the matrix-core kernels take
 
 // Bits of the wait-failure word: which bounded wait gave up.
 constexpr unsigned kWaitBarrier = 1u;  // compute-wave barrier
@@ -210,6 +217,11 @@ struct VTurbo {
         const uint32_t *packed;  // [rows][NW] words
         const float *norms;      // [rows]
         float lv[16];            // the 2^BITS levels, ascending (already x 1/sqrt(D))
+        // keys of mixed-precision codecs: the heavy blocks' dims kept in
+        // fp16 ([rows][nhd], codec basis), scored exactly beside the LUT
+        const __half *kheavy;    // or null
+        const int *heavy_dims;   // [nhd] codec-basis dims
+        int nhd;                 // multiple of 8, <= kMaxHeavyDims
     };
     struct Raw {
         uint32_t w;
@@ -241,7 +253,11 @@ struct VTurbo {
     // word decodes with one bit-field extract and one 8-byte LDS read per two
     // codes; the token's norm scales its softmax weight instead of each value.
     static constexpr int kPairs = 1 << (2 * BITS);
-    static constexpr int kLdsBytes = kPairs * 8;
+    // the pair table, then the heavy dims' query values
+    static constexpr int kMaxHeavyDims = 64;
+    static constexpr int kHeavyOffset = kPairs * 2;  // floats
+    static constexpr int kLdsBytes = kPairs * 8 + 4 * kMaxHeavyDims * 4;
+    static constexpr bool kHeavyKeys = true;
     static constexpr bool kTokenScale = true;
     static_assert(VPW % 2 == 0, "codes pair up within a word");
     __device__ static __forceinline__ void stage(float *lds, const Args &a, int, int tid, int nt) {
@@ -374,6 +390,10 @@ template <class VF>
 struct VfHeavy<VF, std::void_t<decltype(VF::kHeavyKeys)>> {
     static constexpr bool value = VF::kHeavyKeys;
 };
+template <class VF, class = void>
+struct VfHeavyMfma : std::false_type {};  // the matrix-core kernel scores fp16 heavy key dims
+template <class VF>
+struct VfHeavyMfma<VF, std::void_t<decltype(VF::kHeavyMfma)>> : std::integral_constant<bool, VF::kHeavyMfma> {};
 template <class VF, class = void>
 struct VfArgsToLds : std::false_type {};  // the format's accumulator hand-off reads its Args
 template <class VF>
@@ -1012,6 +1032,7 @@ struct VIl8Hyb : VIl8<D> {
         int64_t buf_sb, buf_sh, buf_st, t_buf;
     };
     static constexpr bool kHybridBuffer = true;
+    static constexpr bool kHeavyMfma = true;
 };
 
 // Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
@@ -1076,6 +1097,9 @@ struct VGil {
     static constexpr int kCodeBytes = kSub * kCodeBytes1;
     static constexpr int kSzBytes = kSub * kSzBytes1;
     static constexpr bool kHybridBuffer = true;  // hybrid caches: recent tokens join the pass
+    // fp16 heavy key dims: on the private-ring shapes (the loader-wave shape
+    // has no registers to spare for them)
+    static constexpr bool kHeavyMfma = kPrivateRing;
     static constexpr int kSzLoads = (kSzBytes + 1023) / 1024;
     static constexpr int kTileV = kCodeBytes + 2 * kSzBytes;
     static constexpr int kLoadsV = kCodeBytes / 1024 + 2 * kSzLoads;
@@ -1342,6 +1366,7 @@ struct VTq {
     static constexpr int kCodeBytes = kCodeBytes1;
     static constexpr int kSzBytes = kSzBytes1;
     static constexpr bool kHybridBuffer = false;  // the buffer joins as its own rotated partial
+    static constexpr bool kHeavyMfma = true;
     static constexpr int kTileV = kCodeBytes + 1024;
     static constexpr int kLoadsV = kCodeBytes / 1024 + 1;
     static constexpr int kPRows = 16;
@@ -1928,7 +1953,31 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             else
                 build(std::true_type{});
         }
-        compute_barrier(3);  // LUT complete
+        // fp16 heavy-block key dims (mixed-precision codecs; their LUT
+        // entries are zero): A operands of v_mfma_f32_4x4x4f16 products with
+        // each token's own dims, query row lane%4, dims 4kk .. 4kk+3, split
+        // fp16 hi and lo * 2^11 (the lo part only for non-fp16 queries)
+        constexpr bool HV = VfHeavyMfma<VF>::value;
+        constexpr int HK = HV ? kMaxHeavyMfma / 4 : 1;
+        f16x4 hah[HK], hal[HK];
+        const int nh4 = HV ? c.nhd >> 2 : 0;
+        if constexpr (HV) {
+#pragma unroll
+            for (int kk = 0; kk < HK; ++kk) {
+                hah[kk] = hal[kk] = f16x4{};
+                if (kk < nh4) {
+#pragma unroll
+                    for (int e2 = 0; e2 < 4; ++e2) {
+                        const int hd = min(max(c.heavy_dims[4 * kk + e2], 0), D - 1);
+                        const float x = qp[(lane & 3) * D + hd];
+                        const _Float16 h = (_Float16)x;
+                        hah[kk][e2] = h;
+                        hal[kk][e2] = (_Float16)((x - (float)h) * kSplitScale);
+                    }
+                }
+            }
+        }
+        compute_barrier(3);  // LUT complete (the query in LDS is read for the last time)
         if constexpr (VF::kHybridBuffer)
             if (wv == 0 && has_buf) buffer_share(va);
 
@@ -1936,6 +1985,18 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         for (int u = wv, uk = 0; u < n_units; u += NC, ++uk) {
             const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
             const int slot = K::kPriv ? uk % K::kPrivSlots : j % K::kSlots;
+            // the heavy dims of token `lane` (the split's last token past its
+            // end), loaded while the tile is waited on and the LUT read
+            uint4 khv[HV ? kMaxHeavyMfma / 8 : 1];
+            if constexpr (HV) {
+                if (nh4 > 0) {
+                    const int64_t tk = min(t_beg + (int64_t)u * kWave + lane, t_last);
+                    const uint4 *hp = reinterpret_cast<const uint4 *>(c.kheavy + (bh * c.cap + tk) * c.nhd);
+#pragma unroll
+                    for (int j8 = 0; j8 < kMaxHeavyMfma / 8; ++j8)
+                        if (2 * j8 < nh4) khv[j8] = hp[j8];
+                }
+            }
             if constexpr (K::kPriv) {
                 // this wave's copies of unit u have landed (its later units
                 // stay in flight)
@@ -1990,6 +2051,32 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             float sc[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) sc[r] = e[0][r];
+            if constexpr (HV) {
+                if (nh4 > 0) {  // heavy dims on the matrix cores: D[row][token lane]
+                    f32x4 hs = f32x4{0.f, 0.f, 0.f, 0.f}, hl = hs;
+#pragma unroll
+                    for (int j8 = 0; j8 < kMaxHeavyMfma / 8; ++j8)
+                        if (2 * j8 < nh4) {
+                            const f16x4 b0 = __builtin_bit_cast(f16x4, make_uint2(khv[j8].x, khv[j8].y));
+                            const f16x4 b1 = __builtin_bit_cast(f16x4, make_uint2(khv[j8].z, khv[j8].w));
+                            hs = __builtin_amdgcn_mfma_f32_4x4x4f16(hah[2 * j8], b0, hs, 0, 0, 0);
+                            hs = __builtin_amdgcn_mfma_f32_4x4x4f16(hah[2 * j8 + 1], b1, hs, 0, 0, 0);
+                        }
+                    if (c.q_dtype != SS_F16) {
+#pragma unroll
+                        for (int j8 = 0; j8 < kMaxHeavyMfma / 8; ++j8)
+                            if (2 * j8 < nh4) {
+                                const f16x4 b0 = __builtin_bit_cast(f16x4, make_uint2(khv[j8].x, khv[j8].y));
+                                const f16x4 b1 = __builtin_bit_cast(f16x4, make_uint2(khv[j8].z, khv[j8].w));
+                                hl = __builtin_amdgcn_mfma_f32_4x4x4f16(hal[2 * j8], b0, hl, 0, 0, 0);
+                                hl = __builtin_amdgcn_mfma_f32_4x4x4f16(hal[2 * j8 + 1], b1, hl, 0, 0, 0);
+                            }
+                    }
+                    const f32x4 hv = (hs + hl * (1.f / kSplitScale)) * kLog2e;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) sc[r] += hv[r];
+                }
+            }
             // A whole tile every row sees (no causal cut, no split end) whose
             // scores all stay at or below the rows' running maxima keeps the
             // maxima: no reduction, no rescale.  Otherwise masked lanes add
@@ -3115,6 +3202,9 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
         const int rc = wait_word(&c.wait_fail);
         if (rc != SS_OK) return rc;
     }
+    c.kheavy = nullptr;
+    c.heavy_dims = nullptr;
+    c.nhd = 0;
     c.part_ml = nullptr;
     c.part_acc = nullptr;
     c.part_cnt = nullptr;
@@ -3397,12 +3487,20 @@ extern "C" int ss_decode_attn_turboquant(
     int n_centroids, const uint8_t *idx, const uint32_t *packed, const float *norms,
     const float *levels, const float *rotation, int bits, int64_t cap, int64_t t_kv,
     const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
-    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
-    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int64_t buf_st, int64_t t_buf, const void *k_heavy, const int32_t *heavy_dims, int n_heavy_dims,
+    int causal, int64_t q_offset, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
+    int n_splits, void *stream) {
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
     if (rc) return rc;
     SS_REQUIRE(packed && norms && levels && rotation, "null packed/norms/levels/rotation");
+    if (k_heavy) {
+        SS_REQUIRE(heavy_dims, "null heavy_dims");
+        SS_UNSUPPORTED(n_heavy_dims > 0 && n_heavy_dims % 8 == 0 && n_heavy_dims <= 64,
+                       "n_heavy_dims %d unsupported (a positive multiple of 8, at most 64)",
+                       n_heavy_dims);
+        SS_REQUIRE(((uintptr_t)k_heavy % 16) == 0, "heavy keys must be 16-byte aligned");
+    }
     SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4 (got %d)", bits);
     SS_REQUIRE(!(bits == 2 && head_dim % 16) && !(bits == 4 && head_dim % 8),
                "head_dim %d cannot be packed at %d bits", head_dim, bits);
@@ -3411,7 +3509,9 @@ extern "C" int ss_decode_attn_turboquant(
     auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
 #define SS_TURBO(DD, BB)                                                    \
     {                                                                       \
-        typename VTurbo<DD, BB>::Args va{packed, norms, {}};                \
+        typename VTurbo<DD, BB>::Args va{packed, norms, {},                 \
+                                         static_cast<const __half *>(k_heavy), \
+                                         heavy_dims, k_heavy ? n_heavy_dims : 0}; \
         for (int i = 0; i < (1 << BB); ++i) va.lv[i] = levels[i];           \
         return launch_r<DD, VTurbo<DD, BB>>(c, va, s, st, false);           \
     }
@@ -3596,6 +3696,21 @@ static int check_buffer(const void *k_buf, const void *v_buf, int buf_dtype, int
     return SS_OK;
 }
 
+// fp16 heavy-block key dims of a mixed-precision codec for the matrix-core
+// kernels (hybrid caches): [rows][n] halves at 16-byte aligned rows.
+static int set_heavy(DecodeCommon &c, const void *k_heavy, const int32_t *heavy_dims, int n) {
+    if (!k_heavy) return SS_OK;
+    SS_REQUIRE(heavy_dims, "null heavy_dims");
+    SS_UNSUPPORTED(n > 0 && n % 8 == 0 && n <= kMaxHeavyMfma,
+                   "n_heavy_dims %d unsupported (a positive multiple of 8, at most %d)", n,
+                   kMaxHeavyMfma);
+    SS_REQUIRE(((uintptr_t)k_heavy % 16) == 0, "heavy keys must be 16-byte aligned");
+    c.kheavy = static_cast<const __half *>(k_heavy);
+    c.heavy_dims = heavy_dims;
+    c.nhd = n;
+    return SS_OK;
+}
+
 static int il8_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads,
                     int64_t t_q, int head_dim, float scale, const int32_t *perm,
                     const void *codebook, int n_blocks, int n_centroids, const uint8_t *idx,
@@ -3603,7 +3718,8 @@ static int il8_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads, in
                     int64_t q_offset, void *out, int out_dtype, void *workspace,
                     size_t workspace_bytes, int n_splits, const void *k_buf, const void *v_buf,
                     int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
-                    int64_t t_buf, void *stream) {
+                    int64_t t_buf, void *stream, const void *k_heavy = nullptr,
+                    const int32_t *heavy_dims = nullptr, int n_heavy_dims = 0) {
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
@@ -3626,9 +3742,11 @@ static int il8_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads, in
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     rc = check_buffer(k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, head_dim);
     if (rc) return rc;
+    rc = set_heavy(c, k_heavy, heavy_dims, n_heavy_dims);
+    if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const __half *v8 = reinterpret_cast<const __half *>(values_il8);
-    if (t_buf > 0) {
+    if (t_buf > 0 || c.nhd > 0) {  // the hybrid cache's kernel (buffer share, heavy dims)
         if (head_dim == 128)
             return launch_mfma<128, VIl8Hyb<128>>(
                 c, VIl8Hyb<128>::Args{v8, k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf},
@@ -3659,12 +3777,14 @@ extern "C" int ss_decode_attn_il8_hybrid(
     int head_dim, float scale, const int32_t *perm, const void *codebook, int n_blocks,
     int n_centroids, const uint8_t *idx, const void *values_il8, int v_dtype, int64_t cap,
     int64_t t_kv, const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb,
-    int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out,
-    int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int64_t buf_sh, int64_t buf_st, int64_t t_buf, const void *k_heavy, const int32_t *heavy_dims,
+    int n_heavy_dims, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream) {
     return il8_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
                     codebook, n_blocks, n_centroids, idx, values_il8, v_dtype, cap, t_kv, causal,
                     q_offset, out, out_dtype, workspace, workspace_bytes, n_splits, k_buf, v_buf,
-                    buf_dtype, buf_sb, buf_sh, buf_st, t_buf, stream);
+                    buf_dtype, buf_sb, buf_sh, buf_st, t_buf, stream, k_heavy, heavy_dims,
+                    n_heavy_dims);
 }
 
 // ---------------------------------------------------------------------------
@@ -3753,7 +3873,9 @@ static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_he
                            int64_t q_offset, void *out, int out_dtype, void *workspace,
                            size_t workspace_bytes, int n_splits, const void *k_buf,
                            const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
-                           int64_t buf_st, int64_t t_buf, void *stream) {
+                           int64_t buf_st, int64_t t_buf, void *stream,
+                           const void *k_heavy = nullptr, const int32_t *heavy_dims = nullptr,
+                           int n_heavy_dims = 0) {
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
@@ -3782,11 +3904,15 @@ static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_he
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     rc = check_buffer(k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, t_buf, head_dim);
     if (rc) return rc;
+    rc = set_heavy(c, k_heavy, heavy_dims, n_heavy_dims);
+    if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const int ng = head_dim / group_size;
 #define SS_GIL(DD, BB, NGG, SZT)                                                              \
     {                                                                                         \
         using VF = VGil<DD, BB, NGG, SZT>;                                                    \
+        SS_UNSUPPORTED(c.nhd == 0 || VF::kHeavyMfma,                                          \
+                       "fp16 heavy key dims with %d-bit values at head_dim %d", BB, DD);       \
         return launch_mfma<DD, VF>(                                                           \
             c,                                                                                \
             typename VF::Args{codes_il, static_cast<const SZT *>(scales),                     \
@@ -3837,14 +3963,15 @@ extern "C" int ss_decode_attn_grouped_il_hybrid(
     int n_centroids, const uint8_t *idx, const uint32_t *codes_il, const void *scales,
     const void *zeros, int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv,
     const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
-    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
-    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int64_t buf_st, int64_t t_buf, const void *k_heavy, const int32_t *heavy_dims,
+    int n_heavy_dims, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream) {
     SS_REQUIRE(t_buf >= 0, "negative buffer length");
     return grouped_il_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
                            codebook, n_blocks, n_centroids, idx, codes_il, scales, zeros, sz_dtype,
                            bits, group_size, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
                            workspace_bytes, n_splits, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
-                           buf_st, t_buf, stream);
+                           buf_st, t_buf, stream, k_heavy, heavy_dims, n_heavy_dims);
 }
 
 extern "C" int ss_decode_attn_turboquant_il(
@@ -3853,8 +3980,8 @@ extern "C" int ss_decode_attn_turboquant_il(
     int n_centroids, const uint8_t *idx, const uint32_t *codes_il, const float *norms,
     const float *levels, const float *rotation, int64_t cap, int64_t t_kv, const void *k_buf,
     const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t t_buf,
-    int causal, int64_t q_offset, void *out, int out_dtype, void *workspace, size_t workspace_bytes,
-    int n_splits, void *stream) {
+    const void *k_heavy, const int32_t *heavy_dims, int n_heavy_dims, int causal, int64_t q_offset,
+    void *out, int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents, n_blocks,
                           n_centroids, idx, cap, t_kv, out, out_dtype);
@@ -3877,6 +4004,8 @@ extern "C" int ss_decode_attn_turboquant_il(
         c.codebook_mul = reinterpret_cast<const float *>(
             static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
         c.fused_merge = 0;  // transformed_decode merges (buffer partial, rotation)
+        const int hrc = set_heavy(c, k_heavy, heavy_dims, n_heavy_dims);
+        if (hrc) return hrc;
         auto go = [&](auto dd) -> int {
             constexpr int DD = decltype(dd)::value;
             using VF = VTq<DD>;

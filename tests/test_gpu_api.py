@@ -607,13 +607,17 @@ def test_codec_fit_on_gpu_matches_cpu_fit(mode):
     assert abs(err_gpu / err_ref - 1.0) <= 0.01
 
 
-@pytest.mark.parametrize("value_backend,buffer_size", [("sunshape", 0), ("sunshape", 64),
-                                                       ("fp16", 32)])
-def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
+@pytest.mark.parametrize("value_backend,value_bits,buffer_size", [
+    ("sunshape", 8, 0), ("sunshape", 8, 64), ("fp16", 16, 0), ("fp16", 16, 32),
+    ("grouped", 2, 0), ("grouped", 4, 32), ("turboquant", 2, 0), ("turboquant", 2, 32),
+    ("turboquant", 3, 0), ("turboquant", 4, 32)])
+def test_mixed_precision_heavy_blocks_in_fp16(value_backend, value_bits, buffer_size):
     """A mixed-precision codec with ``heavy_fp16``: the hybrid cache keeps the
-    heavy blocks' key dims in fp16, returns them in ``keys``, and attention
-    scores them exactly -- fused for SunShape values, two-pass otherwise --
-    matching the oracle with heavy keys."""
+    heavy blocks' key dims in fp16, returns them in ``keys``, and every fused
+    kernel of the hybrid layouts scores them exactly (matrix-core decodes for
+    fp16, grouped and 2-bit TurboQuant values, the vector-ALU kernels for
+    SunShape and 3/4-bit TurboQuant values), matching the oracle with heavy
+    keys."""
     rng = np.random.default_rng(50)
     d, nb = 128, 16
     heavy = np.zeros(nb, bool)
@@ -637,8 +641,11 @@ def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
                                 "permutation": rng.permutation(d).astype(np.int32)})
         cache = S.create_kv_cache(codec, value_backend="sunshape", value_bits=8,
                                   value_codec=vcodec, **kw)
-    else:
+    elif value_backend == "fp16":
         cache = S.create_kv_cache(codec, value_backend="fp16", **kw)
+    else:
+        cache = S.create_kv_cache(codec, value_backend=value_backend, value_bits=value_bits,
+                                  **kw)
     cache.update_and_fetch(k, v)
     nc = cache.compressed_offset
     # returned keys carry the fp16 heavy dims in the original basis
@@ -646,8 +653,14 @@ def test_mixed_precision_heavy_blocks_in_fp16(value_backend, buffer_size):
     assert torch.equal(cache.keys[:, :, :nc][..., od].half().cpu(), k[:, :, :nc][..., od].cpu())
     q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
     out = S.sunshape_sdpa(q, cache, 0.088)
-    expect = {"sunshape": "hip_fused_sunshape_v_buffer" if buffer_size else "hip_fused_sunshape_v",
-              "fp16": "hip"}[value_backend]
+    sfx = "_buffer" if buffer_size else ""
+    expect = {"sunshape": "hip_fused_sunshape_v" + sfx,
+              "fp16": "hip_fused_mfma" + (sfx or "_heavy"),
+              # 4-bit grouped codes at head_dim 128 keep the loader-wave
+              # kernel shape, which takes no heavy dims: the two-pass path
+              "grouped": "hip" if value_bits == 4 else "hip_fused_mfma_dequant" + sfx,
+              "turboquant": ("hip_fused_mfma_turboquant" if value_bits == 2
+                             else "hip_fused_turboquant") + sfx}[value_backend]
     assert codec.last_score_backend == expect
     kh = k[:, :, :nc].cpu().numpy()[..., perm][..., hd]
     vals = cache.values.float().cpu().numpy()
@@ -700,6 +713,10 @@ def test_fitted_mixed_codec_heavy_fp16_with_buffer(value_backend):
     nc = cache.compressed_offset
     q = torch.from_numpy((rng.standard_normal((b, hq, 1, d)) * s).astype(np.float16)).to(DEV)
     out = S.sunshape_sdpa(q, cache, 0.088)
+    # the matrix-core fp16 decode takes at most 32 heavy dims (more: two-pass)
+    assert codec.last_score_backend == {
+        "sunshape": "hip_fused_sunshape_v_buffer",
+        "fp16": "hip_fused_mfma_buffer" if hd.size <= 32 else "hip"}[value_backend]
     kh = k[:, :, :nc].cpu().numpy()[..., perm][..., hd]
     vals = cache.values.float().cpu().numpy()
     idx = cache.key_indices.cpu().numpy()

@@ -899,6 +899,108 @@ def test_decode_sunshape_v_heavy_blocks(b, hq, hkv, t_kv, t_buf, t_q, n_heavy, s
     assert rel_err(out0.cpu().numpy(), ref0) <= REL_TOL
 
 
+@pytest.mark.parametrize("kind,bits,b,hq,hkv,d,t_kv,t_buf,t_q,n_heavy,splits", [
+    ("il8", 16, 2, 32, 8, 128, 1500, 0, 1, 4, 0),      # config-5 heads, 4 heavy blocks
+    ("il8", 16, 1, 8, 2, 128, 333, 40, 3, 1, 2),       # buffer, causal prefill rows
+    ("il8", 16, 1, 8, 2, 64, 517, 0, 1, 3, 3),         # head_dim 64, 24 heavy dims
+    ("grouped_il", 2, 1, 8, 2, 128, 700, 20, 1, 2, 0),
+    ("grouped_il", 4, 1, 8, 2, 64, 300, 0, 4, 4, 3),   # 4-bit at head_dim 64, causal rows
+    ("turboquant_il", 2, 8, 32, 8, 128, 2000, 128, 1, 4, 0),  # config-4 heads, hybrid buffer
+    ("turboquant_il", 2, 2, 6, 2, 128, 300, 20, 5, 3, 1),     # causal across the buffer
+    ("turboquant", 3, 1, 8, 2, 128, 777, 16, 1, 8, 0),  # vector-ALU kernel, 64 heavy dims
+    ("turboquant", 4, 1, 8, 2, 128, 400, 0, 4, 2, 2),   # vector-ALU kernel, causal rows
+])
+def test_decode_mfma_heavy_blocks(kind, bits, b, hq, hkv, d, t_kv, t_buf, t_q, n_heavy, splits):
+    """fp16 heavy-block keys on the interleaved fp16, grouped and TurboQuant
+    decodes: the heavy blocks' exact dot products replace their table
+    entries (the matrix-core kernels read a codebook whose heavy blocks are
+    zero; the vector-ALU TurboQuant kernel skips them in its own table), as
+    the oracle's two-pass SDPA with heavy keys does."""
+    cap = max(((t_kv + 15) // 16) * 16, 16)
+    cents, perm, idx, vals16, q = decode_case(200 + n_heavy + t_kv, b, hq, hkv, d, t_kv, t_q, cap)
+    rng = np.random.default_rng(201 + n_heavy + t_buf)
+    heavy = np.sort(rng.permutation(d // 8)[:n_heavy])
+    hd = np.concatenate([np.arange(x * 8, x * 8 + 8) for x in heavy]).astype(np.int32)
+    kh = np.zeros((b, hkv, cap, hd.size), np.float16)
+    kh[:, :, :t_kv] = rng.standard_normal((b, hkv, t_kv, hd.size)).astype(np.float16)
+    scoring = cents.copy()
+    scoring[heavy] = 0.0
+    kb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    vb = rng.standard_normal((b, hkv, t_buf + 3, d)).astype(np.float16)
+    scale = 1.0 / np.sqrt(d)
+    causal = t_q > 1
+    total = t_kv + t_buf
+    kw = dict(causal=causal, q_offset=total - t_q if causal else 0, out_dtype=torch.float32,
+              n_splits=splits, buf_keys=t(kb) if t_buf else None,
+              buf_values=t(vb) if t_buf else None, buf_len=t_buf, k_heavy=t(kh),
+              heavy_dims=t(hd))
+    vals = np.zeros((b, hkv, total, d), np.float64)
+    vals[:, :, t_kv:] = vb[:, :, :t_buf]
+    if kind == "il8":
+        out = _hip.decode_attn_il8(t(q), scale, t(perm), t(scoring), t(idx),
+                                   to_il8(vals16, cap), t_kv, **kw)
+        vals[:, :, :t_kv] = vals16[:, :, :t_kv]
+    elif kind == "grouped_il":
+        group = d // 2
+        _, packed, sc, ze, il = grouped_case(t_kv + 9, b, hkv, t_kv, d, bits, group, cap)
+        out = _hip.decode_attn_grouped_il(t(q), scale, t(perm), t(scoring), t(idx), il, sc, ze,
+                                          bits, group, t_kv, **kw)
+        for bi in range(b):
+            for hi in range(hkv):
+                vals[bi, hi, :t_kv] = O.dequantize_values(
+                    packed[bi, hi, :t_kv].cpu().numpy().view(np.uint32),
+                    sc[bi, hi, :t_kv].float().cpu().numpy(),
+                    ze[bi, hi, :t_kv].float().cpu().numpy(), d, bits, group)
+    else:
+        codes = rng.integers(0, 1 << bits, (b, hkv, cap, d)).astype(np.uint8)
+        packed = O.pack_indices(codes, bits).astype(np.uint32)
+        norms = (rng.random((b, hkv, cap)) * 3 + 0.1).astype(np.float32)
+        levels = (O.lloyd_max_gaussian(bits)[0] / np.sqrt(d)).astype(np.float32)
+        rot = O.rotation_matrix(d, 43)
+        if kind == "turboquant_il":
+            codes_il = torch.zeros((b, hkv, cap // 16, d), dtype=torch.int32, device=DEV)
+            _hip.pack_grouped_il(t(packed.view(np.int32)), 2, codes_il, 0)
+            out = _hip.decode_attn_turboquant_il(t(q), scale, t(perm), t(scoring), t(idx),
+                                                 codes_il, t(norms), levels, t(rot), t_kv, **kw)
+        else:
+            # the raw centroids: this kernel leaves the heavy blocks out itself
+            out = _hip.decode_attn_turboquant(t(q), scale, t(perm), t(cents), t(idx),
+                                              t(packed.view(np.int32)), t(norms), levels,
+                                              t(rot), bits, t_kv, **kw)
+        vals[:, :, :t_kv] = O.turboquant_decode(packed[:, :, :t_kv], norms[:, :, :t_kv], rot,
+                                                levels, d, bits)
+    torch.cuda.synchronize()
+    _hip.check_decode_waits()
+    ref = O.sdpa_two_pass(q, scale, perm, cents, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                          mask="causal" if causal else None, heavy_keys=kh[:, :, :t_kv],
+                          heavy_dims=hd)
+    assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+    # the heavy dims change the result (the check above is not vacuous)
+    ref0 = O.sdpa_two_pass(q, scale, perm, scoring, idx[:, :, :t_kv], kb[:, :, :t_buf], vals,
+                           mask="causal" if causal else None)
+    assert rel_err(ref0, ref) > 10 * REL_TOL
+
+
+def test_decode_mfma_heavy_blocks_limits():
+    """The matrix-core decodes take at most 32 heavy dims, and none on the
+    loader-wave shape (4-bit grouped codes at head_dim 128): both report
+    SunShapeUnsupported, the cue for the caller's two-pass path."""
+    b, hq, hkv, d, t_kv = 1, 8, 2, 128, 300
+    cap = 304
+    cents, perm, idx, vals16, q = decode_case(210, b, hq, hkv, d, t_kv, 1, cap)
+    hd40 = np.arange(40, dtype=np.int32)
+    kh40 = np.zeros((b, hkv, cap, 40), np.float16)
+    with pytest.raises(_hip.SunShapeUnsupported):
+        _hip.decode_attn_il8(t(q), 0.088, t(perm), t(cents), t(idx), to_il8(vals16, cap), t_kv,
+                             k_heavy=t(kh40), heavy_dims=t(hd40))
+    hd8 = np.arange(8, dtype=np.int32)
+    kh8 = np.zeros((b, hkv, cap, 8), np.float16)
+    _, _, sc, ze, il = grouped_case(211, b, hkv, t_kv, d, 4, 64, cap)
+    with pytest.raises(_hip.SunShapeUnsupported):
+        _hip.decode_attn_grouped_il(t(q), 0.088, t(perm), t(cents), t(idx), il, sc, ze, 4, 64,
+                                    t_kv, k_heavy=t(kh8), heavy_dims=t(hd8))
+
+
 @pytest.mark.parametrize("q_dtype", [np.float32, "bf16"])
 def test_decode_sunshape_v_heavy_blocks_wide_queries(q_dtype):
     """bf16 and fp32 queries on the matrix-core SunShape-value decode: the
