@@ -411,8 +411,8 @@ def run_turboquant(args) -> int:
     fn = lib.ss_decode_attn_turboquant_il
     argv = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cb16.data_ptr(),
              nb, 256, t[0].data_ptr(), il.data_ptr(), t[2].data_ptr(), lv_ptr, rot.data_ptr(),
-             t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0, out.data_ptr(), hip.SS_F16,
-             ws.data_ptr(), ws_bytes, args.splits, stream) for t, il in zip(bufs, ils)]
+             t_kv, t_kv, None, None, 0, 0, 0, 0, 0, None, None, 0, 0, 0, out.data_ptr(),
+             hip.SS_F16, ws.data_ptr(), ws_bytes, args.splits, stream) for t, il in zip(bufs, ils)]
     us, per = time_launches(fn, argv, args.steps, args.warmup, hip)
     nbytes = b * hkv * t_kv * (nb + pd * 4 + 4) + b * hq * d * 4
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -421,8 +421,8 @@ def run_turboquant(args) -> int:
     fn_v = lib.ss_decode_attn_turboquant
     argv_v = [(q.data_ptr(), hip.SS_F16, b, hq, hkv, 1, d, scale, perm.data_ptr(), cents.data_ptr(),
                nb, 256, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), lv_ptr, rot.data_ptr(),
-               bits, t_kv, t_kv, None, None, 0, 0, 0, 0, 0, 0, 0, out.data_ptr(), hip.SS_F16,
-               ws.data_ptr(), ws_bytes, args.splits, stream) for t in bufs]
+               bits, t_kv, t_kv, None, None, 0, 0, 0, 0, 0, None, None, 0, 0, 0, out.data_ptr(),
+               hip.SS_F16, ws.data_ptr(), ws_bytes, args.splits, stream) for t in bufs]
     us_v, _ = time_launches(fn_v, argv_v, max(args.steps // 4, 5), args.warmup, hip)
     log(f"turboquant (vector ALUs, packed rows): {us_v:.2f} us/step")
 
@@ -445,7 +445,7 @@ def run_turboquant(args) -> int:
             check = max(check, float(np.abs(got - ref).max() / np.abs(ref).max()))
 
     traffic = None  # HBM bytes per call from the committed counter runs
-    tf = os.path.join(ROOT, "profiles", "decode_turboquant2b_t32k_traffic.json")
+    tf = os.path.join(ROOT, "profiles", "decode_attn_mfma_turboquant2b_t32k_traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
             tr = json.load(f)
