@@ -395,6 +395,22 @@ struct VfHeavyMfma : std::false_type {};  // the matrix-core kernel scores fp16 
 template <class VF>
 struct VfHeavyMfma<VF, std::void_t<decltype(VF::kHeavyMfma)>> : std::integral_constant<bool, VF::kHeavyMfma> {};
 template <class VF, class = void>
+struct VfHeavyCapable : std::false_type {};  // the format has registers to spare for them
+template <class VF>
+struct VfHeavyCapable<VF, std::void_t<decltype(VF::kHeavyCapable)>>
+    : std::integral_constant<bool, VF::kHeavyCapable> {};
+// A matrix-core value format with the heavy-dim products compiled in: a
+// separate kernel, launched only for calls that carry fp16 heavy key dims,
+// so the plain kernels keep their registers and instruction schedule.
+template <class VF>
+struct WithHeavy : VF {
+    static constexpr bool kHeavyMfma = true;
+};
+template <class T>
+struct TypeTag {
+    using type = T;
+};
+template <class VF, class = void>
 struct VfArgsToLds : std::false_type {};  // the format's accumulator hand-off reads its Args
 template <class VF>
 struct VfArgsToLds<VF, std::void_t<decltype(&VF::to_lds_args)>> : std::true_type {};
@@ -1032,7 +1048,7 @@ struct VIl8Hyb : VIl8<D> {
         int64_t buf_sb, buf_sh, buf_st, t_buf;
     };
     static constexpr bool kHybridBuffer = true;
-    static constexpr bool kHeavyMfma = true;
+    static constexpr bool kHeavyCapable = true;
 };
 
 // Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
@@ -1099,7 +1115,7 @@ struct VGil {
     static constexpr bool kHybridBuffer = true;  // hybrid caches: recent tokens join the pass
     // fp16 heavy key dims: on the private-ring shapes (the loader-wave shape
     // has no registers to spare for them)
-    static constexpr bool kHeavyMfma = kPrivateRing;
+    static constexpr bool kHeavyCapable = kPrivateRing;
     static constexpr int kSzLoads = (kSzBytes + 1023) / 1024;
     static constexpr int kTileV = kCodeBytes + 2 * kSzBytes;
     static constexpr int kLoadsV = kCodeBytes / 1024 + 2 * kSzLoads;
@@ -1366,7 +1382,7 @@ struct VTq {
     static constexpr int kCodeBytes = kCodeBytes1;
     static constexpr int kSzBytes = kSzBytes1;
     static constexpr bool kHybridBuffer = false;  // the buffer joins as its own rotated partial
-    static constexpr bool kHeavyMfma = true;
+    static constexpr bool kHeavyCapable = true;
     static constexpr int kTileV = kCodeBytes + 1024;
     static constexpr int kLoadsV = kCodeBytes / 1024 + 1;
     static constexpr int kPRows = 16;
@@ -2237,7 +2253,80 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     __syncthreads();
     if (!*last) return;
 
-    // last split of this column: merge.  LDS (the ring): weights [S][R],
+    // Last split of this column: merge.  With up to kMergeParts * 16
+    // splits, thread (part, chunk) loads float4 `chunk` of the partials of
+    // splits part, part + kMergeParts, ... (and their (m, l)) into registers
+    // with every load in flight at once (one memory round trip), weights them
+    // by its own maximum, and the parts combine through LDS.
+    constexpr int CH = R * D / 4;
+    constexpr int kMergeParts = THREADS / CH >= 4 ? 4 : THREADS / CH;
+    constexpr int kMergeLoads = 16;
+    if (kMergeParts >= 2 && S <= kMergeParts * kMergeLoads) {
+        const int cidx = tid % CH, part = tid / CH;
+        const int mr = cidx / (D / 4), md0 = (cidx - mr * (D / 4)) * 4;
+        float Mr = -1e30f, Lr = 0.f;
+        f32x4 Ar = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (part < kMergeParts) {
+            f32x4 av[kMergeLoads];
+            u32x2 mv[kMergeLoads];
+#pragma unroll
+            for (int j = 0; j < kMergeLoads; ++j) {
+                const int s2 = part + kMergeParts * j;
+                if (s2 < S) {
+                    const int64_t sl = ((int64_t)col * S + s2) * R + mr;
+                    av[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          acc_rs, (uint32_t)((sl * D + md0) * 4), 0, kCpolSc1));
+                    mv[j] = __builtin_amdgcn_raw_buffer_load_b64(ml_rs, (uint32_t)(sl * 8), 0, kCpolSc1);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeLoads; ++j)
+                if (part + kMergeParts * j < S) Mr = fmaxf(Mr, __uint_as_float(mv[j][0]));
+#pragma unroll
+            for (int j = 0; j < kMergeLoads; ++j)
+                if (part + kMergeParts * j < S) {
+                    const float w = fast_exp2(__uint_as_float(mv[j][0]) - Mr);
+                    Lr = fmaf(__uint_as_float(mv[j][1]), w, Lr);
+                    Ar += av[j] * w;
+                }
+        }
+        // parts 1.. hand their (M, L, A) to part 0 through LDS (the ring)
+        float *pm = reinterpret_cast<float *>(ring);  // [kMergeParts - 1][6][CH]
+        static_assert((kMergeParts - 1) * 6 * CH * 4 <= K::kRingBytes, "merge LDS");
+        if (part >= 1 && part < kMergeParts) {
+            float *q6 = pm + (part - 1) * 6 * CH;
+            q6[cidx] = Mr;
+            q6[CH + cidx] = Lr;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q6[(2 + k) * CH + cidx] = Ar[k];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int p2 = 1; p2 < kMergeParts; ++p2) {
+                const float *q6 = pm + (p2 - 1) * 6 * CH;
+                const float m2 = q6[cidx], l2 = q6[CH + cidx];
+                const f32x4 a2 = f32x4{q6[2 * CH + cidx], q6[3 * CH + cidx], q6[4 * CH + cidx],
+                                       q6[5 * CH + cidx]};
+                const float Mn = fmaxf(Mr, m2);
+                const float fo = fast_exp2(Mr - Mn), fn = fast_exp2(m2 - Mn);
+                Ar = Ar * fo + a2 * fn;
+                Lr = Lr * fo + l2 * fn;
+                Mr = Mn;
+            }
+            if (row_ok(mr)) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    store_from_f32(c.out, c.out_dtype, row_off(mr) + md0 + k, Lr > 0.f ? Ar[k] / Lr : 0.f);
+            }
+        }
+        if (tid == 0)
+            __hip_atomic_store(c.part_cnt + (int64_t)col * c.cnt_stride, 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    // More splits: LDS (the ring) holds weights [S][R],
     // row sums [R], the splits' (m, l) [S][R], then a chunk of the partial
     // accumulators.  The (m, l) loads and the first chunk's copy are issued
     // together, so the merge costs one memory round trip per chunk.
@@ -3057,8 +3146,8 @@ static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t
 }
 
 template <int D, class VF>
-static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
-                       hipStream_t st) {
+static int launch_mfma_kernel(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
+                              hipStream_t st) {
     constexpr int NC = VF::kComputeWaves;
     using K = WsCfg<D, NC, VF>;
     auto kern = decode_attn_mfma_kernel<D, NC, VF>;
@@ -3080,6 +3169,19 @@ static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const Decode
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
     if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
     return launch_merge<D>(c, s, st);
+}
+
+// the format's kernel, or its heavy-dim variant when the call carries fp16
+// heavy key dims
+template <int D, class VF>
+static int launch_mfma(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
+                       hipStream_t st) {
+    if (c.nhd > 0) {
+        if constexpr (VfHeavyCapable<VF>::value)
+            return launch_mfma_kernel<D, WithHeavy<VF>>(c, va, s, st);
+        SS_UNSUPPORTED(false, "fp16 heavy key dims are not taken by this decode shape");
+    }
+    return launch_mfma_kernel<D, VF>(c, va, s, st);
 }
 
 template <int NH8>
@@ -3911,7 +4013,7 @@ static int grouped_il_impl(const void *q, int q_dtype, int64_t batch, int n_q_he
 #define SS_GIL(DD, BB, NGG, SZT)                                                              \
     {                                                                                         \
         using VF = VGil<DD, BB, NGG, SZT>;                                                    \
-        SS_UNSUPPORTED(c.nhd == 0 || VF::kHeavyMfma,                                          \
+        SS_UNSUPPORTED(c.nhd == 0 || VF::kHeavyCapable,                                       \
                        "fp16 heavy key dims with %d-bit values at head_dim %d", BB, DD);       \
         return launch_mfma<DD, VF>(                                                           \
             c,                                                                                \
@@ -4006,9 +4108,9 @@ extern "C" int ss_decode_attn_turboquant_il(
         c.fused_merge = 0;  // transformed_decode merges (buffer partial, rotation)
         const int hrc = set_heavy(c, k_heavy, heavy_dims, n_heavy_dims);
         if (hrc) return hrc;
-        auto go = [&](auto dd) -> int {
+        auto go = [&](auto dd, auto vf) -> int {
             constexpr int DD = decltype(dd)::value;
-            using VF = VTq<DD>;
+            using VF = typename decltype(vf)::type;
             constexpr int NC = VF::kComputeWaves;
             using K = WsCfg<DD, NC, VF>;
             auto kern = decode_attn_mfma_kernel<DD, NC, VF>;
@@ -4024,7 +4126,13 @@ extern "C" int ss_decode_attn_turboquant_il(
             SS_LAUNCH_CHECK("decode_attn_mfma_kernel (turboquant) launch");
             return SS_OK;
         };
-        return head_dim == 128 ? go(std::integral_constant<int, 128>{}) : go(std::integral_constant<int, 64>{});
+        using I128 = std::integral_constant<int, 128>;
+        using I64 = std::integral_constant<int, 64>;
+        if (c.nhd > 0)
+            return head_dim == 128 ? go(I128{}, TypeTag<WithHeavy<VTq<128>>>{})
+                                   : go(I64{}, TypeTag<WithHeavy<VTq<64>>>{});
+        return head_dim == 128 ? go(I128{}, TypeTag<VTq<128>>{})
+                               : go(I64{}, TypeTag<VTq<64>>{});
     };
     return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm, cents,
                               n_centroids, idx, cap, t_kv, rotation, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
