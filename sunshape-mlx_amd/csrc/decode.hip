@@ -410,6 +410,43 @@ template <class T>
 struct TypeTag {
     using type = T;
 };
+template <class VF, bool R>
+struct RawUnitOf {  // a format's raw register unit (register-unit formats only)
+    struct type {};
+};
+template <class VF>
+struct RawUnitOf<VF, true> {
+    using type = typename VF::Raw;
+};
+template <class VF, class = void>
+struct VfRegUnits : std::false_type {};  // units loaded into registers, no LDS ring
+template <class VF>
+struct VfRegUnits<VF, std::void_t<decltype(VF::kRegUnits)>> : std::integral_constant<bool, VF::kRegUnits> {};
+
+// The code words of a lane for one 64-token unit of token-interleaved codes
+// ([cap / TPW][D] words per (batch, head)), straight from HBM into
+// registers: per k-step, the NT words of dims NT*(lane%16) .. of the word
+// block holding tokens 32ks + 8*(lane/16) ..; a lane whose tokens all lie
+// past t_last reads the block holding t_last (its probabilities are 0).
+// The words stay raw (the 2-bit shift is applied when the unit is used, so
+// no instruction waits on the loads here).
+template <int D, int NT, int TPW>
+__device__ __forceinline__ void load_code_words(uint32_t (&cw)[2][NT], const uint32_t *codes, int64_t bh,
+                                                int64_t cap, int64_t t0, int64_t t_last, int lane) {
+    const int g = lane >> 4, l16 = lane & 15;
+    const uint32_t *chead = codes + bh * (cap / TPW) * D;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int64_t tk = min(t0 + 32 * ks + 8 * g, t_last);
+        const uint32_t *src = chead + (tk / TPW) * D + (NT * l16) % D;
+        const uint4 a = *reinterpret_cast<const uint4 *>(src);
+        cw[ks][0] = a.x; cw[ks][1] = a.y; cw[ks][2] = a.z; cw[ks][3] = a.w;
+        if constexpr (NT == 8) {
+            const uint4 b = *reinterpret_cast<const uint4 *>(src + 4);
+            cw[ks][4] = b.x; cw[ks][5] = b.y; cw[ks][6] = b.z; cw[ks][7] = b.w;
+        }
+    }
+}
 template <class VF, class = void>
 struct VfArgsToLds : std::false_type {};  // the format's accumulator hand-off reads its Args
 template <class VF>
@@ -1139,6 +1176,35 @@ struct VGil {
         uint32_t cw[2][NT];
         float s[NG], z[NG];  // scale / zero of token `lane`
     };
+    // register units (private-ring shapes): a unit is loaded from HBM into
+    // registers one unit ahead of its use, with no LDS copy
+    static constexpr bool kRegUnits = kPrivateRing;
+    struct Raw {
+        uint32_t cw[2][NT];  // unshifted words
+        SZT s[NG], z[NG];
+    };
+    __device__ static void load(Raw &u, const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+                                int lane) {
+        load_code_words<D, NT, TPW>(u.cw, a.codes, bh, cap, t0, t_last, lane);
+        const int64_t tok = min(t0 + lane, t_last);
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            u.s[k] = a.scales[(bh * cap + tok) * NG + k];
+            u.z[k] = a.zeros[(bh * cap + tok) * NG + k];
+        }
+    }
+    __device__ static void from_raw(Tile &tv, const Raw &u, int lane) {
+        const int sh = BITS == 2 ? 8 * ((lane >> 4) & 1) : 0;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) tv.cw[ks][n] = u.cw[ks][n] >> sh;
+#pragma unroll
+        for (int k = 0; k < NG; ++k) {
+            tv.s[k] = (float)u.s[k];
+            tv.z[k] = (float)u.z[k];
+        }
+    }
     struct State {
         f32x4 bias;               // 128 * sum of the staged A rows, laid out as acc
         float zs[kMfmaRows][NG];  // sum of p * z
@@ -1396,6 +1462,24 @@ struct VTq {
         uint32_t cw[2][NT];  // as VGil: the lane's 8 tokens of dims 8*(lane%16) + n
         float n;             // norm of token `lane`
     };
+    static constexpr bool kRegUnits = false;  // its larger State leaves no registers for two units
+    struct Raw {
+        uint32_t cw[2][NT];
+        float n;
+    };
+    __device__ static void load(Raw &u, const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
+                                int lane) {
+        load_code_words<D, NT, TPW>(u.cw, a.codes, bh, cap, t0, t_last, lane);
+        u.n = a.norms[bh * cap + min(t0 + lane, t_last)];
+    }
+    __device__ static void from_raw(Tile &tv, const Raw &u, int lane) {
+        const int sh = 8 * ((lane >> 4) & 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int n = 0; n < NT; ++n) tv.cw[ks][n] = u.cw[ks][n] >> sh;
+        tv.n = u.n;
+    }
     struct State {
         f32x4 bias;          // 128 * sum of the staged A rows, laid out as acc
         f32x4 b1[NT];        // sum_t A (128 + 2 bit1)
@@ -1667,6 +1751,34 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     auto priv_slot = [&](int s) { return (uint32_t)((wv * K::kPrivSlots + s) * K::kSlot); };
     int nq = 0;  // private rings: units this wave has issued
     int issued = 0, landed = 0;
+    // register units: a wave's unit u (index row, value data, heavy key
+    // dims of token `lane`) loaded into one of two register sets, the next
+    // unit's loads issued before the current one is computed
+    constexpr bool kRegs = VfRegUnits<VF>::value;
+    constexpr bool HV = VfHeavyMfma<VF>::value;
+    constexpr int HVN = HV ? kMaxHeavyMfma / 8 : 1;
+    struct RegUnit {
+        IdxRow<NB> ir;
+        typename RawUnitOf<VF, kRegs>::type raw;
+        uint4 khv[HVN];
+    };
+    auto load_ru = [&](RegUnit &x, int u) {
+        if constexpr (kRegs) {
+            const int64_t t0 = t_beg + (int64_t)u * kWave;
+            const int64_t tk = min(t0 + lane, t_last);
+            x.ir.load(c.idx + (bh * c.cap + tk) * NB, true);
+            VF::load(x.raw, va, bh, c.cap, t0, t_last, lane);
+            if constexpr (HV) {
+                if (c.nhd > 0) {
+                    const uint4 *hp = reinterpret_cast<const uint4 *>(c.kheavy + (bh * c.cap + tk) * c.nhd);
+#pragma unroll
+                    for (int j8 = 0; j8 < HVN; ++j8)
+                        if (8 * j8 < c.nhd) x.khv[j8] = hp[j8];
+                }
+            }
+        }
+    };
+    RegUnit ua, ub;
 
     // Prologue.  The compute waves' small loads (query element, permutation
     // entry, codebook entries) are issued before the loader's first tiles, so
@@ -1867,7 +1979,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 cb_lo[t] = cp[kWave];
             }
         }
-        if constexpr (K::kPriv) {
+        if constexpr (kRegs) {
+            // this wave's first unit streams into registers while the LUT is built
+            if (wv < n_units) load_ru(ua, wv);
+        } else if constexpr (K::kPriv) {
             // this wave's first units (u = wv + k*NC) stream in while the LUT is built
             for (; nq < K::kPrivSlots && wv + nq * NC < n_units; ++nq)
                 issue_at(wv + nq * NC, ring_l + priv_slot(nq));
@@ -1973,7 +2088,6 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         // entries are zero): A operands of v_mfma_f32_4x4x4f16 products with
         // each token's own dims, query row lane%4, dims 4kk .. 4kk+3, split
         // fp16 hi and lo * 2^11 (the lo part only for non-fp16 queries)
-        constexpr bool HV = VfHeavyMfma<VF>::value;
         constexpr int HK = HV ? kMaxHeavyMfma / 4 : 1;
         f16x4 hah[HK], hal[HK];
         const int nh4 = HV ? c.nhd >> 2 : 0;
@@ -1998,60 +2112,9 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             if (wv == 0 && has_buf) buffer_share(va);
 
         _Float16 *pw = pst + wv * VF::kPRows * kPStride;
-        for (int u = wv, uk = 0; u < n_units; u += NC, ++uk) {
-            const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
-            const int slot = K::kPriv ? uk % K::kPrivSlots : j % K::kSlots;
-            // the heavy dims of token `lane` (the split's last token past its
-            // end), loaded while the tile is waited on and the LUT read
-            uint4 khv[HV ? kMaxHeavyMfma / 8 : 1];
-            if constexpr (HV) {
-                if (nh4 > 0) {
-                    const int64_t tk = min(t_beg + (int64_t)u * kWave + lane, t_last);
-                    const uint4 *hp = reinterpret_cast<const uint4 *>(c.kheavy + (bh * c.cap + tk) * c.nhd);
-#pragma unroll
-                    for (int j8 = 0; j8 < kMaxHeavyMfma / 8; ++j8)
-                        if (2 * j8 < nh4) khv[j8] = hp[j8];
-                }
-            }
-            if constexpr (K::kPriv) {
-                // this wave's copies of unit u have landed (its later units
-                // stay in flight)
-                wait_oldest_tile<LPT, K::kPrivSlots>(nq - uk);
-            } else {
-                int spins = 0;
-                while (ready[slot] != j) {
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins > c.spin_limit) {
-                        wait_gave_up(kWaitTile);
-                        break;
-                    }
-                }
-            }
-            asm volatile("" ::: "memory");
-            // copy the tile (index rows and values) into registers and
-            // release the slot at once
-            const char *sb = K::kPriv ? ring + priv_slot(slot) : ring + slot * K::kSlot;
-            const char *ib = sb + K::kTileV + sub * K::kTileI1;
-            IdxRow<NB> ir;
-            if constexpr (NB == 16) {
-                const uint4 w4 = *reinterpret_cast<const uint4 *>(ib + lane * 16);
-                ir.w[0] = w4.x; ir.w[1] = w4.y; ir.w[2] = w4.z; ir.w[3] = w4.w;
-            } else {
-                const uint2 w2 = *reinterpret_cast<const uint2 *>(ib + lane * 8);
-                ir.w[0] = w2.x; ir.w[1] = w2.y;
-            }
-            typename VF::Tile tv;
-            VF::copy(tv, sb, sub, lane);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            if constexpr (K::kPriv) {
-                // the slot's data is in registers: refill it with this wave's next unit
-                if (wv + nq * NC < n_units) {
-                    issue_at(wv + nq * NC, ring_l + priv_slot(nq % K::kPrivSlots));
-                    ++nq;
-                }
-            } else {
-                if (lane == 0) done[slot * K::kSub + sub] = j;
-            }
+        // one 64-token unit of this wave: scores, online softmax, P.V
+        auto step = [&](const IdxRow<NB> &ir, typename VF::Tile &tv, const uint4 (&khv)[HVN],
+                        int u) __attribute__((always_inline)) {
             const int64_t t0 = t_beg + (int64_t)u * kWave;
             // tokens of this tile still inside the split (wave-uniform, 1..64)
             const int n_in = (int)min(t_end - t0, (int64_t)kWave);
@@ -2134,6 +2197,82 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 }
             }
             VF::pv(tv, vst, acc, p, corr, moved, n_in, pw, lane);
+        };
+        if constexpr (kRegs) {
+            // two register sets in turn (past the last unit the loads repeat
+            // the last one, so the loop stays straight-line)
+            for (int u = wv; u < n_units; u += 2 * NC) {
+                load_ru(ub, min(u + NC, n_units - 1));
+                {
+                    typename VF::Tile tv;
+                    VF::from_raw(tv, ua.raw, lane);
+                    step(ua.ir, tv, ua.khv, u);
+                }
+                if (u + NC >= n_units) break;
+                load_ru(ua, min(u + 2 * NC, n_units - 1));
+                {
+                    typename VF::Tile tv;
+                    VF::from_raw(tv, ub.raw, lane);
+                    step(ub.ir, tv, ub.khv, u + NC);
+                }
+            }
+        } else {
+        for (int u = wv, uk = 0; u < n_units; u += NC, ++uk) {
+            const int j = u / K::kSub, sub = u - j * K::kSub;  // ring tile, sub-tile
+            const int slot = K::kPriv ? uk % K::kPrivSlots : j % K::kSlots;
+            // the heavy dims of token `lane` (the split's last token past its
+            // end), loaded while the tile is waited on and the LUT read
+            uint4 khv[HVN];
+            if constexpr (HV) {
+                if (nh4 > 0) {
+                    const int64_t tk = min(t_beg + (int64_t)u * kWave + lane, t_last);
+                    const uint4 *hp = reinterpret_cast<const uint4 *>(c.kheavy + (bh * c.cap + tk) * c.nhd);
+#pragma unroll
+                    for (int j8 = 0; j8 < kMaxHeavyMfma / 8; ++j8)
+                        if (2 * j8 < nh4) khv[j8] = hp[j8];
+                }
+            }
+            if constexpr (K::kPriv) {
+                // this wave's copies of unit u have landed (its later units
+                // stay in flight)
+                wait_oldest_tile<LPT, K::kPrivSlots>(nq - uk);
+            } else {
+                int spins = 0;
+                while (ready[slot] != j) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > c.spin_limit) {
+                        wait_gave_up(kWaitTile);
+                        break;
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");
+            // copy the tile (index rows and values) into registers and
+            // release the slot at once
+            const char *sb = K::kPriv ? ring + priv_slot(slot) : ring + slot * K::kSlot;
+            const char *ib = sb + K::kTileV + sub * K::kTileI1;
+            IdxRow<NB> ir;
+            if constexpr (NB == 16) {
+                const uint4 w4 = *reinterpret_cast<const uint4 *>(ib + lane * 16);
+                ir.w[0] = w4.x; ir.w[1] = w4.y; ir.w[2] = w4.z; ir.w[3] = w4.w;
+            } else {
+                const uint2 w2 = *reinterpret_cast<const uint2 *>(ib + lane * 8);
+                ir.w[0] = w2.x; ir.w[1] = w2.y;
+            }
+            typename VF::Tile tv;
+            VF::copy(tv, sb, sub, lane);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if constexpr (K::kPriv) {
+                // the slot's data is in registers: refill it with this wave's next unit
+                if (wv + nq * NC < n_units) {
+                    issue_at(wv + nq * NC, ring_l + priv_slot(nq % K::kPrivSlots));
+                    ++nq;
+                }
+            } else {
+                if (lane == 0) done[slot * K::kSub + sub] = j;
+            }
+            step(ir, tv, khv, u);
+        }
         }
     }
     __syncthreads();  // every tile consumed; the ring is free for the merge
@@ -2253,14 +2392,16 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     __syncthreads();
     if (!*last) return;
 
-    // Last split of this column: merge.  With up to kMergeParts * 16
-    // splits, thread (part, chunk) loads float4 `chunk` of the partials of
-    // splits part, part + kMergeParts, ... (and their (m, l)) into registers
-    // with every load in flight at once (one memory round trip), weights them
-    // by its own maximum, and the parts combine through LDS.
+    // Last split of this column: merge.  With up to kMergeParts *
+    // kMergeLoads splits, thread (part, chunk) loads float4 `chunk` of the
+    // partials of splits part, part + kMergeParts, ... and their (m, l) into
+    // registers, every load in flight at once (one memory round trip; slots
+    // past the last split reload it and get weight 0, so the loads stay
+    // unconditional), weights them by its own maximum, and the parts
+    // combine through LDS.
     constexpr int CH = R * D / 4;
     constexpr int kMergeParts = THREADS / CH >= 4 ? 4 : THREADS / CH;
-    constexpr int kMergeLoads = 16;
+    constexpr int kMergeLoads = kMergeParts >= 4 ? 8 : 16;
     if (kMergeParts >= 2 && S <= kMergeParts * kMergeLoads) {
         const int cidx = tid % CH, part = tid / CH;
         const int mr = cidx / (D / 4), md0 = (cidx - mr * (D / 4)) * 4;
@@ -2271,24 +2412,21 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             u32x2 mv[kMergeLoads];
 #pragma unroll
             for (int j = 0; j < kMergeLoads; ++j) {
-                const int s2 = part + kMergeParts * j;
-                if (s2 < S) {
-                    const int64_t sl = ((int64_t)col * S + s2) * R + mr;
-                    av[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                          acc_rs, (uint32_t)((sl * D + md0) * 4), 0, kCpolSc1));
-                    mv[j] = __builtin_amdgcn_raw_buffer_load_b64(ml_rs, (uint32_t)(sl * 8), 0, kCpolSc1);
-                }
+                const int s2 = min(part + kMergeParts * j, S - 1);
+                const int64_t sl = ((int64_t)col * S + s2) * R + mr;
+                av[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      acc_rs, (uint32_t)((sl * D + md0) * 4), 0, kCpolSc1));
+                mv[j] = __builtin_amdgcn_raw_buffer_load_b64(ml_rs, (uint32_t)(sl * 8), 0, kCpolSc1);
             }
 #pragma unroll
             for (int j = 0; j < kMergeLoads; ++j)
-                if (part + kMergeParts * j < S) Mr = fmaxf(Mr, __uint_as_float(mv[j][0]));
+                Mr = part + kMergeParts * j < S ? fmaxf(Mr, __uint_as_float(mv[j][0])) : Mr;
 #pragma unroll
-            for (int j = 0; j < kMergeLoads; ++j)
-                if (part + kMergeParts * j < S) {
-                    const float w = fast_exp2(__uint_as_float(mv[j][0]) - Mr);
-                    Lr = fmaf(__uint_as_float(mv[j][1]), w, Lr);
-                    Ar += av[j] * w;
-                }
+            for (int j = 0; j < kMergeLoads; ++j) {
+                const float w = part + kMergeParts * j < S ? fast_exp2(__uint_as_float(mv[j][0]) - Mr) : 0.f;
+                Lr = fmaf(__uint_as_float(mv[j][1]), w, Lr);
+                Ar += av[j] * w;
+            }
         }
         // parts 1.. hand their (M, L, A) to part 0 through LDS (the ring)
         float *pm = reinterpret_cast<float *>(ring);  // [kMergeParts - 1][6][CH]
