@@ -375,6 +375,8 @@ def test_append_values_il8_roundtrip_and_offsets():
         (1, 8, 2, 64, 513, 1, False, 0, None),       # head_dim 64
         (1, 4, 1, 128, 64, 3, True, 0, None),        # prefill rows, causal
         (2, 6, 2, 64, 300, 5, True, 3, 320),         # several row groups
+        (1, 8, 2, 128, 4096, 1, False, 48, None),    # 48 splits: the merge stages partials in LDS
+        (1, 8, 2, 128, 4096, 1, False, 31, None),    # 31 splits: a register merge with one slot past the end
     ])
 def test_decode_il8_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, cap):
     cap = cap or ((t_kv + 7) // 8) * 8
@@ -507,6 +509,8 @@ def test_pack_grouped_il_roundtrip(bits, d, t_kv, cap):
         (1, 4, 1, 64, 600, 1, 4, 64, "f32", False, 3, 608),       # head_dim 64, 1 group, f32
         (1, 4, 1, 128, 64, 3, 2, 64, "f16", True, 0, 64),         # prefill rows, causal
         (2, 6, 2, 128, 300, 5, 2, 64, "f16", True, 3, 320),       # several row groups
+        (1, 8, 2, 128, 4096, 1, 2, 64, "f16", False, 40, 4096),   # 40 splits: partials staged in LDS
+        (1, 8, 2, 128, 4000, 1, 2, 64, "f16", False, 29, 4000),   # 29 splits: four-part register merge
     ])
 def test_decode_grouped_il_matches_oracle(b, hq, hkv, d, t_kv, t_q, bits, group, sz, causal, splits,
                                           cap):
