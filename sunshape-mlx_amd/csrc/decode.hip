@@ -3283,26 +3283,36 @@ static int launch_merge(const DecodeCommon &c, const DecodeShape &s, hipStream_t
     return SS_OK;
 }
 
+// Once per instance of the matrix-core decode kernel: the device must hold
+// its LDS, and its dynamic LDS size is set.
+template <int D, class VF>
+static int mfma_kernel_setup() {
+    constexpr int NC = VF::kComputeWaves;
+    using K = WsCfg<D, NC, VF>;
+    auto kern = decode_attn_mfma_kernel<D, NC, VF>;
+    static bool done = false;
+    if (done) return SS_OK;
+    int dev = 0, max_lds = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(LDS)");
+    SS_UNSUPPORTED(max_lds >= K::kLds, "decode needs %d bytes of LDS per workgroup, device has %d", K::kLds,
+                   max_lds);
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            K::kLds);
+    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
+    done = true;
+    return SS_OK;
+}
+
 template <int D, class VF>
 static int launch_mfma_kernel(DecodeCommon c, const typename VF::Args &va, const DecodeShape &s,
                               hipStream_t st) {
     constexpr int NC = VF::kComputeWaves;
     using K = WsCfg<D, NC, VF>;
     auto kern = decode_attn_mfma_kernel<D, NC, VF>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        int dev = 0, max_lds = 0;
-        hipError_t e = hipGetDevice(&dev);
-        if (e == hipSuccess)
-            e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev);
-        if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(LDS)");
-        SS_UNSUPPORTED(max_lds >= K::kLds, "decode needs %d bytes of LDS per workgroup, device has %d",
-                       K::kLds, max_lds);
-        e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, K::kLds);
-        if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode mfma)");
-        attr_set = true;
-    }
+    const int rc = mfma_kernel_setup<D, VF>();
+    if (rc) return rc;
     hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(K::kWaves * kWave), K::kLds, st, c, va);
     SS_LAUNCH_CHECK("decode_attn_mfma_kernel launch");
     if (c.fused_merge) return SS_OK;  // the kernel merges its splits itself
@@ -4252,13 +4262,8 @@ extern "C" int ss_decode_attn_turboquant_il(
             constexpr int NC = VF::kComputeWaves;
             using K = WsCfg<DD, NC, VF>;
             auto kern = decode_attn_mfma_kernel<DD, NC, VF>;
-            static bool attr_set = false;
-            if (!attr_set) {
-                const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, K::kLds);
-                if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(decode turboquant mfma)");
-                attr_set = true;
-            }
+            const int src = mfma_kernel_setup<DD, VF>();
+            if (src) return src;
             const typename VF::Args va{va128.codes, va128.norms, va128.l0, va128.l1, va128.l2};
             hipLaunchKernelGGL(kern, dim3(s.S, s.n_cols), dim3(K::kWaves * kWave), K::kLds, st, c, va);
             SS_LAUNCH_CHECK("decode_attn_mfma_kernel (turboquant) launch");
