@@ -26,6 +26,18 @@
 // heads sharing every key and value read.  Each wave owns 16 rows outright
 // (its own online softmax and accumulators), so there is no split, merge or
 // cross-wave combine.  Causal rows stop at q_offset + position.
+//
+// fp16 queries take prefill32_il8_kernel instead: waves of 32 rows on
+// v_mfma_f32_32x32x16_f16 (S^T of 32 tokens x 32 rows: lane l holds token
+// l%32's block 2ks + l/32 as A, row l%32's dims 16ks + 8(l/32) .. as B) and
+// v_mfma_f32_32x32x8f16 for P.V (the S^T accumulator entries 4kk .. 4kk+3
+// of lane l are row l%32's tokens 8kk + 4(l/32) .., the A operand of step
+// kk), so every key gather and value load serves 32 rows.  Wider queries
+// need a second (lo) query operand, which leaves no registers for 32 rows.
+//
+// The grid is (batch x KV heads, position groups) with the position groups
+// in reverse order along y: workgroups are dispatched x fastest, so the
+// heaviest causal ranges of every head go first.
 #include "ss_common.hpp"
 
 namespace ss {
@@ -35,9 +47,11 @@ namespace {
 typedef _Float16 pf_f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPfWaves = 8;
-constexpr int kPfRows = 16 * kPfWaves;   // query rows of a workgroup
+constexpr int kPfRows = 16 * kPfWaves;   // query rows of a workgroup (16 per wave)
+constexpr int kPfRows32 = 32 * kPfWaves; // the same with 32 rows per wave (fp16 queries)
 constexpr int kPfD = 128;
 constexpr int kPfNB = 16;
 constexpr int kPfRows16 = kPfNB * 256;   // codebook rows (block, centroid), 16 bytes each
@@ -61,9 +75,14 @@ struct PrefillArgs {
     int64_t q_offset;
     void *out;
     int out_dtype;
-    int npos;                // positions per workgroup = kPfRows / rep
+    int npos;                // positions per workgroup = rows per workgroup / rep
     int n_pg;                // position groups
 };
+
+// x of lane `src` (0..63) of this wave
+__device__ __forceinline__ float lane_read(float x, int src) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
+}
 
 __device__ __forceinline__ float xor_max(float x, int m) {
     return fmaxf(x, __shfl_xor(x, m));
@@ -71,7 +90,7 @@ __device__ __forceinline__ float xor_max(float x, int m) {
 
 }  // namespace
 
-__global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(PrefillArgs a) {
     constexpr int TH = kPfWaves * kWave;
     extern __shared__ __align__(16) float4 pf_smem[];
     char *lds = reinterpret_cast<char *>(pf_smem);
@@ -80,8 +99,10 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, l16 = lane & 15;
     // the longest causal ranges first: position groups in reverse order
-    const int pg = a.n_pg - 1 - (int)blockIdx.x;
-    const int64_t bh = blockIdx.y;
+    // along y, the (batch, KV head) columns along x, so that workgroups are
+    // dispatched heaviest position group first across every head
+    const int pg = a.n_pg - 1 - (int)blockIdx.y;
+    const int64_t bh = blockIdx.x;
     const int64_t bb = bh / a.n_kv_heads;
     const int kvh = (int)(bh - bb * a.n_kv_heads);
 
@@ -294,6 +315,224 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill_il8_kernel(PrefillAr
     }
 }
 
+__global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(PrefillArgs a) {
+    constexpr int TH = kPfWaves * kWave;
+    extern __shared__ __align__(16) float4 pf_smem[];
+    char *lds = reinterpret_cast<char *>(pf_smem);
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hb = lane >> 5, l32 = lane & 31;
+    // the longest causal ranges first: position groups in reverse order
+    const int pg = a.n_pg - 1 - (int)blockIdx.y;
+    const int64_t bh = blockIdx.x;
+    const int64_t bb = bh / a.n_kv_heads;
+    const int kvh = (int)(bh - bb * a.n_kv_heads);
+
+    // 1. the prepared codebook, row-major: the hi part of row (block,
+    //    centroid) at (block * 256 + centroid) * 16 bytes, its lo part 64 KB
+    //    further.  Tile t = (bg, ct) holds 64 lanes' rows: block bg*4 + l/16,
+    //    centroid ct*16 + l%16.
+    uint4 *lds4 = reinterpret_cast<uint4 *>(lds);
+    for (int i = tid; i < 4 * a.nct * kWave; i += TH) {
+        const int t = i >> 6, l = i & 63, bg = t / a.nct, ct = t - bg * a.nct;
+        const int row = (bg * 4 + (l >> 4)) * 256 + ct * 16 + (l & 15);
+        lds4[row] = a.codebook[(int64_t)t * 2 * kWave + l];
+        lds4[kPfRows16 + row] = a.codebook[(int64_t)t * 2 * kWave + kWave + l];
+    }
+
+    // 2. this lane's query row (the S^T column l%32 of wave wv): B operands
+    //    of the 8 k-steps, dims 16*ks + 8*hb .. +7, codec-permuted
+    const int r = wv * 32 + l32;
+    const int p = r / a.rep, h = r - p * a.rep;
+    const int64_t pos = (int64_t)pg * a.npos + p;
+    const bool rok = pos < a.t_q;
+    const int64_t qoff = ((bb * a.n_q_heads + (int64_t)kvh * a.rep + h) * a.t_q + (rok ? pos : 0)) *
+                         kPfD;
+    pf_f16x8 qh[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int j = 16 * ks + 8 * hb + e;
+            const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
+            const float x =
+                rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
+            qh[ks][e] = (_Float16)x;  // fp16 queries: exact
+        }
+    __syncthreads();
+    // a wave whose rows all lie past the prompt has nothing to do (no
+    // barrier follows)
+    const int64_t wave_pos0 = (int64_t)pg * a.npos + (wv * 32) / a.rep;
+    if (wave_pos0 >= a.t_q) return;
+
+    // scores stay in the prepared codebook's units (hi + lo * 2^-11); mul
+    // takes them to log2 units inside the exponent
+    const float mul = *a.cb_mul * kLog2e;
+    // keys this workgroup reads: causal rows stop at q_offset + position
+    const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
+    const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;
+    // token indices below are 32-bit (cap < 2^24 checked on the host)
+    const int t_end32 = (int)t_end;
+    // this lane's row limit; rows past the prompt are never stored, so they
+    // need no mask
+    const int lim32 = (!rok || !a.causal) ? 0x7fffffff : (int)(a.q_offset + pos);
+    // the wave's smallest limit: sub-tiles entirely below it need no mask
+    const int lim_min32 = a.causal ? (int)(a.q_offset + wave_pos0) : 0x7fffffff;
+    const int n_sub = t_end32 > 0 ? (t_end32 + 31) / 32 : 0;
+    const int t_last = max(t_end32 - 1, 0);
+    const uint8_t *idx_head = a.idx + bh * a.cap * kPfNB;
+    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap * kPfD);
+
+    float m = -1e30f, lsum = 0.f;  // row l32 (lsum: this lane's half of its tokens)
+    pf_f32x16 acc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[nt][i] = 0.f;
+
+    // the index row of token t0 + l32 (both lane halves read the same row)
+    auto load_idx = [&](uint4 &ir, int sub) {
+        ir = *reinterpret_cast<const uint4 *>(idx_head + (uint32_t)min(32 * sub + l32, t_last) * kPfNB);
+    };
+    uint4 ir_a, ir_b;
+    if (n_sub > 0) load_idx(ir_a, 0);
+
+    auto do_sub = [&](const uint4 &ir_cur, uint4 &ir_nxt, int sub) __attribute__((always_inline)) {
+        const int t0 = 32 * sub;
+        // the sub-tile's value operands (4 tokens of one dim, 8 bytes) for the
+        // 4 steps of 8 tokens and 4 n-tiles of 32 dims, issued first so they
+        // land while the scores are computed; 8-token blocks past the last
+        // key clamp to its block (their weights are zero)
+        uint2 vop[4][4];
+        const int blk_last = t_last >> 3;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const uint32_t blk = (uint32_t)min((t0 + 8 * kk) >> 3, blk_last);
+            const uint32_t off = ((blk * kPfD + l32) * 8 + 4 * hb) * 2;
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                vop[kk][nt] = *reinterpret_cast<const uint2 *>(v_head + off + nt * 512);
+        }
+        load_idx(ir_nxt, min(sub + 1, n_sub - 1));
+        // scores S^T[token][row] of 32 tokens x 32 rows: lane l holds row
+        // l%32 and tokens 8*(i/4) + 4*hb + i%4 (i = 0..15)
+        pf_f32x16 sh, sl;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sh[i] = sl[i] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int blk = 2 * ks + hb;
+            const uint32_t w = (blk >> 2) == 0 ? ir_cur.x : (blk >> 2) == 1 ? ir_cur.y
+                             : (blk >> 2) == 2 ? ir_cur.z : ir_cur.w;
+            const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * (blk & 3), 8);
+            const char *row = lds + (blk * 256 + c) * 16;
+            const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
+            const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
+            sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+        }
+        float sv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sv[i] = fmaf(sl[i], 1.f / kPfSplit, sh[i]);
+        // a sub-tile below every row's limit and the last key is not masked
+        // (wave-uniform)
+        const bool full = t0 + 31 < t_end32 && t0 + 31 <= lim_min32;
+        if (!full) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int tk = t0 + 8 * (i >> 2) + 4 * hb + (i & 3);
+                sv[i] = (tk < t_end32 && tk <= lim32) ? sv[i] : -INFINITY;
+            }
+        }
+        // online softmax of row l32 over the sub-tile's 32 tokens (16 here,
+        // 16 in lane l ^ 32)
+        float mx = sv[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
+        mx = fmaxf(mx, lane_read(mx, lane ^ 32));
+        const float mn = fmaxf(m, mx);  // raw units (mul > 0)
+        const float corr = fast_exp2((m - mn) * mul);
+        m = mn;
+        // x = p * 2^15 = exp2(s * mul - (mn * mul - 15)), split into fp16 hi
+        // and lo; l sums x and is scaled back at the end
+        float ps = 0.f;
+        const float off = fmaf(mn, mul, -15.f);
+        pf_f16x4 phi[4], plo[4];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float x = fast_exp2(fmaf(sv[i], mul, -off));
+            ps += x;
+            const _Float16 hx = (_Float16)x;
+            phi[i >> 2][i & 3] = hx;
+            plo[i >> 2][i & 3] = (_Float16)__builtin_fmaf((float)hx, -1.f, x);
+        }
+        lsum = fmaf(lsum, corr, ps);
+        // accumulator rows 8*(i/4) + 4*hb + i%4 take the correction of their
+        // own rows (held by lanes 0..31)
+        if (__builtin_amdgcn_ballot_w64(corr != 1.f) != 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float ci = lane_read(corr, 8 * (i >> 2) + 4 * hb + (i & 3));
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) acc[nt][i] *= ci;
+            }
+        }
+        if (t0 + 32 > t_end32) {  // the last sub-tile (wave-uniform)
+            // zero the values of tokens past the last key (their weights are
+            // zero, the stale halves need not be finite)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int n_ok = max(min(t_end32 - (t0 + 8 * kk + 4 * hb), 4), 0);
+                const uint32_t mx_ = n_ok >= 2 ? 0xffffffffu : n_ok == 1 ? 0x0000ffffu : 0u;
+                const uint32_t my_ = n_ok >= 4 ? 0xffffffffu : n_ok == 3 ? 0x0000ffffu : 0u;
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) {
+                    vop[kk][nt].x &= mx_;
+                    vop[kk][nt].y &= my_;
+                }
+            }
+        }
+        // O[row][dim] += P[row][t] V[t][dim]: step kk takes tokens 8kk ..
+        // 8kk+7, the lane's four of them being accumulator entries 4kk ..
+        // 4kk+3 of the scores
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, vop[kk][nt]);
+                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(phi[kk], b, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(plo[kk], b, acc[nt], 0, 0, 0);
+            }
+        }
+    };
+    for (int sub = 0; sub < n_sub; sub += 2) {
+        do_sub(ir_a, ir_b, sub);
+        if (sub + 1 >= n_sub) break;
+        do_sub(ir_b, ir_a, sub + 1);
+    }
+
+    // 3. rows 8*(i/4) + 4*hb + i%4 of the accumulators: their l (the row's
+    //    two lane halves summed), then the output
+    const float L = lsum + lane_read(lsum, lane ^ 32);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int ri = 8 * (i >> 2) + 4 * hb + (i & 3);
+        const float Li = lane_read(L, ri);
+        const int rr = wv * 32 + ri;
+        const int pp = rr / a.rep, hh = rr - pp * a.rep;
+        const int64_t opos = (int64_t)pg * a.npos + pp;
+        if (opos < a.t_q) {
+            const int64_t off =
+                ((bb * a.n_q_heads + (int64_t)kvh * a.rep + hh) * a.t_q + opos) * kPfD;
+            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^15
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                store_from_f32(a.out, a.out_dtype, off + 32 * nt + l32, acc[nt][i] * inv);
+        }
+    }
+}
+
 }  // namespace ss
 
 using namespace ss;
@@ -350,21 +589,26 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
     a.q_offset = q_offset;
     a.out = out;
     a.out_dtype = out_dtype;
-    a.npos = kPfRows / rep;
+    // fp16 queries: waves of 32 rows on 32x32 products (each key gather and
+    // value load serves twice the rows); wider queries, split into fp16 hi
+    // and lo parts, keep 16-row waves (their second query operand leaves no
+    // registers for 32 rows)
+    const bool rows32 = q_dtype == SS_F16;
+    a.npos = (rows32 ? kPfRows32 : kPfRows) / rep;
     const int64_t n_pg = (t_q + a.npos - 1) / a.npos;
-    SS_UNSUPPORTED(n_pg <= 0x7fffffff && batch * n_kv_heads <= 65535, "grid too large");
+    SS_UNSUPPORTED(n_pg <= 65535 && batch * n_kv_heads <= 0x7fffffff, "grid too large");
     a.n_pg = (int)n_pg;
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(prefill_il8_kernel),
+    auto kern = rows32 ? prefill32_il8_kernel : prefill16_il8_kernel;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[rows32]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  kPfLdsBytes);
         if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(prefill)");
-        attr_set = true;
+        attr_set[rows32] = true;
     }
-    hipLaunchKernelGGL(prefill_il8_kernel, dim3(a.n_pg, (unsigned)(batch * n_kv_heads)),
-                       dim3(kPfWaves * kWave), kPfLdsBytes, reinterpret_cast<hipStream_t>(stream),
-                       a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(batch * n_kv_heads), a.n_pg), dim3(kPfWaves * kWave),
+                       kPfLdsBytes, reinterpret_cast<hipStream_t>(stream), a);
     SS_LAUNCH_CHECK("prefill_il8_kernel launch");
     return SS_OK;
 }
