@@ -2351,9 +2351,8 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             f32x4 A;
             combine4(r, d0, M, L, A);
             if (row_ok(r)) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    store_from_f32(c.out, c.out_dtype, row_off(r) + d0 + k, L > 0.f ? A[k] / L : 0.f);
+                const float iv = L > 0.f ? 1.f / L : 0.f;
+                store4_from_f32(c.out, c.out_dtype, row_off(r) + d0, A[0] * iv, A[1] * iv, A[2] * iv, A[3] * iv);
             }
         }
         return;
@@ -2453,9 +2452,9 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 Mr = Mn;
             }
             if (row_ok(mr)) {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    store_from_f32(c.out, c.out_dtype, row_off(mr) + md0 + k, Lr > 0.f ? Ar[k] / Lr : 0.f);
+                const float iv = Lr > 0.f ? 1.f / Lr : 0.f;
+                store4_from_f32(c.out, c.out_dtype, row_off(mr) + md0, Ar[0] * iv, Ar[1] * iv, Ar[2] * iv,
+                                Ar[3] * iv);
             }
         }
         if (tid == 0)
@@ -2548,9 +2547,8 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     if (tid < CH4 && row_ok(mr)) {
         const float L = lrow[mr];
         const f32x4 A = acc0 + acc1;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            store_from_f32(c.out, c.out_dtype, row_off(mr) + md0 + k, L > 0.f ? A[k] / L : 0.f);
+        const float iv = L > 0.f ? 1.f / L : 0.f;
+        store4_from_f32(c.out, c.out_dtype, row_off(mr) + md0, A[0] * iv, A[1] * iv, A[2] * iv, A[3] * iv);
     }
     if (tid == 0)
         __hip_atomic_store(c.part_cnt + (int64_t)col * c.cnt_stride, 0, __ATOMIC_RELAXED,

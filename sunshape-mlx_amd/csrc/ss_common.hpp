@@ -66,6 +66,33 @@ __device__ __forceinline__ void store_from_f32(void *p, int dt, int64_t i, float
         reinterpret_cast<__hip_bfloat16 *>(p)[i] = __float2bfloat16(x);
 }
 
+// Elements i .. i+3 of dtype dt: one 16-byte (float32) or 8-byte (16-bit)
+// store when the destination is aligned for it, else four stores.
+__device__ __forceinline__ void store4_from_f32(void *p, int dt, int64_t i, float x0, float x1, float x2,
+                                                float x3) {
+    if (dt == SS_F32) {
+        float *q = reinterpret_cast<float *>(p) + i;
+        if ((reinterpret_cast<uintptr_t>(q) & 15) == 0) {
+            *reinterpret_cast<float4 *>(q) = make_float4(x0, x1, x2, x3);
+            return;
+        }
+    } else {
+        uint16_t *q = reinterpret_cast<uint16_t *>(p) + i;
+        if ((reinterpret_cast<uintptr_t>(q) & 7) == 0) {
+            auto bits = [&](float x) -> uint32_t {
+                return dt == SS_F16 ? (uint32_t)__half_as_ushort(__float2half(x))
+                                    : (uint32_t)__bfloat16_as_ushort(__float2bfloat16(x));
+            };
+            *reinterpret_cast<uint2 *>(q) = make_uint2(bits(x0) | (bits(x1) << 16), bits(x2) | (bits(x3) << 16));
+            return;
+        }
+    }
+    store_from_f32(p, dt, i, x0);
+    store_from_f32(p, dt, i + 1, x1);
+    store_from_f32(p, dt, i + 2, x2);
+    store_from_f32(p, dt, i + 3, x3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
