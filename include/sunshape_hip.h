@@ -288,8 +288,10 @@ int ss_decode_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q
  * reconstructed from the prepared split-fp16 codebook (held in LDS) and
  * Q.K^T and P.V both run on the matrix cores; every workgroup takes
  * ss_prefill_rows_per_workgroup() query rows of one KV group (its rep query
- * heads at consecutive positions; twice that many for fp16 queries, whose
- * waves take 32 rows), so the GQA group size must divide that number.
+ * heads at consecutive positions; twice that many for fp16 and bf16
+ * queries, whose waves take 32 rows; bf16 queries are taken as fp16, exact
+ * within fp16's range and saturating beyond +-65504), so the GQA group size
+ * must divide that number.
  * head_dim 128, 16 blocks of 8, <= 256 centroids, fp16 values.
  * Row i of a head (position q_offset + i) sees keys 0 .. q_offset + i when
  * causal.  Results equal ss_decode_attn_il8's within the decode tolerance.

@@ -27,12 +27,12 @@
 // (its own online softmax and accumulators), so there is no split, merge or
 // cross-wave combine.  Causal rows stop at q_offset + position.
 //
-// fp16 queries take prefill32_il8_kernel instead: waves of 32 rows on
+// fp16 and bf16 queries take prefill32_il8_kernel instead: waves of 32 rows on
 // v_mfma_f32_32x32x16_f16 (S^T of 32 tokens x 32 rows: lane l holds token
 // l%32's block 2ks + l/32 as A, row l%32's dims 16ks + 8(l/32) .. as B) and
 // v_mfma_f32_32x32x8f16 for P.V (the S^T accumulator entries 4kk .. 4kk+3
 // of lane l are row l%32's tokens 8kk + 4(l/32) .., the A operand of step
-// kk), so every key gather and value load serves 32 rows.  Wider queries
+// kk), so every key gather and value load serves 32 rows.  fp32 queries
 // need a second (lo) query operand, which leaves no registers for 32 rows.
 //
 // The grid is (batch x KV heads, position groups) with the position groups
@@ -358,7 +358,11 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
             const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
             const float x =
                 rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
-            qh[ks][e] = (_Float16)x;  // fp16 queries: exact
+            // fp16 queries are exact in fp16, and so are bf16 ones within
+            // fp16's range (an 8-bit mantissa fits in 11 bits), except
+            // below 2^-14 where fp16 keeps fewer bits (an error under 2^-25
+            // per element); beyond +-65504 they saturate
+            qh[ks][e] = (_Float16)fminf(fmaxf(x, -65504.f), 65504.f);
         }
     __syncthreads();
     // a wave whose rows all lie past the prompt has nothing to do (no
@@ -589,11 +593,11 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
     a.q_offset = q_offset;
     a.out = out;
     a.out_dtype = out_dtype;
-    // fp16 queries: waves of 32 rows on 32x32 products (each key gather and
-    // value load serves twice the rows); wider queries, split into fp16 hi
-    // and lo parts, keep 16-row waves (their second query operand leaves no
-    // registers for 32 rows)
-    const bool rows32 = q_dtype == SS_F16;
+    // fp16 and bf16 queries: waves of 32 rows on 32x32 products (each key
+    // gather and value load serves twice the rows); fp32 queries, split into
+    // fp16 hi and lo parts, keep 16-row waves (their second query operand
+    // leaves no registers for 32 rows)
+    const bool rows32 = q_dtype == SS_F16 || q_dtype == SS_BF16;
     a.npos = (rows32 ? kPfRows32 : kPfRows) / rep;
     const int64_t n_pg = (t_q + a.npos - 1) / a.npos;
     SS_UNSUPPORTED(n_pg <= 65535 && batch * n_kv_heads <= 0x7fffffff, "grid too large");
