@@ -442,6 +442,25 @@ def test_decode_il8_query_dtypes_and_small_codebooks(q_dtype, nc, d):
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_decode_il8_misaligned_output(out_dtype):
+    """An output view that starts one element past an aligned address takes
+    the merge's element-wise stores instead of its packed ones, with the same
+    result."""
+    b, hq, hkv, d, t_kv = 1, 8, 2, 128, 3000
+    cents, perm, idx, vals, q = decode_case(77, b, hq, hkv, d, t_kv)
+    args = (t(q), 1.0 / np.sqrt(d), t(perm), t(cents), t(idx), to_il8(vals, t_kv), t_kv)
+    ref = _hip.decode_attn_il8(*args, out_dtype=out_dtype, n_splits=8)
+    n = b * hq * d
+    base = torch.zeros(n + 1, dtype=out_dtype, device=DEV)
+    out = base[1:].view(b, hq, 1, d)
+    assert out.data_ptr() % 8 != 0
+    _hip.decode_attn_il8(*args, out=out, n_splits=8)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), ref.cpu())
+    assert base[0].item() == 0
+
+
 def test_decode_il8_peaked_and_flat_softmax():
     """Probabilities spanning many orders of magnitude (the hi/lo fp16 split
     must keep small ones) and an almost flat softmax."""
