@@ -422,6 +422,20 @@ template <class VF, class = void>
 struct VfRegUnits : std::false_type {};  // units loaded into registers, no LDS ring
 template <class VF>
 struct VfRegUnits<VF, std::void_t<decltype(VF::kRegUnits)>> : std::integral_constant<bool, VF::kRegUnits> {};
+// How far (log2 units) the scores of a whole tile may rise above the running
+// maxima before the matrix-core decodes reduce the maxima over the wave and
+// rescale: the staged probabilities stay at most 2^lag, and most tiles after
+// a split's first skip the reduction and the rescale.  Formats that stage
+// them as bf16 hi/lo pairs take 8, the fp16 staging of the interleaved fp16
+// values 4; without a kMaxLag a format takes 0 (every rise reduces).
+template <class VF, class = void>
+struct VfMaxLag {
+    static constexpr float value = 0.f;
+};
+template <class VF>
+struct VfMaxLag<VF, std::void_t<decltype(VF::kMaxLag)>> {
+    static constexpr float value = VF::kMaxLag;
+};
 
 // The code words of a lane for one 64-token unit of token-interleaved codes
 // ([cap / TPW][D] words per (batch, head)), straight from HBM into
@@ -964,6 +978,11 @@ struct VIl8 {
     static constexpr int NT = D / 16;
     static constexpr int kSub = SUB;
     static constexpr bool kHybridBuffer = false;  // fp16 caches have no token buffer
+    // probabilities staged as fp16 hi/lo pairs of p * 2^11: up to 2^kMaxLag
+    // they stay below the fp16 maximum, and the lo parts stay normal down to
+    // p = 2^-14
+    static constexpr float kMaxLag = 4.f;
+    static constexpr float kPs = 2048.f;
     static constexpr bool kPrivateRing = false;   // 17 KB units: one loader wave, shared ring
     static constexpr int kTileV1 = kWave * D * 2;  // one 64-token sub-tile
     static constexpr int kTileV = kSub * kTileV1;
@@ -1017,7 +1036,7 @@ struct VIl8 {
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int r = 0; r < kMfmaRows; ++r) {
-            const float x = p[r] * kPScale;
+            const float x = p[r] * kPs;
             const _Float16 hi = (_Float16)x;
             const _Float16 lo = (_Float16)(x - (float)hi);
             pw[r * kPStride + lane] = hi;
@@ -1067,7 +1086,7 @@ struct VIl8 {
             for (int r = 0; r < kMfmaRows; ++r)
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
+                    wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPs);
         }
     }
 };
@@ -1179,6 +1198,7 @@ struct VGil {
     // register units (private-ring shapes): a unit is loaded from HBM into
     // registers one unit ahead of its use, with no LDS copy
     static constexpr bool kRegUnits = kPrivateRing;
+    static constexpr float kMaxLag = 8.f;  // bf16 hi/lo probabilities
     struct Raw {
         uint32_t cw[2][NT];  // unshifted words
         SZT s[NG], z[NG];
@@ -1462,7 +1482,8 @@ struct VTq {
         uint32_t cw[2][NT];  // as VGil: the lane's 8 tokens of dims 8*(lane%16) + n
         float n;             // norm of token `lane`
     };
-    static constexpr bool kRegUnits = false;  // its larger State leaves no registers for two units
+    static constexpr bool kRegUnits = true;
+    static constexpr float kMaxLag = 8.f;  // bf16 hi/lo probabilities
     struct Raw {
         uint32_t cw[2][NT];
         float n;
@@ -1482,7 +1503,6 @@ struct VTq {
     }
     struct State {
         f32x4 bias;          // 128 * sum of the staged A rows, laid out as acc
-        f32x4 b1[NT];        // sum_t A (128 + 2 bit1)
         float ws[kMfmaRows]; // sum of p * norm of this lane's tokens
     };
     __device__ static void issue(const Args &a, int64_t bh, int64_t cap, int64_t t0, int64_t t_last,
@@ -1546,8 +1566,6 @@ struct VTq {
     __device__ static void init(State &st) {
         st.bias = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int n = 0; n < NT; ++n) st.b1[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
         for (int r = 0; r < kMfmaRows; ++r) st.ws[r] = 0.f;
     }
     __device__ static void pv(Tile &tv, State &st, f32x4 (&acc)[NT], const float (&p)[kMfmaRows],
@@ -1560,10 +1578,7 @@ struct VTq {
         if (rescale) {
             const f32x4 cv4 = f32x4{corr[0], corr[1], corr[2], corr[3]};
 #pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                acc[n] *= cv4;
-                st.b1[n] *= cv4;
-            }
+            for (int n = 0; n < NT; ++n) acc[n] *= cv4;
             st.bias *= cv4;
 #pragma unroll
             for (int r = 0; r < kMfmaRows; ++r) st.ws[r] *= corr[r];
@@ -1592,9 +1607,17 @@ struct VTq {
         const uint32_t bm = opaque_u32(kBit1Mask), bm2 = opaque_u32(kBit1Mask << 2),
                        bm4 = opaque_u32(kBit1Mask << 4);
         const bf16x8 b128 = __builtin_bit_cast(bf16x8, make_uint4(cbias, cbias, cbias, cbias));
+        // A rows 0-7 (hi, lo of the four query rows) multiply the codes, the
+        // same rows repeated as A rows 8-15 multiply the high code bits: one
+        // accumulator holds both sums (rows 8-15 of acc are the bit-1 sums)
+        const bool top = l16 < 8;
+        const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 a = *reinterpret_cast<const bf16x8 *>(pw + l16 * kPStride + 32 * ks + 8 * g);
+            const uint4 av = *reinterpret_cast<const uint4 *>(pw + (l16 & 7) * kPStride + 32 * ks + 8 * g);
+            const bf16x8 a = __builtin_bit_cast(bf16x8, av);
+            const bf16x8 a_c = __builtin_bit_cast(bf16x8, top ? av : zero4);
+            const bf16x8 a_b = __builtin_bit_cast(bf16x8, top ? zero4 : av);
             st.bias = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b128, st.bias, 0, 0, 0);
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
@@ -1604,31 +1627,34 @@ struct VTq {
                     bf16x8, make_uint4((y & cm) | cbias, (y & cm2) | cbias, (y & cm4) | cbias, (y6 & cm) | cbias));
                 const bf16x8 bb = __builtin_bit_cast(
                     bf16x8, make_uint4((y & bm) | cbias, (y & bm2) | cbias, (y & bm4) | cbias, (y6 & bm) | cbias));
-                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bc, acc[n], 0, 0, 0);
-                st.b1[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bb, st.b1[n], 0, 0, 0);
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_c, bc, acc[n], 0, 0, 0);
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_b, bb, acc[n], 0, 0, 0);
             }
         }
         wave_lds_sync();
     }
-    // rows 0-3 (lanes 0-15) hold the hi parts, rows 4-7 (lanes 16-31) the lo
-    // parts of the four query rows: acc - bias = sum w c and (b1 - bias)/2 =
-    // sum w bit1 of each part (the A rows carry w times the in-place powers
-    // of two, the bias the same).  The L0 sum w term, from the lanes' fp32
+    // acc rows 0-3 (lanes 0-15) hold the hi parts, rows 4-7 (lanes 16-31)
+    // the lo parts of the four query rows: acc - bias = sum w c; rows 8-15
+    // (lanes 32-63) the same parts of sum w (2 bit1) + bias (the A rows carry
+    // w times the in-place powers of two, the bias the same).  Each lane
+    // scales its part by L1 - L0 or (L2 - 2 L1 + L0) / 2 and lanes 0-31 add
+    // the bit-1 part of lane + 32.  The L0 sum w term, from the lanes' fp32
     // sums of p * norm, goes with the hi part.
     __device__ static void to_lds_args(const f32x4 (&acc)[NT], const State &st, const Args &a, float *wa,
                                        int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         float wsum[kMfmaRows];
         wave_sum4_dpp(st.ws, wsum);
-        if (g < 2) {
+        const float f = g < 2 ? a.l1 : a.l2 * 0.5f;
 #pragma unroll
-            for (int r = 0; r < kMfmaRows; ++r) {
-                const float bz = st.bias[r];
-                const float c0 = g == 0 ? a.l0 * wsum[r] : 0.f;
+        for (int r = 0; r < kMfmaRows; ++r) {
+            const float bz = st.bias[r];
+            const float c0 = g == 0 ? a.l0 * wsum[r] : 0.f;
 #pragma unroll
-                for (int n = 0; n < NT; ++n)
-                    wa[(g * kMfmaRows + r) * D + NT * l16 + n] =
-                        c0 + a.l1 * (acc[n][r] - bz) + a.l2 * 0.5f * (st.b1[n][r] - bz);
+            for (int n = 0; n < NT; ++n) {
+                const float v = f * (acc[n][r] - bz);
+                const float vb = __shfl_xor(v, 32);
+                if (g < 2) wa[(g * kMfmaRows + r) * D + NT * l16 + n] = c0 + v + vb;
             }
         }
     }
@@ -1755,6 +1781,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // dims of token `lane`) loaded into one of two register sets, the next
     // unit's loads issued before the current one is computed
     constexpr bool kRegs = VfRegUnits<VF>::value;
+    constexpr float kLag = VfMaxLag<VF>::value;
     constexpr bool HV = VfHeavyMfma<VF>::value;
     constexpr int HVN = HV ? kMaxHeavyMfma / 8 : 1;
     struct RegUnit {
@@ -2157,15 +2184,17 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 }
             }
             // A whole tile every row sees (no causal cut, no split end) whose
-            // scores all stay at or below the rows' running maxima keeps the
-            // maxima: no reduction, no rescale.  Otherwise masked lanes add
-            // -inf (their index rows are real, clamped tokens, so the sums
-            // are finite) and the maxima are reduced over the wave.
+            // scores all stay at most kLag above the rows' running maxima
+            // keeps the maxima: no reduction, no rescale (its probabilities
+            // are at most 2^kLag; l and acc stay relative to the same
+            // maxima).  Otherwise masked lanes add -inf (their index rows are
+            // real, clamped tokens, so the sums are finite) and the maxima
+            // are reduced over the wave.
             bool moved = true;
             if (n_in == kWave && t0 + (kWave - 1) <= lim_min) {
                 uint64_t above = 0;
 #pragma unroll
-                for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r]);
+                for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r] + kLag);
                 moved = above != 0;
             } else {
                 const bool kok = lane < n_in;

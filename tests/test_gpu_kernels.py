@@ -577,6 +577,49 @@ def test_decode_grouped_il_peaked_and_flat_softmax(bits):
         assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
 
 
+def ramp_case(seed, t_kv, cap, rise):
+    """A cache whose scores climb steadily along the tokens by `rise` log2
+    units in all (block 0's centroid c is c * step on every dim, the query
+    constant, every other block's centroids small): tiles keep rising above
+    the running maxima by less and by more than the kernels' lag before a
+    wave-wide reduction."""
+    d, scale = 128, 0.0883883
+    cents, perm, idx, vals, q = decode_case(seed, 1, 4, 1, d, t_kv, cap=cap)
+    cents[1:] *= 0.01
+    qv = 0.5
+    step = rise / (255 * scale * 1.4426950408889634 * qv * 8)
+    cents[0] = (np.arange(256, dtype=np.float32) * step)[:, None] * np.ones(8, np.float32)
+    idx[0, 0, :t_kv, 0] = (np.arange(t_kv) * 255 // max(t_kv - 1, 1)).astype(np.uint8)
+    q = np.full_like(q, qv)
+    q[:, 1::2] *= -1  # two rows fall along the ramp, two climb it
+    return cents, perm, idx, vals, q, scale
+
+
+@pytest.mark.parametrize("rise", [40.0, 600.0])
+def test_decode_rising_scores(rise):
+    """Scores that keep rising along the cache: the matrix-core decodes skip
+    the wave-wide maximum while a tile stays within a few log2 units of the
+    running maxima (staged probabilities above 1) and rescale past it; the
+    fp16-value and grouped 2-bit kernels match the oracle, with two splits
+    (many tiles per wave) and with the default split count."""
+    t_kv, cap, d, bits, group = 5000, 5008, 128, 2, 64
+    cents, perm, idx, vals, q, scale = ramp_case(17, t_kv, cap, rise)
+    _, packed, sc, ze, il = grouped_case(18, 1, 1, t_kv, d, bits, group, cap)
+    gvals = O.dequantize_values(packed[0, 0, :t_kv].cpu().numpy().view(np.uint32),
+                                sc[0, 0, :t_kv].float().cpu().numpy(),
+                                ze[0, 0, :t_kv].float().cpu().numpy(), d, bits, group)[None, None]
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, scale)
+    gref = O.sdpa(q, idx[:, :, :t_kv], gvals, cents, perm, scale)
+    for splits in (2, 0):
+        out = _hip.decode_attn_il8(t(q), scale, t(perm), t(cents), t(idx), to_il8(vals, cap), t_kv,
+                                   out_dtype=torch.float32, n_splits=splits)
+        gout = _hip.decode_attn_grouped_il(t(q), scale, t(perm), t(cents), t(idx), il, sc, ze, bits, group,
+                                           t_kv, out_dtype=torch.float32, n_splits=splits)
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), ref) <= REL_TOL, splits
+        assert rel_err(gout.cpu().numpy(), gref) <= REL_TOL, splits
+
+
 @pytest.mark.parametrize("b,hq,hkv,d,t_kv,t_buf,bits,group,splits", [
     (1, 8, 2, 128, 0, 40, 2, 64, 0),      # buffer only (no compressed tokens)
     (2, 8, 2, 64, 333, 70, 2, 32, 0),     # head_dim 64, buffer longer than one chunk
