@@ -845,7 +845,12 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr float kPScale = 32768.f;  // 2^15
+// Probabilities staged for fp16 products as hi/lo pairs of p * kPScale: with
+// a running-maximum lag of kPLag log2 units they reach 2^kPLag, and
+// 2^kPLag * kPScale stays below the fp16 maximum; the lo parts stay normal
+// down to p = 2^-14.
+constexpr float kPScale = 2048.f;  // 2^11
+constexpr float kPLag = 4.f;
 constexpr int kMfmaRows = 4;
 // Row stride (16-bit elements) of a wave's P staging: 64 tokens plus 8 of
 // padding, so the 16 rows a matrix-core operand read touches start in
@@ -978,11 +983,8 @@ struct VIl8 {
     static constexpr int NT = D / 16;
     static constexpr int kSub = SUB;
     static constexpr bool kHybridBuffer = false;  // fp16 caches have no token buffer
-    // probabilities staged as fp16 hi/lo pairs of p * 2^11: up to 2^kMaxLag
-    // they stay below the fp16 maximum, and the lo parts stay normal down to
-    // p = 2^-14
-    static constexpr float kMaxLag = 4.f;
-    static constexpr float kPs = 2048.f;
+    // probabilities staged as fp16 hi/lo pairs of p * kPScale
+    static constexpr float kMaxLag = kPLag;
     static constexpr bool kPrivateRing = false;   // 17 KB units: one loader wave, shared ring
     static constexpr int kTileV1 = kWave * D * 2;  // one 64-token sub-tile
     static constexpr int kTileV = kSub * kTileV1;
@@ -1036,7 +1038,7 @@ struct VIl8 {
         const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
         for (int r = 0; r < kMfmaRows; ++r) {
-            const float x = p[r] * kPs;
+            const float x = p[r] * kPScale;
             const _Float16 hi = (_Float16)x;
             const _Float16 lo = (_Float16)(x - (float)hi);
             pw[r * kPStride + lane] = hi;
@@ -1086,7 +1088,7 @@ struct VIl8 {
             for (int r = 0; r < kMfmaRows; ++r)
 #pragma unroll
                 for (int n = 0; n < NT; ++n)
-                    wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPs);
+                    wa[(g * kMfmaRows + r) * D + 16 * n + l16] = acc[n][r] * (1.f / kPScale);
         }
     }
 };
@@ -2831,7 +2833,7 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
         if (n_in == kWave && t0 + (kWave - 1) <= lim_min) {
             uint64_t above = 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r]);
+            for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(sc[r] > m[r] + kPLag);
             moved = above != 0;
         } else {
             const bool kok = lane < n_in;

@@ -18,7 +18,7 @@
 // tokens 4*(l/16) .. +3, which is exactly the A operand layout of
 //   O[row][dim] += sum_t P[row][t] * V[t][dim]
 // on v_mfma_f32_16x16x16f16, so the probabilities never leave registers
-// (hi and lo fp16 parts of p * 2^15, two products); B = 4 consecutive tokens
+// (hi and lo fp16 parts of p * 2^11, two products); B = 4 consecutive tokens
 // of one dim, 8 bytes of the interleaved value layout.
 //
 // A workgroup of kPfWaves waves takes 16 * kPfWaves query rows of one KV
@@ -57,6 +57,12 @@ constexpr int kPfNB = 16;
 constexpr int kPfRows16 = kPfNB * 256;   // codebook rows (block, centroid), 16 bytes each
 constexpr int kPfLdsBytes = 2 * kPfRows16 * 16;  // hi rows, then lo rows: 128 KB
 constexpr float kPfSplit = 2048.f;       // lo parts carry 2^11
+// A row keeps its running maximum while a tile's scores stay within kPfLag
+// log2 units above it (no rescale of its accumulators); its probabilities,
+// staged as fp16 hi/lo of p * 2^kPfPExp, then reach 2^(kPfPExp + kPfLag),
+// below the fp16 maximum.
+constexpr float kPfLag = 4.f;
+constexpr float kPfPExp = 11.f;
 
 struct PrefillArgs {
     const void *q;
@@ -236,13 +242,13 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sv[j][i]);
         mx = xor_max(mx, 16);
         mx = xor_max(mx, 32);
-        const float mn = fmaxf(m, mx);  // raw units (mul > 0)
+        const float mn = (mx - m) * mul > kPfLag ? fmaxf(m, mx) : m;  // raw units (mul > 0)
         const float corr = fast_exp2((m - mn) * mul);
         m = mn;
-        // x = p * 2^15 = exp2(s * mul - (mn * mul - 15)), split into fp16 hi
+        // x = p * 2^11 = exp2(s * mul - (mn * mul - 11)), split into fp16 hi
         // and lo; l sums x and is scaled back at the end
         float ps = 0.f;
-        const float off = fmaf(mn, mul, -15.f);
+        const float off = fmaf(mn, mul, -kPfPExp);
         pf_f16x4 phi[4], plo[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -307,7 +313,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
         if (opos < a.t_q) {
             const int64_t off =
                 ((bb * a.n_q_heads + (int64_t)kvh * a.rep + hh) * a.t_q + opos) * kPfD;
-            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^15
+            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^11
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt)
                 store_from_f32(a.out, a.out_dtype, off + 16 * nt + l16, acc[nt][i] * inv);
@@ -455,13 +461,13 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
 #pragma unroll
         for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sv[i]);
         mx = fmaxf(mx, lane_read(mx, lane ^ 32));
-        const float mn = fmaxf(m, mx);  // raw units (mul > 0)
+        const float mn = (mx - m) * mul > kPfLag ? fmaxf(m, mx) : m;  // raw units (mul > 0)
         const float corr = fast_exp2((m - mn) * mul);
         m = mn;
-        // x = p * 2^15 = exp2(s * mul - (mn * mul - 15)), split into fp16 hi
+        // x = p * 2^11 = exp2(s * mul - (mn * mul - 11)), split into fp16 hi
         // and lo; l sums x and is scaled back at the end
         float ps = 0.f;
-        const float off = fmaf(mn, mul, -15.f);
+        const float off = fmaf(mn, mul, -kPfPExp);
         pf_f16x4 phi[4], plo[4];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -529,7 +535,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
         if (opos < a.t_q) {
             const int64_t off =
                 ((bb * a.n_q_heads + (int64_t)kvh * a.rep + hh) * a.t_q + opos) * kPfD;
-            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^15
+            const float inv = Li > 0.f ? 1.f / Li : 0.f;  // acc and l both carry 2^11
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt)
                 store_from_f32(a.out, a.out_dtype, off + 32 * nt + l32, acc[nt][i] * inv);

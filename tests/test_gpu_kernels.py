@@ -577,14 +577,14 @@ def test_decode_grouped_il_peaked_and_flat_softmax(bits):
         assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
 
 
-def ramp_case(seed, t_kv, cap, rise):
+def ramp_case(seed, t_kv, cap, rise, t_q=1):
     """A cache whose scores climb steadily along the tokens by `rise` log2
     units in all (block 0's centroid c is c * step on every dim, the query
     constant, every other block's centroids small): tiles keep rising above
     the running maxima by less and by more than the kernels' lag before a
     wave-wide reduction."""
     d, scale = 128, 0.0883883
-    cents, perm, idx, vals, q = decode_case(seed, 1, 4, 1, d, t_kv, cap=cap)
+    cents, perm, idx, vals, q = decode_case(seed, 1, 4, 1, d, t_kv, t_q, cap=cap)
     cents[1:] *= 0.01
     qv = 0.5
     step = rise / (255 * scale * 1.4426950408889634 * qv * 8)
@@ -1160,6 +1160,25 @@ def test_bounded_wait_failure_reaches_python():
     _hip.check_decode_waits()
     ref = O.sdpa(q, idx, vals, cents, perm, 1.0 / np.sqrt(d))
     assert rel_err(out.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("rise,qdt", [(40.0, "f16"), (600.0, "f16"), (40.0, "f32")])
+def test_prefill_rising_scores(rise, qdt):
+    """Causal prefill over scores that keep rising along the prompt: rows keep
+    their running maxima while a sub-tile stays within a few log2 units of
+    them (probabilities above 1 in the fp16 staging) and rescale past it."""
+    t_kv = 1000
+    cap = ((t_kv + 15) // 16) * 16
+    cents, perm, idx, vals, q, scale = ramp_case(19, t_kv, cap, rise, t_q=t_kv)
+    qt = t(q) if qdt == "f16" else t(q.astype(np.float32))
+    cb = _hip.codebook_f16x2(t(cents))
+    out = _hip.prefill_attn_il8(qt, scale, t(perm), cb, 256, t(idx), to_il8(vals, cap), t_kv, causal=True,
+                                q_offset=0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.sdpa(q, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, scale, mask="causal")
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) <= REL_TOL
 
 
 @pytest.mark.parametrize("b,hq,hkv,t_q,t_kv,causal,qdt,nc", [
