@@ -522,6 +522,11 @@ constexpr size_t decode_lds_bytes() {
                             (size_t)WAVES * kWave * R);
 }
 
+// The vector-ALU decode keeps a row's running maximum while a tile's scores
+// stay at most kValuLag log2 units above it (fp32 probabilities up to
+// 2^kValuLag).
+constexpr float kValuLag = 8.f;
+
 template <int D, int R, class VF>
 __global__ void __launch_bounds__(VfThreads<VF>::value)
     decode_attn_kernel(DecodeCommon c, typename VF::Args va) {
@@ -688,21 +693,38 @@ __global__ void __launch_bounds__(VfThreads<VF>::value)
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) s[r] = (kok && tk <= lim[r]) ? s[r] : -INFINITY;
-        float corr[R], tmax[R];
-        if constexpr (R == 4) {
-            wave_max4_dpp(s, tmax);  // DPP lane moves, the four rows interleaved
+        // a tile whose scores stay at most kValuLag log2 units above the
+        // running maxima keeps them (fp32 probabilities up to 2^kValuLag):
+        // no wave-wide reduction and no rescale of the accumulators
+        uint64_t above = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) above |= __builtin_amdgcn_ballot_w64(s[r] > m[r] + kValuLag);
+        const bool moved = above != 0;
+        float corr[R];
+        if (moved) {
+            float tmax[R];
+            if constexpr (R == 4) {
+                wave_max4_dpp(s, tmax);  // DPP lane moves, the four rows interleaved
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r) tmax[r] = wave_max(s[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float mn = fmaxf(m[r], tmax[r]);
+                corr[r] = fast_exp2(m[r] - mn);
+                const float p = fast_exp2(s[r] - mn);
+                l[r] = fmaf(l[r], corr[r], p);
+                m[r] = mn;
+                s[r] = p;
+            }
         } else {
 #pragma unroll
-            for (int r = 0; r < R; ++r) tmax[r] = wave_max(s[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float mn = fmaxf(m[r], tmax[r]);
-            corr[r] = fast_exp2(m[r] - mn);
-            const float p = fast_exp2(s[r] - mn);
-            l[r] = fmaf(l[r], corr[r], p);
-            m[r] = mn;
-            s[r] = p;
+            for (int r = 0; r < R; ++r) {
+                corr[r] = 1.f;
+                s[r] = fast_exp2(s[r] - m[r]);
+                l[r] += s[r];
+            }
         }
         if constexpr (R == 4) {
             *reinterpret_cast<float4 *>(pw + lane * 4) = make_float4(s[0], s[1], s[2], s[3]);
@@ -711,10 +733,12 @@ __global__ void __launch_bounds__(VfThreads<VF>::value)
             for (int r = 0; r < R; ++r) pw[lane * R + r] = s[r];
         }
         wave_lds_sync();
+        if (moved) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) acc[r][k] *= corr[r];
+                for (int k = 0; k < DPL; ++k) acc[r][k] *= corr[r];
+        }
 
 #pragma unroll
         for (int ch = 0; ch < ITERS; ch += CHUNK) {
