@@ -47,6 +47,8 @@ namespace {
 typedef _Float16 pf_f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pf_f16x2 __attribute__((ext_vector_type(2)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPfWaves = 8;
@@ -470,12 +472,18 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
         const float off = fmaf(mn, mul, -kPfPExp);
         pf_f16x4 phi[4], plo[4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float x = fast_exp2(fmaf(sv[i], mul, -off));
-            ps += x;
-            const _Float16 hx = (_Float16)x;
-            phi[i >> 2][i & 3] = hx;
-            plo[i >> 2][i & 3] = (_Float16)__builtin_fmaf((float)hx, -1.f, x);
+        for (int i = 0; i < 16; i += 2) {  // pairs: one packed conversion each for hi and lo
+            const float x0 = fast_exp2(fmaf(sv[i], mul, -off));
+            const float x1 = fast_exp2(fmaf(sv[i + 1], mul, -off));
+            ps += x0;
+            ps += x1;
+            const pf_f16x2 h = __builtin_convertvector((pf_f32x2){x0, x1}, pf_f16x2);
+            const pf_f16x2 lo = __builtin_convertvector(
+                (pf_f32x2){__builtin_fmaf((float)h[0], -1.f, x0), __builtin_fmaf((float)h[1], -1.f, x1)}, pf_f16x2);
+            phi[i >> 2][i & 3] = h[0];
+            phi[i >> 2][(i & 3) + 1] = h[1];
+            plo[i >> 2][i & 3] = lo[0];
+            plo[i >> 2][(i & 3) + 1] = lo[1];
         }
         lsum = fmaf(lsum, corr, ps);
         // accumulator rows 8*(i/4) + 4*hb + i%4 take the correction of their
@@ -516,9 +524,12 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
             }
         }
     };
+    // sub-tiles in pairs with no exit between them (one register assignment
+    // of the accumulators for the whole loop): an odd count ends with one
+    // sub-tile past the last key, whose loads clamp to the last key's rows
+    // and whose scores are all masked (weights and values zero)
     for (int sub = 0; sub < n_sub; sub += 2) {
         do_sub(ir_a, ir_b, sub);
-        if (sub + 1 >= n_sub) break;
         do_sub(ir_b, ir_a, sub + 1);
     }
 
