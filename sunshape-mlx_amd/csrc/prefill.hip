@@ -15,11 +15,13 @@
 // B = the query rows (round_to(q_dtype, q * scale), codec-permuted, as
 // registers for the whole kernel; fp16 hi and lo parts unless the query is
 // fp16).  The accumulator of S^T gives lane l the scores of row l%16 for
-// tokens 4*(l/16) .. +3, which is exactly the A operand layout of
+// tokens 4*(l/16) .. +3 of each 16-token sub-tile; two sub-tiles' entries
+// side by side are an A operand of
 //   O[row][dim] += sum_t P[row][t] * V[t][dim]
-// on v_mfma_f32_16x16x16f16, so the probabilities never leave registers
-// (hi and lo fp16 parts of p * 2^11, two products); B = 4 consecutive tokens
-// of one dim, 8 bytes of the interleaved value layout.
+// on v_mfma_f32_16x16x32_f16 (the token order inside a product's K slots
+// is free as long as A and B agree), so the probabilities never leave
+// registers (hi and lo fp16 parts of p * 2^11, two products); B = the same 8
+// tokens of one dim, two 8-byte loads of the interleaved value layout.
 //
 // A workgroup of kPfWaves waves takes 16 * kPfWaves query rows of one KV
 // group: (rows / rep) consecutive positions of its rep query heads, the
@@ -30,9 +32,11 @@
 // fp16 and bf16 queries take prefill32_il8_kernel instead: waves of 32 rows on
 // v_mfma_f32_32x32x16_f16 (S^T of 32 tokens x 32 rows: lane l holds token
 // l%32's block 2ks + l/32 as A, row l%32's dims 16ks + 8(l/32) .. as B) and
-// v_mfma_f32_32x32x8f16 for P.V (the S^T accumulator entries 4kk .. 4kk+3
-// of lane l are row l%32's tokens 8kk + 4(l/32) .., the A operand of step
-// kk), so every key gather and value load serves 32 rows.  fp32 queries
+// v_mfma_f32_32x32x16_f16 for P.V too (the S^T accumulator entries 8k2 ..
+// 8k2+7 of lane l are row l%32's tokens 16k2 + 4(l/32) + 0..3 and
+// 16k2 + 8 + 4(l/32) + 0..3, the A operand of step k2; the legacy
+// 32x32x8 and 16x16x16 shapes issue at half the fp16 rate on gfx950), so
+// every key gather and value load serves 32 rows.  fp32 queries
 // need a second (lo) query operand, which leaves no registers for 32 rows.
 //
 // The grid is (batch x KV heads, position groups) with the position groups
@@ -286,13 +290,20 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
                 }
             }
         }
+        // P.V on v_mfma_f32_16x16x32_f16: step j2 takes the 32 tokens of
+        // sub-tiles 2j2 and 2j2+1, the lane's eight being its four of each;
+        // its B slice holds the same eight tokens' values (slot for slot)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j2 = 0; j2 < 2; ++j2) {
+            const pf_f16x8 ah = __builtin_shufflevector(phi[2 * j2], phi[2 * j2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            const pf_f16x8 al = __builtin_shufflevector(plo[2 * j2], plo[2 * j2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, vop[j][nt]);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi[j], b, acc[nt], 0, 0, 0);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo[j], b, acc[nt], 0, 0, 0);
+                const pf_f16x8 b = __builtin_bit_cast(
+                    pf_f16x8, make_uint4(vop[2 * j2][nt].x, vop[2 * j2][nt].y, vop[2 * j2 + 1][nt].x,
+                                         vop[2 * j2 + 1][nt].y));
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc[nt], 0, 0, 0);
             }
         }
     };
@@ -511,16 +522,23 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
                 }
             }
         }
-        // O[row][dim] += P[row][t] V[t][dim]: step kk takes tokens 8kk ..
-        // 8kk+7, the lane's four of them being accumulator entries 4kk ..
-        // 4kk+3 of the scores
+        // O[row][dim] += P[row][t] V[t][dim] on v_mfma_f32_32x32x16_f16: step
+        // k2 takes tokens 16k2 .. 16k2+15, the lane's eight of them being
+        // accumulator entries 8k2 .. 8k2+7 of the scores (tokens 16k2 + 4hb
+        // + 0..3 and 16k2 + 8 + 4hb + 0..3); its B slice holds the values of
+        // the same eight tokens (the two 8-token blocks' 4-token loads), so A
+        // and B agree slot for slot
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int k2 = 0; k2 < 2; ++k2) {
+            const pf_f16x8 ah = __builtin_shufflevector(phi[2 * k2], phi[2 * k2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            const pf_f16x8 al = __builtin_shufflevector(plo[2 * k2], plo[2 * k2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
-                const pf_f16x4 b = __builtin_bit_cast(pf_f16x4, vop[kk][nt]);
-                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(phi[kk], b, acc[nt], 0, 0, 0);
-                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(plo[kk], b, acc[nt], 0, 0, 0);
+                const pf_f16x8 b = __builtin_bit_cast(
+                    pf_f16x8, make_uint4(vop[2 * k2][nt].x, vop[2 * k2][nt].y, vop[2 * k2 + 1][nt].x,
+                                         vop[2 * k2 + 1][nt].y));
+                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, acc[nt], 0, 0, 0);
             }
         }
     };
