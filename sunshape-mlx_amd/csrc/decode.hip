@@ -880,6 +880,7 @@ constexpr int kMfmaRows = 4;
 // padding, so the 16 rows a matrix-core operand read touches start in
 // different LDS banks.
 constexpr int kPStride = 64 + 8;
+static_assert((kPStride * 2) % 16 == 0, "16-byte P row reads");
 constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr int kSpinLimit = 1 << 20;  // bounded waits: ~0.03 s of s_sleep 1
 
@@ -1085,20 +1086,17 @@ struct VIl8 {
             }
         }
         const bool a_live = l16 < 8;  // A rows 0-3: hi parts, 4-7: lo parts, 8-15: zero
+        // v_mfma_f32_16x16x32_f16 (full fp16 rate): K slots 8g .. 8g+7 of
+        // lane l are tokens 32 s2 + 8g .. +7 in A (its P row) and in B (its
+        // 8 tokens of one dim)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
+            f16x8 a = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+            if (a_live) a = *reinterpret_cast<const f16x8 *>(pw + l16 * kPStride + 32 * s2 + 8 * g);
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                f16x4 a = f16x4{0, 0, 0, 0};
-                if (a_live)
-                    a = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 32 * s2 + 8 * g + 4 * jj);
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    const uint4 u = tv.v[s2][n];
-                    uint2 h = jj == 0 ? make_uint2(u.x, u.y) : make_uint2(u.z, u.w);
-                    const f16x4 bop = *reinterpret_cast<const f16x4 *>(&h);
-                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[n], 0, 0, 0);
-                }
+            for (int n = 0; n < NT; ++n) {
+                const f16x8 bop = __builtin_bit_cast(f16x8, tv.v[s2][n]);
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop, acc[n], 0, 0, 0);
             }
         }
         wave_lds_sync();
