@@ -2,7 +2,7 @@
 //
 // The decode kernel's MFMA path reads values as [cap/8][head_dim][8] per
 // (batch, KV head): the 8 consecutive tokens of one dim are 16 contiguous
-// bytes, the K-major operand of v_mfma_f32_16x16x16f16.  Appending T new
+// bytes, the K-major operand of v_mfma_f32_16x16x32_f16.  Appending T new
 // tokens at position `offset` scatters each token's head_dim values with a
 // 16-byte stride; the index cache keeps the token-major [cap][n_blocks]
 // layout of the reference (cache.py:102-150).

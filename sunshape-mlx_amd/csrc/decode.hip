@@ -844,10 +844,10 @@ __global__ void __launch_bounds__(VfThreads<VF>::value)
 // MFMA decode for fp16 values stored 8-token interleaved: value element
 // (token t, dim d) of a head lives at [t / 8][d][t % 8], so 16 bytes give a
 // lane 8 consecutive tokens of one dim -- the K-major operand layout of
-// v_mfma_f32_16x16x16f16.  P.V runs on the matrix cores as
+// v_mfma_f32_16x16x32_f16.  P.V runs on the matrix cores as
 // O[row][dim] = sum_t P[row][t] V[t][dim] with M = query rows, K = tokens,
 // N = dims.  P enters as an fp16 hi/lo pair (rows 0-3 hi, rows 4-7 lo) of
-// p * 2^15, which keeps ~22 mantissa bits and stays in fp16's normal range;
+// p * 2^11, which keeps ~22 mantissa bits and stays in fp16's normal range;
 // accumulation is fp32.  Four query rows (one GQA group) per workgroup.
 //
 // The workgroup is warp-specialised: NC compute waves and one loader wave.
@@ -998,8 +998,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // format): acc[n] of lane l holds MFMA rows 4*(l/16) .. +3 of dims 16n + l%16.
 
 // fp16 values, 8-token interleaved: element (t, d) at [t/8][d][t%8].  P is
-// staged as fp16 hi/lo rows of p * 2^15 (A rows 0-3 hi, 4-7 lo, 8-15 zero)
-// and P.V is v_mfma_f32_16x16x16f16.
+// staged as fp16 hi/lo rows of p * 2^11 (A rows 0-3 hi, 4-7 lo, 8-15 zero)
+// and P.V is v_mfma_f32_16x16x32_f16.
 template <int D, int SUB = 1>
 struct VIl8 {
     struct Args {
@@ -2614,7 +2614,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 // decode_attn_kernel (fp32 query x centroid LUT in LDS, built here on the
 // vector ALUs, plus exact dot products over fp16 heavy-block key dims when
 // NH8 > 0, NH8*8 of them).  P.V runs as O[row][dim] = sum_t P[row][t] V[t][dim]
-// on v_mfma_f32_16x16x16f16 with P entering as fp16 hi/lo rows of p * 2^15
+// on v_mfma_f32_16x16x32_f16 with P entering as fp16 hi/lo rows of p * 2^11
 // (rows 0-3 hi, 4-7 lo, as in VIl8) and V gathered from the value codebook
 // staged in LDS as fp16 by transposing reads (ds_read_b64_tr_b16): in each
 // 16-lane group lane j reads the 4-dim codebook row of (token j/4, value
@@ -2900,16 +2900,27 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
             for (int nt = 0; nt < 8; ++nt) acc[nt] *= cv4;
         }
         const bool a_live = l16 < 8;
+        // v_mfma_f32_16x16x32_f16 (full fp16 rate) over two 16-token k-steps:
+        // K slots 8g .. 8g+3 of lane l are tokens 16(2k2) + 4g + 0..3, slots
+        // 8g+4 .. 8g+7 tokens 16(2k2+1) + 4g + 0..3, in A (its P row) and in
+        // B (the two transposing reads)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            f16x4 a = f16x4{0, 0, 0, 0};
-            if (a_live) a = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 16 * ks + 4 * g);
+        for (int k2 = 0; k2 < 2; ++k2) {
+            f16x4 a0 = f16x4{0, 0, 0, 0}, a1 = a0;
+            if (a_live) {
+                a0 = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 32 * k2 + 4 * g);
+                a1 = *reinterpret_cast<const f16x4 *>(pw + l16 * kPStride + 32 * k2 + 16 + 4 * g);
+            }
+            const f16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < 8; ++nt) {
-                const uint2 w2 = cur.vi[ks];
-                const uint32_t byte = __builtin_amdgcn_ubfe(nt < 4 ? w2.x : w2.y, (nt & 3) * 8, 8);
-                const f16x4 bop = ds_read_tr16(smem, vbase + byte * 8 + nt * 2048);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[nt], 0, 0, 0);
+                const uint2 w0 = cur.vi[2 * k2], w1 = cur.vi[2 * k2 + 1];
+                const uint32_t b0 = __builtin_amdgcn_ubfe(nt < 4 ? w0.x : w0.y, (nt & 3) * 8, 8);
+                const uint32_t b1 = __builtin_amdgcn_ubfe(nt < 4 ? w1.x : w1.y, (nt & 3) * 8, 8);
+                const f16x4 bop0 = ds_read_tr16(smem, vbase + b0 * 8 + nt * 2048);
+                const f16x4 bop1 = ds_read_tr16(smem, vbase + b1 * 8 + nt * 2048);
+                const f16x8 bop = __builtin_shufflevector(bop0, bop1, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop, acc[nt], 0, 0, 0);
             }
         }
         wave_lds_sync();
