@@ -1102,7 +1102,7 @@ struct VIl8 {
         wave_lds_sync();
     }
     // lanes 0-15 hold rows 0-3 (hi parts) of dims 16n + l16, lanes 16-31 the
-    // lo parts: wa[hl][r][d] = acc / 2^15
+    // lo parts: wa[hl][r][d] = acc / kPScale
     __device__ static void to_lds(const f32x4 (&acc)[NT], const State &, float *wa, int lane) {
         const int g = lane >> 4, l16 = lane & 15;
         if (g < 2) {
@@ -1473,9 +1473,11 @@ struct VGil {
 // w = p * norm: VGil's products (A = w as bf16 hi/lo rows, B = 128 + code)
 // give sum w c, one more product per (k-step, N-tile) with B = 128 + 2 bit1
 // (the bit left in place, the same per-token powers of two as the codes)
-// gives sum w bit1, and sum w accumulates in fp32 on the lanes.  Rows 8-15 of A are
-// unused (one group per row).  The accumulation is in the rotated basis; the
-// rotation is applied per output row after the merge (transformed_decode).
+// gives sum w bit1 into rows 8-15 of the same accumulator (A rows 0-7
+// repeated as rows 8-15, each half zero in the other product), and sum w
+// accumulates in fp32 on the lanes.  The accumulation is in the rotated
+// basis; the rotation is applied per output row after the merge
+// (transformed_decode).
 template <int D>
 struct VTq {
     struct Args {
