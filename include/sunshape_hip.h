@@ -233,7 +233,7 @@ int ss_codebook_f16x2(const float *centroids, int n_blocks, int n_centroids, voi
  * values_il8[((b*n_kv_heads + h)*cap/8 + t/8)*head_dim*8 + d*8 + t%8]
  * (cap % 8 == 0), with the codebook prepared by ss_codebook_f16x2.  Both the
  * query x centroid LUT (split-fp16 v_mfma_f32_16x16x32_f16: exact fp16
- * products, fp32 accumulation) and P.V (v_mfma_f32_16x16x16f16 with the
+ * products, fp32 accumulation) and P.V (v_mfma_f32_16x16x32_f16 with the
  * probabilities split into fp16 hi/lo parts) run on the matrix cores; four
  * query rows per KV group are processed together.  Scaled queries must lie in
  * the fp16 range (always true for fp16 queries).  Same reference semantics as
