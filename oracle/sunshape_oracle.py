@@ -40,6 +40,11 @@ lloyd_max_gaussian             the reference's literal table: symmetric,
 turboquant_encode/decode       rotation orthogonality; round-trip MSE bound
 sdpa                           per-head loop == fused_attention per (b,h,r);
                                GQA head mapping h*rep + r (attention.py:220)
+sdpa_two_pass masks            boolean: == softmax over the kept keys only
+                               (reconstructed keys), fully masked row == mean
+                               of the values; additive: == softmax(q k^T + m)
+                               over reconstructed keys; planted mistakes
+                               (zero rows, a subtracted mask) fail the pins
 kmeans                         hand-worked Lloyd steps from the reference's
                                initial rows (seeds 0, 1), empty cluster kept,
                                zero-padded short data, non-increasing
@@ -204,6 +209,20 @@ def _softmax_rows(scores, valid, values) -> np.ndarray:
         p = np.exp(s - s.max())
         out[r] = (p @ values[v]) / p.sum()
     return out
+
+
+def _softmax_rows_min_fill(scores, valid, values) -> np.ndarray:
+    """The two-pass path's masking and softmax (attention.py:329-346): masked
+    scores are replaced by float32's lowest finite value
+    (``mx.where(mask, scores, finfo(float32).min)``, attention.py:336, 341),
+    then an ordinary max-subtracted softmax runs over the whole row.  A row
+    that keeps at least one key gives its masked keys weight exactly 0; a row
+    with every key masked gets uniform weights, i.e. the mean of the values
+    (the fused kernel's empty row gives 0 instead, ``_softmax_rows``)."""
+    lo = float(np.finfo(np.float32).min)
+    s = np.where(valid, np.asarray(scores, np.float64), lo)
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    return (p @ values) / p.sum(axis=1, keepdims=True)
 
 
 def causal_valid(n_rows: int, t_kv: int, causal: bool, q_offset: int) -> np.ndarray:
@@ -525,7 +544,10 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
     """The two-pass fallback of attention.py:307-350 used when a hybrid cache
     has buffered fp16 tokens: compressed scores ``q_t . k_hat`` concatenated
     with ``q_scaled . k_buf^T`` (original basis), causal or additive/boolean
-    mask, softmax, ``@ values`` (compressed values dequantized, then buffer).
+    mask (causal and boolean masks fill masked scores with float32's lowest
+    value, attention.py:329-341, so a row with every key masked averages the
+    values; an additive mask is added as is), softmax, ``@ values``
+    (compressed values dequantized, then buffer).
     ``key_indices`` (B, Hkv, Tc, NB), ``buffer_keys`` (B, Hkv, Tb, D) or None,
     ``values_all`` (B, Hkv, Tc + Tb, D).
 
@@ -583,7 +605,7 @@ def sdpa_two_pass(queries, scale, perm, centroids, key_indices, buffer_keys,
                 else:
                     valid = np.ones(s.shape, bool)
                 v = np.asarray(values_all[b, h], np.float32).astype(np.float64)
-                out[b, h * rep + r] = _softmax_rows(s, valid, v)
+                out[b, h * rep + r] = _softmax_rows_min_fill(s, valid, v)
     return out
 
 

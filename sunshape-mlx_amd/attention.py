@@ -79,7 +79,8 @@ def _prepared_decode(cache, ops: dict, codec: SunShapeBlockCodec, q: torch.Tenso
     return plan
 
 
-def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int):
+def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int,
+           out_dtype: torch.dtype):
     """One fused launch over the whole cache, or None when no fused kernel
     applies to this cache / shape (the reference's None-fallback,
     kernels.py:259-291)."""
@@ -114,7 +115,7 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         try:
             out = _hip.prefill_attn_il8(q, kscale, perm, codec.kernel_codebook(), codec.n_centroids,
                                         ops["idx"], ops["values"], t_kv, causal=causal,
-                                        q_offset=q_offset, out_dtype=queries.dtype)
+                                        q_offset=q_offset, out_dtype=out_dtype)
         except _hip.SunShapeUnsupported:
             return None
         codec.last_score_backend = "hip_prefill_mfma"
@@ -124,12 +125,12 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     if not buffered and kind in ("il8", "grouped_il") and hv["k_heavy"] is None:
         try:
             plan = _prepared_decode(cache, ops, codec, q, kscale, perm)
-            out = plan(q, t_kv, causal, q_offset, out_dtype=queries.dtype)
+            out = plan(q, t_kv, causal, q_offset, out_dtype=out_dtype)
         except _hip.SunShapeUnsupported:
             return None
         codec.last_score_backend = "hip_fused_mfma" if kind == "il8" else "hip_fused_mfma_dequant"
         return out
-    kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=queries.dtype)
+    kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=out_dtype)
     try:
         if kind == "il8":
             out = _hip.decode_attn_il8(q, kscale, perm, codec.scoring_centroids(), ops["idx"],
@@ -208,7 +209,8 @@ def _compressed_scores(codec: SunShapeBlockCodec, q_t: torch.Tensor,
     return scores.reshape(b_, hkv, rep, tq, tc)
 
 
-def _two_pass(cache, queries: torch.Tensor, scale: float, mask) -> torch.Tensor:
+def _two_pass(cache, queries: torch.Tensor, scale: float, mask,
+              out_dtype: torch.dtype) -> torch.Tensor:
     """Scores (compressed, then buffered keys in the original basis), mask,
     float32 softmax, ``@ values`` (attention.py:307-350)."""
     b_, hq, tq, d = queries.shape
@@ -250,25 +252,29 @@ def _two_pass(cache, queries: torch.Tensor, scale: float, mask) -> torch.Tensor:
     weights = torch.softmax(scores.float(), dim=-1)
     values = cache.values.float()  # (B, Hkv, T_kv, D)
     out = torch.matmul(weights.reshape(b_, hkv, rep * tq, t_kv), values)
-    return out.reshape(b_, hq, tq, d).to(queries.dtype)
+    return out.reshape(b_, hq, tq, d).to(out_dtype)
 
 
 def sunshape_sdpa(queries: torch.Tensor, cache: SunShapeKVCache | HybridSunShapeKVCache,
-                  scale: float, mask: torch.Tensor | str | None = None) -> torch.Tensor:
+                  scale: float, mask: torch.Tensor | str | None = None, *,
+                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """Attention of ``queries`` (B, n_q_heads, T_q, D) against a SunShape cache
     (reference attention.py:166-353).  Query head ``h*rep + r`` reads KV head
     h; ``mask`` is None, ``"causal"`` (query i sees keys ``t <= T_kv - T_q + i``)
     or an additive / boolean array broadcastable to (B, n_q_heads, T_q, T_kv).
-    Returns (B, n_q_heads, T_q, D) in the query dtype."""
+    Returns (B, n_q_heads, T_q, D) in the query dtype, as the reference does
+    (attention.py:292, 304), or in ``out_dtype`` when given (an extension:
+    float32 keeps the kernels' fp32 accumulation in the result)."""
     b_, hq, tq, d = queries.shape
     hkv = cache.n_kv_heads
     if hq % hkv != 0:
         raise ValueError(f"n_q_heads ({hq}) must be a multiple of the cache's n_kv_heads ({hkv})")
     if d != cache.head_dim:
         raise ValueError(f"query head_dim {d} != cache head_dim {cache.head_dim}")
+    out_dtype = out_dtype or queries.dtype
     t_kv = cache.offset
     if t_kv == 0:
-        return torch.zeros_like(queries)
+        return torch.zeros_like(queries, dtype=out_dtype)
     _hip.require_gpu(queries)
     is_hybrid = isinstance(cache, HybridSunShapeKVCache)
     use_causal = isinstance(mask, str) and mask == "causal"
@@ -277,7 +283,8 @@ def sunshape_sdpa(queries: torch.Tensor, cache: SunShapeKVCache | HybridSunShape
     # takes it (_fused returns None otherwise)
     can_fuse = (mask is None or use_causal) and compressed > 0
     if can_fuse:
-        out = _fused(cache, queries, scale, use_causal, t_kv - tq if use_causal else 0)
+        out = _fused(cache, queries, scale, use_causal, t_kv - tq if use_causal else 0,
+                     out_dtype)
         if out is not None:
             return out
-    return _two_pass(cache, queries, scale, mask)
+    return _two_pass(cache, queries, scale, mask, out_dtype)

@@ -22,7 +22,8 @@ import torch
 
 from . import _hip
 from .codec import PERM_MODES, SunShapeBlockCodec
-from .value_codecs import GroupedValueCodec, TurboQuantValueCodec, build_value_codec
+from .value_codecs import (GroupedValueCodec, TurboQuantValueCodec, _packed_dim,
+                           build_value_codec)
 
 _STEP = 256
 _DEFAULT_BUFFER_SIZE = 128
@@ -30,21 +31,6 @@ _DEFAULT_BUFFER_SIZE = 128
 
 def _round_capacity(n: int) -> int:
     return ((n + _STEP - 1) // _STEP) * _STEP
-
-
-def _packed_dim(head_dim: int, bits: int) -> int:
-    """uint32 words per row (reference cache.py:39-56)."""
-    if bits == 2:
-        if head_dim % 16 != 0:
-            raise ValueError(f"head_dim must be divisible by 16 for 2-bit packing, got {head_dim}")
-        return head_dim // 16
-    if bits == 3:
-        return (head_dim + 9) // 10
-    if bits == 4:
-        if head_dim % 8 != 0:
-            raise ValueError(f"head_dim must be divisible by 8 for 4-bit packing, got {head_dim}")
-        return head_dim // 8
-    raise ValueError(f"Unsupported bits: {bits} (must be 2, 3, or 4)")
 
 
 def _grow(buf: torch.Tensor | None, shape, dtype, device, keep: int) -> torch.Tensor:

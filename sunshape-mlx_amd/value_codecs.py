@@ -56,18 +56,20 @@ def lloyd_max_gaussian(bits: int) -> tuple[tuple[float, ...], tuple[float, ...]]
     return levels, bounds
 
 
+_CODES_PER_WORD = {2: 16, 3: 10, 4: 8}
+
+
 def _packed_dim(head_dim: int, bits: int) -> int:
-    if bits == 2:
-        if head_dim % 16 != 0:
-            raise ValueError(f"head_dim must be divisible by 16 for 2-bit packing, got {head_dim}")
-        return head_dim // 16
-    if bits == 3:
-        return (head_dim + 9) // 10
-    if bits == 4:
-        if head_dim % 8 != 0:
-            raise ValueError(f"head_dim must be divisible by 8 for 4-bit packing, got {head_dim}")
-        return head_dim // 8
-    raise ValueError(f"Unsupported bits: {bits}")
+    """uint32 words per packed row: 16 two-bit, 10 three-bit (the last word
+    zero-padded) or 8 four-bit codes per word; 2- and 4-bit rows must fill
+    their words (the format rule of reference cache.py:39-56)."""
+    per_word = _CODES_PER_WORD.get(bits)
+    if per_word is None:
+        raise ValueError(f"Unsupported bits: {bits} (must be 2, 3, or 4)")
+    if bits != 3 and head_dim % per_word:
+        raise ValueError(f"head_dim must be divisible by {per_word} for {bits}-bit packing, "
+                         f"got {head_dim}")
+    return -(-head_dim // per_word)
 
 
 @dataclass

@@ -3,8 +3,12 @@ codecs, SDPA router) against the CPU oracle.
 
 Bars: key indices bit-exact except oracle-flagged near-ties; stored values
 bit-exact; attention outputs max |gpu - oracle| <= 1e-3 * max |oracle| (fp32
-accumulate, float64 oracle), with fp16 outputs compared after rounding the
-oracle to fp16 at a 2e-3 bar.
+accumulate, float64 oracle; the maximum is over every compared element, not
+per element).  The drop-in API returns the query dtype, fp16 here, so those
+outputs are compared with the oracle rounded to fp16 (``rel_err16``): the two
+roundings differ by at most one fp16 step, below 2^-10 = 9.8e-4 of the
+largest element, so the 1e-3 bar still holds the accumulation to a few
+1e-5.
 """
 
 import sys
@@ -25,6 +29,13 @@ REL_TOL = 1e-3
 def rel_err(got, ref):
     ref = np.asarray(ref, np.float64)
     return float(np.abs(np.asarray(got, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def rel_err16(got, ref):
+    """max |got - fp16(ref)| / max |ref| for an fp16 output ``got``."""
+    ref = np.asarray(ref, np.float64)
+    r16 = ref.astype(np.float16).astype(np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - r16).max() / max(np.abs(ref).max(), 1e-30))
 
 
 def make_codec(seed, d=128, nc=256, mode="profileperm_baseline"):
@@ -87,7 +98,7 @@ def test_fp16_cache_store_and_fused_decode(d, prefill, steps):
     ref = O.sdpa(q.cpu().numpy(), got, v.cpu().numpy(), cents, codec.permutation.cpu().numpy(),
                  1.0 / np.sqrt(d))
     assert out.dtype == torch.float16
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
 def test_fp16_cache_causal_prefill_and_capacity_growth():
@@ -104,7 +115,7 @@ def test_fp16_cache_causal_prefill_and_capacity_growth():
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.1,
                  mask="causal")
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
 def test_prompt_prefill_takes_the_prefill_kernel():
@@ -124,13 +135,13 @@ def test_prompt_prefill_takes_the_prefill_kernel():
     perm = codec.permutation.cpu().numpy()
     ref = O.sdpa(q[:, :, :300].cpu().numpy(), cache.key_indices.cpu().numpy(),
                  v[:, :, :300].cpu().numpy(), cents, perm, 0.088, mask="causal")
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     cache.update_and_fetch(k[:, :, 300:], v[:, :, 300:])
     out2 = S.sunshape_sdpa(q[:, :, 300:].contiguous(), cache, 0.088, mask="causal")
     assert codec.last_score_backend == "hip_prefill_mfma"
     ref2 = O.sdpa(q[:, :, 300:].cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                   cents, perm, 0.088, mask="causal")
-    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
+    assert rel_err16(out2.float().cpu().numpy(), ref2) <= REL_TOL
 
 
 def test_prepared_decode_follows_the_cache_and_matches_direct_launch():
@@ -163,7 +174,7 @@ def test_prepared_decode_follows_the_cache_and_matches_direct_launch():
     assert torch.equal(out2, direct(q, 700))
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), scale)
-    assert rel_err(out2.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out2.float().cpu().numpy(), ref) <= REL_TOL
     qb = q.to(torch.bfloat16)
     out3 = S.sunshape_sdpa(qb, cache, scale)
     assert out3.dtype == torch.bfloat16 and torch.equal(out3, direct(qb, 700))
@@ -213,13 +224,17 @@ def test_mask_array_takes_two_pass_and_matches():
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.09, codec.permutation.cpu().numpy(),
                           codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(), None,
                           v.cpu().numpy(), mask=m_add)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     m_bool = rng.random((tq, t_kv)) > 0.3
+    m_bool[1] = False  # every key masked: the reference averages the values
     out = S.sunshape_sdpa(q, cache, 0.09, mask=torch.from_numpy(m_bool))
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.09, codec.permutation.cpu().numpy(),
                           codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(), None,
                           v.cpu().numpy(), mask=m_bool)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
+    mean = v[0, 0].double().mean(dim=0).cpu().numpy()
+    assert np.abs(ref[0, :, 1] - mean).max() < 1e-12
+    assert rel_err16(out[0, :, 1].float().cpu().numpy(), np.broadcast_to(mean, (hq, d))) <= REL_TOL
 
 
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.float16])
@@ -242,7 +257,7 @@ def test_hybrid_grouped_fused_and_buffered(scale_dtype):
                                zr.reshape(-1, zr.shape[-1]), d, 2, 64).reshape(b, hkv, 300, d)
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # default buffer: 128 recent tokens stay fp16, the two-pass path runs
     cache2 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped", value_bits=2,
                                value_scale_dtype=scale_dtype)
@@ -254,7 +269,7 @@ def test_hybrid_grouped_fused_and_buffered(scale_dtype):
     ref2 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                            codec.centroids.cpu().numpy(), cache2.key_indices.cpu().numpy(),
                            cache2.buffer_keys.float().cpu().numpy(), vals_all)
-    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
+    assert rel_err16(out2.float().cpu().numpy(), ref2) <= REL_TOL
     # trim removes buffered tokens first (reference cache.py:954-963)
     cache2.trim(130)
     assert cache2.buffer_offset == 0 and cache2.compressed_offset == 170
@@ -292,7 +307,7 @@ def test_hybrid_grouped_interleaved_appends_and_trim(bits, group):
     vals = O.dequantize_values(packed_ref, sc_ref, zr_ref, d, bits, group).reshape(b, hkv, pos, d)
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # the dequantised values the two-pass path reads agree with the oracle's
     assert rel_err(cache.values.float().cpu().numpy(), vals) <= 1e-3
 
@@ -327,7 +342,7 @@ def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
                           codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
                           cache.buffer_keys.float().cpu().numpy(), vals, mask=mask)
     assert vals.shape[2] == tc + cache.buffer_offset
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
 @pytest.mark.parametrize("buf,t_total,tq,causal", [
@@ -361,7 +376,7 @@ def test_hybrid_fp16_buffer_joins_fused_decode(buf, t_total, tq, causal):
         ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                               codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
                               cache.buffer_keys.float().cpu().numpy(), vals, mask=mask)
-        assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+        assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
     check()
     cache.trim(buf + 5)  # all of the buffer and 5 compressed tokens
@@ -391,7 +406,7 @@ def test_hybrid_buffer_with_rotated_codec_fused(backend):
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, None, codec.centroids.cpu().numpy(),
                           cache.key_indices.cpu().numpy(), cache.buffer_keys.float().cpu().numpy(),
                           vals, rotation=codec.rotation.cpu().numpy())
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
 def test_hybrid_fp16_and_sunshape_value_backends():
@@ -407,7 +422,7 @@ def test_hybrid_fp16_and_sunshape_value_backends():
     assert codec.last_score_backend == "hip_fused_mfma"
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), v.cpu().numpy(),
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # SunShape-coded values: the fused decode over gathered value centroids
     vcodec = make_codec(12)
     cache3 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="sunshape", value_bits=8,
@@ -419,7 +434,7 @@ def test_hybrid_fp16_and_sunshape_value_backends():
     ref3 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                            codec.centroids.cpu().numpy(), cache3.key_indices.cpu().numpy(), None,
                            vals)
-    assert rel_err(out3.float().cpu().numpy(), ref3) <= 2e-3
+    assert rel_err16(out3.float().cpu().numpy(), ref3) <= REL_TOL
 
 
 def test_rotated_codec_fused_decode():
@@ -440,7 +455,7 @@ def test_rotated_codec_fused_decode():
     for h in range(hkv):
         for rr in range(hq // hkv):
             ref[0, h * (hq // hkv) + rr] = O.fused_attention(qt[0, h, rr], cents, idx[0, h], vv[0, h])
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
@@ -514,7 +529,7 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
     ref = O.sdpa(q.cpu().numpy(), cache.key_indices.cpu().numpy(), vals,
                  codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088,
                  mask=mask)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # the default buffer: recent fp16 tokens join the same fused softmax
     cache2 = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend="turboquant",
                                value_bits=bits)
@@ -530,7 +545,7 @@ def test_hybrid_turboquant_fused_decode(bits, t_q):
     ref2 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                            codec.centroids.cpu().numpy(), cache2.key_indices.cpu().numpy(),
                            cache2.buffer_keys.float().cpu().numpy(), vals_all, mask=mask)
-    assert rel_err(out2.float().cpu().numpy(), ref2) <= 2e-3
+    assert rel_err16(out2.float().cpu().numpy(), ref2) <= REL_TOL
     # the value codec's own dequantisation gives the same cache contents
     rows = torch.from_numpy(_tq_rows(cache, n).view(np.int32)).to(DEV)
     rec = tc.dequantize(rows.reshape(-1, tc.packed_dim),
@@ -568,7 +583,7 @@ def test_hybrid_sunshape_values_fused_decode(vbd, buffer_size):
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
                           codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
                           cache.buffer_keys.float().cpu().numpy() if nbuf else None, vals_all)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # the cache's own (two-pass) value read-back agrees with the oracle
     assert rel_err(cache.values[:, :, :nc].float().cpu().numpy(), vals) <= 1e-3
 
@@ -667,7 +682,7 @@ def test_mixed_precision_heavy_blocks_in_fp16(value_backend, value_bits, buffer_
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, cache.key_indices.cpu().numpy(),
                           cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset else None,
                           vals, heavy_keys=kh, heavy_dims=hd)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # the reference's semantics (heavy blocks contribute nothing) differ
     ref0 = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, cache.key_indices.cpu().numpy(),
                            cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset else None,
@@ -723,7 +738,7 @@ def test_fitted_mixed_codec_heavy_fp16_with_buffer(value_backend):
     kb = cache.buffer_keys.float().cpu().numpy()
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, perm, cents, idx, kb, vals,
                           heavy_keys=kh, heavy_dims=hd)
-    assert rel_err(out.float().cpu().numpy(), ref) <= 2e-3
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
     # the same attention written out over rebuilt keys (codec basis: light
     # blocks from their centroids, heavy dims from the fp16 keys)
     qs = O.scale_query(q.cpu().numpy(), 0.088).astype(np.float64)
@@ -738,7 +753,7 @@ def test_fitted_mixed_codec_heavy_fp16_with_buffer(value_backend):
                 w = np.exp(sc - sc.max())
                 o = (w / w.sum()) @ vals[bi, h].astype(np.float64)
                 got = out[bi, h * (hq // hkv) + r, 0].float().cpu().numpy()
-                assert np.abs(got - o).max() <= 2e-3 * np.abs(o).max()
+                assert np.abs(got - o.astype(np.float16)).max() <= REL_TOL * np.abs(o).max()
 
 
 def test_router_sends_sunshape_caches_to_sunshape_sdpa():

@@ -263,3 +263,110 @@ def test_cpu_baseline_forms_agree_with_oracle():
               lambda *a: O.decode_cpu_parallel(*a, n_threads=4, chunk=128)):
         out = f(qt, cents, idx, vals)
         assert np.abs(out - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def _mask_case(seed=34):
+    """A hybrid-shaped two-pass case: compressed keys plus buffered fp16
+    keys, GQA 2:1, three query rows, and the same keys written out in the
+    original basis."""
+    rng = np.random.default_rng(seed)
+    b_, hq, hkv, d, tc, tb, tq = 1, 4, 2, 32, 20, 5, 3
+    perm = rng.permutation(d).astype(np.int32)
+    cents = rng.standard_normal((4, 16, 8)).astype(np.float32)
+    idx = rng.integers(0, 16, (b_, hkv, tc, 4)).astype(np.uint8)
+    kb = rng.standard_normal((b_, hkv, tb, d)).astype(np.float16)
+    vals = rng.standard_normal((b_, hkv, tc + tb, d)).astype(np.float16)
+    q = rng.standard_normal((b_, hq, tq, d)).astype(np.float16)
+    inv = O.invert_permutation(perm)
+    keys = np.stack([np.concatenate([O.dequantize_blockvq(idx[0, h], cents, inv).astype(np.float64),
+                                     kb[0, h].astype(np.float64)]) for h in range(hkv)])
+    return q, perm, cents, idx, kb, vals, keys, rng
+
+
+def _check_bool_mask_pins(two_pass):
+    """The reference's boolean-mask semantics (attention.py:339-346, masked
+    scores filled with float32's lowest value before the softmax), written
+    out over the reconstructed keys: a row that keeps some keys is the
+    softmax over exactly those keys; a row that keeps none is the mean of
+    all the values.  Returns the largest deviation."""
+    q, perm, cents, idx, kb, vals, keys, rng = _mask_case()
+    t_kv = keys.shape[1]
+    m = rng.random((3, t_kv)) > 0.4
+    m[1, :] = False               # every key masked
+    m[2, :] = False
+    m[2, [0, 7, 21]] = True       # compressed and buffered keys kept
+    out = two_pass(q, 0.3, perm, cents, idx, kb, vals, mask=m)
+    qs = O.scale_query(q, 0.3)[0].astype(np.float64)
+    worst = 0.0
+    for hh in range(4):
+        h = hh // 2
+        v = vals[0, h].astype(np.float64)
+        for r in range(3):
+            keep = m[r]
+            if keep.any():
+                ref = explicit_attention(qs[hh, r][None], keys[h][keep], v[keep])[0]
+            else:
+                ref = v.mean(axis=0)
+            worst = max(worst, float(np.abs(out[0, hh, r] - ref).max()))
+    return worst
+
+
+def test_sdpa_two_pass_bool_mask_semantics():
+    assert _check_bool_mask_pins(O.sdpa_two_pass) < 1e-12
+
+
+def test_sdpa_two_pass_bool_mask_pins_catch_planted_mistakes(monkeypatch):
+    """Mistakes planted in the oracle fail the pins: the fused kernel's
+    zero output for an empty row (the reference's two-pass path averages the
+    values), and a mask read the wrong way round."""
+    fill = O._softmax_rows_min_fill
+    monkeypatch.setattr(O, "_softmax_rows_min_fill", O._softmax_rows)
+    assert _check_bool_mask_pins(O.sdpa_two_pass) > 1e-2
+    monkeypatch.setattr(O, "_softmax_rows_min_fill", lambda s, valid, v: fill(s, ~valid, v))
+    assert _check_bool_mask_pins(O.sdpa_two_pass) > 1e-2
+
+
+def test_sdpa_two_pass_additive_mask_semantics():
+    """Float masks are added to the scores (attention.py:342-343): the
+    output is softmax(q k^T + m) V over the reconstructed keys, so a large
+    negative entry all but removes a key.  Planted in the oracle: a mask
+    subtracted instead fails the pin."""
+    q, perm, cents, idx, kb, vals, keys, rng = _mask_case(35)
+    t_kv = keys.shape[1]
+    m = (rng.standard_normal((3, t_kv)) * 2.0).astype(np.float32)
+    m[0, 3] = -1e4
+    qs = O.scale_query(q, 0.3)[0].astype(np.float64)
+
+    def worst_of(out):
+        w = 0.0
+        for hh in range(4):
+            h = hh // 2
+            s = qs[hh] @ keys[h].T + m
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            ref = (p / p.sum(axis=1, keepdims=True)) @ vals[0, h].astype(np.float64)
+            w = max(w, float(np.abs(out[0, hh] - ref).max()))
+        return w
+
+    assert worst_of(O.sdpa_two_pass(q, 0.3, perm, cents, idx, kb, vals, mask=m)) < 1e-12
+    assert worst_of(O.sdpa_two_pass(q, 0.3, perm, cents, idx, kb, vals, mask=-m)) > 1e-2
+
+
+def test_sdpa_two_pass_causal_rows_before_the_cache_average_values():
+    """A causal mask with more query rows than keys (offset T_kv - T_q < 0)
+    masks every key of the first rows; the two-pass path, like the
+    reference's (attention.py:329-336), averages the values there, while
+    the fused kernel's literal loop gives 0 (kernels.py:218-222)."""
+    q, perm, cents, idx, kb, vals, keys, rng = _mask_case(36)
+    idx2 = idx[:, :, :2]
+    vals2 = vals[:, :, :2]
+    # two keys, three query rows (offset -1): row 0 sees no key, row 1 key 0,
+    # row 2 both
+    out = O.sdpa_two_pass(q, 0.3, perm, cents, idx2, None, vals2, mask="causal")
+    qs = O.scale_query(q, 0.3)[0].astype(np.float64)
+    for hh in range(4):
+        h = hh // 2
+        v = vals2[0, h].astype(np.float64)
+        assert np.abs(out[0, hh, 0] - v.mean(axis=0)).max() < 1e-12
+        assert np.abs(out[0, hh, 1] - v[0]).max() < 1e-12
+        ref = explicit_attention(qs[hh, 2][None], keys[h][:2], v)[0]
+        assert np.abs(out[0, hh, 2] - ref).max() < 1e-12
