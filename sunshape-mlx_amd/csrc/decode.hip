@@ -282,10 +282,11 @@ struct VTurbo {
 // SunShape block-VQ values (value backend "sunshape", reference
 // cache.py:614-623, 785-800): per token NBV = D / BD uint8 centroid indices
 // of BD-dim blocks in the value codec's basis.  The value codebook is staged
-// in LDS beside the key LUT as fp16 (64 KB at D = 128, so one workgroup
-// covers the whole head dim and computes each score once; rounding a
-// centroid to fp16 changes it by at most 2^-12 of itself, and the products
-// accumulate in fp32).  A lane takes 16 consecutive codec dims (16 / BD
+// in LDS beside the key LUT in fp32 (64 KB per workgroup: at D = 128 two
+// workgroups each take half the head dim and both compute the scores); an
+// fp16 copy would move each centroid by up to 2^-12 of itself, which over a
+// long cache of near-cancelling values reached 1e-3 of the output.  A lane
+// takes 16 consecutive codec dims (16 / BD
 // blocks, one 4- or 2-byte index group) and reads their centroids from LDS;
 // accumulation runs in the codec basis and the transform back to the
 // original basis (inverse permutation or rotation, as a D x D matrix) is
@@ -294,12 +295,14 @@ template <int D, int BD>
 struct VSunV {
     // three waves per SIMD: the LDS gathers of one hide behind the others' FMAs
     static constexpr int kThreads = 768;
-    static constexpr int kSlabs = D * 256 * 2 > 65536 ? 2 : 1;
+    // the codebook stays fp32 (the values the reference reads, exactly); a
+    // head dim whose codebook passes 64 KB is split over two workgroups
+    static constexpr int kSlabs = D * 256 * 4 > 65536 ? 2 : 1;
     static constexpr int DS = D / kSlabs;            // dims of one workgroup
-    // the slab's fp16 centroids (256 per block), then the heavy dims' query values
+    // the slab's fp32 centroids (256 per block), then the heavy dims' query values
     static constexpr int kMaxHeavyDims = 64;
-    static constexpr int kHeavyOffset = DS * 256 / 2;  // floats
-    static constexpr int kLdsBytes = DS * 256 * 2 + 4 * kMaxHeavyDims * 4;
+    static constexpr int kHeavyOffset = DS * 256;  // floats
+    static constexpr int kLdsBytes = DS * 256 * 4 + 4 * kMaxHeavyDims * 4;
     static constexpr bool kHeavyKeys = true;
     static constexpr int DPL = 16;
     static constexpr int BPL = DPL / BD;  // blocks per lane
@@ -333,11 +336,11 @@ struct VSunV {
         }
         return r;
     }
-    // the slab's centroids -> lds [NBVS][256][BD] fp16, rounded to nearest
-    // (entries past n_centroids zero)
+    // the slab's centroids -> lds [NBVS][256][BD] fp32 (entries past
+    // n_centroids zero)
     __device__ static __forceinline__ void stage(float *lds, const Args &a, int slab, int tid,
                                                  int nt) {
-        uint2 *l2 = reinterpret_cast<uint2 *>(lds);  // 4 halves per entry
+        float4 *l4 = reinterpret_cast<float4 *>(lds);
         for (int i = tid; i < NBVS * 256 * BD / 4; i += nt) {
             const int f = i * 4, bl = f / (256 * BD), within = f - bl * (256 * BD);
             const int cc = within / BD;
@@ -345,28 +348,24 @@ struct VSunV {
             if (cc < a.n_centroids)
                 v = *reinterpret_cast<const float4 *>(
                     a.cb + ((int64_t)(slab * NBVS + bl) * a.n_centroids + cc) * BD + within % BD);
-            const __half2 lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
-            l2[i] = make_uint2(*reinterpret_cast<const uint32_t *>(&lo),
-                               *reinterpret_cast<const uint32_t *>(&hi));
+            l4[i] = v;
         }
     }
     // lt: lane group within the slab
     __device__ static __forceinline__ void decode_lds(const float *lds, const Args &, const Raw &r,
                                                       int lt, float *x) {
-        const uint2 *l2 = reinterpret_cast<const uint2 *>(lds);
+        const float4 *l4 = reinterpret_cast<const float4 *>(lds);
 #pragma unroll
         for (int i = 0; i < BPL; ++i) {
             const int bl = lt * BPL + i;
             const int cc = (int)((r.w >> (8 * i)) & 0xffu);
 #pragma unroll
             for (int h = 0; h < BD / 4; ++h) {
-                const uint2 v = l2[((bl * 256 + cc) * BD) / 4 + h];
-                const float2 a = __half22float2(*reinterpret_cast<const __half2 *>(&v.x));
-                const float2 b = __half22float2(*reinterpret_cast<const __half2 *>(&v.y));
-                x[i * BD + 4 * h + 0] = a.x;
-                x[i * BD + 4 * h + 1] = a.y;
-                x[i * BD + 4 * h + 2] = b.x;
-                x[i * BD + 4 * h + 3] = b.y;
+                const float4 v = l4[((bl * 256 + cc) * BD) / 4 + h];
+                x[i * BD + 4 * h + 0] = v.x;
+                x[i * BD + 4 * h + 1] = v.y;
+                x[i * BD + 4 * h + 2] = v.z;
+                x[i * BD + 4 * h + 3] = v.w;
             }
         }
     }
@@ -865,6 +864,7 @@ __global__ void __launch_bounds__(VfThreads<VF>::value)
 // per-device word c.wait_fail and the kernel ends normally with an invalid
 // output, which ss_decode_wait_failures reports to the host.
 // ---------------------------------------------------------------------------
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -2618,11 +2618,22 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 // NH8 > 0, NH8*8 of them).  P.V runs as O[row][dim] = sum_t P[row][t] V[t][dim]
 // on v_mfma_f32_16x16x32_f16 with P entering as fp16 hi/lo rows of p * 2^11
 // (rows 0-3 hi, 4-7 lo, as in VIl8) and V gathered from the value codebook
-// staged in LDS as fp16 by transposing reads (ds_read_b64_tr_b16): in each
-// 16-lane group lane j reads the 4-dim codebook row of (token j/4, value
-// block 8*(j%4) + nt), and the read hands lane i the column i of that 4 x 16
-// block, i.e. dim i%4 of block 8*(i/4) + nt for the 4 tokens -- the B operand,
-// with no value converted, packed or multiplied on the vector ALUs.  MFMA
+// staged in LDS as 16-bit fixed point by transposing reads
+// (ds_read_b64_tr_b16): in each 16-lane group lane j reads the 4-dim codebook
+// row of (token j/4, value block 8*(j%4) + nt), and the read hands lane i the
+// column i of that 4 x 16 block, i.e. dim i%4 of block 8*(i/4) + nt for the 4
+// tokens -- the B operand's codes.  Each codebook dim (value block, dim j)
+// holds u = rint((C - zero)/scale) with zero = min, scale = (max - min)/65535
+// over its centroids, so |C - (zero + scale*u)| <= scale/2 (an fp16 copy of C
+// leaves up to 2^-11 |C|, which at 131072 tokens of N(0,1) values came to
+// 1.1e-3 of the output).  The code's bytes u = 256 h + l enter as two fp16
+// operands of the same product, each byte placed under a constant exponent
+// byte by one v_perm_b32: 0x78hh = 32768 + 32 h and 0x58ll = 128 + l/8, both
+// exact, so the accumulator sums p (32896 + u/8); one rounding per product
+// of 32 tokens keeps that offset's cost to a few 1e-5 of the output (fp32
+// emulation at 131072 tokens: 1.6e-4 of the output in all, 1.3e-4 of it the
+// codes' own step).  The combine turns the sums into p-weighted values with
+// each dim's scale and zero.  MFMA
 // column n of n-tile nt therefore holds codec dim ((8*(n/4) + nt)*4 + n%4),
 // and a lane's eight n-tiles read index bytes 8*(n%4) .. +7 of one token, an
 // 8-byte load per 16 tokens.  The heavy-dim dot products run on
@@ -2641,10 +2652,14 @@ constexpr int kSvNB = 16;    // key blocks of head_dim 128
 constexpr int kSvNBV = 32;   // value blocks of block_dim 4
 constexpr int kSvD = 128;
 constexpr int kSvWaves = 8;
-constexpr int kSvVcbBytes = kSvNBV * 256 * 8;  // fp16 [value block][256][4], at LDS offset 0
+constexpr int kSvVcbBytes = kSvNBV * 256 * 8;  // u16 codes [value block][256][4], at LDS offset 0
 constexpr int kSvLutBytes = kSvNB * 256 * 16;  // float4 (4 rows) [key block][256]
 constexpr int kSvPstBytes = kSvWaves * 8 * kPStride * 2;
-constexpr int kSvLdsBytes = kSvVcbBytes + kSvLutBytes + kSvPstBytes;
+constexpr int kSvSzBytes = kSvD * 2 * 4;      // per codebook dim: zero, scale (f32)
+constexpr int kSvLdsBytes = kSvVcbBytes + kSvLutBytes + kSvPstBytes + kSvSzBytes;
+// the code bytes' fp16 operand patterns: 0x78hh = 32768 + 32 h, 0x58ll = 128 + l / 8
+constexpr uint32_t kSvHiPat = 0x78787878u, kSvLoPat = 0x58585858u;
+constexpr float kSvCodeOff = -32896.f;  // the operands sum to u/8 - kSvCodeOff
 static_assert(kSvLdsBytes <= kLdsMax, "SunShape-value MFMA LDS budget");
 static_assert(kSvVcbBytes <= 65536, "value codebook addressed with 16-bit LDS offsets");
 
@@ -2674,6 +2689,7 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
     uint2 *vcb = reinterpret_cast<uint2 *>(smem);                            // [32][256]
     float4 *lut4 = reinterpret_cast<float4 *>(smem + kSvVcbBytes);           // [16][256]
     _Float16 *pst = reinterpret_cast<_Float16 *>(smem + kSvVcbBytes + kSvLutBytes);
+    float *vsz = reinterpret_cast<float *>(smem + kSvVcbBytes + kSvLutBytes + kSvPstBytes);  // [D][2]
     const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)(smem + kSvVcbBytes);
 
     const int tid = threadIdx.x;
@@ -2708,15 +2724,45 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
     uint32_t heavy_blocks = 0;
     for (int j = 0; j < NH8 * 8; ++j)
         heavy_blocks |= 1u << (min(max(va.heavy_dims[j], 0), D - 1) / kBlockDim);
-    // value codebook -> fp16 (rounded to nearest), entries past n_centroids zero
+    // value codebook -> 16-bit codes.  Each codebook dim d = 4 vb + j takes
+    // zero = min, scale = (max - min) / 65535 over its n_centroids entries:
+    // four adjacent threads scan a quarter of them each and combine
+    {
+        static_assert(TH == 4 * D, "four threads per codebook dim");
+        const int d = tid >> 2, part = tid & 3, vb = d >> 2, j = d & 3;
+        const float *col_p = va.cb + (int64_t)vb * va.n_centroids * 4 + j;
+        float lo = INFINITY, hi = -INFINITY;
+        for (int cc = part; cc < va.n_centroids; cc += 4) {
+            const float x = col_p[(int64_t)cc * 4];
+            lo = fminf(lo, x);
+            hi = fmaxf(hi, x);
+        }
+        lo = fminf(lo, __shfl_xor(lo, 1));
+        hi = fmaxf(hi, __shfl_xor(hi, 1));
+        lo = fminf(lo, __shfl_xor(lo, 2));
+        hi = fmaxf(hi, __shfl_xor(hi, 2));
+        if (part == 0) {
+            const bool ok = va.n_centroids > 0 && hi > lo;
+            vsz[2 * d] = va.n_centroids > 0 ? lo : 0.f;
+            vsz[2 * d + 1] = ok ? (hi - lo) * (1.f / 65535.f) : 0.f;
+        }
+    }
+    __syncthreads();
     for (int i = tid; i < kSvNBV * 256; i += TH) {
         const int vb = i >> 8, cc = i & 255;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (cc < va.n_centroids)
-            v = *reinterpret_cast<const float4 *>(va.cb + ((int64_t)vb * va.n_centroids + cc) * 4);
-        const __half2 lo = __floats2half2_rn(v.x, v.y), hi = __floats2half2_rn(v.z, v.w);
-        vcb[i] = make_uint2(*reinterpret_cast<const uint32_t *>(&lo),
-                            *reinterpret_cast<const uint32_t *>(&hi));
+        uint32_t uc[4] = {0u, 0u, 0u, 0u};
+        if (cc < va.n_centroids) {
+            const float4 v =
+                *reinterpret_cast<const float4 *>(va.cb + ((int64_t)vb * va.n_centroids + cc) * 4);
+            const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float z = vsz[2 * (4 * vb + j)], sc = vsz[2 * (4 * vb + j) + 1];
+                const float q = sc > 0.f ? rintf(__fdiv_rn(x[j] - z, sc)) : 0.f;
+                uc[j] = (uint32_t)fminf(fmaxf(q, 0.f), 65535.f);
+            }
+        }
+        vcb[i] = make_uint2(uc[0] | (uc[1] << 16), uc[2] | (uc[3] << 16));
     }
     __syncthreads();
     // 2. LUT[b][cc] = the 4 rows' q'[b-block] . C[b][cc] in log2 units
@@ -2919,10 +2965,22 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
                 const uint2 w0 = cur.vi[2 * k2], w1 = cur.vi[2 * k2 + 1];
                 const uint32_t b0 = __builtin_amdgcn_ubfe(nt < 4 ? w0.x : w0.y, (nt & 3) * 8, 8);
                 const uint32_t b1 = __builtin_amdgcn_ubfe(nt < 4 ? w1.x : w1.y, (nt & 3) * 8, 8);
-                const f16x4 bop0 = ds_read_tr16(smem, vbase + b0 * 8 + nt * 2048);
-                const f16x4 bop1 = ds_read_tr16(smem, vbase + b1 * 8 + nt * 2048);
-                const f16x8 bop = __builtin_shufflevector(bop0, bop1, 0, 1, 2, 3, 4, 5, 6, 7);
-                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop, acc[nt], 0, 0, 0);
+                const uint2 c0 = __builtin_bit_cast(uint2, ds_read_tr16(smem, vbase + b0 * 8 + nt * 2048));
+                const uint2 c1 = __builtin_bit_cast(uint2, ds_read_tr16(smem, vbase + b1 * 8 + nt * 2048));
+                // codes u (two per word) -> operands 32768 + 32 h and 128 + l / 8:
+                // v_perm_b32 places each code byte under its exponent byte
+                // (selector bytes 0-3 pick the code word's bytes, 4 the pattern's)
+                const uint32_t cw[4] = {c0.x, c0.y, c1.x, c1.y};
+                uint32_t bh[4], bl[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bh[q] = __builtin_amdgcn_perm(kSvHiPat, cw[q], 0x04030401u);
+                    bl[q] = __builtin_amdgcn_perm(kSvLoPat, cw[q], 0x04020400u);
+                }
+                const f16x8 bop_h = __builtin_bit_cast(f16x8, make_uint4(bh[0], bh[1], bh[2], bh[3]));
+                const f16x8 bop_l = __builtin_bit_cast(f16x8, make_uint4(bl[0], bl[1], bl[2], bl[3]));
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop_h, acc[nt], 0, 0, 0);
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop_l, acc[nt], 0, 0, 0);
             }
         }
         wave_lds_sync();
@@ -2980,6 +3038,11 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
             const float f = fast_exp2(wm[w * R + r] - M);
             L = fmaf(wl[w * R + r], f, L);
             A = fmaf(wa[((w * 2) * R + r) * D + d] + wa[((w * 2 + 1) * R + r) * D + d], f, A);
+        }
+        // sum p (u/8 - kSvCodeOff) -> sum p C = (zero + 8 kSvCodeOff scale) L + 8 scale A
+        {
+            const float z = vsz[2 * d], sc = vsz[2 * d + 1];
+            A = fmaf(8.f * sc, A, (z + (8.f * kSvCodeOff) * sc) * L);
         }
         if (S == 1) {
             if (row_ok(r)) store_from_f32(c.out, c.out_dtype, row_off(r) + d, L > 0.f ? A / L : 0.f);
