@@ -156,6 +156,17 @@ size_t ss_decode_workspace_bytes(int64_t batch, int n_q_heads, int n_kv_heads,
 int ss_decode_wait_failures(void *stream, int clear, unsigned int *flags);
 
 /*
+ * Address (in *flag) of a word of pinned, host-mapped memory into which a
+ * wait that gives up also stores its bits (the last give-up's bits), in any
+ * process-wide launch; ss_decode_wait_failures folds it into its report and
+ * clears it with the device word.  The host can poll it with a plain load
+ * and no synchronisation: it is nonzero once a failed launch has finished
+ * running, so a caller that checks it before each launch reports a failure
+ * on a later call without waiting on any stream.  No reference counterpart.
+ */
+int ss_decode_wait_flag_host(unsigned int **flag);
+
+/*
  * Test hook: the number of sleeps after which those waits give up, for
  * launches issued after this call (process-wide); a negative value restores
  * the default (2^20, about 0.03 s).  A small limit makes waits give up while

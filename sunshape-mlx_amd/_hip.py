@@ -72,6 +72,7 @@ _SIGNATURES = {
                                _i64, _c_void_p]),
     "ss_decode_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
     "ss_decode_wait_failures": (_int, [_c_void_p, _int, ctypes.POINTER(ctypes.c_uint)]),
+    "ss_decode_wait_flag_host": (_int, [ctypes.POINTER(ctypes.POINTER(ctypes.c_uint))]),
     "ss_debug_set_spin_limit": (_int, [_int]),
     "ss_stream_read": (_int, [_c_void_p, _i64, _int, _c_void_p, _c_void_p]),
     "ss_decode_default_splits": (_int, [_i64, _int, _int, _i64, _int, _i64]),
@@ -266,8 +267,31 @@ def stream_handle(device: torch.device | None = None) -> int:
 
 # Check the wait-failure word after every matrix-core decode launch (one
 # stream synchronisation per call); off by default, on with
-# SUNSHAPE_CHECK_WAITS=1 or set_wait_checks(True).
+# SUNSHAPE_CHECK_WAITS=1 or set_wait_checks(True).  Without it, every decode
+# launch first polls the library's pinned host copy of the flags (a plain
+# load, no synchronisation), so a give-up is raised by the first decode call
+# made after the failing launch has run.
 _check_waits = os.environ.get("SUNSHAPE_CHECK_WAITS", "0") == "1"
+_wait_flag = None  # ctypes.c_uint over the pinned host word
+
+
+def decode_wait_flag() -> int:
+    """The pinned host copy of the wait-failure flags, read without
+    synchronising (nonzero once a failed launch has finished running)."""
+    global _wait_flag
+    if _wait_flag is None:
+        p = ctypes.POINTER(ctypes.c_uint)()
+        check(load_library().ss_decode_wait_flag_host(ctypes.byref(p)))
+        _wait_flag = p.contents
+    return int(_wait_flag.value)
+
+
+def _poll_waits(device) -> None:
+    """Before a matrix-core decode launch: raise ``SunShapeWaitError`` if an
+    earlier launch's bounded wait gave up (the host word is set; the
+    synchronising check then reports and clears both words)."""
+    if (_wait_flag.value if _wait_flag is not None else decode_wait_flag()):
+        check_decode_waits(device)
 
 
 def set_wait_checks(enabled: bool) -> bool:
@@ -359,6 +383,7 @@ class PreparedDecode:
             out = torch.empty(self.shape, dtype=out_dtype or self.dtype, device=q.device)
         elif tuple(out.shape) != self.shape or not out.is_contiguous() or out.device != q.device:
             raise ValueError(f"out must be contiguous {self.shape} on cuda:{self.dev}")
+        _poll_waits(self.dev)
         st = stream_handle(self.dev)
         ws = _ws_cache.get((self.dev, st))
         if ws is None:
@@ -672,6 +697,7 @@ def decode_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
             ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device))
     stat = _attn_stat("sunshape_fused_attention_mfma", causal)
     heavy = _heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32)
+    _poll_waits(q.device)
     if (buf_keys is None or buf_len == 0) and k_heavy is None:
         _launched(stat, load_library().ss_decode_attn_il8(*common, *tail))
     else:
@@ -742,6 +768,7 @@ def decode_attn_il8_noalloc(q: torch.Tensor, scale: float, perm: torch.Tensor | 
     lib = load_library()
     if codebook.numel() != lib.ss_codebook_f16x2_bytes(*centroids.shape[:2]):
         raise ValueError("codebook does not match the centroids' shape")
+    _poll_waits(q.device)
     _launched(_attn_stat("sunshape_fused_attention_mfma", causal), lib.ss_decode_attn_il8_noalloc(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
         nb, centroids.shape[1], ptr(idx), ptr(values_il8), SS_F16, cap, int(t_kv),
@@ -1012,13 +1039,17 @@ def decode_attn_turboquant_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
     ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv), buf_len,
                                                         int(n_splits))
     ws = decode_workspace(q.device, ws_bytes)
+    _poll_waits(q.device)
     _launched(_attn_stat("sunshape_fused_attention_turboquant", causal),
               lib.ss_decode_attn_turboquant_il(
         ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
         nb, nc, ptr(idx), ptr(codes_il), ptr(norms), ctypes.cast(lv_host, ctypes.c_void_p).value,
         ptr(rotation), cap, int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh,
-        bst, buf_len, *_heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32), int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+        bst, buf_len, *_heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32), int(bool(causal)),
+        int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
         ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
+    if _check_waits:
+        check_decode_waits(q.device)
     return out
 
 
@@ -1066,6 +1097,7 @@ def decode_attn_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | N
     tail = (ptr(out), dtype_code(out.dtype), ptr(ws), ws_bytes if ws is not None else 0,
             int(n_splits), stream_handle(q.device))
     heavy = _heavy_args(k_heavy, heavy_dims, b_, hkv, cap, 32)
+    _poll_waits(q.device)
     if (buf_keys is None or buf_len == 0) and k_heavy is None:
         _launched(_attn_stat("sunshape_fused_attention_dequant_mfma", causal), load_library().ss_decode_attn_grouped_il(
             *common, int(bool(causal)), int(q_offset), *tail))

@@ -55,6 +55,9 @@ struct DecodeCommon {
     // up, and the sticky per-device word a give-up sets (kWait* bits)
     int spin_limit;
     unsigned int *wait_fail;
+    // the same bits stored (not accumulated) into a word of pinned host
+    // memory, which the host reads after the fact without synchronising
+    unsigned int *wait_host;
     // fp16 heavy-block key dims of a mixed-precision codec (matrix-core
     // kernels of hybrid caches): [rows][nhd] halves of codec-basis dims
     // heavy_dims[0..nhd); nhd 0: none (every block scores from the LUT)
@@ -1756,8 +1759,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // A bounded wait gave up: record which kind in the sticky word (one
     // vector atomic per wave; the host reads and clears it).
     auto wait_gave_up = [&](unsigned kind) {
-        if (lane == 0)
+        if (lane == 0) {
             __hip_atomic_fetch_or(c.wait_fail, kind, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(c.wait_host, kind, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     };
     // Barrier among the NC compute waves only (the loader never joins it):
     // each wave adds 1 to an LDS counter once its LDS writes are done and
@@ -2072,6 +2077,23 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             }
         }
         compute_barrier(2);
+        // Non-fp16 queries enter the split-fp16 products scaled per row by the
+        // power of two 2^-s_r that brings row r's largest element into
+        // [2^14, 2^15), so their fp16 hi parts never overflow whatever the
+        // query's magnitude; the products are multiplied back by 2^s_r.
+        f32x4 qsc = f32x4{1.f, 1.f, 1.f, 1.f};  // 2^s_r of rows 0..3
+        float qinv = 1.f;                         // 2^-s of query row lane & 3
+        if (c.q_dtype != SS_F16) {
+            static_assert(R == 4, "four query rows per column");
+            float mx = 0.f;
+            for (int j = l16; j < D; j += 16) mx = fmaxf(mx, fabsf(qp[g * D + j]));
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            const int sh = row_exp_shift(mx);  // row g's shift, lanes 16g .. 16g+15
+            qsc = f32x4{exp2i(__shfl(sh, 0)), exp2i(__shfl(sh, 16)), exp2i(__shfl(sh, 32)),
+                        exp2i(__shfl(sh, 48))};
+            qinv = exp2i(-__shfl(sh, 16 * (lane & 3)));
+        }
         {
             // LUT entry (b, cc) holds the 4 rows' dot products, in log2 units,
             // computed on the matrix cores: for 4 blocks bg*4+s and 16
@@ -2093,7 +2115,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             f16x8 a_hi, a_lo;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float x = a_live ? xs[i] : 0.f;
+                const float x = a_live ? xs[i] * qinv : 0.f;
                 const _Float16 h = (_Float16)x;
                 a_hi[i] = h;
                 a_lo[i] = (_Float16)((x - (float)h) * kSplitScale);
@@ -2124,7 +2146,8 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     products(t0);
 #pragma unroll
                     for (int u = 0; u < G; ++u) {
-                        const f32x4 e = hh[u] * mul + cr[u] * mul_lo;
+                        f32x4 e = hh[u] * mul + cr[u] * mul_lo;
+                        if constexpr (decltype(q_split)::value) e *= qsc;
                         const int cc = ((wv * LT + t0 + u) % 16) * 16 + l16;
                         if (cc < c.n_centroids)
                             lut4[(bg * 4 + g) * kLutStride + cc] = make_float4(e.x, e.y, e.z, e.w);
@@ -2152,7 +2175,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 #pragma unroll
                     for (int e2 = 0; e2 < 4; ++e2) {
                         const int hd = min(max(c.heavy_dims[4 * kk + e2], 0), D - 1);
-                        const float x = qp[(lane & 3) * D + hd];
+                        const float x = qp[(lane & 3) * D + hd] * qinv;
                         const _Float16 h = (_Float16)x;
                         hah[kk][e2] = h;
                         hal[kk][e2] = (_Float16)((x - (float)h) * kSplitScale);
@@ -2204,7 +2227,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                                 hl = __builtin_amdgcn_mfma_f32_4x4x4f16(hal[2 * j8 + 1], b1, hl, 0, 0, 0);
                             }
                     }
-                    const f32x4 hv = (hs + hl * (1.f / kSplitScale)) * kLog2e;
+                    const f32x4 hv = (hs + hl * (1.f / kSplitScale)) * (qsc * kLog2e);
 #pragma unroll
                     for (int r = 0; r < R; ++r) sc[r] += hv[r];
                 }
@@ -2788,8 +2811,21 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
         lut4[b * 256 + cc] = make_float4(dt[0], dt[1], dt[2], dt[3]);
     }
     // A operands of the heavy-dim products: query row lane%4, heavy dims
-    // 4kk .. 4kk+3, as fp16 hi and (scaled by 2^11) lo parts
+    // 4kk .. 4kk+3, as fp16 hi and (scaled by 2^11) lo parts; non-fp16 rows
+    // scaled by 2^-s_r so the hi parts stay in range (products times 2^s_r)
     const bool qsplit = c.q_dtype != SS_F16;
+    f32x4 qsc = f32x4{1.f, 1.f, 1.f, 1.f};
+    float qinv = 1.f;
+    if (NH8 > 0 && qsplit) {
+        float mx = 0.f;
+        for (int j = l16; j < D; j += 16) mx = fmaxf(mx, fabsf(qp[g * D + j]));
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const int sh = row_exp_shift(mx);
+        qsc = f32x4{exp2i(__shfl(sh, 0)), exp2i(__shfl(sh, 16)), exp2i(__shfl(sh, 32)),
+                    exp2i(__shfl(sh, 48))};
+        qinv = exp2i(-__shfl(sh, 16 * (lane & 3)));
+    }
     f16x4 ah[NH8 > 0 ? 2 * NH8 : 1], al[NH8 > 0 ? 2 * NH8 : 1];
     if constexpr (NH8 > 0) {
 #pragma unroll
@@ -2797,7 +2833,7 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
 #pragma unroll
             for (int e2 = 0; e2 < 4; ++e2) {
                 const int hd = min(max(va.heavy_dims[4 * kk + e2], 0), D - 1);
-                const float x = qp[(lane & 3) * D + hd];
+                const float x = qp[(lane & 3) * D + hd] * qinv;
                 const _Float16 h = (_Float16)x;
                 ah[kk][e2] = h;
                 al[kk][e2] = (_Float16)((x - (float)h) * kSplitScale);
@@ -2896,7 +2932,7 @@ __global__ void __launch_bounds__(kSvWaves * kWave)
                     hl = __builtin_amdgcn_mfma_f32_4x4x4f16(al[2 * j + 1], b1, hl, 0, 0, 0);
                 }
             }
-            s4 += (hs + hl * (1.f / kSplitScale)) * kLog2e;
+            s4 += (hs + hl * (1.f / kSplitScale)) * (qsc * kLog2e);
         }
         float sc[R] = {s4.x, s4.y, s4.z, s4.w};
         bool moved = true;
@@ -3528,6 +3564,33 @@ __device__ unsigned int g_wait_fail_word;
 // Spin limit of the bounded waits for later launches (ss_debug_set_spin_limit).
 static std::atomic<int> g_spin_limit{kSpinLimit};
 
+// Pinned host word that a give-up also stores its bits into (one per
+// process, mapped into every device): the host polls it after the fact
+// with a plain load, so the check costs no synchronisation.
+static int wait_host_word(unsigned int **host, unsigned int **dev_ptr) {
+    static std::mutex mu;
+    static unsigned int *h = nullptr, *d = nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!h) {
+        void *p = nullptr;
+        hipError_t e = hipHostMalloc(&p, 64, hipHostMallocPortable | hipHostMallocMapped |
+                                                 hipHostMallocCoherent);
+        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(wait flag)");
+        void *dp = nullptr;
+        e = hipHostGetDevicePointer(&dp, p, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(p);
+            return hip_fail(e, "hipHostGetDevicePointer(wait flag)");
+        }
+        h = static_cast<unsigned int *>(p);
+        *h = 0u;
+        d = static_cast<unsigned int *>(dp);
+    }
+    if (host) *host = h;
+    if (dev_ptr) *dev_ptr = d;
+    return SS_OK;
+}
+
 // Device address of g_wait_fail_word on the current device, looked up once
 // per device.
 static int wait_word(unsigned int **out) {
@@ -3576,7 +3639,8 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.tiles_per_split = s.tiles_per_split;
     c.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
     {
-        const int rc = wait_word(&c.wait_fail);
+        int rc = wait_word(&c.wait_fail);
+        if (rc == SS_OK) rc = wait_host_word(nullptr, &c.wait_host);
         if (rc != SS_OK) return rc;
     }
     c.kheavy = nullptr;
@@ -3622,11 +3686,16 @@ extern "C" int ss_decode_wait_failures(void *stream, int clear, unsigned int *fl
     unsigned int v = 0;
     e = hipMemcpy(&v, w, sizeof(v), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy(wait word)");
+    unsigned int *hw = nullptr;
+    rc = wait_host_word(&hw, nullptr);
+    if (rc != SS_OK) return rc;
+    v |= __atomic_load_n(hw, __ATOMIC_ACQUIRE);
     if (flags) *flags = v;
     if (v && clear) {
         const unsigned int zero = 0;
         e = hipMemcpy(w, &zero, sizeof(zero), hipMemcpyHostToDevice);
         if (e != hipSuccess) return hip_fail(e, "hipMemcpy(clear wait word)");
+        __atomic_store_n(hw, 0u, __ATOMIC_RELEASE);
     }
     if (v) {
         set_error("a bounded wait of a fused decode gave up (flags 0x%x: %s%s%s); the output of "
@@ -3635,6 +3704,11 @@ extern "C" int ss_decode_wait_failures(void *stream, int clear, unsigned int *fl
         return SS_ERR_WAIT;
     }
     return SS_OK;
+}
+
+extern "C" int ss_decode_wait_flag_host(unsigned int **flag) {
+    SS_REQUIRE(flag, "null pointer argument");
+    return wait_host_word(flag, nullptr);
 }
 
 extern "C" int ss_debug_set_spin_limit(int limit) {

@@ -139,15 +139,27 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
     const bool rok = pos < a.t_q;
     const int64_t qoff = ((bb * a.n_q_heads + (int64_t)kvh * a.rep + h) * a.t_q + (rok ? pos : 0)) *
                          kPfD;
+    // the row enters scaled by a power of two 2^-s that brings its largest
+    // element into [2^14, 2^15), so the fp16 hi part never overflows (the
+    // scores are multiplied back by 2^s in the exponent below)
+    auto q_at = [&](int j) {
+        const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
+        return rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
+    };
+    float qmax = 0.f;
+    for (int j = 8 * g; j < kPfD; j += 32)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(q_at(j + e)));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 16));  // lanes l16 + 16 g hold the row's quarters
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));
+    const int qshift = row_exp_shift(qmax);
+    const float qinv = exp2i(-qshift);
     pf_f16x8 qh[4], ql[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int j = 32 * ks + 8 * g + e;
-            const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
-            const float x =
-                rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
+            const float x = q_at(32 * ks + 8 * g + e) * qinv;
             const _Float16 hx = (_Float16)x;
             qh[ks][e] = hx;
             ql[ks][e] = (_Float16)((x - (float)hx) * kPfSplit);
@@ -159,9 +171,9 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
     const int64_t wave_pos0 = (int64_t)pg * a.npos + (wv * 16) / a.rep;
     if (wave_pos0 >= a.t_q) return;
 
-    // scores stay in the prepared codebook's units (hi + lo * 2^-11); mul
-    // takes them to log2 units inside the exponent
-    const float mul = *a.cb_mul * kLog2e;
+    // scores stay in the prepared codebook's units (hi + lo * 2^-11) and the
+    // row's query scale; mul takes them to log2 units inside the exponent
+    const float mul = *a.cb_mul * kLog2e * exp2i(qshift);
     // keys this workgroup reads: causal rows stop at q_offset + position
     const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
     const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;
@@ -368,30 +380,35 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
     const bool rok = pos < a.t_q;
     const int64_t qoff = ((bb * a.n_q_heads + (int64_t)kvh * a.rep + h) * a.t_q + (rok ? pos : 0)) *
                          kPfD;
+    // the row enters scaled by a power of two 2^-s that brings its largest
+    // element into [2^14, 2^15): fp16 and bf16 elements are then exact in
+    // fp16 (down to 2^-29 of the largest), whatever the row's magnitude, and
+    // the scores are multiplied back by 2^s in the exponent below
+    auto q_at = [&](int j) {
+        const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
+        return rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
+    };
+    float qmax = 0.f;
+    for (int j = 8 * hb; j < kPfD; j += 16)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(q_at(j + e)));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32));  // lanes l and l ^ 32 hold the row's two halves
+    const int qshift = row_exp_shift(qmax);
+    const float qinv = exp2i(-qshift);
     pf_f16x8 qh[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int j = 16 * ks + 8 * hb + e;
-            const int src = a.perm ? min(max(a.perm[j], 0), kPfD - 1) : j;
-            const float x =
-                rok ? round_to(a.q_dtype, load_as_f32(a.q, a.q_dtype, qoff + src) * a.scale) : 0.f;
-            // fp16 queries are exact in fp16, and so are bf16 ones within
-            // fp16's range (an 8-bit mantissa fits in 11 bits), except
-            // below 2^-14 where fp16 keeps fewer bits (an error under 2^-25
-            // per element); beyond +-65504 they saturate
-            qh[ks][e] = (_Float16)fminf(fmaxf(x, -65504.f), 65504.f);
-        }
+        for (int e = 0; e < 8; ++e) qh[ks][e] = (_Float16)(q_at(16 * ks + 8 * hb + e) * qinv);
     __syncthreads();
     // a wave whose rows all lie past the prompt has nothing to do (no
     // barrier follows)
     const int64_t wave_pos0 = (int64_t)pg * a.npos + (wv * 32) / a.rep;
     if (wave_pos0 >= a.t_q) return;
 
-    // scores stay in the prepared codebook's units (hi + lo * 2^-11); mul
-    // takes them to log2 units inside the exponent
-    const float mul = *a.cb_mul * kLog2e;
+    // scores stay in the prepared codebook's units (hi + lo * 2^-11) and the
+    // row's query scale; mul takes them to log2 units inside the exponent
+    const float mul = *a.cb_mul * kLog2e * exp2i(qshift);
     // keys this workgroup reads: causal rows stop at q_offset + position
     const int64_t pos_last = min((int64_t)(pg + 1) * a.npos, a.t_q) - 1;
     const int64_t t_end = a.causal ? min(a.t_kv, a.q_offset + pos_last + 1) : a.t_kv;

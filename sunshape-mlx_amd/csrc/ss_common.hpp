@@ -57,6 +57,20 @@ __device__ __forceinline__ float round_to(int dt, float x) {
     return x;
 }
 
+// Exponent s of the power of two 2^s that brings m = max |x| of a query row
+// into [2^14, 2^15) as m * 2^-s, so every element of the row scaled by 2^-s
+// lies within fp16's range and an element of at most 11 significant bits
+// (fp16, bf16) stays exact unless it is below 2^-29 of m.  0 for a zero or
+// non-finite m; clamped so both 2^s and 2^-s are normal floats.
+__device__ __forceinline__ int row_exp_shift(float m) {
+    if (!(m > 0.f) || !(m < INFINITY)) return 0;
+    const int e = (int)((__float_as_uint(m) >> 23) & 0xffu) - 127;  // m in [2^e, 2^(e+1))
+    return max(-126, min(126, e - 14));
+}
+
+// 2^s as a float for |s| <= 126.
+__device__ __forceinline__ float exp2i(int s) { return __uint_as_float((uint32_t)(127 + s) << 23); }
+
 __device__ __forceinline__ void store_from_f32(void *p, int dt, int64_t i, float x) {
     if (dt == SS_F32)
         reinterpret_cast<float *>(p)[i] = x;

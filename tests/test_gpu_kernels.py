@@ -1131,23 +1131,34 @@ def test_bounded_wait_failure_reaches_python():
     """A bounded in-kernel wait that gives up is reported, not hidden: with
     the spin limit forced to 0 from the host (every wait gives up after one
     sleep while every wave still ends normally) the matrix-core decode sets
-    the sticky wait-failure word, ss_decode_wait_failures returns SS_ERR_WAIT
-    and the Python layer raises SunShapeWaitError (per call when wait checks
-    are on).  With the default limit restored the same decode is correct and
+    the sticky wait-failure word and its pinned host copy; the next decode
+    call raises SunShapeWaitError before launching (a plain load of the host
+    copy, no synchronisation), ss_decode_wait_failures returns SS_ERR_WAIT,
+    and with wait checks on the failing call itself raises.  With the default limit restored the same decode is correct and
     reports nothing."""
     b, hq, hkv, d, t_kv = 1, 32, 8, 128, 32768
     cents, perm, idx, vals, q = decode_case(71, b, hq, hkv, d, t_kv)
     args = (t(q), 1.0 / np.sqrt(d), t(perm), t(cents), t(idx), to_il8(vals, t_kv), t_kv)
-    assert _hip.decode_wait_failures() == 0
+    assert _hip.decode_wait_failures() == 0 and _hip.decode_wait_flag() == 0
     prev = _hip.set_wait_checks(False)
     try:
         _hip.set_spin_limit(0)
+        _hip.decode_attn_il8(*args, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        # the pinned host copy is set once the failed launch has run ...
+        assert _hip.decode_wait_flag() != 0
+        # ... so the next decode call raises before it launches, without a
+        # per-call synchronisation (the check clears both words)
+        with pytest.raises(_hip.SunShapeWaitError):
+            _hip.decode_attn_il8(*args, out_dtype=torch.float32)
+        assert _hip.decode_wait_flag() == 0 and _hip.decode_wait_failures() == 0
         _hip.decode_attn_il8(*args, out_dtype=torch.float32)
         flags = _hip.decode_wait_failures(clear=False)
         assert flags != 0 and flags & ~7 == 0
         with pytest.raises(_hip.SunShapeWaitError):
             _hip.check_decode_waits()
         assert _hip.decode_wait_failures() == 0  # cleared by the check
+        assert _hip.decode_wait_flag() == 0
         _hip.set_wait_checks(True)
         with pytest.raises(_hip.SunShapeWaitError):
             _hip.decode_attn_il8(*args, out_dtype=torch.float32)
@@ -1185,7 +1196,7 @@ def test_prefill_rising_scores(rise, qdt):
     (1, 32, 8, 200, 200, True, "f16", 256),      # rep 4: 32 positions per workgroup, ragged
     (2, 8, 8, 96, 300, True, "f16", 256),        # rep 1, chunked prefill after 204 cached tokens
     (1, 16, 2, 64, 64, False, "f16", 256),       # rep 8, unmasked
-    (1, 8, 2, 130, 1000, True, "bf16", 100),     # bf16 queries (hi/lo split), 100 centroids
+    (1, 8, 2, 130, 1000, True, "bf16", 100),     # bf16 queries (32-row kernel), 100 centroids
     (1, 4, 1, 33, 77, True, "f32", 256),         # f32 queries, partial tiles everywhere
 ])
 def test_prefill_il8_matches_oracle(b, hq, hkv, t_q, t_kv, causal, qdt, nc):
@@ -1219,3 +1230,38 @@ def test_prefill_il8_matches_oracle(b, hq, hkv, t_q, t_kv, causal, qdt, nc):
     assert np.isfinite(got).all()
     assert rel_err(got, ref) <= REL_TOL
     assert rel_err(got, ref_dec.cpu().numpy()) <= REL_TOL
+
+
+@pytest.mark.parametrize("e2", [20, -20])
+def test_queries_beyond_fp16_range_prefill_and_decode(e2):
+    """bf16 and float32 queries whose scaled elements lie beyond fp16's range
+    (2^20 times larger than usual, past +-65504) or below its normal range
+    (2^20 times smaller, under 2^-14), against centroids scaled the other
+    way so the scores stay of order one: the prefill kernels (32-row for
+    bf16, 16-row for float32) and the matrix-core decode's LUT take each
+    query row scaled by a power of two into fp16's range, so the outputs
+    match the oracle at the usual bar instead of saturating or flushing."""
+    b, hq, hkv, d, t_q, t_kv = 1, 8, 2, 128, 96, 700
+    cap = 704
+    cents, perm, idx, vals, q16 = decode_case(880 + e2, b, hq, hkv, d, t_kv, t_q, cap)
+    cents = (cents * np.float32(2.0 ** -e2)).astype(np.float32)
+    scale = 1.0 / np.sqrt(d)
+    v8 = to_il8(vals, cap)
+    cb = _hip.codebook_f16x2(t(cents))
+    for qdt in (torch.bfloat16, torch.float32):
+        # pre-scaled so q * 1 rounds to itself in the query dtype and the oracle
+        qt = t(q16.astype(np.float32) * np.float32(scale * 2.0 ** e2)).to(qdt)
+        qref = qt.float().cpu().numpy()
+        big = np.abs(qref).max()
+        assert (big > 65504) if e2 > 0 else (big < 2.0 ** -14)
+        out = _hip.prefill_attn_il8(qt, 1.0, t(perm), cb, 256, t(idx), v8, t_kv, causal=True,
+                                    q_offset=t_kv - t_q, out_dtype=torch.float32)
+        dec = _hip.decode_attn_il8(qt[:, :, -4:].contiguous(), 1.0, t(perm), t(cents), t(idx), v8,
+                                   t_kv, causal=True, q_offset=t_kv - 4, out_dtype=torch.float32,
+                                   codebook=cb)
+        torch.cuda.synchronize()
+        ref = O.sdpa(qref, idx[:, :, :t_kv], vals[:, :, :t_kv], cents, perm, 1.0, mask="causal")
+        got = out.cpu().numpy()
+        assert np.isfinite(got).all() and rel_err(got, ref) <= REL_TOL, qdt
+        gd = dec.cpu().numpy()
+        assert np.isfinite(gd).all() and rel_err(gd, ref[:, :, -4:]) <= REL_TOL, qdt
