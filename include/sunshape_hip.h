@@ -356,6 +356,54 @@ int ss_append_values_il8(const void *values, int v_dtype, int64_t n_b, int64_t n
                          void *stream);
 
 /*
+ * The whole KV append of an fp16-value cache (reference
+ * SunShapeKVCache.update_and_fetch, cache.py:156-205, which quantises per
+ * (batch, head) on the host and re-uploads every buffer): n_b x n_h x n_t
+ * tokens of keys (strides k_*) are encoded as ss_encode_blockvq does into
+ * rows offset .. offset + n_t of idx_cache [n_b][n_h][cap][n_blocks], and
+ * their values (strides v_*) are stored as ss_append_values_il8 does into
+ * values_il8 [n_b][n_h][cap/8][head_dim][8].  A decode step's few tokens take
+ * one launch (a wave per (token, block) beside the value stores); a prompt
+ * (more than 4096 token-blocks) takes the bulk encoders (the matrix-core one
+ * with `prepared`, ss_encode_codebook's buffer, may be NULL) and then the
+ * value stores.  Indices are identical to ss_encode_blockvq's.
+ */
+int ss_append_kv_il8(const void *keys, int keys_dtype, const void *values, int v_dtype,
+                     int64_t n_b, int64_t n_h, int64_t n_t, int64_t k_sb, int64_t k_sh,
+                     int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int head_dim,
+                     const int32_t *perm, const float *centroids, int n_blocks,
+                     int n_centroids, int block_dim, const void *prepared,
+                     uint8_t *idx_cache, void *values_il8, int64_t cap, int64_t offset,
+                     void *stream);
+
+/*
+ * One decode step of a hybrid cache with grouped 2/4-bit values kept in the
+ * interleaved code layout (ss_pack_grouped_il), in one launch (reference
+ * HybridSunShapeKVCache.update_and_fetch + _flush_buffer, cache.py:463-710,
+ * which shifts the buffer and re-quantises per (batch, head) on the host):
+ *   - n_new new tokens (keys/values strides k_*, v_*, dtype kv_dtype) are
+ *     stored at buffer positions put_pos .. of buf_keys / buf_values
+ *     [n_b][n_h][buf_cap][head_dim] (dtype buf_dtype);
+ *   - the n_flush buffered tokens at positions flush_pos .. are encoded as
+ *     ss_encode_blockvq does into rows offset .. of idx_cache
+ *     [n_b][n_h][cap][n_blocks], and their values quantised as
+ *     ss_quantize_values_grouped does (identical codes, scale and zero) into
+ *     codes_il [n_b][n_h][cap / (32 / bits)][head_dim] (bits of other tokens
+ *     kept) and scales / zeros [n_b][n_h][cap][head_dim / group_size].
+ * The stored and flushed buffer ranges must not overlap.  Codecs with
+ * block_dim 8 and at most 256 centroids; a step of more than 65536 flushed
+ * token-blocks returns SS_ERR_UNSUPPORTED (take the separate appends).
+ */
+int ss_hybrid_append_grouped_il(
+    const void *keys, const void *values, int kv_dtype, int64_t n_b, int64_t n_h, int64_t n_new,
+    int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    void *buf_keys, void *buf_values, int buf_dtype, int64_t buf_cap, int64_t put_pos,
+    int64_t flush_pos, int64_t n_flush, int head_dim, const int32_t *perm, const float *centroids,
+    int n_blocks, int n_centroids, int block_dim, uint8_t *idx_cache, int bits, int group_size,
+    uint32_t *codes_il, void *scales, void *zeros, int sz_dtype, int64_t cap, int64_t offset,
+    void *stream);
+
+/*
  * As ss_decode_attn_dense with grouped asymmetric-quantised values decoded in
  * registers: v = ((w >> ((d % vpw) * bits)) & (2^bits - 1)) * scale + zero.
  * Replaces fused_attention_dequant_metal / _causal_metal (reference

@@ -104,6 +104,14 @@ _SIGNATURES = {
     "ss_codebook_f16x2": (_int, [_c_void_p, _int, _int, _c_void_p, _c_void_p]),
     "ss_append_values_il8": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                                     _c_void_p, _i64, _i64, _c_void_p]),
+    "ss_hybrid_append_grouped_il": (_int, [
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _int, _c_void_p, _c_void_p, _int,
+        _int, _int, _c_void_p, _int, _int, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
+        _c_void_p]),
+    "ss_append_kv_il8": (_int, [_c_void_p, _int, _c_void_p, _int, _i64, _i64, _i64, _i64, _i64,
+                                _i64, _i64, _i64, _i64, _int, _c_void_p, _c_void_p, _int, _int,
+                                _int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "ss_decode_attn_grouped": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
@@ -794,6 +802,55 @@ def append_values_il8(values: torch.Tensor, out_il8: torch.Tensor, offset: int) 
     check(load_library().ss_append_values_il8(
         ptr(values), dtype_code(values.dtype), b_, h_, t_, values.stride(0), values.stride(1),
         values.stride(2), d, ptr(out_il8), cap, int(offset), stream_handle(values.device)))
+
+
+class PreparedAppend:
+    """``ss_append_kv_il8`` into fixed cache buffers: the codebook, the
+    permutation and the cache pointers are checked and packed once; a call
+    passes the new keys and values (B, H, T, D, unit last stride) and the
+    cache offset.  The caller (the cache that built it) keeps the buffers
+    alive and builds a new one when they change."""
+
+    __slots__ = ("fn", "mid", "tail", "shape_bh", "d", "cap", "dev")
+
+    def __init__(self, perm: torch.Tensor | None, centroids: torch.Tensor,
+                 prepared: torch.Tensor | None, idx_cache: torch.Tensor, values_il8: torch.Tensor):
+        require_gpu(centroids, idx_cache, values_il8)
+        if centroids.dtype != torch.float32 or not centroids.is_contiguous():
+            raise ValueError("centroids must be contiguous float32 (n_blocks, n_centroids, block_dim)")
+        nb, nc, bd = centroids.shape
+        b_, h_, cap, nb2 = idx_cache.shape
+        if nb2 != nb or idx_cache.dtype != torch.uint8 or not idx_cache.is_contiguous():
+            raise ValueError("idx_cache must be contiguous uint8 (B, H, cap, n_blocks)")
+        if values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+                tuple(values_il8.shape) != (b_, h_, cap // 8, nb * bd, 8):
+            raise ValueError(f"values_il8 must be contiguous float16 {(b_, h_, cap // 8, nb * bd, 8)}")
+        if perm is not None and (perm.dtype != torch.int32 or perm.numel() != nb * bd):
+            raise ValueError("perm must be int32 of length head_dim")
+        lib = load_library()
+        if prepared is not None and (prepared.dtype != torch.uint8 or
+                                     prepared.numel() < lib.ss_encode_codebook_bytes(nb)):
+            raise ValueError("prepared must be the uint8 buffer of encode_codebook(centroids)")
+        self.fn = lib.ss_append_kv_il8
+        self.mid = (nb * bd, ptr(perm), ptr(centroids), nb, nc, bd, ptr(prepared))
+        self.tail = (ptr(idx_cache), ptr(values_il8), cap)
+        self.shape_bh = (b_, h_)
+        self.d = nb * bd
+        self.cap = cap
+        self.dev = device_index(idx_cache.device)
+
+    def __call__(self, keys: torch.Tensor, values: torch.Tensor, offset: int) -> None:
+        b_, h_, t_, d = keys.shape
+        if (b_, h_) != self.shape_bh or d != self.d or tuple(values.shape) != (b_, h_, t_, d) or \
+                keys.stride(3) != 1 or values.stride(3) != 1 or keys.device.index != self.dev or \
+                values.device.index != self.dev:
+            raise ValueError(f"keys/values must be {self.shape_bh + ('T', self.d)} with unit last "
+                             f"stride on cuda:{self.dev}")
+        ks, vs = keys.stride(), values.stride()
+        rc = self.fn(keys.data_ptr(), dtype_code(keys.dtype), values.data_ptr(),
+                     dtype_code(values.dtype), b_, h_, t_, ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                     *self.mid, *self.tail, int(offset), stream_handle(self.dev))
+        _launched("sunshape_block_vq_quantize_hip", rc)
 
 
 def il8_to_dense(values_il8: torch.Tensor, t_kv: int | None = None) -> torch.Tensor:

@@ -33,6 +33,59 @@ def _round_capacity(n: int) -> int:
     return ((n + _STEP - 1) // _STEP) * _STEP
 
 
+class DeferredTensor(torch.Tensor):
+    """A tensor ``update_and_fetch`` returns but builds only if something
+    reads it.  The reference returns the whole cache dequantised on every
+    call (cache.py:156-205, 656-710), O(T) work per decode step that the
+    patched SDPA never reads.  Shape, dtype and device are known at once;
+    any torch operation on the tensor (indexing, arithmetic, ``.cpu()``,
+    passing it to a torch function) builds it once, from the cache as it
+    stood when ``update_and_fetch`` returned, and runs on the result.  The
+    cache must not change in between: building it after a later append,
+    trim or flush raises."""
+
+    @staticmethod
+    def __new__(cls, build, shape, dtype, device, cache):
+        t = torch.Tensor._make_wrapper_subclass(cls, shape, dtype=dtype, device=device)
+        t._build = build
+        t._cache = cache
+        t._stamp = cache._version
+        t._value = None
+        return t
+
+    def materialize(self) -> torch.Tensor:
+        """The tensor itself (built on first use)."""
+        if self._value is None:
+            if self._cache._version != self._stamp:
+                raise RuntimeError(
+                    "the cache has changed since update_and_fetch returned this tensor; use it "
+                    "before the next append, trim or flush, or build the cache with "
+                    "lazy_fetch=False")
+            self._value = self._build()
+        return self._value
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        def real(x):
+            return x.materialize() if isinstance(x, DeferredTensor) else x
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
+        return func(*args, **kwargs)
+
+    def __repr__(self) -> str:
+        return f"DeferredTensor({self.materialize()!r})"
+
+
+def _fetched(cache, build, b_: int, last: int, dtype):
+    """What ``update_and_fetch`` returns for one of keys / values (batch
+    ``b_``): the built tensor with ``lazy_fetch`` off (the reference's
+    behaviour), else a ``DeferredTensor`` over ``build``."""
+    if not cache.lazy_fetch:
+        return build()
+    return DeferredTensor(build, (b_, cache.n_kv_heads, cache.offset, last), dtype,
+                          cache.codec.device, cache)
+
+
 def _grow(buf: torch.Tensor | None, shape, dtype, device, keep: int) -> torch.Tensor:
     """New zeroed buffer of ``shape`` holding the first ``keep`` tokens of ``buf``."""
     new = torch.zeros(shape, dtype=dtype, device=device)
@@ -85,7 +138,8 @@ class SunShapeKVCache:
 
     def __init__(self, codec: SunShapeBlockCodec, *, n_kv_heads: int = 1,
                  head_dim: int | None = None, dtype: torch.dtype = torch.float16,
-                 max_tokens: int | None = None, return_dequantized_keys: bool = True):
+                 max_tokens: int | None = None, return_dequantized_keys: bool = True,
+                 lazy_fetch: bool = True):
         self.codec = codec
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim or codec.head_dim
@@ -97,8 +151,12 @@ class SunShapeKVCache:
         self.max_tokens = max_tokens
         # The reference returns dequantised keys from update_and_fetch (an
         # O(T) reconstruction per call that the patched SDPA never reads);
-        # serving loops can switch it off.
+        # serving loops can switch it off.  With lazy_fetch (the default)
+        # both returned tensors are DeferredTensors, built only if read.
         self.return_dequantized_keys = return_dequantized_keys
+        self.lazy_fetch = lazy_fetch
+        self._version = 0  # bumped by every change of the stored tokens
+        self._append_plan = None
         self._key_indices: torch.Tensor | None = None  # (B, H, cap, NB) uint8
         # (B, H, cap/8, D, 8) fp16 when interleaved, else (B, H, cap, D) dtype
         self._values: torch.Tensor | None = None
@@ -131,15 +189,41 @@ class SunShapeKVCache:
         assert d == self.head_dim, f"Expected head_dim {self.head_dim}, got {d}"
         _hip.require_gpu(keys, values)
         self._ensure_capacity(b_, t_, keys.device)
-        sl = slice(self.offset, self.offset + t_)
-        _encode_into(self.codec, keys, self._key_indices[:, :, sl])
-        if self.values_interleaved:
+        plan = self._append_kv_plan()
+        if plan is not None:  # encode + value store, one launch per decode step
+            k = keys if keys.stride(-1) == 1 else keys.contiguous()
             v = values if values.stride(-1) == 1 else values.contiguous()
-            _hip.append_values_il8(v, self._values, self.offset)
+            plan(k, v, self.offset)
         else:
-            self._values[:, :, sl] = values.to(self.dtype)
+            sl = slice(self.offset, self.offset + t_)
+            _encode_into(self.codec, keys, self._key_indices[:, :, sl])
+            if self.values_interleaved:
+                v = values if values.stride(-1) == 1 else values.contiguous()
+                _hip.append_values_il8(v, self._values, self.offset)
+            else:
+                self._values[:, :, sl] = values.to(self.dtype)
         self.offset += t_
-        return (self.keys if self.return_dequantized_keys else None), self.values
+        self._version += 1
+        keys_out = (_fetched(self, lambda: self.keys, b_, self.head_dim, torch.float32)
+                    if self.return_dequantized_keys else None)
+        return keys_out, _fetched(self, lambda: self.values, b_, self.head_dim, self.dtype)
+
+    def _append_kv_plan(self):
+        """The prepared ``ss_append_kv_il8`` for the current buffers and
+        codebook (None where that path does not apply: non-interleaved
+        values, or codecs whose keys the HIP encoder does not take)."""
+        c = self.codec
+        if not self.values_interleaved or c.mode != "profileperm_baseline" or c.n_centroids > 256:
+            return None
+        cb, pm, pre = c.centroids, c.permutation, c.encode_codebook()
+        key = (self._key_indices, self._values, cb, cb._version, pm,
+               pm._version if pm is not None else 0, pre)
+        held = self._append_plan
+        if held is None or len(held[0]) != len(key) or \
+                not all(a is b or (isinstance(a, int) and a == b) for a, b in zip(held[0], key)):
+            held = (key, _hip.PreparedAppend(pm, cb, pre, self._key_indices, self._values))
+            self._append_plan = held
+        return held[1]
 
     # ----------------------------------------------------------- accessors
     @property
@@ -210,6 +294,7 @@ class SunShapeKVCache:
 
     def trim(self, n: int) -> None:
         self.offset = max(0, self.offset - n)
+        self._version += 1
 
     def empty(self) -> bool:
         return self.offset == 0
@@ -248,8 +333,13 @@ class HybridSunShapeKVCache:
                  buffer_size: int = _DEFAULT_BUFFER_SIZE, value_backend: str | None = None,
                  value_bits: int | None = None, value_group_size: int = 64, value_seed: int = 43,
                  value_codec: SunShapeBlockCodec | None = None, prefer_metal_kernels: bool = True,
-                 value_scale_dtype: torch.dtype = torch.float32, max_tokens: int | None = None):
+                 value_scale_dtype: torch.dtype = torch.float32, max_tokens: int | None = None,
+                 lazy_fetch: bool = True):
         self.codec = codec
+        # update_and_fetch returns DeferredTensors (built only if read)
+        # unless lazy_fetch is off (the reference's eager O(T) return)
+        self.lazy_fetch = lazy_fetch
+        self._version = 0  # bumped by every change of the stored tokens
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim or codec.head_dim
         self.block_dim = codec.block_dim
@@ -290,8 +380,14 @@ class HybridSunShapeKVCache:
             prefer_metal=self.prefer_metal_kernels)
         self._compressed_offset = 0
         self._buffer_offset = 0
+        # the buffered tokens are the window [_buf_start, _buf_start +
+        # _buffer_offset) of the buffer stores: a flush advances the start
+        # instead of shifting the rest, and the window slides back to the
+        # front only when it reaches the end of the store
+        self._buf_start = 0
         self._key_buffer: torch.Tensor | None = None
         self._value_buffer: torch.Tensor | None = None
+        self._step_plan = None
         self._key_indices: torch.Tensor | None = None
         self._values_packed: torch.Tensor | None = None
         self._value_scales: torch.Tensor | None = None
@@ -389,8 +485,9 @@ class HybridSunShapeKVCache:
         dev = self._key_buffer.device
         self._grow_compressed(b_, self._compressed_offset + n, dev)
         c0, c1 = self._compressed_offset, self._compressed_offset + n
-        kf = self._key_buffer[:, :, :n]
-        vf = self._value_buffer[:, :, :n]
+        s0 = self._buf_start
+        kf = self._key_buffer[:, :, s0:s0 + n]
+        vf = self._value_buffer[:, :, s0:s0 + n]
         _encode_into(self.codec, kf, self._key_indices[:, :, c0:c1])
         if self._heavy_dims is not None:
             kp = kf[..., self.codec.permutation.long()]
@@ -432,40 +529,116 @@ class HybridSunShapeKVCache:
         else:
             self._values_fp16[:, :, c0:c1] = vf.to(self.dtype)
             self.last_value_quant_backend = "fp16"
-        remaining = self._buffer_offset - n
-        if remaining > 0:
-            self._key_buffer[:, :, :remaining] = self._key_buffer[:, :, n:n + remaining].clone()
-            self._value_buffer[:, :, :remaining] = self._value_buffer[:, :, n:n + remaining].clone()
-        self._key_buffer[:, :, remaining:] = 0
-        self._value_buffer[:, :, remaining:] = 0
         self._compressed_offset = c1
-        self._buffer_offset = remaining
+        self._buffer_offset -= n
+        self._buf_start = s0 + n if self._buffer_offset else 0
+
+    def _ensure_buffer(self, b_: int, t_: int, dev) -> None:
+        """Room in the buffer stores for ``t_`` tokens after the window: the
+        window slides to the front when it reaches the end of the store
+        (at most buffer_size tokens moved once per store length of appends),
+        and the store grows when the window itself would not fit."""
+        h_, d = self.n_kv_heads, self.head_dim
+        if self._key_buffer is None:
+            size = max(2 * self.buffer_size, t_, 1)
+            self._key_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
+            self._value_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
+            self._buf_start = 0
+            return
+        n, s0, cap = self._buffer_offset, self._buf_start, self._key_buffer.shape[2]
+        if s0 + n + t_ <= cap:
+            return
+        if n + t_ > cap:
+            size = max(n + t_, 2 * cap)
+            for name in ("_key_buffer", "_value_buffer"):
+                old = getattr(self, name)
+                new = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
+                new[:, :, :n] = old[:, :, s0:s0 + n]
+                setattr(self, name, new)
+        elif n:
+            self._key_buffer[:, :, :n] = self._key_buffer[:, :, s0:s0 + n].clone()
+            self._value_buffer[:, :, :n] = self._value_buffer[:, :, s0:s0 + n].clone()
+        self._buf_start = 0
+
+    def _grouped_step_plan(self):
+        """The C-ABI arguments of ss_hybrid_append_grouped_il that stay fixed
+        for the current buffers and codebook (None where that fused step does
+        not apply: other value backends, fp16 heavy blocks, codecs the HIP
+        encoder does not take)."""
+        c = self.codec
+        if not self._grouped_il or self._heavy_dims is not None or \
+                c.mode != "profileperm_baseline" or c.n_centroids > 256:
+            return None
+        cb, pm = c.centroids, c.permutation
+        key = (self._key_buffer, self._value_buffer, self._key_indices, self._values_il,
+               self._value_scales, self._value_zeros, cb, cb._version, pm,
+               pm._version if pm is not None else 0)
+        held = self._step_plan
+        if held is not None and len(held[0]) == len(key) and \
+                all(a is b or (isinstance(a, int) and a == b) for a, b in zip(held[0], key)):
+            return held[1]
+        gc = self._value_codec_impl
+        for t in (self._key_buffer, self._value_buffer, self._key_indices, self._values_il,
+                  self._value_scales, self._value_zeros):
+            if not t.is_contiguous():
+                return None
+        nb, nc, bd = cb.shape
+        args = {
+            "buf": (self._key_buffer.data_ptr(), self._value_buffer.data_ptr(),
+                    _hip.dtype_code(self.dtype), self._key_buffer.shape[2]),
+            "codec": (self.head_dim, _hip.ptr(pm), cb.data_ptr(), nb, nc, bd,
+                      self._key_indices.data_ptr(), gc.bits, gc.group_size,
+                      self._values_il.data_ptr(), self._value_scales.data_ptr(),
+                      self._value_zeros.data_ptr(), _hip.dtype_code(self.value_scale_dtype),
+                      self._compressed_capacity),
+            "fn": _hip.load_library().ss_hybrid_append_grouped_il,
+        }
+        self._step_plan = (key, args)
+        return args
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         """Append to the buffer; flush the overflow beyond ``buffer_size``
-        (reference cache.py:656-710)."""
+        (reference cache.py:656-710).  A decode step of a grouped-value cache
+        (the new tokens fit beside the ones that leave) is one launch: the
+        new tokens stored, the oldest buffered ones encoded and quantised
+        into compressed storage.  Returns ``(keys, values)`` of every token,
+        as DeferredTensors unless ``lazy_fetch`` is off."""
         b_, h_, t_, d = keys.shape
         assert h_ == self.n_kv_heads
         assert d == self.head_dim
         _hip.require_gpu(keys, values)
         dev = keys.device
-        if self._key_buffer is None:
-            size = max(self.buffer_size, t_)
-            self._key_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
-            self._value_buffer = torch.zeros((b_, h_, size, d), dtype=self.dtype, device=dev)
-        if self._buffer_offset + t_ > self._key_buffer.shape[2]:
-            size = max(self._buffer_offset + t_, self._key_buffer.shape[2] * 2)
-            self._key_buffer = _grow(self._key_buffer, (b_, h_, size, d), self.dtype, dev,
-                                     self._buffer_offset)
-            self._value_buffer = _grow(self._value_buffer, (b_, h_, size, d), self.dtype, dev,
-                                       self._buffer_offset)
-        sl = slice(self._buffer_offset, self._buffer_offset + t_)
-        self._key_buffer[:, :, sl] = keys.to(self.dtype)
-        self._value_buffer[:, :, sl] = values.to(self.dtype)
-        self._buffer_offset += t_
-        if self._buffer_offset > self.buffer_size:
-            self._flush_buffer(b_, self._buffer_offset - self.buffer_size)
-        return self.keys, self.values
+        self._ensure_buffer(b_, t_, dev)
+        n_flush = max(0, self._buffer_offset + t_ - self.buffer_size)
+        plan = None
+        if self._grouped_il and 0 < n_flush <= self._buffer_offset and t_ <= 64:
+            self._grow_compressed(b_, self._compressed_offset + n_flush, dev)
+            plan = self._grouped_step_plan()
+        k = keys if keys.stride(-1) == 1 else keys.contiguous()
+        v = values if values.stride(-1) == 1 else values.contiguous()
+        if plan is not None and k.dtype == v.dtype:
+            s0, n = self._buf_start, self._buffer_offset
+            ks, vs = k.stride(), v.stride()
+            rc = plan["fn"](k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype), b_, h_, t_,
+                            ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], *plan["buf"], s0 + n,
+                            s0, n_flush, *plan["codec"], self._compressed_offset,
+                            _hip.stream_handle(dev))
+            _hip._launched("sunshape_block_vq_quantize_hip", rc)
+            self._compressed_offset += n_flush
+            self._buffer_offset += t_ - n_flush
+            self._buf_start = s0 + n_flush if self._buffer_offset else 0
+            self.last_value_quant_backend = "hip"
+        else:
+            sl = slice(self._buf_start + self._buffer_offset,
+                       self._buf_start + self._buffer_offset + t_)
+            self._key_buffer[:, :, sl] = keys.to(self.dtype)
+            self._value_buffer[:, :, sl] = values.to(self.dtype)
+            self._buffer_offset += t_
+            if self._buffer_offset > self.buffer_size:
+                self._flush_buffer(b_, self._buffer_offset - self.buffer_size)
+        self._version += 1
+        return (_fetched(self, lambda: self.keys, b_, self.head_dim, torch.float32),
+                _fetched(self, lambda: self.values, b_, self.head_dim, self.dtype))
 
     # ---------------------------------------------------------- accessors
     def _zeros(self, last: int, dtype) -> torch.Tensor:
@@ -481,7 +654,7 @@ class HybridSunShapeKVCache:
                 k[..., od] = self._key_heavy[:, :, :self._compressed_offset].float()
             parts.append(k)
         if self._buffer_offset > 0 and self._key_buffer is not None:
-            parts.append(self._key_buffer[:, :, :self._buffer_offset].float())
+            parts.append(self.buffer_keys.float())
         if not parts:
             return self._zeros(self.head_dim, torch.float32)
         return torch.cat(parts, dim=2)
@@ -522,7 +695,7 @@ class HybridSunShapeKVCache:
         if cv is not None:
             parts.append(cv)
         if self._buffer_offset > 0 and self._value_buffer is not None:
-            parts.append(self._value_buffer[:, :, :self._buffer_offset])
+            parts.append(self.buffer_values)
         if not parts:
             return self._zeros(self.head_dim, self.dtype)
         return torch.cat(parts, dim=2)
@@ -537,13 +710,20 @@ class HybridSunShapeKVCache:
     def buffer_keys(self) -> torch.Tensor:
         if self._key_buffer is None or self._buffer_offset == 0:
             return self._zeros(self.head_dim, self.dtype)
-        return self._key_buffer[:, :, :self._buffer_offset]
+        s0 = self._buf_start
+        return self._key_buffer[:, :, s0:s0 + self._buffer_offset]
 
     @property
     def buffer_values(self) -> torch.Tensor:
         if self._value_buffer is None or self._buffer_offset == 0:
             return self._zeros(self.head_dim, self.dtype)
-        return self._value_buffer[:, :, :self._buffer_offset]
+        s0 = self._buf_start
+        return self._value_buffer[:, :, s0:s0 + self._buffer_offset]
+
+    def _window(self, buf: torch.Tensor | None) -> torch.Tensor | None:
+        """A buffer store from the window's first token on (the view the
+        fused kernels read ``buffer_offset`` tokens of)."""
+        return None if buf is None else buf[:, :, self._buf_start:]
 
     @property
     def compressed_offset(self) -> int:
@@ -598,7 +778,8 @@ class HybridSunShapeKVCache:
             return {"kind": "grouped_il", "idx": self._key_indices, "codes_il": self._values_il,
                     "scales": self._value_scales, "zeros": self._value_zeros,
                     "bits": gc.bits, "group_size": gc.group_size,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer), **heavy}
         if self._heavy_dims is not None and (self.value_backend == "grouped" or
                                              (self.value_backend == "fp16" and
                                               self._values_il8 is None)):
@@ -615,24 +796,28 @@ class HybridSunShapeKVCache:
             return {"kind": "turboquant_il", "idx": self._key_indices, "codes_il": self._values_il,
                     "norms": self._value_norms, "levels": tc.levels_host(),
                     "rotation": tc.rotation,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer), **heavy}
         if self.value_backend == "turboquant" and self._values_packed is not None:
             tc = self._value_codec_impl
             tc._on(self._values_packed.device)
             return {"kind": "turboquant", "idx": self._key_indices,
                     "packed": self._values_packed, "norms": self._value_norms,
                     "levels": tc.levels_host(), "rotation": tc.rotation, "bits": tc.bits,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer), **heavy}
         if self.value_backend == "sunshape" and self._value_indices is not None \
                 and self.value_codec.n_centroids <= 256:
             vc = self.value_codec
             return {"kind": "sunshape_v", "idx": self._key_indices, "v_idx": self._value_indices,
                     "v_centroids": vc.centroids.float().contiguous(),
                     "v_transform": vc.kernel_value_transform(),
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer), **heavy}
         if self.value_backend == "fp16" and self._values_il8 is not None:
             return {"kind": "il8", "idx": self._key_indices, "values": self._values_il8,
-                    "buf_keys": self._key_buffer, "buf_values": self._value_buffer, **heavy}
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer), **heavy}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None
@@ -681,9 +866,12 @@ class HybridSunShapeKVCache:
             return
         b = min(n, self._buffer_offset)
         self._buffer_offset -= b
+        if self._buffer_offset == 0:
+            self._buf_start = 0
         rest = n - b
         if rest > 0:
             self._compressed_offset = max(0, self._compressed_offset - rest)
+        self._version += 1
 
     def empty(self) -> bool:
         return self.offset == 0
@@ -704,7 +892,7 @@ class HybridSunShapeKVCache:
         if self._key_indices is not None and self._compressed_offset > 0:
             parts.append(self._key_indices[:, :, :self._compressed_offset])
         if self._key_buffer is not None and self._buffer_offset > 0:
-            parts.append(self._key_buffer[:, :, :self._buffer_offset])
+            parts.append(self.buffer_keys)
         if not parts:
             parts.append(torch.zeros((1,)))
         return tuple(parts)

@@ -23,9 +23,7 @@ __global__ void __launch_bounds__(256)
     const int64_t h = rem / n_t;
     const int64_t t = rem - h * n_t;
     const float x = load_as_f32(v, v_dtype, b * v_sb + h * v_sh + t * v_st + j);
-    const int64_t pos = offset + t;
-    const int64_t head = b * n_h + h;
-    out[((head * (cap / 8) + pos / 8) * d + j) * 8 + (pos & 7)] = __float2half(x);
+    store_value_il8(out, b * n_h + h, cap, d, offset + t, j, x);
 }
 
 }  // namespace ss

@@ -193,6 +193,168 @@ __global__ void __launch_bounds__(kEncThreads) encode_small_kernel(EncodeArgs a)
     if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
 }
 
+// ---- decode-step KV append: keys encoded and values stored in one launch ----
+//
+// Workgroups [0, n_enc) run encode_small_kernel's waves (one per (token,
+// block)); the rest store the tokens' values into the 8-token interleaved
+// fp16 cache (cache_ops.hip's append_il8_kernel), one element per thread.
+struct ValueAppend {
+    const void *values;
+    int v_dtype;
+    int64_t v_sb, v_sh, v_st;
+    int d;
+    __half *out_il8;
+    int64_t cap, offset;
+};
+
+template <int BD>
+__global__ void __launch_bounds__(kEncThreads) append_kv_small_kernel(EncodeArgs a, ValueAppend v,
+                                                                      int n_enc) {
+    if ((int)blockIdx.x < n_enc) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int64_t job = (int64_t)blockIdx.x * (kEncThreads / kWave) + (threadIdx.x >> 6);
+        if (job >= a.n_tok * a.n_blocks) return;  // wave-uniform
+        const int64_t n = job / a.n_blocks;
+        const int blk = (int)(job - n * a.n_blocks);
+        const TokAddr ad = token_addr(a, n);
+        float kv[BD];
+#pragma unroll
+        for (int k = 0; k < BD; ++k) {
+            const int j = blk * BD + k;
+            kv[k] = load_as_f32(a.keys, a.keys_dtype, ad.key + (a.perm ? a.perm[j] : j));
+        }
+        const int bi = exact_block_wave<BD>(kv, a.centroids + (int64_t)blk * a.n_centroids * BD,
+                                            a.n_centroids, lane);
+        if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
+        return;
+    }
+    const int64_t e = (int64_t)(blockIdx.x - n_enc) * kEncThreads + threadIdx.x;
+    if (e >= a.n_tok * v.d) return;
+    const int64_t n = e / v.d;
+    const int j = (int)(e - n * v.d);
+    const int64_t b = n / (a.n_h * a.n_t);
+    const int64_t rem = n - b * a.n_h * a.n_t;
+    const int64_t h = rem / a.n_t;
+    const int64_t t = rem - h * a.n_t;
+    const float x = load_as_f32(v.values, v.v_dtype, b * v.v_sb + h * v.v_sh + t * v.v_st + j);
+    store_value_il8(v.out_il8, b * a.n_h + h, v.cap, v.d, v.offset + t, j, x);
+}
+
+// ---- one decode step of a hybrid cache with grouped values (interleaved codes) ----
+//
+// Three kinds of workgroups in one launch:
+//   [0, n_put):            the step's new keys and values stored into the
+//                          full-precision buffer at buffer position put_pos;
+//   [n_put, n_put + n_enc): a wave per (flushed token, block) encodes the
+//                          oldest buffered keys (exact_block_wave);
+//   the rest:              a thread per (interleaved code word, dim) of the
+//                          flushed range quantises its tokens' values with the
+//                          grouped min/max rule of quantize_grouped_kernel
+//                          (values.hip; the same IEEE steps, so codes and
+//                          scale/zero are identical) and rewrites the word,
+//                          keeping the bits of tokens outside the range; the
+//                          thread of a group's first dim stores that token's
+//                          scale and zero.
+// The flushed buffer range and the stored range are disjoint (checked on
+// the host), so no workgroup reads what another writes.
+struct HybridGroupedStep {
+    // new tokens (n_b x n_h x n_new) and the buffer [n_b][n_h][buf_cap][d]
+    const void *keys, *values;
+    int kv_dtype;
+    int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+    int64_t n_new;
+    void *buf_keys, *buf_values;
+    int buf_dtype;
+    int64_t buf_cap, put_pos;
+    // flushed buffer tokens [flush_pos, flush_pos + n_flush) -> compressed
+    // positions [offset, offset + n_flush) of a cache of capacity cap
+    int64_t flush_pos, n_flush, offset, cap;
+    int d, bits, group;
+    uint32_t *codes_il;  // [n_b][n_h][cap / (32 / bits)][d]
+    void *scales, *zeros;
+    int sz_dtype;
+    int64_t blk0, n_blk;  // code words touched: word rows blk0 .. blk0 + n_blk - 1
+    int64_t n_bh;         // batch x heads
+};
+
+template <int BD>
+__global__ void __launch_bounds__(kEncThreads)
+    hybrid_grouped_step_kernel(EncodeArgs a, HybridGroupedStep s, int n_put, int n_enc) {
+    const int64_t n_bh = s.n_bh;
+    if ((int)blockIdx.x < n_put) {
+        const int64_t e = (int64_t)blockIdx.x * kEncThreads + threadIdx.x;
+        const int64_t per = s.n_new * s.d;
+        if (e >= 2 * n_bh * per) return;
+        const bool is_v = e >= n_bh * per;
+        const int64_t r = is_v ? e - n_bh * per : e;
+        const int64_t bh = r / per, rem = r - bh * per;
+        const int64_t t = rem / s.d;
+        const int j = (int)(rem - t * s.d);
+        const int64_t b = bh / a.n_h, h = bh - b * a.n_h;
+        const float x = is_v ? load_as_f32(s.values, s.kv_dtype, b * s.v_sb + h * s.v_sh + t * s.v_st + j)
+                             : load_as_f32(s.keys, s.kv_dtype, b * s.k_sb + h * s.k_sh + t * s.k_st + j);
+        store_from_f32(is_v ? s.buf_values : s.buf_keys, s.buf_dtype,
+                       (bh * s.buf_cap + s.put_pos + t) * s.d + j, x);
+        return;
+    }
+    if ((int)blockIdx.x < n_put + n_enc) {
+        const int lane = threadIdx.x & (kWave - 1);
+        const int64_t job = (int64_t)(blockIdx.x - n_put) * (kEncThreads / kWave) + (threadIdx.x >> 6);
+        if (job >= a.n_tok * a.n_blocks) return;  // wave-uniform
+        const int64_t n = job / a.n_blocks;
+        const int blk = (int)(job - n * a.n_blocks);
+        const TokAddr ad = token_addr(a, n);
+        float kv[BD];
+#pragma unroll
+        for (int k = 0; k < BD; ++k) {
+            const int j = blk * BD + k;
+            kv[k] = load_as_f32(a.keys, a.keys_dtype, ad.key + (a.perm ? a.perm[j] : j));
+        }
+        const int bi = exact_block_wave<BD>(kv, a.centroids + (int64_t)blk * a.n_centroids * BD,
+                                            a.n_centroids, lane);
+        if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
+        return;
+    }
+    // values: thread (bh, word row, dim)
+    const int64_t e = (int64_t)(blockIdx.x - n_put - n_enc) * kEncThreads + threadIdx.x;
+    if (e >= n_bh * s.n_blk * s.d) return;
+    const int64_t bh = e / (s.n_blk * s.d), rem = e - bh * s.n_blk * s.d;
+    const int64_t blk = s.blk0 + rem / s.d;
+    const int dd = (int)(rem % s.d);
+    const int vpw = 32 / s.bits;
+    const uint32_t mask = (1u << s.bits) - 1u;
+    const float maxv = (float)((1 << s.bits) - 1);
+    const int g = dd / s.group, n_groups = s.d / s.group;
+    uint32_t *wp = s.codes_il + (bh * (s.cap / vpw) + blk) * s.d + dd;
+    uint32_t word = *wp;
+    for (int i = 0; i < vpw; ++i) {
+        const int64_t t = blk * vpw + i - s.offset;  // flushed token of this slot
+        if (t < 0 || t >= s.n_flush) continue;
+        const int64_t vin = (bh * s.buf_cap + s.flush_pos + t) * s.d;
+        float mn = INFINITY, mx = -INFINITY;
+        for (int k = 0; k < s.group; ++k) {
+            const float v = load_as_f32(s.buf_values, s.buf_dtype, vin + g * s.group + k);
+            mn = fminf(mn, v);
+            mx = fmaxf(mx, v);
+        }
+        float sc = __fdiv_rn(__fsub_rn(mx, mn), maxv);
+        if (sc < 1e-8f) sc = 1e-8f;
+        const float v = load_as_f32(s.buf_values, s.buf_dtype, vin + dd);
+        float qf = rintf(__fdiv_rn(__fsub_rn(v, mn), sc));
+        qf = fminf(fmaxf(qf, 0.f), maxv);
+        const uint32_t code = (uint32_t)qf & mask;
+        // token i of the word: bits*(i/2) in the low half for even i, +16 for odd i
+        const int pos = s.bits * (i >> 1) + 16 * (i & 1);
+        word = (word & ~(mask << pos)) | (code << pos);
+        if (dd == g * s.group) {
+            const int64_t srow = (bh * s.cap + s.offset + t) * n_groups + g;
+            store_from_f32(s.scales, s.sz_dtype, srow, sc);
+            store_from_f32(s.zeros, s.sz_dtype, srow, mn);
+        }
+    }
+    *wp = word;
+}
+
 // ---- bulk on the matrix cores (block_dim 8): a bounded filter, then exact ties ----
 //
 // Per block b the codebook and the keys are scaled by s_b, a power of two
@@ -739,4 +901,113 @@ extern "C" int ss_encode_blockvq_prepared(const void *keys, int keys_dtype, int6
                                           const void *prepared, void *stream) {
     return encode_impl(keys, keys_dtype, n_b, n_h, n_t, k_sb, k_sh, k_st, head_dim, perm, centroids,
                        n_blocks, n_centroids, block_dim, out, o_sb, o_sh, o_st, prepared, stream);
+}
+
+extern "C" int ss_append_kv_il8(const void *keys, int keys_dtype, const void *values, int v_dtype,
+                                int64_t n_b, int64_t n_h, int64_t n_t, int64_t k_sb, int64_t k_sh,
+                                int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st, int head_dim,
+                                const int32_t *perm, const float *centroids, int n_blocks,
+                                int n_centroids, int block_dim, const void *prepared,
+                                uint8_t *idx_cache, void *values_il8, int64_t cap, int64_t offset,
+                                void *stream) {
+    SS_REQUIRE(valid_dtype(keys_dtype) && valid_dtype(v_dtype), "bad key or value dtype");
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0, "negative token counts");
+    SS_REQUIRE(head_dim > 0 && block_dim > 0 && n_blocks * block_dim == head_dim,
+               "n_blocks (%d) * block_dim (%d) != head_dim (%d)", n_blocks, block_dim, head_dim);
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256,
+                   "n_centroids %d unsupported for uint8 indices (1..256)", n_centroids);
+    SS_UNSUPPORTED(block_dim == 4 || block_dim == 8 || block_dim == 16,
+                   "block_dim %d unsupported (4, 8, 16)", block_dim);
+    SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8");
+    SS_REQUIRE(offset >= 0 && offset + n_t <= cap, "tokens [%lld, %lld) exceed cap %lld",
+               (long long)offset, (long long)(offset + n_t), (long long)cap);
+    const int64_t n_tok = n_b * n_h * n_t;
+    if (n_tok == 0) return SS_OK;
+    SS_REQUIRE(keys && values && centroids && idx_cache && values_il8, "null pointer argument");
+    SS_UNSUPPORTED(n_tok * head_dim < (1LL << 31), "too many elements for one launch");
+    // the index cache [n_b][n_h][cap][n_blocks], rows from `offset` on
+    uint8_t *out = idx_cache + offset * n_blocks;
+    const int64_t o_st = n_blocks, o_sh = cap * n_blocks, o_sb = n_h * o_sh;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (n_tok * n_blocks > 4096) {  // a prompt: the bulk encoders, then the values
+        const int rc = encode_impl(keys, keys_dtype, n_b, n_h, n_t, k_sb, k_sh, k_st, head_dim, perm,
+                                   centroids, n_blocks, n_centroids, block_dim, out, o_sb, o_sh, o_st,
+                                   prepared, stream);
+        if (rc != SS_OK) return rc;
+        return ss_append_values_il8(values, v_dtype, n_b, n_h, n_t, v_sb, v_sh, v_st, head_dim,
+                                    values_il8, cap, offset, stream);
+    }
+    EncodeArgs a{keys, keys_dtype, n_h,  n_t,        n_tok,     k_sb, k_sh, k_st,
+                 perm, centroids,  n_blocks, n_centroids, out, o_sb, o_sh, o_st};
+    const ValueAppend v{values, v_dtype, v_sb, v_sh, v_st, head_dim,
+                        static_cast<__half *>(values_il8), cap, offset};
+    const int per = kEncThreads / kWave;
+    const int n_enc = (int)((n_tok * n_blocks + per - 1) / per);
+    const int n_val = (int)((n_tok * head_dim + kEncThreads - 1) / kEncThreads);
+    const dim3 grid((unsigned)(n_enc + n_val));
+    if (block_dim == 8)
+        hipLaunchKernelGGL(append_kv_small_kernel<8>, grid, dim3(kEncThreads), 0, st, a, v, n_enc);
+    else if (block_dim == 4)
+        hipLaunchKernelGGL(append_kv_small_kernel<4>, grid, dim3(kEncThreads), 0, st, a, v, n_enc);
+    else
+        hipLaunchKernelGGL(append_kv_small_kernel<16>, grid, dim3(kEncThreads), 0, st, a, v, n_enc);
+    SS_LAUNCH_CHECK("append_kv_small_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_hybrid_append_grouped_il(
+    const void *keys, const void *values, int kv_dtype, int64_t n_b, int64_t n_h, int64_t n_new,
+    int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    void *buf_keys, void *buf_values, int buf_dtype, int64_t buf_cap, int64_t put_pos,
+    int64_t flush_pos, int64_t n_flush, int head_dim, const int32_t *perm, const float *centroids,
+    int n_blocks, int n_centroids, int block_dim, uint8_t *idx_cache, int bits, int group_size,
+    uint32_t *codes_il, void *scales, void *zeros, int sz_dtype, int64_t cap, int64_t offset,
+    void *stream) {
+    SS_REQUIRE(valid_dtype(kv_dtype) && valid_dtype(buf_dtype), "bad key/value or buffer dtype");
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_UNSUPPORTED(block_dim == 8 && n_blocks * 8 == head_dim, "block_dim 8 codecs only");
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256, "n_centroids %d unsupported (1..256)",
+                   n_centroids);
+    SS_UNSUPPORTED(bits == 2 || bits == 4, "interleaved codes are 2- or 4-bit");
+    SS_REQUIRE(group_size >= 1 && head_dim % group_size == 0, "head_dim %d not divisible by %d",
+               head_dim, group_size);
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_new >= 0 && n_flush >= 0, "negative sizes");
+    SS_REQUIRE(put_pos >= 0 && put_pos + n_new <= buf_cap && flush_pos >= 0 &&
+                   flush_pos + n_flush <= buf_cap,
+               "buffer ranges exceed its capacity %lld", (long long)buf_cap);
+    SS_REQUIRE(n_new == 0 || n_flush == 0 || put_pos >= flush_pos + n_flush ||
+                   put_pos + n_new <= flush_pos,
+               "the stored and flushed buffer ranges overlap");
+    const int vpw = 32 / bits;
+    SS_REQUIRE(cap % vpw == 0 && offset >= 0 && offset + n_flush <= cap,
+               "compressed range [%lld, %lld) exceeds cap %lld", (long long)offset,
+               (long long)(offset + n_flush), (long long)cap);
+    const int64_t n_bh = n_b * n_h;
+    if (n_bh == 0 || (n_new == 0 && n_flush == 0)) return SS_OK;
+    SS_REQUIRE(buf_keys && buf_values && (n_new == 0 || (keys && values)), "null pointer argument");
+    SS_REQUIRE(n_flush == 0 || (centroids && idx_cache && codes_il && scales && zeros),
+               "null pointer argument");
+    SS_UNSUPPORTED(n_flush * n_blocks <= 65536 && n_new * head_dim <= (1 << 20),
+                   "step too large for one launch (take the separate appends)");
+    // keys to encode: the flushed buffer rows; indices at compressed rows offset ..
+    EncodeArgs a{reinterpret_cast<const char *>(buf_keys) +
+                     flush_pos * head_dim * dtype_bytes(buf_dtype),
+                 buf_dtype, n_h, n_flush, n_bh * n_flush, n_h * buf_cap * head_dim,
+                 buf_cap * head_dim, head_dim, perm, centroids, n_blocks, n_centroids,
+                 idx_cache + offset * n_blocks, n_h * cap * n_blocks, cap * n_blocks, n_blocks};
+    HybridGroupedStep hs{keys, values, kv_dtype, k_sb, k_sh, k_st, v_sb, v_sh, v_st, n_new,
+                         buf_keys, buf_values, buf_dtype, buf_cap, put_pos, flush_pos, n_flush,
+                         offset, cap, head_dim, bits, group_size, codes_il, scales, zeros, sz_dtype,
+                         offset / vpw, n_flush ? (offset + n_flush - 1) / vpw - offset / vpw + 1 : 0,
+                         n_bh};
+    const int n_put = (int)((2 * n_bh * n_new * head_dim + kEncThreads - 1) / kEncThreads);
+    const int per = kEncThreads / kWave;
+    const int n_enc = (int)((n_bh * n_flush * n_blocks + per - 1) / per);
+    const int64_t n_val = (n_bh * hs.n_blk * head_dim + kEncThreads - 1) / kEncThreads;
+    SS_UNSUPPORTED(n_put + n_enc + n_val < (1LL << 31), "step too large for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(hybrid_grouped_step_kernel<8>, dim3((unsigned)(n_put + n_enc + n_val)),
+                       dim3(kEncThreads), 0, st, a, hs, n_put, n_enc);
+    SS_LAUNCH_CHECK("hybrid_grouped_step_kernel launch");
+    return SS_OK;
 }

@@ -57,6 +57,13 @@ __device__ __forceinline__ float round_to(int dt, float x) {
     return x;
 }
 
+// Value element j of token (b, h, t) -> the 8-token interleaved fp16 cache
+// layout [b*n_h + h][cap/8][d][8] at position offset + t.
+__device__ __forceinline__ void store_value_il8(__half *out, int64_t head, int64_t cap, int d,
+                                                int64_t pos, int j, float x) {
+    out[((head * (cap / 8) + pos / 8) * d + j) * 8 + (pos & 7)] = __float2half(x);
+}
+
 // Exponent s of the power of two 2^s that brings m = max |x| of a query row
 // into [2^14, 2^15) as m * 2^-s, so every element of the row scaled by 2^-s
 // lies within fp16's range and an element of at most 11 significant bits

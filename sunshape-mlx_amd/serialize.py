@@ -42,7 +42,7 @@ _CACHE_TENSORS = {
 _CACHE_SCALARS = {
     "SunShapeKVCache": ("offset", "_capacity"),
     "HybridSunShapeKVCache": ("_compressed_offset", "_buffer_offset", "_compressed_capacity",
-                              "_value_n_groups"),
+                              "_value_n_groups", "_buf_start"),
 }
 
 

@@ -785,3 +785,83 @@ def test_router_sends_sunshape_caches_to_sunshape_sdpa():
         S.patch.revert()
         S.patch._extra_targets.clear()
         sys.modules.pop("ss_test_models_base", None)
+
+
+def test_decode_step_append_is_one_fused_launch_and_returns_deferred():
+    """SunShapeKVCache.update_and_fetch on decode steps: one
+    ss_append_kv_il8 launch per step writes the same indices and values as
+    the separate encoder and value append (bit for bit, against the oracle's
+    encode and the stored fp16 values), and the returned keys / values are
+    DeferredTensors: built only when read, equal to the reference's eager
+    return, refused once the cache has changed."""
+    codec = make_codec(70)
+    b, hkv, d = 2, 4, 128
+    k, v = kv(71, b, hkv, 300, d)
+    lazy = S.create_kv_cache(codec, n_kv_heads=hkv)
+    eager = S.create_kv_cache(codec, n_kv_heads=hkv, lazy_fetch=False)
+    ko, vo = lazy.update_and_fetch(k[:, :, :290], v[:, :, :290])  # prompt: bulk encoders
+    eager.update_and_fetch(k[:, :, :290], v[:, :, :290])
+    assert isinstance(ko, S.cache.DeferredTensor) and ko.shape == (b, hkv, 290, d)
+    for i in range(290, 300):  # decode steps: the fused append
+        before = dict(S.kernels.get_kernel_stats())
+        ko, vo = lazy.update_and_fetch(k[:, :, i:i + 1], v[:, :, i:i + 1])
+        after = S.kernels.get_kernel_stats()
+        assert sum(after.values()) - sum(before.values()) == 1  # one launch, one count
+        eko, evo = eager.update_and_fetch(k[:, :, i:i + 1], v[:, :, i:i + 1])
+    assert ko.shape == eko.shape and vo.dtype == evo.dtype
+    assert torch.equal(ko + 0, eko) and torch.equal(vo.float(), evo.float())
+    assert torch.equal(lazy.key_indices, eager.key_indices)
+    assert torch.equal(lazy.values, v)
+    idx, near = oracle_indices(codec, k)
+    got = lazy.key_indices.cpu().numpy()
+    assert np.array_equal(got[~near], idx[~near])
+    ko2, _ = lazy.update_and_fetch(k[:, :, :1], v[:, :, :1])
+    ko3, _ = lazy.update_and_fetch(k[:, :, 1:2], v[:, :, 1:2])
+    with pytest.raises(RuntimeError):
+        ko2.cpu()  # not built before the cache moved on
+    assert ko.cpu().shape == (b, hkv, 300, d)  # built earlier: a snapshot, still valid
+    assert ko3.cpu().shape == (b, hkv, 302, d)
+
+
+@pytest.mark.parametrize("bits,buf", [(2, 128), (4, 16)])
+def test_hybrid_grouped_decode_steps_fused_equal_separate_appends(bits, buf):
+    """HybridSunShapeKVCache decode steps with grouped interleaved values: the
+    one-launch step (new tokens stored into the buffer window, the oldest
+    encoded and quantised) leaves exactly the state the separate appends
+    leave (indices, code words, scale/zero, buffer window), across window
+    slides and capacity growth, and the fused decode over it matches the
+    oracle's two-pass path."""
+    codec = make_codec(72)
+    b, hq, hkv, d = 2, 8, 2, 128
+    t_all = 700
+    k, v = kv(73, b, hkv, t_all, d)
+    kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=bits, buffer_size=buf,
+              value_scale_dtype=torch.float16)
+    fused = S.create_kv_cache(codec, **kw)
+    plain = S.create_kv_cache(codec, **kw)
+    plain._grouped_step_plan = lambda: None  # the separate appends
+    fused.update_and_fetch(k[:, :, :300], v[:, :, :300])
+    plain.update_and_fetch(k[:, :, :300], v[:, :, :300])
+    n_fused = 0
+    for i in range(300, t_all):
+        before = sum(S.kernels.get_kernel_stats().values())
+        fused.update_and_fetch(k[:, :, i:i + 1], v[:, :, i:i + 1])
+        n_fused += sum(S.kernels.get_kernel_stats().values()) - before == 1
+        plain.update_and_fetch(k[:, :, i:i + 1], v[:, :, i:i + 1])
+    assert n_fused == t_all - 300  # every decode step was one launch
+    assert fused.compressed_offset == plain.compressed_offset == t_all - buf
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values_packed_raw, plain.values_packed_raw)
+    assert torch.equal(fused.value_scales_raw, plain.value_scales_raw)
+    assert torch.equal(fused.value_zeros_raw, plain.value_zeros_raw)
+    assert torch.equal(fused.buffer_keys, plain.buffer_keys)
+    assert torch.equal(fused.buffer_values, v[:, :, t_all - buf:])
+    q = torch.randn((b, hq, 1, d), device=DEV).to(torch.float16)
+    out = S.sunshape_sdpa(q, fused, 0.088)
+    assert codec.last_score_backend == "hip_fused_mfma_dequant_buffer"
+    assert torch.equal(out, S.sunshape_sdpa(q, plain, 0.088))
+    vals = fused.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
+                          fused.buffer_keys.float().cpu().numpy(), vals)
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
