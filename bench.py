@@ -147,6 +147,38 @@ def stream_ceiling(nbytes: int, steps: int, warmup: int, hip, n_workgroups: int 
             "kernel": "ss_stream_read (plain 16-byte non-temporal loads, 4 in flight per thread)"}
 
 
+def time_api_steps(pkg, caches, q, scale, steps, warmup, kv_step=None) -> dict:
+    """The drop-in path per decode step over caches built through the API,
+    rotated so every step reads HBM: ``sunshape_sdpa`` alone, or (with
+    ``kv_step`` = (keys, values) of one token) ``update_and_fetch`` of that
+    token first, as mlx-lm runs a decode step.  HIP events bracket all the
+    steps; the host clock gives the Python time per step."""
+    import torch
+
+    n = len(caches)
+
+    def one(i):
+        c = caches[i % n]
+        if kv_step is not None:
+            c.update_and_fetch(*kv_step)
+        pkg.sunshape_sdpa(q, c, scale)
+
+    for i in range(warmup):
+        one(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    h0 = time.perf_counter()
+    for i in range(steps):
+        one(i)
+    h1 = time.perf_counter()
+    e1.record()
+    torch.cuda.synchronize()
+    return {"us_per_step": round(e0.elapsed_time(e1) * 1e3 / steps, 3),
+            "host_us_per_step": round((h1 - h0) * 1e6 / steps, 3),
+            "backend": caches[0].codec.last_score_backend}
+
+
 def cpu_threads() -> int:
     """Host threads the CPU baseline uses: the CPUs this process may run on,
     capped at 16 (one GPU's share of the box)."""
@@ -222,6 +254,36 @@ def run_hybrid(args) -> int:
         got = out[bi, hi * 4:(hi + 1) * 4].float().cpu().numpy().reshape(ref.shape)
         check = float(np.abs(got - ref).max() / np.abs(ref).max())
 
+    # ---- the drop-in path: hybrid caches built through the API (default
+    # 128-token fp16 buffer, 2-bit grouped values, fp16 scale/zero), rotated;
+    # sunshape_sdpa alone, then whole decode steps (update_and_fetch of one
+    # token: stored, the oldest buffered token encoded and quantised) ----
+    del bufs, argv, packed0, il0
+    codec = pkg.codec.SunShapeBlockCodec(d, device=dev)
+    codec.load_state_dict({"centroids": cents.cpu().numpy(), "permutation": perm.cpu().numpy()})
+    kk = torch.randn((b, hkv, t_kv, d), generator=g, device=dev).to(torch.float16)
+    vv = torch.randn((b, hkv, t_kv, d), generator=g, device=dev).to(torch.float16)
+    caches = []
+    for _ in range(n_copies):
+        c = pkg.cache.create_kv_cache(codec, n_kv_heads=hkv, value_backend="grouped",
+                                      value_bits=bits, value_group_size=group,
+                                      value_scale_dtype=torch.float16, max_tokens=t_kv + 1024)
+        c.update_and_fetch(kk, vv)
+        caches.append(c)
+    del kk, vv
+    torch.cuda.synchronize()
+    sdpa = time_api_steps(pkg, caches, q, scale, args.steps, args.warmup)
+    log(f"hybrid sunshape_sdpa end to end: {sdpa['us_per_step']:.2f} us/step "
+        f"(host {sdpa['host_us_per_step']:.1f} us/call, {sdpa['backend']})")
+    k1 = torch.randn((b, hkv, 1, d), generator=g, device=dev).to(torch.float16)
+    v1 = torch.randn((b, hkv, 1, d), generator=g, device=dev).to(torch.float16)
+    n_step = min(args.steps, 1024 * n_copies // 2)
+    step = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
+    step["t_kv_range"] = [t_kv, caches[0].offset]
+    log(f"hybrid decode step end to end: {step['us_per_step']:.2f} us/step "
+        f"(host {step['host_us_per_step']:.1f} us/step)")
+    del caches
+
     traffic = None  # HBM bytes per launch from the committed counter runs
     tf = os.path.join(ROOT, "profiles", "decode_grouped2b_t32k_traffic.json")
     if os.path.exists(tf):
@@ -246,6 +308,8 @@ def run_hybrid(args) -> int:
         "per_launch_us": {"mean": round(float(np.mean(per)), 3),
                           "median": round(float(np.median(per)), 3)},
         "check_max_rel_err_vs_oracle": check,
+        "sdpa_end_to_end": sdpa,
+        "decode_step_end_to_end": step,
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -909,36 +973,31 @@ def main() -> int:
     kernel_gbs = gbs
 
     # ---- the drop-in path end to end: sunshape_sdpa on caches built through
-    # the API (create_kv_cache + update_and_fetch), rotated like the kernel ----
-    sdpa = None
+    # the API (create_kv_cache + update_and_fetch), rotated like the kernel;
+    # then whole decode steps (update_and_fetch of one token, then
+    # sunshape_sdpa) on the same caches ----
+    sdpa = step = None
     if args.layout == "il8":
         caches = []
         for i in range(n_copies):
-            cache = pkg.cache.create_kv_cache(codec, n_kv_heads=hkv, max_tokens=t_kv)
+            cache = pkg.cache.create_kv_cache(codec, n_kv_heads=hkv, max_tokens=t_kv + 1024)
             g2 = torch.Generator(device=dev).manual_seed(100 + i)
             kk = (torch.randn((b, hkv, t_kv, d), generator=g2, device=dev) * s_t).to(torch.float16)
             cache.update_and_fetch(kk, v0)
             caches.append(cache)
             del kk
         torch.cuda.synchronize()
-        for i in range(args.warmup):
-            pkg.sunshape_sdpa(q, caches[i % n_copies], scale)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        h0 = time.perf_counter()
-        for i in range(steps):
-            pkg.sunshape_sdpa(q, caches[i % n_copies], scale)
-        h1 = time.perf_counter()
-        e1.record()
-        torch.cuda.synchronize()
-        sdpa_us = e0.elapsed_time(e1) * 1e3 / steps
-        sdpa = {"us_per_step": round(sdpa_us, 3),
-                "host_us_per_call": round((h1 - h0) * 1e6 / steps, 3),
-                "backend": codec.last_score_backend,
-                "gbs": round(nbytes / (sdpa_us * 1e-6) / 1e9, 2)}
-        log(f"sunshape_sdpa end to end: {sdpa_us:.2f} us/step "
-            f"(host {sdpa['host_us_per_call']:.1f} us/call, {codec.last_score_backend})")
+        sdpa = time_api_steps(pkg, caches, q, scale, steps, args.warmup)
+        sdpa["gbs"] = round(nbytes / (sdpa["us_per_step"] * 1e-6) / 1e9, 2)
+        log(f"sunshape_sdpa end to end: {sdpa['us_per_step']:.2f} us/step "
+            f"(host {sdpa['host_us_per_step']:.1f} us/call, {sdpa['backend']})")
+        k1 = (torch.randn((b, hkv, 1, d), generator=g, device=dev) * s_t).to(torch.float16)
+        v1 = torch.randn((b, hkv, 1, d), generator=g, device=dev).to(torch.float16)
+        n_step = min(steps, 1024 * n_copies // 2)
+        step = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
+        step["t_kv_range"] = [t_kv, caches[0].offset]
+        log(f"decode step end to end (update_and_fetch of one token + sunshape_sdpa): "
+            f"{step['us_per_step']:.2f} us/step (host {step['host_us_per_step']:.1f} us/step)")
         del caches
     ceiling = stream_ceiling(nbytes, steps, args.warmup, hip)
     log(f"read ceiling: {ceiling['us_per_launch']:.2f} us ({ceiling['gbs']:.0f} GB/s)")
@@ -1042,6 +1101,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "check_max_rel_err_vs_cpu": check,
         "sdpa_end_to_end": sdpa,
+        "decode_step_end_to_end": step,
         "stream_ceiling": ceiling,
         "frac_of_stream_ceiling": round(ceiling["us_per_launch"] / (ms_step * 1e3), 4),
     }

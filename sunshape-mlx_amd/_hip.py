@@ -409,11 +409,62 @@ class PreparedDecode:
         return out
 
 
+class PreparedDecodeBuffered(PreparedDecode):
+    """:class:`PreparedDecode` of the hybrid-cache variants
+    (ss_decode_attn_il8_hybrid, ss_decode_attn_grouped_il_hybrid): a call
+    also passes the buffered tokens, ``buf_keys`` / ``buf_values`` (B, Hkv,
+    >= buf_len, D) views of the cache's buffer stores (the window moves, the
+    stores and their strides are fixed with the plan)."""
+
+    __slots__ = ("buf_code", "buf_strides")
+
+    def __init__(self, fn, pre: tuple, q: torch.Tensor, stat: str, buf_keys: torch.Tensor):
+        super().__init__(fn, pre, q, stat)
+        self.buf_code = dtype_code(buf_keys.dtype)
+        self.buf_strides = tuple(buf_keys.stride()[:3])
+
+    def __call__(self, q: torch.Tensor, t_kv: int, buf_keys: torch.Tensor,
+                 buf_values: torch.Tensor, buf_len: int, causal: bool = False, q_offset: int = 0,
+                 out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if q.shape != self.shape or q.dtype != self.dtype or not q.is_contiguous() or \
+                q.device.index != self.dev:
+            raise ValueError(f"query must be contiguous {self.dtype} {self.shape} on cuda:{self.dev}")
+        if tuple(buf_keys.stride()[:3]) != self.buf_strides or \
+                tuple(buf_values.stride()[:3]) != self.buf_strides or \
+                buf_keys.shape[2] < buf_len or buf_values.shape[2] < buf_len:
+            raise ValueError("buffer views must keep the plan's strides and hold buf_len tokens")
+        if out is None:
+            out = torch.empty(self.shape, dtype=out_dtype or self.dtype, device=q.device)
+        elif tuple(out.shape) != self.shape or not out.is_contiguous() or out.device != q.device:
+            raise ValueError(f"out must be contiguous {self.shape} on cuda:{self.dev}")
+        _poll_waits(self.dev)
+        st = stream_handle(self.dev)
+        ws = _ws_cache.get((self.dev, st))
+        if ws is None:
+            ws = decode_workspace(self.dev, 1, st)
+        mid = (int(t_kv), buf_keys.data_ptr(), buf_values.data_ptr(), self.buf_code,
+               *self.buf_strides, int(buf_len), None, None, 0, int(bool(causal)), int(q_offset),
+               out.data_ptr(), dtype_code(out.dtype))
+        rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        if rc == SS_ERR_WORKSPACE:
+            _, need = decode_plan(KIND_IL8, *self.plan_args, int(t_kv), 0)
+            ws = decode_workspace(self.dev, need, st)
+            rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        _launched(_attn_stat(self.stat, causal), rc)
+        if _check_waits:
+            check_decode_waits(self.dev)
+        return out
+
+
 def prepare_decode_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                        codebook: torch.Tensor, n_blocks: int, n_centroids: int,
-                       idx: torch.Tensor, values_il8: torch.Tensor) -> PreparedDecode:
+                       idx: torch.Tensor, values_il8: torch.Tensor,
+                       buf_keys: torch.Tensor | None = None) -> PreparedDecode:
     """:class:`PreparedDecode` of :func:`decode_attn_il8` for queries shaped
-    like ``q`` (the same checks, done once)."""
+    like ``q`` (the same checks, done once); with ``buf_keys`` (a view of a
+    hybrid cache's buffer store) the buffered variant,
+    :class:`PreparedDecodeBuffered`."""
     _check_decode_common(q, idx, None, perm)
     require_gpu(values_il8, codebook)
     b_, hq, tq, d = q.shape
@@ -426,15 +477,20 @@ def prepare_decode_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         raise ValueError("codebook does not match the centroids' shape")
     pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
            nb, n_centroids, ptr(idx), ptr(values_il8), SS_F16, cap)
+    if buf_keys is not None:
+        _buffer_args(buf_keys, buf_keys, 1, b_, hkv, d)
+        return PreparedDecodeBuffered(lib.ss_decode_attn_il8_hybrid, pre, q,
+                                      "sunshape_fused_attention_mfma", buf_keys)
     return PreparedDecode(lib.ss_decode_attn_il8, pre, q, "sunshape_fused_attention_mfma")
 
 
 def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                               codebook: torch.Tensor, n_blocks: int, n_centroids: int,
                               idx: torch.Tensor, codes_il: torch.Tensor, scales: torch.Tensor,
-                              zeros: torch.Tensor, bits: int, group_size: int) -> PreparedDecode:
-    """:class:`PreparedDecode` of :func:`decode_attn_grouped_il` (no token
-    buffer) for queries shaped like ``q``."""
+                              zeros: torch.Tensor, bits: int, group_size: int,
+                              buf_keys: torch.Tensor | None = None) -> PreparedDecode:
+    """:class:`PreparedDecode` of :func:`decode_attn_grouped_il` for queries
+    shaped like ``q``; with ``buf_keys`` the buffered variant."""
     _check_decode_common(q, idx, None, perm)
     require_gpu(codes_il, scales, zeros, codebook)
     b_, hq, tq, d = q.shape
@@ -455,6 +511,10 @@ def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
     pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
            nb, n_centroids, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros),
            dtype_code(scales.dtype), int(bits), int(group_size), cap)
+    if buf_keys is not None:
+        _buffer_args(buf_keys, buf_keys, 1, b_, hkv, d)
+        return PreparedDecodeBuffered(lib.ss_decode_attn_grouped_il_hybrid, pre, q,
+                                      "sunshape_fused_attention_dequant_mfma", buf_keys)
     return PreparedDecode(lib.ss_decode_attn_grouped_il, pre, q,
                           "sunshape_fused_attention_dequant_mfma")
 

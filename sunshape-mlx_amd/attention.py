@@ -50,10 +50,11 @@ def _transform_grouped(codec: SunShapeBlockCodec, q_grouped: torch.Tensor) -> to
 
 
 def _prepared_decode(cache, ops: dict, codec: SunShapeBlockCodec, q: torch.Tensor,
-                     kscale: float, perm):
-    """The cache's prepared matrix-core decode (``_hip.PreparedDecode``) for
-    queries shaped like ``q``: built on the first call and again whenever a
-    cache buffer, the codebook or the query layout changes (the plan holds
+                     kscale: float, perm, buffered: bool = False):
+    """The cache's prepared matrix-core decode (``_hip.PreparedDecode``, or
+    ``PreparedDecodeBuffered`` for a hybrid cache holding buffered tokens)
+    for queries shaped like ``q``: built on the first call and again whenever
+    a cache buffer, the codebook or the query layout changes (the plan holds
     weak references, so it never keeps a replaced buffer alive)."""
     kind = ops["kind"]
     cb = codec.kernel_codebook()
@@ -63,18 +64,23 @@ def _prepared_decode(cache, ops: dict, codec: SunShapeBlockCodec, q: torch.Tenso
         tensors = (ops["idx"], ops["codes_il"], ops["scales"], ops["zeros"], cb)
     if perm is not None:
         tensors += (perm,)
-    key = (kind, q.shape, q.dtype, q.device, kscale, ops.get("bits"), ops.get("group_size"))
+    if buffered:  # the buffer stores (their windows move from call to call)
+        tensors += (cache._key_buffer, cache._value_buffer)
+    key = (kind, q.shape, q.dtype, q.device, kscale, ops.get("bits"), ops.get("group_size"),
+           buffered)
     held = getattr(cache, "_decode_prepared", None)
     if held is not None and held[0] == key and len(held[1]) == len(tensors) and \
             all(r() is t for r, t in zip(held[1], tensors)):
         return held[2]
     nb, nc = codec.n_blocks, codec.n_centroids
+    bk = ops["buf_keys"] if buffered else None
     if kind == "il8":
-        plan = _hip.prepare_decode_il8(q, kscale, perm, cb, nb, nc, ops["idx"], ops["values"])
+        plan = _hip.prepare_decode_il8(q, kscale, perm, cb, nb, nc, ops["idx"], ops["values"],
+                                       buf_keys=bk)
     else:
         plan = _hip.prepare_decode_grouped_il(q, kscale, perm, cb, nb, nc, ops["idx"],
                                               ops["codes_il"], ops["scales"], ops["zeros"],
-                                              ops["bits"], ops["group_size"])
+                                              ops["bits"], ops["group_size"], buf_keys=bk)
     cache._decode_prepared = (key, tuple(weakref.ref(t) for t in tensors), plan)
     return plan
 
@@ -129,6 +135,20 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         except _hip.SunShapeUnsupported:
             return None
         codec.last_score_backend = "hip_fused_mfma" if kind == "il8" else "hip_fused_mfma_dequant"
+        return out
+    # the same with a hybrid cache's buffered tokens (the buffer window
+    # passed per call); rotated codecs hand the kernel rotated buffer copies
+    # and take the checked launch below
+    if buffered and kind in ("il8", "grouped_il") and hv["k_heavy"] is None and \
+            (codec.mode in PERM_MODES or not codec.use_rotation):
+        try:
+            plan = _prepared_decode(cache, ops, codec, q, kscale, perm, buffered=True)
+            out = plan(q, t_kv, ops["buf_keys"], ops["buf_values"], buffered, causal, q_offset,
+                       out_dtype=out_dtype)
+        except _hip.SunShapeUnsupported:
+            return None
+        codec.last_score_backend = ("hip_fused_mfma_buffer" if kind == "il8"
+                                    else "hip_fused_mfma_dequant_buffer")
         return out
     kw = dict(t_kv=t_kv, causal=causal, q_offset=q_offset, out_dtype=out_dtype)
     try:

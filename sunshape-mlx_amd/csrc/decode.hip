@@ -1940,16 +1940,38 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             pb[lane] = f32x4{p[0], p[1], p[2], p[3]};
             wave_lds_sync();
             const int nj = (int)min(bj1 - j0, (int64_t)kWave);
-            for (int jj = 0; jj < nj; ++jj) {
-                const f32x4 pj = pb[jj];
-                const int64_t vo = head + (j0 + jj) * bv.buf_st + lane;
+            // P.V over the chunk's tokens, eight at a time: their values'
+            // loads (lane-contiguous dims) are all issued before the FMAs, so
+            // the chunk waits on memory once per eight tokens, not per token
+            auto pv = [&](auto tag) {
+                using T = decltype(tag);
+                const T *vb = static_cast<const T *>(bv.vbuf);
+                for (int jb = 0; jb < nj; jb += 8) {
+                    float vv[8][DL];
 #pragma unroll
-                for (int k = 0; k < DL; ++k) {
-                    const float v = load_as_f32(bv.vbuf, bv.buf_dtype, vo + k * kWave);
+                    for (int u = 0; u < 8; ++u) {
+                        const int64_t vo = head + (j0 + min(jb + u, nj - 1)) * bv.buf_st + lane;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) ba[r][k] = fmaf(pj[r], v, ba[r][k]);
+                        for (int k = 0; k < DL; ++k) vv[u][k] = to_f32(vb[vo + k * kWave]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        if (jb + u < nj) {
+                            const f32x4 pj = pb[jb + u];
+#pragma unroll
+                            for (int k = 0; k < DL; ++k)
+#pragma unroll
+                                for (int r = 0; r < R; ++r) ba[r][k] = fmaf(pj[r], vv[u][k], ba[r][k]);
+                        }
+                    }
                 }
-            }
+            };
+            if (bv.buf_dtype == SS_F16)
+                pv(__half{});
+            else if (bv.buf_dtype == SS_BF16)
+                pv(__hip_bfloat16{});
+            else
+                pv(float{});
             wave_lds_sync();
         }
         // the query copy is no longer read: the partial takes its place

@@ -247,14 +247,14 @@ __global__ void __launch_bounds__(kEncThreads) append_kv_small_kernel(EncodeArgs
 //                          full-precision buffer at buffer position put_pos;
 //   [n_put, n_put + n_enc): a wave per (flushed token, block) encodes the
 //                          oldest buffered keys (exact_block_wave);
-//   the rest:              a thread per (interleaved code word, dim) of the
-//                          flushed range quantises its tokens' values with the
-//                          grouped min/max rule of quantize_grouped_kernel
+//   the rest:              a wave per (head, interleaved code-word row) of
+//                          the flushed range quantises its tokens' values with
+//                          the grouped min/max rule of quantize_grouped_kernel
 //                          (values.hip; the same IEEE steps, so codes and
-//                          scale/zero are identical) and rewrites the word,
-//                          keeping the bits of tokens outside the range; the
-//                          thread of a group's first dim stores that token's
-//                          scale and zero.
+//                          scale/zero are identical), lane l owning dims
+//                          l*d/64 .., and rewrites its words, keeping the bits
+//                          of tokens outside the range; a group's first lane
+//                          stores that token's scale and zero.
 // The flushed buffer range and the stored range are disjoint (checked on
 // the host), so no workgroup reads what another writes.
 struct HybridGroupedStep {
@@ -315,44 +315,53 @@ __global__ void __launch_bounds__(kEncThreads)
         if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
         return;
     }
-    // values: thread (bh, word row, dim)
-    const int64_t e = (int64_t)(blockIdx.x - n_put - n_enc) * kEncThreads + threadIdx.x;
-    if (e >= n_bh * s.n_blk * s.d) return;
-    const int64_t bh = e / (s.n_blk * s.d), rem = e - bh * s.n_blk * s.d;
-    const int64_t blk = s.blk0 + rem / s.d;
-    const int dd = (int)(rem % s.d);
+    // values: a wave per (bh, code-word row) of the flushed range; lane l
+    // owns dims l * dpl .. + dpl - 1 (dpl = d / 64), so a token's group
+    // min / max is a reduction over the group's aligned lanes and each
+    // token costs one load per lane
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t job = (int64_t)(blockIdx.x - n_put - n_enc) * (kEncThreads / kWave) +
+                        (threadIdx.x >> 6);
+    if (job >= n_bh * s.n_blk) return;  // wave-uniform
+    const int64_t bh = job / s.n_blk;
+    const int64_t blk = s.blk0 + (job - bh * s.n_blk);
+    const int dpl = s.d / kWave;         // 1 or 2 (checked on the host)
+    const int glanes = s.group / dpl;    // lanes of one group: 32 or 64
     const int vpw = 32 / s.bits;
     const uint32_t mask = (1u << s.bits) - 1u;
     const float maxv = (float)((1 << s.bits) - 1);
-    const int g = dd / s.group, n_groups = s.d / s.group;
-    uint32_t *wp = s.codes_il + (bh * (s.cap / vpw) + blk) * s.d + dd;
-    uint32_t word = *wp;
+    const int n_groups = s.d / s.group;
+    uint32_t *wp = s.codes_il + (bh * (s.cap / vpw) + blk) * s.d + lane * dpl;
+    uint32_t word[2] = {wp[0], dpl > 1 ? wp[1] : 0u};
     for (int i = 0; i < vpw; ++i) {
         const int64_t t = blk * vpw + i - s.offset;  // flushed token of this slot
-        if (t < 0 || t >= s.n_flush) continue;
-        const int64_t vin = (bh * s.buf_cap + s.flush_pos + t) * s.d;
-        float mn = INFINITY, mx = -INFINITY;
-        for (int k = 0; k < s.group; ++k) {
-            const float v = load_as_f32(s.buf_values, s.buf_dtype, vin + g * s.group + k);
-            mn = fminf(mn, v);
-            mx = fmaxf(mx, v);
+        if (t < 0 || t >= s.n_flush) continue;       // wave-uniform
+        const int64_t vin = (bh * s.buf_cap + s.flush_pos + t) * s.d + lane * dpl;
+        float x[2];
+        x[0] = load_as_f32(s.buf_values, s.buf_dtype, vin);
+        x[1] = dpl > 1 ? load_as_f32(s.buf_values, s.buf_dtype, vin + 1) : x[0];
+        float mn = fminf(x[0], x[1]), mx = fmaxf(x[0], x[1]);
+        for (int o = glanes / 2; o > 0; o >>= 1) {
+            mn = fminf(mn, __shfl_xor(mn, o));
+            mx = fmaxf(mx, __shfl_xor(mx, o));
         }
         float sc = __fdiv_rn(__fsub_rn(mx, mn), maxv);
         if (sc < 1e-8f) sc = 1e-8f;
-        const float v = load_as_f32(s.buf_values, s.buf_dtype, vin + dd);
-        float qf = rintf(__fdiv_rn(__fsub_rn(v, mn), sc));
-        qf = fminf(fmaxf(qf, 0.f), maxv);
-        const uint32_t code = (uint32_t)qf & mask;
         // token i of the word: bits*(i/2) in the low half for even i, +16 for odd i
         const int pos = s.bits * (i >> 1) + 16 * (i & 1);
-        word = (word & ~(mask << pos)) | (code << pos);
-        if (dd == g * s.group) {
-            const int64_t srow = (bh * s.cap + s.offset + t) * n_groups + g;
+        for (int k = 0; k < dpl; ++k) {
+            float qf = rintf(__fdiv_rn(__fsub_rn(x[k], mn), sc));
+            qf = fminf(fmaxf(qf, 0.f), maxv);
+            word[k] = (word[k] & ~(mask << pos)) | (((uint32_t)qf & mask) << pos);
+        }
+        if (lane % glanes == 0) {
+            const int64_t srow = (bh * s.cap + s.offset + t) * n_groups + lane / glanes;
             store_from_f32(s.scales, s.sz_dtype, srow, sc);
             store_from_f32(s.zeros, s.sz_dtype, srow, mn);
         }
     }
-    *wp = word;
+    wp[0] = word[0];
+    if (dpl > 1) wp[1] = word[1];
 }
 
 // ---- bulk on the matrix cores (block_dim 8): a bounded filter, then exact ties ----
@@ -481,9 +490,6 @@ __global__ void __launch_bounds__(256) encode_codebook_kernel(const float *cents
     if (c == 0) sig[nb + b] = red[0];
 }
 
-__device__ __forceinline__ float to_f32(float v) { return v; }
-__device__ __forceinline__ float to_f32(__half v) { return __half2float(v); }
-__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
 // a key element from its LDS-DMA dword slot (2-byte types in the low half)
 template <class KT>
 __device__ __forceinline__ float slot_f32(uint32_t w) {
@@ -969,8 +975,10 @@ extern "C" int ss_hybrid_append_grouped_il(
     SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256, "n_centroids %d unsupported (1..256)",
                    n_centroids);
     SS_UNSUPPORTED(bits == 2 || bits == 4, "interleaved codes are 2- or 4-bit");
-    SS_REQUIRE(group_size >= 1 && head_dim % group_size == 0, "head_dim %d not divisible by %d",
-               head_dim, group_size);
+    SS_UNSUPPORTED((head_dim == 64 || head_dim == 128) &&
+                       (group_size == head_dim || 2 * group_size == head_dim),
+                   "head_dim %d with group_size %d unsupported (64 or 128, group head_dim or "
+                   "half of it)", head_dim, group_size);
     SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_new >= 0 && n_flush >= 0, "negative sizes");
     SS_REQUIRE(put_pos >= 0 && put_pos + n_new <= buf_cap && flush_pos >= 0 &&
                    flush_pos + n_flush <= buf_cap,
@@ -1003,7 +1011,7 @@ extern "C" int ss_hybrid_append_grouped_il(
     const int n_put = (int)((2 * n_bh * n_new * head_dim + kEncThreads - 1) / kEncThreads);
     const int per = kEncThreads / kWave;
     const int n_enc = (int)((n_bh * n_flush * n_blocks + per - 1) / per);
-    const int64_t n_val = (n_bh * hs.n_blk * head_dim + kEncThreads - 1) / kEncThreads;
+    const int64_t n_val = (n_bh * hs.n_blk + per - 1) / per;  // a wave per (bh, word row)
     SS_UNSUPPORTED(n_put + n_enc + n_val < (1LL << 31), "step too large for one launch");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     hipLaunchKernelGGL(hybrid_grouped_step_kernel<8>, dim3((unsigned)(n_put + n_enc + n_val)),

@@ -50,6 +50,10 @@ __device__ __forceinline__ float load_as_f32(const void *p, int dt, int64_t i) {
     return __bfloat162float(reinterpret_cast<const __hip_bfloat16 *>(p)[i]);
 }
 
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__half x) { return __half2float(x); }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 x) { return __bfloat162float(x); }
+
 // Round a float32 to the precision of dtype dt (identity for float32).
 __device__ __forceinline__ float round_to(int dt, float x) {
     if (dt == SS_F16) return __half2float(__float2half(x));
