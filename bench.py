@@ -59,14 +59,16 @@ def parse_args():
                         "(default: keep them in fp16 and score them exactly)")
     p.add_argument("--t-q", type=int, default=4096, help="prefill: prompt tokens")
     p.add_argument("--workload", choices=("metric", "hybrid", "encode", "turboquant", "config5",
-                                          "fit", "prefill"),
+                                          "fit", "prefill", "scores"),
                    default="metric",
                    help="metric: the headline metric decode (fp16 values, B=1); hybrid: config 4 "
                         "(B=8, 2-bit grouped values, g=64, fp16 scale/zero); encode: config 3 "
                         "(65,536 fp16 keys block-VQ encoded); turboquant: the config-4 shape "
                         "with 2-bit TurboQuant values; config5: 28 layers x B=16, "
                         "T_kv=131072, mixed-precision keys, SunShape values; prefill: one "
-                        "causal prompt of --t-q tokens against its own cache")
+                        "causal prompt of --t-q tokens against its own cache; scores: the "
+                        "score-only path (LUT + one gather over all heads) at the config-4 "
+                        "shape")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                    help="only run a plain device copy of MB megabytes --steps times (the "
                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -673,6 +675,84 @@ def run_config5(args) -> int:
     return 0
 
 
+def run_scores(args) -> int:
+    """The score-only path (attention_scores, the two-pass fallback's
+    compressed scores, attention.py:44-73 / codec.py:575-637) at the config-4
+    shape: B=8, 32 query / 8 KV heads (4 query rows per KV head), T=32768,
+    16 uint8 indices per token.  One LUT build for all 256 rows, then one
+    score-gather launch over every (batch, KV head); the gather is the
+    HBM-bound kernel (indices in, 4 fp32 scores per token out)."""
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    hip = pkg._hip
+    lib = hip.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b, hq, hkv, d, t_kv, nb, nc = 8, 32, 8, 128, args.t_kv, 16, 256
+    rows = hq // hkv
+    g = torch.Generator(device=dev).manual_seed(8)
+    cents = torch.randn((nb, nc, 8), generator=g, device=dev)
+    perm = torch.randperm(d, generator=g, device=dev).to(torch.int32)
+    q = torch.randn((b * hq, d), generator=g, device=dev).to(torch.float16)
+    per_copy = b * hkv * t_kv * (nb + rows * 4)
+    n_copies = args.copies or max(2, math.ceil(3 * MALL_BYTES / per_copy))
+    idxs = [torch.randint(0, nc, (b, hkv, t_kv, nb), generator=g, device=dev).to(torch.uint8)
+            for _ in range(n_copies)]
+    outs = [torch.empty((b, hkv, rows, t_kv), dtype=torch.float32, device=dev)
+            for _ in range(n_copies)]
+    lut = hip.build_lut(q, perm, 1.0 / math.sqrt(d), cents).reshape(b, hkv, rows, nb, nc)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream().cuda_stream
+    fn = lib.ss_score_gather_heads
+    argv = [(lut.data_ptr(), rows, nb, nc, ix.data_ptr(), b, hkv, ix.stride(0), ix.stride(1),
+             ix.stride(2), t_kv, o.data_ptr(), stream) for ix, o in zip(idxs, outs)]
+    us, per = time_launches(fn, argv, args.steps, args.warmup, hip)
+    nbytes = b * hkv * t_kv * nb + b * hkv * rows * t_kv * 4 + b * hkv * rows * nb * nc * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"score gather: {us:.2f} us/launch, {gbs:.1f} GB/s ({n_copies} copies)")
+    # the whole score call as the two-pass path makes it (LUT build + gather)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(args.steps):
+        lt = hip.build_lut(q, perm, 1.0 / math.sqrt(d), cents).reshape(b, hkv, rows, nb, nc)
+        hip.score_gather_heads(lt, idxs[i % n_copies])
+    e1.record()
+    torch.cuda.synchronize()
+    whole = e0.elapsed_time(e1) * 1e3 / args.steps
+    check = None
+    if args.cpu_seconds > 0:  # one head against the oracle's gather
+        from oracle import sunshape_oracle as O
+
+        hip.check(fn(*argv[0]))
+        torch.cuda.synchronize()
+        ref = O.gather_scores(lut[3, 5].cpu().numpy(), idxs[0][3, 5].cpu().numpy())
+        got = outs[0][3, 5].cpu().numpy()
+        check = float(np.abs(got - ref).max() / np.abs(ref).max())
+    line = {
+        "metric": "compressed score gather µs/launch and achieved HBM GB/s (config-4 shape)",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us * 1e-3, 6), "us_per_step": round(us, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"score gather B=8 Hkv=8 rows=4 per KV head T={t_kv}, u8 indices "
+                               "(16 blocks x 256 centroids), f32 scores; one launch over all "
+                               "heads", "t_kv": t_kv, "cache_copies": n_copies,
+                   "algorithmic_bytes_per_launch": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "per_launch_us": {"mean": round(float(np.mean(per)), 3),
+                          "median": round(float(np.median(per)), 3)},
+        "lut_plus_gather_us": round(whole, 3),
+        "check_max_rel_err_vs_oracle": check,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def run_fit(args) -> int:
     """Codec fit of config 1 (seed 42: q_cal (1024, 128) and k_cal (2048, 128)
     N(0,1), profileperm_baseline, 15 k-means iterations): the per-block
@@ -849,6 +929,8 @@ def main() -> int:
         return run_encode(args)
     if args.workload == "prefill":
         return run_prefill(args)
+    if args.workload == "scores":
+        return run_scores(args)
 
     import numpy as np
     import torch

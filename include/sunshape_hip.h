@@ -125,6 +125,19 @@ int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centro
                     float *scores, int64_t out_row_stride, void *stream);
 
 /*
+ * The same gather for every (batch, KV head) pair in one launch (the
+ * reference loops over them with one dispatch each, attention.py:44-73,
+ * 268-305): head (b, h) uses lut[b][h] [n_rows][n_blocks][n_centroids]
+ * (float32, contiguous over all heads) and the indices of token t at
+ * idx[b*idx_sb + h*idx_sh + t*idx_st] (bytes; a cache's [B][H][cap][NB]
+ * buffer read up to n_tok), and writes scores[b][h] [n_rows][n_tok].
+ */
+int ss_score_gather_heads(const float *lut, int64_t n_rows, int n_blocks, int n_centroids,
+                          const uint8_t *idx, int64_t n_b, int64_t n_h, int64_t idx_sb,
+                          int64_t idx_sh, int64_t idx_st, int64_t n_tok, float *scores,
+                          void *stream);
+
+/*
  * Workspace bytes needed by ss_decode_attn_* for the given shape and split
  * count (n_splits <= 0 selects the library's choice for the current device);
  * 0 when a single split suffices.  With more than one split the split
@@ -326,8 +339,12 @@ int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads
  *  - A shape whose split scratch exceeds the static array returns
  *    SS_ERR_WORKSPACE (pass fewer splits, or use ss_decode_attn_il8).
  *  - The first call on a device looks the array up and clears its counter
- *    area with a fill kernel on `stream`; every completed call leaves the
- *    counters zero again.
+ *    area with a fill kernel on `stream`, and the first call of a kernel
+ *    variant sets its dynamic-LDS attribute; every completed call leaves the
+ *    counters zero again.  Under HIP graph capture that set-up would only
+ *    run at replay (and the attribute call may be refused), so make one
+ *    eager call with the shape's query dtype before capturing; captured
+ *    calls then record the decode kernel alone and replay unchanged.
  *  - All calls on one GPU share the array: calls that overlap in time on
  *    the same GPU (different streams or threads) race and give undefined
  *    results.

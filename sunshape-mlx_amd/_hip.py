@@ -70,6 +70,8 @@ _SIGNATURES = {
                             _int, _int, _int, _c_void_p, _c_void_p]),
     "ss_score_gather": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _i64, _i64, _c_void_p,
                                _i64, _c_void_p]),
+    "ss_score_gather_heads": (_int, [_c_void_p, _i64, _int, _int, _c_void_p, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _c_void_p, _c_void_p]),
     "ss_decode_workspace_bytes": (_size, [_i64, _int, _int, _i64, _int, _i64, _int]),
     "ss_decode_wait_failures": (_int, [_c_void_p, _int, ctypes.POINTER(ctypes.c_uint)]),
     "ss_decode_wait_flag_host": (_int, [ctypes.POINTER(ctypes.POINTER(ctypes.c_uint))]),
@@ -609,6 +611,24 @@ def score_gather(lut: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     _launched("sunshape_block_vq_score_hip", load_library().ss_score_gather(
         ptr(lut), r_, nb, nc, ptr(idx), idx.shape[0], idx.stride(0), ptr(scores), idx.shape[0],
         stream_handle(lut.device)))
+    return scores
+
+
+def score_gather_heads(lut: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """lut (B, H, R, NB, NC) f32, idx (B, H, T, NB) uint8 (a strided view of a
+    cache is fine) -> scores (B, H, R, T) f32, one launch for every head."""
+    require_gpu(lut, idx)
+    if idx.dtype != torch.uint8 or idx.dim() != 4 or idx.stride(-1) != 1:
+        raise ValueError("indices must be uint8 (B, H, T, n_blocks) with unit last stride")
+    lut = lut.contiguous().float()
+    b_, h_, r_, nb, nc = lut.shape
+    if tuple(idx.shape[:2]) != (b_, h_) or idx.shape[3] != nb:
+        raise ValueError("lut and indices disagree on (B, H, n_blocks)")
+    t_ = idx.shape[2]
+    scores = torch.empty((b_, h_, r_, t_), dtype=torch.float32, device=lut.device)
+    _launched("sunshape_block_vq_score_hip", load_library().ss_score_gather_heads(
+        ptr(lut), r_, nb, nc, ptr(idx), b_, h_, idx.stride(0), idx.stride(1), idx.stride(2), t_,
+        ptr(scores), stream_handle(lut.device)))
     return scores
 
 

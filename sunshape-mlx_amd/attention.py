@@ -211,8 +211,8 @@ def _compressed_scores(codec: SunShapeBlockCodec, q_t: torch.Tensor,
                        key_indices: torch.Tensor) -> torch.Tensor:
     """(B, Hkv, rep, Tq, Tc) float32 scores of codec-space queries q_t
     (B, Hkv, rep, Tq, D) against (B, Hkv, Tc, NB) indices
-    (attention.py:44-73): one HIP LUT build for all rows, one gather per
-    (batch, KV head).  Fp16 heavy blocks add nothing here (their exact dot
+    (attention.py:44-73): one HIP LUT build for all rows and one gather
+    launch over every (batch, KV head).  Fp16 heavy blocks add nothing here (their exact dot
     products are added by the caller)."""
     b_, hkv, rep, tq, d = q_t.shape
     rows = q_t.reshape(-1, d)
@@ -221,10 +221,7 @@ def _compressed_scores(codec: SunShapeBlockCodec, q_t: torch.Tensor,
     lut = _hip.build_lut(rows.contiguous(), None, 1.0, codec.scoring_centroids())
     lut = lut.reshape(b_, hkv, rep * tq, codec.n_blocks, codec.n_centroids)
     tc = key_indices.shape[2]
-    scores = torch.empty((b_, hkv, rep * tq, tc), dtype=torch.float32, device=q_t.device)
-    for b in range(b_):
-        for h in range(hkv):
-            scores[b, h] = _hip.score_gather(lut[b, h], key_indices[b, h])
+    scores = _hip.score_gather_heads(lut, key_indices)  # every (batch, KV head) in one launch
     codec.last_score_backend = "hip"
     return scores.reshape(b_, hkv, rep, tq, tc)
 

@@ -32,27 +32,130 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// grid (ceil(T/256), ceil(n_rows/rows_per_wg)); the WG's LUT rows live in LDS.
+// grid (ceil(T/256), n_heads * n_rgrp): workgroup (x, y) scores tokens
+// 256x .. 256x + 255 of head y / n_rgrp (a (batch, KV head) pair) for its
+// query rows (y % n_rgrp) * rows_per_wg ..; those rows' LUTs live in LDS.  A
+// token's 16-block index row is one 16-byte load when rows are 16-byte
+// aligned, else one byte per block.
 __global__ void __launch_bounds__(256)
-    score_gather_kernel(const float *lut, int64_t n_rows, int rows_per_wg, int n_blocks,
-                        int n_centroids, const uint8_t *idx, int64_t n_tok,
-                        int64_t idx_row_stride, float *scores, int64_t out_row_stride) {
+    score_gather_kernel(const float *lut, int64_t lut_head_stride, int64_t n_rows,
+                        int rows_per_wg, int n_rgrp, int n_blocks, int n_centroids,
+                        const uint8_t *idx, int64_t n_h, int64_t idx_sb, int64_t idx_sh,
+                        int64_t idx_st, int64_t n_tok, float *scores, int64_t out_head_stride,
+                        int64_t out_row_stride, int rows16) {
     extern __shared__ float tab[];  // [rows_per_wg][n_blocks][n_centroids]
-    const int64_t r0 = (int64_t)blockIdx.y * rows_per_wg;
+    const int64_t head = blockIdx.y / n_rgrp;
+    const int64_t r0 = (int64_t)(blockIdx.y % n_rgrp) * rows_per_wg;
     const int nr = (int)min((int64_t)rows_per_wg, n_rows - r0);
     const int per_row = n_blocks * n_centroids;
-    for (int i = threadIdx.x; i < nr * per_row; i += blockDim.x)
-        tab[i] = lut[r0 * per_row + i];
+    const float *lh = lut + head * lut_head_stride + r0 * per_row;
+    for (int i = threadIdx.x; i < nr * per_row; i += blockDim.x) tab[i] = lh[i];
     __syncthreads();
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_tok) return;
-    const uint8_t *ip = idx + t * idx_row_stride;
+    const int64_t b = head / n_h, h = head - b * n_h;
+    const uint8_t *ip = idx + b * idx_sb + h * idx_sh + t * idx_st;
+    uint32_t code[16];
+    if (rows16) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(ip);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int b2 = 0; b2 < 16; ++b2) code[b2] = (ws[b2 >> 2] >> (8 * (b2 & 3))) & 0xffu;
+    }
+    float *out = scores + head * out_head_stride + t;
     for (int r = 0; r < nr; ++r) {
         const float *tr = tab + r * per_row;
         float s = 0.f;
-        for (int b = 0; b < n_blocks; ++b)
-            s += tr[b * n_centroids + min((int)ip[b], n_centroids - 1)];
-        scores[(r0 + r) * out_row_stride + t] = s;
+        if (rows16) {
+#pragma unroll
+            for (int b2 = 0; b2 < 16; ++b2) s += tr[b2 * n_centroids + min((int)code[b2], n_centroids - 1)];
+        } else {
+            for (int b2 = 0; b2 < n_blocks; ++b2)
+                s += tr[b2 * n_centroids + min((int)ip[b2], n_centroids - 1)];
+        }
+        out[(r0 + r) * out_row_stride] = s;
+    }
+}
+
+// The same for codecs of at most 16 blocks, four query rows per row group:
+// the group's LUT sits in LDS as a float4 (its four rows) per (block,
+// centroid), so a token's scores for all four rows take one 16-byte LDS
+// gather per block; a workgroup scores kGatherTokens tokens so its 64 KB
+// LUT copy is amortised over them.
+constexpr int kGatherTokens = 4096;
+constexpr int kGatherThreads = 512;
+
+__global__ void __launch_bounds__(kGatherThreads)
+    score_gather4_kernel(const float *lut, int64_t lut_head_stride, int64_t n_rows, int n_rgrp,
+                         int n_blocks, int n_centroids, const uint8_t *idx, int64_t n_h,
+                         int64_t idx_sb, int64_t idx_sh, int64_t idx_st, int64_t n_tok,
+                         float *scores, int64_t out_head_stride, int64_t out_row_stride,
+                         int rows16) {
+    extern __shared__ float4 tab4[];  // [n_blocks][256] float4
+    const int64_t head = blockIdx.y / n_rgrp;
+    const int64_t r0 = (int64_t)(blockIdx.y % n_rgrp) * 4;
+    const int nr = (int)min((int64_t)4, n_rows - r0);
+    const int per_row = n_blocks * n_centroids;
+    const float *lh = lut + head * lut_head_stride + r0 * per_row;
+    if (n_centroids == 256) {
+        // four centroids of each row per thread (16-byte loads), transposed
+        // into four float4 entries in registers
+        for (int i = threadIdx.x; i < n_blocks * 64; i += blockDim.x) {
+            const int b = i >> 6, c4 = (i & 63) * 4;
+            float4 v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                v[r] = r < nr ? *reinterpret_cast<const float4 *>(lh + r * per_row + b * 256 + c4)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            tab4[b * 256 + c4 + 0] = make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+            tab4[b * 256 + c4 + 1] = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
+            tab4[b * 256 + c4 + 2] = make_float4(v[0].z, v[1].z, v[2].z, v[3].z);
+            tab4[b * 256 + c4 + 3] = make_float4(v[0].w, v[1].w, v[2].w, v[3].w);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n_blocks * 256; i += blockDim.x) {
+            const int b = i >> 8, c = i & 255;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (c < n_centroids)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (r < nr) v[r] = lh[r * per_row + b * n_centroids + c];
+            tab4[i] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    __syncthreads();
+    const int64_t b0 = head / n_h, h0 = head - b0 * n_h;
+    const uint8_t *ih = idx + b0 * idx_sb + h0 * idx_sh;
+    float *out = scores + head * out_head_stride + r0 * out_row_stride;
+    const int64_t t_end = min(n_tok, (int64_t)(blockIdx.x + 1) * kGatherTokens);
+    for (int64_t t = (int64_t)blockIdx.x * kGatherTokens + threadIdx.x; t < t_end; t += blockDim.x) {
+        const uint8_t *ip = ih + t * idx_st;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rows16) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(ip);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int c = min((int)((ws[b >> 2] >> (8 * (b & 3))) & 0xffu), n_centroids - 1);
+                const float4 e = tab4[b * 256 + c];
+                acc.x += e.x;
+                acc.y += e.y;
+                acc.z += e.z;
+                acc.w += e.w;
+            }
+        } else {
+            for (int b = 0; b < n_blocks; ++b) {
+                const float4 e = tab4[b * 256 + min((int)ip[b], n_centroids - 1)];
+                acc.x += e.x;
+                acc.y += e.y;
+                acc.z += e.z;
+                acc.w += e.w;
+            }
+        }
+        const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (r < nr) out[r * out_row_stride + t] = a4[r];
     }
 }
 
@@ -97,27 +200,68 @@ extern "C" int ss_build_lut(const void *q, int q_dtype, int64_t n_rows, int64_t 
     return SS_OK;
 }
 
-extern "C" int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centroids,
-                               const uint8_t *idx, int64_t n_tok, int64_t idx_row_stride,
-                               float *scores, int64_t out_row_stride, void *stream) {
-    SS_REQUIRE(n_rows >= 0 && n_tok >= 0, "negative sizes");
+static int score_gather_impl(const float *lut, int64_t lut_head_stride, int64_t n_rows,
+                             int n_blocks, int n_centroids, const uint8_t *idx, int64_t n_b,
+                             int64_t n_h, int64_t idx_sb, int64_t idx_sh, int64_t idx_st,
+                             int64_t n_tok, float *scores, int64_t out_head_stride,
+                             int64_t out_row_stride, void *stream) {
+    SS_REQUIRE(n_rows >= 0 && n_tok >= 0 && n_b >= 0 && n_h >= 0, "negative sizes");
     SS_REQUIRE(n_blocks >= 1 && n_centroids >= 1 && n_centroids <= 256,
                "n_centroids must be 1..256 for uint8 indices");
-    if (n_rows == 0 || n_tok == 0) return SS_OK;
+    if (n_rows == 0 || n_tok == 0 || n_b * n_h == 0) return SS_OK;
     SS_REQUIRE(lut && idx && scores, "null pointer argument");
     const int per_row = n_blocks * n_centroids;
     SS_UNSUPPORTED(per_row <= 16384, "n_blocks * n_centroids %d > 16384", per_row);
     int rpw = 16384 / per_row;
     if (rpw > 4) rpw = 4;
-    const int64_t ry = (n_rows + rpw - 1) / rpw;
-    SS_REQUIRE(ry <= 65535, "too many rows for one launch");
+    const int64_t n_rgrp = (n_rows + rpw - 1) / rpw;
+    const int64_t ry = n_b * n_h * n_rgrp;
+    SS_UNSUPPORTED(ry <= 65535, "too many (head, row group) pairs for one launch");
+    const int rows16 = n_blocks == 16 && ((uintptr_t)idx % 16) == 0 && idx_sb % 16 == 0 &&
+                       idx_sh % 16 == 0 && idx_st % 16 == 0;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (n_blocks <= 16) {  // float4 LUT of four rows, many tokens per workgroup
+        const int64_t n_rg4 = (n_rows + 3) / 4;
+        const int64_t ry4 = n_b * n_h * n_rg4;
+        SS_UNSUPPORTED(ry4 <= 65535, "too many (head, row group) pairs for one launch");
+        dim3 grid4((unsigned)((n_tok + kGatherTokens - 1) / kGatherTokens), (unsigned)ry4);
+        const size_t lds4 = sizeof(float4) * n_blocks * 256;
+        if (lds4 > 65536) {
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(score_gather4_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)lds4);
+            if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(score gather)");
+        }
+        hipLaunchKernelGGL(score_gather4_kernel, grid4, dim3(kGatherThreads), lds4, st, lut,
+                           lut_head_stride,
+                           n_rows, (int)n_rg4, n_blocks, n_centroids, idx, n_h, idx_sb, idx_sh,
+                           idx_st, n_tok, scores, out_head_stride, out_row_stride, rows16);
+        SS_LAUNCH_CHECK("score_gather4_kernel launch");
+        return SS_OK;
+    }
     dim3 grid((unsigned)((n_tok + 255) / 256), (unsigned)ry);
     const size_t lds = sizeof(float) * rpw * per_row;
-    hipLaunchKernelGGL(score_gather_kernel, grid, dim3(256), lds, st, lut, n_rows, rpw, n_blocks,
-                       n_centroids, idx, n_tok, idx_row_stride, scores, out_row_stride);
+    hipLaunchKernelGGL(score_gather_kernel, grid, dim3(256), lds, st, lut, lut_head_stride, n_rows,
+                       rpw, (int)n_rgrp, n_blocks, n_centroids, idx, n_h, idx_sb, idx_sh, idx_st,
+                       n_tok, scores, out_head_stride, out_row_stride, rows16);
     SS_LAUNCH_CHECK("score_gather_kernel launch");
     return SS_OK;
+}
+
+extern "C" int ss_score_gather(const float *lut, int64_t n_rows, int n_blocks, int n_centroids,
+                               const uint8_t *idx, int64_t n_tok, int64_t idx_row_stride,
+                               float *scores, int64_t out_row_stride, void *stream) {
+    return score_gather_impl(lut, 0, n_rows, n_blocks, n_centroids, idx, 1, 1, 0, 0,
+                             idx_row_stride, n_tok, scores, 0, out_row_stride, stream);
+}
+
+extern "C" int ss_score_gather_heads(const float *lut, int64_t n_rows, int n_blocks,
+                                     int n_centroids, const uint8_t *idx, int64_t n_b,
+                                     int64_t n_h, int64_t idx_sb, int64_t idx_sh, int64_t idx_st,
+                                     int64_t n_tok, float *scores, void *stream) {
+    const int64_t per_row = (int64_t)n_blocks * n_centroids;
+    return score_gather_impl(lut, n_rows * per_row, n_rows, n_blocks, n_centroids, idx, n_b, n_h,
+                             idx_sb, idx_sh, idx_st, n_tok, scores, n_rows * n_tok, n_tok, stream);
 }
 
 extern "C" int ss_dequantize_blockvq(const uint8_t *idx, int64_t n_tok, int64_t idx_row_stride,

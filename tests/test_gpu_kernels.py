@@ -1265,3 +1265,26 @@ def test_queries_beyond_fp16_range_prefill_and_decode(e2):
         assert np.isfinite(got).all() and rel_err(got, ref) <= REL_TOL, qdt
         gd = dec.cpu().numpy()
         assert np.isfinite(gd).all() and rel_err(gd, ref[:, :, -4:]) <= REL_TOL, qdt
+
+
+def test_score_gather_heads_matches_per_head_and_oracle():
+    """ss_score_gather_heads: every (batch, KV head) of a cache-shaped,
+    strided index view in one launch -- bit-identical to the per-head
+    ss_score_gather (same sums in the same order), and the oracle's gather
+    within float32 rounding; also rows not a multiple of the row group and
+    a codebook of 100 centroids (the byte-wise index path)."""
+    rng = np.random.default_rng(91)
+    for (b, hkv, rows, t_kv, cap, nb, nc) in ((2, 3, 4, 1000, 1024, 16, 256),
+                                               (1, 2, 7, 333, 512, 16, 100),
+                                               (2, 2, 3, 200, 256, 8, 256)):
+        lut = t(rng.standard_normal((b, hkv, rows, nb, nc)).astype(np.float32))
+        idx_full = t(rng.integers(0, nc, (b, hkv, cap, nb)).astype(np.uint8))
+        idx = idx_full[:, :, :t_kv]
+        got = _hip.score_gather_heads(lut, idx)
+        for bi in range(b):
+            for h in range(hkv):
+                one = _hip.score_gather(lut[bi, h], idx[bi, h])
+                assert torch.equal(got[bi, h], one)
+        ref = np.stack([np.stack([O.gather_scores(lut[bi, h].cpu().numpy(), idx[bi, h].cpu().numpy())
+                                  for h in range(hkv)]) for bi in range(b)])
+        assert np.abs(got.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
