@@ -329,6 +329,29 @@ int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads
                         void *out, int out_dtype, void *stream);
 
 /*
+ * ss_prefill_attn_il8 over a hybrid cache: keys at positions 0 .. t_raw0 - 1
+ * are indices (idx, capacity cap), keys at t_raw0 .. t_kv - 1 (its buffered
+ * full-precision tokens) are given whole in kraw [batch][n_kv_heads]
+ * [t_kv - t_raw0][2][128] fp16: per token its key in the codec's basis (the
+ * permutation applied, or the rotation), times 2^-s (row 0) and the
+ * remainder times 2^11 (row 1), with kfac[...][token] = 2^s (float32), s
+ * chosen per token so both rows hold the key exactly (fp16 or bf16 keys)
+ * or to 22 bits (float32 keys).  values_il8 [batch][n_kv_heads][cap_v/8]
+ * [128][8] holds the values of all t_kv tokens.  Replaces the reference's
+ * two-pass path for prompts against a cache with buffered tokens
+ * (attention.py:307-350, keys scored against the unpermuted query at
+ * attention.py:318-321; the result is the same as scoring the whole key in
+ * the codec's basis).  fp16 and bf16 queries only.
+ */
+int ss_prefill_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                               int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                               const int32_t *perm, const void *codebook, int n_blocks,
+                               int n_centroids, const uint8_t *idx, int64_t cap,
+                               const void *values_il8, int64_t cap_v, int64_t t_kv,
+                               const void *kraw, const float *kfac, int64_t t_raw0, int causal,
+                               int64_t q_offset, void *out, int out_dtype, void *stream);
+
+/*
  * ss_decode_attn_il8 without a workspace: the same kernel, arguments and
  * result, with its split partials and per-column split counters in a static
  * device array of the library (ss_decode_static_scratch_bytes() = 4 MiB,

@@ -97,6 +97,10 @@ _SIGNATURES = {
     "ss_prefill_attn_il8": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                    _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
                                    _i64, _i64, _int, _i64, _c_void_p, _int, _c_void_p]),
+    "ss_prefill_attn_il8_hybrid": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
+                                          _c_void_p, _c_void_p, _int, _int, _c_void_p, _i64,
+                                          _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64,
+                                          _int, _i64, _c_void_p, _int, _c_void_p]),
     "ss_decode_attn_il8_noalloc": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                           _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                           _int, _i64, _i64, _int, _i64, _c_void_p, _int, _int,
@@ -823,6 +827,59 @@ def prefill_attn_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
         int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype),
         stream_handle(q.device)))
     return out
+
+
+def prefill_attn_il8_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                            codebook: torch.Tensor, n_centroids: int, idx: torch.Tensor,
+                            values_il8: torch.Tensor, t_kv: int, kraw: torch.Tensor,
+                            kfac: torch.Tensor, t_raw0: int, causal: bool = True,
+                            q_offset: int = 0, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """:func:`prefill_attn_il8` over a hybrid cache (``ss_prefill_attn_il8_hybrid``):
+    positions below ``t_raw0`` scored from ``idx``, the rest from the whole
+    keys ``kraw`` (B, Hkv, t_kv - t_raw0, 2, 128) fp16 with factors ``kfac``
+    (B, Hkv, t_kv - t_raw0) float32 (:func:`raw_key_rows`); ``values_il8``
+    holds all t_kv tokens' values."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(values_il8, codebook, kraw, kfac)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    cap_v = values_il8.shape[2] * 8
+    n_raw = int(t_kv) - int(t_raw0)
+    if values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap_v // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 (B, Hkv, cap/8, {d}, 8)")
+    if kraw.dtype != torch.float16 or not kraw.is_contiguous() or \
+            tuple(kraw.shape) != (b_, hkv, max(n_raw, 1), 2, d) or \
+            kfac.dtype != torch.float32 or not kfac.is_contiguous() or \
+            tuple(kfac.shape) != (b_, hkv, max(n_raw, 1)):
+        raise ValueError("kraw / kfac do not match the buffered tokens")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(nb, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    _launched(_attn_stat("sunshape_prefill_attention_mfma", causal), lib.ss_prefill_attn_il8_hybrid(
+        ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+        nb, int(n_centroids), ptr(idx), cap, ptr(values_il8), cap_v, int(t_kv), ptr(kraw),
+        ptr(kfac), int(t_raw0), int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype),
+        stream_handle(q.device)))
+    return out
+
+
+def raw_key_rows(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Whole keys (B, H, T, D) in the codec's basis -> (rows, factors) for
+    :func:`prefill_attn_il8_hybrid`: per token s with max |key| * 2^-s in
+    [2^14, 2^15) (s = 0 for a zero key), row 0 = fp16(key * 2^-s), row 1 =
+    fp16((key * 2^-s - row 0) * 2^11), factor 2^s.  Both rows are exact for
+    fp16 and bf16 keys (at most 11 significant bits)."""
+    k = keys.float()
+    m = k.abs().amax(dim=-1)
+    e = torch.frexp(m).exponent.to(torch.int32)  # m = f * 2^e, f in [0.5, 1)
+    sh = torch.where(m > 0, e - 15, torch.zeros_like(e)).clamp(-126, 126)
+    ks = torch.ldexp(k, -sh.unsqueeze(-1))
+    hi = ks.to(torch.float16)
+    lo = ((ks - hi.float()) * 2048.0).to(torch.float16)
+    rows = torch.stack((hi, lo), dim=-2).contiguous()
+    return rows, torch.ldexp(torch.ones_like(m), sh).contiguous()
 
 
 def prefill_supported(n_q_heads: int, n_kv_heads: int, t_q: int, head_dim: int,

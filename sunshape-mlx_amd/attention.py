@@ -95,12 +95,33 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         return None
     codec = cache.codec
     buffered = cache.buffer_offset if isinstance(cache, HybridSunShapeKVCache) else 0
+    q, kscale, perm = _kernel_query(codec, queries, scale)
+    # a prompt against a hybrid cache (fp16, grouped or TurboQuant values):
+    # compressed keys from the codebook, buffered keys whole, values
+    # materialised once in the interleaved fp16 layout
+    b_, hq, tq, d = queries.shape
+    if isinstance(cache, HybridSunShapeKVCache) and tq > 1 and ops.get("k_heavy") is None and \
+            q.dtype in (torch.float16, torch.bfloat16) and \
+            _hip.prefill_supported(hq, cache.n_kv_heads, tq, d, codec.n_blocks):
+        pf = cache.prefill_operands()
+        if pf is not None:
+            vil8, rows, fac, t_raw0 = pf
+            try:
+                out = _hip.prefill_attn_il8_hybrid(q, kscale, perm, codec.kernel_codebook(),
+                                                   codec.n_centroids, ops["idx"], vil8,
+                                                   t_raw0 + buffered, rows, fac, t_raw0,
+                                                   causal=causal, q_offset=q_offset,
+                                                   out_dtype=out_dtype)
+            except _hip.SunShapeUnsupported:
+                out = None
+            if out is not None:
+                codec.last_score_backend = "hip_prefill_mfma_hybrid"
+                return out
     # the buffer joins the fused softmax on the interleaved fp16, grouped
     # interleaved, TurboQuant (both layouts) and SunShape-value kernels
     if buffered and ops["kind"] not in ("il8", "grouped_il", "turboquant_il", "turboquant",
                                         "sunshape_v"):
         return None
-    q, kscale, perm = _kernel_query(codec, queries, scale)
     if buffered and codec.mode not in PERM_MODES and codec.use_rotation:
         # the kernels score buffered keys against the query they are given,
         # here the rotated one: (q R^T) . (k R^T) = q . k for orthogonal R,

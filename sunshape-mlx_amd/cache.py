@@ -822,6 +822,49 @@ class HybridSunShapeKVCache:
             return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
         return None
 
+    def prefill_operands(self):
+        """What the prompt kernel (``ss_prefill_attn_il8_hybrid``) reads of
+        this cache: ``(values_il8, key_rows, key_factors, t_raw0)`` -- every
+        token's value in the 8-token interleaved fp16 layout (compressed values
+        dequantised, then the buffer's), and the buffered keys whole in the
+        codec's basis (``_hip.raw_key_rows``), which start at position t_raw0
+        = compressed_offset.  O(T) work, against the prompt's O(T x T_q).
+        None for SunShape-coded values (an fp16 copy of each value codeword
+        would move every token that uses it the same way) and for fp16 heavy
+        blocks."""
+        if self.value_backend == "sunshape" or self._heavy_dims is not None or \
+                self._key_buffer is None:
+            return None
+        tc, tb = self._compressed_offset, self._buffer_offset
+        t_kv = tc + tb
+        b_, h_, d = self._key_buffer.shape[0], self.n_kv_heads, self.head_dim
+        dev = self._key_buffer.device
+        vil8 = torch.zeros((b_, h_, (t_kv + 7) // 8, d, 8), dtype=torch.float16, device=dev)
+        if tc:
+            if self._values_il8 is not None:
+                nblk = (tc + 7) // 8
+                vil8[:, :, :nblk] = self._values_il8[:, :, :nblk]
+            else:
+                dense = self._compressed_values()
+                if dense is None:
+                    return None
+                _hip.append_values_il8(dense.to(torch.float16).contiguous(), vil8, 0)
+        if tb:
+            _hip.append_values_il8(self.buffer_values, vil8, tc)
+            kb = self.buffer_keys
+            c = self.codec
+            if c.mode in PERM_MODES:
+                kc = kb[..., c.permutation.long()]
+            elif c.use_rotation:
+                kc = kb.float() @ c.rotation.t()
+            else:
+                kc = kb
+            rows, fac = _hip.raw_key_rows(kc)
+        else:
+            rows = torch.zeros((b_, h_, 1, 2, d), dtype=torch.float16, device=dev)
+            fac = torch.ones((b_, h_, 1), dtype=torch.float32, device=dev)
+        return vil8, rows, fac, tc
+
     @property
     def can_fuse_value_dequant(self) -> bool:
         return (self.value_backend == "grouped" and self._compressed_offset > 0

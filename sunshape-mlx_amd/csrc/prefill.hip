@@ -81,8 +81,15 @@ struct PrefillArgs {
     const float *cb_mul;     // their power-of-two multiplier
     int nct;                 // centroid tiles of 16
     const uint8_t *idx;      // [B][Hkv][cap][16]
-    const __half *v8;        // [B][Hkv][cap/8][128][8]
-    int64_t cap, t_kv;
+    const __half *v8;        // [B][Hkv][cap_v/8][128][8]
+    int64_t cap, cap_v, t_kv;
+    // keys from position t_raw0 on (a hybrid cache's buffered tokens) are
+    // given whole instead of as indices: kraw [B][Hkv][n_raw][2][128] fp16,
+    // per token its codec-basis key times 2^-s (hi) and the remainder times
+    // 2^11 (lo), kfac [B][Hkv][n_raw] = 2^s; t_raw0 = t_kv when there are none
+    const __half *kraw;
+    const float *kfac;
+    int64_t t_raw0, n_raw;
     int causal;
     int64_t q_offset;
     void *out;
@@ -187,7 +194,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill16_il8_kernel(Prefill
     const int n_tiles = t_end32 > 0 ? (t_end32 + kWave - 1) / kWave : 0;
     const int t_last = max(t_end32 - 1, 0);
     const uint8_t *idx_head = a.idx + bh * a.cap * kPfNB;
-    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap * kPfD);
+    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap_v * kPfD);
 
     float m = -1e30f, lsum = 0.f;  // row l16 (lsum: this lane's share)
     pf_f32x4 acc[8];
@@ -422,7 +429,15 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
     const int n_sub = t_end32 > 0 ? (t_end32 + 31) / 32 : 0;
     const int t_last = max(t_end32 - 1, 0);
     const uint8_t *idx_head = a.idx + bh * a.cap * kPfNB;
-    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap * kPfD);
+    const char *v_head = reinterpret_cast<const char *>(a.v8 + bh * a.cap_v * kPfD);
+    // whole keys from position t_raw0 on (none without kraw: no sub-tile
+    // reaches INT_MAX); index rows only below it
+    const int t_raw0 = a.kraw ? (int)a.t_raw0 : INT_MAX;
+    const int idx_last = max(min(t_last, t_raw0 - 1), 0);
+    const int n_raw32 = (int)max(a.n_raw, (int64_t)1);
+    const __half *kraw_head = a.kraw ? a.kraw + bh * a.n_raw * 2 * kPfD : nullptr;
+    const float *kfac_head = a.kfac ? a.kfac + bh * a.n_raw : nullptr;
+    const float inv_cb_mul = 1.f / *a.cb_mul;  // a power of two
 
     float m = -1e30f, lsum = 0.f;  // row l32 (lsum: this lane's half of its tokens)
     pf_f32x16 acc[4];
@@ -433,7 +448,7 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
 
     // the index row of token t0 + l32 (both lane halves read the same row)
     auto load_idx = [&](uint4 &ir, int sub) {
-        ir = *reinterpret_cast<const uint4 *>(idx_head + (uint32_t)min(32 * sub + l32, t_last) * kPfNB);
+        ir = *reinterpret_cast<const uint4 *>(idx_head + (uint32_t)min(32 * sub + l32, idx_last) * kPfNB);
     };
     uint4 ir_a, ir_b;
     if (n_sub > 0) load_idx(ir_a, 0);
@@ -460,21 +475,58 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
         pf_f32x16 sh, sl;
 #pragma unroll
         for (int i = 0; i < 16; ++i) sh[i] = sl[i] = 0.f;
+        // a sub-tile reaching the whole keys (wave-uniform): lanes whose
+        // token is past t_raw0 take its key rows from kraw
+        const bool raw_tile = t0 + 31 >= t_raw0;
+        if (!raw_tile) {
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const int blk = 2 * ks + hb;
-            const uint32_t w = (blk >> 2) == 0 ? ir_cur.x : (blk >> 2) == 1 ? ir_cur.y
-                             : (blk >> 2) == 2 ? ir_cur.z : ir_cur.w;
-            const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * (blk & 3), 8);
-            const char *row = lds + (blk * 256 + c) * 16;
-            const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
-            const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
-            sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+            for (int ks = 0; ks < 8; ++ks) {
+                const int blk = 2 * ks + hb;
+                const uint32_t w = (blk >> 2) == 0 ? ir_cur.x : (blk >> 2) == 1 ? ir_cur.y
+                                 : (blk >> 2) == 2 ? ir_cur.z : ir_cur.w;
+                const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * (blk & 3), 8);
+                const char *row = lds + (blk * 256 + c) * 16;
+                const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
+                const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
+                sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+            }
+        } else {
+            const int tk = t0 + l32;
+            const bool mine_raw = tk >= t_raw0;
+            const __half *kr = kraw_head + (uint32_t)min(max(tk - t_raw0, 0), n_raw32 - 1) * 2 * kPfD;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const int blk = 2 * ks + hb;
+                pf_f16x8 ah, al;
+                if (mine_raw) {
+                    ah = *reinterpret_cast<const pf_f16x8 *>(kr + blk * 8);
+                    al = *reinterpret_cast<const pf_f16x8 *>(kr + kPfD + blk * 8);
+                } else {
+                    const uint32_t w = (blk >> 2) == 0 ? ir_cur.x : (blk >> 2) == 1 ? ir_cur.y
+                                     : (blk >> 2) == 2 ? ir_cur.z : ir_cur.w;
+                    const uint32_t c = __builtin_amdgcn_ubfe(w, 8 * (blk & 3), 8);
+                    const char *row = lds + (blk * 256 + c) * 16;
+                    ah = *reinterpret_cast<const pf_f16x8 *>(row);
+                    al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
+                }
+                sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+            }
         }
         float sv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) sv[i] = fmaf(sl[i], 1.f / kPfSplit, sh[i]);
+        if (raw_tile) {
+            // whole keys' scores into the codebook's units: times their own
+            // 2^s and the codebook's power of two
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int tk = t0 + 8 * (i >> 2) + 4 * hb + (i & 3);
+                if (tk >= t_raw0)
+                    sv[i] *= kfac_head[min(tk - t_raw0, n_raw32 - 1)] * inv_cb_mul;
+            }
+        }
         // a sub-tile below every row's limit and the last key is not masked
         // (wave-uniform)
         const bool full = t0 + 31 < t_end32 && t0 + 31 <= lim_min32;
@@ -597,12 +649,12 @@ using namespace ss;
 // must divide it) and the fewest query tokens it is meant for.
 extern "C" int ss_prefill_rows_per_workgroup(void) { return kPfRows; }
 
-extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
-                                   int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                   const int32_t *perm, const void *codebook, int n_blocks,
-                                   int n_centroids, const uint8_t *idx, const void *values_il8,
-                                   int v_dtype, int64_t cap, int64_t t_kv, int causal,
-                                   int64_t q_offset, void *out, int out_dtype, void *stream) {
+static int prefill_impl(const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads,
+                        int64_t t_q, int head_dim, float scale, const int32_t *perm,
+                        const void *codebook, int n_blocks, int n_centroids, const uint8_t *idx,
+                        int64_t cap, const void *values_il8, int v_dtype, int64_t cap_v,
+                        int64_t t_kv, const void *kraw, const float *kfac, int64_t t_raw0,
+                        int causal, int64_t q_offset, void *out, int out_dtype, void *stream) {
     SS_REQUIRE(q && codebook && idx && values_il8 && out, "null pointer argument");
     SS_REQUIRE(valid_dtype(q_dtype) && valid_dtype(out_dtype), "bad dtype code");
     SS_REQUIRE(batch >= 1 && n_q_heads >= 1 && n_kv_heads >= 1 && t_q >= 1 &&
@@ -617,8 +669,16 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
     SS_UNSUPPORTED(kPfRows % rep == 0, "GQA group of %d query heads does not divide %d rows", rep,
                    kPfRows);
     SS_UNSUPPORTED(v_dtype == SS_F16, "interleaved values must be float16");
-    SS_REQUIRE(cap % 8 == 0 && t_kv >= 0 && t_kv <= cap, "bad cap/t_kv (cap %% 8 == 0, t_kv <= cap)");
-    SS_UNSUPPORTED(cap < (int64_t(1) << 24) && t_q + q_offset < (int64_t(1) << 30),
+    SS_REQUIRE(cap_v % 8 == 0 && t_kv >= 0 && t_kv <= cap_v,
+               "bad cap/t_kv (the value capacity a multiple of 8, t_kv <= it)");
+    const bool raw = kraw != nullptr;
+    SS_REQUIRE(!raw || (kfac && t_raw0 >= 0 && t_raw0 <= t_kv && t_raw0 <= cap),
+               "whole keys need their factors and 0 <= t_raw0 <= min(t_kv, cap)");
+    SS_REQUIRE(raw || t_kv <= cap, "t_kv exceeds the index capacity");
+    SS_UNSUPPORTED(!raw || q_dtype != SS_F32,
+                   "whole keys (a hybrid buffer) are taken with fp16 or bf16 queries only");
+    SS_UNSUPPORTED(cap < (int64_t(1) << 24) && cap_v < (int64_t(1) << 24) &&
+                       t_q + q_offset < (int64_t(1) << 30),
                    "prefill kernel takes caches below 2^24 tokens");
     SS_REQUIRE(q_offset >= 0, "negative q_offset");
     SS_REQUIRE(((uintptr_t)codebook % 16) == 0 && ((uintptr_t)idx % 16) == 0 &&
@@ -640,7 +700,12 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
     a.idx = idx;
     a.v8 = static_cast<const __half *>(values_il8);
     a.cap = cap;
+    a.cap_v = cap_v;
     a.t_kv = t_kv;
+    a.kraw = static_cast<const __half *>(kraw);
+    a.kfac = kfac;
+    a.t_raw0 = raw ? t_raw0 : t_kv;
+    a.n_raw = raw ? t_kv - t_raw0 : 0;
     a.causal = causal ? 1 : 0;
     a.q_offset = q_offset;
     a.out = out;
@@ -667,4 +732,31 @@ extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, in
                        kPfLdsBytes, reinterpret_cast<hipStream_t>(stream), a);
     SS_LAUNCH_CHECK("prefill_il8_kernel launch");
     return SS_OK;
+}
+
+extern "C" int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                   int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                   const int32_t *perm, const void *codebook, int n_blocks,
+                                   int n_centroids, const uint8_t *idx, const void *values_il8,
+                                   int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                   int64_t q_offset, void *out, int out_dtype, void *stream) {
+    return prefill_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                        codebook, n_blocks, n_centroids, idx, cap, values_il8, v_dtype, cap, t_kv,
+                        nullptr, nullptr, 0, causal, q_offset, out, out_dtype, stream);
+}
+
+extern "C" int ss_prefill_attn_il8_hybrid(const void *q, int q_dtype, int64_t batch,
+                                          int n_q_heads, int n_kv_heads, int64_t t_q,
+                                          int head_dim, float scale, const int32_t *perm,
+                                          const void *codebook, int n_blocks, int n_centroids,
+                                          const uint8_t *idx, int64_t cap, const void *values_il8,
+                                          int64_t cap_v, int64_t t_kv, const void *kraw,
+                                          const float *kfac, int64_t t_raw0, int causal,
+                                          int64_t q_offset, void *out, int out_dtype,
+                                          void *stream) {
+    SS_REQUIRE(kraw && kfac, "null pointer argument");
+    SS_REQUIRE(((uintptr_t)kraw % 16) == 0, "kraw must be 16-byte aligned");
+    return prefill_impl(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                        codebook, n_blocks, n_centroids, idx, cap, values_il8, SS_F16, cap_v, t_kv,
+                        kraw, kfac, t_raw0, causal, q_offset, out, out_dtype, stream);
 }

@@ -865,3 +865,49 @@ def test_hybrid_grouped_decode_steps_fused_equal_separate_appends(bits, buf):
                           codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
                           fused.buffer_keys.float().cpu().numpy(), vals)
     assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("backend,bits,buf,qdt", [
+    ("grouped", 2, 128, torch.float16),     # config 4's cache: 2-bit grouped, default buffer
+    ("grouped", 4, 64, torch.bfloat16),
+    ("turboquant", 2, 128, torch.float16),
+    ("fp16", None, 96, torch.float16),      # fp16 values, a buffer
+    ("grouped", 2, 0, torch.float16),       # no buffer
+])
+def test_hybrid_prompt_takes_the_prefill_kernel(backend, bits, buf, qdt):
+    """A prompt (mask "causal") against a hybrid cache runs on the
+    matrix-core prefill kernel: compressed keys from the codebook, the
+    buffered keys whole, every value in one interleaved fp16 copy.  It
+    matches the reference's two-pass path (the oracle) over the same cache,
+    for the first prompt and for a second chunk after it (rows offset by the
+    cached tokens)."""
+    codec = make_codec(80)
+    b, hq, hkv, d = 1, 32, 8, 128
+    kw = dict(n_kv_heads=hkv, value_backend=backend, buffer_size=buf)
+    if bits:
+        kw.update(value_bits=bits, value_scale_dtype=torch.float16)
+    cache = S.create_kv_cache(codec, **kw)
+    assert isinstance(cache, S.HybridSunShapeKVCache)
+    k, v = kv(81, b, hkv, 700, d)
+    q = torch.randn((b, hq, 700, d), device=DEV).to(qdt)
+    cents = codec.centroids.cpu().numpy()
+    perm = codec.permutation.cpu().numpy()
+    for lo, hi in ((0, 500), (500, 700)):
+        cache.update_and_fetch(k[:, :, lo:hi], v[:, :, lo:hi])
+        qq = q[:, :, lo:hi].contiguous()
+        out = S.sunshape_sdpa(qq, cache, 0.088, mask="causal")
+        assert codec.last_score_backend == "hip_prefill_mfma_hybrid"
+        out32 = S.sunshape_sdpa(qq, cache, 0.088, mask="causal", out_dtype=torch.float32)
+        vals = cache.values.float().cpu().numpy()  # compressed values dequantised, then buffer
+        if qdt == torch.bfloat16:  # q * scale rounded to bf16, as the kernels form it
+            qref, sc = (qq.float() * 0.088).to(torch.bfloat16).float().cpu().numpy(), 1.0
+        else:
+            qref, sc = qq.cpu().numpy(), 0.088
+        ref = O.sdpa_two_pass(qref, sc, perm, cents, cache.key_indices.cpu().numpy(),
+                              cache.buffer_keys.float().cpu().numpy() if cache.buffer_offset
+                              else None, vals, mask="causal")
+        # values enter the prompt kernel rounded to fp16 (dequantised codes
+        # take more bits): within 2^-12 of each, a few 1e-4 of the output
+        assert rel_err(out32.cpu().numpy(), ref) <= REL_TOL
+        if qdt == torch.float16:
+            assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
