@@ -630,6 +630,43 @@ int ss_pack_grouped_il(const uint32_t *packed, int64_t n_b, int64_t n_h, int64_t
                        uint32_t *out_il, int64_t cap, int64_t offset, void *stream);
 
 /*
+ * The inverse of ss_pack_grouped_il: the first n_t tokens of interleaved
+ * codes codes_il [n_bh][cap/tpw][head_dim] (n_bh = batch x heads rows) as
+ * pack_indices rows out [n_bh][n_t][head_dim*bits/32].  Replaces the
+ * reference's values_packed_raw accessor (cache.py:858-866), whose rows
+ * this layout stores rearranged; bits 2 or 4.
+ */
+int ss_grouped_il_to_packed(const uint32_t *codes_il, int64_t n_bh, int64_t cap, int head_dim,
+                            int bits, int64_t n_t, uint32_t *out, void *stream);
+
+/*
+ * Dequantise the first n_t tokens of interleaved grouped codes (codes_il as
+ * above; scales/zeros [n_bh][sz_cap][head_dim/group_size], f32 or f16)
+ * straight into the 8-token interleaved fp16 layout out_il8
+ * [n_bh][cap_out/8][head_dim][8] at positions 0 .. n_t-1, for the hybrid
+ * prompt kernel (ss_prefill_attn_il8_hybrid).  v = fp16(q*scale + zero), the
+ * product and the sum rounded in float32 as dequantize_values (reference
+ * kernels.py:1231-1269) does before the cast.  Positions n_t .. of the last
+ * 8-token group are written as zero; later groups are not written.
+ */
+int ss_grouped_il_to_il8(const uint32_t *codes_il, int64_t n_bh, int64_t cap, int head_dim,
+                         int bits, int group_size, const void *scales, const void *zeros,
+                         int sz_dtype, int64_t sz_cap, int64_t n_t, void *out_il8,
+                         int64_t cap_out, void *stream);
+
+/*
+ * The whole-key rows kraw / kfac of ss_prefill_attn_il8_hybrid from buffered
+ * keys: token (b,h,t) reads keys[b*k_sb + h*k_sh + t*k_st + perm[j]] for dim
+ * j (perm NULL = identity), writes rows [n_b][n_h][n_t][2][head_dim] fp16
+ * and factors [n_b][n_h][n_t] float32 as described there, s from max |key|.
+ * No counterpart in the reference (its two-pass path, attention.py:307-350,
+ * multiplies the buffered fp16 keys directly); one launch per prompt.
+ */
+int ss_raw_key_rows(const void *keys, int k_dtype, int64_t n_b, int64_t n_h, int64_t n_t,
+                    int64_t k_sb, int64_t k_sh, int64_t k_st, int head_dim, const int32_t *perm,
+                    void *rows, float *factors, void *stream);
+
+/*
  * Grouped asymmetric min-max quantisation of values (encode-on-append).
  * Replaces quantize_values (reference kernels.py:1173-1228): per token and
  * group, zero = min, scale = max((max - min) / (2^bits - 1), 1e-8),

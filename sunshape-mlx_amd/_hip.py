@@ -152,6 +152,12 @@ _SIGNATURES = {
         _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                                   _c_void_p, _i64, _i64, _c_void_p]),
+    "ss_grouped_il_to_packed": (_int, [_c_void_p, _i64, _i64, _int, _int, _i64, _c_void_p,
+                                       _c_void_p]),
+    "ss_grouped_il_to_il8": (_int, [_c_void_p, _i64, _i64, _int, _int, _int, _c_void_p,
+                                    _c_void_p, _int, _i64, _i64, _c_void_p, _i64, _c_void_p]),
+    "ss_raw_key_rows": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                               _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "ss_quantize_values_grouped": (_int, [_c_void_p, _int, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _int, _int, _int, _c_void_p, _c_void_p, _c_void_p, _int,
                                           _i64, _i64, _i64, _c_void_p]),
@@ -865,21 +871,28 @@ def prefill_attn_il8_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | 
     return out
 
 
-def raw_key_rows(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Whole keys (B, H, T, D) in the codec's basis -> (rows, factors) for
-    :func:`prefill_attn_il8_hybrid`: per token s with max |key| * 2^-s in
-    [2^14, 2^15) (s = 0 for a zero key), row 0 = fp16(key * 2^-s), row 1 =
-    fp16((key * 2^-s - row 0) * 2^11), factor 2^s.  Both rows are exact for
-    fp16 and bf16 keys (at most 11 significant bits)."""
-    k = keys.float()
-    m = k.abs().amax(dim=-1)
-    e = torch.frexp(m).exponent.to(torch.int32)  # m = f * 2^e, f in [0.5, 1)
-    sh = torch.where(m > 0, e - 15, torch.zeros_like(e)).clamp(-126, 126)
-    ks = torch.ldexp(k, -sh.unsqueeze(-1))
-    hi = ks.to(torch.float16)
-    lo = ((ks - hi.float()) * 2048.0).to(torch.float16)
-    rows = torch.stack((hi, lo), dim=-2).contiguous()
-    return rows, torch.ldexp(torch.ones_like(m), sh).contiguous()
+def raw_key_rows(keys: torch.Tensor, perm: torch.Tensor | None = None
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Whole keys (B, H, T, D) -> (rows, factors) for
+    :func:`prefill_attn_il8_hybrid` in one launch (``ss_raw_key_rows``), dim j
+    taken from dim ``perm[j]`` of the key (the codec's basis).  Per token s
+    brings max |key| * 2^-s into [2^14, 2^15) (s = 0 for a zero key); row 0 =
+    fp16(key * 2^-s), row 1 = fp16((key * 2^-s - row 0) * 2^11), factor 2^s.
+    Both rows are exact for fp16 and bf16 keys (at most 11 significant bits)."""
+    require_gpu(keys)
+    if keys.dim() != 4 or keys.stride(-1) != 1:
+        raise ValueError("keys must be (B, H, T, D) with unit last stride")
+    b_, h_, t_, d = keys.shape
+    if perm is not None:
+        require_gpu(perm)
+        if perm.dtype != torch.int32 or not perm.is_contiguous() or perm.numel() != d:
+            raise ValueError(f"perm must be a contiguous int32 vector of {d} entries")
+    rows = torch.empty((b_, h_, t_, 2, d), dtype=torch.float16, device=keys.device)
+    fac = torch.empty((b_, h_, t_), dtype=torch.float32, device=keys.device)
+    check(load_library().ss_raw_key_rows(
+        ptr(keys), dtype_code(keys.dtype), b_, h_, t_, keys.stride(0), keys.stride(1),
+        keys.stride(2), d, ptr(perm), ptr(rows), ptr(fac), stream_handle(keys.device)))
+    return rows, fac
 
 
 def prefill_supported(n_q_heads: int, n_kv_heads: int, t_q: int, head_dim: int,
@@ -1328,21 +1341,45 @@ def pack_grouped_il(packed: torch.Tensor, bits: int, codes_il: torch.Tensor, off
 
 def grouped_il_to_packed(codes_il: torch.Tensor, bits: int, t: int | None = None) -> torch.Tensor:
     """(B, H, cap*bits/32, D) token-interleaved codes -> reference-layout
-    packed rows (B, H, cap, D*bits/32) uint32 (first ``t`` tokens)."""
+    packed rows (B, H, t, D*bits/32) uint32 of the first ``t`` tokens (all
+    cap when None), one launch (``ss_grouped_il_to_packed``)."""
+    require_gpu(codes_il)
+    if codes_il.dim() != 4 or not codes_il.is_contiguous() or \
+            codes_il.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("codes_il must be a contiguous 32-bit (B, H, cap*bits/32, D) buffer")
     b_, h_, nblk, d = codes_il.shape
-    tpw = 32 // bits
-    w = codes_il.view(torch.int32).to(torch.int64) & 0xffffffff
-    # token i of an interleaved word sits at bit bits*(i//2) + 16*(i%2)
-    il_shifts = torch.tensor([bits * (i // 2) + 16 * (i % 2) for i in range(tpw)],
-                             device=w.device, dtype=torch.int64)
-    shifts = torch.arange(tpw, device=w.device, dtype=torch.int64) * bits
-    codes = (w.unsqueeze(3) >> il_shifts.view(1, 1, 1, tpw, 1)) & ((1 << bits) - 1)  # (B,H,blk,tpw,D)
-    codes = codes.reshape(b_, h_, nblk * tpw, d)
-    if t is not None:
-        codes = codes[:, :, :t]
-    words = (codes.reshape(b_, h_, codes.shape[2], d // tpw, tpw) << shifts).sum(-1)
-    return words.to(torch.int64).to(torch.int32).view(torch.uint32) if hasattr(torch, "uint32") \
-        else words.to(torch.int32)
+    cap = nblk * (32 // bits)
+    t = cap if t is None else int(t)
+    out = torch.empty((b_, h_, t, d * bits // 32), dtype=torch.int32, device=codes_il.device)
+    check(load_library().ss_grouped_il_to_packed(ptr(codes_il), b_ * h_, cap, d, int(bits), t,
+                                                 ptr(out), stream_handle(codes_il.device)))
+    return out.view(torch.uint32) if hasattr(torch, "uint32") else out
+
+
+def grouped_il_to_il8(codes_il: torch.Tensor, bits: int, group_size: int, scales: torch.Tensor,
+                      zeros: torch.Tensor, t: int, out_il8: torch.Tensor) -> None:
+    """Dequantise the first ``t`` tokens of interleaved codes (scales/zeros
+    (B, H, cap, n_groups), float16 or float32, contiguous) straight into the
+    8-token interleaved fp16 buffer (B, H, cap_out/8, D, 8) at positions
+    [0, t), one launch (``ss_grouped_il_to_il8``); v = fp16(q * scale + zero)
+    as :func:`dequantize_values_grouped` then a cast.  Positions past t in
+    the last 8-token group are set to zero."""
+    require_gpu(codes_il, scales, zeros, out_il8)
+    if codes_il.dim() != 4 or not codes_il.is_contiguous():
+        raise ValueError("codes_il must be a contiguous (B, H, cap*bits/32, D) buffer")
+    b_, h_, nblk, d = codes_il.shape
+    cap = nblk * (32 // bits)
+    if scales.dtype != zeros.dtype or scales.shape != zeros.shape or \
+            not scales.is_contiguous() or not zeros.is_contiguous() or \
+            tuple(scales.shape[:2]) != (b_, h_) or scales.shape[3] * group_size != d:
+        raise ValueError("scales/zeros must be contiguous (B, H, cap, D/group_size) of one dtype")
+    if out_il8.dtype != torch.float16 or not out_il8.is_contiguous() or out_il8.dim() != 5 or \
+            tuple(out_il8.shape[:2]) != (b_, h_) or tuple(out_il8.shape[3:]) != (d, 8):
+        raise ValueError(f"out_il8 must be a contiguous float16 (B, H, cap/8, {d}, 8) buffer")
+    check(load_library().ss_grouped_il_to_il8(
+        ptr(codes_il), b_ * h_, cap, d, int(bits), int(group_size), ptr(scales), ptr(zeros),
+        dtype_code(scales.dtype), scales.shape[2], int(t), ptr(out_il8), out_il8.shape[2] * 8,
+        stream_handle(codes_il.device)))
 
 
 def quantize_values_grouped(values: torch.Tensor, bits: int, group_size: int,

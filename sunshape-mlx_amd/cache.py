@@ -844,6 +844,10 @@ class HybridSunShapeKVCache:
             if self._values_il8 is not None:
                 nblk = (tc + 7) // 8
                 vil8[:, :, :nblk] = self._values_il8[:, :, :nblk]
+            elif self.value_backend == "grouped" and self._values_il is not None:
+                gc = self._value_codec_impl
+                _hip.grouped_il_to_il8(self._values_il, gc.bits, gc.group_size,
+                                       self._value_scales, self._value_zeros, tc, vil8)
             else:
                 dense = self._compressed_values()
                 if dense is None:
@@ -854,12 +858,11 @@ class HybridSunShapeKVCache:
             kb = self.buffer_keys
             c = self.codec
             if c.mode in PERM_MODES:
-                kc = kb[..., c.permutation.long()]
+                rows, fac = _hip.raw_key_rows(kb, c.permutation)
             elif c.use_rotation:
-                kc = kb.float() @ c.rotation.t()
+                rows, fac = _hip.raw_key_rows((kb.float() @ c.rotation.t()).contiguous())
             else:
-                kc = kb
-            rows, fac = _hip.raw_key_rows(kc)
+                rows, fac = _hip.raw_key_rows(kb)
         else:
             rows = torch.zeros((b_, h_, 1, 2, d), dtype=torch.float16, device=dev)
             fac = torch.ones((b_, h_, 1), dtype=torch.float32, device=dev)

@@ -26,6 +26,40 @@ __global__ void __launch_bounds__(256)
     store_value_il8(out, b * n_h + h, cap, d, offset + t, j, x);
 }
 
+// Whole keys for the hybrid prompt kernel: one wave per token.  Dim j of the
+// output is dim perm[j] of the key (the codec's basis; perm null = identity).
+// With s = row_exp_shift(max |key|), row 0 = fp16(key * 2^-s) and row 1 =
+// fp16((key * 2^-s - row 0) * 2^11); factor = 2^s.  Multiplying by a power of
+// two is exact, so both rows are exact for keys of at most 22 significant bits
+// whose scaled magnitude stays above fp16's subnormal range.
+__global__ void __launch_bounds__(256)
+    raw_key_rows_kernel(const void *k, int k_dtype, int64_t n_h, int64_t n_t, int64_t n_tok,
+                        int64_t k_sb, int64_t k_sh, int64_t k_st, int d, const int32_t *perm,
+                        __half *rows, float *fac) {
+    const int64_t n = (int64_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (n >= n_tok) return;  // whole waves leave together
+    const int64_t b = n / (n_h * n_t);
+    const int64_t rem = n - b * n_h * n_t;
+    const int64_t h = rem / n_t;
+    const int64_t t = rem - h * n_t;
+    const int64_t base = b * k_sb + h * k_sh + t * k_st;
+    float m = 0.f;
+    for (int j = lane; j < d; j += 64)
+        m = fmaxf(m, fabsf(load_as_f32(k, k_dtype, base + (perm ? perm[j] : j))));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const int s = row_exp_shift(m);
+    const float down = exp2i(-s);
+    __half *r0 = rows + n * 2 * d;
+    for (int j = lane; j < d; j += 64) {
+        const float x = load_as_f32(k, k_dtype, base + (perm ? perm[j] : j)) * down;
+        const __half hi = __float2half(x);
+        r0[j] = hi;
+        r0[d + j] = __float2half((x - __half2float(hi)) * 2048.f);
+    }
+    if (lane == 0) fac[n] = exp2i(s);
+}
+
 }  // namespace ss
 
 using namespace ss;
@@ -49,5 +83,23 @@ extern "C" int ss_append_values_il8(const void *values, int v_dtype, int64_t n_b
                        values, v_dtype, n_h, n_t, n_tok, v_sb, v_sh, v_st, head_dim,
                        reinterpret_cast<__half *>(out_il8), cap, offset);
     SS_LAUNCH_CHECK("append_il8_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_raw_key_rows(const void *keys, int k_dtype, int64_t n_b, int64_t n_h,
+                               int64_t n_t, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                               int head_dim, const int32_t *perm, void *rows, float *factors,
+                               void *stream) {
+    SS_REQUIRE(valid_dtype(k_dtype), "bad key dtype");
+    SS_REQUIRE(n_b >= 0 && n_h >= 0 && n_t >= 0 && head_dim >= 1, "bad sizes");
+    const int64_t n_tok = n_b * n_h * n_t;
+    if (n_tok == 0) return SS_OK;
+    SS_REQUIRE(keys && rows && factors, "null pointer argument");
+    SS_UNSUPPORTED(n_tok < (1LL << 31), "too many tokens for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(raw_key_rows_kernel, dim3((unsigned)((n_tok + 3) / 4)), dim3(256), 0, st,
+                       keys, k_dtype, n_h, n_t, n_tok, k_sb, k_sh, k_st, head_dim, perm,
+                       reinterpret_cast<__half *>(rows), factors);
+    SS_LAUNCH_CHECK("raw_key_rows_kernel launch");
     return SS_OK;
 }

@@ -124,9 +124,13 @@ __global__ void __launch_bounds__(256)
     out[e] = (uint8_t)cnt;
 }
 
+// Bit offset of token i inside an interleaved word: bits*(i/2) in the low
+// half for even i, +16 for odd i.
+__device__ __forceinline__ int il_pos(int bits, int i) { return bits * (i >> 1) + 16 * (i & 1); }
+
 // Interleaved code layout of the fused grouped-value decode: per (b, h), word
 // (blk, d) of [cap / vpw][D] holds dim d of tokens blk*vpw .. blk*vpw + vpw - 1,
-// token i of the block at bits [bits*i, bits*(i+1)).  One thread per (block,
+// token i of the block at bit bits*(i/2) + 16*(i%2).  One thread per (block,
 // dim) of the appended range; bits of tokens outside [offset, offset + n_t)
 // are kept.
 __global__ void __launch_bounds__(256)
@@ -149,11 +153,72 @@ __global__ void __launch_bounds__(256)
         if (t < 0 || t >= n_t) continue;
         const uint32_t w = packed[(b * p_sb + h * p_sh + t * p_st) * nw + dd / vpw];
         const uint32_t code = (w >> ((dd % vpw) * bits)) & mask;
-        // token i of the word: bits*(i/2) in the low half for even i, +16 for odd i
-        const int pos = bits * (i >> 1) + 16 * (i & 1);
+        const int pos = il_pos(bits, i);
         word = (word & ~(mask << pos)) | (code << pos);
     }
     *wp = word;
+}
+
+// The inverse of pack_grouped_il_kernel: one thread per output packed word
+// (row t of (B, H) row bh, word w) gathers its vpw dims' codes of token t.
+__global__ void __launch_bounds__(256)
+    grouped_il_unpack_kernel(const uint32_t *codes_il, int64_t n_t, int64_t cap, int d, int bits,
+                             uint32_t *out) {
+    const int nw = d / vals_per_word(bits);
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t bh = blockIdx.y;
+    if (e >= n_t * nw) return;
+    const int64_t t = e / nw;
+    const int w = (int)(e - t * nw);
+    const int vpw = vals_per_word(bits);
+    const uint32_t mask = (1u << bits) - 1u;
+    const int pos = il_pos(bits, (int)(t % vpw));
+    const uint32_t *src = codes_il + (bh * (cap / vpw) + t / vpw) * d + w * vpw;
+    uint32_t word = 0u;
+    for (int k = 0; k < vpw; ++k) word |= ((src[k] >> pos) & mask) << (k * bits);
+    out[bh * n_t * nw + e] = word;
+}
+
+// Interleaved codes -> values in the 8-token interleaved fp16 layout
+// [cap_out/8][d][8] per (B, H) row: one thread per (row, code word, dim)
+// decodes the word's vpw tokens, v = fp16(q * scale + zero) (multiply and add
+// rounded separately in float32, as dequantize_grouped_kernel), and writes
+// each 8-token group it covers as one 16-byte store.  Tokens at or past n_t
+// inside the last group are written as zero; groups starting at or past n_t
+// are not written.
+__global__ void __launch_bounds__(256)
+    grouped_il_to_il8_kernel(const uint32_t *codes_il, int64_t cap, int d, int bits, int group,
+                             const void *scales, const void *zeros, int sz_dtype, int64_t sz_cap,
+                             int64_t n_t, int64_t n_blk, __half *out, int64_t cap_out) {
+#pragma clang fp contract(off)
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t bh = blockIdx.y;
+    if (e >= n_blk * d) return;
+    const int64_t blk = e / d;
+    const int dd = (int)(e - blk * d);
+    const int vpw = vals_per_word(bits);
+    const uint32_t mask = (1u << bits) - 1u;
+    const int n_groups = d / group;
+    const uint32_t word = codes_il[(bh * (cap / vpw) + blk) * d + dd];
+    for (int h8 = 0; h8 < vpw / 8; ++h8) {
+        const int64_t t0 = blk * vpw + h8 * 8;
+        if (t0 >= n_t) break;
+        __half v8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t t = t0 + i;
+            float x = 0.f;
+            if (t < n_t) {
+                const float q = (float)((word >> il_pos(bits, h8 * 8 + i)) & mask);
+                const int64_t gi = (bh * sz_cap + t) * n_groups + dd / group;
+                const float prod = q * load_as_f32(scales, sz_dtype, gi);
+                x = prod + load_as_f32(zeros, sz_dtype, gi);
+            }
+            v8[i] = __float2half(x);
+        }
+        *reinterpret_cast<uint4 *>(out + ((bh * (cap_out / 8) + t0 / 8) * d + dd) * 8) =
+            *reinterpret_cast<const uint4 *>(v8);
+    }
 }
 
 static inline unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -275,5 +340,58 @@ extern "C" int ss_pack_grouped_il(const uint32_t *packed, int64_t n_b, int64_t n
                        dim3(256), 0, st, packed, n_h, n_t, p_sb, p_sh, p_st, head_dim, bits, out_il,
                        cap, offset, b0, n_blk);
     SS_LAUNCH_CHECK("pack_grouped_il_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_grouped_il_to_packed(const uint32_t *codes_il, int64_t n_bh, int64_t cap,
+                                       int head_dim, int bits, int64_t n_t, uint32_t *out,
+                                       void *stream) {
+    SS_REQUIRE(bits == 2 || bits == 4, "interleaved codes need bits 2 or 4 (got %d)", bits);
+    SS_REQUIRE(head_dim >= 1 && head_dim % (32 / bits) == 0, "head_dim %d cannot be packed at %d bits",
+               head_dim, bits);
+    SS_REQUIRE(n_bh >= 0 && n_t >= 0, "negative sizes");
+    SS_REQUIRE(cap % (32 / bits) == 0 && n_t <= cap, "n_t %lld past cap %lld (a multiple of %d)",
+               (long long)n_t, (long long)cap, 32 / bits);
+    if (n_bh * n_t == 0) return SS_OK;
+    SS_REQUIRE(codes_il && out, "null pointer argument");
+    SS_UNSUPPORTED(n_bh < 65536, "too many (batch, head) rows for one launch");
+    const int64_t total = n_t * (head_dim / (32 / bits));
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(grouped_il_unpack_kernel, dim3(blocks_for(total), (unsigned)n_bh), dim3(256),
+                       0, st, codes_il, n_t, cap, head_dim, bits, out);
+    SS_LAUNCH_CHECK("grouped_il_unpack_kernel launch");
+    return SS_OK;
+}
+
+extern "C" int ss_grouped_il_to_il8(const uint32_t *codes_il, int64_t n_bh, int64_t cap,
+                                    int head_dim, int bits, int group_size, const void *scales,
+                                    const void *zeros, int sz_dtype, int64_t sz_cap, int64_t n_t,
+                                    void *out_il8, int64_t cap_out, void *stream) {
+    SS_REQUIRE(bits == 2 || bits == 4, "interleaved codes need bits 2 or 4 (got %d)", bits);
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(head_dim >= 1 && head_dim % (32 / bits) == 0, "head_dim %d cannot be packed at %d bits",
+               head_dim, bits);
+    SS_REQUIRE(group_size >= 1 && head_dim % group_size == 0,
+               "group_size %d does not divide head_dim %d", group_size, head_dim);
+    SS_REQUIRE(n_bh >= 0 && n_t >= 0, "negative sizes");
+    SS_REQUIRE(cap % (32 / bits) == 0 && n_t <= cap, "n_t %lld past the codes' cap %lld",
+               (long long)n_t, (long long)cap);
+    SS_REQUIRE(n_t <= sz_cap, "n_t %lld past the scales' cap %lld", (long long)n_t,
+               (long long)sz_cap);
+    SS_REQUIRE(cap_out % 8 == 0 && n_t <= cap_out, "n_t %lld past cap_out %lld (a multiple of 8)",
+               (long long)n_t, (long long)cap_out);
+    if (n_bh * n_t == 0) return SS_OK;
+    SS_REQUIRE(codes_il && scales && zeros && out_il8, "null pointer argument");
+    SS_UNSUPPORTED(n_bh < 65536, "too many (batch, head) rows for one launch");
+    const int vpw = 32 / bits;
+    const int64_t n_blk = (n_t + vpw - 1) / vpw;
+    const int64_t total = n_blk * head_dim;
+    SS_UNSUPPORTED(total < (1LL << 32), "too many elements for one launch");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(grouped_il_to_il8_kernel, dim3(blocks_for(total), (unsigned)n_bh), dim3(256),
+                       0, st, codes_il, cap, head_dim, bits, group_size, scales, zeros, sz_dtype,
+                       sz_cap, n_t, n_blk, reinterpret_cast<__half *>(out_il8), cap_out);
+    SS_LAUNCH_CHECK("grouped_il_to_il8_kernel launch");
     return SS_OK;
 }

@@ -517,6 +517,72 @@ def test_pack_grouped_il_roundtrip(bits, d, t_kv, cap):
     assert np.array_equal(il.cpu().numpy().view(np.uint32).astype(np.uint64), want)
 
 
+@pytest.mark.parametrize("bits,d,group,t_kv,cap,sz", [
+    (2, 128, 64, 1000, 1024, torch.float16),    # config 4's codes, ragged end
+    (4, 128, 128, 77, 96, torch.float32),       # 4-bit, one group, f32 scale/zero
+    (2, 64, 32, 301, 320, torch.float16),       # head_dim 64
+    (4, 64, 64, 8, 16, torch.float16),          # one 8-token group
+])
+def test_grouped_il_to_il8_equals_dequantise_then_interleave(bits, d, group, t_kv, cap, sz):
+    """ss_grouped_il_to_il8 (one launch) writes the same fp16 words as the
+    reference-layout dequantisation (float32) cast to fp16 and interleaved by
+    ss_append_values_il8; positions past t_kv in the last 8-token group are
+    zero and later groups are left alone."""
+    _, packed, sc, ze, il = grouped_case(40 + bits, 2, 3, t_kv, d, bits, group, cap, sz_dtype=sz)
+    dense = _hip.dequantize_values_grouped(packed[:, :, :t_kv].view(torch.uint32),
+                                           sc[:, :, :t_kv], ze[:, :, :t_kv], d, bits, group)
+    cap_out = cap + 16
+    want = torch.zeros((2, 3, cap_out // 8, d, 8), dtype=torch.float16, device=DEV)
+    _hip.append_values_il8(dense.to(torch.float16).contiguous(), want, 0)
+    got = torch.full_like(want, 7.0)
+    _hip.grouped_il_to_il8(il, bits, group, sc, ze, t_kv, got)
+    torch.cuda.synchronize()
+    n8 = (t_kv + 7) // 8
+    assert torch.equal(got[:, :, :n8].view(torch.int16), want[:, :, :n8].view(torch.int16))
+    assert bool((got[:, :, n8:] == 7.0).all())
+
+
+@pytest.mark.parametrize("dtype,use_perm,d,t_", [
+    (torch.float16, True, 128, 200),
+    (torch.bfloat16, True, 128, 33),
+    (torch.float32, False, 64, 65),
+])
+def test_raw_key_rows_are_the_power_of_two_split(dtype, use_perm, d, t_):
+    """ss_raw_key_rows from a strided window of a buffer: per token the
+    power of two 2^s with max |k| * 2^-s in [2^14, 2^15) (s = 0 for a zero
+    key), row 0 = fp16(k * 2^-s), row 1 = fp16((k * 2^-s - row 0) * 2^11),
+    written out with frexp / ldexp in float64; keys in the permuted basis.
+    For 16-bit keys row 0 + row 1 * 2^-11 times 2^s is the key exactly."""
+    g = torch.Generator(device=DEV).manual_seed(d + t_)
+    buf = torch.randn((2, 3, t_ + 40, d), generator=g, device=DEV)
+    e_lo, e_hi = (-8, 4) if dtype == torch.float16 else (-60, 60)  # per-token magnitudes
+    buf *= torch.exp2(torch.randint(e_lo, e_hi, (2, 3, t_ + 40, 1), generator=g,
+                                    device=DEV).float())
+    buf[0, 1, 5] = 0.0  # a zero key
+    buf = buf.to(dtype)
+    win = buf[:, :, 17:17 + t_]  # a window view, as the hybrid buffer hands over
+    perm = torch.randperm(d, generator=g, device=DEV).to(torch.int32) if use_perm else None
+    rows, fac = _hip.raw_key_rows(win, perm)
+    torch.cuda.synchronize()
+    k = win.double().cpu().numpy()
+    if use_perm:
+        k = k[..., perm.long().cpu().numpy()]
+    m = np.abs(k).max(axis=-1)
+    _, e = np.frexp(m)  # m = f * 2^e, f in [0.5, 1)
+    s = np.where(m > 0, e - 15, 0).clip(-126, 126)
+    ks = np.ldexp(k, -s[..., None])
+    hi = ks.astype(np.float32).astype(np.float16)
+    lo = ((ks - hi.astype(np.float64)) * 2048.0).astype(np.float32).astype(np.float16)
+    got = rows.cpu().numpy()
+    assert np.array_equal(got[..., 0, :].view(np.int16), hi.view(np.int16))
+    assert np.array_equal(got[..., 1, :].view(np.int16), lo.view(np.int16))
+    assert np.array_equal(fac.cpu().numpy(), np.ldexp(1.0, s).astype(np.float32))
+    if dtype != torch.float32:
+        back = (got[..., 0, :].astype(np.float64) + got[..., 1, :] * 2.0 ** -11) * \
+            fac.cpu().numpy()[..., None]
+        assert np.array_equal(back, k)
+
+
 @pytest.mark.parametrize(
     "b,hq,hkv,d,t_kv,t_q,bits,group,sz,causal,splits,cap",
     [
@@ -1230,6 +1296,31 @@ def test_prefill_il8_matches_oracle(b, hq, hkv, t_q, t_kv, causal, qdt, nc):
     assert np.isfinite(got).all()
     assert rel_err(got, ref) <= REL_TOL
     assert rel_err(got, ref_dec.cpu().numpy()) <= REL_TOL
+
+
+def test_prefill_il8_at_the_benchmarked_prompt():
+    """The prefill kernel at the benchmarked shape (B=1, 32 query / 8 KV
+    heads, a causal 4096-token prompt against its own cache): every row of
+    every head agrees with the decode kernel over the same prompt, and two
+    query heads (on different KV heads, all 4096 rows) with the oracle."""
+    b, hq, hkv, d, t_kv = 1, 32, 8, 128, 4096
+    cents, perm, idx, vals, q16 = decode_case(4096, b, hq, hkv, d, t_kv, t_kv)
+    scale = 1.0 / np.sqrt(d)
+    v8 = to_il8(vals, t_kv)
+    cb = _hip.codebook_f16x2(t(cents))
+    out = _hip.prefill_attn_il8(t(q16), scale, t(perm), cb, 256, t(idx), v8, t_kv, causal=True,
+                                q_offset=0, out_dtype=torch.float32)
+    ref_dec = _hip.decode_attn_il8(t(q16), scale, t(perm), t(cents), t(idx), v8, t_kv,
+                                   causal=True, q_offset=0, out_dtype=torch.float32, codebook=cb)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref_dec.cpu().numpy()) <= REL_TOL
+    for qh in (3, 21):
+        kh = qh // (hq // hkv)
+        ref = O.sdpa(q16[:, qh:qh + 1], idx[:, kh:kh + 1], vals[:, kh:kh + 1], cents, perm,
+                     scale, mask="causal")
+        assert rel_err(got[:, qh:qh + 1], ref) <= REL_TOL
 
 
 @pytest.mark.parametrize("e2", [20, -20])
