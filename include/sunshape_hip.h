@@ -333,10 +333,10 @@ int ss_prefill_attn_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads
  * are indices (idx, capacity cap), keys at t_raw0 .. t_kv - 1 (its buffered
  * full-precision tokens) are given whole in kraw [batch][n_kv_heads]
  * [t_kv - t_raw0][2][128] fp16: per token its key in the codec's basis (the
- * permutation applied, or the rotation), times 2^-s (row 0) and the
- * remainder times 2^11 (row 1), with kfac[...][token] = 2^s (float32), s
- * chosen per token so both rows hold the key exactly (fp16 or bf16 keys)
- * or to 22 bits (float32 keys).  values_il8 [batch][n_kv_heads][cap_v/8]
+ * permutation applied, or the rotation), times 2^-s, as fp16 (row 0) and
+ * the fp16 remainder (row 1), with kfac[...][token] = 2^s (float32), s
+ * chosen per token (ss_raw_key_rows) so the rows hold the key exactly (fp16
+ * or bf16 keys) or to 22 bits (float32 keys).  values_il8 [batch][n_kv_heads][cap_v/8]
  * [128][8] holds the values of all t_kv tokens.  Replaces the reference's
  * two-pass path for prompts against a cache with buffered tokens
  * (attention.py:307-350, keys scored against the unpermuted query at

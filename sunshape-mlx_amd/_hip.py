@@ -877,8 +877,9 @@ def raw_key_rows(keys: torch.Tensor, perm: torch.Tensor | None = None
     :func:`prefill_attn_il8_hybrid` in one launch (``ss_raw_key_rows``), dim j
     taken from dim ``perm[j]`` of the key (the codec's basis).  Per token s
     brings max |key| * 2^-s into [2^14, 2^15) (s = 0 for a zero key); row 0 =
-    fp16(key * 2^-s), row 1 = fp16((key * 2^-s - row 0) * 2^11), factor 2^s.
-    Both rows are exact for fp16 and bf16 keys (at most 11 significant bits)."""
+    fp16(key * 2^-s), row 1 = fp16(key * 2^-s - row 0), factor 2^s.  The
+    rows hold the scaled key to 22 bits, exactly for fp16 and bf16 keys (at
+    most 11 significant bits, row 1 = 0)."""
     require_gpu(keys)
     if keys.dim() != 4 or keys.stride(-1) != 1:
         raise ValueError("keys must be (B, H, T, D) with unit last stride")

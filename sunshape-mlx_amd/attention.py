@@ -100,7 +100,16 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
     # compressed keys from the codebook, buffered keys whole, values
     # materialised once in the interleaved fp16 layout
     b_, hq, tq, d = queries.shape
+    if buffered and cache.dtype == torch.bfloat16 and \
+            ops["kind"] in ("grouped_il", "grouped", "turboquant_il", "turboquant", "sunshape_v"):
+        # with buffered tokens the reference attends over cache.values, the
+        # dequantised values rounded to the cache dtype (cache.py:754-784,
+        # attention.py:307-350); the fused kernels keep them in float32,
+        # which for bf16 (8 significant bits) moves outputs by ~2^-9 of
+        # their scale, so bf16 caches keep the reference's two passes
+        return None
     if isinstance(cache, HybridSunShapeKVCache) and tq > 1 and ops.get("k_heavy") is None and \
+            cache.dtype == torch.float16 and \
             q.dtype in (torch.float16, torch.bfloat16) and \
             _hip.prefill_supported(hq, cache.n_kv_heads, tq, d, codec.n_blocks):
         pf = cache.prefill_operands()

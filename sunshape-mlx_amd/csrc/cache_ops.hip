@@ -29,9 +29,10 @@ __global__ void __launch_bounds__(256)
 // Whole keys for the hybrid prompt kernel: one wave per token.  Dim j of the
 // output is dim perm[j] of the key (the codec's basis; perm null = identity).
 // With s = row_exp_shift(max |key|), row 0 = fp16(key * 2^-s) and row 1 =
-// fp16((key * 2^-s - row 0) * 2^11); factor = 2^s.  Multiplying by a power of
-// two is exact, so both rows are exact for keys of at most 22 significant bits
-// whose scaled magnitude stays above fp16's subnormal range.
+// fp16(key * 2^-s - row 0); factor = 2^s.  Multiplying by a power of two is
+// exact, so row 0 + row 1 is the key times 2^-s to 22 significant bits, and
+// exactly for fp16 and bf16 keys (row 1 = 0); a remainder below fp16's
+// normal range is rounded there, under 2^-38 of the row's largest element.
 __global__ void __launch_bounds__(256)
     raw_key_rows_kernel(const void *k, int k_dtype, int64_t n_h, int64_t n_t, int64_t n_tok,
                         int64_t k_sb, int64_t k_sh, int64_t k_st, int d, const int32_t *perm,
@@ -55,7 +56,7 @@ __global__ void __launch_bounds__(256)
         const float x = load_as_f32(k, k_dtype, base + (perm ? perm[j] : j)) * down;
         const __half hi = __float2half(x);
         r0[j] = hi;
-        r0[d + j] = __float2half((x - __half2float(hi)) * 2048.f);
+        r0[d + j] = __float2half(x - __half2float(hi));
     }
     if (lane == 0) fac[n] = exp2i(s);
 }

@@ -36,13 +36,18 @@
 // 8k2+7 of lane l are row l%32's tokens 16k2 + 4(l/32) + 0..3 and
 // 16k2 + 8 + 4(l/32) + 0..3, the A operand of step k2; the legacy
 // 32x32x8 and 16x16x16 shapes issue at half the fp16 rate on gfx950), so
-// every key gather and value load serves 32 rows.  fp32 queries
+// every key gather and value load serves 32 rows.  There the key's hi and
+// lo parts accumulate into one S (the lo rows taken back to the hi units
+// in LDS) and P enters P.V as one fp16 operand (p * 2^11 rounded: each
+// weight within 2^-12 of itself), one product per k-step.  fp32 queries
 // need a second (lo) query operand, which leaves no registers for 32 rows.
 //
 // The grid is (batch x KV heads, position groups) with the position groups
 // in reverse order along y: workgroups are dispatched x fastest, so the
 // heaviest causal ranges of every head go first.
 #include "ss_common.hpp"
+
+#include <type_traits>
 
 namespace ss {
 
@@ -85,8 +90,8 @@ struct PrefillArgs {
     int64_t cap, cap_v, t_kv;
     // keys from position t_raw0 on (a hybrid cache's buffered tokens) are
     // given whole instead of as indices: kraw [B][Hkv][n_raw][2][128] fp16,
-    // per token its codec-basis key times 2^-s (hi) and the remainder times
-    // 2^11 (lo), kfac [B][Hkv][n_raw] = 2^s; t_raw0 = t_kv when there are none
+    // per token its codec-basis key times 2^-s (hi) and the remainder (lo),
+    // kfac [B][Hkv][n_raw] = 2^s; t_raw0 = t_kv when there are none
     const __half *kraw;
     const float *kfac;
     int64_t t_raw0, n_raw;
@@ -369,14 +374,19 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
 
     // 1. the prepared codebook, row-major: the hi part of row (block,
     //    centroid) at (block * 256 + centroid) * 16 bytes, its lo part 64 KB
-    //    further.  Tile t = (bg, ct) holds 64 lanes' rows: block bg*4 + l/16,
+    //    further, taken back to the hi part's units (lo * 2^-11, exact but
+    //    for lo parts below fp16's normal range, which are under 2^-38 of
+    //    the largest hi part) so both products accumulate into one S.
+    //    Tile t = (bg, ct) holds 64 lanes' rows: block bg*4 + l/16,
     //    centroid ct*16 + l%16.
     uint4 *lds4 = reinterpret_cast<uint4 *>(lds);
     for (int i = tid; i < 4 * a.nct * kWave; i += TH) {
         const int t = i >> 6, l = i & 63, bg = t / a.nct, ct = t - bg * a.nct;
         const int row = (bg * 4 + (l >> 4)) * 256 + ct * 16 + (l & 15);
         lds4[row] = a.codebook[(int64_t)t * 2 * kWave + l];
-        lds4[kPfRows16 + row] = a.codebook[(int64_t)t * 2 * kWave + kWave + l];
+        const pf_f16x8 lo = __builtin_bit_cast(pf_f16x8, a.codebook[(int64_t)t * 2 * kWave + kWave + l]) *
+                            (_Float16)(1.f / kPfSplit);
+        lds4[kPfRows16 + row] = __builtin_bit_cast(uint4, lo);
     }
 
     // 2. this lane's query row (the S^T column l%32 of wave wv): B operands
@@ -453,7 +463,12 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
     uint4 ir_a, ir_b;
     if (n_sub > 0) load_idx(ir_a, 0);
 
-    auto do_sub = [&](const uint4 &ir_cur, uint4 &ir_nxt, int sub) __attribute__((always_inline)) {
+    // raw_c: std::true_type for the sub-tiles that may reach the whole keys
+    // (from t_raw0 on), which get the per-lane key source; the others
+    // compile without it
+    auto do_sub = [&](auto raw_c, const uint4 &ir_cur, uint4 &ir_nxt, int sub)
+                      __attribute__((always_inline)) {
+        constexpr bool kRaw = decltype(raw_c)::value;
         const int t0 = 32 * sub;
         // the sub-tile's value operands (4 tokens of one dim, 8 bytes) for the
         // 4 steps of 8 tokens and 4 n-tiles of 32 dims, issued first so they
@@ -471,13 +486,14 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
         }
         load_idx(ir_nxt, min(sub + 1, n_sub - 1));
         // scores S^T[token][row] of 32 tokens x 32 rows: lane l holds row
-        // l%32 and tokens 8*(i/4) + 4*hb + i%4 (i = 0..15)
-        pf_f32x16 sh, sl;
+        // l%32 and tokens 8*(i/4) + 4*hb + i%4 (i = 0..15); the hi and lo
+        // parts of the keys accumulate into the same S
+        pf_f32x16 sv;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sh[i] = sl[i] = 0.f;
+        for (int i = 0; i < 16; ++i) sv[i] = 0.f;
         // a sub-tile reaching the whole keys (wave-uniform): lanes whose
         // token is past t_raw0 take its key rows from kraw
-        const bool raw_tile = t0 + 31 >= t_raw0;
+        const bool raw_tile = kRaw && t0 + 31 >= t_raw0;
         if (!raw_tile) {
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
@@ -488,8 +504,8 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
                 const char *row = lds + (blk * 256 + c) * 16;
                 const pf_f16x8 ah = *reinterpret_cast<const pf_f16x8 *>(row);
                 const pf_f16x8 al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
-                sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
-                sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sv, 0, 0, 0);
             }
         } else {
             const int tk = t0 + l32;
@@ -510,13 +526,10 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
                     ah = *reinterpret_cast<const pf_f16x8 *>(row);
                     al = *reinterpret_cast<const pf_f16x8 *>(row + kPfRows16 * 16);
                 }
-                sh = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sh, 0, 0, 0);
-                sl = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sl, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[ks], sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[ks], sv, 0, 0, 0);
             }
         }
-        float sv[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sv[i] = fmaf(sl[i], 1.f / kPfSplit, sh[i]);
         if (raw_tile) {
             // whole keys' scores into the codebook's units: times their own
             // 2^s and the codebook's power of two
@@ -546,24 +559,22 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
         const float mn = (mx - m) * mul > kPfLag ? fmaxf(m, mx) : m;  // raw units (mul > 0)
         const float corr = fast_exp2((m - mn) * mul);
         m = mn;
-        // x = p * 2^11 = exp2(s * mul - (mn * mul - 11)), split into fp16 hi
-        // and lo; l sums x and is scaled back at the end
+        // x = p * 2^11 = exp2(s * mul - (mn * mul - 11)), rounded to fp16:
+        // one product per k-step (each weight moves by at most 2^-12 of
+        // itself, independently of the others); l sums x and is scaled back
+        // at the end
         float ps = 0.f;
         const float off = fmaf(mn, mul, -kPfPExp);
-        pf_f16x4 phi[4], plo[4];
+        pf_f16x4 phi[4];
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) {  // pairs: one packed conversion each for hi and lo
+        for (int i = 0; i < 16; i += 2) {  // pairs: one packed conversion each
             const float x0 = fast_exp2(fmaf(sv[i], mul, -off));
             const float x1 = fast_exp2(fmaf(sv[i + 1], mul, -off));
+            const pf_f16x2 h = __builtin_convertvector((pf_f32x2){x0, x1}, pf_f16x2);
             ps += x0;
             ps += x1;
-            const pf_f16x2 h = __builtin_convertvector((pf_f32x2){x0, x1}, pf_f16x2);
-            const pf_f16x2 lo = __builtin_convertvector(
-                (pf_f32x2){__builtin_fmaf((float)h[0], -1.f, x0), __builtin_fmaf((float)h[1], -1.f, x1)}, pf_f16x2);
             phi[i >> 2][i & 3] = h[0];
             phi[i >> 2][(i & 3) + 1] = h[1];
-            plo[i >> 2][i & 3] = lo[0];
-            plo[i >> 2][(i & 3) + 1] = lo[1];
         }
         lsum = fmaf(lsum, corr, ps);
         // accumulator rows 8*(i/4) + 4*hb + i%4 take the correction of their
@@ -600,14 +611,12 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) {
             const pf_f16x8 ah = __builtin_shufflevector(phi[2 * k2], phi[2 * k2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-            const pf_f16x8 al = __builtin_shufflevector(plo[2 * k2], plo[2 * k2 + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) {
                 const pf_f16x8 b = __builtin_bit_cast(
                     pf_f16x8, make_uint4(vop[2 * k2][nt].x, vop[2 * k2][nt].y, vop[2 * k2 + 1][nt].x,
                                          vop[2 * k2 + 1][nt].y));
                 acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, b, acc[nt], 0, 0, 0);
-                acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, b, acc[nt], 0, 0, 0);
             }
         }
     };
@@ -615,9 +624,17 @@ __global__ void __launch_bounds__(kPfWaves * kWave) prefill32_il8_kernel(Prefill
     // of the accumulators for the whole loop): an odd count ends with one
     // sub-tile past the last key, whose loads clamp to the last key's rows
     // and whose scores are all masked (weights and values zero)
-    for (int sub = 0; sub < n_sub; sub += 2) {
-        do_sub(ir_a, ir_b, sub);
-        do_sub(ir_b, ir_a, sub + 1);
+    // (sub-tiles wholly below t_raw0 first, in pairs; the rest, the last
+    // plain one of an odd count included, on the code that reads whole keys)
+    const int n_plain = min(n_sub, t_raw0 / 32);
+    int sub = 0;
+    for (; sub + 1 < n_plain; sub += 2) {
+        do_sub(std::false_type{}, ir_a, ir_b, sub);
+        do_sub(std::false_type{}, ir_b, ir_a, sub + 1);
+    }
+    for (; sub < n_sub; sub += 2) {
+        do_sub(std::true_type{}, ir_a, ir_b, sub);
+        do_sub(std::true_type{}, ir_b, ir_a, sub + 1);
     }
 
     // 3. rows 8*(i/4) + 4*hb + i%4 of the accumulators: their l (the row's

@@ -321,7 +321,10 @@ def test_hybrid_grouped_interleaved_appends_and_trim(bits, group):
 ])
 def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
     """Hybrid grouped caches with buffered tokens stay on the fused kernel;
-    the result equals the reference's two-pass path over the same cache."""
+    the result equals the reference's two-pass path over the same cache.
+    bf16 caches keep the two passes: the reference rounds the dequantised
+    values to bf16 there, which the fused kernel (float32 values) would
+    not reproduce to 1e-3."""
     codec = make_codec(31)
     b, hq, hkv, d = 2, 8, 2, 128
     k, v = kv(32 + buf, b, hkv, t_total, d, dtype=dtype)
@@ -335,7 +338,8 @@ def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
     q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
     mask = "causal" if causal else None
     out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
-    assert codec.last_score_backend == "hip_fused_mfma_dequant_buffer"
+    assert codec.last_score_backend == ("hip" if dtype == torch.bfloat16
+                                        else "hip_fused_mfma_dequant_buffer")
     tc = cache.compressed_offset
     vals = cache.values.float().cpu().numpy()  # compressed values dequantised, then buffer
     ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),

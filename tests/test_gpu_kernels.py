@@ -550,9 +550,9 @@ def test_grouped_il_to_il8_equals_dequantise_then_interleave(bits, d, group, t_k
 def test_raw_key_rows_are_the_power_of_two_split(dtype, use_perm, d, t_):
     """ss_raw_key_rows from a strided window of a buffer: per token the
     power of two 2^s with max |k| * 2^-s in [2^14, 2^15) (s = 0 for a zero
-    key), row 0 = fp16(k * 2^-s), row 1 = fp16((k * 2^-s - row 0) * 2^11),
+    key), row 0 = fp16(k * 2^-s), row 1 = fp16(k * 2^-s - row 0),
     written out with frexp / ldexp in float64; keys in the permuted basis.
-    For 16-bit keys row 0 + row 1 * 2^-11 times 2^s is the key exactly."""
+    For 16-bit keys (row 0 + row 1) times 2^s is the key exactly."""
     g = torch.Generator(device=DEV).manual_seed(d + t_)
     buf = torch.randn((2, 3, t_ + 40, d), generator=g, device=DEV)
     e_lo, e_hi = (-8, 4) if dtype == torch.float16 else (-60, 60)  # per-token magnitudes
@@ -572,13 +572,13 @@ def test_raw_key_rows_are_the_power_of_two_split(dtype, use_perm, d, t_):
     s = np.where(m > 0, e - 15, 0).clip(-126, 126)
     ks = np.ldexp(k, -s[..., None])
     hi = ks.astype(np.float32).astype(np.float16)
-    lo = ((ks - hi.astype(np.float64)) * 2048.0).astype(np.float32).astype(np.float16)
+    lo = (ks - hi.astype(np.float64)).astype(np.float32).astype(np.float16)
     got = rows.cpu().numpy()
     assert np.array_equal(got[..., 0, :].view(np.int16), hi.view(np.int16))
     assert np.array_equal(got[..., 1, :].view(np.int16), lo.view(np.int16))
     assert np.array_equal(fac.cpu().numpy(), np.ldexp(1.0, s).astype(np.float32))
     if dtype != torch.float32:
-        back = (got[..., 0, :].astype(np.float64) + got[..., 1, :] * 2.0 ** -11) * \
+        back = (got[..., 0, :].astype(np.float64) + got[..., 1, :]) * \
             fac.cpu().numpy()[..., None]
         assert np.array_equal(back, k)
 
