@@ -1132,7 +1132,14 @@ def main() -> int:
         step = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
         step["t_kv_range"] = [t_kv, caches[0].offset]
         log(f"decode step end to end (update_and_fetch of one token + sunshape_sdpa): "
-            f"{step['us_per_step']:.2f} us/step (host {step['host_us_per_step']:.1f} us/step)")
+            f"{step['us_per_step']:.2f} us/step (host {step['host_us_per_step']:.1f} us/step, "
+            f"{step['backend']})")
+        # the same steps with the append as its own launch (fuse_steps off)
+        for c in caches:
+            c.fuse_steps = False
+        sep = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
+        step["separate_append"] = {k_: sep[k_] for k_ in ("us_per_step", "host_us_per_step")}
+        log(f"  ... with the append launched separately: {sep['us_per_step']:.2f} us/step")
         del caches
     ceiling = stream_ceiling(nbytes, steps, args.warmup, hip)
     log(f"read ceiling: {ceiling['us_per_launch']:.2f} us ({ceiling['gbs']:.0f} GB/s)")

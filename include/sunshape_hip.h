@@ -243,7 +243,9 @@ int ss_decode_plan(int kind, int64_t batch, int n_q_heads, int n_kv_heads, int64
  * kernel's operand order: for 4-block group bg < n_blocks/4 and centroid
  * tile ct < ceil(n_centroids/16), tile (bg*ceil(n_centroids/16) + ct) holds
  * hi[64][8] then lo[64][8], row l being centroid ct*16 + l%16 of block
- * bg*4 + l/16 (zero past the last centroid); the float 2^e follows.
+ * bg*4 + l/16 (zero past the last centroid); the float 2^e follows in a
+ * 16-byte field, then |C|^2 (float32, unscaled) of every tile row in the
+ * same order (the exact encode of ss_decode_step_il8 uses them).
  * n_blocks must be a multiple of 4.  ss_codebook_f16x2_bytes gives the
  * size; out must be 16-byte aligned.
  */
@@ -628,6 +630,33 @@ int ss_decode_attn_grouped_il_hybrid(const void *q, int q_dtype, int64_t batch, 
 int ss_pack_grouped_il(const uint32_t *packed, int64_t n_b, int64_t n_h, int64_t n_t,
                        int64_t p_sb, int64_t p_sh, int64_t p_st, int head_dim, int bits,
                        uint32_t *out_il, int64_t cap, int64_t offset, void *stream);
+
+/*
+ * One decode step of an fp16-value cache in one launch: the cache holds
+ * t_cache tokens (idx [batch][n_kv_heads][cap][n_blocks], values_il8 as
+ * ss_decode_attn_il8), and the step's n_new (1..4) new tokens arrive as fp16
+ * keys / values at k_new / v_new [b*kv_sb + h*kv_sh + j*kv_st + dim].  The
+ * kernel encodes the new keys (indices identical to ss_append_kv_il8's:
+ * key . centroid products on the matrix cores from the prepared codebook,
+ * accepted under a proven float error bound, else ranked exactly over the
+ * float32 centroids), attends all t_cache + n_new tokens as
+ * ss_decode_attn_il8 would after the append (the new tokens' weights and
+ * values in float32), and stores the new tokens' index rows and values at
+ * positions t_cache .. t_cache + n_new - 1.  Replaces the reference's decode
+ * step, update_and_fetch (cache.py:156-205) followed by the fused attention
+ * (kernels.py:142-230, attention.py:236-305), which touch the cache twice.
+ * Other arguments as ss_decode_attn_il8; centroids float32
+ * [n_blocks][n_centroids][8] (16-byte aligned), codebook their
+ * ss_codebook_f16x2.  Calls sharing a cache must not overlap.
+ */
+int ss_decode_step_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads,
+                       int64_t t_q, int head_dim, float scale, const int32_t *perm,
+                       const void *codebook, const float *centroids, int n_blocks,
+                       int n_centroids, uint8_t *idx, void *values_il8, int64_t cap,
+                       int64_t t_cache, const void *k_new, const void *v_new, int kv_dtype,
+                       int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t n_new, int causal,
+                       int64_t q_offset, void *out, int out_dtype, void *workspace,
+                       size_t workspace_bytes, int n_splits, void *stream);
 
 /*
  * The inverse of ss_pack_grouped_il: the first n_t tokens of interleaved

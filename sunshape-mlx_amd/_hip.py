@@ -93,6 +93,11 @@ _SIGNATURES = {
         _c_void_p, _c_void_p, _int, _i64, _i64,
         _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
         _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_step_il8": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _c_void_p,
+        _int, _int, _c_void_p, _c_void_p, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_prefill_rows_per_workgroup": (_int, []),
     "ss_prefill_attn_il8": (_int, [_c_void_p, _int, _i64, _int, _int, _i64, _int, _f32,
                                    _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p, _int,
@@ -467,6 +472,92 @@ class PreparedDecodeBuffered(PreparedDecode):
         if _check_waits:
             check_decode_waits(self.dev)
         return out
+
+
+MAX_STEP_TOKENS = 4  # new tokens one fused decode step takes (kMaxStepTokens)
+
+
+class PreparedDecodeStep(PreparedDecode):
+    """One decode step of an fp16-value cache in one launch
+    (``ss_decode_step_il8``): a call passes the step's new keys and values
+    (B, Hkv, n_new, D) float16 (equal strides, unit last stride) and the
+    number of tokens already in the cache; the kernel encodes the new keys,
+    attends all tokens and stores the new ones at positions t_cache ..
+    t_cache + n_new - 1."""
+
+    __slots__ = ()
+
+    def __call__(self, q: torch.Tensor, t_cache: int, k_new: torch.Tensor, v_new: torch.Tensor,
+                 causal: bool = False, q_offset: int = 0, out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if q.shape != self.shape or q.dtype != self.dtype or not q.is_contiguous() or \
+                q.device.index != self.dev:
+            raise ValueError(f"query must be contiguous {self.dtype} {self.shape} on cuda:{self.dev}")
+        st3 = k_new.stride()[:3]
+        if k_new.dtype != torch.float16 or v_new.dtype != torch.float16 or \
+                k_new.shape != v_new.shape or v_new.stride()[:3] != st3 or \
+                k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or \
+                k_new.device.index != self.dev or v_new.device.index != self.dev:
+            raise ValueError("new keys and values must be float16 (B, Hkv, n, D) with equal "
+                             "strides and unit last stride")
+        if out is None:
+            out = torch.empty(self.shape, dtype=out_dtype or self.dtype, device=q.device)
+        elif tuple(out.shape) != self.shape or not out.is_contiguous() or out.device != q.device:
+            raise ValueError(f"out must be contiguous {self.shape} on cuda:{self.dev}")
+        _poll_waits(self.dev)
+        st = stream_handle(self.dev)
+        ws = _ws_cache.get((self.dev, st))
+        if ws is None:
+            ws = decode_workspace(self.dev, 1, st)
+        mid = (int(t_cache), k_new.data_ptr(), v_new.data_ptr(), SS_F16, *st3,
+               int(k_new.shape[2]), int(bool(causal)), int(q_offset), out.data_ptr(),
+               dtype_code(out.dtype))
+        rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        if rc == SS_ERR_WORKSPACE:
+            _, need = decode_plan(KIND_IL8, *self.plan_args, int(t_cache), 0)
+            ws = decode_workspace(self.dev, need, st)
+            rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        _launched(_attn_stat(self.stat, causal), rc)
+        if _check_waits:
+            check_decode_waits(self.dev)
+        return out
+
+
+def prepare_decode_step_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                            codebook: torch.Tensor, centroids: torch.Tensor, n_blocks: int,
+                            n_centroids: int, idx: torch.Tensor,
+                            values_il8: torch.Tensor) -> PreparedDecodeStep:
+    """:class:`PreparedDecodeStep` for queries shaped like ``q`` over the
+    cache buffers ``idx`` / ``values_il8`` (written by the call), with the
+    float32 ``centroids`` (n_blocks, n_centroids, 8) for the exact encode and
+    their prepared ``codebook`` for the LUT."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(values_il8, codebook, centroids)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if nb != n_blocks or values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    if centroids.dtype != torch.float32 or not centroids.is_contiguous() or \
+            tuple(centroids.shape) != (n_blocks, n_centroids, 8):
+        raise ValueError(f"centroids must be contiguous float32 {(n_blocks, n_centroids, 8)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(n_blocks, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+           ptr(centroids), nb, n_centroids, ptr(idx), ptr(values_il8), cap)
+    return PreparedDecodeStep(lib.ss_decode_step_il8, pre, q, "sunshape_fused_attention_mfma")
+
+
+def decode_step_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                    codebook: torch.Tensor, centroids: torch.Tensor, idx: torch.Tensor,
+                    values_il8: torch.Tensor, t_cache: int, k_new: torch.Tensor,
+                    v_new: torch.Tensor, causal: bool = False, q_offset: int = 0,
+                    out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """One launch of :class:`PreparedDecodeStep` (checks every call)."""
+    nb, nc = int(centroids.shape[0]), int(centroids.shape[1])
+    plan = prepare_decode_step_il8(q, scale, perm, codebook, centroids, nb, nc, idx, values_il8)
+    return plan(q, t_cache, k_new, v_new, causal, q_offset, out_dtype=out_dtype)
 
 
 def prepare_decode_il8(q: torch.Tensor, scale: float, perm: torch.Tensor | None,

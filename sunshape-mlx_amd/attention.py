@@ -85,12 +85,50 @@ def _prepared_decode(cache, ops: dict, codec: SunShapeBlockCodec, q: torch.Tenso
     return plan
 
 
+def _fused_step(cache: SunShapeKVCache, queries: torch.Tensor, scale: float, causal: bool,
+                q_offset: int, out_dtype: torch.dtype):
+    """The decode step whose new tokens the cache holds back
+    (``cache.fuse_steps``): one ``ss_decode_step_il8`` launch encodes them,
+    attends every token and stores them; None (tokens still held) when that
+    launch does not apply."""
+    codec = cache.codec
+    q, kscale, perm = _kernel_query(codec, queries, scale)
+    tensors = (cache._key_indices, cache._values, codec.kernel_codebook(), codec.centroids)
+    if perm is not None:
+        tensors += (perm,)
+    key = ("step", q.shape, q.dtype, q.device, kscale)
+    held = getattr(cache, "_step_prepared", None)
+    if held is not None and held[0] == key and len(held[1]) == len(tensors) and \
+            all(r() is t for r, t in zip(held[1], tensors)):
+        plan = held[2]
+    else:
+        try:
+            plan = _hip.prepare_decode_step_il8(q, kscale, perm, tensors[2], codec.centroids,
+                                                codec.n_blocks, codec.n_centroids,
+                                                cache._key_indices, cache._values)
+        except (_hip.SunShapeUnsupported, ValueError):
+            return None
+        cache._step_prepared = (key, tuple(weakref.ref(t) for t in tensors), plan)
+    k, v, pos = cache._take_pending()
+    try:
+        out = plan(q, pos, k, v, causal, q_offset, out_dtype=out_dtype)
+    except _hip.SunShapeUnsupported:
+        cache._pending = (k, v, k._version, v._version, pos)
+        return None
+    codec.last_score_backend = "hip_fused_mfma_step"
+    return out
+
+
 def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int,
            out_dtype: torch.dtype):
     """One fused launch over the whole cache, or None when no fused kernel
     applies to this cache / shape (the reference's None-fallback,
     kernels.py:259-291)."""
-    ops = cache.fused_operands()
+    if getattr(cache, "_pending", None) is not None and queries.shape[2] <= _hip.MAX_STEP_TOKENS:
+        out = _fused_step(cache, queries, scale, causal, q_offset, out_dtype)
+        if out is not None:
+            return out
+    ops = cache.fused_operands()  # (stores held tokens first)
     if ops is None:
         return None
     codec = cache.codec

@@ -155,6 +155,13 @@ class SunShapeKVCache:
         # both returned tensors are DeferredTensors, built only if read.
         self.return_dequantized_keys = return_dequantized_keys
         self.lazy_fetch = lazy_fetch
+        # With lazy_fetch, a decode step's few new fp16 tokens are held back
+        # (their tensors, not copies) and stored by the next attention call
+        # in its own launch (encode, attend, store); anything that reads the
+        # storage first stores them.  Tensors passed to update_and_fetch
+        # must then not be modified in place before that (checked: raises).
+        self.fuse_steps = True
+        self._pending = None  # (keys, values, their _version counters, position)
         self._version = 0  # bumped by every change of the stored tokens
         self._append_plan = None
         self._key_indices: torch.Tensor | None = None  # (B, H, cap, NB) uint8
@@ -188,12 +195,20 @@ class SunShapeKVCache:
         assert h_ == self.n_kv_heads, f"Expected {self.n_kv_heads} kv heads, got {h_}"
         assert d == self.head_dim, f"Expected head_dim {self.head_dim}, got {d}"
         _hip.require_gpu(keys, values)
+        self.flush()
         self._ensure_capacity(b_, t_, keys.device)
         plan = self._append_kv_plan()
         if plan is not None:  # encode + value store, one launch per decode step
             k = keys if keys.stride(-1) == 1 else keys.contiguous()
             v = values if values.stride(-1) == 1 else values.contiguous()
-            plan(k, v, self.offset)
+            if self.fuse_steps and self.lazy_fetch and self.offset > 0 and \
+                    1 <= t_ <= _hip.MAX_STEP_TOKENS and k.dtype == torch.float16 and \
+                    v.dtype == torch.float16 and k.stride()[:3] == v.stride()[:3] and \
+                    tuple(v.shape) == tuple(k.shape):
+                # held for the next attention call's fused step
+                self._pending = (k, v, k._version, v._version, self.offset)
+            else:
+                plan(k, v, self.offset)
         else:
             sl = slice(self.offset, self.offset + t_)
             _encode_into(self.codec, keys, self._key_indices[:, :, sl])
@@ -207,6 +222,24 @@ class SunShapeKVCache:
         keys_out = (_fetched(self, lambda: self.keys, b_, self.head_dim, torch.float32)
                     if self.return_dequantized_keys else None)
         return keys_out, _fetched(self, lambda: self.values, b_, self.head_dim, self.dtype)
+
+    def _take_pending(self):
+        """The held step's (keys, values, position), cleared; raises if a
+        tensor was modified in place since update_and_fetch received it."""
+        k, v, kv_, vv_, pos = self._pending
+        self._pending = None
+        if k._version != kv_ or v._version != vv_:
+            raise RuntimeError("keys/values passed to update_and_fetch were modified in place "
+                               "before the cache stored them; pass fresh tensors, or set "
+                               "cache.fuse_steps = False")
+        return k, v, pos
+
+    def flush(self) -> None:
+        """Store a held decode step's tokens now (one append launch)."""
+        if self._pending is None:
+            return
+        k, v, pos = self._take_pending()
+        self._append_kv_plan()(k, v, pos)
 
     def _append_kv_plan(self):
         """The prepared ``ss_append_kv_il8`` for the current buffers and
@@ -229,6 +262,7 @@ class SunShapeKVCache:
     @property
     def keys(self) -> torch.Tensor:
         """Dequantised keys up to ``offset`` (float32)."""
+        self.flush()
         if self._key_indices is None or self.offset == 0:
             dev = self.codec.device
             return torch.zeros((1, self.n_kv_heads, 0, self.head_dim), dtype=torch.float32,
@@ -239,6 +273,7 @@ class SunShapeKVCache:
     def values(self) -> torch.Tensor:
         """Values up to ``offset``, token-major (B, H, T, D) (a copy when the
         storage is interleaved)."""
+        self.flush()
         if self._values is None or self.offset == 0:
             return torch.zeros((1, self.n_kv_heads, 0, self.head_dim), dtype=self.dtype,
                                device=self.codec.device)
@@ -249,6 +284,7 @@ class SunShapeKVCache:
     def fused_operands(self) -> dict | None:
         """Full-capacity device buffers for the fused decode kernels:
         {"kind": "il8"|"dense", "idx", "values"}; None when empty."""
+        self.flush()
         if self._key_indices is None or self.offset == 0:
             return None
         return {"kind": "il8" if self.values_interleaved else "dense",
@@ -256,6 +292,7 @@ class SunShapeKVCache:
 
     @property
     def key_indices(self) -> torch.Tensor:
+        self.flush()
         if self._key_indices is None or self.offset == 0:
             return torch.zeros((1, self.n_kv_heads, 0, self.n_blocks), dtype=torch.uint8,
                                device=self.codec.device)
@@ -263,6 +300,7 @@ class SunShapeKVCache:
 
     @property
     def state(self):
+        self.flush()
         z = torch.zeros((1,))
         return (self._key_indices[:, :, :self.offset] if self._key_indices is not None else z,
                 self.values if self._values is not None else z)
@@ -293,6 +331,7 @@ class SunShapeKVCache:
         return True
 
     def trim(self, n: int) -> None:
+        self.flush()
         self.offset = max(0, self.offset - n)
         self._version += 1
 

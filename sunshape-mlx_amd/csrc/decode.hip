@@ -25,7 +25,7 @@
 #include <mutex>
 #include <type_traits>
 
-#include "ss_common.hpp"
+#include "encode_wave.hpp"
 
 namespace ss {
 
@@ -51,6 +51,10 @@ struct DecodeCommon {
     int causal;
     int64_t q_offset;
     int n_splits, tiles_per_split;
+    // matrix-core kernel: tokens (a multiple of 8) every split but the last
+    // takes beyond tiles_per_split * 64, so the last split, which then
+    // ends at t_kv with that many fewer, has room for a fused step's work
+    int split_pad = 0;
     // bounded waits of the matrix-core kernel: sleeps before a wait gives
     // up, and the sticky per-device word a give-up sets (kWait* bits)
     int spin_limit;
@@ -932,6 +936,12 @@ __device__ __forceinline__ void wait_oldest_tile(int k) {
     }
 }
 
+// Value formats that append a fused decode step's tokens (kStepShare).
+template <class VF, class = void>
+struct StepShareOf : std::false_type {};
+template <class VF>
+struct StepShareOf<VF, std::void_t<decltype(VF::kStepShare)>> : std::bool_constant<VF::kStepShare> {};
+
 template <int D, int NC, class VF>
 struct WsCfg {
     static constexpr int kNB = D / kBlockDim;
@@ -949,7 +959,10 @@ struct WsCfg {
     // the split's share of a hybrid cache's token buffer: its query copy,
     // then its (m[R], l[R], acc[R][D]) partial
     static constexpr int kBufPart = VF::kHybridBuffer ? (2 * kMfmaRows + kMfmaRows * D) * 4 : 0;
-    static constexpr int kRing = kLut + kPst + kFlags + kBufPart;
+    // a fused step's new index rows (4 tokens x NB bytes, 64 reserved) and
+    // its encode's per-wave candidates (NC x 4 blocks x 4 tokens x 16 B)
+    static constexpr int kStepLds = StepShareOf<VF>::value ? 64 + NC * 16 * 16 : 0;
+    static constexpr int kRing = kLut + kPst + kFlags + kBufPart + kStepLds;
     static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
     static constexpr int kSlots = kSlotsFit < VF::kMaxSlots ? kSlotsFit : VF::kMaxSlots;
     static constexpr int kLoadsPerTile = VF::kLoadsV + kLoadsI;
@@ -1133,6 +1146,37 @@ struct VIl8Hyb : VIl8<D> {
     static constexpr bool kHybridBuffer = true;
     static constexpr bool kHeavyCapable = true;
 };
+
+// VIl8 for one decode step that also appends its tokens: the cache holds
+// t_kv tokens and the step's n_new newest (keys and values at
+// kbuf / vbuf [b*buf_sb + h*buf_sh + j*buf_st + dim], t_buf = n_new) arrive
+// with the call.  The last split encodes their keys exactly (the float32
+// centroids, as the encoder), scores them from the LUT by their indices, as
+// the cache's own tokens, and attends them with its tiles (the buffer-share
+// partial of VIl8Hyb); the last split of row group 0 of each (batch, KV
+// head) also writes their index rows and fp16 values into the cache at
+// positions t_kv .. t_kv + n_new - 1, which the next call reads.
+template <int D>
+struct VIl8Step : VIl8<D> {
+    struct Args {
+        const __half *v8;
+        const void *kbuf, *vbuf;
+        int buf_dtype;
+        int64_t buf_sb, buf_sh, buf_st, t_buf;
+        const float *centroids;  // [n_blocks][n_centroids][8] float32
+        const float *cb_norms;   // |C|^2 per prepared codebook lane (ss_codebook_f16x2)
+        uint8_t *idx_out;        // the index cache the kernel reads (c.idx)
+        __half *v8_out;          // the value cache (v8)
+    };
+    static constexpr bool kHybridBuffer = true;
+    static constexpr bool kStepShare = true;
+    static constexpr bool kHeavyCapable = false;
+};
+constexpr int kMaxStepTokens = 4;  // new tokens of one fused decode step (A rows 4s + r)
+// cache tokens the last split of a fused step hands to the other splits
+// (about the time of its encode and share)
+constexpr int64_t kStepShareTokens = 192;
+
 
 // Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
 __device__ __forceinline__ uint32_t bf16x2_rn(float a, float b) {
@@ -1710,6 +1754,11 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // buffer partial: m [R], l [R], acc [R][D] (acc holds the query copy
     // until the share is done)
     float *bpart = reinterpret_cast<float *>(smem + K::kLut + K::kPst + K::kFlags);
+    // a fused step's new tokens' index rows [kMaxStepTokens][NB] (the step
+    // share scores them from the LUT)
+    uint8_t *step_idx = reinterpret_cast<uint8_t *>(smem + K::kLut + K::kPst + K::kFlags + K::kBufPart);
+    // and the encode's per-wave candidates [NC][4 blocks][4 tokens]
+    f32x4 *step_part = reinterpret_cast<f32x4 *>(step_idx + 64);
     // 16-byte LUT reads through the LDS object itself (an address-space
     // cast the compiler folds to the constant LDS address)
     const lds_t<f32x4> *lut_l = (const lds_t<f32x4> *)smem4;
@@ -1732,8 +1781,9 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     };
     auto row_ok = [&](int r) -> bool { return (int64_t)rg * R + r < c.rows_total; };
 
-    const int64_t t_beg = (int64_t)split * c.tiles_per_split * kWave;
-    const int64_t t_end = min(c.t_kv, t_beg + (int64_t)c.tiles_per_split * kWave);
+    const int64_t span = (int64_t)c.tiles_per_split * kWave + c.split_pad;
+    const int64_t t_beg = (int64_t)split * span;
+    const int64_t t_end = min(c.t_kv, t_beg + span);
     // 64-token units (one per compute step) and ring tiles of kSub units
     const int n_units = t_end > t_beg ? (int)((t_end - t_beg + kWave - 1) / kWave) : 0;
     const int n_tiles = (n_units + K::kSub - 1) / K::kSub;
@@ -1743,9 +1793,11 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // this split's share of the token buffer (wave-uniform)
     int64_t t_buf = 0;
     if constexpr (VF::kHybridBuffer) t_buf = va.t_buf;
-    const int64_t bshare = (t_buf + c.n_splits - 1) / c.n_splits;
-    const int64_t bj0 = min((int64_t)split * bshare, t_buf);
-    const int64_t bj1 = min(bj0 + bshare, t_buf);
+    constexpr bool kStep = StepShareOf<VF>::value;
+    // (a fused step's new tokens all go to the last split)
+    const int64_t bshare = kStep ? t_buf : (t_buf + c.n_splits - 1) / c.n_splits;
+    const int64_t bj0 = kStep ? 0 : min((int64_t)split * bshare, t_buf);
+    const int64_t bj1 = kStep ? (split == c.n_splits - 1 ? t_buf : 0) : min(bj0 + bshare, t_buf);
     const bool has_buf = VF::kHybridBuffer && bj1 > bj0;
 
     // Barrier that orders LDS only: a wave's outstanding global loads (the
@@ -1884,6 +1936,11 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // unpermuted scaled query, before its tiles; the share's (m, l, acc)
     // join the workgroup combine as one more wave.  Keys in log2 units, as
     // the LUT.
+    // a fused step's new tokens (the last split): key and value dims
+    // lane + 64k of each, loaded in the prologue
+    constexpr int DLs = kStep ? D / kWave : 1;
+    constexpr int NS = kStep ? kMaxStepTokens : 1;
+    float kpre[NS][DLs], vpre[NS][DLs];
     auto buffer_share = [&](const auto &bv) {
         constexpr int DL = D / kWave;  // value dims per lane
         float bm[R], bl[R], ba[R][DL];
@@ -1902,24 +1959,37 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             const bool ok = j < bj1;
             const int64_t ko = head + (ok ? j : j0) * bv.buf_st;
             float sc[R] = {};
-            for (int d0 = 0; d0 < D; d0 += 8) {
-                float kx[8];
-                if (bv.buf_dtype == SS_F16) {
-                    unpack16<__half>(*reinterpret_cast<const uint4 *>(
-                                         static_cast<const __half *>(bv.kbuf) + ko + d0),
-                                     kx);
-                } else {
+            if constexpr (kStep) {
+                // a new token: its encoded index row (LDS) scored from the
+                // LUT, already in log2 units
+                const lds_t<uint8_t> *row = to_lds<uint8_t>(step_idx) + (ok ? j : j0) * NB;
+                f32x4 e = lut_l[row[0]];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) kx[i] = load_as_f32(bv.kbuf, bv.buf_dtype, ko + d0 + i);
+                for (int b = 1; b < NB; ++b) e += lut_l[b * kLutStride + row[b]];
+#pragma unroll
+                for (int r = 0; r < R; ++r) sc[r] = e[r];
+            } else {
+                for (int d0 = 0; d0 < D; d0 += 8) {
+                    float kx[8];
+                    if (bv.buf_dtype == SS_F16) {
+                        unpack16<__half>(*reinterpret_cast<const uint4 *>(
+                                             static_cast<const __half *>(bv.kbuf) + ko + d0),
+                                         kx);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) kx[i] = load_as_f32(bv.kbuf, bv.buf_dtype, ko + d0 + i);
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) sc[r] = fmaf(bq[r * D + d0 + i], kx[i], sc[r]);
                 }
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) sc[r] = fmaf(bq[r * D + d0 + i], kx[i], sc[r]);
+                for (int r = 0; r < R; ++r) sc[r] *= kLog2e;
             }
             const int64_t pos = c.t_kv + j;
 #pragma unroll
-            for (int r = 0; r < R; ++r) sc[r] = (ok && pos <= lim[r]) ? sc[r] * kLog2e : -INFINITY;
+            for (int r = 0; r < R; ++r) sc[r] = (ok && pos <= lim[r]) ? sc[r] : -INFINITY;
             float tmax[R], p[R], corr[R];
             wave_max4_dpp(sc, tmax);
 #pragma unroll
@@ -1966,7 +2036,19 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     }
                 }
             };
-            if (bv.buf_dtype == SS_F16)
+            if constexpr (kStep) {
+                // a fused step's values, prefetched into registers
+#pragma unroll
+                for (int u = 0; u < kMaxStepTokens; ++u) {
+                    if (u < nj) {
+                        const f32x4 pj = pb[u];
+#pragma unroll
+                        for (int k = 0; k < DL; ++k)
+#pragma unroll
+                            for (int r = 0; r < R; ++r) ba[r][k] = fmaf(pj[r], vpre[u][k], ba[r][k]);
+                    }
+                }
+            } else if (bv.buf_dtype == SS_F16)
                 pv(__half{});
             else if (bv.buf_dtype == SS_BF16)
                 pv(__hip_bfloat16{});
@@ -2067,6 +2149,51 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             for (; nq < K::kPrivSlots && wv + nq * NC < n_units; ++nq)
                 issue_at(wv + nq * NC, ring_l + priv_slot(nq));
         }
+        // A fused step's last split: the new tokens' key and value rows
+        // (lane: dims lane + 64k), the permutation entries of the key dims
+        // its A lanes hold and its centroids' norms load here, before the
+        // loader streams anything, so none of them waits behind its tiles
+        const int n_step = kStep && has_buf ? (int)bj1 : 0;
+        int pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        float nrm[kStep ? LT : 1];
+        if constexpr (kStep) {
+            if (has_buf) {
+                // (float16 tokens, checked on the host: plain 2-byte loads,
+                // all in flight together)
+                const int64_t head = bb * va.buf_sb + kvh * va.buf_sh;
+                const __half *kh = static_cast<const __half *>(va.kbuf);
+                const __half *vh = static_cast<const __half *>(va.vbuf);
+                __half kraw[NS][DLs], vraw[NS][DLs];
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int k = 0; k < DLs; ++k) {
+                        const int64_t o = head + (int64_t)min(j, n_step - 1) * va.buf_st + lane + kWave * k;
+                        kraw[j][k] = kh[o];
+                        vraw[j][k] = vh[o];
+                    }
+#pragma unroll
+                for (int j = 0; j < NS; ++j)
+#pragma unroll
+                    for (int k = 0; k < DLs; ++k) {
+                        kpre[j][k] = __half2float(kraw[j][k]);
+                        vpre[j][k] = __half2float(vraw[j][k]);
+                    }
+                // lane l of the key products holds K slice l/16 (block
+                // (wv*LT/16)*4 + l/16) of row l%16
+                const int kb = ((wv * LT) / 16) * 4 + g;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pk[i] = c.perm ? c.perm[kb * 8 + i] : kb * 8 + i;
+                // (the prepared tiles' order; tiles past the last centroid
+                // reread the last one, as the LUT build's loads)
+                const int nct = (c.n_centroids + 15) / 16;
+#pragma unroll
+                for (int t = 0; t < LT; ++t) {
+                    const int flat = wv * LT + t;
+                    nrm[t] = va.cb_norms[((flat / 16) * nct + min(flat % 16, nct - 1)) * kWave + lane];
+                }
+            }
+        }
         lds_barrier();  // small loads issued, flags initialised
         // query elements: round_to(q_dtype, q * scale) (attention.py:208)
 #pragma unroll
@@ -2085,7 +2212,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                         qv = __uint_as_float(h << 16);
                 }
                 qraw[e] = round_to(c.q_dtype, qv * c.scale);
-                if (has_buf) bpart[2 * R + e] = qraw[e];
+                if (has_buf && !kStep) bpart[2 * R + e] = qraw[e];
             }
         }
         compute_barrier(1);  // raw query staged
@@ -2182,6 +2309,109 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             else
                 build(std::true_type{});
         }
+        // a fused step's new keys, this lane's block (token l%4's dims in A
+        // lanes), and |k|^2 of its block for the four tokens
+        float kd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float kkr[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (kStep) {
+            if (has_buf) {
+                // The new tokens' keys encoded from the codebook operands
+                // this wave holds for the LUT (its 4 blocks x 256 centroids):
+                // the key . centroid products on the matrix cores (token r of
+                // block bg*4 + s in A row 4s + r, fp16 keys exact), then
+                // D'(c) = |k|^2 + |C_c|^2 - 2 k . C_c in float32, |C_c|^2 from
+                // the prepared codebook.  The prepared centroids hold 22 bits
+                // (|C - C'| <= 2^-22 |C| per element, plus a floor under 2^-45
+                // of the largest), so |D' - D| <= E = 2^-20 (|k| + max|C|)^2 +
+                // 2^-31 m |k| (m the codebook's power-of-two scale, the
+                // product and sum roundings included): when the runner-up
+                // clears the best by 2E the best is the exact nearest centroid;
+                // otherwise the block is ranked exactly (the encoder's
+                // exact_block_wave over the float32 centroids).
+                const int bg = (wv * LT) / 16;
+                const int ar = l16 & 3;
+                const bool a_row = (l16 >> 2) == g;
+#pragma unroll
+                for (int j = 0; j < NS; ++j) {
+                    if (j < n_step) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const int p = min(max(pk[i], 0), D - 1);
+                            const float x0 = __shfl(kpre[j][0], p & (kWave - 1));
+                            const float x1 = __shfl(kpre[j][DLs - 1], p & (kWave - 1));
+                            kd[i] = ar == j ? ((p >> 6) ? x1 : x0) : kd[i];
+                        }
+                    }
+                }
+                f16x8 ak;
+                float kk = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const bool live = a_row && ar < n_step;
+                    ak[i] = live ? (_Float16)kd[i] : (_Float16)0.f;
+                    kk = fmaf(kd[i], kd[i], kk);
+                }
+                // |k|^2 of (this lane's block g, token r) sits in lane 20g + r
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kkr[r] = __shfl(kk, 20 * g + r);
+                const float m2 = -2.f * cb_mul;
+                float best[4], second[4], nmax = 0.f;
+                int bidx[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    best[r] = INFINITY;
+                    second[r] = INFINITY;
+                    bidx[r] = 0x7fffffff;
+                }
+                const int nct_ = (c.n_centroids + 15) / 16;
+#pragma unroll
+                for (int t = 0; t < LT; ++t) {
+                    const f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const f32x4 dh = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        ak, __builtin_bit_cast(f16x8, cb_hi[t]), z, 0, 0, 0);
+                    const f32x4 dl = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        ak, __builtin_bit_cast(f16x8, cb_lo[t]), z, 0, 0, 0);
+                    const int ct = (wv * LT + t) % 16;
+                    const int cc = ct * 16 + l16;
+                    if (ct < nct_ && cc < c.n_centroids) {
+                        nmax = fmaxf(nmax, nrm[t]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float dot = dh[r] + dl[r] * (1.f / kSplitScale);
+                            const float dd = fmaf(m2, dot, kkr[r] + nrm[t]);
+                            const bool lt = dd < best[r];
+                            second[r] = lt ? best[r] : fminf(second[r], dd);
+                            bidx[r] = lt ? cc : bidx[r];
+                            best[r] = lt ? dd : best[r];
+                        }
+                    }
+                }
+                // the 16 lanes of each block: (best, runner-up, index), the
+                // largest norm
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    nmax = fmaxf(nmax, __shfl_xor(nmax, o));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float ob = __shfl_xor(best[r], o), os = __shfl_xor(second[r], o);
+                        const int oi = __shfl_xor(bidx[r], o);
+                        const bool mine = best[r] < ob || (best[r] == ob && bidx[r] < oi);
+                        second[r] = mine ? fminf(second[r], ob) : fminf(os, best[r]);
+                        best[r] = mine ? best[r] : ob;
+                        bidx[r] = mine ? bidx[r] : oi;
+                    }
+                }
+                // this wave's candidates: (best, runner-up, index, largest
+                // norm) per (block, token), merged below with the waves that
+                // hold the group's other centroid tiles (head_dim 64)
+                if (l16 == 0) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        step_part[(wv * 4 + g) * 4 + r] =
+                            f32x4{best[r], second[r], __int_as_float(bidx[r]), nmax};
+                }
+            }
+        }
         // fp16 heavy-block key dims (mixed-precision codecs; their LUT
         // entries are zero): A operands of v_mfma_f32_4x4x4f16 products with
         // each token's own dims, query row lane%4, dims 4kk .. 4kk+3, split
@@ -2206,6 +2436,76 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             }
         }
         compute_barrier(3);  // LUT complete (the query in LDS is read for the last time)
+        if constexpr (kStep) {
+            if (has_buf) {
+                // the first wave of each block group merges the group's
+                // waves' candidates (16 / LT of them) and decides
+                constexpr int WPG = 16 / LT;  // waves per 4-block group
+                if ((wv * LT) % 16 == 0) {
+                    const int bg = (wv * LT) / 16;
+                    uint32_t need = 0u;
+                    if (l16 == 0) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (r < n_step) {
+                                f32x4 a = step_part[(wv * 4 + g) * 4 + r];
+#pragma unroll
+                                for (int w2 = 1; w2 < WPG; ++w2) {
+                                    const f32x4 o = step_part[((wv + w2) * 4 + g) * 4 + r];
+                                    const int ai = __float_as_int(a[2]), oi = __float_as_int(o[2]);
+                                    const bool mine = a[0] < o[0] || (a[0] == o[0] && ai < oi);
+                                    const float sec = mine ? fminf(a[1], o[0]) : fminf(o[1], a[0]);
+                                    a = mine ? f32x4{a[0], sec, a[2], fmaxf(a[3], o[3])}
+                                             : f32x4{o[0], sec, o[2], fmaxf(a[3], o[3])};
+                                }
+                                const float kn = __builtin_sqrtf(kkr[r]);
+                                const float a2 = kn + __builtin_sqrtf(a[3]);
+                                const float e = fmaf(0x1p-20f * a2, a2, 0x1p-31f * cb_mul * kn);
+                                const int bi = __float_as_int(a[2]);
+                                const bool ok = a[1] - a[0] > 2.f * e && bi != 0x7fffffff;
+                                if (ok) step_idx[r * NB + bg * 4 + g] = (uint8_t)bi;
+                                need |= ok ? 0u : (1u << r);
+                            }
+                        }
+                    }
+                    // exact ranking for the pairs not cleared (rare): the whole
+                    // wave over the float32 centroids, one pair at a time
+#pragma unroll
+                    for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const bool any =
+                                __builtin_amdgcn_ballot_w64(g == s2 && ((need >> r) & 1u)) != 0;
+                            if (any) {
+                                float kv[8];
+#pragma unroll
+                                for (int i = 0; i < 8; ++i) kv[i] = __shfl(kd[i], 20 * s2 + r);
+                                const int b = bg * 4 + s2;
+                                const int bi = exact_block_wave<8>(
+                                    kv, va.centroids + (int64_t)b * c.n_centroids * 8, c.n_centroids, lane);
+                                if (lane == 0) step_idx[r * NB + b] = (uint8_t)bi;
+                            }
+                        }
+                    }
+                }
+                compute_barrier(4);  // the new tokens' index rows are complete
+                if (rg == 0) {
+                    // the cache's copy at positions t_kv .. t_kv + n_new - 1:
+                    // index rows, then (wave 0's lanes) the fp16 values
+                    for (int e = wv * kWave + lane; e < n_step * NB; e += NC * kWave)
+                        va.idx_out[(bh * c.cap + c.t_kv + e / NB) * NB + e % NB] = step_idx[e];
+                    if (wv == 0) {
+#pragma unroll
+                        for (int j = 0; j < NS; ++j)
+                            if (j < n_step)
+#pragma unroll
+                                for (int k = 0; k < DLs; ++k)
+                                    store_value_il8(va.v8_out, bh, c.cap, D, c.t_kv + j, lane + kWave * k,
+                                                    vpre[j][k]);
+                    }
+                }
+            }
+        }
         if constexpr (VF::kHybridBuffer)
             if (wv == 0 && has_buf) buffer_share(va);
 
@@ -4131,11 +4431,26 @@ __global__ void __launch_bounds__(1024) codebook_f16x2_kernel(const float *cents
     }
     if (threadIdx.x == 0)
         *reinterpret_cast<float *>(out + (int64_t)n_lanes * 2 * kBlockDim) = ldexpf(1.f, -sh);
+    // |C|^2 of each lane's centroid (unscaled float32, 0 past the last
+    // centroid), in the tiles' lane order, after the scale's 16 bytes
+    float *nrm = reinterpret_cast<float *>(out + (int64_t)n_lanes * 2 * kBlockDim) + 4;
+    for (int i = threadIdx.x; i < n_lanes; i += 1024) {
+        const int lane = i % kWave, tile = i / kWave;
+        const int bg = tile / nct, ct = tile % nct;
+        const int b = bg * 4 + lane / 16, cc = ct * 16 + lane % 16;
+        float acc = 0.f;
+        if (cc < n_centroids)
+            for (int j = 0; j < kBlockDim; ++j) {
+                const float x = cents[((int64_t)b * n_centroids + cc) * kBlockDim + j];
+                acc = fmaf(x, x, acc);
+            }
+        nrm[i] = acc;
+    }
 }
 
 extern "C" size_t ss_codebook_f16x2_bytes(int n_blocks, int n_centroids) {
     if (n_blocks < 4 || n_blocks % 4 || n_centroids < 1) return 0;
-    return (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16 + 16;
+    return (size_t)cb_tiles(n_blocks, n_centroids) * kWave * (2 * 16 + 4) + 16;
 }
 
 extern "C" int ss_codebook_f16x2(const float *centroids, int n_blocks, int n_centroids,
@@ -4258,6 +4573,68 @@ extern "C" int ss_decode_attn_il8_hybrid(
                     q_offset, out, out_dtype, workspace, workspace_bytes, n_splits, k_buf, v_buf,
                     buf_dtype, buf_sb, buf_sh, buf_st, t_buf, stream, k_heavy, heavy_dims,
                     n_heavy_dims);
+}
+
+extern "C" int ss_decode_step_il8(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, void *values_il8, int64_t cap, int64_t t_cache,
+    const void *k_new, const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+    int64_t n_new, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream) {
+    SS_UNSUPPORTED(n_new >= 1 && n_new <= kMaxStepTokens, "a fused step takes 1..%d new tokens",
+                   kMaxStepTokens);
+    SS_REQUIRE(t_cache >= 1, "a fused step needs a non-empty cache (t_cache %lld)",
+               (long long)t_cache);
+    SS_REQUIRE(t_cache + n_new <= cap, "new tokens [%lld, %lld) past cap %lld", (long long)t_cache,
+               (long long)(t_cache + n_new), (long long)cap);
+    SS_UNSUPPORTED(kv_dtype == SS_F16, "a fused step takes float16 keys and values");
+    SS_REQUIRE(k_new && v_new && centroids, "null new keys, values or centroids");
+    SS_UNSUPPORTED(n_centroids >= 1 && n_centroids <= 256 && n_blocks * 8 == head_dim,
+                   "a fused step needs 8-dim blocks of at most 256 centroids");
+    const float *cents = static_cast<const float *>(codebook);
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, cents,
+                          n_blocks, n_centroids, idx, cap, t_cache, out, out_dtype);
+    if (rc) return rc;
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
+    SS_REQUIRE(((uintptr_t)centroids % 16) == 0, "centroids must be 16-byte aligned");
+    SS_REQUIRE(values_il8, "null values");
+    SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8 for interleaved values");
+    SS_REQUIRE(((uintptr_t)values_il8 % 16) == 0, "values must be 16-byte aligned");
+    rc = check_buffer(k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, head_dim);
+    if (rc) return rc;
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_cache, n_splits,
+                                       kKindMfma);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents,
+                     n_centroids, idx, cap, t_cache, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    c.centroids = nullptr;
+    c.codebook = static_cast<const uint4 *>(codebook);
+    c.codebook_mul = reinterpret_cast<const float *>(
+        static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+    if (s.S > 1) {
+        // the last split encodes and attends the new tokens before its tiles:
+        // it gives up about kStepShareTokens cache tokens to the others, 8 at
+        // a time, as far as its own range allows
+        const int64_t room = t_cache - (int64_t)(s.S - 1) * s.tiles_per_split * kWave;
+        const int64_t want = (kStepShareTokens + (s.S - 1) * 8 - 1) / ((int64_t)(s.S - 1) * 8) * 8;
+        const int64_t most = room > 0 ? room / (s.S - 1) / 8 * 8 : 0;
+        c.split_pad = (int)(want < most ? want : most);
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    __half *v8 = reinterpret_cast<__half *>(values_il8);
+    const float *norms = c.codebook_mul + 4;
+    if (head_dim == 128)
+        return launch_mfma<128, VIl8Step<128>>(
+            c, VIl8Step<128>::Args{v8, k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, centroids,
+                                   norms, idx, v8},
+            s, st);
+    return launch_mfma<64, VIl8Step<64>>(
+        c, VIl8Step<64>::Args{v8, k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, centroids, norms,
+                              idx, v8},
+        s, st);
 }
 
 // ---------------------------------------------------------------------------

@@ -15,11 +15,10 @@
 //     every lane of a wave reads the same codeword (LDS broadcast);
 //   * small (decode-step append, few tokens): one wave per (token, block),
 //     lanes split the codebook and reduce (distance, index) across the wave.
-#include "ss_common.hpp"
+#include "encode_wave.hpp"
 
 namespace ss {
 
-constexpr float kSuspectRel = 4e-6f;
 constexpr int kEncThreads = 256;
 constexpr int kBlocksPerWG = 4;
 
@@ -111,131 +110,7 @@ __global__ void __launch_bounds__(kEncThreads) encode_bulk_kernel(EncodeArgs a) 
     }
 }
 
-// Exact nearest codeword of one block, the whole wave cooperating: lanes
-// split the codebook, direct-form float32 ranking, (distance, index)
-// reduced across the wave with lowest-index ties, and a float64 re-rank
-// when the runner-up is within kSuspectRel of the best.
-template <int BD>
-__device__ int exact_block_wave(const float (&kv)[BD], const float *cb, int nc, int lane) {
-    float best = INFINITY, second = INFINITY;
-    int bi = 0x7fffffff;
-    for (int c = lane; c < nc; c += kWave) {
-        const float *cv = cb + c * BD;
-        float df = kv[0] - cv[0];
-        float d = df * df;
-#pragma unroll
-        for (int k = 1; k < BD; ++k) {
-            df = kv[k] - cv[k];
-            d = fmaf(df, df, d);
-        }
-        const bool lt = d < best;
-        second = lt ? best : fminf(second, d);
-        bi = lt ? c : bi;
-        best = lt ? d : best;
-    }
-    // wave reduction of (best, index) with lowest-index ties, keeping the
-    // runner-up distance
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(best, o);
-        const float os = __shfl_xor(second, o);
-        const int oi = __shfl_xor(bi, o);
-        const bool mine = best < ob || (best == ob && bi < oi);
-        second = mine ? fminf(second, ob) : fminf(os, best);
-        best = mine ? best : ob;
-        bi = mine ? bi : oi;
-    }
-    if (!(second > best * (1.0f + kSuspectRel))) {
-        double b64 = INFINITY;
-        int i64 = 0x7fffffff;
-        for (int c = lane; c < nc; c += kWave) {
-            double d = 0.0;
-#pragma unroll
-            for (int k = 0; k < BD; ++k) {
-                const double df = (double)kv[k] - (double)cb[c * BD + k];
-                d = fma(df, df, d);
-            }
-            if (d < b64) {
-                b64 = d;
-                i64 = c;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const double ob = __shfl_xor(b64, o);
-            const int oi = __shfl_xor(i64, o);
-            const bool mine = b64 < ob || (b64 == ob && i64 < oi);
-            b64 = mine ? b64 : ob;
-            i64 = mine ? i64 : oi;
-        }
-        bi = i64;
-    }
-    return bi == 0x7fffffff ? 0 : bi;  // every distance NaN: the reference keeps index 0
-}
 
-// exact_block_wave for 8-dim blocks of at most 256 centroids with the
-// lane's centroids (c = lane + 64 i) already in registers, so their loads
-// overlap the key's; the same float steps, ties and refinement.
-__device__ int exact_block_wave_regs8(const float (&kv)[8], const float4 (&cv)[4][2],
-                                      const float *cb, int nc, int lane) {
-    float best = INFINITY, second = INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = lane + kWave * i;
-        if (c < nc) {
-            const float x[8] = {cv[i][0].x, cv[i][0].y, cv[i][0].z, cv[i][0].w,
-                                cv[i][1].x, cv[i][1].y, cv[i][1].z, cv[i][1].w};
-            float df = kv[0] - x[0];
-            float d = df * df;
-#pragma unroll
-            for (int k = 1; k < 8; ++k) {
-                df = kv[k] - x[k];
-                d = fmaf(df, df, d);
-            }
-            const bool lt = d < best;
-            second = lt ? best : fminf(second, d);
-            bi = lt ? c : bi;
-            best = lt ? d : best;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(best, o);
-        const float os = __shfl_xor(second, o);
-        const int oi = __shfl_xor(bi, o);
-        const bool mine = best < ob || (best == ob && bi < oi);
-        second = mine ? fminf(second, ob) : fminf(os, best);
-        best = mine ? best : ob;
-        bi = mine ? bi : oi;
-    }
-    if (!(second > best * (1.0f + kSuspectRel))) {
-        double b64 = INFINITY;
-        int i64 = 0x7fffffff;
-        for (int c = lane; c < nc; c += kWave) {
-            double d = 0.0;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const double df = (double)kv[k] - (double)cb[c * 8 + k];
-                d = fma(df, df, d);
-            }
-            if (d < b64) {
-                b64 = d;
-                i64 = c;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const double ob = __shfl_xor(b64, o);
-            const int oi = __shfl_xor(i64, o);
-            const bool mine = b64 < ob || (b64 == ob && i64 < oi);
-            b64 = mine ? b64 : ob;
-            i64 = mine ? i64 : oi;
-        }
-        bi = i64;
-    }
-    return bi == 0x7fffffff ? 0 : bi;
-}
 
 // Index of block blk of token n (a wave per (token, block); lane 0 stores
 // it).  8-dim blocks of at most 256 centroids take one memory round trip:
@@ -251,28 +126,14 @@ __device__ __forceinline__ void encode_block_wave(const EncodeArgs &a, int64_t n
         if (a.n_centroids <= 4 * kWave && d <= 4 * kWave) {
             const float *cbb = a.centroids + (int64_t)blk * a.n_centroids * 8;
             float4 cv[4][2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int c = min(lane + kWave * i, a.n_centroids - 1);
-                cv[i][0] = *reinterpret_cast<const float4 *>(cbb + c * 8);
-                cv[i][1] = *reinterpret_cast<const float4 *>(cbb + c * 8 + 4);
-            }
+            load_centroids8(cbb, a.n_centroids, lane, cv);
             float kr[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 kr[u] = lane + kWave * u < d ? load_as_f32(a.keys, a.keys_dtype, ad.key + lane + kWave * u)
                                              : 0.f;
-            int pj[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) pj[k] = a.perm ? a.perm[blk * 8 + k] : blk * 8 + k;
             float kv[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int src = __builtin_amdgcn_readfirstlane(pj[k]);  // wave-uniform
-                const int u = src >> 6;
-                const float x = u == 0 ? kr[0] : u == 1 ? kr[1] : u == 2 ? kr[2] : kr[3];
-                kv[k] = __shfl(x, src & (kWave - 1));
-            }
+            block_dims8(kr, a.perm, blk, kv);
             const int bi = exact_block_wave_regs8(kv, cv, cbb, a.n_centroids, lane);
             if (lane == 0) a.out[ad.out + blk] = (uint8_t)bi;
             return;

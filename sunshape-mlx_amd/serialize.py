@@ -116,6 +116,8 @@ def save_cache(path: str, cache) -> None:
     kind = type(cache).__name__
     if kind not in _CACHE_TENSORS:
         raise TypeError(f"cannot serialise {kind}")
+    if hasattr(cache, "flush"):
+        cache.flush()  # a held decode step's tokens into storage first
     tensors, codec_cfg = _codec_tensors(cache.codec, "codec")
     meta = {"format": FORMAT, "codec": json.dumps(codec_cfg), "cache_class": kind,
             "cache_config": json.dumps(_cache_config(cache))}

@@ -802,6 +802,7 @@ def test_decode_step_append_is_one_fused_launch_and_returns_deferred():
     b, hkv, d = 2, 4, 128
     k, v = kv(71, b, hkv, 300, d)
     lazy = S.create_kv_cache(codec, n_kv_heads=hkv)
+    lazy.fuse_steps = False  # every step's append launches at once (the fused step: below)
     eager = S.create_kv_cache(codec, n_kv_heads=hkv, lazy_fetch=False)
     ko, vo = lazy.update_and_fetch(k[:, :, :290], v[:, :, :290])  # prompt: bulk encoders
     eager.update_and_fetch(k[:, :, :290], v[:, :, :290])
@@ -825,6 +826,60 @@ def test_decode_step_append_is_one_fused_launch_and_returns_deferred():
         ko2.cpu()  # not built before the cache moved on
     assert ko.cpu().shape == (b, hkv, 300, d)  # built earlier: a snapshot, still valid
     assert ko3.cpu().shape == (b, hkv, 302, d)
+
+
+@pytest.mark.parametrize("hq,hkv,n_new,causal", [(16, 4, 1, False), (16, 2, 3, True)])
+def test_decode_steps_fuse_append_into_attention(hq, hkv, n_new, causal):
+    """With fuse_steps (the default) a decode step's new tokens wait in the
+    cache and the next sunshape_sdpa encodes, attends and stores them in one
+    launch: the cache ends bit-identical to the separate appends, the
+    outputs match them (the new tokens attended in float32: within 2e-5)
+    and the oracle, update_and_fetch itself launches nothing, and a read of
+    the cache, a trim, a save or the next update stores held tokens first.
+    A held tensor changed in place is refused."""
+    codec = make_codec(74)
+    b, d = 2, 128
+    t0, steps = 300, 6
+    k, v = kv(75, b, hkv, t0 + steps * n_new, d)
+    fused = S.create_kv_cache(codec, n_kv_heads=hkv, max_tokens=512)
+    plain = S.create_kv_cache(codec, n_kv_heads=hkv, max_tokens=512)
+    plain.fuse_steps = False
+    fused.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+    plain.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+    g = torch.Generator(device=DEV).manual_seed(76)
+    mask = "causal" if causal else None
+    for i in range(steps):
+        sl = slice(t0 + i * n_new, t0 + (i + 1) * n_new)
+        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).half()
+        before = sum(S.kernels.get_kernel_stats().values())
+        fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        assert sum(S.kernels.get_kernel_stats().values()) == before  # held, nothing launched
+        out_f = S.sunshape_sdpa(q, fused, 0.088, mask=mask, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_step"
+        assert sum(S.kernels.get_kernel_stats().values()) == before + 1
+        plain.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_p = S.sunshape_sdpa(q, plain, 0.088, mask=mask, out_dtype=torch.float32)
+        assert rel_err(out_f.cpu().numpy(), out_p.cpu().numpy()) <= 2e-5
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values, plain.values)
+    ref = O.sdpa(q.cpu().numpy(), plain.key_indices.cpu().numpy(), plain.values.cpu().numpy(),
+                 codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), 0.088, mask=mask)
+    assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
+    # held tokens are stored before anything reads or moves the cache
+    t_end = fused.offset
+    k1, v1 = kv(77, b, hkv, 1, d)
+    ko, vo = fused.update_and_fetch(k1, v1)
+    assert fused._pending is not None
+    assert torch.equal(vo[:, :, -1:], v1)  # building the deferred values stores them
+    assert fused._pending is None and fused.offset == t_end + 1
+    fused.update_and_fetch(k1 + 1, v1)
+    fused.trim(1)
+    assert fused._pending is None and fused.offset == t_end + 1
+    k2, v2 = kv(78, b, hkv, 1, d)
+    fused.update_and_fetch(k2, v2)
+    k2.add_(1.0)  # changed in place while held
+    with pytest.raises(RuntimeError):
+        S.sunshape_sdpa(q[:, :, :1], fused, 0.088)
 
 
 @pytest.mark.parametrize("bits,buf", [(2, 128), (4, 16)])

@@ -401,7 +401,8 @@ def test_decode_il8_matches_oracle(b, hq, hkv, d, t_kv, t_q, causal, splits, cap
 def test_codebook_f16x2_reconstructs_the_centroids():
     """hi + lo * 2^-11, times the stored power of two, gives back every
     centroid to about 2^-22 of the codebook's largest magnitude, for codebooks
-    far outside the fp16 range, tiny ones and an all-zero one."""
+    far outside the fp16 range, tiny ones and an all-zero one; the squared
+    norms that follow are every tile row's |C|^2 (float32)."""
     rng = np.random.default_rng(5)
     for mag, nc in ((1.0, 256), (3e6, 40), (2e-7, 16), (0.0, 8)):
         c = (rng.standard_normal((16, nc, 8)) * mag).astype(np.float32)
@@ -411,7 +412,7 @@ def test_codebook_f16x2_reconstructs_the_centroids():
         raw = buf.cpu().numpy()
         nct = (nc + 15) // 16
         body = 4 * nct * 2048
-        assert raw.size == body + 16
+        assert raw.size == body + 16 + 4 * nct * 64 * 4
         # tile (bg, ct), part (hi, lo), lane l: centroid ct*16 + l%16 of block bg*4 + l/16
         hl = raw[:body].view(np.float16).reshape(4, nct, 2, 4, 16, 8).astype(np.float64)
         mul = float(raw[body:body + 4].view(np.float32)[0])
@@ -423,6 +424,12 @@ def test_codebook_f16x2_reconstructs_the_centroids():
         assert not full[:, nc:].any()  # padding lanes are zero
         tol = max(np.abs(c).max(), 1e-30) * 2.0 ** -21
         assert np.abs(back - c).max() <= tol
+        # |C|^2 per tile row, rows laid out as the hi parts
+        nrm = raw[body + 16:].view(np.float32).reshape(4, nct, 4, 16)  # (bg, ct, bs, n)
+        nrm = nrm.transpose(0, 2, 1, 3).reshape(16, nct * 16)
+        want = (c.astype(np.float64) ** 2).sum(-1)
+        assert not nrm[:, nc:].any()
+        assert np.allclose(nrm[:, :nc], want, rtol=2e-6, atol=0.0)
 
 
 @pytest.mark.parametrize("q_dtype,nc,d", [(np.float32, 256, 128), (np.float32, 40, 64),
@@ -1296,6 +1303,76 @@ def test_prefill_il8_matches_oracle(b, hq, hkv, t_q, t_kv, causal, qdt, nc):
     assert np.isfinite(got).all()
     assert rel_err(got, ref) <= REL_TOL
     assert rel_err(got, ref_dec.cpu().numpy()) <= REL_TOL
+
+
+@pytest.mark.parametrize("b,hq,hkv,d,t_cache,n_new,t_q,causal", [
+    (1, 32, 8, 128, 4096, 1, 1, False),   # the metric shape's decode step
+    (2, 16, 2, 128, 1003, 3, 1, False),   # rep 8: two row groups of a head, one writes
+    (1, 8, 2, 64, 515, 4, 4, True),       # head_dim 64, four new tokens as causal rows
+    (2, 8, 8, 128, 40, 2, 1, False),      # a short cache (one split), rep 1
+])
+def test_decode_step_il8_equals_append_then_decode(b, hq, hkv, d, t_cache, n_new, t_q, causal):
+    """ss_decode_step_il8 (encode the new tokens, attend every token, store
+    the new ones, one launch) leaves the cache exactly as ss_append_kv_il8
+    does (index rows and interleaved values, bit for bit) and returns the
+    decode over the appended cache (the new tokens attended in float32
+    instead of through the matrix cores: within a few 1e-6), which matches
+    the oracle."""
+    rng = np.random.default_rng(900 + t_cache + n_new)
+    nb = d // 8
+    cents = t(rng.standard_normal((nb, 256, 8)).astype(np.float32))
+    perm = t(rng.permutation(d).astype(np.int32))
+    t_all = t_cache + n_new
+    cap = ((t_all + 31) // 8) * 8
+    keys = t(rng.standard_normal((b, hkv, t_all, d)).astype(np.float16))
+    vals = t(rng.standard_normal((b, hkv, t_all, d)).astype(np.float16))
+    q = t(rng.standard_normal((b, hq, t_q, d)).astype(np.float16))
+    idx_a = torch.zeros((b, hkv, cap, nb), dtype=torch.uint8, device=DEV)
+    v8_a = torch.zeros((b, hkv, cap // 8, d, 8), dtype=torch.float16, device=DEV)
+    app = _hip.PreparedAppend(perm, cents, None, idx_a, v8_a)
+    app(keys[:, :, :t_cache], vals[:, :, :t_cache], 0)
+    idx_b, v8_b = idx_a.clone(), v8_a.clone()
+    k_new, v_new = keys[:, :, t_cache:].contiguous(), vals[:, :, t_cache:].contiguous()
+    app(k_new, v_new, t_cache)
+    cb = _hip.codebook_f16x2(cents)
+    scale = 1.0 / np.sqrt(d)
+    q_off = t_all - t_q if causal else 0
+    ref = _hip.decode_attn_il8(q, scale, perm, cents, idx_a, v8_a, t_all, causal=causal,
+                               q_offset=q_off, out_dtype=torch.float32, codebook=cb)
+    got = _hip.decode_step_il8(q, scale, perm, cb, cents, idx_b, v8_b, t_cache, k_new, v_new,
+                               causal=causal, q_offset=q_off, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(idx_b, idx_a)
+    assert torch.equal(v8_b.view(torch.int16), v8_a.view(torch.int16))
+    assert rel_err(got.cpu().numpy(), ref.cpu().numpy()) <= 2e-5
+    oref = O.sdpa(q.cpu().numpy(), idx_a[:, :, :t_all].cpu().numpy(),
+                  vals.cpu().numpy(), cents.cpu().numpy(), perm.cpu().numpy(), scale,
+                  mask="causal" if causal else None)
+    assert rel_err(got.cpu().numpy(), oref) <= REL_TOL
+
+
+def test_decode_step_il8_rejects_what_it_cannot_take():
+    """Host checks before any launch: no new tokens or more than
+    MAX_STEP_TOKENS, an empty cache, tokens past the capacity, non-fp16 new
+    tokens."""
+    rng = np.random.default_rng(5)
+    cents = t(rng.standard_normal((16, 256, 8)).astype(np.float32))
+    idx = torch.zeros((1, 2, 64, 16), dtype=torch.uint8, device=DEV)
+    v8 = torch.zeros((1, 2, 8, 128, 8), dtype=torch.float16, device=DEV)
+    cb = _hip.codebook_f16x2(cents)
+    q = torch.randn((1, 8, 1, 128), device=DEV).half()
+
+    def new(n, dt=torch.float16):
+        return (torch.randn((1, 2, n, 128), device=DEV).to(dt),
+                torch.randn((1, 2, n, 128), device=DEV).to(dt))
+    for t_cache, kv_, err in ((10, new(_hip.MAX_STEP_TOKENS + 1), _hip.SunShapeUnsupported),
+                              (0, new(1), _hip.SunShapeHIPError),
+                              (60, new(5), _hip.SunShapeHIPError),
+                              (10, new(1, torch.float32), ValueError)):
+        with pytest.raises(err):
+            _hip.decode_step_il8(q, 0.088, None, cb, cents, idx, v8, t_cache, *kv_)
+    torch.cuda.synchronize()
+    assert not idx.any() and not v8.any()
 
 
 def test_prefill_il8_at_the_benchmarked_prompt():
