@@ -1941,6 +1941,19 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     constexpr int DLs = kStep ? D / kWave : 1;
     constexpr int NS = kStep ? kMaxStepTokens : 1;
     float kpre[NS][DLs], vpre[NS][DLs];
+    // A hybrid cache's share of at most kShareRegs 16-bit buffered tokens
+    // (wave 0): their key and value dims lane + 64k, loaded in the prologue
+    // too (the heavy-dim kernels have no registers to spare)
+    constexpr bool kShPre = VF::kHybridBuffer && !kStep && !HV;
+    constexpr int kShareRegs = 8;
+    constexpr int NSH = kShPre ? kShareRegs : 1;
+    constexpr int DLh = kShPre ? D / kWave : 1;
+    unsigned short hk_raw[NSH][DLh], hv_raw[NSH][DLh];
+    const int n_sh = (int)(bj1 - bj0);
+    bool sh_pre = false;
+    if constexpr (kShPre)
+        sh_pre = has_buf && wv == 0 && n_sh <= kShareRegs &&
+                 (va.buf_dtype == SS_F16 || va.buf_dtype == SS_BF16);
     auto buffer_share = [&](const auto &bv) {
         constexpr int DL = D / kWave;  // value dims per lane
         float bm[R], bl[R], ba[R][DL];
@@ -1954,7 +1967,54 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         const float *bq = bpart + 2 * R;  // [R][D] query copy
         f32x4 *pb = reinterpret_cast<f32x4 *>(pst);  // wave 0's P staging: p of 64 tokens
         const int64_t head = bb * bv.buf_sb + kvh * bv.buf_sh;
-        for (int64_t j0 = bj0; j0 < bj1; j0 += kWave) {
+        if constexpr (kShPre) {
+            if (sh_pre) {
+                // the prefetched share: each token's four scores as wave sums
+                // of the lanes' partial dot products, then one softmax over
+                // the share and P.V from registers
+                const bool bf = bv.buf_dtype == SS_BF16;
+                auto f32 = [&](unsigned short h) {
+                    return bf ? __uint_as_float((uint32_t)h << 16) : __half2float(__ushort_as_half(h));
+                };
+                float qv[R][DLh];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int k = 0; k < DLh; ++k) qv[r][k] = bq[r * D + lane + kWave * k];
+                float sc[NSH][R];
+#pragma unroll
+                for (int j = 0; j < NSH; ++j) {
+                    float part[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        part[r] = 0.f;
+#pragma unroll
+                        for (int k = 0; k < DLh; ++k) part[r] = fmaf(qv[r][k], f32(hk_raw[j][k]), part[r]);
+                    }
+                    wave_sum4_dpp(part, sc[j]);
+                    const int64_t pos = c.t_kv + bj0 + j;
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+                        sc[j][r] = (j < n_sh && pos <= lim[r]) ? sc[j][r] * kLog2e : -INFINITY;
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float mx = sc[0][r];
+#pragma unroll
+                    for (int j = 1; j < NSH; ++j) mx = fmaxf(mx, sc[j][r]);
+                    if (mx == -INFINITY) continue;  // nothing visible: the partial stays empty
+                    bm[r] = mx;
+#pragma unroll
+                    for (int j = 0; j < NSH; ++j) {
+                        const float pj = fast_exp2(sc[j][r] - mx);
+                        bl[r] += pj;
+#pragma unroll
+                        for (int k = 0; k < DLh; ++k) ba[r][k] = fmaf(pj, f32(hv_raw[j][k]), ba[r][k]);
+                    }
+                }
+            }
+        }
+        for (int64_t j0 = sh_pre ? bj1 : bj0; j0 < bj1; j0 += kWave) {
             const int64_t j = j0 + lane;
             const bool ok = j < bj1;
             const int64_t ko = head + (ok ? j : j0) * bv.buf_st;
@@ -2139,6 +2199,21 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 const uint4 *cp = c.codebook + (bg * nct + ct) * 2 * kWave + lane;
                 cb_hi[t] = cp[0];
                 cb_lo[t] = cp[kWave];
+            }
+        }
+        if constexpr (kShPre) {
+            if (sh_pre) {
+                const unsigned short *kb = static_cast<const unsigned short *>(va.kbuf);
+                const unsigned short *vb = static_cast<const unsigned short *>(va.vbuf);
+                const int64_t head = bb * va.buf_sb + kvh * va.buf_sh;
+#pragma unroll
+                for (int j = 0; j < NSH; ++j)
+#pragma unroll
+                    for (int k = 0; k < DLh; ++k) {
+                        const int64_t o = head + (bj0 + min(j, n_sh - 1)) * va.buf_st + lane + kWave * k;
+                        hk_raw[j][k] = kb[o];
+                        hv_raw[j][k] = vb[o];
+                    }
             }
         }
         if constexpr (kRegs) {

@@ -1351,6 +1351,42 @@ def test_decode_step_il8_equals_append_then_decode(b, hq, hkv, d, t_cache, n_new
     assert rel_err(got.cpu().numpy(), oref) <= REL_TOL
 
 
+def test_decode_step_il8_ties_take_the_exact_ranking():
+    """New keys exactly halfway between two centroids of every block (an exact
+    tie, which no float error bound can clear) and keys a hair closer to the
+    second: the step's encode falls back to the exact ranking, giving the
+    lower index on the tie and the nearer centroid otherwise, as the encoder
+    does (ss_append_kv_il8)."""
+    rng = np.random.default_rng(77)
+    b, hq, hkv, d, t_cache, nb = 1, 8, 2, 128, 300, 16
+    c = rng.standard_normal((nb, 256, 8)).astype(np.float32) * 0.5
+    c[:, 3, :] = 1.0   # the two centroids every new key sits between
+    c[:, 7, :] = 3.0
+    cents = t(c)
+    perm = t(rng.permutation(d).astype(np.int32))
+    keys = t(rng.standard_normal((b, hkv, t_cache + 2, d)).astype(np.float16))
+    vals = t(rng.standard_normal((b, hkv, t_cache + 2, d)).astype(np.float16))
+    keys[:, :, t_cache] = 2.0                                  # tie: index 3
+    near = np.full(d, 2.0, np.float32)
+    near[perm.cpu().numpy()[0::8]] = np.float16(2.0 + 2.0 ** -9)  # block dim 0 a hair nearer 7
+    keys[:, :, t_cache + 1] = t(near.astype(np.float16))
+    cap = t_cache + 12 - (t_cache + 12) % 8
+    idx_a = torch.zeros((b, hkv, cap, nb), dtype=torch.uint8, device=DEV)
+    v8_a = torch.zeros((b, hkv, cap // 8, d, 8), dtype=torch.float16, device=DEV)
+    app = _hip.PreparedAppend(perm, cents, None, idx_a, v8_a)
+    app(keys[:, :, :t_cache], vals[:, :, :t_cache], 0)
+    idx_b, v8_b = idx_a.clone(), v8_a.clone()
+    k_new, v_new = keys[:, :, t_cache:].contiguous(), vals[:, :, t_cache:].contiguous()
+    app(k_new, v_new, t_cache)
+    q = t(rng.standard_normal((b, hq, 1, d)).astype(np.float16))
+    cb = _hip.codebook_f16x2(cents)
+    _hip.decode_step_il8(q, 0.088, perm, cb, cents, idx_b, v8_b, t_cache, k_new, v_new)
+    torch.cuda.synchronize()
+    assert torch.equal(idx_b, idx_a)
+    got = idx_b[:, :, t_cache:t_cache + 2].cpu().numpy()
+    assert (got[:, :, 0] == 3).all() and (got[:, :, 1] == 7).all()
+
+
 def test_decode_step_il8_rejects_what_it_cannot_take():
     """Host checks before any launch: no new tokens or more than
     MAX_STEP_TOKENS, an empty cache, tokens past the capacity, non-fp16 new
