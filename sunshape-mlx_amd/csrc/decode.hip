@@ -962,7 +962,16 @@ struct WsCfg {
     // a fused step's new index rows (4 tokens x NB bytes, 64 reserved) and
     // its encode's per-wave candidates (NC x 4 blocks x 4 tokens x 16 B)
     static constexpr int kStepLds = StepShareOf<VF>::value ? 64 + NC * 16 * 16 : 0;
-    static constexpr int kRing = kLut + kPst + kFlags + kBufPart + kStepLds;
+    // a hybrid split's share of up to kShareLdsTok 16-bit buffered tokens,
+    // keys then values [tok][D], copied in the prologue: on the private-ring
+    // shapes (their ring has a fixed size, so the copy costs no ring slot)
+    static constexpr int kShareFree = kLdsMax - (kLut + kPst + kFlags + kBufPart + kStepLds) -
+                                      NC * 2 * kSlot;  // beside a private ring of 2 slots a wave
+    static constexpr int kShareFit = kShareFree > 0 ? kShareFree / (4 * D) / 8 * 8 : 0;
+    static constexpr int kShareLdsTok = (VF::kHybridBuffer && !StepShareOf<VF>::value &&
+                                         VF::kPrivateRing) ? (kShareFit < 32 ? kShareFit : 32) : 0;
+    static constexpr int kShareLds = kShareLdsTok * D * 2 * 2;
+    static constexpr int kRing = kLut + kPst + kFlags + kBufPart + kStepLds + kShareLds;
     static constexpr int kSlotsFit = (kLdsMax - kRing) / kSlot;
     static constexpr int kSlots = kSlotsFit < VF::kMaxSlots ? kSlotsFit : VF::kMaxSlots;
     static constexpr int kLoadsPerTile = VF::kLoadsV + kLoadsI;
@@ -1950,10 +1959,16 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     constexpr int DLh = kShPre ? D / kWave : 1;
     unsigned short hk_raw[NSH][DLh], hv_raw[NSH][DLh];
     const int n_sh = (int)(bj1 - bj0);
-    bool sh_pre = false;
-    if constexpr (kShPre)
-        sh_pre = has_buf && wv == 0 && n_sh <= kShareRegs &&
-                 (va.buf_dtype == SS_F16 || va.buf_dtype == SS_BF16);
+    bool sh_pre = false, sh_lds = false;
+    if constexpr (kShPre) {
+        const bool b16 = va.buf_dtype == SS_F16 || va.buf_dtype == SS_BF16;
+        sh_pre = has_buf && wv == 0 && n_sh <= kShareRegs && b16;
+        sh_lds = has_buf && n_sh > kShareRegs && n_sh <= K::kShareLdsTok && b16;
+    }
+    // the LDS copy of the share: keys [kShareLdsTok][D], then values
+    const unsigned short *sh_k = reinterpret_cast<const unsigned short *>(
+        smem + K::kLut + K::kPst + K::kFlags + K::kBufPart + K::kStepLds);
+    const unsigned short *sh_v = sh_k + K::kShareLdsTok * D;
     auto buffer_share = [&](const auto &bv) {
         constexpr int DL = D / kWave;  // value dims per lane
         float bm[R], bl[R], ba[R][DL];
@@ -1968,10 +1983,12 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         f32x4 *pb = reinterpret_cast<f32x4 *>(pst);  // wave 0's P staging: p of 64 tokens
         const int64_t head = bb * bv.buf_sb + kvh * bv.buf_sh;
         if constexpr (kShPre) {
-            if (sh_pre) {
-                // the prefetched share: each token's four scores as wave sums
-                // of the lanes' partial dot products, then one softmax over
-                // the share and P.V from registers
+            if (sh_pre || sh_lds) {
+                // the prefetched share (registers, or the LDS copy), eight
+                // tokens at a time: each token's four scores as wave sums of
+                // the lanes' partial dot products (lane: dims lane + 64k),
+                // online softmax over the chunks, P.V on the lanes' dims
+                if (sh_lds) wait_vmcnt<0>();  // wave 0's copies have landed
                 const bool bf = bv.buf_dtype == SS_BF16;
                 auto f32 = [&](unsigned short h) {
                     return bf ? __uint_as_float((uint32_t)h << 16) : __half2float(__ushort_as_half(h));
@@ -1981,40 +1998,61 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 for (int r = 0; r < R; ++r)
 #pragma unroll
                     for (int k = 0; k < DLh; ++k) qv[r][k] = bq[r * D + lane + kWave * k];
-                float sc[NSH][R];
+                for (int c0 = 0; c0 < n_sh; c0 += NSH) {
+                    unsigned short kc[NSH][DLh], vc[NSH][DLh];
 #pragma unroll
-                for (int j = 0; j < NSH; ++j) {
-                    float part[R];
+                    for (int j = 0; j < NSH; ++j)
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        part[r] = 0.f;
-#pragma unroll
-                        for (int k = 0; k < DLh; ++k) part[r] = fmaf(qv[r][k], f32(hk_raw[j][k]), part[r]);
-                    }
-                    wave_sum4_dpp(part, sc[j]);
-                    const int64_t pos = c.t_kv + bj0 + j;
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        sc[j][r] = (j < n_sh && pos <= lim[r]) ? sc[j][r] * kLog2e : -INFINITY;
-                }
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float mx = sc[0][r];
-#pragma unroll
-                    for (int j = 1; j < NSH; ++j) mx = fmaxf(mx, sc[j][r]);
-                    if (mx == -INFINITY) continue;  // nothing visible: the partial stays empty
-                    bm[r] = mx;
+                        for (int k = 0; k < DLh; ++k) {
+                            if (sh_lds) {
+                                const int row = min(c0 + j, n_sh - 1);
+                                kc[j][k] = sh_k[row * D + lane + kWave * k];
+                                vc[j][k] = sh_v[row * D + lane + kWave * k];
+                            } else {
+                                kc[j][k] = hk_raw[j][k];
+                                vc[j][k] = hv_raw[j][k];
+                            }
+                        }
+                    float sc[NSH][R];
 #pragma unroll
                     for (int j = 0; j < NSH; ++j) {
-                        const float pj = fast_exp2(sc[j][r] - mx);
-                        bl[r] += pj;
+                        float part[R];
 #pragma unroll
-                        for (int k = 0; k < DLh; ++k) ba[r][k] = fmaf(pj, f32(hv_raw[j][k]), ba[r][k]);
+                        for (int r = 0; r < R; ++r) {
+                            part[r] = 0.f;
+#pragma unroll
+                            for (int k = 0; k < DLh; ++k) part[r] = fmaf(qv[r][k], f32(kc[j][k]), part[r]);
+                        }
+                        wave_sum4_dpp(part, sc[j]);
+                        const int64_t pos = c.t_kv + bj0 + c0 + j;
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            sc[j][r] = (c0 + j < n_sh && pos <= lim[r]) ? sc[j][r] * kLog2e : -INFINITY;
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float mx = sc[0][r];
+#pragma unroll
+                        for (int j = 1; j < NSH; ++j) mx = fmaxf(mx, sc[j][r]);
+                        if (mx == -INFINITY) continue;  // nothing visible in this chunk
+                        const float mn = fmaxf(bm[r], mx);
+                        const float corr = fast_exp2(bm[r] - mn);
+                        bm[r] = mn;
+                        bl[r] *= corr;
+#pragma unroll
+                        for (int k = 0; k < DLh; ++k) ba[r][k] *= corr;
+#pragma unroll
+                        for (int j = 0; j < NSH; ++j) {
+                            const float pj = fast_exp2(sc[j][r] - mn);
+                            bl[r] += pj;
+#pragma unroll
+                            for (int k = 0; k < DLh; ++k) ba[r][k] = fmaf(pj, f32(vc[j][k]), ba[r][k]);
+                        }
                     }
                 }
             }
         }
-        for (int64_t j0 = sh_pre ? bj1 : bj0; j0 < bj1; j0 += kWave) {
+        for (int64_t j0 = (sh_pre || sh_lds) ? bj1 : bj0; j0 < bj1; j0 += kWave) {
             const int64_t j = j0 + lane;
             const bool ok = j < bj1;
             const int64_t ko = head + (ok ? j : j0) * bv.buf_st;
@@ -2199,6 +2237,26 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 const uint4 *cp = c.codebook + (bg * nct + ct) * 2 * kWave + lane;
                 cb_hi[t] = cp[0];
                 cb_lo[t] = cp[kWave];
+            }
+        }
+        if constexpr (kShPre && K::kShareLdsTok > 0) {
+            if (sh_lds) {
+                // 16 bytes a lane: copy i of the share's rows covers rows
+                // (i*64 + lane) / (D/8), keys for i < n_copies, then values
+                constexpr int CPR = D / 8;  // 16-byte chunks per row
+                const int64_t head = bb * va.buf_sb + kvh * va.buf_sh;
+                const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sh_k));
+                const int n_copies = (n_sh * CPR + kWave - 1) / kWave;
+                for (int i = 0; wv == 0 && i < 2 * n_copies; ++i) {  // wave 0, which attends it
+                    const bool is_v = i >= n_copies;
+                    const int ci = (is_v ? i - n_copies : i) * kWave + lane;
+                    const int row = min(ci / CPR, n_sh - 1), chunk = ci % CPR;
+                    const char *src = static_cast<const char *>(is_v ? va.vbuf : va.kbuf) +
+                                      ((head + (bj0 + row) * va.buf_st) * 2 + chunk * 16);
+                    const uint32_t dst = lds0 + (uint32_t)((is_v ? K::kShareLdsTok * D * 2 : 0) +
+                                                           (is_v ? i - n_copies : i) * 1024);
+                    __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_t<void> *>(dst), 16, 0, 0);
+                }
             }
         }
         if constexpr (kShPre) {
