@@ -81,37 +81,68 @@ __global__ void __launch_bounds__(256)
 // the group's LUT sits in LDS as a float4 (its four rows) per (block,
 // centroid), so a token's scores for all four rows take one 16-byte LDS
 // gather per block; a workgroup scores kGatherTokens tokens so its 64 KB
-// LUT copy is amortised over them.
+// LUT copy is amortised over them.  Workgroups are handed to the 8 XCDs in
+// turn by their linear id L, so work item w = (L % 8) * per_xcd + L / 8
+// keeps a row group's token chunks on one XCD: its LUT is fetched from HBM
+// into that XCD's L2 once, not once per XCD.
 constexpr int kGatherTokens = 4096;
 constexpr int kGatherThreads = 512;
 
+template <bool kRows16>
 __global__ void __launch_bounds__(kGatherThreads)
     score_gather4_kernel(const float *lut, int64_t lut_head_stride, int64_t n_rows, int n_rgrp,
                          int n_blocks, int n_centroids, const uint8_t *idx, int64_t n_h,
                          int64_t idx_sb, int64_t idx_sh, int64_t idx_st, int64_t n_tok,
                          float *scores, int64_t out_head_stride, int64_t out_row_stride,
-                         int rows16) {
+                         int64_t n_chunk, int64_t n_work, int64_t per_xcd) {
     extern __shared__ float4 tab4[];  // [n_blocks][256] float4
-    const int64_t head = blockIdx.y / n_rgrp;
-    const int64_t r0 = (int64_t)(blockIdx.y % n_rgrp) * 4;
+    const int64_t w = (int64_t)(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (w >= n_work) return;  // the grid is padded to a multiple of 8
+    const int64_t grp = w / n_chunk, chunk = w - grp * n_chunk;
+    const int64_t head = grp / n_rgrp;
+    const int64_t r0 = (grp % n_rgrp) * 4;
     const int nr = (int)min((int64_t)4, n_rows - r0);
     const int per_row = n_blocks * n_centroids;
     const float *lh = lut + head * lut_head_stride + r0 * per_row;
-    if (n_centroids == 256) {
-        // four centroids of each row per thread (16-byte loads), transposed
-        // into four float4 entries in registers
-        for (int i = threadIdx.x; i < n_blocks * 64; i += blockDim.x) {
-            const int b = i >> 6, c4 = (i & 63) * 4;
-            float4 v[4];
+    const int64_t b0 = head / n_h, h0 = head - b0 * n_h;
+    const uint8_t *ih = idx + b0 * idx_sb + h0 * idx_sh;
+    const int64_t t0 = chunk * kGatherTokens;
+    const int64_t t_end = min(n_tok, t0 + kGatherTokens);
+    // 16-byte index rows: the thread's kTokPer rows are requested right
+    // after the LUT loads, so they stream while the LUT reaches LDS
+    constexpr int kTokPer = kGatherTokens / kGatherThreads;
+    uint4 rq[kTokPer];
+    const auto load_rows = [&]() {
+        if (!kRows16) return;
+#pragma unroll
+        for (int k = 0; k < kTokPer; ++k) {
+            // rows past t_end read the last row again (their scores are not stored)
+            const int64_t t = min(t0 + threadIdx.x + k * kGatherThreads, t_end - 1);
+            rq[k] = *reinterpret_cast<const uint4 *>(ih + t * idx_st);
+        }
+    };
+    if (n_centroids == 256 && n_blocks == 16) {
+        // entry i = block * 256 + centroid: consecutive threads take
+        // consecutive entries, so each row's loads are coalesced and the
+        // float4 stores fall in distinct LDS banks
+        constexpr int kPer = 16 * 256 / kGatherThreads;
+        float v[kPer][4];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                v[r] = r < nr ? *reinterpret_cast<const float4 *>(lh + r * per_row + b * 256 + c4)
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
-            tab4[b * 256 + c4 + 0] = make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
-            tab4[b * 256 + c4 + 1] = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
-            tab4[b * 256 + c4 + 2] = make_float4(v[0].z, v[1].z, v[2].z, v[3].z);
-            tab4[b * 256 + c4 + 3] = make_float4(v[0].w, v[1].w, v[2].w, v[3].w);
-        }
+                v[k][r] = lh[min(r, nr - 1) * per_row + threadIdx.x + k * kGatherThreads];
+        __builtin_amdgcn_sched_barrier(0);  // LUT loads issue before the index rows
+        load_rows();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+#pragma unroll
+            for (int r = 1; r < 4; ++r)
+                if (r >= nr) v[k][r] = 0.f;  // rows past the last read row nr - 1 again
+#pragma unroll
+        for (int k = 0; k < kPer; ++k)
+            tab4[threadIdx.x + k * kGatherThreads] = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
     } else {
         for (int i = threadIdx.x; i < n_blocks * 256; i += blockDim.x) {
             const int b = i >> 8, c = i & 255;
@@ -122,40 +153,45 @@ __global__ void __launch_bounds__(kGatherThreads)
                     if (r < nr) v[r] = lh[r * per_row + b * n_centroids + c];
             tab4[i] = make_float4(v[0], v[1], v[2], v[3]);
         }
+        load_rows();
     }
     __syncthreads();
-    const int64_t b0 = head / n_h, h0 = head - b0 * n_h;
-    const uint8_t *ih = idx + b0 * idx_sb + h0 * idx_sh;
     float *out = scores + head * out_head_stride + r0 * out_row_stride;
-    const int64_t t_end = min(n_tok, (int64_t)(blockIdx.x + 1) * kGatherTokens);
-    for (int64_t t = (int64_t)blockIdx.x * kGatherTokens + threadIdx.x; t < t_end; t += blockDim.x) {
-        const uint8_t *ip = ih + t * idx_st;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (rows16) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(ip);
-            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const int c = min((int)((ws[b >> 2] >> (8 * (b & 3))) & 0xffu), n_centroids - 1);
-                const float4 e = tab4[b * 256 + c];
-                acc.x += e.x;
-                acc.y += e.y;
-                acc.z += e.z;
-                acc.w += e.w;
-            }
-        } else {
-            for (int b = 0; b < n_blocks; ++b) {
-                const float4 e = tab4[b * 256 + min((int)ip[b], n_centroids - 1)];
-                acc.x += e.x;
-                acc.y += e.y;
-                acc.z += e.z;
-                acc.w += e.w;
-            }
-        }
+    const auto emit = [&](int64_t t, float4 acc) {
         const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (r < nr) out[r * out_row_stride + t] = a4[r];
+    };
+    if (kRows16) {
+#pragma unroll
+        for (int k = 0; k < kTokPer; ++k) {
+            const int64_t t = t0 + threadIdx.x + k * kGatherThreads;
+            if (t >= t_end) break;
+            const uint32_t ws[4] = {rq[k].x, rq[k].y, rq[k].z, rq[k].w};
+            typedef float f4v __attribute__((ext_vector_type(4)));
+            const f4v *tv = reinterpret_cast<const f4v *>(tab4);
+            f4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int c = min((int)((ws[b >> 2] >> (8 * (b & 3))) & 0xffu), n_centroids - 1);
+                acc += tv[b * 256 + c];
+            }
+            emit(t, make_float4(acc.x, acc.y, acc.z, acc.w));
+        }
+        return;
+    }
+    for (int64_t t = t0 + threadIdx.x; t < t_end; t += blockDim.x) {
+        const uint8_t *ip = ih + t * idx_st;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int b = 0; b < n_blocks; ++b) {
+            const float4 e = tab4[b * 256 + min((int)ip[b], n_centroids - 1)];
+            acc.x += e.x;
+            acc.y += e.y;
+            acc.z += e.z;
+            acc.w += e.w;
+        }
+        emit(t, acc);
     }
 }
 
@@ -223,19 +259,22 @@ static int score_gather_impl(const float *lut, int64_t lut_head_stride, int64_t 
     if (n_blocks <= 16) {  // float4 LUT of four rows, many tokens per workgroup
         const int64_t n_rg4 = (n_rows + 3) / 4;
         const int64_t ry4 = n_b * n_h * n_rg4;
-        SS_UNSUPPORTED(ry4 <= 65535, "too many (head, row group) pairs for one launch");
-        dim3 grid4((unsigned)((n_tok + kGatherTokens - 1) / kGatherTokens), (unsigned)ry4);
+        const int64_t n_chunk = (n_tok + kGatherTokens - 1) / kGatherTokens;
+        const int64_t n_work = ry4 * n_chunk, per_xcd = (n_work + 7) / 8;
+        SS_UNSUPPORTED(per_xcd * 8 <= 0x7fffffff, "too many workgroups for one launch");
+        const dim3 grid4((unsigned)(per_xcd * 8));
         const size_t lds4 = sizeof(float4) * n_blocks * 256;
+        const auto kern = rows16 ? score_gather4_kernel<true> : score_gather4_kernel<false>;
         if (lds4 > 65536) {
-            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(score_gather4_kernel),
+            const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
                                                      (int)lds4);
             if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(score gather)");
         }
-        hipLaunchKernelGGL(score_gather4_kernel, grid4, dim3(kGatherThreads), lds4, st, lut,
-                           lut_head_stride,
+        hipLaunchKernelGGL(kern, grid4, dim3(kGatherThreads), lds4, st, lut, lut_head_stride,
                            n_rows, (int)n_rg4, n_blocks, n_centroids, idx, n_h, idx_sb, idx_sh,
-                           idx_st, n_tok, scores, out_head_stride, out_row_stride, rows16);
+                           idx_st, n_tok, scores, out_head_stride, out_row_stride, n_chunk,
+                           n_work, per_xcd);
         SS_LAUNCH_CHECK("score_gather4_kernel launch");
         return SS_OK;
     }
