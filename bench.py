@@ -785,6 +785,13 @@ def run_scores(args) -> int:
         ref = O.gather_scores(lut[3, 5].cpu().numpy(), idxs[0][3, 5].cpu().numpy())
         got = outs[0][3, 5].cpu().numpy()
         check = float(np.abs(got - ref).max() / np.abs(ref).max())
+    traffic = None  # HBM bytes per launch from the committed counter runs
+    tf = os.path.join(ROOT, "profiles", "score_gather4_config4_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            tr = json.load(f)
+        if tr.get("t_kv") == t_kv:
+            traffic = tr.get("hbm_bytes_per_launch")
     line = {
         "metric": "compressed score gather µs/launch and achieved HBM GB/s (config-4 shape)",
         "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -796,7 +803,7 @@ def run_scores(args) -> int:
                                "heads", "t_kv": t_kv, "cache_copies": n_copies,
                    "algorithmic_bytes_per_launch": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic},
         "per_launch_us": {"mean": round(float(np.mean(per)), 3),
                           "median": round(float(np.median(per)), 3)},
         "lut_plus_gather_us": round(whole, 3),
