@@ -466,6 +466,33 @@ int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_he
                            void *stream);
 
 /*
+ * ss_decode_attn_grouped and ss_decode_attn_dense over a hybrid cache: the
+ * recent-token buffer (k_buf / v_buf, buf_dtype SS_F16 / SS_BF16 / SS_F32,
+ * element j of token t of (b, h) at b*buf_sb + h*buf_sh + t*buf_st + j,
+ * original basis) joins the same softmax as positions t_kv .. t_kv + t_buf - 1
+ * (one more split partial: fp32 dot products with the unpermuted scaled
+ * query, online softmax over 256-token chunks).  The reference runs its
+ * two-pass path whenever the buffer holds tokens (attention.py:238,
+ * 307-350).  Workspace: ss_decode_turboquant_workspace_bytes(..., t_buf, ...)
+ * bytes, the same layout.
+ */
+int ss_decode_attn_grouped_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint32_t *packed, const void *scales,
+    const void *zeros, int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv,
+    const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
+    void *workspace, size_t workspace_bytes, int n_splits, void *stream);
+int ss_decode_attn_dense_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const void *values, int v_dtype, int64_t cap,
+    int64_t t_kv, const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb,
+    int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out,
+    int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream);
+
+/*
  * As ss_decode_attn_dense with TurboQuant values (reference
  * value_codecs.py:136-177): token t's value is norms[t] * (levels[code_t] @
  * rotation), code_t its packed BITS-bit codes.  The reference has no fused

@@ -127,6 +127,16 @@ _SIGNATURES = {
                                       _c_void_p, _c_void_p, _int, _int, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64, _int,
                                       _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_attn_grouped_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_attn_dense_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
+        _c_void_p, _c_void_p, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_decode_attn_turboquant": (_int, [
         _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _int, _int,
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
@@ -773,9 +783,13 @@ def decode_attn_dense(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
                       centroids: torch.Tensor, idx: torch.Tensor, values: torch.Tensor,
                       t_kv: int, causal: bool = False, q_offset: int = 0,
                       out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                      n_splits: int = 0) -> torch.Tensor:
+                      n_splits: int = 0, buf_keys: torch.Tensor | None = None,
+                      buf_values: torch.Tensor | None = None, buf_len: int = 0) -> torch.Tensor:
     """Fused decode over a (B, Hkv, cap, NB) index buffer and (B, Hkv, cap, D)
-    dense values; returns (B, Hq, T_q, D)."""
+    dense values; returns (B, Hq, T_q, D).  A hybrid cache's recent tokens
+    ``buf_keys``/``buf_values`` (B, Hkv, >= buf_len, D) join the same
+    softmax as positions t_kv .. t_kv + buf_len - 1
+    (``ss_decode_attn_dense_hybrid``)."""
     _check_decode_common(q, idx, centroids, perm)
     require_gpu(values)
     if values.dim() != 4 or not values.is_contiguous():
@@ -787,6 +801,21 @@ def decode_attn_dense(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
     nc = centroids.shape[1]
     if out is None:
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    buf_len = int(buf_len)
+    if buf_len > 0:
+        buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
+                                                                b_, hkv, d)
+        lib = load_library()
+        ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv),
+                                                            buf_len, int(n_splits))
+        ws = decode_workspace(q.device, ws_bytes)
+        _launched(_attn_stat("sunshape_fused_attention", causal), lib.ss_decode_attn_dense_hybrid(
+            ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm),
+            ptr(centroids), nb, nc, ptr(idx), ptr(values), dtype_code(values.dtype), cap,
+            int(t_kv), ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh, bst, buf_len,
+            int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+            ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
+        return out
     ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
     _launched(_attn_stat("sunshape_fused_attention", causal), load_library().ss_decode_attn_dense(
@@ -1107,8 +1136,12 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
                         scales: torch.Tensor, zeros: torch.Tensor, bits: int, group_size: int,
                         t_kv: int, causal: bool = False, q_offset: int = 0,
                         out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                        n_splits: int = 0) -> torch.Tensor:
-    """Fused decode with grouped-quantised values decoded in registers."""
+                        n_splits: int = 0, buf_keys: torch.Tensor | None = None,
+                        buf_values: torch.Tensor | None = None,
+                        buf_len: int = 0) -> torch.Tensor:
+    """Fused decode with grouped-quantised values decoded in registers.  A
+    hybrid cache's recent tokens join the softmax as in
+    :func:`decode_attn_dense` (``ss_decode_attn_grouped_hybrid``)."""
     _check_decode_common(q, idx, centroids, perm)
     require_gpu(packed, scales, zeros)
     for name, t in (("packed", packed), ("scales", scales), ("zeros", zeros)):
@@ -1123,6 +1156,23 @@ def decode_attn_grouped(q: torch.Tensor, scale: float, perm: torch.Tensor | None
     nc = centroids.shape[1]
     if out is None:
         out = torch.empty((b_, hq, tq, d), dtype=out_dtype or q.dtype, device=q.device)
+    buf_len = int(buf_len)
+    if buf_len > 0:
+        buf_keys, buf_values, bdt, bsb, bsh, bst = _buffer_args(buf_keys, buf_values, buf_len,
+                                                                b_, hkv, d)
+        lib = load_library()
+        ws_bytes = lib.ss_decode_turboquant_workspace_bytes(b_, hq, hkv, tq, d, int(t_kv),
+                                                            buf_len, int(n_splits))
+        ws = decode_workspace(q.device, ws_bytes)
+        _launched(_attn_stat("sunshape_fused_attention_dequant", causal),
+                  lib.ss_decode_attn_grouped_hybrid(
+                      ptr(q), dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm),
+                      ptr(centroids), nb, nc, ptr(idx), ptr(packed), ptr(scales), ptr(zeros),
+                      dtype_code(scales.dtype), int(bits), int(group_size), cap, int(t_kv),
+                      ptr(buf_keys), ptr(buf_values), bdt, bsb, bsh, bst, buf_len,
+                      int(bool(causal)), int(q_offset), ptr(out), dtype_code(out.dtype), ptr(ws),
+                      ws_bytes if ws is not None else 0, int(n_splits), stream_handle(q.device)))
+        return out
     ws_bytes = decode_workspace_bytes(b_, hq, hkv, tq, d, t_kv, n_splits)
     ws = decode_workspace(q.device, ws_bytes)
     _launched(_attn_stat("sunshape_fused_attention_dequant", causal), load_library().ss_decode_attn_grouped(

@@ -164,11 +164,7 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
             if out is not None:
                 codec.last_score_backend = "hip_prefill_mfma_hybrid"
                 return out
-    # the buffer joins the fused softmax on the interleaved fp16, grouped
-    # interleaved, TurboQuant (both layouts) and SunShape-value kernels
-    if buffered and ops["kind"] not in ("il8", "grouped_il", "turboquant_il", "turboquant",
-                                        "sunshape_v"):
-        return None
+    # the buffer joins the fused softmax on every fused kernel
     if buffered and codec.mode not in PERM_MODES and codec.use_rotation:
         # the kernels score buffered keys against the query they are given,
         # here the rotated one: (q R^T) . (k R^T) = q . k for orthogonal R,
@@ -264,12 +260,16 @@ def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: i
         elif ops["kind"] == "grouped":
             out = _hip.decode_attn_grouped(q, kscale, perm, codec.centroids, ops["idx"],
                                            ops["packed"], ops["scales"], ops["zeros"],
-                                           ops["bits"], ops["group_size"], **kw)
-            codec.last_score_backend = "hip_fused_dequant"
+                                           ops["bits"], ops["group_size"],
+                                           buf_keys=ops.get("buf_keys"),
+                                           buf_values=ops.get("buf_values"), buf_len=buffered,
+                                           **kw)
+            codec.last_score_backend = "hip_fused_dequant_buffer" if buffered else "hip_fused_dequant"
         else:
             out = _hip.decode_attn_dense(q, kscale, perm, codec.centroids, ops["idx"],
-                                         ops["values"], **kw)
-            codec.last_score_backend = "hip_fused"
+                                         ops["values"], buf_keys=ops.get("buf_keys"),
+                                         buf_values=ops.get("buf_values"), buf_len=buffered, **kw)
+            codec.last_score_backend = "hip_fused_buffer" if buffered else "hip_fused"
     except _hip.SunShapeUnsupported:
         return None
     return out

@@ -828,7 +828,9 @@ class HybridSunShapeKVCache:
             return {"kind": "grouped", "idx": self._key_indices,
                     "packed": self._values_packed.view(torch.uint32),
                     "scales": self._value_scales, "zeros": self._value_zeros,
-                    "bits": gc.bits, "group_size": gc.group_size}
+                    "bits": gc.bits, "group_size": gc.group_size,
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer)}
         if self.value_backend == "turboquant" and self._values_il is not None:
             tc = self._value_codec_impl
             tc._on(self._values_il.device)
@@ -858,7 +860,9 @@ class HybridSunShapeKVCache:
                     "buf_keys": self._window(self._key_buffer),
                     "buf_values": self._window(self._value_buffer), **heavy}
         if self.value_backend == "fp16" and self._values_fp16 is not None:
-            return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16}
+            return {"kind": "dense", "idx": self._key_indices, "values": self._values_fp16,
+                    "buf_keys": self._window(self._key_buffer),
+                    "buf_values": self._window(self._value_buffer)}
         return None
 
     def prefill_operands(self):

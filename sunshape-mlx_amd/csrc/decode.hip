@@ -3690,7 +3690,8 @@ __global__ void __launch_bounds__(256)
 // scaled query, in log2 units, at positions t_kv + t; online softmax over
 // chunks of 256 tokens; P.V in the original basis.  The accumulators are then
 // taken into the rotated basis, acc @ R^T (R orthogonal), where the merge
-// adds them to the compressed splits' before the output rotation.
+// adds them to the compressed splits' before the output rotation; with no
+// R (rot null: values in the original basis) they are stored as they are.
 template <int D, int R>
 __global__ void __launch_bounds__(256)
     buffer_partial_kernel(DecodeCommon c, const void *kbuf, const void *vbuf, int buf_dtype,
@@ -3809,7 +3810,10 @@ __global__ void __launch_bounds__(256)
         if (e < R * D) {
             const int r = e / D, kk = e - r * D;
             float a = 0.f;
-            for (int d = 0; d < D; ++d) a = fmaf(acc_s[r][d], rot[kk * D + d], a);
+            if (rot)
+                for (int d = 0; d < D; ++d) a = fmaf(acc_s[r][d], rot[kk * D + d], a);
+            else
+                a = acc_s[r][kk];
             c.part_acc[(slot0 + r) * D + kk] = a;
             if (kk == 0)
                 *reinterpret_cast<float2 *>(c.part_ml + (slot0 + r) * 2) = make_float2(m[r], l[r]);
@@ -4188,30 +4192,20 @@ extern "C" int ss_decode_default_splits(int64_t batch, int n_q_heads, int n_kv_h
     return decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, 0).S;
 }
 
-extern "C" int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_heads,
-                                    int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                    const int32_t *perm, const float *centroids, int n_blocks,
-                                    int n_centroids, const uint8_t *idx, const void *values,
-                                    int v_dtype, int64_t cap, int64_t t_kv, int causal,
-                                    int64_t q_offset, void *out, int out_dtype, void *workspace,
-                                    size_t workspace_bytes, int n_splits, void *stream) {
-    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
-                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
-    if (rc) return rc;
+static int dense_checks(const void *values, int v_dtype) {
     SS_REQUIRE(values, "null values");
     SS_REQUIRE(valid_dtype(v_dtype), "bad value dtype");
     SS_REQUIRE(((uintptr_t)values % 16) == 0, "values must be 16-byte aligned");
-    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
-    DecodeCommon c;
-    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
-                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
-                     workspace_bytes, head_dim);
-    if (rc) return rc;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    return SS_OK;
+}
+
+// The VALU decode over dense values (merge: whether it launches its own merge).
+static int launch_dense(const DecodeCommon &c, const DecodeShape &s, hipStream_t st, int head_dim,
+                        const void *values, int v_dtype, bool merge) {
 #define SS_DENSE(DD, TT)                                                                  \
     {                                                                                     \
         typename VDense<DD, TT>::Args va{reinterpret_cast<const TT *>(values)};           \
-        return launch_r<DD, VDense<DD, TT>>(c, va, s, st);                                \
+        return launch_r<DD, VDense<DD, TT>>(c, va, s, st, merge);                         \
     }
     if (head_dim == 128) {
         if (v_dtype == SS_F16) SS_DENSE(128, __half)
@@ -4225,18 +4219,29 @@ extern "C" int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, i
 #undef SS_DENSE
 }
 
-extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_heads,
-                                      int n_kv_heads, int64_t t_q, int head_dim, float scale,
-                                      const int32_t *perm, const float *centroids, int n_blocks,
-                                      int n_centroids, const uint8_t *idx,
-                                      const uint32_t *packed, const void *scales,
-                                      const void *zeros, int sz_dtype, int bits,
-                                      int group_size, int64_t cap, int64_t t_kv, int causal,
-                                      int64_t q_offset, void *out, int out_dtype, void *workspace,
-                                      size_t workspace_bytes, int n_splits, void *stream) {
+extern "C" int ss_decode_attn_dense(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                    int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                    const int32_t *perm, const float *centroids, int n_blocks,
+                                    int n_centroids, const uint8_t *idx, const void *values,
+                                    int v_dtype, int64_t cap, int64_t t_kv, int causal,
+                                    int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                    size_t workspace_bytes, int n_splits, void *stream) {
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
                           n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
     if (rc) return rc;
+    if ((rc = dense_checks(values, v_dtype))) return rc;
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    return launch_dense(c, s, reinterpret_cast<hipStream_t>(stream), head_dim, values, v_dtype,
+                        true);
+}
+
+static int grouped_checks(int head_dim, const uint32_t *packed, const void *scales,
+                          const void *zeros, int sz_dtype, int bits, int group_size) {
     SS_REQUIRE(packed && scales && zeros, "null packed/scales/zeros");
     SS_REQUIRE(bits == 2 || bits == 3 || bits == 4, "bits must be 2, 3 or 4 (got %d)", bits);
     SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
@@ -4248,20 +4253,21 @@ extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch,
     SS_UNSUPPORTED(group_size >= 32 / bits, "group_size %d < %d values per word", group_size,
                    32 / bits);
     SS_REQUIRE(((uintptr_t)packed % 4) == 0, "packed values must be 4-byte aligned");
-    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
-    DecodeCommon c;
-    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
-                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
-                     workspace_bytes, head_dim);
-    if (rc) return rc;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    return SS_OK;
+}
+
+// The VALU decode over reference-format grouped values (merge: whether it
+// launches its own merge).
+static int launch_grouped(const DecodeCommon &c, const DecodeShape &s, hipStream_t st,
+                          int head_dim, const uint32_t *packed, const void *scales,
+                          const void *zeros, int sz_dtype, int bits, int group_size, bool merge) {
     const int n_groups = head_dim / group_size;
 #define SS_GROUPED(DD, BB, SZT)                                                          \
     {                                                                                    \
         typename VGrouped<DD, BB, SZT>::Args va{packed, reinterpret_cast<const SZT *>(scales), \
                                                 reinterpret_cast<const SZT *>(zeros),    \
                                                 group_size, n_groups};                   \
-        return launch_r<DD, VGrouped<DD, BB, SZT>>(c, va, s, st);                        \
+        return launch_r<DD, VGrouped<DD, BB, SZT>>(c, va, s, st, merge);                 \
     }
 #define SS_GROUPED_BITS(DD, SZT)            \
     {                                       \
@@ -4278,6 +4284,30 @@ extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch,
     }
 #undef SS_GROUPED_BITS
 #undef SS_GROUPED
+}
+
+extern "C" int ss_decode_attn_grouped(const void *q, int q_dtype, int64_t batch, int n_q_heads,
+                                      int n_kv_heads, int64_t t_q, int head_dim, float scale,
+                                      const int32_t *perm, const float *centroids, int n_blocks,
+                                      int n_centroids, const uint8_t *idx,
+                                      const uint32_t *packed, const void *scales,
+                                      const void *zeros, int sz_dtype, int bits,
+                                      int group_size, int64_t cap, int64_t t_kv, int causal,
+                                      int64_t q_offset, void *out, int out_dtype, void *workspace,
+                                      size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    if ((rc = grouped_checks(head_dim, packed, scales, zeros, sz_dtype, bits, group_size)))
+        return rc;
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, centroids,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    return launch_grouped(c, s, reinterpret_cast<hipStream_t>(stream), head_dim, packed, scales,
+                          zeros, sz_dtype, bits, group_size, true);
 }
 
 // Workspace of the TurboQuant decode: the split partials (as for the other
@@ -4319,7 +4349,10 @@ extern "C" size_t ss_decode_turboquant_workspace_bytes(int64_t batch, int n_q_he
 // rotation): the VALU decode writes y (fp32, that basis) or split partials;
 // buffered original-basis tokens become one more partial, taken into that
 // basis with transform^T (orthogonal); the merge launch, or rotate_rows_kernel
-// for a single split, writes out = y @ transform in out_dtype.
+// for a single split, writes out = y @ transform in out_dtype.  A null
+// transform is the identity (values in the original basis: the grouped and
+// dense VALU decodes with a hybrid cache's buffer): the kernels and the merge
+// write out directly.
 template <class MainLaunch>
 static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq, int hkv,
                               int64_t t_q, int head_dim, float scale, const int32_t *perm,
@@ -4330,8 +4363,8 @@ static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq,
                               int causal, int64_t q_offset, void *out, int out_dtype,
                               void *workspace, size_t workspace_bytes, int n_splits,
                               void *stream, MainLaunch &&launch_main, int kind = kKindValu) {
-    SS_REQUIRE(transform && ((uintptr_t)transform % 4) == 0,
-               "null or misaligned transform/rotation matrix");
+    const bool ident = transform == nullptr;
+    SS_REQUIRE(((uintptr_t)transform % 4) == 0, "misaligned transform/rotation matrix");
     SS_REQUIRE(t_buf >= 0, "negative buffer length");
     if (t_buf > 0) {
         SS_REQUIRE(k_buf && v_buf, "null buffer keys/values");
@@ -4354,8 +4387,8 @@ static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq,
                                          (size_t)rows * head_dim * sizeof(float));
     DecodeCommon c;
     int rc = fill_common(c, sw, q, q_dtype, hq, hkv, t_q, scale, perm, centroids, n_centroids,
-                         idx, cap, t_kv, causal, q_offset, y, SS_F32, workspace, workspace_bytes,
-                         head_dim);
+                         idx, cap, t_kv, causal, q_offset, ident ? out : y,
+                         ident ? out_dtype : SS_F32, workspace, workspace_bytes, head_dim);
     if (rc) return rc;
     c.tiles_per_split = s.tiles_per_split;  // the compressed tokens' splits: grid s.S
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -4376,6 +4409,7 @@ static int transformed_decode(const void *q, int q_dtype, int64_t batch, int hq,
     if (sw.S > 1)
         return head_dim == 128 ? launch_merge<128>(c, sw, st, transform, out, out_dtype)
                                : launch_merge<64>(c, sw, st, transform, out, out_dtype);
+    if (ident) return SS_OK;  // the one split wrote out
     const unsigned blocks = (unsigned)((rows + kRotRows - 1) / kRotRows);
     if (head_dim == 128)
         hipLaunchKernelGGL(rotate_rows_kernel<128>, dim3(blocks), dim3(256), 0, st, y, transform,
@@ -4433,6 +4467,49 @@ extern "C" int ss_decode_attn_turboquant(
     };
     return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
                               centroids, n_centroids, idx, cap, t_kv, rotation, k_buf, v_buf,
+                              buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
+                              out_dtype, workspace, workspace_bytes, n_splits, stream, main);
+}
+
+extern "C" int ss_decode_attn_grouped_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const uint32_t *packed, const void *scales,
+    const void *zeros, int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv,
+    const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+    int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out, int out_dtype,
+    void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    if ((rc = grouped_checks(head_dim, packed, scales, zeros, sz_dtype, bits, group_size)))
+        return rc;
+    auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
+        return launch_grouped(c, s, st, head_dim, packed, scales, zeros, sz_dtype, bits,
+                              group_size, false);
+    };
+    return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                              centroids, n_centroids, idx, cap, t_kv, nullptr, k_buf, v_buf,
+                              buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
+                              out_dtype, workspace, workspace_bytes, n_splits, stream, main);
+}
+
+extern "C" int ss_decode_attn_dense_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const float *centroids, int n_blocks,
+    int n_centroids, const uint8_t *idx, const void *values, int v_dtype, int64_t cap,
+    int64_t t_kv, const void *k_buf, const void *v_buf, int buf_dtype, int64_t buf_sb,
+    int64_t buf_sh, int64_t buf_st, int64_t t_buf, int causal, int64_t q_offset, void *out,
+    int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    if ((rc = dense_checks(values, v_dtype))) return rc;
+    auto main = [&](const DecodeCommon &c, const DecodeShape &s, hipStream_t st) -> int {
+        return launch_dense(c, s, st, head_dim, values, v_dtype, false);
+    };
+    return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm,
+                              centroids, n_centroids, idx, cap, t_kv, nullptr, k_buf, v_buf,
                               buf_dtype, buf_sb, buf_sh, buf_st, t_buf, causal, q_offset, out,
                               out_dtype, workspace, workspace_bytes, n_splits, stream, main);
 }

@@ -349,6 +349,43 @@ def test_hybrid_buffer_joins_fused_decode(buf, t_total, tq, causal, dtype):
     assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("backend,bits,dtype,buf,t_total,tq,causal", [
+    ("grouped", 3, torch.float16, 128, 700, 1, False),   # 3-bit codes: reference packed rows
+    ("grouped", 3, torch.float16, 64, 300, 5, True),     # prefill rows, causal across the buffer
+    ("grouped", 3, torch.float32, 200, 1000, 1, False),  # buffer past one 256-token chunk
+    ("fp16", None, torch.bfloat16, 120, 450, 1, False),  # bf16 values: token-major storage
+    ("fp16", None, torch.float32, 96, 300, 5, True),
+])
+def test_hybrid_buffer_joins_fused_valu_decode(backend, bits, dtype, buf, t_total, tq, causal):
+    """Hybrid caches whose values take the vector-ALU decodes (3-bit grouped
+    codes in the reference's packed rows, token-major bf16 / f32 values) keep
+    their buffered tokens in the fused launch (one more split partial), equal
+    to the reference's two-pass path over the same cache."""
+    codec = make_codec(33)
+    b, hq, hkv, d = 2, 8, 2, 128
+    k, v = kv(34 + buf, b, hkv, t_total, d, dtype=dtype)
+    kw = {"value_bits": bits} if bits else {}
+    cache = S.create_kv_cache(codec, n_kv_heads=hkv, value_backend=backend, buffer_size=buf,
+                              dtype=dtype, **kw)
+    assert isinstance(cache, S.HybridSunShapeKVCache)
+    pos = 0
+    for n in (t_total - 37, 30, 7):
+        cache.update_and_fetch(k[:, :, pos:pos + n], v[:, :, pos:pos + n])
+        pos += n
+    assert cache.buffer_offset > 0 and cache.compressed_offset > 0
+    assert cache.fused_operands()["kind"] == ("grouped" if backend == "grouped" else "dense")
+    q = torch.randn((b, hq, tq, d), device=DEV).to(torch.float16)
+    mask = "causal" if causal else None
+    out = S.sunshape_sdpa(q, cache, 0.088, mask=mask)
+    assert codec.last_score_backend == ("hip_fused_dequant_buffer" if backend == "grouped"
+                                        else "hip_fused_buffer")
+    vals = cache.values.float().cpu().numpy()  # compressed values dequantised, then buffer
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), cache.key_indices.cpu().numpy(),
+                          cache.buffer_keys.float().cpu().numpy(), vals, mask=mask)
+    assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
 @pytest.mark.parametrize("buf,t_total,tq,causal", [
     (96, 700, 1, False),     # decode step (a 128-token buffer makes a SunShapeKVCache)
     (64, 300, 5, True),      # prefill rows, causal across the buffer
