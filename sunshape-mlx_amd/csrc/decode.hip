@@ -68,6 +68,10 @@ struct DecodeCommon {
     const __half *kheavy;
     const int32_t *heavy_dims;
     int nhd;
+    // matrix-core kernel writing the output itself (one split, or the
+    // in-kernel merge): rows accumulated in a transformed basis leave as
+    // y @ rot ([D][D] float32, row k = basis vector k); null: as they are
+    const float *rot = nullptr;
 };
 constexpr int kMaxHeavyMfma = 32;  // heavy dims the matrix-core kernels take
 
@@ -2876,6 +2880,33 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             A += ab * f;
         }
     };
+    // Output rows: stored as they are, or, with c.rot, staged in LDS (the
+    // LUT's space, free after the tile loop) and stored as y @ rot once
+    // every dim of the rows is there (rot_rows, called by every thread).
+    float *yrows = reinterpret_cast<float *>(smem);  // [R][D]
+    auto put4 = [&](int r, int d0, f32x4 y) {
+        if (c.rot) {
+            *reinterpret_cast<float4 *>(yrows + r * D + d0) = make_float4(y[0], y[1], y[2], y[3]);
+        } else if (row_ok(r)) {
+            store4_from_f32(c.out, c.out_dtype, row_off(r) + d0, y[0], y[1], y[2], y[3]);
+        }
+    };
+    auto rot_rows = [&]() {
+        if (!c.rot) return;
+        __syncthreads();
+        for (int i = tid; i < R * D; i += THREADS) {
+            const int r = i / D, d = i - r * D;
+            if (!row_ok(r)) continue;
+            const float *yr = yrows + r * D;
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+            for (int k = 0; k < D; k += 2) {
+                a0 = fmaf(yr[k], c.rot[k * D + d], a0);
+                a1 = fmaf(yr[k + 1], c.rot[(k + 1) * D + d], a1);
+            }
+            store_from_f32(c.out, c.out_dtype, row_off(r) + d, a0 + a1);
+        }
+    };
     const int S = c.n_splits;
     if (S == 1) {
         for (int i = tid; i < R * D / 4; i += THREADS) {
@@ -2883,11 +2914,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             float M, L;
             f32x4 A;
             combine4(r, d0, M, L, A);
-            if (row_ok(r)) {
-                const float iv = L > 0.f ? 1.f / L : 0.f;
-                store4_from_f32(c.out, c.out_dtype, row_off(r) + d0, A[0] * iv, A[1] * iv, A[2] * iv, A[3] * iv);
-            }
+            const float iv = L > 0.f ? 1.f / L : 0.f;
+            put4(r, d0, A * iv);
         }
+        rot_rows();
         return;
     }
 
@@ -2984,12 +3014,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 Lr = Lr * fo + l2 * fn;
                 Mr = Mn;
             }
-            if (row_ok(mr)) {
-                const float iv = Lr > 0.f ? 1.f / Lr : 0.f;
-                store4_from_f32(c.out, c.out_dtype, row_off(mr) + md0, Ar[0] * iv, Ar[1] * iv, Ar[2] * iv,
-                                Ar[3] * iv);
-            }
+            const float iv = Lr > 0.f ? 1.f / Lr : 0.f;
+            put4(mr, md0, Ar * iv);
         }
+        rot_rows();
         if (tid == 0)
             __hip_atomic_store(c.part_cnt + (int64_t)col * c.cnt_stride, 0, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -3077,12 +3105,13 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             if (s2 < cs) acc0 += cf4[((s2 * R + mr) * D + md0) / 4] * wts[(s0 + s2) * R + mr];
         }
     }
-    if (tid < CH4 && row_ok(mr)) {
+    if (tid < CH4) {
         const float L = lrow[mr];
         const f32x4 A = acc0 + acc1;
         const float iv = L > 0.f ? 1.f / L : 0.f;
-        store4_from_f32(c.out, c.out_dtype, row_off(mr) + md0, A[0] * iv, A[1] * iv, A[2] * iv, A[3] * iv);
+        put4(mr, md0, A * iv);
     }
+    rot_rows();
     if (tid == 0)
         __hip_atomic_store(c.part_cnt + (int64_t)col * c.cnt_stride, 0, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -4105,6 +4134,7 @@ static int fill_common(DecodeCommon &c, const DecodeShape &s, const void *q, int
     c.kheavy = nullptr;
     c.heavy_dims = nullptr;
     c.nhd = 0;
+    c.rot = nullptr;
     c.part_ml = nullptr;
     c.part_acc = nullptr;
     c.part_cnt = nullptr;
@@ -5057,13 +5087,20 @@ extern "C" int ss_decode_attn_turboquant_il(
                    "2-bit levels are not affine in the code bits (L3 != L2 + L1 - L0)");
     typename VTq<128>::Args va128{codes_il, norms, levels[0], levels[1] - levels[0],
                                   levels[2] - 2.f * levels[1] + levels[0]};
-    auto main = [&](const DecodeCommon &c0, const DecodeShape &s, hipStream_t st) -> int {
+    // fused: the kernel writes out itself, rotated (one split, or its
+    // in-kernel merge); else split partials that transformed_decode merges
+    // with the buffer's partial and rotates
+    auto launch_tq = [&](const DecodeCommon &c0, const DecodeShape &s, hipStream_t st,
+                         bool fused) -> int {
         DecodeCommon c = c0;
         c.centroids = nullptr;
         c.codebook = static_cast<const uint4 *>(codebook);
         c.codebook_mul = reinterpret_cast<const float *>(
             static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
-        c.fused_merge = 0;  // transformed_decode merges (buffer partial, rotation)
+        if (fused)
+            c.rot = rotation;
+        else
+            c.fused_merge = 0;
         const int hrc = set_heavy(c, k_heavy, heavy_dims, n_heavy_dims);
         if (hrc) return hrc;
         auto go = [&](auto dd, auto vf) -> int {
@@ -5086,6 +5123,21 @@ extern "C" int ss_decode_attn_turboquant_il(
                                    : go(I64{}, TypeTag<WithHeavy<VTq<64>>>{});
         return head_dim == 128 ? go(I128{}, TypeTag<VTq<128>>{})
                                : go(I64{}, TypeTag<VTq<64>>{});
+    };
+    if (t_buf == 0) {
+        // no buffered tokens: one launch, rotation applied by the kernel
+        const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits, kKindMfma);
+        DecodeCommon c;
+        rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents, n_centroids,
+                         idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace, workspace_bytes,
+                         head_dim);
+        if (rc) return rc;
+        SS_REQUIRE(((uintptr_t)rotation % 4) == 0, "misaligned rotation matrix");
+        if (s.S == 1 || c.fused_merge)
+            return launch_tq(c, s, reinterpret_cast<hipStream_t>(stream), true);
+    }
+    auto main = [&](const DecodeCommon &c0, const DecodeShape &s, hipStream_t st) -> int {
+        return launch_tq(c0, s, st, false);
     };
     return transformed_decode(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale, perm, cents,
                               n_centroids, idx, cap, t_kv, rotation, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
