@@ -283,7 +283,14 @@ def run_hybrid(args) -> int:
     step = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
     step["t_kv_range"] = [t_kv, caches[0].offset]
     log(f"hybrid decode step end to end: {step['us_per_step']:.2f} us/step "
-        f"(host {step['host_us_per_step']:.1f} us/step)")
+        f"(host {step['host_us_per_step']:.1f} us/step, {step['backend']})")
+    # the same steps with the flush and buffer store as their own launch
+    # (fuse_steps off)
+    for c in caches:
+        c.fuse_steps = False
+    sep = time_api_steps(pkg, caches, q, scale, n_step, args.warmup, kv_step=(k1, v1))
+    step["separate_append"] = {k_: sep[k_] for k_ in ("us_per_step", "host_us_per_step")}
+    log(f"  ... with the step launched separately: {sep['us_per_step']:.2f} us/step")
     del caches
 
     traffic = None  # HBM bytes per launch from the committed counter runs

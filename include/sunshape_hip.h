@@ -686,6 +686,40 @@ int ss_decode_step_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                        size_t workspace_bytes, int n_splits, void *stream);
 
 /*
+ * One decode step of a hybrid cache with 2-bit interleaved grouped values
+ * (ss_decode_attn_grouped_il_hybrid's layouts) in one launch.  The cache holds
+ * t_kv (>= 1) compressed tokens and n_buf buffered float16 tokens, the buffer
+ * window at k_buf / v_buf [b*buf_sb + h*buf_sh + row*buf_st + dim], rows 0 ..
+ * n_buf-1 oldest first; the step's n_new (1..4) float16 tokens arrive at
+ * k_new / v_new [b*kv_sb + h*kv_sh + j*kv_st + dim].  As the reference's
+ * HybridSunShapeKVCache.update_and_fetch (cache.py:656-710) followed by its
+ * attention (attention.py:307-350), the n_flush (0..4, <= n_buf) oldest
+ * buffered tokens move into compressed storage and the new tokens into the
+ * buffer, and every token is attended: the kernel encodes the flushed keys
+ * (indices identical to ss_hybrid_append_grouped_il's, as ss_decode_step_il8
+ * encodes), quantises their values with the grouped min/max rule (codes,
+ * scale and zero identical to it), attends them in that compressed form at
+ * positions t_kv .., the remaining buffered and the new tokens exactly after
+ * them, and stores the flushed tokens' index rows, codes, scales and zeros
+ * at positions t_kv .. t_kv + n_flush - 1 and the new tokens at buffer rows
+ * n_buf .. n_buf + n_new - 1 (the caller's buffer store must hold them).
+ * Other arguments as ss_decode_attn_grouped_il (bits 2); centroids float32
+ * [n_blocks][n_centroids][8] (16-byte aligned), codebook their
+ * ss_codebook_f16x2.  The caller then counts t_kv + n_flush compressed and
+ * n_buf - n_flush + n_new buffered tokens, the window starting n_flush rows
+ * later.  Calls sharing a cache must not overlap.
+ */
+int ss_decode_step_grouped_il_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, uint32_t *codes_il, void *scales, void *zeros,
+    int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv, void *k_buf, void *v_buf,
+    int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t n_buf, int64_t n_flush,
+    const void *k_new, const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+    int64_t n_new, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream);
+
+/*
  * The inverse of ss_pack_grouped_il: the first n_t tokens of interleaved
  * codes codes_il [n_bh][cap/tpw][head_dim] (n_bh = batch x heads rows) as
  * pack_indices rows out [n_bh][n_t][head_dim*bits/32].  Replaces the

@@ -165,6 +165,12 @@ _SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64,
         _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _int,
         _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_step_grouped_il_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _c_void_p,
+        _int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _int, _int, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                                   _c_void_p, _i64, _i64, _c_void_p]),
     "ss_grouped_il_to_packed": (_int, [_c_void_p, _i64, _i64, _int, _int, _i64, _c_void_p,
@@ -630,6 +636,126 @@ def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
                                       "sunshape_fused_attention_dequant_mfma", buf_keys)
     return PreparedDecode(lib.ss_decode_attn_grouped_il, pre, q,
                           "sunshape_fused_attention_dequant_mfma")
+
+
+class PreparedHybridStep(PreparedDecode):
+    """One decode step of a hybrid cache with 2-bit interleaved grouped
+    values in one launch (``ss_decode_step_grouped_il_hybrid``): a call
+    passes the buffer stores' window (``buf_keys`` / ``buf_values``, (B, Hkv,
+    >= n_buf + n_new, D) float16 views starting at the oldest buffered
+    token), the number of buffered tokens, how many of the oldest leave the
+    buffer, and the step's new keys and values (B, Hkv, n_new, D) float16;
+    the kernel writes the leaving tokens' index rows, codes, scales and
+    zeros at compressed positions t_kv .., the new tokens at buffer rows
+    n_buf .., and attends every token as the reference does after its
+    append and flush."""
+
+    __slots__ = ("buf_strides",)
+
+    def __init__(self, fn, pre: tuple, q: torch.Tensor, stat: str, buf_keys: torch.Tensor):
+        super().__init__(fn, pre, q, stat)
+        self.buf_strides = tuple(buf_keys.stride()[:3])
+
+    def __call__(self, q: torch.Tensor, t_kv: int, buf_keys: torch.Tensor,
+                 buf_values: torch.Tensor, n_buf: int, n_flush: int, k_new: torch.Tensor,
+                 v_new: torch.Tensor, causal: bool = False, q_offset: int = 0,
+                 out: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if q.shape != self.shape or q.dtype != self.dtype or not q.is_contiguous() or \
+                q.device.index != self.dev:
+            raise ValueError(f"query must be contiguous {self.dtype} {self.shape} on cuda:{self.dev}")
+        n_new = int(k_new.shape[2])
+        if buf_keys.dtype != torch.float16 or buf_values.dtype != torch.float16 or \
+                tuple(buf_keys.stride()[:3]) != self.buf_strides or \
+                tuple(buf_values.stride()[:3]) != self.buf_strides or \
+                buf_keys.shape[2] < n_buf + n_new or buf_values.shape[2] < n_buf + n_new:
+            raise ValueError("buffer views must be float16, keep the plan's strides and hold "
+                             "n_buf + n_new rows")
+        st3 = k_new.stride()[:3]
+        if k_new.dtype != torch.float16 or v_new.dtype != torch.float16 or \
+                k_new.shape != v_new.shape or v_new.stride()[:3] != st3 or \
+                k_new.stride(-1) != 1 or v_new.stride(-1) != 1 or \
+                k_new.device.index != self.dev or v_new.device.index != self.dev:
+            raise ValueError("new keys and values must be float16 (B, Hkv, n, D) with equal "
+                             "strides and unit last stride")
+        if out is None:
+            out = torch.empty(self.shape, dtype=out_dtype or self.dtype, device=q.device)
+        elif tuple(out.shape) != self.shape or not out.is_contiguous() or out.device != q.device:
+            raise ValueError(f"out must be contiguous {self.shape} on cuda:{self.dev}")
+        _poll_waits(self.dev)
+        st = stream_handle(self.dev)
+        ws = _ws_cache.get((self.dev, st))
+        if ws is None:
+            ws = decode_workspace(self.dev, 1, st)
+        mid = (int(t_kv), buf_keys.data_ptr(), buf_values.data_ptr(), SS_F16, *self.buf_strides,
+               int(n_buf), int(n_flush), k_new.data_ptr(), v_new.data_ptr(), SS_F16, *st3, n_new,
+               int(bool(causal)), int(q_offset), out.data_ptr(), dtype_code(out.dtype))
+        rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        if rc == SS_ERR_WORKSPACE:
+            _, need = decode_plan(KIND_IL8, *self.plan_args, int(t_kv), 0)
+            ws = decode_workspace(self.dev, need, st)
+            rc = self.fn(q.data_ptr(), *self.pre, *mid, ws.data_ptr(), ws.numel(), 0, st)
+        _launched(_attn_stat(self.stat, causal), rc)
+        if _check_waits:
+            check_decode_waits(self.dev)
+        return out
+
+
+def prepare_decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                                          codebook: torch.Tensor, centroids: torch.Tensor,
+                                          n_blocks: int, n_centroids: int, idx: torch.Tensor,
+                                          codes_il: torch.Tensor, scales: torch.Tensor,
+                                          zeros: torch.Tensor, bits: int, group_size: int,
+                                          buf_keys: torch.Tensor) -> PreparedHybridStep:
+    """:class:`PreparedHybridStep` for queries shaped like ``q`` over the
+    compressed stores (``idx``, ``codes_il``, ``scales``, ``zeros``; written
+    by the call) and buffer stores shaped like ``buf_keys``, with the float32
+    ``centroids`` (n_blocks, n_centroids, 8) for the exact encode and their
+    prepared ``codebook`` for the LUT."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(codes_il, scales, zeros, codebook, centroids, buf_keys)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if bits != 2:
+        raise SunShapeUnsupported("a fused hybrid step takes 2-bit grouped codes")
+    if nb != n_blocks or codes_il.dim() != 4 or not codes_il.is_contiguous() or \
+            tuple(codes_il.shape) != (b_, hkv, cap // 16, d) or \
+            codes_il.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("codes_il does not match the cache shape")
+    for t in (scales, zeros):
+        if t.dim() != 4 or not t.is_contiguous() or t.shape[:3] != idx.shape[:3]:
+            raise ValueError("scales/zeros must be contiguous (B, n_kv_heads, cap, n_groups)")
+    if scales.dtype != zeros.dtype or scales.dtype not in (torch.float32, torch.float16):
+        raise ValueError("scales/zeros must share dtype float32 or float16")
+    if centroids.dtype != torch.float32 or not centroids.is_contiguous() or \
+            tuple(centroids.shape) != (n_blocks, n_centroids, 8):
+        raise ValueError(f"centroids must be contiguous float32 {(n_blocks, n_centroids, 8)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(n_blocks, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    _buffer_args(buf_keys, buf_keys, 1, b_, hkv, d)
+    pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+           ptr(centroids), nb, n_centroids, ptr(idx), ptr(codes_il), ptr(scales), ptr(zeros),
+           dtype_code(scales.dtype), int(bits), int(group_size), cap)
+    return PreparedHybridStep(lib.ss_decode_step_grouped_il_hybrid, pre, q,
+                              "sunshape_fused_attention_dequant_mfma", buf_keys)
+
+
+def decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                                  codebook: torch.Tensor, centroids: torch.Tensor,
+                                  idx: torch.Tensor, codes_il: torch.Tensor, scales: torch.Tensor,
+                                  zeros: torch.Tensor, bits: int, group_size: int, t_kv: int,
+                                  buf_keys: torch.Tensor, buf_values: torch.Tensor, n_buf: int,
+                                  n_flush: int, k_new: torch.Tensor, v_new: torch.Tensor,
+                                  causal: bool = False, q_offset: int = 0,
+                                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """One launch of :class:`PreparedHybridStep` (checks every call)."""
+    nb, nc = int(centroids.shape[0]), int(centroids.shape[1])
+    plan = prepare_decode_step_grouped_il_hybrid(q, scale, perm, codebook, centroids, nb, nc, idx,
+                                                 codes_il, scales, zeros, bits, group_size,
+                                                 buf_keys)
+    return plan(q, t_kv, buf_keys, buf_values, n_buf, n_flush, k_new, v_new, causal, q_offset,
+                out_dtype=out_dtype)
 
 
 # --------------------------------------------------------------------------- #

@@ -119,13 +119,56 @@ def _fused_step(cache: SunShapeKVCache, queries: torch.Tensor, scale: float, cau
     return out
 
 
+def _fused_hybrid_step(cache: HybridSunShapeKVCache, queries: torch.Tensor, scale: float,
+                       causal: bool, q_offset: int, out_dtype: torch.dtype):
+    """The decode step a hybrid cache with 2-bit grouped values holds back
+    (``cache.fuse_steps``): one ``ss_decode_step_grouped_il_hybrid`` launch
+    moves the tokens that leave the buffer into compressed storage, stores
+    the new ones in the buffer and attends every token; None (step still
+    held) when that launch does not apply."""
+    codec = cache.codec
+    q, kscale, perm = _kernel_query(codec, queries, scale)
+    tensors = (cache._key_indices, cache._values_il, cache._value_scales, cache._value_zeros,
+               codec.kernel_codebook(), codec.centroids, cache._key_buffer, cache._value_buffer)
+    if perm is not None:
+        tensors += (perm,)
+    key = ("hstep", q.shape, q.dtype, q.device, kscale)
+    held = getattr(cache, "_hstep_prepared", None)
+    if held is not None and held[0] == key and len(held[1]) == len(tensors) and \
+            all(r() is t for r, t in zip(held[1], tensors)):
+        plan = held[2]
+    else:
+        gc = cache._value_codec_impl
+        try:
+            plan = _hip.prepare_decode_step_grouped_il_hybrid(
+                q, kscale, perm, tensors[4], codec.centroids, codec.n_blocks, codec.n_centroids,
+                cache._key_indices, cache._values_il, cache._value_scales, cache._value_zeros,
+                gc.bits, gc.group_size, cache._key_buffer)
+        except (_hip.SunShapeUnsupported, ValueError):
+            return None
+        cache._hstep_prepared = (key, tuple(weakref.ref(t) for t in tensors), plan)
+    pend = cache._pending
+    k, v, tc, s0, n, nf = cache._take_pending()
+    try:
+        out = plan(q, tc, cache._key_buffer[:, :, s0:], cache._value_buffer[:, :, s0:], n, nf,
+                   k, v, causal, q_offset, out_dtype=out_dtype)
+    except (_hip.SunShapeUnsupported, ValueError):  # raised before any launch
+        cache._pending = pend
+        return None
+    codec.last_score_backend = "hip_fused_mfma_dequant_step"
+    return out
+
+
 def _fused(cache, queries: torch.Tensor, scale: float, causal: bool, q_offset: int,
            out_dtype: torch.dtype):
     """One fused launch over the whole cache, or None when no fused kernel
     applies to this cache / shape (the reference's None-fallback,
     kernels.py:259-291)."""
     if getattr(cache, "_pending", None) is not None and queries.shape[2] <= _hip.MAX_STEP_TOKENS:
-        out = _fused_step(cache, queries, scale, causal, q_offset, out_dtype)
+        if isinstance(cache, HybridSunShapeKVCache):
+            out = _fused_hybrid_step(cache, queries, scale, causal, q_offset, out_dtype)
+        else:
+            out = _fused_step(cache, queries, scale, causal, q_offset, out_dtype)
         if out is not None:
             return out
     ops = cache.fused_operands()  # (stores held tokens first)

@@ -427,6 +427,13 @@ class HybridSunShapeKVCache:
         self._key_buffer: torch.Tensor | None = None
         self._value_buffer: torch.Tensor | None = None
         self._step_plan = None
+        # With lazy_fetch, a decode step of a 2-bit grouped-value cache (a
+        # few fp16 tokens) is held back (its tensors, not copies) and done by
+        # the next attention call in its own launch (ss_decode_step_grouped_il_hybrid:
+        # flush, store and attention); anything that reads the storage first
+        # does it with flush().  The counters already include the step.
+        self.fuse_steps = True
+        self._pending = None  # (keys, values, _version counters, t_c, buf start, n_buf, n_flush)
         self._key_indices: torch.Tensor | None = None
         self._values_packed: torch.Tensor | None = None
         self._value_scales: torch.Tensor | None = None
@@ -635,6 +642,48 @@ class HybridSunShapeKVCache:
         self._step_plan = (key, args)
         return args
 
+    def _held_step_ok(self, k: torch.Tensor, v: torch.Tensor, t_: int, n_flush: int) -> bool:
+        """Whether update_and_fetch may hold this step for the fused
+        attention launch: 1..4 fp16 tokens of a 2-bit grouped-value fp16
+        cache with compressed tokens, at most 4 of them flushed."""
+        return (self.fuse_steps and self.lazy_fetch and self.value_bits == 2 and
+                self.dtype == torch.float16 and self._compressed_offset > 0 and
+                1 <= t_ <= _hip.MAX_STEP_TOKENS and n_flush <= _hip.MAX_STEP_TOKENS and
+                k.dtype == torch.float16 and v.dtype == torch.float16 and
+                k.stride(-1) == 1 and v.stride(-1) == 1 and
+                k.stride()[:3] == v.stride()[:3] and tuple(v.shape) == tuple(k.shape))
+
+    def _run_grouped_step(self, plan, k, v, tc: int, s0: int, n: int, n_flush: int) -> None:
+        """One ss_hybrid_append_grouped_il launch: the new tokens stored at
+        buffer row s0 + n, the n_flush tokens from row s0 encoded and
+        quantised into compressed positions tc .."""
+        b_, h_, t_, _ = k.shape
+        ks, vs = k.stride(), v.stride()
+        rc = plan["fn"](k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype), b_, h_, t_,
+                        ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], *plan["buf"], s0 + n,
+                        s0, n_flush, *plan["codec"], tc, _hip.stream_handle(k.device))
+        _hip._launched("sunshape_block_vq_quantize_hip", rc)
+
+    def _take_pending(self):
+        """The held step's (keys, values, t_c, buffer start, n_buf, n_flush)
+        as it was received, cleared; raises if a tensor was modified in place
+        since update_and_fetch received it."""
+        k, v, kv_, vv_, tc, s0, n, nf = self._pending
+        self._pending = None
+        if k._version != kv_ or v._version != vv_:
+            raise RuntimeError("keys/values passed to update_and_fetch were modified in place "
+                               "before the cache stored them; pass fresh tensors, or set "
+                               "cache.fuse_steps = False")
+        return k, v, tc, s0, n, nf
+
+    def flush(self) -> None:
+        """Do a held decode step's flush and buffer store now (one
+        ss_hybrid_append_grouped_il launch)."""
+        if self._pending is None:
+            return
+        k, v, tc, s0, n, nf = self._take_pending()
+        self._run_grouped_step(self._grouped_step_plan(), k, v, tc, s0, n, nf)
+
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         """Append to the buffer; flush the overflow beyond ``buffer_size``
         (reference cache.py:656-710).  A decode step of a grouped-value cache
@@ -646,23 +695,24 @@ class HybridSunShapeKVCache:
         assert h_ == self.n_kv_heads
         assert d == self.head_dim
         _hip.require_gpu(keys, values)
+        self.flush()
         dev = keys.device
         self._ensure_buffer(b_, t_, dev)
         n_flush = max(0, self._buffer_offset + t_ - self.buffer_size)
         plan = None
-        if self._grouped_il and 0 < n_flush <= self._buffer_offset and t_ <= 64:
+        if self._grouped_il and 0 <= n_flush <= self._buffer_offset and t_ <= 64 and \
+                (n_flush > 0 or self._held_step_ok(keys, values, t_, n_flush)):
             self._grow_compressed(b_, self._compressed_offset + n_flush, dev)
             plan = self._grouped_step_plan()
         k = keys if keys.stride(-1) == 1 else keys.contiguous()
         v = values if values.stride(-1) == 1 else values.contiguous()
         if plan is not None and k.dtype == v.dtype:
-            s0, n = self._buf_start, self._buffer_offset
-            ks, vs = k.stride(), v.stride()
-            rc = plan["fn"](k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype), b_, h_, t_,
-                            ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], *plan["buf"], s0 + n,
-                            s0, n_flush, *plan["codec"], self._compressed_offset,
-                            _hip.stream_handle(dev))
-            _hip._launched("sunshape_block_vq_quantize_hip", rc)
+            s0, n, tc = self._buf_start, self._buffer_offset, self._compressed_offset
+            if self._held_step_ok(k, v, t_, n_flush):
+                # held for the next attention call's fused step
+                self._pending = (k, v, k._version, v._version, tc, s0, n, n_flush)
+            else:
+                self._run_grouped_step(plan, k, v, tc, s0, n, n_flush)
             self._compressed_offset += n_flush
             self._buffer_offset += t_ - n_flush
             self._buf_start = s0 + n_flush if self._buffer_offset else 0
@@ -685,6 +735,7 @@ class HybridSunShapeKVCache:
 
     @property
     def keys(self) -> torch.Tensor:
+        self.flush()
         parts = []
         if self._compressed_offset > 0 and self._key_indices is not None:
             k = _dequantize_keys(self.codec, self._key_indices[:, :, :self._compressed_offset])
@@ -729,6 +780,7 @@ class HybridSunShapeKVCache:
 
     @property
     def values(self) -> torch.Tensor:
+        self.flush()
         parts = []
         cv = self._compressed_values()
         if cv is not None:
@@ -741,12 +793,14 @@ class HybridSunShapeKVCache:
 
     @property
     def key_indices(self) -> torch.Tensor:
+        self.flush()
         if self._key_indices is None or self._compressed_offset == 0:
             return self._zeros(self.n_blocks, torch.uint8)
         return self._key_indices[:, :, :self._compressed_offset]
 
     @property
     def buffer_keys(self) -> torch.Tensor:
+        self.flush()
         if self._key_buffer is None or self._buffer_offset == 0:
             return self._zeros(self.head_dim, self.dtype)
         s0 = self._buf_start
@@ -754,6 +808,7 @@ class HybridSunShapeKVCache:
 
     @property
     def buffer_values(self) -> torch.Tensor:
+        self.flush()
         if self._value_buffer is None or self._buffer_offset == 0:
             return self._zeros(self.head_dim, self.dtype)
         s0 = self._buf_start
@@ -777,6 +832,7 @@ class HybridSunShapeKVCache:
         """Grouped codes of the compressed tokens as reference packed rows
         (B, H, T, packed_dim) uint32 (converted from the interleaved words
         when the cache holds those)."""
+        self.flush()
         if self.value_backend != "grouped" or self._compressed_offset == 0:
             return None
         if self._values_il is not None:
@@ -788,6 +844,7 @@ class HybridSunShapeKVCache:
 
     @property
     def value_scales_raw(self):
+        self.flush()
         if self.value_backend != "grouped" or self._value_scales is None \
                 or self._compressed_offset == 0:
             return None
@@ -795,6 +852,7 @@ class HybridSunShapeKVCache:
 
     @property
     def value_zeros_raw(self):
+        self.flush()
         if self.value_backend != "grouped" or self._value_zeros is None \
                 or self._compressed_offset == 0:
             return None
@@ -806,6 +864,7 @@ class HybridSunShapeKVCache:
         ...});
         None when there is nothing compressed or the value backend has no
         fused kernel."""
+        self.flush()
         if self._key_indices is None or self._compressed_offset == 0:
             return None
         # fp16 heavy-block key dims of a mixed-precision codec, scored exactly
@@ -875,6 +934,7 @@ class HybridSunShapeKVCache:
         None for SunShape-coded values (an fp16 copy of each value codeword
         would move every token that uses it the same way) and for fp16 heavy
         blocks."""
+        self.flush()
         if self.value_backend == "sunshape" or self._heavy_dims is not None or \
                 self._key_buffer is None:
             return None
@@ -951,6 +1011,7 @@ class HybridSunShapeKVCache:
 
     def trim(self, n: int) -> None:
         """Trim the buffer first, then compressed storage (cache.py:954-963)."""
+        self.flush()
         if n <= 0:
             return
         b = min(n, self._buffer_offset)
@@ -977,6 +1038,7 @@ class HybridSunShapeKVCache:
 
     @property
     def state(self):
+        self.flush()
         parts = []
         if self._key_indices is not None and self._compressed_offset > 0:
             parts.append(self._key_indices[:, :, :self._compressed_offset])

@@ -945,6 +945,12 @@ template <class VF, class = void>
 struct StepShareOf : std::false_type {};
 template <class VF>
 struct StepShareOf<VF, std::void_t<decltype(VF::kStepShare)>> : std::bool_constant<VF::kStepShare> {};
+// Step formats whose step also attends a share of exact buffered tokens
+// (VGilStep): the encoded tokens are the ones the buffer flushes.
+template <class VF, class = void>
+struct HybridStepOf : std::false_type {};
+template <class VF>
+struct HybridStepOf<VF, std::void_t<decltype(VF::kHybridStep)>> : std::bool_constant<VF::kHybridStep> {};
 
 template <int D, int NC, class VF>
 struct WsCfg {
@@ -972,7 +978,8 @@ struct WsCfg {
     static constexpr int kShareFree = kLdsMax - (kLut + kPst + kFlags + kBufPart + kStepLds) -
                                       NC * 2 * kSlot;  // beside a private ring of 2 slots a wave
     static constexpr int kShareFit = kShareFree > 0 ? kShareFree / (4 * D) / 8 * 8 : 0;
-    static constexpr int kShareLdsTok = (VF::kHybridBuffer && !StepShareOf<VF>::value &&
+    static constexpr int kShareLdsTok = (VF::kHybridBuffer &&
+                                         (!StepShareOf<VF>::value || HybridStepOf<VF>::value) &&
                                          VF::kPrivateRing) ? (kShareFit < 32 ? kShareFit : 32) : 0;
     static constexpr int kShareLds = kShareLdsTok * D * 2 * 2;
     static constexpr int kRing = kLut + kPst + kFlags + kBufPart + kStepLds + kShareLds;
@@ -1189,6 +1196,18 @@ constexpr int kMaxStepTokens = 4;  // new tokens of one fused decode step (A row
 // cache tokens the last split of a fused step hands to the other splits
 // (about the time of its encode and share)
 constexpr int64_t kStepShareTokens = 192;
+// the same for a hybrid cache's fused step (VGilStep): its last split also
+// waits, before its LUT barrier, for the flushed tokens' rows, cold in HBM
+// (about 5 us at B=8, T=32K); measured there, the step took 43.6 / 42.4 /
+// 41.1 / 40.2 us with 192 / 512 / 1024 / 1536 tokens handed over, and no
+// less with more
+constexpr int64_t kHybridStepShareTokens = 1536;
+// Register-unit splits: rounds of units that wave 0 hands to the other waves
+// when it first attends a share of buffered tokens (its copy waits behind
+// the start-up traffic), and the rounds added when it also scores a hybrid
+// step's flushed tokens
+constexpr int kShareSkipRounds = 6;
+constexpr int kStepSkipRounds = 3;
 
 
 // Round two floats to bf16 (nearest even), packed: a in bits 0-15, b in 16-31.
@@ -1523,6 +1542,86 @@ struct VGil {
     }
 };
 
+// VGil for one decode step of a hybrid cache (float16 buffer) that also moves
+// its tokens: the cache holds t_kv compressed tokens and a buffer window of
+// n_flush + n_rem tokens (rows 0 .. at kbuf / vbuf, [b*buf_sb + h*buf_sh +
+// row*buf_st + dim]); the step's n_new tokens arrive at knew / vnew.  The
+// reference appends them to the buffer and flushes its n_flush oldest tokens
+// into compressed storage (cache.py:656-710), then attends everything
+// (attention.py:307-350).  Here one launch does both: the last split encodes
+// the flushed keys (the step encode of VIl8Step), quantises their values with
+// the grouped min/max rule and attends them in that compressed form at
+// positions t_kv .., while every split attends its share of the t_buf =
+// n_rem + n_new exact tokens (the buffer rows n_flush .., then the new
+// tokens) after them; the last split of row group 0 of each (batch, KV head)
+// stores the flushed tokens' index rows, codes, scales and zeros at
+// positions t_kv .. and the new tokens at buffer rows n_flush + n_rem ..
+template <int D, int BITS, int NG, class SZT>
+struct VGilStep : VGil<D, BITS, NG, SZT> {
+    struct Args : VGil<D, BITS, NG, SZT>::Args {
+        const void *knew, *vnew;  // float16 [b*new_sb + h*new_sh + j*new_st + dim]
+        int64_t new_sb, new_sh, new_st, n_rem, n_flush;
+        const float *centroids;  // [n_blocks][n_centroids][8] float32
+        const float *cb_norms;   // |C|^2 per prepared codebook lane (ss_codebook_f16x2)
+        uint8_t *idx_out;        // the index cache the kernel reads (c.idx)
+        uint32_t *codes_out;     // the code words (codes)
+        SZT *scales_out, *zeros_out;
+        void *kput, *vput;       // the buffer stores at the window (kbuf / vbuf)
+    };
+    static constexpr bool kStepShare = true;
+    static constexpr bool kHybridStep = true;
+    static constexpr bool kHeavyCapable = false;
+    static constexpr int kBits = BITS;
+    static constexpr int kNG = NG;
+    using SzT = SZT;
+};
+
+// The grouped min/max quantisation of one token's values (reference
+// kernels.py:1173-1228: scale = (max - min) / (2^bits - 1), at least 1e-8;
+// code = clamp(round((x - min) / scale)), the same IEEE steps as
+// values.hip's quantize_grouped_kernel), the wave holding dims lane + 64k:
+// codes q[k], and the scale and zero of dim lane + 64k's group.
+template <int D, int BITS, int NG>
+__device__ __forceinline__ void quantize_token_wave(const float (&x)[D / kWave], float (&q)[D / kWave],
+                                                    float (&sc)[D / kWave], float (&mn)[D / kWave]) {
+    constexpr int DL = D / kWave;
+    constexpr int G = D / NG;                  // group size: 32, 64 or 128
+    constexpr int SPAN = G < kWave ? G : kWave;  // lanes of one group per k
+    constexpr float maxv = (float)((1 << BITS) - 1);
+    float lo[DL], hi[DL];
+#pragma unroll
+    for (int k = 0; k < DL; ++k) lo[k] = hi[k] = x[k];
+    if constexpr (G > kWave) {  // one group spans every k (G = 128 = D)
+        float a = lo[0], b = hi[0];
+#pragma unroll
+        for (int k = 1; k < DL; ++k) {
+            a = fminf(a, lo[k]);
+            b = fmaxf(b, hi[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < DL; ++k) {
+            lo[k] = a;
+            hi[k] = b;
+        }
+    }
+#pragma unroll
+    for (int o = SPAN / 2; o > 0; o >>= 1)
+#pragma unroll
+        for (int k = 0; k < DL; ++k) {
+            lo[k] = fminf(lo[k], __shfl_xor(lo[k], o));
+            hi[k] = fmaxf(hi[k], __shfl_xor(hi[k], o));
+        }
+#pragma unroll
+    for (int k = 0; k < DL; ++k) {
+        float s = __fdiv_rn(__fsub_rn(hi[k], lo[k]), maxv);
+        if (s < 1e-8f) s = 1e-8f;
+        const float qf = rintf(__fdiv_rn(__fsub_rn(x[k], lo[k]), s));
+        q[k] = fminf(fmaxf(qf, 0.f), maxv);
+        sc[k] = s;
+        mn[k] = lo[k];
+    }
+}
+
 // TurboQuant 2-bit values (reference value_codecs.py:136-177) on the matrix
 // cores: per token a norm and 2-bit codes of the rotated unit vector, held
 // token-interleaved as VGil's words ([cap/16][D] per (b, h)); norms [cap].
@@ -1806,12 +1905,22 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // this split's share of the token buffer (wave-uniform)
     int64_t t_buf = 0;
     if constexpr (VF::kHybridBuffer) t_buf = va.t_buf;
-    constexpr bool kStep = StepShareOf<VF>::value;
-    // (a fused step's new tokens all go to the last split)
-    const int64_t bshare = kStep ? t_buf : (t_buf + c.n_splits - 1) / c.n_splits;
-    const int64_t bj0 = kStep ? 0 : min((int64_t)split * bshare, t_buf);
-    const int64_t bj1 = kStep ? (split == c.n_splits - 1 ? t_buf : 0) : min(bj0 + bshare, t_buf);
-    const bool has_buf = VF::kHybridBuffer && bj1 > bj0;
+    constexpr bool kStep = StepShareOf<VF>::value;     // a fused step encodes tokens
+    constexpr bool kHStep = HybridStepOf<VF>::value;   // ... beside a share of exact tokens
+    constexpr bool kStepOnly = kStep && !kHStep;       // ... that are its whole share
+    // (a fused step's new tokens all go to the last split; a hybrid step's
+    // exact tokens are shared out as a hybrid cache's buffer)
+    const int64_t bshare = kStepOnly ? t_buf : (t_buf + c.n_splits - 1) / c.n_splits;
+    const int64_t bj0 = kStepOnly ? 0 : min((int64_t)split * bshare, t_buf);
+    const int64_t bj1 = kStepOnly ? (split == c.n_splits - 1 ? t_buf : 0) : min(bj0 + bshare, t_buf);
+    // tokens the split encodes (and scores from the LUT): a step's new
+    // tokens, or a hybrid step's flushed ones, all in the last split
+    int n_step = 0;
+    if constexpr (kStepOnly) n_step = (int)bj1;
+    if constexpr (kHStep) n_step = split == c.n_splits - 1 ? (int)va.n_flush : 0;
+    // the split's share of exact (buffered or new) tokens
+    const bool has_ex = VF::kHybridBuffer && !kStepOnly && bj1 > bj0;
+    const bool has_buf = VF::kHybridBuffer && (bj1 > bj0 || n_step > 0);
 
     // Barrier that orders LDS only: a wave's outstanding global loads (the
     // loader's tile copies) do not have to land first, which __syncthreads'
@@ -1902,6 +2011,26 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         }
     };
     RegUnit ua, ub;
+    // Wave w takes units w, w + NC, ... of the split.  Where wave 0 first
+    // attends the split's share of buffered tokens (and, in a hybrid step,
+    // scores the flushed tokens), it skips its first share_skip units, which
+    // waves 1, 2, ... take after their own: a fixed schedule (the sums, and so
+    // the results, never depend on timing) that evens out the waves' ends.
+    int share_skip = 0;
+    if constexpr (kRegs && VF::kHybridBuffer) {
+        if (has_ex) share_skip += kShareSkipRounds;
+        if (n_step > 0) share_skip += kStepSkipRounds;
+    }
+    const int n_own = wv < n_units ? (n_units - wv + NC - 1) / NC : 0;
+    auto unit_of = [&](int i) -> int {  // this wave's i-th unit (n_units: none)
+        if (wv == 0) {
+            const int u = (i + share_skip) * NC;
+            return u < n_units ? u : n_units;
+        }
+        if (i < n_own) return wv + i * NC;
+        const int j = (wv - 1) + (i - n_own) * (NC - 1);  // wave 0's skipped unit j * NC
+        return (j < share_skip && j * NC < n_units) ? j * NC : n_units;
+    };
 
     // Prologue.  The compute waves' small loads (query element, permutation
     // entry, codebook entries) are issued before the loader's first tiles, so
@@ -1913,7 +2042,10 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     constexpr int CT = NC * kWave;             // compute threads
     constexpr int QE = (R * D + CT - 1) / CT;  // query elements per compute thread
     if (tid < K::kFlagWords * (1 + K::kSub)) ready[tid] = -1;  // ready[] and done[][]
-    if (tid == 0) *cbar = 0;
+    if (tid == 0) {
+        cbar[0] = 0;
+        cbar[2] = 0;   // hybrid step: block groups whose flushed tokens' indices are decided
+    }
     int64_t lim[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -1957,7 +2089,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     // A hybrid cache's share of at most kShareRegs 16-bit buffered tokens
     // (wave 0): their key and value dims lane + 64k, loaded in the prologue
     // too (the heavy-dim kernels have no registers to spare)
-    constexpr bool kShPre = VF::kHybridBuffer && !kStep && !HV;
+    constexpr bool kShPre = VF::kHybridBuffer && !kStepOnly && !HV;
     constexpr int kShareRegs = 8;
     constexpr int NSH = kShPre ? kShareRegs : 1;
     constexpr int DLh = kShPre ? D / kWave : 1;
@@ -1966,9 +2098,26 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
     bool sh_pre = false, sh_lds = false;
     if constexpr (kShPre) {
         const bool b16 = va.buf_dtype == SS_F16 || va.buf_dtype == SS_BF16;
-        sh_pre = has_buf && wv == 0 && n_sh <= kShareRegs && b16;
-        sh_lds = has_buf && n_sh > kShareRegs && n_sh <= K::kShareLdsTok && b16;
+        sh_pre = has_ex && wv == 0 && n_sh <= kShareRegs && b16;
+        sh_lds = has_ex && n_sh > kShareRegs && n_sh <= K::kShareLdsTok && b16;
     }
+    // Exact token j of the share (its key or value row): buffer row j; in a
+    // hybrid step buffer row n_flush + j for the n_rem buffered tokens that
+    // stay, then the step's new tokens (float16, checked on the host).  Its
+    // position is ex_pos0 + j.
+    auto ex_row = [&](const auto &bv, bool is_v, int64_t j) -> const char * {
+        if constexpr (kHStep) {
+            if (j >= bv.n_rem)
+                return static_cast<const char *>(is_v ? bv.vnew : bv.knew) +
+                       (bb * bv.new_sb + kvh * bv.new_sh + (j - bv.n_rem) * bv.new_st) * 2;
+            j += bv.n_flush;
+        }
+        const int64_t es = bv.buf_dtype == SS_F32 ? 4 : 2;
+        return static_cast<const char *>(is_v ? bv.vbuf : bv.kbuf) +
+               (bb * bv.buf_sb + kvh * bv.buf_sh + j * bv.buf_st) * es;
+    };
+    int64_t ex_pos0 = c.t_kv;
+    if constexpr (kHStep) ex_pos0 += va.n_flush;
     // the LDS copy of the share: keys [kShareLdsTok][D], then values
     const unsigned short *sh_k = reinterpret_cast<const unsigned short *>(
         smem + K::kLut + K::kPst + K::kFlags + K::kBufPart + K::kStepLds);
@@ -1986,6 +2135,13 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         const float *bq = bpart + 2 * R;  // [R][D] query copy
         f32x4 *pb = reinterpret_cast<f32x4 *>(pst);  // wave 0's P staging: p of 64 tokens
         const int64_t head = bb * bv.buf_sb + kvh * bv.buf_sh;
+        // key / value row of exact-share token j (the buffer's own rows,
+        // indexed directly, outside a hybrid step)
+        auto krow_of = [&](int64_t j) -> const char * {
+            if constexpr (kHStep) return ex_row(bv, false, j);
+            return static_cast<const char *>(bv.kbuf) +
+                   (head + j * bv.buf_st) * (bv.buf_dtype == SS_F32 ? 4 : 2);
+        };
         if constexpr (kShPre) {
             if (sh_pre || sh_lds) {
                 // the prefetched share (registers, or the LDS copy), eight
@@ -2028,7 +2184,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                             for (int k = 0; k < DLh; ++k) part[r] = fmaf(qv[r][k], f32(kc[j][k]), part[r]);
                         }
                         wave_sum4_dpp(part, sc[j]);
-                        const int64_t pos = c.t_kv + bj0 + c0 + j;
+                        const int64_t pos = ex_pos0 + bj0 + c0 + j;
 #pragma unroll
                         for (int r = 0; r < R; ++r)
                             sc[j][r] = (c0 + j < n_sh && pos <= lim[r]) ? sc[j][r] * kLog2e : -INFINITY;
@@ -2059,9 +2215,8 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         for (int64_t j0 = (sh_pre || sh_lds) ? bj1 : bj0; j0 < bj1; j0 += kWave) {
             const int64_t j = j0 + lane;
             const bool ok = j < bj1;
-            const int64_t ko = head + (ok ? j : j0) * bv.buf_st;
             float sc[R] = {};
-            if constexpr (kStep) {
+            if constexpr (kStepOnly) {
                 // a new token: its encoded index row (LDS) scored from the
                 // LUT, already in log2 units
                 const lds_t<uint8_t> *row = to_lds<uint8_t>(step_idx) + (ok ? j : j0) * NB;
@@ -2071,15 +2226,16 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 #pragma unroll
                 for (int r = 0; r < R; ++r) sc[r] = e[r];
             } else {
+                const char *krow = krow_of(ok ? j : j0);
                 for (int d0 = 0; d0 < D; d0 += 8) {
                     float kx[8];
                     if (bv.buf_dtype == SS_F16) {
                         unpack16<__half>(*reinterpret_cast<const uint4 *>(
-                                             static_cast<const __half *>(bv.kbuf) + ko + d0),
+                                             reinterpret_cast<const __half *>(krow) + d0),
                                          kx);
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 8; ++i) kx[i] = load_as_f32(bv.kbuf, bv.buf_dtype, ko + d0 + i);
+                        for (int i = 0; i < 8; ++i) kx[i] = load_as_f32(krow, bv.buf_dtype, d0 + i);
                     }
 #pragma unroll
                     for (int r = 0; r < R; ++r)
@@ -2089,7 +2245,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
 #pragma unroll
                 for (int r = 0; r < R; ++r) sc[r] *= kLog2e;
             }
-            const int64_t pos = c.t_kv + j;
+            const int64_t pos = (kStepOnly ? c.t_kv : ex_pos0) + j;
 #pragma unroll
             for (int r = 0; r < R; ++r) sc[r] = (ok && pos <= lim[r]) ? sc[r] : -INFINITY;
             float tmax[R], p[R], corr[R];
@@ -2122,9 +2278,11 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     float vv[8][DL];
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
-                        const int64_t vo = head + (j0 + min(jb + u, nj - 1)) * bv.buf_st + lane;
+                        const int64_t jt = j0 + min(jb + u, nj - 1);
+                        const T *vr = vb + head + jt * bv.buf_st;
+                        if constexpr (kHStep) vr = reinterpret_cast<const T *>(ex_row(bv, true, jt));
 #pragma unroll
-                        for (int k = 0; k < DL; ++k) vv[u][k] = to_f32(vb[vo + k * kWave]);
+                        for (int k = 0; k < DL; ++k) vv[u][k] = to_f32(vr[lane + k * kWave]);
                     }
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
@@ -2138,7 +2296,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     }
                 }
             };
-            if constexpr (kStep) {
+            if constexpr (kStepOnly) {
                 // a fused step's values, prefetched into registers
 #pragma unroll
                 for (int u = 0; u < kMaxStepTokens; ++u) {
@@ -2157,6 +2315,62 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
             else
                 pv(float{});
             wave_lds_sync();
+        }
+        if constexpr (kHStep) {
+            if (n_step > 0) {
+                // a hybrid step's flushed tokens in their compressed form, at
+                // positions t_kv ..: scores from the LUT by their new index
+                // rows (log2 units), values code * scale + zero with the
+                // scale and zero rounded to their stored type.  Their index
+                // rows are complete once every block group's leader has
+                // signalled (bounded wait).
+                int spins = 0;
+                while (cbar[2] < NB / 4) {
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins > c.spin_limit) {
+                        wait_gave_up(kWaitBarrier);
+                        break;
+                    }
+                }
+                asm volatile("" ::: "memory");
+                using SZT = typename VF::SzT;
+                float sc[NS][R], vh[NS][DL];
+#pragma unroll
+                for (int j = 0; j < NS; ++j) {
+                    const lds_t<uint8_t> *row = to_lds<uint8_t>(step_idx) + min(j, n_step - 1) * NB;
+                    f32x4 e = lut_l[row[0]];
+#pragma unroll
+                    for (int b = 1; b < NB; ++b) e += lut_l[b * kLutStride + row[b]];
+                    const int64_t pos = c.t_kv + j;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) sc[j][r] = (j < n_step && pos <= lim[r]) ? e[r] : -INFINITY;
+                    float qc[DL], qs[DL], qz[DL];
+                    quantize_token_wave<D, VF::kBits, VF::kNG>(vpre[j], qc, qs, qz);
+#pragma unroll
+                    for (int k = 0; k < DL; ++k)
+                        vh[j][k] = fmaf(qc[k], (float)(SZT)qs[k], (float)(SZT)qz[k]);
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float mx = sc[0][r];
+#pragma unroll
+                    for (int j = 1; j < NS; ++j) mx = fmaxf(mx, sc[j][r]);
+                    if (mx == -INFINITY) continue;  // none visible to this row
+                    const float mn = fmaxf(bm[r], mx);
+                    const float corr = fast_exp2(bm[r] - mn);
+                    bm[r] = mn;
+                    bl[r] *= corr;
+#pragma unroll
+                    for (int k = 0; k < DL; ++k) ba[r][k] *= corr;
+#pragma unroll
+                    for (int j = 0; j < NS; ++j) {
+                        const float pj = fast_exp2(sc[j][r] - mn);
+                        bl[r] += pj;
+#pragma unroll
+                        for (int k = 0; k < DL; ++k) ba[r][k] = fmaf(pj, vh[j][k], ba[r][k]);
+                    }
+                }
+            }
         }
         // the query copy is no longer read: the partial takes its place
         if (lane == 0) {
@@ -2257,6 +2471,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     const int row = min(ci / CPR, n_sh - 1), chunk = ci % CPR;
                     const char *src = static_cast<const char *>(is_v ? va.vbuf : va.kbuf) +
                                       ((head + (bj0 + row) * va.buf_st) * 2 + chunk * 16);
+                    if constexpr (kHStep) src = ex_row(va, is_v, bj0 + row) + chunk * 16;
                     const uint32_t dst = lds0 + (uint32_t)((is_v ? K::kShareLdsTok * D * 2 : 0) +
                                                            (is_v ? i - n_copies : i) * 1024);
                     __builtin_amdgcn_global_load_lds(src, reinterpret_cast<lds_t<void> *>(dst), 16, 0, 0);
@@ -2269,32 +2484,59 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 const unsigned short *vb = static_cast<const unsigned short *>(va.vbuf);
                 const int64_t head = bb * va.buf_sb + kvh * va.buf_sh;
 #pragma unroll
-                for (int j = 0; j < NSH; ++j)
+                for (int j = 0; j < NSH; ++j) {
+                    const int64_t jt = bj0 + min(j, n_sh - 1);
+                    const unsigned short *kr = kb + head + jt * va.buf_st;
+                    const unsigned short *vr = vb + head + jt * va.buf_st;
+                    if constexpr (kHStep) {
+                        kr = reinterpret_cast<const unsigned short *>(ex_row(va, false, jt));
+                        vr = reinterpret_cast<const unsigned short *>(ex_row(va, true, jt));
+                    }
 #pragma unroll
                     for (int k = 0; k < DLh; ++k) {
-                        const int64_t o = head + (bj0 + min(j, n_sh - 1)) * va.buf_st + lane + kWave * k;
-                        hk_raw[j][k] = kb[o];
-                        hv_raw[j][k] = vb[o];
+                        hk_raw[j][k] = kr[lane + kWave * k];
+                        hv_raw[j][k] = vr[lane + kWave * k];
                     }
+                }
             }
-        }
-        if constexpr (kRegs) {
-            // this wave's first unit streams into registers while the LUT is built
-            if (wv < n_units) load_ru(ua, wv);
-        } else if constexpr (K::kPriv) {
-            // this wave's first units (u = wv + k*NC) stream in while the LUT is built
-            for (; nq < K::kPrivSlots && wv + nq * NC < n_units; ++nq)
-                issue_at(wv + nq * NC, ring_l + priv_slot(nq));
         }
         // A fused step's last split: the new tokens' key and value rows
         // (lane: dims lane + 64k), the permutation entries of the key dims
         // its A lanes hold and its centroids' norms load here, before the
         // loader streams anything, so none of them waits behind its tiles
-        const int n_step = kStep && has_buf ? (int)bj1 : 0;
+        // (a hybrid step: the flushed tokens' rows, the code words their
+        // codes go into, and the new tokens that go into the buffer)
         int pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         float nrm[kStep ? LT : 1];
+        using PutT = std::conditional_t<D == 128, uint32_t, unsigned short>;  // a lane's dims of a row
+        static_assert(D == 128 || D == 64, "head_dim");
+        PutT kput_r[kHStep ? NS : 1], vput_r[kHStep ? NS : 1];
+        uint32_t cw_pre[2][DLs];
+        const bool put_wave = kHStep && split == c.n_splits - 1 && rg == 0 && wv == NC - 1;
+        const bool code_wave = kHStep && n_step > 0 && rg == 0 && wv == (NC > 1 ? 1 : 0);
+        if constexpr (kHStep) {
+            if (put_wave) {
+                const int n_new = (int)(va.t_buf - va.n_rem);  // >= 1 (checked on the host)
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    const int ii = min(i, n_new - 1);
+                    kput_r[i] = reinterpret_cast<const PutT *>(ex_row(va, false, va.n_rem + ii))[lane];
+                    vput_r[i] = reinterpret_cast<const PutT *>(ex_row(va, true, va.n_rem + ii))[lane];
+                }
+            }
+            if (code_wave) {
+                constexpr int TPW = 32 / VF::kBits;
+                const int64_t w0 = c.t_kv / TPW, wmax = c.cap / TPW - 1;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                    for (int k = 0; k < DLs; ++k)
+                        cw_pre[s2][k] = va.codes_out[(bh * (c.cap / TPW) + min(w0 + s2, wmax)) * D +
+                                                     lane + kWave * k];
+            }
+        }
         if constexpr (kStep) {
-            if (has_buf) {
+            if (n_step > 0) {
                 // (float16 tokens, checked on the host: plain 2-byte loads,
                 // all in flight together)
                 const int64_t head = bb * va.buf_sb + kvh * va.buf_sh;
@@ -2331,6 +2573,17 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                 }
             }
         }
+        // (after a step's loads, which the step's encode waits on before the
+        // unit is needed)
+        if constexpr (kRegs) {
+            // this wave's first unit streams into registers while the LUT is built
+            const int u0 = unit_of(0);
+            if (u0 < n_units) load_ru(ua, u0);
+        } else if constexpr (K::kPriv) {
+            // this wave's first units (u = wv + k*NC) stream in while the LUT is built
+            for (; nq < K::kPrivSlots && wv + nq * NC < n_units; ++nq)
+                issue_at(wv + nq * NC, ring_l + priv_slot(nq));
+        }
         lds_barrier();  // small loads issued, flags initialised
         // query elements: round_to(q_dtype, q * scale) (attention.py:208)
 #pragma unroll
@@ -2349,7 +2602,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                         qv = __uint_as_float(h << 16);
                 }
                 qraw[e] = round_to(c.q_dtype, qv * c.scale);
-                if (has_buf && !kStep) bpart[2 * R + e] = qraw[e];
+                if (has_ex) bpart[2 * R + e] = qraw[e];
             }
         }
         compute_barrier(1);  // raw query staged
@@ -2451,7 +2704,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         float kd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         float kkr[4] = {0.f, 0.f, 0.f, 0.f};
         if constexpr (kStep) {
-            if (has_buf) {
+            if (n_step > 0) {
                 // The new tokens' keys encoded from the codebook operands
                 // this wave holds for the LUT (its 4 blocks x 256 centroids):
                 // the key . centroid products on the matrix cores (token r of
@@ -2574,7 +2827,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         }
         compute_barrier(3);  // LUT complete (the query in LDS is read for the last time)
         if constexpr (kStep) {
-            if (has_buf) {
+            if (n_step > 0) {
                 // the first wave of each block group merges the group's
                 // waves' candidates (16 / LT of them) and decides
                 constexpr int WPG = 16 / LT;  // waves per 4-block group
@@ -2600,16 +2853,24 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                                 const float e = fmaf(0x1p-20f * a2, a2, 0x1p-31f * cb_mul * kn);
                                 const int bi = __float_as_int(a[2]);
                                 const bool ok = a[1] - a[0] > 2.f * e && bi != 0x7fffffff;
-                                if (ok) step_idx[r * NB + bg * 4 + g] = (uint8_t)bi;
+                                if (ok) {
+                                    step_idx[r * NB + bg * 4 + g] = (uint8_t)bi;
+                                    if (kHStep && rg == 0)
+                                        va.idx_out[(bh * c.cap + c.t_kv + r) * NB + bg * 4 + g] = (uint8_t)bi;
+                                }
                                 need |= ok ? 0u : (1u << r);
                             }
                         }
                     }
                     // exact ranking for the pairs not cleared (rare): the whole
-                    // wave over the float32 centroids, one pair at a time
-#pragma unroll
+                    // wave over the float32 centroids, one pair at a time (one
+                    // copy of the code, entered only when some pair needs it:
+                    // unrolled, its sixteen inlined copies cost instruction
+                    // fetches on every step)
+                    if (__builtin_amdgcn_ballot_w64(need != 0u) != 0) {
+#pragma unroll 1
                     for (int s2 = 0; s2 < 4; ++s2) {
-#pragma unroll
+#pragma unroll 1
                         for (int r = 0; r < 4; ++r) {
                             const bool any =
                                 __builtin_amdgcn_ballot_w64(g == s2 && ((need >> r) & 1u)) != 0;
@@ -2620,25 +2881,107 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                                 const int b = bg * 4 + s2;
                                 const int bi = exact_block_wave<8>(
                                     kv, va.centroids + (int64_t)b * c.n_centroids * 8, c.n_centroids, lane);
-                                if (lane == 0) step_idx[r * NB + b] = (uint8_t)bi;
+                                if (lane == 0) {
+                                    step_idx[r * NB + b] = (uint8_t)bi;
+                                    if (kHStep && rg == 0)
+                                        va.idx_out[(bh * c.cap + c.t_kv + r) * NB + b] = (uint8_t)bi;
+                                }
                             }
                         }
                     }
+                    }
+                    if constexpr (kHStep) {
+                        // this group's indices are in LDS (and stored): tell
+                        // wave 0, which scores the flushed tokens; the other
+                        // waves go on to their units
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        if (lane == 0)
+                            __hip_atomic_fetch_add(const_cast<lds_t<int> *>(cbar + 2), 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+                    }
                 }
-                compute_barrier(4);  // the new tokens' index rows are complete
-                if (rg == 0) {
+                if constexpr (kStepOnly) compute_barrier(4);  // the new tokens' index rows are complete
+                if (kStepOnly && rg == 0) {
                     // the cache's copy at positions t_kv .. t_kv + n_new - 1:
                     // index rows, then (wave 0's lanes) the fp16 values
                     for (int e = wv * kWave + lane; e < n_step * NB; e += NC * kWave)
                         va.idx_out[(bh * c.cap + c.t_kv + e / NB) * NB + e % NB] = step_idx[e];
-                    if (wv == 0) {
+                    if constexpr (kStepOnly) {
+                        if (wv == 0) {
 #pragma unroll
-                        for (int j = 0; j < NS; ++j)
-                            if (j < n_step)
+                            for (int j = 0; j < NS; ++j)
+                                if (j < n_step)
 #pragma unroll
-                                for (int k = 0; k < DLs; ++k)
-                                    store_value_il8(va.v8_out, bh, c.cap, D, c.t_kv + j, lane + kWave * k,
-                                                    vpre[j][k]);
+                                    for (int k = 0; k < DLs; ++k)
+                                        store_value_il8(va.v8_out, bh, c.cap, D, c.t_kv + j,
+                                                        lane + kWave * k, vpre[j][k]);
+                        }
+                    }
+                }
+                if constexpr (kHStep) {
+                    if (code_wave) {
+                        // the flushed tokens' codes into their words (the
+                        // other tokens' bits kept: token i of a word at bit
+                        // bits*(i/2) + 16*(i%2)), and each group's scale and
+                        // zero from the lane holding its first dim
+                        using SZT = typename VF::SzT;
+                        constexpr int TPW = 32 / VF::kBits;
+                        constexpr uint32_t cmask = (1u << VF::kBits) - 1u;
+                        constexpr int G = D / VF::kNG;
+                        const int64_t w0 = c.t_kv / TPW;
+                        const int64_t cw_head = bh * (c.cap / TPW);
+                        uint32_t wa0[DLs], wa1[DLs];
+#pragma unroll
+                        for (int k = 0; k < DLs; ++k) {
+                            wa0[k] = cw_pre[0][k];
+                            wa1[k] = cw_pre[1][k];
+                        }
+#pragma unroll
+                        for (int j = 0; j < NS; ++j) {
+                            if (j < n_step) {
+                                float qc[DLs], qs[DLs], qz[DLs];
+                                quantize_token_wave<D, VF::kBits, VF::kNG>(vpre[j], qc, qs, qz);
+                                const int64_t t = c.t_kv + j;
+                                const bool second = t / TPW != w0;
+                                const int i = (int)(t % TPW);
+                                const int pos = VF::kBits * (i >> 1) + 16 * (i & 1);
+#pragma unroll
+                                for (int k = 0; k < DLs; ++k) {
+                                    const uint32_t cv = ((uint32_t)qc[k] & cmask) << pos;
+                                    if (second)
+                                        wa1[k] = (wa1[k] & ~(cmask << pos)) | cv;
+                                    else
+                                        wa0[k] = (wa0[k] & ~(cmask << pos)) | cv;
+                                    const int d = lane + kWave * k;
+                                    if (d % G == 0) {
+                                        const int64_t srow = (bh * c.cap + t) * VF::kNG + d / G;
+                                        va.scales_out[srow] = (SZT)qs[k];
+                                        va.zeros_out[srow] = (SZT)qz[k];
+                                    }
+                                }
+                            }
+                        }
+                        const bool two = (c.t_kv + n_step - 1) / TPW != w0;
+#pragma unroll
+                        for (int k = 0; k < DLs; ++k) {
+                            va.codes_out[(cw_head + w0) * D + lane + kWave * k] = wa0[k];
+                            if (two) va.codes_out[(cw_head + w0 + 1) * D + lane + kWave * k] = wa1[k];
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (kHStep) {
+            if (put_wave) {
+                // the step's new tokens into the buffer rows after the window
+                const int n_new = (int)(va.t_buf - va.n_rem);
+                const int64_t row0 = va.n_flush + va.n_rem;
+#pragma unroll
+                for (int i = 0; i < NS; ++i) {
+                    if (i < n_new) {
+                        const int64_t o = (bb * va.buf_sb + kvh * va.buf_sh + (row0 + i) * va.buf_st) * 2;
+                        reinterpret_cast<PutT *>(static_cast<char *>(va.kput) + o)[lane] = kput_r[i];
+                        reinterpret_cast<PutT *>(static_cast<char *>(va.vput) + o)[lane] = vput_r[i];
                     }
                 }
             }
@@ -2738,20 +3081,23 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
         if constexpr (kRegs) {
             // two register sets in turn (past the last unit the loads repeat
             // the last one, so the loop stays straight-line)
-            for (int u = wv; u < n_units; u += 2 * NC) {
-                load_ru(ub, min(u + NC, n_units - 1));
+            for (int i = 0, u = unit_of(0); u < n_units;) {
+                const int u1 = unit_of(++i);
+                load_ru(ub, min(u1, n_units - 1));
                 {
                     typename VF::Tile tv;
                     VF::from_raw(tv, ua.raw, lane);
                     step(ua.ir, tv, ua.khv, u);
                 }
-                if (u + NC >= n_units) break;
-                load_ru(ua, min(u + 2 * NC, n_units - 1));
+                if (u1 >= n_units) break;
+                const int u2 = unit_of(++i);
+                load_ru(ua, min(u2, n_units - 1));
                 {
                     typename VF::Tile tv;
                     VF::from_raw(tv, ub.raw, lane);
-                    step(ub.ir, tv, ub.khv, u + NC);
+                    step(ub.ir, tv, ub.khv, u1);
                 }
+                u = u2;
             }
         } else {
         for (int u = wv, uk = 0; u < n_units; u += NC, ++uk) {
@@ -5062,6 +5408,117 @@ extern "C" int ss_decode_attn_grouped_il_hybrid(
                            bits, group_size, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
                            workspace_bytes, n_splits, k_buf, v_buf, buf_dtype, buf_sb, buf_sh,
                            buf_st, t_buf, stream, k_heavy, heavy_dims, n_heavy_dims);
+}
+
+extern "C" int ss_decode_step_grouped_il_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, uint32_t *codes_il, void *scales, void *zeros,
+    int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv, void *k_buf, void *v_buf,
+    int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t n_buf, int64_t n_flush,
+    const void *k_new, const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+    int64_t n_new, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream) {
+    SS_UNSUPPORTED(n_new >= 1 && n_new <= kMaxStepTokens, "a fused step takes 1..%d new tokens",
+                   kMaxStepTokens);
+    SS_UNSUPPORTED(n_flush >= 0 && n_flush <= kMaxStepTokens,
+                   "a fused hybrid step flushes 0..%d tokens (got %lld)", kMaxStepTokens,
+                   (long long)n_flush);
+    SS_REQUIRE(n_buf >= n_flush, "n_flush %lld exceeds the %lld buffered tokens", (long long)n_flush,
+               (long long)n_buf);
+    SS_REQUIRE(t_kv >= 1, "a fused hybrid step needs compressed tokens (t_kv %lld)", (long long)t_kv);
+    SS_REQUIRE(t_kv + n_flush <= cap, "flushed tokens [%lld, %lld) past cap %lld", (long long)t_kv,
+               (long long)(t_kv + n_flush), (long long)cap);
+    SS_UNSUPPORTED(kv_dtype == SS_F16 && buf_dtype == SS_F16,
+                   "a fused hybrid step takes a float16 buffer and float16 new tokens");
+    SS_REQUIRE(k_new && v_new && centroids && codes_il && scales && zeros,
+               "null new keys, values, centroids, codes, scales or zeros");
+    SS_UNSUPPORTED(bits == 2, "a fused hybrid step takes 2-bit codes (got %d)", bits);
+    SS_UNSUPPORTED(group_size == head_dim || 2 * group_size == head_dim,
+                   "group_size %d: the fused kernel takes one or two groups per row", group_size);
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(cap % 16 == 0, "cap must be a multiple of 16 for interleaved grouped values");
+    SS_REQUIRE(((uintptr_t)codes_il % 16) == 0 && ((uintptr_t)scales % 16) == 0 &&
+                   ((uintptr_t)zeros % 16) == 0,
+               "codes, scales and zeros must be 16-byte aligned");
+    SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
+    const float *cents = static_cast<const float *>(codebook);
+    int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
+                          n_blocks, n_centroids, idx, cap, t_kv, out, out_dtype);
+    if (rc) return rc;
+    // buffer rows 0 .. n_buf + n_new - 1 are read or written
+    rc = check_buffer(k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, n_buf + n_new, head_dim);
+    if (rc) return rc;
+    rc = check_buffer(k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, head_dim);
+    if (rc) return rc;
+    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
+                                       kKindMfma);
+    DecodeCommon c;
+    rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents,
+                     n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
+                     workspace_bytes, head_dim);
+    if (rc) return rc;
+    c.centroids = nullptr;
+    c.codebook = static_cast<const uint4 *>(codebook);
+    c.codebook_mul = reinterpret_cast<const float *>(
+        static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
+    if (s.S > 1 && n_flush > 0) {
+        // the last split encodes and attends the flushed tokens before its
+        // tiles: it gives up some cache tokens to the others (as
+        // ss_decode_step_il8)
+        const int64_t room = t_kv - (int64_t)(s.S - 1) * s.tiles_per_split * kWave;
+        const int64_t want =
+            (kHybridStepShareTokens + (s.S - 1) * 8 - 1) / ((int64_t)(s.S - 1) * 8) * 8;
+        const int64_t most = room > 0 ? room / (s.S - 1) / 8 * 8 : 0;
+        c.split_pad = (int)(want < most ? want : most);
+    }
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float *norms = c.codebook_mul + 4;
+    const int ng = head_dim / group_size;
+#define SS_GSTEP(DD, NGG, SZT)                                                                  \
+    {                                                                                           \
+        using VF = VGilStep<DD, 2, NGG, SZT>;                                                   \
+        typename VF::Args a{};                                                                  \
+        a.codes = codes_il;                                                                     \
+        a.scales = static_cast<const SZT *>(scales);                                            \
+        a.zeros = static_cast<const SZT *>(zeros);                                              \
+        a.kbuf = k_buf;                                                                         \
+        a.vbuf = v_buf;                                                                         \
+        a.buf_dtype = buf_dtype;                                                                \
+        a.buf_sb = buf_sb;                                                                      \
+        a.buf_sh = buf_sh;                                                                      \
+        a.buf_st = buf_st;                                                                      \
+        a.t_buf = n_buf - n_flush + n_new;                                                      \
+        a.knew = k_new;                                                                         \
+        a.vnew = v_new;                                                                         \
+        a.new_sb = kv_sb;                                                                       \
+        a.new_sh = kv_sh;                                                                       \
+        a.new_st = kv_st;                                                                       \
+        a.n_rem = n_buf - n_flush;                                                              \
+        a.n_flush = n_flush;                                                                    \
+        a.centroids = centroids;                                                                \
+        a.cb_norms = norms;                                                                     \
+        a.idx_out = idx;                                                                        \
+        a.codes_out = codes_il;                                                                 \
+        a.scales_out = static_cast<SZT *>(scales);                                              \
+        a.zeros_out = static_cast<SZT *>(zeros);                                                \
+        a.kput = k_buf;                                                                         \
+        a.vput = v_buf;                                                                         \
+        return launch_mfma<DD, VF>(c, a, s, st);                                                \
+    }
+#define SS_GSTEP_SZ(DD, NGG)                        \
+    {                                               \
+        if (sz_dtype == SS_F16) SS_GSTEP(DD, NGG, __half) \
+        SS_GSTEP(DD, NGG, float)                    \
+    }
+    if (head_dim == 128) {
+        if (ng == 2) SS_GSTEP_SZ(128, 2)
+        SS_GSTEP_SZ(128, 1)
+    }
+    if (ng == 2) SS_GSTEP_SZ(64, 2)
+    SS_GSTEP_SZ(64, 1)
+#undef SS_GSTEP_SZ
+#undef SS_GSTEP
 }
 
 extern "C" int ss_decode_attn_turboquant_il(

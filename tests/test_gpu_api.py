@@ -934,6 +934,7 @@ def test_hybrid_grouped_decode_steps_fused_equal_separate_appends(bits, buf):
     kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=bits, buffer_size=buf,
               value_scale_dtype=torch.float16)
     fused = S.create_kv_cache(codec, **kw)
+    fused.fuse_steps = False  # the append launch itself (held steps: below)
     plain = S.create_kv_cache(codec, **kw)
     plain._grouped_step_plan = lambda: None  # the separate appends
     fused.update_and_fetch(k[:, :, :300], v[:, :, :300])
@@ -961,6 +962,79 @@ def test_hybrid_grouped_decode_steps_fused_equal_separate_appends(bits, buf):
                           codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
                           fused.buffer_keys.float().cpu().numpy(), vals)
     assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("d,group,szdt,n_new,buf,causal,trim", [
+    (128, 64, torch.float16, 1, 128, False, 0),   # config 4's cache, one token a step
+    (128, 64, torch.float16, 1, 128, False, 5),   # the buffer not full: steps flush nothing
+    (128, 128, torch.float32, 3, 64, True, 0),
+    (64, 32, torch.float16, 2, 32, True, 0),
+    (64, 64, torch.float32, 4, 16, False, 0),
+])
+def test_hybrid_grouped_steps_fuse_into_attention(d, group, szdt, n_new, buf, causal, trim):
+    """With fuse_steps (the default) a decode step of a 2-bit grouped-value
+    hybrid cache waits in the cache, and the next sunshape_sdpa does the
+    buffer flush, the buffer store and the attention in one launch
+    (ss_decode_step_grouped_il_hybrid): update_and_fetch launches nothing,
+    the cache ends bit-identical to the separate step launches (indices,
+    codes, scales, zeros, buffer), the outputs match those over the
+    separately stepped cache (the flushed tokens attended in float32: within
+    2e-5) and the oracle's two-pass path, and a read of the cache or the next
+    update stores a held step first."""
+    codec = make_codec(90 + d, d=d)
+    b, hq, hkv = 2, 8, 2
+    t0, steps = 300, 7
+    k, v = kv(91, b, hkv, t0 + steps * n_new + 1, d)
+    kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=2, value_group_size=group,
+              buffer_size=buf, value_scale_dtype=szdt)
+    fused = S.create_kv_cache(codec, **kw)
+    plain = S.create_kv_cache(codec, **kw)
+    plain.fuse_steps = False
+    for c in (fused, plain):
+        c.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+        if trim:
+            c.trim(trim)
+    t_at = t0 - trim
+    g = torch.Generator(device=DEV).manual_seed(92)
+    mask = "causal" if causal else None
+    for i in range(steps):
+        sl = slice(t_at + i * n_new, t_at + (i + 1) * n_new)
+        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).half()
+        before = sum(S.kernels.get_kernel_stats().values())
+        fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        assert fused._pending is not None
+        assert sum(S.kernels.get_kernel_stats().values()) == before  # held, nothing launched
+        out_f = S.sunshape_sdpa(q, fused, 0.088, mask=mask, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_dequant_step"
+        assert sum(S.kernels.get_kernel_stats().values()) == before + 1
+        assert fused._pending is None
+        plain.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_p = S.sunshape_sdpa(q, plain, 0.088, mask=mask, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_dequant_buffer"
+        assert rel_err(out_f.cpu().numpy(), out_p.cpu().numpy()) <= 2e-5
+    assert fused.compressed_offset == plain.compressed_offset
+    assert fused.buffer_offset == plain.buffer_offset
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values_packed_raw, plain.values_packed_raw)
+    assert torch.equal(fused.value_scales_raw, plain.value_scales_raw)
+    assert torch.equal(fused.value_zeros_raw, plain.value_zeros_raw)
+    assert torch.equal(fused.buffer_keys, plain.buffer_keys)
+    assert torch.equal(fused.buffer_values, plain.buffer_values)
+    vals = fused.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
+                          fused.buffer_keys.float().cpu().numpy(), vals,
+                          mask="causal" if causal else None)
+    assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
+    # a held step is done before anything reads the cache
+    k1, v1 = k[:, :, -1:].contiguous(), v[:, :, -1:].contiguous()
+    _, vo = fused.update_and_fetch(k1, v1)
+    assert fused._pending is not None
+    assert torch.equal(vo[:, :, -1:], v1)  # building the deferred values stores the step
+    assert fused._pending is None
+    plain.update_and_fetch(k1, v1)
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values_packed_raw, plain.values_packed_raw)
 
 
 @pytest.mark.parametrize("backend,bits,buf,qdt", [
