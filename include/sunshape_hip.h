@@ -686,8 +686,8 @@ int ss_decode_step_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
                        size_t workspace_bytes, int n_splits, void *stream);
 
 /*
- * One decode step of a hybrid cache with 2-bit interleaved grouped values
- * (ss_decode_attn_grouped_il_hybrid's layouts) in one launch.  The cache holds
+ * One decode step of a hybrid cache with 2- or 4-bit interleaved grouped
+ * values (ss_decode_attn_grouped_il_hybrid's layouts) in one launch.  The cache holds
  * t_kv (>= 1) compressed tokens and n_buf buffered float16 tokens, the buffer
  * window at k_buf / v_buf [b*buf_sb + h*buf_sh + row*buf_st + dim], rows 0 ..
  * n_buf-1 oldest first; the step's n_new (1..4) float16 tokens arrive at
@@ -703,7 +703,7 @@ int ss_decode_step_il8(const void *q, int q_dtype, int64_t batch, int n_q_heads,
  * them, and stores the flushed tokens' index rows, codes, scales and zeros
  * at positions t_kv .. t_kv + n_flush - 1 and the new tokens at buffer rows
  * n_buf .. n_buf + n_new - 1 (the caller's buffer store must hold them).
- * Other arguments as ss_decode_attn_grouped_il (bits 2); centroids float32
+ * Other arguments as ss_decode_attn_grouped_il; centroids float32
  * [n_blocks][n_centroids][8] (16-byte aligned), codebook their
  * ss_codebook_f16x2.  The caller then counts t_kv + n_flush compressed and
  * n_buf - n_flush + n_new buffered tokens, the window starting n_flush rows

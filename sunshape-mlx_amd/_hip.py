@@ -639,8 +639,8 @@ def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
 
 
 class PreparedHybridStep(PreparedDecode):
-    """One decode step of a hybrid cache with 2-bit interleaved grouped
-    values in one launch (``ss_decode_step_grouped_il_hybrid``): a call
+    """One decode step of a hybrid cache with 2- or 4-bit interleaved
+    grouped values in one launch (``ss_decode_step_grouped_il_hybrid``): a call
     passes the buffer stores' window (``buf_keys`` / ``buf_values``, (B, Hkv,
     >= n_buf + n_new, D) float16 views starting at the oldest buffered
     token), the number of buffered tokens, how many of the oldest leave the
@@ -716,10 +716,10 @@ def prepare_decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: t
     require_gpu(codes_il, scales, zeros, codebook, centroids, buf_keys)
     b_, hq, tq, d = q.shape
     _, hkv, cap, nb = idx.shape
-    if bits != 2:
-        raise SunShapeUnsupported("a fused hybrid step takes 2-bit grouped codes")
+    if bits not in (2, 4):
+        raise SunShapeUnsupported("a fused hybrid step takes 2- or 4-bit grouped codes")
     if nb != n_blocks or codes_il.dim() != 4 or not codes_il.is_contiguous() or \
-            tuple(codes_il.shape) != (b_, hkv, cap // 16, d) or \
+            tuple(codes_il.shape) != (b_, hkv, cap // (32 // bits), d) or \
             codes_il.dtype not in (torch.int32, torch.uint32):
         raise ValueError("codes_il does not match the cache shape")
     for t in (scales, zeros):

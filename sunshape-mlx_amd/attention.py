@@ -121,7 +121,7 @@ def _fused_step(cache: SunShapeKVCache, queries: torch.Tensor, scale: float, cau
 
 def _fused_hybrid_step(cache: HybridSunShapeKVCache, queries: torch.Tensor, scale: float,
                        causal: bool, q_offset: int, out_dtype: torch.dtype):
-    """The decode step a hybrid cache with 2-bit grouped values holds back
+    """The decode step a hybrid cache with 2/4-bit grouped values holds back
     (``cache.fuse_steps``): one ``ss_decode_step_grouped_il_hybrid`` launch
     moves the tokens that leave the buffer into compressed storage, stores
     the new ones in the buffer and attends every token; None (step still

@@ -427,7 +427,7 @@ class HybridSunShapeKVCache:
         self._key_buffer: torch.Tensor | None = None
         self._value_buffer: torch.Tensor | None = None
         self._step_plan = None
-        # With lazy_fetch, a decode step of a 2-bit grouped-value cache (a
+        # With lazy_fetch, a decode step of a grouped-value cache (a
         # few fp16 tokens) is held back (its tensors, not copies) and done by
         # the next attention call in its own launch (ss_decode_step_grouped_il_hybrid:
         # flush, store and attention); anything that reads the storage first
@@ -644,9 +644,9 @@ class HybridSunShapeKVCache:
 
     def _held_step_ok(self, k: torch.Tensor, v: torch.Tensor, t_: int, n_flush: int) -> bool:
         """Whether update_and_fetch may hold this step for the fused
-        attention launch: 1..4 fp16 tokens of a 2-bit grouped-value fp16
-        cache with compressed tokens, at most 4 of them flushed."""
-        return (self.fuse_steps and self.lazy_fetch and self.value_bits == 2 and
+        attention launch: 1..4 fp16 tokens of a 2- or 4-bit grouped-value
+        fp16 cache with compressed tokens, at most 4 of them flushed."""
+        return (self.fuse_steps and self.lazy_fetch and self.value_bits in (2, 4) and
                 self.dtype == torch.float16 and self._compressed_offset > 0 and
                 1 <= t_ <= _hip.MAX_STEP_TOKENS and n_flush <= _hip.MAX_STEP_TOKENS and
                 k.dtype == torch.float16 and v.dtype == torch.float16 and

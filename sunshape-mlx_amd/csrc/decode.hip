@@ -5433,7 +5433,8 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
                    "a fused hybrid step takes a float16 buffer and float16 new tokens");
     SS_REQUIRE(k_new && v_new && centroids && codes_il && scales && zeros,
                "null new keys, values, centroids, codes, scales or zeros");
-    SS_UNSUPPORTED(bits == 2, "a fused hybrid step takes 2-bit codes (got %d)", bits);
+    SS_UNSUPPORTED(bits == 2 || bits == 4, "a fused hybrid step takes 2- or 4-bit codes (got %d)",
+                   bits);
     SS_UNSUPPORTED(group_size == head_dim || 2 * group_size == head_dim,
                    "group_size %d: the fused kernel takes one or two groups per row", group_size);
     SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
@@ -5475,9 +5476,9 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float *norms = c.codebook_mul + 4;
     const int ng = head_dim / group_size;
-#define SS_GSTEP(DD, NGG, SZT)                                                                  \
+#define SS_GSTEP(DD, BB, NGG, SZT)                                                              \
     {                                                                                           \
-        using VF = VGilStep<DD, 2, NGG, SZT>;                                                   \
+        using VF = VGilStep<DD, BB, NGG, SZT>;                                                  \
         typename VF::Args a{};                                                                  \
         a.codes = codes_il;                                                                     \
         a.scales = static_cast<const SZT *>(scales);                                            \
@@ -5506,17 +5507,23 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
         a.vput = v_buf;                                                                         \
         return launch_mfma<DD, VF>(c, a, s, st);                                                \
     }
-#define SS_GSTEP_SZ(DD, NGG)                        \
-    {                                               \
-        if (sz_dtype == SS_F16) SS_GSTEP(DD, NGG, __half) \
-        SS_GSTEP(DD, NGG, float)                    \
+#define SS_GSTEP_SZ(DD, BB, NGG)                             \
+    {                                                        \
+        if (sz_dtype == SS_F16) SS_GSTEP(DD, BB, NGG, __half) \
+        SS_GSTEP(DD, BB, NGG, float)                         \
+    }
+#define SS_GSTEP_NG(DD, BB)                  \
+    {                                        \
+        if (ng == 2) SS_GSTEP_SZ(DD, BB, 2)  \
+        SS_GSTEP_SZ(DD, BB, 1)               \
     }
     if (head_dim == 128) {
-        if (ng == 2) SS_GSTEP_SZ(128, 2)
-        SS_GSTEP_SZ(128, 1)
+        if (bits == 2) SS_GSTEP_NG(128, 2)
+        SS_GSTEP_NG(128, 4)
     }
-    if (ng == 2) SS_GSTEP_SZ(64, 2)
-    SS_GSTEP_SZ(64, 1)
+    if (bits == 2) SS_GSTEP_NG(64, 2)
+    SS_GSTEP_NG(64, 4)
+#undef SS_GSTEP_NG
 #undef SS_GSTEP_SZ
 #undef SS_GSTEP
 }

@@ -964,15 +964,17 @@ def test_hybrid_grouped_decode_steps_fused_equal_separate_appends(bits, buf):
     assert rel_err16(out.float().cpu().numpy(), ref) <= REL_TOL
 
 
-@pytest.mark.parametrize("d,group,szdt,n_new,buf,causal,trim", [
-    (128, 64, torch.float16, 1, 128, False, 0),   # config 4's cache, one token a step
-    (128, 64, torch.float16, 1, 128, False, 5),   # the buffer not full: steps flush nothing
-    (128, 128, torch.float32, 3, 64, True, 0),
-    (64, 32, torch.float16, 2, 32, True, 0),
-    (64, 64, torch.float32, 4, 16, False, 0),
+@pytest.mark.parametrize("d,bits,group,szdt,n_new,buf,causal,trim", [
+    (128, 2, 64, torch.float16, 1, 128, False, 0),   # config 4's cache, one token a step
+    (128, 2, 64, torch.float16, 1, 128, False, 5),   # the buffer not full: steps flush nothing
+    (128, 2, 128, torch.float32, 3, 64, True, 0),
+    (64, 2, 32, torch.float16, 2, 32, True, 0),
+    (64, 2, 64, torch.float32, 4, 16, False, 0),
+    (128, 4, 64, torch.float16, 1, 64, False, 0),    # 4-bit codes: the loader-wave shape
+    (64, 4, 32, torch.float32, 3, 32, True, 0),
 ])
-def test_hybrid_grouped_steps_fuse_into_attention(d, group, szdt, n_new, buf, causal, trim):
-    """With fuse_steps (the default) a decode step of a 2-bit grouped-value
+def test_hybrid_grouped_steps_fuse_into_attention(d, bits, group, szdt, n_new, buf, causal, trim):
+    """With fuse_steps (the default) a decode step of a 2/4-bit grouped-value
     hybrid cache waits in the cache, and the next sunshape_sdpa does the
     buffer flush, the buffer store and the attention in one launch
     (ss_decode_step_grouped_il_hybrid): update_and_fetch launches nothing,
@@ -985,7 +987,7 @@ def test_hybrid_grouped_steps_fuse_into_attention(d, group, szdt, n_new, buf, ca
     b, hq, hkv = 2, 8, 2
     t0, steps = 300, 7
     k, v = kv(91, b, hkv, t0 + steps * n_new + 1, d)
-    kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=2, value_group_size=group,
+    kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=bits, value_group_size=group,
               buffer_size=buf, value_scale_dtype=szdt)
     fused = S.create_kv_cache(codec, **kw)
     plain = S.create_kv_cache(codec, **kw)
@@ -1035,6 +1037,47 @@ def test_hybrid_grouped_steps_fuse_into_attention(d, group, szdt, n_new, buf, ca
     plain.update_and_fetch(k1, v1)
     assert torch.equal(fused.key_indices, plain.key_indices)
     assert torch.equal(fused.values_packed_raw, plain.values_packed_raw)
+
+
+def test_hybrid_grouped_step_ties_take_the_exact_ranking():
+    """A flushed key exactly halfway between two centroids of every block
+    (an exact tie, which no float error bound clears) and one a hair nearer
+    the second: the one-launch hybrid step's encode ranks the tie exactly
+    (the lower index) and stores the indices the separate step launch
+    stores."""
+    rng = np.random.default_rng(93)
+    d, nb, b, hq, hkv, buf, t0 = 128, 16, 1, 8, 2, 16, 100
+    c = rng.standard_normal((nb, 256, 8)).astype(np.float32) * 0.5
+    c[:, 3, :] = 1.0   # the two centroids the keys sit between
+    c[:, 7, :] = 3.0
+    perm = rng.permutation(d).astype(np.int32)
+    codec = S.SunShapeBlockCodec(d, n_centroids=256, device=DEV)
+    codec.load_state_dict({"centroids": c, "permutation": perm})
+    k, v = kv(94, b, hkv, t0 + 2, d)
+    # the buffer's two oldest tokens, which the next two steps flush
+    k[:, :, t0 - buf] = 2.0                                        # tie: index 3
+    near = np.full(d, 2.0, np.float32)
+    near[perm[0::8]] = np.float16(2.0 + 2.0 ** -9)                 # block dim 0 nearer 7
+    k[:, :, t0 - buf + 1] = torch.tensor(near.astype(np.float16), device=DEV)
+    kw = dict(n_kv_heads=hkv, value_backend="grouped", value_bits=2, buffer_size=buf,
+              value_scale_dtype=torch.float16)
+    fused = S.create_kv_cache(codec, **kw)
+    plain = S.create_kv_cache(codec, **kw)
+    plain.fuse_steps = False
+    for cc in (fused, plain):
+        cc.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+    q = torch.randn((b, hq, 1, d), device=DEV).half()
+    for i in range(2):
+        sl = slice(t0 + i, t0 + i + 1)
+        fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_f = S.sunshape_sdpa(q, fused, 0.088, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_dequant_step"
+        plain.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_p = S.sunshape_sdpa(q, plain, 0.088, out_dtype=torch.float32)
+        assert rel_err(out_f.cpu().numpy(), out_p.cpu().numpy()) <= 2e-5
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    got = fused.key_indices[:, :, t0 - buf:t0 - buf + 2].cpu().numpy()
+    assert (got[:, :, 0] == 3).all() and (got[:, :, 1] == 7).all()
 
 
 @pytest.mark.parametrize("backend,bits,buf,qdt", [
