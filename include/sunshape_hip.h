@@ -720,6 +720,24 @@ int ss_decode_step_grouped_il_hybrid(
     size_t workspace_bytes, int n_splits, void *stream);
 
 /*
+ * The same step for a hybrid cache with fp16 values held 8-token interleaved
+ * (ss_decode_attn_il8_hybrid's layouts, value_backend "fp16"): the flushed
+ * tokens' keys are encoded as above, their fp16 values attended as they are
+ * and stored into values_il8 at positions t_kv .. (as ss_append_values_il8);
+ * the rest as ss_decode_step_grouped_il_hybrid.  Replaces the reference's
+ * HybridSunShapeKVCache.update_and_fetch (cache.py:656-710) and its two-pass
+ * attention (attention.py:307-350) for such caches.
+ */
+int ss_decode_step_il8_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, void *values_il8, int64_t cap, int64_t t_kv,
+    void *k_buf, void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
+    int64_t n_buf, int64_t n_flush, const void *k_new, const void *v_new, int kv_dtype,
+    int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t n_new, int causal, int64_t q_offset,
+    void *out, int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream);
+
+/*
  * The inverse of ss_pack_grouped_il: the first n_t tokens of interleaved
  * codes codes_il [n_bh][cap/tpw][head_dim] (n_bh = batch x heads rows) as
  * pack_indices rows out [n_bh][n_t][head_dim*bits/32].  Replaces the

@@ -171,6 +171,12 @@ _SIGNATURES = {
         _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _i64,
         _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
         _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
+    "ss_decode_step_il8_hybrid": (_int, [
+        _c_void_p, _int, _i64, _int, _int, _i64, _int, _f32, _c_void_p, _c_void_p, _c_void_p,
+        _int, _int, _c_void_p, _c_void_p, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64, _i64,
+        _c_void_p, _c_void_p, _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _c_void_p, _int, _c_void_p, _size, _int, _c_void_p]),
     "ss_pack_grouped_il": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int,
                                   _c_void_p, _i64, _i64, _c_void_p]),
     "ss_grouped_il_to_packed": (_int, [_c_void_p, _i64, _i64, _int, _int, _i64, _c_void_p,
@@ -640,7 +646,8 @@ def prepare_decode_grouped_il(q: torch.Tensor, scale: float, perm: torch.Tensor 
 
 class PreparedHybridStep(PreparedDecode):
     """One decode step of a hybrid cache with 2- or 4-bit interleaved
-    grouped values in one launch (``ss_decode_step_grouped_il_hybrid``): a call
+    grouped values (``ss_decode_step_grouped_il_hybrid``), or with fp16
+    values held interleaved (``ss_decode_step_il8_hybrid``), in one launch: a call
     passes the buffer stores' window (``buf_keys`` / ``buf_values``, (B, Hkv,
     >= n_buf + n_new, D) float16 views starting at the oldest buffered
     token), the number of buffered tokens, how many of the oldest leave the
@@ -739,6 +746,33 @@ def prepare_decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: t
            dtype_code(scales.dtype), int(bits), int(group_size), cap)
     return PreparedHybridStep(lib.ss_decode_step_grouped_il_hybrid, pre, q,
                               "sunshape_fused_attention_dequant_mfma", buf_keys)
+
+
+def prepare_decode_step_il8_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | None,
+                                   codebook: torch.Tensor, centroids: torch.Tensor, n_blocks: int,
+                                   n_centroids: int, idx: torch.Tensor, values_il8: torch.Tensor,
+                                   buf_keys: torch.Tensor) -> PreparedHybridStep:
+    """:class:`PreparedHybridStep` of a hybrid cache with fp16 values held
+    8-token interleaved (``ss_decode_step_il8_hybrid``): the flushed tokens'
+    index rows and values are written into ``idx`` / ``values_il8``."""
+    _check_decode_common(q, idx, None, perm)
+    require_gpu(values_il8, codebook, centroids, buf_keys)
+    b_, hq, tq, d = q.shape
+    _, hkv, cap, nb = idx.shape
+    if nb != n_blocks or values_il8.dtype != torch.float16 or not values_il8.is_contiguous() or \
+            tuple(values_il8.shape) != (b_, hkv, cap // 8, d, 8):
+        raise ValueError(f"values_il8 must be contiguous float16 {(b_, hkv, cap // 8, d, 8)}")
+    if centroids.dtype != torch.float32 or not centroids.is_contiguous() or \
+            tuple(centroids.shape) != (n_blocks, n_centroids, 8):
+        raise ValueError(f"centroids must be contiguous float32 {(n_blocks, n_centroids, 8)}")
+    lib = load_library()
+    if codebook.numel() != lib.ss_codebook_f16x2_bytes(n_blocks, n_centroids):
+        raise ValueError("codebook does not match the centroids' shape")
+    _buffer_args(buf_keys, buf_keys, 1, b_, hkv, d)
+    pre = (dtype_code(q.dtype), b_, hq, hkv, tq, d, float(scale), ptr(perm), ptr(codebook),
+           ptr(centroids), nb, n_centroids, ptr(idx), ptr(values_il8), cap)
+    return PreparedHybridStep(lib.ss_decode_step_il8_hybrid, pre, q,
+                              "sunshape_fused_attention_mfma", buf_keys)
 
 
 def decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: torch.Tensor | None,

@@ -121,15 +121,19 @@ def _fused_step(cache: SunShapeKVCache, queries: torch.Tensor, scale: float, cau
 
 def _fused_hybrid_step(cache: HybridSunShapeKVCache, queries: torch.Tensor, scale: float,
                        causal: bool, q_offset: int, out_dtype: torch.dtype):
-    """The decode step a hybrid cache with 2/4-bit grouped values holds back
-    (``cache.fuse_steps``): one ``ss_decode_step_grouped_il_hybrid`` launch
+    """The decode step a hybrid cache with 2/4-bit grouped or fp16 values
+    holds back (``cache.fuse_steps``): one ``ss_decode_step_grouped_il_hybrid``
+    (or ``ss_decode_step_il8_hybrid``) launch
     moves the tokens that leave the buffer into compressed storage, stores
     the new ones in the buffer and attends every token; None (step still
     held) when that launch does not apply."""
     codec = cache.codec
     q, kscale, perm = _kernel_query(codec, queries, scale)
-    tensors = (cache._key_indices, cache._values_il, cache._value_scales, cache._value_zeros,
-               codec.kernel_codebook(), codec.centroids, cache._key_buffer, cache._value_buffer)
+    grouped = cache._grouped_il
+    vals = ((cache._values_il, cache._value_scales, cache._value_zeros) if grouped
+            else (cache._values_il8,))
+    tensors = (cache._key_indices,) + vals + (codec.kernel_codebook(), codec.centroids,
+                                               cache._key_buffer, cache._value_buffer)
     if perm is not None:
         tensors += (perm,)
     key = ("hstep", q.shape, q.dtype, q.device, kscale)
@@ -138,12 +142,18 @@ def _fused_hybrid_step(cache: HybridSunShapeKVCache, queries: torch.Tensor, scal
             all(r() is t for r, t in zip(held[1], tensors)):
         plan = held[2]
     else:
-        gc = cache._value_codec_impl
+        cb = codec.kernel_codebook()
         try:
-            plan = _hip.prepare_decode_step_grouped_il_hybrid(
-                q, kscale, perm, tensors[4], codec.centroids, codec.n_blocks, codec.n_centroids,
-                cache._key_indices, cache._values_il, cache._value_scales, cache._value_zeros,
-                gc.bits, gc.group_size, cache._key_buffer)
+            if grouped:
+                gc = cache._value_codec_impl
+                plan = _hip.prepare_decode_step_grouped_il_hybrid(
+                    q, kscale, perm, cb, codec.centroids, codec.n_blocks, codec.n_centroids,
+                    cache._key_indices, cache._values_il, cache._value_scales,
+                    cache._value_zeros, gc.bits, gc.group_size, cache._key_buffer)
+            else:
+                plan = _hip.prepare_decode_step_il8_hybrid(
+                    q, kscale, perm, cb, codec.centroids, codec.n_blocks, codec.n_centroids,
+                    cache._key_indices, cache._values_il8, cache._key_buffer)
         except (_hip.SunShapeUnsupported, ValueError):
             return None
         cache._hstep_prepared = (key, tuple(weakref.ref(t) for t in tensors), plan)
@@ -155,7 +165,7 @@ def _fused_hybrid_step(cache: HybridSunShapeKVCache, queries: torch.Tensor, scal
     except (_hip.SunShapeUnsupported, ValueError):  # raised before any launch
         cache._pending = pend
         return None
-    codec.last_score_backend = "hip_fused_mfma_dequant_step"
+    codec.last_score_backend = "hip_fused_mfma_dequant_step" if grouped else "hip_fused_mfma_step"
     return out
 
 

@@ -644,9 +644,14 @@ class HybridSunShapeKVCache:
 
     def _held_step_ok(self, k: torch.Tensor, v: torch.Tensor, t_: int, n_flush: int) -> bool:
         """Whether update_and_fetch may hold this step for the fused
-        attention launch: 1..4 fp16 tokens of a 2- or 4-bit grouped-value
-        fp16 cache with compressed tokens, at most 4 of them flushed."""
-        return (self.fuse_steps and self.lazy_fetch and self.value_bits in (2, 4) and
+        attention launch: 1..4 fp16 tokens of an fp16 cache with compressed
+        tokens, at most 4 of them flushed, whose values are 2- or 4-bit
+        interleaved grouped codes or interleaved fp16, keys of the
+        permutation codec (no fp16 heavy blocks)."""
+        c = self.codec
+        kind_ok = ((self._grouped_il and self.value_bits in (2, 4)) or self._fp16_il8) and \
+            self._heavy_dims is None and c.mode == "profileperm_baseline" and c.n_centroids <= 256
+        return (kind_ok and self.fuse_steps and self.lazy_fetch and
                 self.dtype == torch.float16 and self._compressed_offset > 0 and
                 1 <= t_ <= _hip.MAX_STEP_TOKENS and n_flush <= _hip.MAX_STEP_TOKENS and
                 k.dtype == torch.float16 and v.dtype == torch.float16 and
@@ -677,12 +682,23 @@ class HybridSunShapeKVCache:
         return k, v, tc, s0, n, nf
 
     def flush(self) -> None:
-        """Do a held decode step's flush and buffer store now (one
-        ss_hybrid_append_grouped_il launch)."""
+        """Do a held decode step's buffer store and flush now: one
+        ss_hybrid_append_grouped_il launch for grouped values; for fp16
+        values the buffer store, then the flush of the oldest tokens as an
+        unheld step does it."""
         if self._pending is None:
             return
         k, v, tc, s0, n, nf = self._take_pending()
-        self._run_grouped_step(self._grouped_step_plan(), k, v, tc, s0, n, nf)
+        if self._grouped_il:
+            self._run_grouped_step(self._grouped_step_plan(), k, v, tc, s0, n, nf)
+            return
+        after = (self._compressed_offset, self._buffer_offset, self._buf_start)
+        t_ = k.shape[2]
+        self._compressed_offset, self._buffer_offset, self._buf_start = tc, n + t_, s0
+        self._key_buffer[:, :, s0 + n:s0 + n + t_] = k
+        self._value_buffer[:, :, s0 + n:s0 + n + t_] = v
+        self._flush_buffer(k.shape[0], nf)
+        assert (self._compressed_offset, self._buffer_offset, self._buf_start) == after
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         """Append to the buffer; flush the overflow beyond ``buffer_size``
@@ -699,20 +715,27 @@ class HybridSunShapeKVCache:
         dev = keys.device
         self._ensure_buffer(b_, t_, dev)
         n_flush = max(0, self._buffer_offset + t_ - self.buffer_size)
-        plan = None
-        if self._grouped_il and 0 <= n_flush <= self._buffer_offset and t_ <= 64 and \
-                (n_flush > 0 or self._held_step_ok(keys, values, t_, n_flush)):
-            self._grow_compressed(b_, self._compressed_offset + n_flush, dev)
-            plan = self._grouped_step_plan()
         k = keys if keys.stride(-1) == 1 else keys.contiguous()
         v = values if values.stride(-1) == 1 else values.contiguous()
-        if plan is not None and k.dtype == v.dtype:
+        hold = n_flush <= self._buffer_offset and self._held_step_ok(k, v, t_, n_flush)
+        plan = None
+        if self._grouped_il and 0 <= n_flush <= self._buffer_offset and t_ <= 64 and \
+                (n_flush > 0 or hold):
+            self._grow_compressed(b_, self._compressed_offset + n_flush, dev)
+            plan = self._grouped_step_plan()
+        if hold and (plan is not None or self._fp16_il8):
+            # held for the next attention call's fused step (the counters
+            # include it already; flush() stores it)
+            self._grow_compressed(b_, self._compressed_offset + n_flush, dev)
             s0, n, tc = self._buf_start, self._buffer_offset, self._compressed_offset
-            if self._held_step_ok(k, v, t_, n_flush):
-                # held for the next attention call's fused step
-                self._pending = (k, v, k._version, v._version, tc, s0, n, n_flush)
-            else:
-                self._run_grouped_step(plan, k, v, tc, s0, n, n_flush)
+            self._pending = (k, v, k._version, v._version, tc, s0, n, n_flush)
+            self._compressed_offset += n_flush
+            self._buffer_offset += t_ - n_flush
+            self._buf_start = s0 + n_flush if self._buffer_offset else 0
+            self.last_value_quant_backend = "hip" if plan is not None else "fp16"
+        elif plan is not None and k.dtype == v.dtype:
+            s0, n, tc = self._buf_start, self._buffer_offset, self._compressed_offset
+            self._run_grouped_step(plan, k, v, tc, s0, n, n_flush)
             self._compressed_offset += n_flush
             self._buffer_offset += t_ - n_flush
             self._buf_start = s0 + n_flush if self._buffer_offset else 0

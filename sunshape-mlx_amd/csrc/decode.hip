@@ -951,6 +951,12 @@ template <class VF, class = void>
 struct HybridStepOf : std::false_type {};
 template <class VF>
 struct HybridStepOf<VF, std::void_t<decltype(VF::kHybridStep)>> : std::bool_constant<VF::kHybridStep> {};
+// Hybrid-step formats whose flushed values are quantised (VGilStep) rather
+// than stored as fp16 (VIl8HybStep).
+template <class VF, class = void>
+struct StepQuantOf : std::false_type {};
+template <class VF>
+struct StepQuantOf<VF, std::void_t<decltype(VF::kStepQuant)>> : std::bool_constant<VF::kStepQuant> {};
 
 template <int D, int NC, class VF>
 struct WsCfg {
@@ -1193,6 +1199,28 @@ struct VIl8Step : VIl8<D> {
     static constexpr bool kHeavyCapable = false;
 };
 constexpr int kMaxStepTokens = 4;  // new tokens of one fused decode step (A rows 4s + r)
+
+// VIl8Hyb for one decode step of a hybrid cache with fp16 values that also
+// moves its tokens (the VGilStep protocol, below): the flushed tokens' fp16
+// values are attended as they are and stored into the interleaved values
+// (v8_out) at positions t_kv .., beside their index rows.
+template <int D>
+struct VIl8HybStep : VIl8<D> {
+    struct Args : VIl8Hyb<D>::Args {
+        const void *knew, *vnew;  // float16 [b*new_sb + h*new_sh + j*new_st + dim]
+        int64_t new_sb, new_sh, new_st, n_rem, n_flush;
+        const float *centroids;  // [n_blocks][n_centroids][8] float32
+        const float *cb_norms;   // |C|^2 per prepared codebook lane (ss_codebook_f16x2)
+        uint8_t *idx_out;        // the index cache the kernel reads (c.idx)
+        __half *v8_out;          // the value cache (v8)
+        void *kput, *vput;       // the buffer stores at the window (kbuf / vbuf)
+    };
+    static constexpr bool kHybridBuffer = true;
+    static constexpr bool kStepShare = true;
+    static constexpr bool kHybridStep = true;
+    static constexpr bool kStepQuant = false;
+    static constexpr bool kHeavyCapable = false;
+};
 // cache tokens the last split of a fused step hands to the other splits
 // (about the time of its encode and share)
 constexpr int64_t kStepShareTokens = 192;
@@ -1570,6 +1598,7 @@ struct VGilStep : VGil<D, BITS, NG, SZT> {
     };
     static constexpr bool kStepShare = true;
     static constexpr bool kHybridStep = true;
+    static constexpr bool kStepQuant = true;  // the flushed values are quantised
     static constexpr bool kHeavyCapable = false;
     static constexpr int kBits = BITS;
     static constexpr int kNG = NG;
@@ -2333,7 +2362,6 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     }
                 }
                 asm volatile("" ::: "memory");
-                using SZT = typename VF::SzT;
                 float sc[NS][R], vh[NS][DL];
 #pragma unroll
                 for (int j = 0; j < NS; ++j) {
@@ -2344,11 +2372,17 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     const int64_t pos = c.t_kv + j;
 #pragma unroll
                     for (int r = 0; r < R; ++r) sc[j][r] = (j < n_step && pos <= lim[r]) ? e[r] : -INFINITY;
-                    float qc[DL], qs[DL], qz[DL];
-                    quantize_token_wave<D, VF::kBits, VF::kNG>(vpre[j], qc, qs, qz);
+                    if constexpr (VF::kStepQuant) {
+                        using SZT = typename VF::SzT;
+                        float qc[DL], qs[DL], qz[DL];
+                        quantize_token_wave<D, VF::kBits, VF::kNG>(vpre[j], qc, qs, qz);
 #pragma unroll
-                    for (int k = 0; k < DL; ++k)
-                        vh[j][k] = fmaf(qc[k], (float)(SZT)qs[k], (float)(SZT)qz[k]);
+                        for (int k = 0; k < DL; ++k)
+                            vh[j][k] = fmaf(qc[k], (float)(SZT)qs[k], (float)(SZT)qz[k]);
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < DL; ++k) vh[j][k] = vpre[j][k];  // fp16 values as they are
+                    }
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
@@ -2524,6 +2558,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     vput_r[i] = reinterpret_cast<const PutT *>(ex_row(va, true, va.n_rem + ii))[lane];
                 }
             }
+            if constexpr (VF::kStepQuant) {
             if (code_wave) {
                 constexpr int TPW = 32 / VF::kBits;
                 const int64_t w0 = c.t_kv / TPW, wmax = c.cap / TPW - 1;
@@ -2533,6 +2568,7 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                     for (int k = 0; k < DLs; ++k)
                         cw_pre[s2][k] = va.codes_out[(bh * (c.cap / TPW) + min(w0 + s2, wmax)) * D +
                                                      lane + kWave * k];
+            }
             }
         }
         if constexpr (kStep) {
@@ -2918,7 +2954,19 @@ __global__ void __launch_bounds__((VF::kPrivateRing ? NC : NC + 1) * kWave)
                         }
                     }
                 }
-                if constexpr (kHStep) {
+                if constexpr (kHStep && !StepQuantOf<VF>::value) {
+                    if (code_wave) {
+                        // the flushed tokens' fp16 values into the interleaved values
+#pragma unroll
+                        for (int j = 0; j < NS; ++j)
+                            if (j < n_step)
+#pragma unroll
+                                for (int k = 0; k < DLs; ++k)
+                                    store_value_il8(va.v8_out, bh, c.cap, D, c.t_kv + j, lane + kWave * k,
+                                                    vpre[j][k]);
+                    }
+                }
+                if constexpr (StepQuantOf<VF>::value) {
                     if (code_wave) {
                         // the flushed tokens' codes into their words (the
                         // other tokens' bits kept: token i of a word at bit
@@ -5410,15 +5458,19 @@ extern "C" int ss_decode_attn_grouped_il_hybrid(
                            buf_st, t_buf, stream, k_heavy, heavy_dims, n_heavy_dims);
 }
 
-extern "C" int ss_decode_step_grouped_il_hybrid(
-    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
-    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
-    int n_blocks, int n_centroids, uint8_t *idx, uint32_t *codes_il, void *scales, void *zeros,
-    int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv, void *k_buf, void *v_buf,
-    int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t n_buf, int64_t n_flush,
-    const void *k_new, const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
-    int64_t n_new, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
-    size_t workspace_bytes, int n_splits, void *stream) {
+// The checks and launch set-up shared by the hybrid-step entry points:
+// step sizes, the buffer window and the new tokens, then the common decode
+// arguments and the last split's hand-over of cache tokens.
+static int hybrid_step_setup(DecodeCommon &c, DecodeShape &s, const void *q, int q_dtype,
+                             int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+                             int head_dim, float scale, const int32_t *perm, const void *codebook,
+                             const float *centroids, int n_blocks, int n_centroids,
+                             const uint8_t *idx, int64_t cap, int64_t t_kv, const void *k_buf,
+                             const void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh,
+                             int64_t buf_st, int64_t n_buf, int64_t n_flush, const void *k_new,
+                             const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh,
+                             int64_t kv_st, int64_t n_new, int causal, int64_t q_offset, void *out,
+                             int out_dtype, void *workspace, size_t workspace_bytes, int n_splits) {
     SS_UNSUPPORTED(n_new >= 1 && n_new <= kMaxStepTokens, "a fused step takes 1..%d new tokens",
                    kMaxStepTokens);
     SS_UNSUPPORTED(n_flush >= 0 && n_flush <= kMaxStepTokens,
@@ -5431,17 +5483,7 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
                (long long)(t_kv + n_flush), (long long)cap);
     SS_UNSUPPORTED(kv_dtype == SS_F16 && buf_dtype == SS_F16,
                    "a fused hybrid step takes a float16 buffer and float16 new tokens");
-    SS_REQUIRE(k_new && v_new && centroids && codes_il && scales && zeros,
-               "null new keys, values, centroids, codes, scales or zeros");
-    SS_UNSUPPORTED(bits == 2 || bits == 4, "a fused hybrid step takes 2- or 4-bit codes (got %d)",
-                   bits);
-    SS_UNSUPPORTED(group_size == head_dim || 2 * group_size == head_dim,
-                   "group_size %d: the fused kernel takes one or two groups per row", group_size);
-    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
-    SS_REQUIRE(cap % 16 == 0, "cap must be a multiple of 16 for interleaved grouped values");
-    SS_REQUIRE(((uintptr_t)codes_il % 16) == 0 && ((uintptr_t)scales % 16) == 0 &&
-                   ((uintptr_t)zeros % 16) == 0,
-               "codes, scales and zeros must be 16-byte aligned");
+    SS_REQUIRE(k_new && v_new && centroids, "null new keys, values or centroids");
     SS_REQUIRE(((uintptr_t)codebook % 16) == 0, "prepared codebook must be 16-byte aligned");
     const float *cents = static_cast<const float *>(codebook);
     int rc = check_common(q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, centroids,
@@ -5452,9 +5494,7 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
     if (rc) return rc;
     rc = check_buffer(k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, head_dim);
     if (rc) return rc;
-    const DecodeShape s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits,
-                                       kKindMfma);
-    DecodeCommon c;
+    s = decode_shape(batch, n_q_heads, n_kv_heads, t_q, t_kv, n_splits, kKindMfma);
     rc = fill_common(c, s, q, q_dtype, n_q_heads, n_kv_heads, t_q, scale, perm, cents,
                      n_centroids, idx, cap, t_kv, causal, q_offset, out, out_dtype, workspace,
                      workspace_bytes, head_dim);
@@ -5473,6 +5513,36 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
         const int64_t most = room > 0 ? room / (s.S - 1) / 8 * 8 : 0;
         c.split_pad = (int)(want < most ? want : most);
     }
+    return SS_OK;
+}
+
+extern "C" int ss_decode_step_grouped_il_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, uint32_t *codes_il, void *scales, void *zeros,
+    int sz_dtype, int bits, int group_size, int64_t cap, int64_t t_kv, void *k_buf, void *v_buf,
+    int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st, int64_t n_buf, int64_t n_flush,
+    const void *k_new, const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+    int64_t n_new, int causal, int64_t q_offset, void *out, int out_dtype, void *workspace,
+    size_t workspace_bytes, int n_splits, void *stream) {
+    SS_REQUIRE(codes_il && scales && zeros, "null codes, scales or zeros");
+    SS_UNSUPPORTED(bits == 2 || bits == 4, "a fused hybrid step takes 2- or 4-bit codes (got %d)",
+                   bits);
+    SS_UNSUPPORTED(group_size == head_dim || 2 * group_size == head_dim,
+                   "group_size %d: the fused kernel takes one or two groups per row", group_size);
+    SS_REQUIRE(sz_dtype == SS_F32 || sz_dtype == SS_F16, "scale/zero dtype must be f32 or f16");
+    SS_REQUIRE(cap % 16 == 0, "cap must be a multiple of 16 for interleaved grouped values");
+    SS_REQUIRE(((uintptr_t)codes_il % 16) == 0 && ((uintptr_t)scales % 16) == 0 &&
+                   ((uintptr_t)zeros % 16) == 0,
+               "codes, scales and zeros must be 16-byte aligned");
+    DecodeCommon c;
+    DecodeShape s;
+    int rc = hybrid_step_setup(c, s, q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale,
+                               perm, codebook, centroids, n_blocks, n_centroids, idx, cap, t_kv,
+                               k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, n_buf, n_flush,
+                               k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, causal, q_offset,
+                               out, out_dtype, workspace, workspace_bytes, n_splits);
+    if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float *norms = c.codebook_mul + 4;
     const int ng = head_dim / group_size;
@@ -5526,6 +5596,59 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
 #undef SS_GSTEP_NG
 #undef SS_GSTEP_SZ
 #undef SS_GSTEP
+}
+
+extern "C" int ss_decode_step_il8_hybrid(
+    const void *q, int q_dtype, int64_t batch, int n_q_heads, int n_kv_heads, int64_t t_q,
+    int head_dim, float scale, const int32_t *perm, const void *codebook, const float *centroids,
+    int n_blocks, int n_centroids, uint8_t *idx, void *values_il8, int64_t cap, int64_t t_kv,
+    void *k_buf, void *v_buf, int buf_dtype, int64_t buf_sb, int64_t buf_sh, int64_t buf_st,
+    int64_t n_buf, int64_t n_flush, const void *k_new, const void *v_new, int kv_dtype,
+    int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t n_new, int causal, int64_t q_offset,
+    void *out, int out_dtype, void *workspace, size_t workspace_bytes, int n_splits, void *stream) {
+    SS_REQUIRE(values_il8, "null values");
+    SS_REQUIRE(cap % 8 == 0, "cap must be a multiple of 8 for interleaved values");
+    SS_REQUIRE(((uintptr_t)values_il8 % 16) == 0, "values must be 16-byte aligned");
+    DecodeCommon c;
+    DecodeShape s;
+    int rc = hybrid_step_setup(c, s, q, q_dtype, batch, n_q_heads, n_kv_heads, t_q, head_dim, scale,
+                               perm, codebook, centroids, n_blocks, n_centroids, idx, cap, t_kv,
+                               k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, n_buf, n_flush,
+                               k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, causal, q_offset,
+                               out, out_dtype, workspace, workspace_bytes, n_splits);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const float *norms = c.codebook_mul + 4;
+    __half *v8 = static_cast<__half *>(values_il8);
+    auto run = [&](auto dtag) {
+        constexpr int DD = decltype(dtag)::value;
+        using VF = VIl8HybStep<DD>;
+        typename VF::Args a{};
+        a.v8 = v8;
+        a.kbuf = k_buf;
+        a.vbuf = v_buf;
+        a.buf_dtype = buf_dtype;
+        a.buf_sb = buf_sb;
+        a.buf_sh = buf_sh;
+        a.buf_st = buf_st;
+        a.t_buf = n_buf - n_flush + n_new;
+        a.knew = k_new;
+        a.vnew = v_new;
+        a.new_sb = kv_sb;
+        a.new_sh = kv_sh;
+        a.new_st = kv_st;
+        a.n_rem = n_buf - n_flush;
+        a.n_flush = n_flush;
+        a.centroids = centroids;
+        a.cb_norms = norms;
+        a.idx_out = idx;
+        a.v8_out = v8;
+        a.kput = k_buf;
+        a.vput = v_buf;
+        return launch_mfma<DD, VF>(c, a, s, st);
+    };
+    if (head_dim == 128) return run(std::integral_constant<int, 128>{});
+    return run(std::integral_constant<int, 64>{});
 }
 
 extern "C" int ss_decode_attn_turboquant_il(

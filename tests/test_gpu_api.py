@@ -1039,6 +1039,59 @@ def test_hybrid_grouped_steps_fuse_into_attention(d, bits, group, szdt, n_new, b
     assert torch.equal(fused.values_packed_raw, plain.values_packed_raw)
 
 
+@pytest.mark.parametrize("d,n_new,buf,causal", [(128, 1, 64, False), (64, 3, 32, True)])
+def test_hybrid_fp16_steps_fuse_into_attention(d, n_new, buf, causal):
+    """A hybrid cache with fp16 values (a non-default buffer size) holds its
+    decode steps too: one ss_decode_step_il8_hybrid launch per step encodes
+    the keys leaving the buffer, stores their values interleaved and the new
+    tokens in the buffer, and attends every token.  The cache ends
+    bit-identical to the unheld steps (buffer copies, then the flush), the
+    outputs match the decode over that cache within 2e-5 and the oracle's
+    two-pass path within 1e-3."""
+    codec = make_codec(95 + d, d=d)
+    b, hq, hkv = 2, 8, 2
+    t0, steps = 300, 6
+    k, v = kv(96, b, hkv, t0 + steps * n_new, d)
+    kw = dict(n_kv_heads=hkv, value_backend="fp16", buffer_size=buf)
+    fused = S.create_kv_cache(codec, **kw)
+    plain = S.create_kv_cache(codec, **kw)
+    plain.fuse_steps = False
+    assert isinstance(fused, S.HybridSunShapeKVCache) and fused._fp16_il8
+    for c in (fused, plain):
+        c.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+    g = torch.Generator(device=DEV).manual_seed(97)
+    mask = "causal" if causal else None
+    for i in range(steps):
+        sl = slice(t0 + i * n_new, t0 + (i + 1) * n_new)
+        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).half()
+        before = sum(S.kernels.get_kernel_stats().values())
+        fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        assert sum(S.kernels.get_kernel_stats().values()) == before  # held, nothing launched
+        out_f = S.sunshape_sdpa(q, fused, 0.088, mask=mask, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_step"
+        assert sum(S.kernels.get_kernel_stats().values()) == before + 1
+        plain.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_p = S.sunshape_sdpa(q, plain, 0.088, mask=mask, out_dtype=torch.float32)
+        assert codec.last_score_backend == "hip_fused_mfma_buffer"
+        assert rel_err(out_f.cpu().numpy(), out_p.cpu().numpy()) <= 2e-5
+    assert fused.compressed_offset == plain.compressed_offset
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values, plain.values)
+    assert torch.equal(fused.buffer_keys, plain.buffer_keys)
+    vals = fused.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
+                          fused.buffer_keys.float().cpu().numpy(), vals, mask=mask)
+    assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
+    # a held step is stored before the cache is read
+    k1, v1 = k[:, :, -1:].contiguous(), v[:, :, -1:].contiguous()
+    fused.update_and_fetch(k1, v1)
+    plain.update_and_fetch(k1, v1)
+    assert fused._pending is not None
+    assert torch.equal(fused.values, plain.values) and fused._pending is None
+    assert torch.equal(fused.key_indices, plain.key_indices)
+
+
 def test_hybrid_grouped_step_ties_take_the_exact_ranking():
     """A flushed key exactly halfway between two centroids of every block
     (an exact tie, which no float error bound clears) and one a hair nearer
