@@ -5505,12 +5505,12 @@ static int hybrid_step_setup(DecodeCommon &c, DecodeShape &s, const void *q, int
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     if (s.S > 1 && n_flush > 0) {
         // the last split encodes and attends the flushed tokens before its
-        // tiles: it gives up some cache tokens to the others (as
-        // ss_decode_step_il8)
+        // tiles: it gives up some cache tokens to the others, whole 64-token
+        // units (a split must start on a code word: 16 tokens of 2-bit codes)
         const int64_t room = t_kv - (int64_t)(s.S - 1) * s.tiles_per_split * kWave;
-        const int64_t want =
-            (kHybridStepShareTokens + (s.S - 1) * 8 - 1) / ((int64_t)(s.S - 1) * 8) * 8;
-        const int64_t most = room > 0 ? room / (s.S - 1) / 8 * 8 : 0;
+        const int64_t want = (kHybridStepShareTokens + (s.S - 1) * kWave - 1) /
+                             ((int64_t)(s.S - 1) * kWave) * kWave;
+        const int64_t most = room > 0 ? room / (s.S - 1) / kWave * kWave : 0;
         c.split_pad = (int)(want < most ? want : most);
     }
     return SS_OK;

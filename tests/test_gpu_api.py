@@ -1092,6 +1092,60 @@ def test_hybrid_fp16_steps_fuse_into_attention(d, n_new, buf, causal):
     assert torch.equal(fused.key_indices, plain.key_indices)
 
 
+@pytest.mark.parametrize("backend,b,hq,hkv,t0,buf,n_new", [
+    ("grouped", 1, 4, 4, 20, 8, 1),      # a dozen compressed tokens: one split, fewer units than waves
+    ("grouped", 3, 32, 8, 5000, 8, 4),   # every step flushes four tokens; two splits
+    ("grouped", 3, 32, 8, 5000, 8, 1),   # ten splits (the last hands over whole units only)
+    ("grouped", 1, 32, 8, 5000, 8, 4),   # eight splits
+    ("grouped", 2, 16, 2, 1100, 128, 2),  # eight query heads a KV head: two row groups
+    ("fp16", 1, 4, 4, 20, 8, 1),
+    ("fp16", 3, 32, 8, 5000, 16, 4),
+])
+def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new):
+    """One-launch hybrid steps at shapes the other tests do not reach: a
+    single split holding fewer 64-token units than waves, steps that flush
+    the most tokens, up to ten splits, several row groups a KV head.  The
+    cache ends bit-identical to the unheld steps; the outputs match the
+    oracle's two-pass path over that cache within 1e-3 and the decode over
+    it within 5e-4 (fp16 values: 2e-5).  The grouped kernels' sums carry the
+    codes' bf16 bias (128 + code) and lose about 7 bits to its subtraction,
+    so two split layouts of 5000 tokens differ by up to 1.2e-4 of the largest
+    output, each within 1.2e-4 of the exact float32-value result."""
+    codec = make_codec(98)
+    d = 128
+    steps = 3
+    k, v = kv(99, b, hkv, t0 + steps * n_new, d)
+    kw = dict(n_kv_heads=hkv, value_backend=backend, buffer_size=buf)
+    if backend == "grouped":
+        kw.update(value_bits=2, value_scale_dtype=torch.float16)
+    fused = S.create_kv_cache(codec, **kw)
+    plain = S.create_kv_cache(codec, **kw)
+    plain.fuse_steps = False
+    for c in (fused, plain):
+        c.update_and_fetch(k[:, :, :t0], v[:, :, :t0])
+    g = torch.Generator(device=DEV).manual_seed(100)
+    for i in range(steps):
+        sl = slice(t0 + i * n_new, t0 + (i + 1) * n_new)
+        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).half()
+        fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        assert fused._pending is not None
+        out_f = S.sunshape_sdpa(q, fused, 0.088, mask="causal", out_dtype=torch.float32)
+        assert codec.last_score_backend in ("hip_fused_mfma_dequant_step", "hip_fused_mfma_step")
+        plain.update_and_fetch(k[:, :, sl], v[:, :, sl])
+        out_p = S.sunshape_sdpa(q, plain, 0.088, mask="causal", out_dtype=torch.float32)
+        tol = 5e-4 if backend == "grouped" else 2e-5
+        assert rel_err(out_f.cpu().numpy(), out_p.cpu().numpy()) <= tol
+    assert fused.compressed_offset == plain.compressed_offset
+    assert torch.equal(fused.key_indices, plain.key_indices)
+    assert torch.equal(fused.values, plain.values)
+    assert torch.equal(fused.buffer_keys, plain.buffer_keys)
+    vals = fused.values.float().cpu().numpy()
+    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+                          codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
+                          fused.buffer_keys.float().cpu().numpy(), vals, mask="causal")
+    assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
+
+
 def test_hybrid_grouped_step_ties_take_the_exact_ranking():
     """A flushed key exactly halfway between two centroids of every block
     (an exact tie, which no float error bound clears) and one a hair nearer
