@@ -724,7 +724,7 @@ def prepare_decode_step_grouped_il_hybrid(q: torch.Tensor, scale: float, perm: t
     b_, hq, tq, d = q.shape
     _, hkv, cap, nb = idx.shape
     if bits not in (2, 4):
-        raise SunShapeUnsupported("a fused hybrid step takes 2- or 4-bit grouped codes")
+        raise SunShapeUnsupported(-2, "a fused hybrid step takes 2- or 4-bit grouped codes")
     if nb != n_blocks or codes_il.dim() != 4 or not codes_il.is_contiguous() or \
             tuple(codes_il.shape) != (b_, hkv, cap // (32 // bits), d) or \
             codes_il.dtype not in (torch.int32, torch.uint32):

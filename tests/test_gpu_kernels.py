@@ -1411,6 +1411,48 @@ def test_decode_step_il8_rejects_what_it_cannot_take():
     assert not idx.any() and not v8.any()
 
 
+def test_hybrid_steps_reject_what_they_cannot_take():
+    """Host checks of the one-launch hybrid steps before any launch: no new
+    tokens or more than MAX_STEP_TOKENS, more tokens flushed than buffered
+    or than a step takes, an empty compressed part, flushed positions past
+    the capacity, non-fp16 new tokens, 3-bit codes; nothing is written."""
+    rng = np.random.default_rng(6)
+    cents = t(rng.standard_normal((16, 256, 8)).astype(np.float32))
+    cb = _hip.codebook_f16x2(cents)
+    cap = 64
+    idx = torch.zeros((1, 2, cap, 16), dtype=torch.uint8, device=DEV)
+    il = torch.zeros((1, 2, cap // 16, 128), dtype=torch.int32, device=DEV)
+    sc = torch.zeros((1, 2, cap, 2), dtype=torch.float16, device=DEV)
+    ze = torch.zeros_like(sc)
+    v8 = torch.zeros((1, 2, cap // 8, 128, 8), dtype=torch.float16, device=DEV)
+    bk = torch.zeros((1, 2, 32, 128), dtype=torch.float16, device=DEV)
+    bv = torch.zeros_like(bk)
+    q = torch.randn((1, 8, 1, 128), device=DEV).half()
+
+    def new(n, dt=torch.float16):
+        return (torch.randn((1, 2, n, 128), device=DEV).to(dt),
+                torch.randn((1, 2, n, 128), device=DEV).to(dt))
+    cases = ((10, 8, 1, new(_hip.MAX_STEP_TOKENS + 1), _hip.SunShapeUnsupported),
+             (10, 8, 5, new(1), _hip.SunShapeUnsupported),      # more than a step flushes
+             (10, 2, 3, new(1), _hip.SunShapeHIPError),         # more than buffered
+             (0, 8, 1, new(1), _hip.SunShapeHIPError),          # nothing compressed
+             (63, 8, 2, new(1), _hip.SunShapeHIPError),         # flushed past the capacity
+             (10, 8, 1, new(1, torch.float32), ValueError))
+    plan_g = _hip.prepare_decode_step_grouped_il_hybrid(q, 0.088, None, cb, cents, 16, 256, idx, il,
+                                                        sc, ze, 2, 64, bk)
+    plan_f = _hip.prepare_decode_step_il8_hybrid(q, 0.088, None, cb, cents, 16, 256, idx, v8, bk)
+    for plan in (plan_g, plan_f):
+        for t_kv, n_buf, n_flush, kv_, err in cases:
+            with pytest.raises(err):
+                plan(q, t_kv, bk, bv, n_buf, n_flush, *kv_)
+    with pytest.raises(_hip.SunShapeUnsupported):
+        _hip.prepare_decode_step_grouped_il_hybrid(q, 0.088, None, cb, cents, 16, 256, idx, il, sc,
+                                                   ze, 3, 64, bk)
+    torch.cuda.synchronize()
+    for x in (idx, il, sc, ze, v8, bk, bv):
+        assert not x.any()
+
+
 def test_prefill_il8_at_the_benchmarked_prompt():
     """The prefill kernel at the benchmarked shape (B=1, 32 query / 8 KV
     heads, a causal 4096-token prompt against its own cache): every row of
