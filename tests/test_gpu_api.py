@@ -1092,16 +1092,16 @@ def test_hybrid_fp16_steps_fuse_into_attention(d, n_new, buf, causal):
     assert torch.equal(fused.key_indices, plain.key_indices)
 
 
-@pytest.mark.parametrize("backend,b,hq,hkv,t0,buf,n_new", [
-    ("grouped", 1, 4, 4, 20, 8, 1),      # a dozen compressed tokens: one split, fewer units than waves
-    ("grouped", 3, 32, 8, 5000, 8, 4),   # every step flushes four tokens; two splits
-    ("grouped", 3, 32, 8, 5000, 8, 1),   # ten splits (the last hands over whole units only)
-    ("grouped", 1, 32, 8, 5000, 8, 4),   # eight splits
-    ("grouped", 2, 16, 2, 1100, 128, 2),  # eight query heads a KV head: two row groups
-    ("fp16", 1, 4, 4, 20, 8, 1),
-    ("fp16", 3, 32, 8, 5000, 16, 4),
+@pytest.mark.parametrize("backend,b,hq,hkv,t0,buf,n_new,qdt", [
+    ("grouped", 1, 4, 4, 20, 8, 1, torch.float16),      # a dozen compressed tokens: one split, fewer units than waves
+    ("grouped", 3, 32, 8, 5000, 8, 4, torch.float16),   # every step flushes four tokens; two splits
+    ("grouped", 3, 32, 8, 5000, 8, 1, torch.float16),   # ten splits (the last hands over whole units only)
+    ("grouped", 1, 32, 8, 5000, 8, 4, torch.bfloat16),  # eight splits; bf16 queries
+    ("grouped", 2, 16, 2, 1100, 128, 2, torch.float32),  # eight query heads a KV head: two row groups
+    ("fp16", 1, 4, 4, 20, 8, 1, torch.float16),
+    ("fp16", 3, 32, 8, 5000, 16, 4, torch.bfloat16),
 ])
-def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new):
+def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new, qdt):
     """One-launch hybrid steps at shapes the other tests do not reach: a
     single split holding fewer 64-token units than waves, steps that flush
     the most tokens, up to ten splits, several row groups a KV head.  The
@@ -1126,7 +1126,7 @@ def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new):
     g = torch.Generator(device=DEV).manual_seed(100)
     for i in range(steps):
         sl = slice(t0 + i * n_new, t0 + (i + 1) * n_new)
-        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).half()
+        q = torch.randn((b, hq, n_new, d), generator=g, device=DEV).to(qdt)
         fused.update_and_fetch(k[:, :, sl], v[:, :, sl])
         assert fused._pending is not None
         out_f = S.sunshape_sdpa(q, fused, 0.088, mask="causal", out_dtype=torch.float32)
@@ -1140,7 +1140,11 @@ def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new):
     assert torch.equal(fused.values, plain.values)
     assert torch.equal(fused.buffer_keys, plain.buffer_keys)
     vals = fused.values.float().cpu().numpy()
-    ref = O.sdpa_two_pass(q.cpu().numpy(), 0.088, codec.permutation.cpu().numpy(),
+    if qdt == torch.bfloat16:  # q * scale rounded to bf16, as the kernels form it
+        qref, sc = (q.float() * 0.088).to(torch.bfloat16).float().cpu().numpy(), 1.0
+    else:
+        qref, sc = q.cpu().numpy(), 0.088
+    ref = O.sdpa_two_pass(qref, sc, codec.permutation.cpu().numpy(),
                           codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
                           fused.buffer_keys.float().cpu().numpy(), vals, mask="causal")
     assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
