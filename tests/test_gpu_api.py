@@ -1148,6 +1148,7 @@ def test_hybrid_steps_fuse_at_edge_shapes(backend, b, hq, hkv, t0, buf, n_new, q
                           codec.centroids.cpu().numpy(), fused.key_indices.cpu().numpy(),
                           fused.buffer_keys.float().cpu().numpy(), vals, mask="causal")
     assert rel_err(out_f.cpu().numpy(), ref) <= REL_TOL
+    assert rel_err(out_p.cpu().numpy(), ref) <= REL_TOL  # the buffered decode, same splits as ever
 
 
 def test_hybrid_grouped_step_ties_take_the_exact_ranking():
