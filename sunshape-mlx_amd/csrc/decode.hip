@@ -5470,7 +5470,8 @@ static int hybrid_step_setup(DecodeCommon &c, DecodeShape &s, const void *q, int
                              int64_t buf_st, int64_t n_buf, int64_t n_flush, const void *k_new,
                              const void *v_new, int kv_dtype, int64_t kv_sb, int64_t kv_sh,
                              int64_t kv_st, int64_t n_new, int causal, int64_t q_offset, void *out,
-                             int out_dtype, void *workspace, size_t workspace_bytes, int n_splits) {
+                             int out_dtype, void *workspace, size_t workspace_bytes, int n_splits,
+                             int pad_unit) {
     SS_UNSUPPORTED(n_new >= 1 && n_new <= kMaxStepTokens, "a fused step takes 1..%d new tokens",
                    kMaxStepTokens);
     SS_UNSUPPORTED(n_flush >= 0 && n_flush <= kMaxStepTokens,
@@ -5505,12 +5506,13 @@ static int hybrid_step_setup(DecodeCommon &c, DecodeShape &s, const void *q, int
         static_cast<const char *>(codebook) + (size_t)cb_tiles(n_blocks, n_centroids) * 2 * kWave * 16);
     if (s.S > 1 && n_flush > 0) {
         // the last split encodes and attends the flushed tokens before its
-        // tiles: it gives up some cache tokens to the others, whole 64-token
-        // units (a split must start on a code word: 16 tokens of 2-bit codes)
+        // tiles: it gives up some cache tokens to the others, in units of
+        // pad_unit tokens (a split must start on a code word: 64 for grouped
+        // codes, whose 2-bit words hold 16 tokens; 8 for interleaved fp16)
+        const int64_t pu = pad_unit;
         const int64_t room = t_kv - (int64_t)(s.S - 1) * s.tiles_per_split * kWave;
-        const int64_t want = (kHybridStepShareTokens + (s.S - 1) * kWave - 1) /
-                             ((int64_t)(s.S - 1) * kWave) * kWave;
-        const int64_t most = room > 0 ? room / (s.S - 1) / kWave * kWave : 0;
+        const int64_t want = (kHybridStepShareTokens + (s.S - 1) * pu - 1) / ((int64_t)(s.S - 1) * pu) * pu;
+        const int64_t most = room > 0 ? room / (s.S - 1) / pu * pu : 0;
         c.split_pad = (int)(want < most ? want : most);
     }
     return SS_OK;
@@ -5541,7 +5543,7 @@ extern "C" int ss_decode_step_grouped_il_hybrid(
                                perm, codebook, centroids, n_blocks, n_centroids, idx, cap, t_kv,
                                k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, n_buf, n_flush,
                                k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, causal, q_offset,
-                               out, out_dtype, workspace, workspace_bytes, n_splits);
+                               out, out_dtype, workspace, workspace_bytes, n_splits, kWave);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float *norms = c.codebook_mul + 4;
@@ -5615,7 +5617,7 @@ extern "C" int ss_decode_step_il8_hybrid(
                                perm, codebook, centroids, n_blocks, n_centroids, idx, cap, t_kv,
                                k_buf, v_buf, buf_dtype, buf_sb, buf_sh, buf_st, n_buf, n_flush,
                                k_new, v_new, kv_dtype, kv_sb, kv_sh, kv_st, n_new, causal, q_offset,
-                               out, out_dtype, workspace, workspace_bytes, n_splits);
+                               out, out_dtype, workspace, workspace_bytes, n_splits, 8);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const float *norms = c.codebook_mul + 4;
